@@ -1,0 +1,37 @@
+"""MI355X-native routed sparse path of the foveal sparse indexer.
+
+Mirrors the public names of foveal_indexer/__init__.py:3-95 for the routed
+sparse path (indexer routing, block-sparse Pattention MLP, foveal decode
+attention, block-sparse linear / 2-D tiled matmul).  Compute runs in the HIP
+library libfsi_amd.so (C ABI: include/fsi.h); there is no CPU path.
+"""
+from . import _lib
+from .pattention import (
+    HAS_HIP,
+    HAS_TRITON,
+    TritonSwiGLUPattentionMLP,
+    convert_llm_mlp_to_pattention,
+    fused_swiglu,
+    pattention_forward,
+    triton_fused_swiglu,
+    triton_pattention,
+)
+from .foveal_pattention import (
+    FovealPattentionMLP,
+    mlp_pooled_route,
+    sparsify_model_with_foveal_pattention,
+)
+
+__all__ = [
+    "FovealPattentionMLP",
+    "sparsify_model_with_foveal_pattention",
+    "mlp_pooled_route",
+    "triton_pattention",
+    "triton_fused_swiglu",
+    "fused_swiglu",
+    "pattention_forward",
+    "TritonSwiGLUPattentionMLP",
+    "convert_llm_mlp_to_pattention",
+    "HAS_HIP",
+    "HAS_TRITON",
+]

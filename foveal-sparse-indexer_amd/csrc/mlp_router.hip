@@ -1,0 +1,142 @@
+// Pooled 16-D router of FovealPattentionMLP in eval mode
+// (foveal_indexer/foveal_pattention.py:310-322):
+//
+//   q      = rms_norm(q_proj_16d(mean_over_tokens(x)))         (bf16 rounding after each op)
+//   s[b]   = q . block_keys_16d[b]                              (no 1/sqrt(16) in eval)
+//   top    = topk(s[base:], remote_blocks)                      (descending; ties -> lower index)
+//   active = [0, 1, ..., base-1] ++ (top + base)
+//
+// Rounding points mirror torch's CPU bf16 ops: the token mean accumulates
+// sequentially in fp32 (torch's outer-dim reduction order) and rounds once;
+// the projection and scores accumulate in fp32 and round once; rms_norm runs in
+// fp32 with eps = FLT_EPSILON and rounds once.
+#include "fsi_common.h"
+
+using namespace fsi;
+
+namespace {
+
+constexpr int MAX_INDEX_DIM = 64;
+
+// Sequential-over-tokens mean of x[:, d], rounded to the storage dtype.
+template <bool BF16>
+__global__ void token_mean(const void* __restrict__ x, int64_t ldx, int M, int D, float* __restrict__ xm) {
+  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= D) return;
+  float acc = 0.f;
+  if (BF16) {
+    const bf16_t* p = static_cast<const bf16_t*>(x) + d;
+    for (int m = 0; m < M; ++m) acc += bf16_to_f32(p[static_cast<int64_t>(m) * ldx]);
+    xm[d] = round_bf16(acc / static_cast<float>(M));
+  } else {
+    const float* p = static_cast<const float*>(x) + d;
+    for (int m = 0; m < M; ++m) acc += p[static_cast<int64_t>(m) * ldx];
+    xm[d] = acc / static_cast<float>(M);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ float ldval(const void* p, int64_t i) {
+  return BF16 ? bf16_to_f32(static_cast<const bf16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+}
+
+// One workgroup: projection, rms_norm, scores and top-k selection.
+template <bool BF16>
+__global__ __launch_bounds__(256) void pooled_route(const float* __restrict__ xm, int D,
+                                                    const void* __restrict__ wq, int index_dim,
+                                                    const void* __restrict__ keys, int n_blocks,
+                                                    int base_blocks, int remote_blocks, float score_scale,
+                                                    int32_t* __restrict__ active, float* __restrict__ scores_out,
+                                                    float* __restrict__ scratch) {
+  __shared__ float q[MAX_INDEX_DIM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // q_j = x_mean . Wq[j]  (wave w handles j = w, w + 4, ...)
+  for (int j = wave; j < index_dim; j += 4) {
+    float acc = 0.f;
+    for (int d = lane; d < D; d += 64) acc = fmaf(xm[d], ldval<BF16>(wq, static_cast<int64_t>(j) * D + d), acc);
+    acc = wave_sum(acc);
+    if (lane == 0) q[j] = BF16 ? round_bf16(acc) : acc;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float ss = 0.f;
+    for (int j = 0; j < index_dim; ++j) ss += q[j] * q[j];
+    const float r = 1.0f / sqrtf(ss / static_cast<float>(index_dim) + 1.1920928955078125e-07f);
+    for (int j = 0; j < index_dim; ++j) q[j] = BF16 ? round_bf16(q[j] * r) : q[j] * r;
+  }
+  __syncthreads();
+  // scores
+  for (int b = tid; b < n_blocks; b += 256) {
+    float acc = 0.f;
+    for (int j = 0; j < index_dim; ++j) acc = fmaf(q[j], ldval<BF16>(keys, static_cast<int64_t>(b) * index_dim + j), acc);
+    if (score_scale != 1.0f) {
+      if (BF16) acc = round_bf16(acc);
+      acc = acc * score_scale;
+    }
+    const float s = BF16 ? round_bf16(acc) : acc;
+    scratch[b] = s;
+    if (scores_out) scores_out[b] = s;
+  }
+  __syncthreads();
+  // Rank among remote candidates: larger score first, ties broken by lower index.
+  for (int b = base_blocks + tid; b < n_blocks; b += 256) {
+    const float s = scratch[b];
+    int rank = 0;
+    for (int o = base_blocks; o < n_blocks; ++o) {
+      const float t = scratch[o];
+      rank += (t > s) || (t == s && o < b);
+    }
+    if (rank < remote_blocks) active[base_blocks + rank] = b;
+  }
+  for (int b = tid; b < base_blocks; b += 256) active[b] = b;
+}
+
+}  // namespace
+
+extern "C" {
+
+FSI_API size_t fsi_mlp_router_workspace_size(int64_t D, int64_t n_blocks) {
+  return FSI_WORKSPACE_COUNTER_BYTES + fsi_host::align_up(sizeof(float) * D, 256) + fsi_host::align_up(sizeof(float) * n_blocks, 256);
+}
+
+FSI_API int fsi_mlp_router(const void* x, int64_t ldx, int64_t M, int64_t D, const void* q_proj_w, int64_t index_dim,
+                           const void* block_keys, int64_t n_blocks, int64_t base_blocks, int64_t remote_blocks,
+                           float score_scale, int dtype, int32_t* out_active, float* out_scores, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16 || dtype == FSI_DTYPE_F32, FSI_ERR_DTYPE, "mlp_router: dtype %d", dtype);
+  FSI_CHECK_ARG(x && q_proj_w && block_keys && out_active, FSI_ERR_INVALID_ARG, "mlp_router: null pointer");
+  FSI_CHECK_ARG(M > 0 && D > 0 && ldx >= D && n_blocks > 0, FSI_ERR_SHAPE, "mlp_router: M=%lld D=%lld n_blocks=%lld",
+                (long long)M, (long long)D, (long long)n_blocks);
+  FSI_CHECK_ARG(index_dim > 0 && index_dim <= MAX_INDEX_DIM, FSI_ERR_SHAPE, "mlp_router: index_dim %lld > %d",
+                (long long)index_dim, MAX_INDEX_DIM);
+  FSI_CHECK_ARG(base_blocks >= 0 && remote_blocks >= 0 && base_blocks <= n_blocks, FSI_ERR_SHAPE,
+                "mlp_router: base=%lld remote=%lld", (long long)base_blocks, (long long)remote_blocks);
+  // torch.topk raises when k exceeds the candidate count (foveal_pattention.py:314).
+  FSI_CHECK_ARG(remote_blocks <= n_blocks - base_blocks, FSI_ERR_CAPACITY,
+                "mlp_router: remote_blocks=%lld > candidates=%lld", (long long)remote_blocks,
+                (long long)(n_blocks - base_blocks));
+  const size_t need = fsi_mlp_router_workspace_size(D, n_blocks);
+  FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE, "mlp_router: workspace %zu < %zu",
+                workspace_bytes, need);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  float* xm = reinterpret_cast<float*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES);
+  float* scratch = reinterpret_cast<float*>(reinterpret_cast<char*>(xm) + fsi_host::align_up(sizeof(float) * D, 256));
+  const dim3 g1((unsigned)((D + 63) / 64));
+  if (dtype == FSI_DTYPE_BF16) {
+    token_mean<true><<<g1, 64, 0, st>>>(x, ldx, (int)M, (int)D, xm);
+    FSI_HIP_LAUNCH_CHECK("mlp_router mean");
+    pooled_route<true><<<1, 256, 0, st>>>(xm, (int)D, q_proj_w, (int)index_dim, block_keys, (int)n_blocks,
+                                          (int)base_blocks, (int)remote_blocks, score_scale, out_active, out_scores,
+                                          scratch);
+  } else {
+    token_mean<false><<<g1, 64, 0, st>>>(x, ldx, (int)M, (int)D, xm);
+    FSI_HIP_LAUNCH_CHECK("mlp_router mean");
+    pooled_route<false><<<1, 256, 0, st>>>(xm, (int)D, q_proj_w, (int)index_dim, block_keys, (int)n_blocks,
+                                           (int)base_blocks, (int)remote_blocks, score_scale, out_active, out_scores,
+                                           scratch);
+  }
+  FSI_HIP_LAUNCH_CHECK("mlp_router route");
+  return FSI_OK;
+}
+
+}  // extern "C"

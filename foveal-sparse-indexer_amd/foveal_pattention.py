@@ -1,0 +1,227 @@
+"""FovealPattentionMLP on MI355X: drop-in for foveal_indexer/foveal_pattention.py.
+
+Same constructor, parameter names (state_dict compatible), eval routing,
+active-block cache and forward signature as the reference
+(foveal_pattention.py:54-352).  Differences by design:
+  * No gathered weight copies: the reference slices the active rows of k_gate,
+    k_up and v into contiguous caches (set_active_blocks, :115-122); here the
+    HIP kernels stream those rows from the full tensors by block index, so the
+    cache holds only the int32 block list.
+  * bf16 rounding follows the reference's GPU path when use_fused_kernel=True
+    (fused SwiGLU, one rounding of silu(g)*u; :281-282) and its eager path
+    otherwise (silu(g) and the product rounded separately; :283-284).
+  * Inference only: training-mode forward raises NotImplementedError.
+"""
+from __future__ import annotations
+
+import math
+from typing import Any, Dict, List, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from . import _lib
+from .pattention import pattention_forward
+
+
+def mlp_pooled_route(
+    x2d: Tensor,
+    q_proj_weight: Tensor,
+    block_keys: Tensor,
+    base_blocks: int,
+    remote_blocks: int,
+    score_scale: float = 1.0,
+    return_scores: bool = False,
+):
+    """Eval-mode pooled routing (foveal_pattention.py:310-321) on the GPU.
+
+    Returns the int32 active block list [0..base) ++ (topk(s[base:]) + base);
+    with return_scores, also the (n_blocks,) fp32 router scores."""
+    what = "mlp_router"
+    dev = _lib.require_gpu(x2d, q_proj_weight, block_keys, what=what)
+    dt = x2d.dtype
+    if q_proj_weight.dtype != dt or block_keys.dtype != dt:
+        raise TypeError(f"{what}: dtype mismatch {dt}/{q_proj_weight.dtype}/{block_keys.dtype}")
+    code = _lib.dtype_code(dt, what)
+    if x2d.stride(-1) != 1:
+        x2d = x2d.contiguous()
+    wq = q_proj_weight.contiguous()
+    keys = block_keys.contiguous()
+    M, D = x2d.shape
+    index_dim = wq.shape[0]
+    n_blocks = keys.shape[0]
+    if remote_blocks > n_blocks - base_blocks:
+        # torch.topk: "selected index k out of range" (foveal_pattention.py:314)
+        raise RuntimeError(f"{what}: selected index k out of range ({remote_blocks} > {n_blocks - base_blocks})")
+    active = torch.empty(base_blocks + remote_blocks, dtype=torch.int32, device=dev)
+    scores = torch.empty(n_blocks, dtype=torch.float32, device=dev) if return_scores else None
+    stream = _lib.stream_handle(dev)
+    L = _lib.lib()
+    ws = _lib.workspace(dev, L.fsi_mlp_router_workspace_size(D, n_blocks), stream)
+    st = L.fsi_mlp_router(x2d.data_ptr(), x2d.stride(0), M, D, wq.data_ptr(), index_dim, keys.data_ptr(), n_blocks,
+                          base_blocks, remote_blocks, float(score_scale), code, active.data_ptr(), _lib.ptr(scores),
+                          ws.data_ptr(), ws.numel(), stream)
+    _lib.check(st, what)
+    if return_scores:
+        return active, scores
+    return active
+
+
+class FovealPattentionMLP(nn.Module):
+    """Foveal block-sparse SwiGLU Pattention layer (foveal_pattention.py:54-352)."""
+
+    def __init__(
+        self,
+        hidden_dim: int = 2048,
+        intermediate_dim: int = 6144,
+        block_size: int = 64,
+        base_blocks: int = 4,
+        remote_blocks: int = 20,
+        index_dim: int = 16,
+        temperature: float = 1.0,
+        dtype: torch.dtype = torch.bfloat16,
+        use_fused_kernel: bool = True,
+    ):
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.intermediate_dim = intermediate_dim
+        self.block_size = block_size
+        self.num_blocks = intermediate_dim // block_size
+        self.base_blocks = base_blocks
+        self.remote_blocks = remote_blocks
+        self.total_active_blocks = base_blocks + remote_blocks
+        self.active_channels = self.total_active_blocks * block_size
+        self.index_dim = index_dim
+        self.temperature = temperature
+        self.dtype = dtype
+        self.use_fused_kernel = use_fused_kernel
+
+        self.k_gate = nn.Parameter(torch.empty(intermediate_dim, hidden_dim, dtype=dtype))
+        self.k_up = nn.Parameter(torch.empty(intermediate_dim, hidden_dim, dtype=dtype))
+        # v is logically (N_p, D) as in the reference; its storage is the row-major
+        # (D, N_p) down_proj layout, which the decode kernel streams in full lines.
+        self.v = nn.Parameter(torch.empty(hidden_dim, intermediate_dim, dtype=dtype).t())
+        self.q_proj_16d = nn.Linear(hidden_dim, index_dim, bias=False, dtype=dtype)
+        self.block_keys_16d = nn.Parameter(torch.empty(self.num_blocks, index_dim, dtype=dtype))
+        self.out_proj_16d = nn.Linear(index_dim, hidden_dim, bias=False, dtype=dtype)
+        self.register_buffer("offsets", torch.arange(block_size, dtype=torch.int64))
+
+        self._cached_active_blocks: Optional[Tensor] = None
+        self.reset_parameters()
+
+    # -- cache state machine (foveal_pattention.py:108-122) -----------------
+    def clear_cache(self) -> None:
+        self._cached_active_blocks = None
+
+    def set_active_blocks(self, active_blocks: Tensor) -> None:
+        """Fix the active block list used by later eval calls until clear_cache()."""
+        active_blocks = torch.as_tensor(active_blocks)
+        if active_blocks.device.type == "cpu" and active_blocks.numel() > 0:
+            lo, hi = int(active_blocks.min()), int(active_blocks.max())
+            if lo < 0 or hi >= self.num_blocks:
+                raise IndexError(f"active block index out of range [0, {self.num_blocks}): min {lo}, max {hi}")
+        self._cached_active_blocks = active_blocks.reshape(-1).to(device=self.k_gate.device,
+                                                                  dtype=torch.int32).contiguous()
+
+    def reset_parameters(self) -> None:
+        std = self.hidden_dim ** -0.5
+        nn.init.normal_(self.k_gate, std=std)
+        nn.init.normal_(self.k_up, std=std)
+        nn.init.normal_(self.v, std=std)
+        nn.init.normal_(self.q_proj_16d.weight, std=std)
+        nn.init.normal_(self.block_keys_16d, std=self.index_dim ** -0.5)
+        nn.init.normal_(self.out_proj_16d.weight, std=1e-3)
+
+    @classmethod
+    def from_dense_mlp(
+        cls,
+        dense_mlp: nn.Module,
+        block_size: int = 64,
+        base_blocks: int = 4,
+        remote_blocks: int = 20,
+        index_dim: int = 16,
+        temperature: float = 1.0,
+        use_fused_kernel: bool = True,
+    ) -> "FovealPattentionMLP":
+        """Exact reparameterisation K_gate = W_gate, K_up = W_up, V = W_down^T
+        (foveal_pattention.py:133-173)."""
+        hidden_dim = dense_mlp.gate_proj.in_features
+        intermediate_dim = dense_mlp.gate_proj.out_features
+        dtype = dense_mlp.gate_proj.weight.dtype
+        device = dense_mlp.gate_proj.weight.device
+        patt = cls(hidden_dim=hidden_dim, intermediate_dim=intermediate_dim, block_size=block_size,
+                   base_blocks=base_blocks, remote_blocks=remote_blocks, index_dim=index_dim,
+                   temperature=temperature, dtype=dtype, use_fused_kernel=use_fused_kernel).to(device)
+        with torch.no_grad():
+            patt.k_gate = nn.Parameter(dense_mlp.gate_proj.weight.data)
+            patt.k_up = nn.Parameter(dense_mlp.up_proj.weight.data)
+            patt.v = nn.Parameter(dense_mlp.down_proj.weight.data.t())
+            nn.init.zeros_(patt.out_proj_16d.weight)
+        return patt
+
+    def calibrate_offline_svd(self, features: Tensor, ridge_lambda: float = 1e-2) -> Dict[str, float]:
+        raise NotImplementedError("offline SVD calibration is outside the MI355X inference path")
+
+    def compute_router_scores(self, x: Tensor) -> Tensor:
+        """Per-token router scores rms_norm(q_proj(x)) @ K_16^T / sqrt(16)
+        (foveal_pattention.py:257-262); reported in router info only."""
+        q_16 = F.rms_norm(self.q_proj_16d(x), (self.index_dim,))
+        return torch.matmul(q_16, self.block_keys_16d.t()) / math.sqrt(self.index_dim)
+
+    def _rounding(self) -> str:
+        return "fused" if self.use_fused_kernel else "eager"
+
+    def forward(self, x: Tensor, return_router_info: bool = False):
+        if self.training:
+            raise NotImplementedError(
+                "FovealPattentionMLP training forward is not implemented on the MI355X path; call .eval()"
+            )
+        orig_shape = x.shape
+        D = orig_shape[-1]
+        x_2d = x.reshape(-1, D)
+        is_prefill = (len(orig_shape) >= 3 and orig_shape[-2] > 1) or (
+            len(orig_shape) == 2 and orig_shape[0] > 1 and self.training)
+
+        fast = self._cached_active_blocks is not None and not is_prefill
+        if self._cached_active_blocks is None:
+            active = mlp_pooled_route(x_2d, self.q_proj_16d.weight, self.block_keys_16d, self.base_blocks,
+                                      self.remote_blocks)
+            self._cached_active_blocks = active
+        active_blocks = self._cached_active_blocks
+        out = pattention_forward(x_2d, self.k_gate, self.k_up, self.v, active_blocks, self.block_size,
+                                 activation="swiglu", rounding=self._rounding()).reshape(*orig_shape)
+        if return_router_info:
+            if fast:
+                return out, {"active_blocks": active_blocks}
+            return out, {
+                "scores": self.compute_router_scores(x_2d),
+                "active_blocks": active_blocks,
+                "sparsity": (1.0 - self.total_active_blocks / self.num_blocks) * 100.0,
+            }
+        return out
+
+
+def sparsify_model_with_foveal_pattention(
+    model: nn.Module,
+    layers_to_sparsify: Optional[List[int]] = None,
+    block_size: int = 64,
+    base_blocks: int = 4,
+    remote_blocks: int = 20,
+    index_dim: int = 16,
+    temperature: float = 1.0,
+    use_fused_kernel: bool = True,
+) -> nn.Module:
+    """Replace `model.model.layers[i].mlp` with FovealPattentionMLP (foveal_pattention.py:355-387)."""
+    layers = getattr(model, "model", model).layers
+    targets = layers_to_sparsify if layers_to_sparsify is not None else list(range(len(layers)))
+    for idx in targets:
+        if hasattr(layers[idx], "mlp"):
+            dense_mlp = layers[idx].mlp
+            layers[idx].mlp = FovealPattentionMLP.from_dense_mlp(
+                dense_mlp, block_size=block_size, base_blocks=base_blocks, remote_blocks=remote_blocks,
+                index_dim=index_dim, temperature=temperature, use_fused_kernel=use_fused_kernel)
+            del dense_mlp
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()
+    return model

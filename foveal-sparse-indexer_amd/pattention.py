@@ -1,0 +1,232 @@
+"""Fused non-softmax Pattention and SwiGLU on MI355X.
+
+Drop-in for foveal_indexer/pattention_triton.py: `triton_pattention`
+(:204-277), `triton_fused_swiglu` (:98-104) and `TritonSwiGLUPattentionMLP`
+(:314-375).  The `triton_*` names are kept for compatibility; the kernels are
+hand-written HIP for gfx950 (csrc/pattention.hip), not Triton.
+"""
+from __future__ import annotations
+
+from typing import Literal, Optional
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from . import _lib
+
+# The reference exports HAS_TRITON to say "the GPU kernel path exists".  Here the
+# kernel path is the HIP library.
+HAS_HIP = _lib.LIB_PATH.exists()
+HAS_TRITON = HAS_HIP
+
+
+def _as_index_tensor(active_blocks, device: torch.device) -> Tensor:
+    if isinstance(active_blocks, Tensor):
+        t = active_blocks
+    else:
+        t = torch.as_tensor(active_blocks)
+    return t.reshape(-1).to(device=device, dtype=torch.int32).contiguous()
+
+
+def _rows_contig(t: Tensor) -> Tensor:
+    """2-D view with unit stride along the last dim (copies only when needed)."""
+    if t.dim() != 2:
+        raise ValueError(f"expected a 2-D tensor, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        t = t.contiguous()
+    return t
+
+
+def pattention_forward(
+    x2d: Tensor,
+    k_gate: Tensor,
+    k_up: Optional[Tensor],
+    v: Tensor,
+    active_blocks: Optional[Tensor],
+    block_n: int,
+    activation: str = "swiglu",
+    rounding: str = "fp32",
+    out: Optional[Tensor] = None,
+) -> Tensor:
+    """out[M, D_out] = act(x K_gate[S]^T [, x K_up[S]^T]) V[S] on the GPU.
+
+    x2d: (M, K); k_gate/k_up: (N_p, K); v: (N_p, D_out); active_blocks: int
+    block ids (or None for all channels).  rounding selects the bf16 rounding
+    points ("eager", "fused" or "fp32"; see include/fsi.h)."""
+    what = "pattention"
+    dev = _lib.require_gpu(x2d, k_gate, k_up, v, what=what)
+    dt = x2d.dtype
+    for t in (k_gate, k_up, v):
+        if t is not None and t.dtype != dt:
+            raise TypeError(f"{what}: mixed dtypes {dt} and {t.dtype}")
+    code = _lib.dtype_code(dt, what)
+    act = _lib.ACTIVATIONS.get(activation.lower())
+    if act is None:
+        raise ValueError(f"{what}: unknown activation {activation!r}")
+    if act == 0 and k_up is None:
+        raise ValueError(f"{what}: k_up required for swiglu")
+    rnd = _lib.ROUNDING[rounding]
+
+    x2d = _rows_contig(x2d)
+    k_gate = _rows_contig(k_gate)
+    # V may be stored [N_p, D_out] row-major or, as FovealPattentionMLP keeps it,
+    # as the transpose of a row-major [D_out, N_p] (a dense MLP's down_proj layout).
+    if v.dim() != 2:
+        raise ValueError(f"{what}: v must be 2-D, got {tuple(v.shape)}")
+    v_transposed = v.stride(0) == 1 and v.stride(1) >= v.shape[0] and v.shape[1] > 1
+    if v_transposed and code != _lib.DTYPE_BF16:
+        v_transposed = False  # the fp32 kernels read V as [N_p, D_out]
+    if not v_transposed:
+        v = _rows_contig(v)
+    ldv = v.stride(1) if v_transposed else v.stride(0)
+    if k_up is not None:
+        k_up = _rows_contig(k_up)
+        if k_up.stride(0) != k_gate.stride(0):
+            k_up = k_up.contiguous()
+            k_gate = k_gate.contiguous()
+    M, K = x2d.shape
+    N_p, K2 = k_gate.shape
+    if K2 != K:
+        raise ValueError(f"{what}: x has K={K} but k_gate has {K2}")
+    if k_up is not None and tuple(k_up.shape) != (N_p, K):
+        raise ValueError(f"{what}: k_up shape {tuple(k_up.shape)} != {(N_p, K)}")
+    if v.shape[0] != N_p:
+        raise ValueError(f"{what}: v has {v.shape[0]} rows, k_gate has {N_p}")
+    D_out = v.shape[1]
+
+    if active_blocks is not None:
+        idx = _as_index_tensor(active_blocks, dev)
+        n_active = idx.numel()
+    else:
+        idx, n_active = None, 0
+    n_channels = N_p if idx is None else n_active * block_n
+
+    if out is None:
+        out = torch.empty((M, D_out), dtype=dt, device=dev)
+    if idx is not None and n_active == 0:
+        # An empty block list contributes nothing (pattention_triton.py:141 loop never runs).  The
+        # ABI reads a null list as "all blocks", and an empty tensor's data pointer is null.
+        return out.zero_()
+    stream = _lib.stream_handle(dev)
+    L = _lib.lib()
+    ws_bytes = L.fsi_pattention_workspace_size(M, K, D_out, max(n_channels, 1), code)
+    ws = _lib.workspace(dev, ws_bytes, stream)
+    err = _lib.error_word(dev)
+    st = L.fsi_pattention_fwd(
+        x2d.data_ptr(), x2d.stride(0), k_gate.data_ptr(), _lib.ptr(k_up), k_gate.stride(0),
+        v.data_ptr(), ldv, int(v_transposed), _lib.ptr(idx), n_active, block_n, M, K, N_p, D_out, code, act, rnd,
+        out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), err.data_ptr(), stream,
+    )
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+    return out
+
+
+def triton_pattention(
+    x: Tensor,
+    k_gate: Tensor,
+    v: Tensor,
+    k_up: Optional[Tensor] = None,
+    active_blocks: Optional[Tensor] = None,
+    activation: Literal["swiglu", "silu", "gelu", "relu", "relu2"] = "swiglu",
+    block_n: int = 64,
+) -> Tensor:
+    """Fused non-softmax Pattention (pattention_triton.py:204-277).
+
+    Same signature and output as the reference op.  bf16 rounds the activation
+    once from the fp32 accumulators before the V contraction, as the
+    reference's fused kernel does (pattention_triton.py:197).  GeLU is the exact
+    erf form of the reference's PyTorch path (pattention_triton.py:300).
+    Unknown activation names fall back to SwiGLU like the reference kernel's
+    code map (pattention_triton.py:245-246)."""
+    act = activation.lower() if activation.lower() in _lib.ACTIVATIONS else "swiglu"
+    orig_shape = x.shape
+    x2d = x.reshape(-1, x.shape[-1])
+    out = pattention_forward(x2d, k_gate, k_up, v, active_blocks, block_n, act, rounding="fp32")
+    if len(orig_shape) > 2:
+        return out.reshape(*orig_shape[:-1], v.shape[-1])
+    return out
+
+
+def triton_fused_swiglu(g: Tensor, u: Tensor) -> Tensor:
+    """silu(g) * u in fp32, rounded once (pattention_triton.py:30-47, 98-104).
+    Forward only: the HIP build targets inference."""
+    return fused_swiglu(g, u, rounding="fused")
+
+
+def fused_swiglu(g: Tensor, u: Tensor, rounding: str = "fused") -> Tensor:
+    what = "swiglu"
+    dev = _lib.require_gpu(g, u, what=what)
+    if g.shape != u.shape or g.dtype != u.dtype:
+        raise ValueError(f"{what}: g {tuple(g.shape)}/{g.dtype} vs u {tuple(u.shape)}/{u.dtype}")
+    if torch.is_grad_enabled() and (g.requires_grad or u.requires_grad):
+        raise NotImplementedError(f"{what}: backward is not implemented on the MI355X inference path")
+    code = _lib.dtype_code(g.dtype, what)
+    g_c, u_c = g.contiguous(), u.contiguous()
+    out = torch.empty_like(g_c)
+    st = _lib.lib().fsi_swiglu(g_c.data_ptr(), u_c.data_ptr(), out.data_ptr(), g_c.numel(), code,
+                               _lib.ROUNDING[rounding], _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return out
+
+
+class TritonSwiGLUPattentionMLP(nn.Module):
+    """Drop-in SwiGLU MLP via fused Pattention (pattention_triton.py:314-375)."""
+
+    def __init__(
+        self,
+        hidden_dim: int = 2048,
+        num_param_tokens: int = 6144,
+        block_size: int = 64,
+        activation: str = "swiglu",
+        dtype: torch.dtype = torch.bfloat16,
+    ):
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.num_param_tokens = num_param_tokens
+        self.block_size = block_size
+        self.activation = activation
+        self.num_blocks = num_param_tokens // block_size
+        self.k_gate = nn.Parameter(torch.empty(num_param_tokens, hidden_dim, dtype=dtype))
+        self.k_up = nn.Parameter(torch.empty(num_param_tokens, hidden_dim, dtype=dtype))
+        self.v = nn.Parameter(torch.empty(num_param_tokens, hidden_dim, dtype=dtype))
+        nn.init.normal_(self.k_gate, std=hidden_dim ** -0.5)
+        nn.init.normal_(self.k_up, std=hidden_dim ** -0.5)
+        nn.init.normal_(self.v, std=num_param_tokens ** -0.5)
+
+    @classmethod
+    def from_dense_mlp(cls, dense_mlp: nn.Module, block_size: int = 64) -> "TritonSwiGLUPattentionMLP":
+        hidden_dim = dense_mlp.gate_proj.in_features
+        intermediate_dim = dense_mlp.gate_proj.out_features
+        dtype = dense_mlp.gate_proj.weight.dtype
+        device = dense_mlp.gate_proj.weight.device
+        mlp = cls(hidden_dim=hidden_dim, num_param_tokens=intermediate_dim, block_size=block_size,
+                  activation="swiglu", dtype=dtype).to(device)
+        with torch.no_grad():
+            mlp.k_gate.copy_(dense_mlp.gate_proj.weight)
+            mlp.k_up.copy_(dense_mlp.up_proj.weight)
+            mlp.v.copy_(dense_mlp.down_proj.weight.t())
+        return mlp
+
+    def forward(self, x: Tensor, active_blocks: Optional[Tensor] = None) -> Tensor:
+        return triton_pattention(x, self.k_gate, self.v, k_up=self.k_up, active_blocks=active_blocks,
+                                 activation=self.activation, block_n=self.block_size)
+
+
+def convert_llm_mlp_to_pattention(
+    model: nn.Module,
+    layers: Optional[list] = None,
+    block_size: int = 64,
+    activation: str = "swiglu",
+) -> nn.Module:
+    """Replace `model.model.layers[i].mlp` with TritonSwiGLUPattentionMLP
+    (pattention_triton.py:378-395)."""
+    model_layers = getattr(model, "model", model).layers
+    target_layers = layers if layers is not None else list(range(len(model_layers)))
+    for idx in target_layers:
+        if hasattr(model_layers[idx], "mlp") and not isinstance(model_layers[idx].mlp, TritonSwiGLUPattentionMLP):
+            model_layers[idx].mlp = TritonSwiGLUPattentionMLP.from_dense_mlp(model_layers[idx].mlp,
+                                                                            block_size=block_size)
+    return model

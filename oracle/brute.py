@@ -1,0 +1,74 @@
+"""Pure-Python brute-force selection on tiny rows — TEST INFRASTRUCTURE ONLY.
+
+Written independently of oracle/routing.py (no torch): fp64 softmax, an
+explicit ranking by (probability desc, index asc), a running fp64 sum, and the
+count rule of foveal_indexer/core.py:111-119 spelled out step by step.  Used to
+pin oracle.routing.select_route on inputs whose margins are far above fp32
+rounding, so both must agree exactly on counts and selected sets.
+"""
+from __future__ import annotations
+
+import math
+
+
+def select_row(scores, complete, local, remote, top_p, k_min, k_max, capacity):
+    """One (batch, query-block) row.  scores: floats; complete/local/remote: bools.
+    Returns (indices[:capacity] in rank order, count)."""
+    n = len(scores)
+    valid = [i for i in range(n) if complete[i]]
+    probs = [0.0] * n
+    if valid:
+        m = max(scores[i] for i in valid)
+        z = sum(math.exp(scores[i] - m) for i in valid)
+        for i in valid:
+            probs[i] = math.exp(scores[i] - m) / z
+    local_mass = sum(probs[i] for i in range(n) if local[i])
+    remote_ids = [i for i in range(n) if remote[i]]
+    ranked = sorted(remote_ids, key=lambda i: (-probs[i], i))
+    rest = [i for i in range(n) if not remote[i]]
+    order = ranked + rest
+
+    target = max(top_p - local_mass, 0.0)
+    running, below = 0.0, 0
+    for pos, i in enumerate(order):
+        if remote[i]:
+            running += probs[i]
+        if running < target:
+            below += 1
+    needed = below + (1 if target > 0 else 0)
+    available = len(remote_ids)
+    if available > 0:
+        needed = max(needed, k_min)
+    else:
+        needed = 0
+    count = min(needed, available, k_max)
+    idx = order[:capacity] + [0] * max(0, capacity - n)
+    return idx, count
+
+
+def masks(qb, nb, causal, local_window_blocks):
+    """Row masks for query block qb (core.py:79-99)."""
+    complete, local, remote = [], [], []
+    for p in range(nb):
+        if causal:
+            c = p < qb
+            first = max(qb - local_window_blocks, 0)
+            if local_window_blocks > 0:
+                loc, rem = c and p >= first, c and p < first
+            else:
+                loc, rem = False, c
+        else:
+            c = True
+            if local_window_blocks > 0:
+                loc, rem = p < local_window_blocks, p >= local_window_blocks
+            else:
+                loc, rem = False, True
+        complete.append(c)
+        local.append(loc)
+        remote.append(rem)
+    return complete, local, remote
+
+
+def topk_desc(values, k):
+    """Indices of the k largest values, ties to the lower index."""
+    return sorted(range(len(values)), key=lambda i: (-values[i], i))[:k]

@@ -1,0 +1,114 @@
+"""Oracle for the block-sparse Pattention MLP — TEST INFRASTRUCTURE ONLY.
+
+Restates, with the same torch CPU ops in the same order (so bf16 rounding
+lands at the same points as the reference):
+  * FovealPattentionMLP eval body       foveal_indexer/foveal_pattention.py:115-122 (gather),
+                                        :329-335 (3x F.linear + SwiGLU)
+  * _pytorch_pattention_fallback        foveal_indexer/pattention_triton.py:280-311
+  * _pattention_fused_kernel numerics   foveal_indexer/pattention_triton.py:153-201
+                                        (fp32 accumulation, act cast to V dtype, fp32 acc)
+  * _swiglu_fwd_kernel numerics         foveal_indexer/pattention_triton.py:40-47
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+
+def rel_l2(a: Tensor, b: Tensor) -> float:
+    a64, b64 = a.double(), b.double()
+    return float((a64 - b64).norm() / b64.norm().clamp_min(1e-300))
+
+
+def channel_index(active: Tensor, block_n: int) -> Tensor:
+    """Row ids of the active channels, block-major (foveal_pattention.py:118)."""
+    a = torch.as_tensor(active).reshape(-1, 1).to(torch.int64)
+    return (a * block_n + torch.arange(block_n, dtype=torch.int64)).reshape(-1)
+
+
+def swiglu_eager(g: Tensor, u: Tensor) -> Tensor:
+    """`F.silu(kg) * ku` (foveal_pattention.py:284): silu and product each rounded."""
+    return F.silu(g) * u
+
+
+def swiglu_fused(g: Tensor, u: Tensor) -> Tensor:
+    """silu(g) * u in fp32, one rounding to g's dtype (pattention_triton.py:40-47)."""
+    gf, uf = g.float(), u.float()
+    return (gf * torch.sigmoid(gf) * uf).to(g.dtype)
+
+
+def mlp_eval_forward(x2d: Tensor, k_gate: Tensor, k_up: Tensor, v: Tensor, active: Tensor, block_n: int,
+                     fused: bool) -> Tensor:
+    """Eval forward of FovealPattentionMLP over a fixed active set
+    (foveal_pattention.py:119-121 gather, :329-335 body)."""
+    rows = channel_index(active, block_n)
+    kg_act, ku_act, v_act = k_gate[rows], k_up[rows], v[rows]
+    g = F.linear(x2d, kg_act)
+    u = F.linear(x2d, ku_act)
+    act = swiglu_fused(g, u) if fused else swiglu_eager(g, u)
+    return F.linear(act, v_act.t())
+
+
+def _activation(name: str, g: Tensor, u: Tensor | None) -> Tensor:
+    if name == "swiglu":
+        return F.silu(g) * u
+    if name == "silu":
+        return F.silu(g)
+    if name == "gelu":
+        return F.gelu(g)
+    if name == "relu":
+        return F.relu(g)
+    if name == "relu2":
+        return F.relu(g) ** 2
+    return g
+
+
+def pattention_eager(x: Tensor, k_gate: Tensor, v: Tensor, k_up: Tensor | None, active: Tensor | None,
+                     activation: str, block_n: int) -> Tensor:
+    """The reference's PyTorch fallback (pattention_triton.py:280-311)."""
+    x2d = x.reshape(-1, x.shape[-1])
+    if active is not None:
+        rows = channel_index(active, block_n)
+        k_gate, v = k_gate[rows], v[rows]
+        if k_up is not None:
+            k_up = k_up[rows]
+    g = torch.matmul(x2d, k_gate.t())
+    u = torch.matmul(x2d, k_up.t()) if k_up is not None else None
+    out = torch.matmul(_activation(activation, g, u), v)
+    return out.reshape(*x.shape[:-1], v.shape[-1])
+
+
+def pattention_fp32_act(x: Tensor, k_gate: Tensor, v: Tensor, k_up: Tensor | None, active: Tensor | None,
+                        activation: str, block_n: int) -> Tensor:
+    """Numerics of the fused kernel (pattention_triton.py:153-201): gate/up
+    accumulate in fp32, the activation runs in fp32 and is cast to V's dtype,
+    the V contraction accumulates in fp32 and the result is cast to x's dtype.
+    GeLU is the exact erf form (the fallback's F.gelu, :300)."""
+    x2d = x.reshape(-1, x.shape[-1])
+    N_p = k_gate.shape[0]
+    if active is not None:
+        rows = channel_index(active, block_n)
+        valid = rows < N_p  # the kernel masks rows beyond N_p (pattention_triton.py:151)
+        rows = rows[valid]
+        k_gate, v = k_gate[rows], v[rows]
+        if k_up is not None:
+            k_up = k_up[rows]
+    xf = x2d.double()
+    g = (xf @ k_gate.double().t()).float()
+    u = (xf @ k_up.double().t()).float() if k_up is not None else None
+    act = _activation(activation, g, u).to(v.dtype)
+    out = (act.double() @ v.double()).float().to(x.dtype)
+    return out.reshape(*x.shape[:-1], v.shape[-1])
+
+
+def dense_swiglu_f64(x2d: Tensor, k_gate: Tensor, k_up: Tensor, v: Tensor, channel_mask: Tensor | None = None) -> Tensor:
+    """Exact dense SwiGLU (silu(x Wg^T) * (x Wu^T)) Wd^T in fp64, optionally with
+    the inactive channels zeroed — the closed form a sparse Pattention must equal."""
+    xf = x2d.double()
+    g = xf @ k_gate.double().t()
+    u = xf @ k_up.double().t()
+    h = g * torch.sigmoid(g) * u
+    if channel_mask is not None:
+        h = h * channel_mask.double()
+    return h @ v.double()

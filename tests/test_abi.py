@@ -1,0 +1,109 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol declared in
+include/fsi.h, and rejects bad arguments with the documented status codes
+before touching the GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    text = (ROOT / "include" / "fsi.h").read_text()
+    return sorted(set(re.findall(r"FSI_API[^;(]*?\b(fsi_\w+)\s*\(", text, flags=re.S)))
+
+
+def test_header_declares_symbols():
+    syms = _declared_symbols()
+    assert "fsi_pattention_fwd" in syms and len(syms) >= 5
+
+
+def test_library_exports_every_declared_symbol(fsi):
+    from foveal_sparse_indexer_amd import _lib
+
+    L = _lib.lib()
+    for name in _declared_symbols():
+        assert hasattr(L, name), name
+        assert name in _lib.SIGNATURES, f"{name} missing from the ctypes signature table"
+    assert set(_lib.SIGNATURES) == set(_declared_symbols())
+    assert L.fsi_abi_version() == 1
+
+
+def test_status_strings(fsi):
+    from foveal_sparse_indexer_amd import _lib
+
+    L = _lib.lib()
+    assert L.fsi_status_string(0) == b"ok"
+    assert L.fsi_status_string(-3) == b"index out of range"
+
+
+def _patt(L, **over):
+    # Fake but aligned addresses: every case below must be rejected by host-side
+    # validation, which runs before any HIP call (these tests also run on GPU boxes).
+    a = dict(x=4096, ldx=64, kg=8192, ku=12288, ldk=64, v=16384, ldv=64, act_ptr=None, n_active=0, block_n=64, M=4,
+             K=64, N_p=128, D_out=64, dtype=1, activation=0, rounding=1, out=20480, ldo=64, ws=24576, ws_bytes=16,
+             err=None, stream=None)
+    a.update(over)
+    return L.fsi_pattention_fwd(a["x"], a["ldx"], a["kg"], a["ku"], a["ldk"], a["v"], a["ldv"], a.get("vt", 0), a["act_ptr"],
+                                a["n_active"], a["block_n"], a["M"], a["K"], a["N_p"], a["D_out"], a["dtype"],
+                                a["activation"], a["rounding"], a["out"], a["ldo"], a["ws"], a["ws_bytes"], a["err"],
+                                a["stream"])
+
+
+def test_pattention_argument_errors(fsi):
+    """Validation happens on the host and returns before any HIP call."""
+    from foveal_sparse_indexer_amd import _lib
+
+    L = _lib.lib()
+    assert _patt(L, dtype=7) == _lib.FSI_ERR_DTYPE
+    assert _patt(L, activation=9) == _lib.FSI_ERR_INVALID_ARG
+    assert _patt(L, rounding=5) == _lib.FSI_ERR_INVALID_ARG
+    assert _patt(L, block_n=48) == _lib.FSI_ERR_SHAPE
+    assert _patt(L, ku=None) == _lib.FSI_ERR_INVALID_ARG            # swiglu needs k_up
+    assert _patt(L, K=60, ldx=60, ldk=60) == _lib.FSI_ERR_ALIGN      # bf16 K % 8
+    assert _patt(L, ldx=32) == _lib.FSI_ERR_SHAPE                    # ld < K
+    assert _patt(L, n_active=3) == _lib.FSI_ERR_INVALID_ARG          # list length without list
+    assert _patt(L) == _lib.FSI_ERR_WORKSPACE                         # 16-byte workspace
+    assert _patt(L, x=None) == _lib.FSI_ERR_INVALID_ARG
+    assert b"null" in L.fsi_last_error()
+    assert _patt(L, dtype=7) == _lib.FSI_ERR_DTYPE
+    assert b"dtype" in L.fsi_last_error()
+
+
+def test_workspace_sizes_are_consistent(fsi):
+    from foveal_sparse_indexer_amd import _lib
+
+    L = _lib.lib()
+    a = L.fsi_pattention_workspace_size(64, 4096, 4096, 4096, 1)
+    b = L.fsi_pattention_workspace_size(64, 4096, 4096, 4096 * 2, 1)
+    assert 0 < a < b
+    assert L.fsi_pattention_workspace_size(64, 512, 512, 512, 0) >= 64 * 512 * 4
+
+
+def test_python_ops_refuse_cpu_tensors(fsi):
+    import torch
+
+    x = torch.randn(4, 64).bfloat16()
+    w = torch.randn(128, 64).bfloat16()
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fsi.triton_pattention(x, w, w, k_up=w)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fsi.triton_fused_swiglu(x, x)
+
+
+def test_module_matches_reference_interface(fsi):
+    import torch
+
+    m = fsi.FovealPattentionMLP(hidden_dim=128, intermediate_dim=512, base_blocks=2, remote_blocks=3,
+                                dtype=torch.float32)
+    names = set(dict(m.named_parameters()))
+    assert names == {"k_gate", "k_up", "v", "q_proj_16d.weight", "block_keys_16d", "out_proj_16d.weight"}
+    assert "offsets" in dict(m.named_buffers())
+    assert m.num_blocks == 8 and m.total_active_blocks == 5
+    with pytest.raises(IndexError):
+        m.set_active_blocks(torch.tensor([0, 9]))
+    m.train()
+    with pytest.raises(NotImplementedError):
+        m(torch.randn(2, 3, 128))

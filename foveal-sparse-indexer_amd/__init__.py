@@ -16,6 +16,16 @@ from .pattention import (
     triton_fused_swiglu,
     triton_pattention,
 )
+from .core import (
+    FovealIndexer,
+    Route,
+    block_scores,
+    index_rms_norm,
+    masked_softmax,
+    score_and_route,
+    select_blocks,
+)
+from .attention import decode_route
 from .foveal_pattention import (
     FovealPattentionMLP,
     mlp_pooled_route,
@@ -23,6 +33,14 @@ from .foveal_pattention import (
 )
 
 __all__ = [
+    "Route",
+    "masked_softmax",
+    "select_blocks",
+    "score_and_route",
+    "block_scores",
+    "index_rms_norm",
+    "FovealIndexer",
+    "decode_route",
     "FovealPattentionMLP",
     "sparsify_model_with_foveal_pattention",
     "mlp_pooled_route",

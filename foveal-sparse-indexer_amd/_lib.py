@@ -56,7 +56,35 @@ SIGNATURES: dict[str, tuple] = {
         [_c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_int,
          _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr],
     ),
+    "fsi_masked_softmax": (
+        _c_int, [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
+    "fsi_route_from_scores": (
+        _c_int,
+        [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, ctypes.c_float, _c_int, _c_int, _c_int, _c_ptr,
+         _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
+    ),
+    "fsi_score_and_route": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, ctypes.c_float, _c_int,
+         _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
+    ),
+    "fsi_decode_route": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64,
+         ctypes.c_float, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
+    ),
+    "fsi_index_rms_norm": (_c_int, [_c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_ptr]),
+    "fsi_index_pool_kv": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr]),
+    "fsi_block_scores": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
+    "fsi_additive_context": (
+        _c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_ptr],
+    ),
 }
+
+ROUTE_MAX_BLOCKS = 4096
+SCORE_ROUTE_MAX_KEYS = 4096
+ROUTE_MAX_RANKED = 256
 
 _lib = None
 _lib_lock = threading.Lock()

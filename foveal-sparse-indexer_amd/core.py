@@ -1,0 +1,373 @@
+"""16-D Foveal Indexer on MI355X: drop-in for foveal_indexer/core.py.
+
+Same names, signatures, defaults and return structures as the reference
+(`Route` core.py:23-33, `masked_softmax` :36-43, `select_blocks` :46-160,
+`FovealIndexer` :163-353).  Softmax, ranking, prefix mass, counts, scoring,
+pooling and the additive-stream contraction run in the HIP library
+(csrc/routing.hip, csrc/indexer.hip); the D -> 16 projections are library
+GEMMs (nn.Linear).  Inference only: the HIP ops have no backward and refuse
+inputs that require grad while autograd is recording.
+
+Differences by design:
+  * equal probabilities are ranked lower index first (torch.sort leaves their
+    order unspecified);
+  * select_blocks handles up to 4096 blocks per row and
+    min(max(K_max, capacity), blocks) <= 256 (RuntimeError beyond);
+  * scores must be float32 or bfloat16.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from . import _lib
+
+
+@dataclass
+class Route:
+    """Routing decisions for foveal block selection (core.py:23-33)."""
+
+    remote_indices: Tensor  # (B, Q_blocks, remote_capacity) int32
+    remote_counts: Tensor  # (B, Q_blocks) int32
+    base_indices: Optional[Tensor]  # (B, Q_blocks, max_base_blocks) int32
+    base_counts: Optional[Tensor]  # (B, Q_blocks) int32
+    block_scores: Tensor  # (B, Q_blocks, total_blocks)
+    cap_rate: Tensor
+    mean_remote_blocks: Tensor
+    base_only_rate: Tensor
+
+
+def _forward_only(what: str, *tensors: Optional[Tensor]) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise NotImplementedError(
+            f"{what}: the MI355X path is inference-only (no backward); "
+            "call it under torch.no_grad() or torch.inference_mode()"
+        )
+
+
+def _as_3d(scores: Tensor, what: str) -> Tensor:
+    if scores.dim() != 3:
+        raise ValueError(f"{what}: expected (B, Q_blocks, total_blocks) scores, got {tuple(scores.shape)}")
+    return scores.contiguous()
+
+
+def masked_softmax(scores: Tensor, mask: Tensor) -> Tensor:
+    """Softmax over `mask` with masked entries and all-masked rows exactly zero,
+    computed in fp32 and returned in the scores' dtype (core.py:36-43).
+    scores: (..., N); mask: bool, broadcastable to scores."""
+    what = "masked_softmax"
+    dev = _lib.require_gpu(scores, mask, what=what)
+    _forward_only(what, scores)
+    code = _lib.dtype_code(scores.dtype, what)
+    shape = scores.shape
+    if scores.dim() == 0:
+        raise ValueError(f"{what}: scores must have at least one dimension")
+    N = shape[-1]
+    m = torch.broadcast_to(mask.to(device=dev, dtype=torch.bool), shape)
+    if scores.dim() == 3:
+        s3 = scores.contiguous()
+    else:
+        s3 = scores.contiguous().reshape(-1, 1, N)
+        m = m.reshape(-1, 1, N)
+    m8 = m.view(torch.uint8)  # bool and uint8 share the element size; strides carry over
+    out = torch.empty_like(s3)
+    B, Q, _ = s3.shape
+    st = _lib.lib().fsi_masked_softmax(s3.data_ptr(), code, B, Q, N, m8.data_ptr(), m8.stride(0), m8.stride(1),
+                                       m8.stride(2), out.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return out.reshape(shape)
+
+
+def _per_row(value, B: int, Qb: int, dtype: torch.dtype, dev: torch.device):
+    """Scalar -> (python value, None); tensor -> (None, contiguous (B*Qb,) device tensor)."""
+    if isinstance(value, Tensor):
+        if value.numel() == 1:
+            return value.reshape(()).item(), None
+        t = torch.broadcast_to(value.to(device=dev, dtype=dtype), (B, Qb)).contiguous().reshape(-1)
+        return None, t
+    return value, None
+
+
+def _route_tables(B: int, Qb: int, causal: bool, local_window_blocks: int, dev: torch.device):
+    """Base / local block tables of select_blocks (core.py:125-145)."""
+    if local_window_blocks <= 0:
+        return None, None
+    if causal:
+        width = local_window_blocks + 1
+        offs = torch.arange(width, device=dev)
+        qb = torch.arange(Qb, device=dev)
+        start = (qb - local_window_blocks).clamp_min(0)
+        n_local = qb - start + 1
+        base = torch.where(offs[None] < n_local[:, None], start[:, None] + offs[None], torch.zeros_like(offs[None]))
+        return base[None].expand(B, -1, -1).to(torch.int32), n_local[None].expand(B, -1).to(torch.int32)
+    base = torch.arange(local_window_blocks, device=dev, dtype=torch.int32)[None, None].expand(B, Qb, -1)
+    return base, torch.full((B, Qb), local_window_blocks, device=dev, dtype=torch.int32)
+
+
+def _route_stats(counts: Tensor, max_remote, dev: torch.device):
+    kmax_t = torch.as_tensor(max_remote, device=dev, dtype=torch.int64)
+    cap_rate = torch.where(kmax_t > 0, (counts >= kmax_t).float().mean(),
+                           counts.new_zeros((), dtype=torch.float32))
+    return cap_rate, counts.float().mean(), (counts == 0).float().mean()
+
+
+def select_blocks(
+    block_scores: Tensor,
+    *,
+    causal: bool = True,
+    block_size: int = 64,
+    local_window_blocks: int = 0,
+    top_p: float | Tensor = 0.95,
+    min_remote_blocks: int | Tensor = 0,
+    max_remote_blocks: int | Tensor = 16,
+    remote_capacity: int = 16,
+) -> Route:
+    """Adaptive top-p mass routing over block scores (core.py:46-160)."""
+    what = "select_blocks"
+    dev = _lib.require_gpu(block_scores, what=what)
+    scores = _as_3d(block_scores.detach(), what)
+    code = _lib.dtype_code(scores.dtype, what)
+    B, Qb, Nb = scores.shape
+    p_val, p_rows = _per_row(top_p, B, Qb, torch.float32, dev)
+    kmin_val, kmin_rows = _per_row(min_remote_blocks, B, Qb, torch.int32, dev)
+    kmax_val, kmax_rows = _per_row(max_remote_blocks, B, Qb, torch.int32, dev)
+    kmax_bound = int(kmax_rows.max().item()) if kmax_rows is not None and kmax_rows.numel() else 0
+    indices = torch.empty((B, Qb, remote_capacity), dtype=torch.int32, device=dev)
+    counts = torch.empty((B, Qb), dtype=torch.int32, device=dev)
+    st = _lib.lib().fsi_route_from_scores(
+        scores.data_ptr(), code, B, Qb, Nb, int(bool(causal)), int(local_window_blocks),
+        float(p_val if p_val is not None else 0.0), int(kmin_val if kmin_val is not None else 0),
+        int(kmax_val if kmax_val is not None else 0), int(remote_capacity), _lib.ptr(p_rows), _lib.ptr(kmin_rows),
+        _lib.ptr(kmax_rows), kmax_bound, indices.data_ptr(), counts.data_ptr(), None, _lib.stream_handle(dev))
+    _lib.check(st, what)
+    base_indices, base_counts = _route_tables(B, Qb, causal, local_window_blocks, dev)
+    cap_rate, mean_remote, base_only = _route_stats(counts, max_remote_blocks, dev)
+    return Route(remote_indices=indices, remote_counts=counts, base_indices=base_indices, base_counts=base_counts,
+                 block_scores=block_scores, cap_rate=cap_rate, mean_remote_blocks=mean_remote,
+                 base_only_rate=base_only)
+
+
+def score_and_route(
+    q: Tensor,
+    k: Tensor,
+    *,
+    causal: bool = False,
+    local_window_blocks: int = 0,
+    top_p: float = 0.95,
+    min_remote_blocks: int = 0,
+    max_remote_blocks: int = 16,
+    remote_capacity: int = 16,
+    return_mass: bool = False,
+):
+    """Fused fp32 cosine scoring + select_blocks without materialising scores.
+
+    Equivalent to select_blocks(normalize(q) . normalize(k)^T / sqrt(d)) with
+    every step in fp32 (the fp32 form of compute_block_scores, core.py:254-266).
+    q: (B, Q, 16) or (Q, 16); k: (B, N, 16), (1, N, 16) or (N, 16) (shared).
+    Returns (indices (B, Q, capacity) int32, counts (B, Q) int32[, mass (B, Q) fp32])."""
+    what = "score_and_route"
+    dev = _lib.require_gpu(q, k, what=what)
+    if q.dtype != k.dtype:
+        raise TypeError(f"{what}: q {q.dtype} and k {k.dtype} differ")
+    code = _lib.dtype_code(q.dtype, what)
+    q3 = (q if q.dim() == 3 else q.unsqueeze(0)).contiguous()
+    k3 = (k if k.dim() == 3 else k.unsqueeze(0)).contiguous()
+    B, Q, d = q3.shape
+    Bk, N, dk = k3.shape
+    if dk != d or Bk not in (1, B):
+        raise ValueError(f"{what}: q {tuple(q3.shape)} and k {tuple(k3.shape)} do not match")
+    k_stride = 0 if Bk == 1 else N * d
+    indices = torch.empty((B, Q, remote_capacity), dtype=torch.int32, device=dev)
+    counts = torch.empty((B, Q), dtype=torch.int32, device=dev)
+    mass = torch.empty((B, Q), dtype=torch.float32, device=dev) if return_mass else None
+    st = _lib.lib().fsi_score_and_route(
+        q3.data_ptr(), k3.data_ptr(), code, B, Q, N, d, k_stride, int(bool(causal)), int(local_window_blocks),
+        float(top_p), int(min_remote_blocks), int(max_remote_blocks), int(remote_capacity), indices.data_ptr(),
+        counts.data_ptr(), _lib.ptr(mass), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    if return_mass:
+        return indices, counts, mass
+    return indices, counts
+
+
+class FovealIndexer(nn.Module):
+    """Modular 16-dimensional Foveal Indexer (core.py:163-353)."""
+
+    def __init__(
+        self,
+        hidden_size: int,
+        index_dim: int = 16,
+        block_size: int = 64,
+        local_window_blocks: int = 8,
+        top_p: float = 0.95,
+        min_remote_blocks: int = 0,
+        max_remote_blocks: int = 16,
+        remote_capacity: int = 16,
+        causal: bool = True,
+        use_additive_stream: bool = True,
+        distill_temperature: float = 1.0,
+    ):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.index_dim = index_dim
+        self.block_size = block_size
+        self.local_window_blocks = local_window_blocks
+        self.top_p = top_p
+        self.min_remote_blocks = min_remote_blocks
+        self.max_remote_blocks = max_remote_blocks
+        self.remote_capacity = remote_capacity
+        self.causal = causal
+        self.use_additive_stream = use_additive_stream
+        self.distill_temperature = distill_temperature
+
+        self.q_proj = nn.Linear(hidden_size, index_dim, bias=False)
+        self.k_proj = nn.Linear(hidden_size, index_dim, bias=False)
+        self.v_proj = nn.Linear(hidden_size, index_dim, bias=False)
+        self.out_proj = nn.Linear(index_dim, hidden_size, bias=False)
+        nn.init.normal_(self.q_proj.weight, std=hidden_size ** -0.5)
+        nn.init.normal_(self.k_proj.weight, std=hidden_size ** -0.5)
+        nn.init.normal_(self.v_proj.weight, std=hidden_size ** -0.5)
+        nn.init.normal_(self.out_proj.weight, std=1e-3)
+
+    def compute_query_16d(self, x: Tensor) -> Tensor:
+        """rms_norm(q_proj(x)) (core.py:214-222)."""
+        what = "compute_query_16d"
+        q = self.q_proj(x)
+        return index_rms_norm(q, what)
+
+    def compute_kv_blocks_16d(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        """Pooled, normalised 16-D keys and mean values per block (core.py:224-250)."""
+        what = "compute_kv_blocks_16d"
+        if x.ndim == 2:
+            x = x.unsqueeze(0)
+        batch, n_elements, _ = x.shape
+        if n_elements % self.block_size != 0:
+            raise ValueError(f"Element length {n_elements} must be divisible by block_size={self.block_size}")
+        k_lin = self.k_proj(x)
+        v_lin = self.v_proj(x)
+        dev = _lib.require_gpu(k_lin, v_lin, what=what)
+        _forward_only(what, k_lin, v_lin)
+        code = _lib.dtype_code(k_lin.dtype, what)
+        k_lin, v_lin = k_lin.contiguous(), v_lin.contiguous()
+        nb = n_elements // self.block_size
+        k_blocks = torch.empty((batch, nb, self.index_dim), dtype=k_lin.dtype, device=dev)
+        v_blocks = torch.empty_like(k_blocks)
+        st = _lib.lib().fsi_index_pool_kv(k_lin.data_ptr(), v_lin.data_ptr(), code, batch, n_elements,
+                                          self.index_dim, self.block_size, k_blocks.data_ptr(), v_blocks.data_ptr(),
+                                          _lib.stream_handle(dev))
+        _lib.check(st, what)
+        return k_blocks, v_blocks
+
+    def compute_block_scores(self, q_blocks: Tensor, k_blocks: Tensor) -> Tensor:
+        """Cosine / sqrt(index_dim) block scores (core.py:254-266)."""
+        return block_scores(q_blocks, k_blocks)
+
+    def route(
+        self,
+        block_scores: Tensor,
+        top_p: Optional[float] = None,
+        max_remote_blocks: Optional[int] = None,
+        min_remote_blocks: Optional[int] = None,
+    ) -> Route:
+        """Adaptive top-p routing with this module's settings (core.py:268-286)."""
+        return select_blocks(
+            block_scores.detach(),
+            causal=self.causal,
+            block_size=self.block_size,
+            local_window_blocks=self.local_window_blocks,
+            top_p=self.top_p if top_p is None else top_p,
+            min_remote_blocks=self.min_remote_blocks if min_remote_blocks is None else min_remote_blocks,
+            max_remote_blocks=self.max_remote_blocks if max_remote_blocks is None else max_remote_blocks,
+            remote_capacity=self.remote_capacity,
+        )
+
+    def additive_stream(self, block_scores: Tensor, v_blocks: Tensor) -> Tensor:
+        """Soft 16-D read over the valid blocks, projected to hidden_size and
+        repeated over each block's elements (core.py:288-312)."""
+        what = "additive_stream"
+        dev = _lib.require_gpu(block_scores, v_blocks, what=what)
+        _forward_only(what, block_scores, v_blocks)
+        if block_scores.dtype != v_blocks.dtype:
+            raise TypeError(f"{what}: scores {block_scores.dtype} and values {v_blocks.dtype} differ")
+        code = _lib.dtype_code(v_blocks.dtype, what)
+        s = _as_3d(block_scores, what)
+        v = v_blocks.contiguous()
+        B, Qb, Nb = s.shape
+        if tuple(v.shape) != (B, Nb, self.index_dim):
+            raise ValueError(f"{what}: values {tuple(v.shape)} != {(B, Nb, self.index_dim)}")
+        context = torch.empty((B, Qb, self.index_dim), dtype=v.dtype, device=dev)
+        st = _lib.lib().fsi_additive_context(s.data_ptr(), v.data_ptr(), code, B, Qb, Nb, self.index_dim,
+                                             int(bool(self.causal)), context.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        out_blocks = self.out_proj(context)
+        return out_blocks.repeat_interleave(self.block_size, dim=1)
+
+    def distillation_loss(
+        self,
+        student_scores: Tensor,
+        teacher_block_mass: Tensor,
+        valid_mask: Optional[Tensor] = None,
+    ) -> Tensor:
+        """Block-level KL loss against teacher mass (core.py:314-353).  A
+        training objective, evaluated with autograd-capable torch ops."""
+        if valid_mask is None:
+            if self.causal:
+                _, qb_len, pb_len = student_scores.shape
+                qb = torch.arange(qb_len, device=student_scores.device)
+                pb = torch.arange(pb_len, device=student_scores.device)
+                valid_mask = (pb.view(1, pb_len) < qb.view(qb_len, 1))[None].expand_as(student_scores)
+            else:
+                valid_mask = torch.ones_like(student_scores, dtype=torch.bool)
+        masked = student_scores.masked_fill(~valid_mask, -float("inf"))
+        log_student = F.log_softmax(masked.float() / self.distill_temperature, dim=-1)
+        log_student = torch.where(valid_mask, log_student, torch.zeros_like(log_student))
+        teacher = teacher_block_mass.float().clamp_min(0.0).masked_fill(~valid_mask, 0.0)
+        denom = teacher.sum(dim=-1, keepdim=True)
+        uniform = valid_mask.float() / valid_mask.float().sum(dim=-1, keepdim=True).clamp_min(1.0)
+        target = torch.where(denom > 1e-12, teacher / denom.clamp_min(1e-12), uniform)
+        kl = -(target.detach() * log_student).sum(dim=-1)
+        has_valid = valid_mask.any(dim=-1)
+        if has_valid.any():
+            return kl[has_valid].mean()
+        return student_scores.sum() * 0.0
+
+
+def index_rms_norm(x: Tensor, what: str = "index_rms_norm") -> Tensor:
+    """F.rms_norm over the last (16-wide) dimension, eps = FLT_EPSILON."""
+    dev = _lib.require_gpu(x, what=what)
+    _forward_only(what, x)
+    code = _lib.dtype_code(x.dtype, what)
+    xc = x.contiguous()
+    d = xc.shape[-1]
+    out = torch.empty_like(xc)
+    st = _lib.lib().fsi_index_rms_norm(xc.data_ptr(), code, xc.numel() // max(d, 1), d, out.data_ptr(),
+                                       _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return out
+
+
+def block_scores(q_blocks: Tensor, k_blocks: Tensor) -> Tensor:
+    """normalize(q) . normalize(k)^T / sqrt(d) with the reference's rounding
+    points (core.py:254-266).  q: (B, Q, 16); k: (B, N, 16)."""
+    what = "compute_block_scores"
+    dev = _lib.require_gpu(q_blocks, k_blocks, what=what)
+    _forward_only(what, q_blocks, k_blocks)
+    if q_blocks.dtype != k_blocks.dtype:
+        raise TypeError(f"{what}: q {q_blocks.dtype} and k {k_blocks.dtype} differ")
+    code = _lib.dtype_code(q_blocks.dtype, what)
+    q = q_blocks.contiguous()
+    k = k_blocks.contiguous()
+    if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError(f"{what}: q {tuple(q.shape)} and k {tuple(k.shape)} do not match")
+    B, Q, d = q.shape
+    N = k.shape[1]
+    out = torch.empty((B, Q, N), dtype=q.dtype, device=dev)
+    st = _lib.lib().fsi_block_scores(q.data_ptr(), k.data_ptr(), code, B, Q, N, d, out.data_ptr(),
+                                     _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return out

@@ -1,0 +1,882 @@
+// 16-D indexer routing on MI355X (gfx950): adaptive top-p / K_min / K_max
+// block selection, fused cosine scoring + selection, and decode-step page
+// routing with the additive 16-D stream.
+//
+// Semantics follow foveal_indexer/core.py:36-160 (masked_softmax,
+// select_blocks), core.py:263-265 (cosine / sqrt(d) scoring, computed here in
+// fp32 end to end) and foveal_indexer/attention.py:313-337,369-377 (decode_step
+// page routing and additive stream).
+//
+// One wavefront owns one row.  Element j of a row lives in lane j % 64,
+// register slot j / 64.  Per row:
+//   1. fp32 softmax over the valid entries (max, exp, sum; masked entries 0);
+//   2. every candidate gets an order-preserving 32-bit key (prob bits + 1;
+//      0 = not a candidate; probabilities are >= 0 so their bit patterns sort
+//      like the values);
+//   3. the R-th largest key T is found exactly by bisection over key values;
+//      keys > T are taken and the rest of the R come from keys == T in
+//      ascending index order;
+//   4. the R winners are sorted by (prob desc, index asc) with a bitonic network
+//      across lanes and register slots;
+//   5. their running mass is accumulated sequentially in fp64 and rounded to
+//      fp32 per element (ATen's CPU cumsum of fp32 accumulates in double), and
+//      the reference's count rule is applied.
+// torch.sort leaves the order of equal probabilities unspecified; lower index
+// first is used here.  That, and ulp-level exp/sum differences, are the only
+// ways a selection can differ from the CPU reference (near-ties).
+#include "fsi_common.h"
+
+using namespace fsi;
+
+namespace {
+
+constexpr int R_MAX = FSI_ROUTE_MAX_RANKED;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m, 64);
+  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m, 64);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Composite sort key: larger probability first, then lower index.
+__device__ __forceinline__ uint64_t comp_key(uint32_t key, uint32_t idx) {
+  return (static_cast<uint64_t>(key) << 32) | (0xffffffffu - idx);
+}
+__device__ __forceinline__ int32_t comp_index(uint64_t c) {
+  return static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(c));
+}
+__device__ __forceinline__ float comp_prob(uint64_t c) {
+  return __uint_as_float(static_cast<uint32_t>(c >> 32) - 1u);
+}
+
+// Bitonic sort (descending) of 64 * E composite keys; element k lives in lane
+// k % 64, slot k / 64.
+template <int E>
+__device__ __forceinline__ void bitonic_desc(uint64_t (&v)[E]) {
+  constexpr int n = 64 * E;
+  const int lane = lane_id();
+#pragma unroll
+  for (int s = 2; s <= n; s <<= 1) {
+#pragma unroll
+    for (int j = s >> 1; j > 0; j >>= 1) {
+      uint64_t nv[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int k = e * 64 + lane;
+        const int p = k ^ j;
+        const uint64_t other = j < 64 ? shfl_xor_u64(v[e], j) : v[(e * 64 ^ j) >> 6];
+        const bool want_max = (k < p) == ((k & s) == 0);
+        const uint64_t mx = v[e] > other ? v[e] : other;
+        const uint64_t mn = v[e] > other ? other : v[e];
+        nv[e] = want_max ? mx : mn;
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[e] = nv[e];
+    }
+  }
+}
+
+// Number of keys >= t in the row.
+template <int PL>
+__device__ __forceinline__ int count_ge(const uint32_t (&key)[PL], uint32_t t) {
+  int c = 0;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) c += key[i] >= t;
+  return wave_sum_i(c);
+}
+
+// The R largest keys (0 < R <= min(64 E, #candidates)), sorted descending into
+// out[] (element k at lane k % 64, slot k / 64); entries k >= R hold 0.
+// lds_k / lds_i: this wave's 64 E words each.
+template <int PL, int E>
+__device__ void rank_top(const uint32_t (&key)[PL], int R, uint64_t (&out)[E], uint32_t* lds_k, uint32_t* lds_i) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int e = 0; e < E; ++e) out[e] = 0;
+  if (R <= 0) return;
+  uint32_t mx = 0;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) mx = key[i] > mx ? key[i] : mx;
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t o = __shfl_xor(mx, off, 64);
+    mx = o > mx ? o : mx;
+  }
+  // Invariant: count_ge(lo) >= R > count_ge(hi).
+  uint32_t lo = 1, hi = mx + 1;
+  int clo = count_ge<PL>(key, lo);
+  while (clo != R && hi - lo > 1) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    const int c = count_ge<PL>(key, mid);
+    if (c >= R) {
+      lo = mid;
+      clo = c;
+    } else {
+      hi = mid;
+    }
+  }
+  const uint32_t T = lo;
+  // clo == R: take every key >= T.  Otherwise take keys > T, then keys == T by index.
+  const uint32_t strict = clo == R ? T : T + 1;
+  int base = 0;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const bool take = key[i] >= strict;
+    const uint64_t b = __ballot(take);
+    if (take) {
+      const int pos = base + lanes_below(b);
+      lds_k[pos] = key[i];
+      lds_i[pos] = static_cast<uint32_t>(i * 64 + lane);
+    }
+    base += __popcll(b);
+  }
+  if (base < R) {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const bool eq = key[i] == T;
+      const uint64_t b = __ballot(eq);
+      const int pos = base + lanes_below(b);
+      if (eq && pos < R) {
+        lds_k[pos] = key[i];
+        lds_i[pos] = static_cast<uint32_t>(i * 64 + lane);
+      }
+      base += __popcll(b);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int k = e * 64 + lane;
+    out[e] = k < R ? comp_key(lds_k[k], lds_i[k]) : 0;
+  }
+  bitonic_desc<E>(out);
+}
+
+// Running mass of the sorted probabilities for k < n; 0 elsewhere.
+//   fp32 rows: cum[k] = fp32(sum_{i<=k} p_i accumulated in fp64) (ATen CPU
+//              cumsum of float accumulates in double);
+//   bf16 rows: cum[k] = bf16(sum_{i<=k} p_i accumulated in fp32) (its
+//              accumulator for bfloat16 is float).
+template <int E, bool RB>
+__device__ __forceinline__ void running_mass(const uint64_t (&sorted)[E], int n, float (&cum)[E]) {
+  const int lane = lane_id();
+  double acc = 0.0;
+  float accf = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float p = comp_prob(sorted[e]);
+    cum[e] = 0.f;
+    const int m = n - e * 64 < 64 ? n - e * 64 : 64;
+    for (int l = 0; l < m; ++l) {
+      const float pl = __shfl(p, l, 64);
+      float c;
+      if (RB) {
+        accf += pl;
+        c = round_bf16(accf);
+      } else {
+        acc += static_cast<double>(pl);
+        c = static_cast<float>(acc);
+      }
+      if (lane == l) cum[e] = c;
+    }
+  }
+}
+
+// First k < n with cum[k] >= target, or n if there is none.
+template <int E>
+__device__ __forceinline__ int first_reaching(const float (&cum)[E], int n, float target) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const uint64_t b = __ballot(e * 64 + lane < n && cum[e] >= target);
+    if (b) return e * 64 + __ffsll(static_cast<long long>(b)) - 1;
+  }
+  return n;
+}
+
+// Value of a per-lane register array at element k (uniform k).
+template <int E>
+__device__ __forceinline__ float element_at(const float (&v)[E], int k) {
+  float r = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float x = __shfl(v[e], k & 63, 64);
+    if ((k >> 6) == e) r = x;
+  }
+  return r;
+}
+
+// Row masks of select_blocks (core.py:79-99): 0 = not complete, 1 = local, 2 = remote.
+__device__ __forceinline__ int mask_kind(int p, int qb, int causal, int lw) {
+  if (causal) {
+    if (p >= qb) return 0;
+    if (lw > 0) return p >= (qb - lw > 0 ? qb - lw : 0) ? 1 : 2;
+    return 2;
+  }
+  if (lw > 0) return p < lw ? 1 : 2;
+  return 2;
+}
+
+struct SelectParams {
+  int causal, local_window, capacity;
+  float top_p;
+  int k_min, k_max;
+  const float* top_p_rows;  // optional per-row values (B * Qb)
+  const int32_t* k_min_rows;
+  const int32_t* k_max_rows;
+};
+
+// select_blocks for one row whose scores (upcast to fp32) are s[] (slot
+// layout).  RB: the scores tensor is bf16, so masked_softmax returns bf16
+// probabilities and local mass, cumulative mass and target are bf16 values
+// (core.py:43,103,111 evaluated in bfloat16).  Writes indices[capacity], count
+// and (optionally) mass = local mass + cum[count-1].
+template <int PL, int E, bool RB>
+__device__ void select_row(float (&s)[PL], int N, int qb, int64_t row, const SelectParams& sp,
+                           int32_t* __restrict__ out_idx, int32_t* __restrict__ out_cnt,
+                           float* __restrict__ out_mass, uint32_t* lds_k, uint32_t* lds_i) {
+  const int lane = lane_id();
+  const float top_p = sp.top_p_rows ? sp.top_p_rows[row] : sp.top_p;
+  const int k_min = sp.k_min_rows ? sp.k_min_rows[row] : sp.k_min;
+  const int k_max = sp.k_max_rows ? sp.k_max_rows[row] : sp.k_max;
+
+  // masked_softmax over complete entries (core.py:36-43)
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int j = i * 64 + lane;
+    if (j < N && mask_kind(j, qb, sp.causal, sp.local_window)) mx = fmaxf(mx, s[i]);
+  }
+  mx = wave_max(mx);
+  if (!isfinite(mx)) mx = 0.0f;
+  float z = 0.f;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int j = i * 64 + lane;
+    s[i] = j < N && mask_kind(j, qb, sp.causal, sp.local_window) ? expf(s[i] - mx) : 0.0f;
+    z += s[i];
+  }
+  z = fmaxf(wave_sum(z), 1e-20f);
+  float lmass = 0.f;
+  int avail = 0;
+  uint32_t key[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int j = i * 64 + lane;
+    const int kind = j < N ? mask_kind(j, qb, sp.causal, sp.local_window) : 0;
+    float p = s[i] / z;
+    if (RB) p = round_bf16(p);
+    if (kind == 1) lmass += p;
+    key[i] = kind == 2 ? __float_as_uint(p) + 1u : 0u;
+    avail += kind == 2;
+  }
+  lmass = wave_sum(lmass);
+  if (RB) lmass = round_bf16(lmass);
+  avail = wave_sum_i(avail);
+
+  int R = k_max > sp.capacity ? k_max : sp.capacity;
+  R = R < avail ? R : avail;
+  R = R < 64 * E ? R : 64 * E;  // the host guarantees this does not truncate
+  uint64_t sorted[E];
+  rank_top<PL, E>(key, R, sorted, lds_k, lds_i);
+
+  // counts (core.py:107-119)
+  const float target = RB ? fmaxf(round_bf16(round_bf16(top_p) - lmass), 0.0f) : fmaxf(top_p - lmass, 0.0f);
+  int nr = k_max < avail ? k_max : avail;  // cum is only consulted below this rank
+  nr = nr < 0 ? 0 : nr;
+  nr = nr < R ? nr : R;
+  float cum[E];
+  running_mass<E, RB>(sorted, nr, cum);
+  int count;
+  if (avail <= 0) {
+    count = 0;
+  } else {
+    // needed = #(cum < target) + (target > 0); any value past nr caps to min(avail, K_max)
+    const int first = first_reaching<E>(cum, nr, target);
+    int needed = first >= nr ? 0x7fffffff : first + (target > 0.0f ? 1 : 0);
+    needed = needed > k_min ? needed : k_min;
+    count = needed < avail ? needed : avail;
+  }
+  count = count < k_max ? count : k_max;
+
+  // indices: ranked candidates, then the other entries in index order, then
+  // zero padding past N (sorted_idx[..., :capacity] padded, core.py:121-123).
+  int32_t* idx = out_idx + row * sp.capacity;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int k = e * 64 + lane;
+    if (k < R && k < sp.capacity) idx[k] = comp_index(sorted[e]);
+  }
+  if (sp.capacity > R) {
+    // R == avail here: the non-remote entries (ranked -1) follow, lowest index first
+    int base = R;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int j = i * 64 + lane;
+      const bool other = j < N && mask_kind(j, qb, sp.causal, sp.local_window) != 2;
+      const uint64_t b = __ballot(other);
+      const int pos = base + lanes_below(b);
+      if (other && pos < sp.capacity) idx[pos] = j;
+      base += __popcll(b);
+    }
+    for (int k = N + lane; k < sp.capacity; k += 64) idx[k] = 0;
+  }
+  const float ck = count > 0 ? element_at<E>(cum, count - 1) : 0.f;
+  if (lane == 0) {
+    out_cnt[row] = count;
+    if (out_mass) out_mass[row] = count > 0 ? (RB ? round_bf16(lmass + ck) : lmass + ck) : lmass;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// select_blocks on materialised scores (B, Qb, Nb): one wave per row.
+// ---------------------------------------------------------------------------
+constexpr int RS_WAVES = 4;
+
+template <int PL, int E, bool BF16>
+__global__ __launch_bounds__(64 * RS_WAVES) void route_scores_kernel(const void* __restrict__ scores,
+                                                                     int64_t n_rows, int Qb, int N,
+                                                                     SelectParams sp,
+                                                                     int32_t* __restrict__ out_idx,
+                                                                     int32_t* __restrict__ out_cnt,
+                                                                     float* __restrict__ out_mass) {
+  __shared__ uint32_t lk[RS_WAVES][64 * E], li[RS_WAVES][64 * E];
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RS_WAVES + wave;
+  if (row >= n_rows) return;  // whole wave leaves; no workgroup barrier follows
+  float s[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int j = i * 64 + lane;
+    if (BF16) s[i] = j < N ? bf16_to_f32(static_cast<const bf16_t*>(scores)[row * N + j]) : 0.f;
+    else s[i] = j < N ? static_cast<const float*>(scores)[row * N + j] : 0.f;
+  }
+  select_row<PL, E, BF16>(s, N, static_cast<int>(row % Qb), row, sp, out_idx, out_cnt, out_mass, lk[wave],
+                          li[wave]);
+}
+
+// ---------------------------------------------------------------------------
+// Fused fp32 cosine scoring + select_blocks (the indexer routing workload).
+// One query row per wave, SR_WAVES rows per workgroup.  Keys are staged through
+// LDS in chunks of SR_CHUNK: the workgroup L2-normalises the chunk into
+// component-major float4 planes, then every wave scores its row against the
+// chunk, each lane taking the keys of its own register slots.  The query is
+// normalised once and held in scalar registers.
+// q: (B, Q, 16), k: (N, 16) per batch entry at b * k_batch_stride elements.
+// ---------------------------------------------------------------------------
+constexpr int SR_WAVES = 8;
+constexpr int SR_CHUNK = 1024;
+constexpr int SR_D = 16;
+
+template <int PL, int E, bool BF16>
+__global__ __launch_bounds__(64 * SR_WAVES) void score_route_kernel(const void* __restrict__ q,
+                                                                    const void* __restrict__ k, int Q, int N,
+                                                                    int64_t k_batch_stride, float sqrt_d,
+                                                                    SelectParams sp,
+                                                                    int32_t* __restrict__ out_idx,
+                                                                    int32_t* __restrict__ out_cnt,
+                                                                    float* __restrict__ out_mass) {
+  __shared__ float4 kn[SR_D / 4][SR_CHUNK];
+  __shared__ float qn[SR_WAVES][SR_D];
+  __shared__ uint32_t lk[SR_WAVES][64 * E], li[SR_WAVES][64 * E];
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int b = blockIdx.y;
+  const int row_q = blockIdx.x * SR_WAVES + wave;
+
+  // query: x / max(||x||, 1e-12) in fp32 (F.normalize)
+  if (lane == 0) {
+    float v[SR_D];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < SR_D; ++c) {
+      float x = 0.f;
+      if (row_q < Q) {
+        const int64_t off = (static_cast<int64_t>(b) * Q + row_q) * SR_D + c;
+        x = BF16 ? bf16_to_f32(static_cast<const bf16_t*>(q)[off]) : static_cast<const float*>(q)[off];
+      }
+      v[c] = x;
+      ss = fmaf(x, x, ss);
+    }
+    const float nrm = fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+    for (int c = 0; c < SR_D; ++c) qn[wave][c] = v[c] / nrm;
+  }
+  __syncthreads();
+  float qa[SR_D];
+#pragma unroll
+  for (int c = 0; c < SR_D; ++c) qa[c] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(qn[wave][c])));
+
+  float sa[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) sa[i] = 0.f;
+  const char* kb = static_cast<const char*>(k) + static_cast<int64_t>(b) * k_batch_stride * (BF16 ? 2 : 4);
+  constexpr int SLOTS_PER_CHUNK = SR_CHUNK / 64;
+#pragma unroll
+  for (int ch = 0; ch < (PL + SLOTS_PER_CHUNK - 1) / SLOTS_PER_CHUNK; ++ch) {
+    if (ch * SR_CHUNK >= N) break;  // uniform
+    __syncthreads();                // previous chunk fully consumed
+    for (int t = threadIdx.x; t < SR_CHUNK; t += 64 * SR_WAVES) {
+      const int j = ch * SR_CHUNK + t;
+      float v[SR_D];
+      float ss = 0.f;
+      if (j < N) {
+        if (BF16) {
+          const u32x4_t* src = reinterpret_cast<const u32x4_t*>(reinterpret_cast<const bf16_t*>(kb) +
+                                                                 static_cast<int64_t>(j) * SR_D);
+          const u32x4_t a = src[0], c2 = src[1];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            v[2 * w] = lo_bf16(a[w]);
+            v[2 * w + 1] = hi_bf16(a[w]);
+            v[8 + 2 * w] = lo_bf16(c2[w]);
+            v[8 + 2 * w + 1] = hi_bf16(c2[w]);
+          }
+        } else {
+          const float4* src = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(kb) +
+                                                              static_cast<int64_t>(j) * SR_D);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float4 f = src[w];
+            v[4 * w] = f.x;
+            v[4 * w + 1] = f.y;
+            v[4 * w + 2] = f.z;
+            v[4 * w + 3] = f.w;
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < SR_D; ++c) ss = fmaf(v[c], v[c], ss);
+      } else {
+#pragma unroll
+        for (int c = 0; c < SR_D; ++c) v[c] = 0.f;
+      }
+      const float nrm = fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        kn[w][t] = make_float4(v[4 * w] / nrm, v[4 * w + 1] / nrm, v[4 * w + 2] / nrm, v[4 * w + 3] / nrm);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < SLOTS_PER_CHUNK; ++i) {
+      const int slot = ch * SLOTS_PER_CHUNK + i;
+      if (slot < PL) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float4 f = kn[w][i * 64 + lane];
+          acc = fmaf(qa[4 * w], f.x, acc);
+          acc = fmaf(qa[4 * w + 1], f.y, acc);
+          acc = fmaf(qa[4 * w + 2], f.z, acc);
+          acc = fmaf(qa[4 * w + 3], f.w, acc);
+        }
+        sa[slot] = acc / sqrt_d;
+      }
+    }
+  }
+  if (row_q < Q)
+    select_row<PL, E, false>(sa, N, row_q, static_cast<int64_t>(b) * Q + row_q, sp, out_idx, out_cnt, out_mass, lk[wave],
+                      li[wave]);
+}
+
+// ---------------------------------------------------------------------------
+// decode_step page routing (attention.py:313-337) and additive-stream context
+// (attention.py:369-376), one sequence per wave.
+//   qi: (B, d) 16-D query (dtype), kp: (B, P, d) fp32 page keys,
+//   vp: (B, P, d) page values (dtype); pages [0, completed) are complete.
+// Routing runs when completed > flp > 0 (flp = first local page): softmax over
+// pages [0, flp), count = max(K_min, min(#(cum < top_p) + 1, min(K_max, flp))),
+// at most flp.  The context is softmax over every completed page (probabilities
+// cast to vp's dtype) contracted with vp, in vp's dtype.
+// ---------------------------------------------------------------------------
+template <int PL, int E, bool BF16>
+__global__ __launch_bounds__(64) void decode_route_kernel(const void* __restrict__ qi, const float* __restrict__ kp,
+                                                          const void* __restrict__ vp, int P,
+                                                          const int32_t* __restrict__ pos_rows, int pos, int page,
+                                                          int window, int completed, float top_p, int k_min,
+                                                          int k_max, int cap, float sqrt_d,
+                                                          int32_t* __restrict__ out_pages,
+                                                          int32_t* __restrict__ out_cnt, void* __restrict__ out_ctx) {
+  __shared__ uint32_t lk[64 * E], li[64 * E];
+  const int lane = lane_id();
+  const int b = blockIdx.x;
+  const int mypos = pos_rows ? pos_rows[b] : pos;
+  const int local_start = mypos + 1 - window > 0 ? mypos + 1 - window : 0;
+  const int flp = local_start / page;
+
+  float qv[SR_D];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < SR_D; ++c) {
+    const int64_t off = static_cast<int64_t>(b) * SR_D + c;
+    qv[c] = BF16 ? bf16_to_f32(static_cast<const bf16_t*>(qi)[off]) : static_cast<const float*>(qi)[off];
+    ss = fmaf(qv[c], qv[c], ss);
+  }
+  const float nrm = fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+  for (int c = 0; c < SR_D; ++c) qv[c] = qv[c] / nrm;
+
+  float s[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int j = i * 64 + lane;
+    float acc = 0.f;
+    if (j < completed) {
+      const float4* kr = reinterpret_cast<const float4*>(kp + (static_cast<int64_t>(b) * P + j) * SR_D);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float4 f = kr[w];
+        acc = fmaf(qv[4 * w], f.x, acc);
+        acc = fmaf(qv[4 * w + 1], f.y, acc);
+        acc = fmaf(qv[4 * w + 2], f.z, acc);
+        acc = fmaf(qv[4 * w + 3], f.w, acc);
+      }
+    }
+    s[i] = acc / sqrt_d;
+  }
+
+  if (out_ctx) {
+    float ctx = 0.f;  // lane c < 16 accumulates context component c
+    if (completed > 0) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < PL; ++i)
+        if (i * 64 + lane < completed) mx = fmaxf(mx, s[i]);
+      mx = wave_max(mx);
+      float e[PL], z = 0.f;
+#pragma unroll
+      for (int i = 0; i < PL; ++i) {
+        e[i] = i * 64 + lane < completed ? expf(s[i] - mx) : 0.f;
+        z += e[i];
+      }
+      z = wave_sum(z);
+      float part[SR_D];
+#pragma unroll
+      for (int c = 0; c < SR_D; ++c) part[c] = 0.f;
+#pragma unroll
+      for (int i = 0; i < PL; ++i) {
+        const int j = i * 64 + lane;
+        if (j < completed) {
+          float p = e[i] / z;
+          const int64_t off = (static_cast<int64_t>(b) * P + j) * SR_D;
+          if (BF16) {
+            p = round_bf16(p);
+            const u32x4_t* vr = reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(vp) + off);
+            const u32x4_t a = vr[0], c2 = vr[1];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              part[2 * w] = fmaf(p, lo_bf16(a[w]), part[2 * w]);
+              part[2 * w + 1] = fmaf(p, hi_bf16(a[w]), part[2 * w + 1]);
+              part[8 + 2 * w] = fmaf(p, lo_bf16(c2[w]), part[8 + 2 * w]);
+              part[9 + 2 * w] = fmaf(p, hi_bf16(c2[w]), part[9 + 2 * w]);
+            }
+          } else {
+            const float4* vr = reinterpret_cast<const float4*>(static_cast<const float*>(vp) + off);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const float4 f = vr[w];
+              part[4 * w] = fmaf(p, f.x, part[4 * w]);
+              part[4 * w + 1] = fmaf(p, f.y, part[4 * w + 1]);
+              part[4 * w + 2] = fmaf(p, f.z, part[4 * w + 2]);
+              part[4 * w + 3] = fmaf(p, f.w, part[4 * w + 3]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < SR_D; ++c) {
+        const float t = wave_sum(part[c]);
+        if (lane == c) ctx = t;
+      }
+    }
+    if (lane < SR_D) {
+      const int64_t off = static_cast<int64_t>(b) * SR_D + lane;
+      if (BF16) static_cast<bf16_t*>(out_ctx)[off] = f32_to_bf16(ctx);
+      else static_cast<float*>(out_ctx)[off] = ctx;
+    }
+  }
+
+  int count = 0;
+  uint64_t sorted[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) sorted[e] = 0;
+  if (completed > flp && flp > 0) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PL; ++i)
+      if (i * 64 + lane < flp) mx = fmaxf(mx, s[i]);
+    mx = wave_max(mx);
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      s[i] = i * 64 + lane < flp ? expf(s[i] - mx) : 0.f;
+      z += s[i];
+    }
+    z = wave_sum(z);
+    uint32_t key[PL];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) key[i] = i * 64 + lane < flp ? __float_as_uint(s[i] / z) + 1u : 0u;
+    const int kcap = k_max < flp ? k_max : flp;  // k_max = min(K_max, first_local_page)
+    int R = kcap > k_min ? kcap : k_min;
+    R = R < flp ? R : flp;
+    R = R < cap ? R : cap;
+    rank_top<PL, E>(key, R, sorted, lk, li);
+    float cum[E];
+    running_mass<E, false>(sorted, R, cum);
+    const int first = first_reaching<E>(cum, R, top_p);
+    const int needed = first >= R ? 0x7fffffff : first + 1;  // #(cum < top_p) + 1
+    count = needed < kcap ? needed : kcap;
+    count = count > k_min ? count : k_min;
+    count = count < flp ? count : flp;  // sorted_idx[b, :needed] has flp entries
+    count = count < cap ? count : cap;
+  }
+  int32_t* pages = out_pages + static_cast<int64_t>(b) * cap;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int k = e * 64 + lane;
+    if (k < cap) pages[k] = k < count ? comp_index(sorted[e]) : -1;
+  }
+  for (int k = 64 * E + lane; k < cap; k += 64) pages[k] = -1;
+  if (lane == 0) out_cnt[b] = count;
+}
+
+// ---------------------------------------------------------------------------
+// masked_softmax (core.py:36-43): fp32 softmax over mask, masked entries 0,
+// all-masked rows 0, result in the scores' dtype.  One workgroup per row;
+// three passes over the row (max, sum, write), the later two from L2.
+// mask: uint8 with element strides (msb, msq, msn) over (B, Q, N).
+// ---------------------------------------------------------------------------
+constexpr int MS_THREADS = 256;
+
+__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  v = is_max ? wave_max(v) : wave_sum(v);
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < MS_THREADS / 64; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+  __syncthreads();
+  return r;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(MS_THREADS) void masked_softmax_kernel(const void* __restrict__ scores, int Q, int N,
+                                                                    const uint8_t* __restrict__ mask, int64_t msb,
+                                                                    int64_t msq, int64_t msn, void* __restrict__ out) {
+  __shared__ float red[MS_THREADS / 64];
+  const int q = blockIdx.x, b = blockIdx.y;
+  const int64_t row = static_cast<int64_t>(b) * Q + q;
+  const uint8_t* mrow = mask + b * msb + q * msq;
+  auto load = [&](int j) -> float {
+    return BF16 ? bf16_to_f32(static_cast<const bf16_t*>(scores)[row * N + j])
+                : static_cast<const float*>(scores)[row * N + j];
+  };
+  float mx = -INFINITY;
+  for (int j = threadIdx.x; j < N; j += MS_THREADS)
+    if (mrow[j * msn]) mx = fmaxf(mx, load(j));
+  mx = block_reduce(mx, red, true);
+  if (!isfinite(mx)) mx = 0.0f;
+  float z = 0.f;
+  for (int j = threadIdx.x; j < N; j += MS_THREADS)
+    if (mrow[j * msn]) z += expf(load(j) - mx);
+  z = fmaxf(block_reduce(z, red, false), 1e-20f);
+  for (int j = threadIdx.x; j < N; j += MS_THREADS) {
+    const float p = mrow[j * msn] ? expf(load(j) - mx) / z : 0.0f;
+    if (BF16) static_cast<bf16_t*>(out)[row * N + j] = f32_to_bf16(p);
+    else static_cast<float*>(out)[row * N + j] = p;
+  }
+}
+
+int pick_pl(int64_t n) {
+  const int pl = static_cast<int>((n + 63) / 64);
+  if (pl <= 4) return 4;
+  if (pl <= 16) return 16;
+  if (pl <= 32) return 32;
+  return 64;
+}
+
+int pick_e(int64_t r) { return r <= 64 ? 1 : 4; }
+
+#define FSI_DISPATCH_PL(PLV, ...) \
+  switch (PLV) {                  \
+    case 4: {                     \
+      constexpr int PL = 4;       \
+      __VA_ARGS__;                \
+    } break;                      \
+    case 16: {                    \
+      constexpr int PL = 16;      \
+      __VA_ARGS__;                \
+    } break;                      \
+    case 32: {                    \
+      constexpr int PL = 32;      \
+      __VA_ARGS__;                \
+    } break;                      \
+    default: {                    \
+      constexpr int PL = 64;      \
+      __VA_ARGS__;                \
+    } break;                      \
+  }
+
+#define FSI_DISPATCH_E(EV, ...) \
+  if ((EV) == 1) {              \
+    constexpr int E = 1;        \
+    __VA_ARGS__;                \
+  } else {                      \
+    constexpr int E = 4;        \
+    __VA_ARGS__;                \
+  }
+
+}  // namespace
+
+extern "C" {
+
+FSI_API int fsi_route_from_scores(const void* scores, int dtype, int64_t B, int64_t Qb, int64_t Nb, int causal,
+                                  int local_window_blocks, float top_p, int k_min, int k_max, int capacity,
+                                  const float* top_p_rows, const int32_t* k_min_rows, const int32_t* k_max_rows,
+                                  int k_max_bound, int32_t* out_indices, int32_t* out_counts, float* out_mass,
+                                  void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "route_from_scores: dtype %d",
+                dtype);
+  FSI_CHECK_ARG(B >= 0 && Qb >= 0 && Nb >= 0 && capacity >= 0 && local_window_blocks >= 0, FSI_ERR_SHAPE,
+                "route_from_scores: negative size");
+  FSI_CHECK_ARG(Nb <= FSI_ROUTE_MAX_BLOCKS, FSI_ERR_CAPACITY, "route_from_scores: %lld blocks per row > %d",
+                (long long)Nb, FSI_ROUTE_MAX_BLOCKS);
+  const int kmax_all = k_max_rows ? k_max_bound : k_max;
+  int64_t want = kmax_all > capacity ? kmax_all : capacity;
+  want = want < Nb ? want : Nb;
+  FSI_CHECK_ARG(want <= R_MAX, FSI_ERR_CAPACITY,
+                "route_from_scores: min(max(K_max, capacity), blocks) = %lld > %d ranked candidates", (long long)want,
+                R_MAX);
+  const int64_t rows = B * Qb;
+  if (rows == 0) return FSI_OK;
+  FSI_CHECK_ARG(rows <= (int64_t)0x7fffffff * RS_WAVES, FSI_ERR_SHAPE, "route_from_scores: too many rows");
+  FSI_CHECK_ARG(scores && out_indices && out_counts, FSI_ERR_INVALID_ARG, "route_from_scores: null pointer");
+  SelectParams sp{causal, local_window_blocks, capacity, top_p, k_min, k_max, top_p_rows, k_min_rows, k_max_rows};
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((rows + RS_WAVES - 1) / RS_WAVES));
+  FSI_DISPATCH_PL(pick_pl(Nb), FSI_DISPATCH_E(pick_e(want), {
+    if (dtype == FSI_DTYPE_BF16)
+      route_scores_kernel<PL, E, true><<<grid, 64 * RS_WAVES, 0, st>>>(scores, rows, (int)Qb, (int)Nb, sp,
+                                                                      out_indices, out_counts, out_mass);
+    else
+      route_scores_kernel<PL, E, false><<<grid, 64 * RS_WAVES, 0, st>>>(scores, rows, (int)Qb, (int)Nb, sp,
+                                                                       out_indices, out_counts, out_mass);
+  }))
+  FSI_HIP_LAUNCH_CHECK("route_from_scores");
+  return FSI_OK;
+}
+
+FSI_API int fsi_score_and_route(const void* q, const void* k, int dtype, int64_t B, int64_t Q,
+                                int64_t N, int64_t index_dim, int64_t k_batch_stride, int causal,
+                                int local_window_blocks, float top_p, int k_min, int k_max, int capacity,
+                                int32_t* out_indices, int32_t* out_counts, float* out_mass, void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "score_and_route: dtype %d", dtype);
+  FSI_CHECK_ARG(index_dim == SR_D, FSI_ERR_SHAPE, "score_and_route: index_dim %lld != %d", (long long)index_dim,
+                SR_D);
+  FSI_CHECK_ARG(B >= 0 && Q >= 0 && N >= 0 && capacity >= 0 && local_window_blocks >= 0 && k_batch_stride >= 0,
+                FSI_ERR_SHAPE, "score_and_route: negative size");
+  FSI_CHECK_ARG(N <= FSI_SCORE_ROUTE_MAX_KEYS, FSI_ERR_CAPACITY, "score_and_route: %lld keys > %d", (long long)N,
+                FSI_SCORE_ROUTE_MAX_KEYS);
+  int64_t want = k_max > capacity ? k_max : capacity;
+  want = want < N ? want : N;
+  FSI_CHECK_ARG(want <= R_MAX, FSI_ERR_CAPACITY, "score_and_route: min(max(K_max, capacity), keys) = %lld > %d",
+                (long long)want, R_MAX);
+  if (B == 0 || Q == 0) return FSI_OK;
+  FSI_CHECK_ARG(B <= 65535 && Q <= (int64_t)0x7fffffff, FSI_ERR_SHAPE, "score_and_route: grid too large");
+  FSI_CHECK_ARG(q && k && out_indices && out_counts, FSI_ERR_INVALID_ARG, "score_and_route: null pointer");
+  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                    (k_batch_stride * (dtype == FSI_DTYPE_BF16 ? 2 : 4)) % 16 == 0,
+                FSI_ERR_ALIGN, "score_and_route: keys must be 16-byte aligned");
+  SelectParams sp{causal, local_window_blocks, capacity, top_p, k_min, k_max, nullptr, nullptr, nullptr};
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((Q + SR_WAVES - 1) / SR_WAVES), static_cast<unsigned>(B));
+  const float sqrt_d = static_cast<float>(sqrt(static_cast<double>(index_dim)));
+  int pl = pick_pl(N);
+  pl = pl < 16 ? 16 : pl;
+  FSI_DISPATCH_PL(pl, FSI_DISPATCH_E(pick_e(want), {
+    if constexpr (PL >= 16) {
+      if (dtype == FSI_DTYPE_BF16)
+        score_route_kernel<PL, E, true><<<grid, 64 * SR_WAVES, 0, st>>>(q, k, (int)Q, (int)N, k_batch_stride, sqrt_d,
+                                                                       sp, out_indices, out_counts, out_mass);
+      else
+        score_route_kernel<PL, E, false><<<grid, 64 * SR_WAVES, 0, st>>>(q, k, (int)Q, (int)N, k_batch_stride,
+                                                                        sqrt_d, sp, out_indices, out_counts, out_mass);
+    }
+  }))
+  FSI_HIP_LAUNCH_CHECK("score_and_route");
+  return FSI_OK;
+}
+
+FSI_API int fsi_decode_route(const void* qi, const float* kp, const void* vp, int dtype, int64_t B, int64_t P,
+                             int64_t index_dim, const int32_t* pos_rows, int64_t pos, int64_t page_size,
+                             int64_t window, int64_t completed_pages, float top_p, int k_min, int k_max,
+                             int capacity, int32_t* out_pages, int32_t* out_counts, void* out_context,
+                             void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "decode_route: dtype %d", dtype);
+  FSI_CHECK_ARG(index_dim == SR_D, FSI_ERR_SHAPE, "decode_route: index_dim %lld != %d", (long long)index_dim, SR_D);
+  FSI_CHECK_ARG(B >= 0 && P >= 0 && page_size > 0 && window >= 0 && pos >= 0 && completed_pages >= 0 &&
+                    completed_pages <= P && pos < (int64_t)0x7fffffff,
+                FSI_ERR_SHAPE, "decode_route: inconsistent sizes");
+  FSI_CHECK_ARG(completed_pages <= FSI_ROUTE_MAX_BLOCKS, FSI_ERR_CAPACITY, "decode_route: %lld pages > %d",
+                (long long)completed_pages, FSI_ROUTE_MAX_BLOCKS);
+  FSI_CHECK_ARG(capacity >= 0 && capacity <= R_MAX, FSI_ERR_CAPACITY, "decode_route: capacity %d > %d", capacity,
+                R_MAX);
+  if (B == 0) return FSI_OK;
+  FSI_CHECK_ARG(B <= (int64_t)0x7fffffff, FSI_ERR_SHAPE, "decode_route: batch too large");
+  FSI_CHECK_ARG(qi && kp && out_pages && out_counts && (vp || !out_context), FSI_ERR_INVALID_ARG,
+                "decode_route: null pointer");
+  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(kp) % 16 == 0 &&
+                    (!out_context || reinterpret_cast<uintptr_t>(vp) % 16 == 0),
+                FSI_ERR_ALIGN, "decode_route: page keys/values must be 16-byte aligned");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const float sqrt_d = static_cast<float>(sqrt(static_cast<double>(index_dim)));
+  int64_t want = k_max > k_min ? k_max : k_min;
+  want = want < capacity ? want : capacity;
+  const int win = static_cast<int>(window < 0x7fffffff ? window : 0x7fffffff);
+  FSI_DISPATCH_PL(pick_pl(completed_pages), FSI_DISPATCH_E(pick_e(want), {
+    if (dtype == FSI_DTYPE_BF16)
+      decode_route_kernel<PL, E, true><<<(unsigned)B, 64, 0, st>>>(
+          qi, kp, vp, (int)P, pos_rows, (int)pos, (int)page_size, win, (int)completed_pages, top_p, k_min, k_max,
+          capacity, sqrt_d, out_pages, out_counts, out_context);
+    else
+      decode_route_kernel<PL, E, false><<<(unsigned)B, 64, 0, st>>>(
+          qi, kp, vp, (int)P, pos_rows, (int)pos, (int)page_size, win, (int)completed_pages, top_p, k_min, k_max,
+          capacity, sqrt_d, out_pages, out_counts, out_context);
+  }))
+  FSI_HIP_LAUNCH_CHECK("decode_route");
+  return FSI_OK;
+}
+
+FSI_API int fsi_masked_softmax(const void* scores, int dtype, int64_t B, int64_t Q, int64_t N, const uint8_t* mask,
+                               int64_t mask_stride_b, int64_t mask_stride_q, int64_t mask_stride_n, void* out,
+                               void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "masked_softmax: dtype %d", dtype);
+  FSI_CHECK_ARG(B >= 0 && Q >= 0 && N >= 0, FSI_ERR_SHAPE, "masked_softmax: negative size");
+  if (B == 0 || Q == 0 || N == 0) return FSI_OK;
+  FSI_CHECK_ARG(B <= 65535 && Q <= (int64_t)0x7fffffff && N <= (int64_t)0x7fffffff, FSI_ERR_SHAPE,
+                "masked_softmax: grid too large");
+  FSI_CHECK_ARG(scores && mask && out, FSI_ERR_INVALID_ARG, "masked_softmax: null pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(Q), static_cast<unsigned>(B));
+  if (dtype == FSI_DTYPE_BF16)
+    masked_softmax_kernel<true><<<grid, MS_THREADS, 0, st>>>(scores, (int)Q, (int)N, mask, mask_stride_b,
+                                                             mask_stride_q, mask_stride_n, out);
+  else
+    masked_softmax_kernel<false><<<grid, MS_THREADS, 0, st>>>(scores, (int)Q, (int)N, mask, mask_stride_b,
+                                                              mask_stride_q, mask_stride_n, out);
+  FSI_HIP_LAUNCH_CHECK("masked_softmax");
+  return FSI_OK;
+}
+
+}  // extern "C"

@@ -128,6 +128,103 @@ FSI_API int fsi_mlp_router(const void* x, int64_t ldx, int64_t M, int64_t D, con
                            int64_t remote_blocks, float score_scale, int dtype, int32_t* out_active,
                            float* out_scores, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------- *
+ * 16-D indexer routing.
+ * Selection semantics (every entry point below): fp32 masked softmax over the
+ * complete entries, remote candidates ranked by probability (equal
+ * probabilities: lower index first), running mass accumulated in fp64 and
+ * rounded to fp32 per rank, and
+ *   target = max(top_p - local_mass, 0)
+ *   needed = #(cum < target) + (target > 0); max(needed, K_min) if any remote
+ *   count  = min(needed, available, K_max)
+ * ------------------------------------------------------------------------- */
+#define FSI_ROUTE_MAX_BLOCKS 4096      /* blocks (or pages) per routed row           */
+#define FSI_SCORE_ROUTE_MAX_KEYS 4096  /* keys per row of fsi_score_and_route        */
+#define FSI_ROUTE_MAX_RANKED 256       /* bound on min(max(K_max, capacity), blocks) */
+
+/* masked_softmax (foveal_indexer/core.py:36-43): fp32 softmax of scores over
+ * the entries where mask != 0, masked entries exactly 0, rows without a valid
+ * entry all 0, written in the scores' dtype.  scores/out: contiguous (B, Q, N);
+ * mask: uint8 with element strides over (B, Q, N) (0 = broadcast). */
+FSI_API int fsi_masked_softmax(const void* scores, int dtype, int64_t B, int64_t Q, int64_t N, const uint8_t* mask,
+                               int64_t mask_stride_b, int64_t mask_stride_q, int64_t mask_stride_n, void* out,
+                               void* stream);
+
+/* select_blocks on materialised scores
+ * (foveal_indexer/core.py:46-160, via FovealIndexer.route core.py:268-286).
+ * scores: (B, Qb, Nb) contiguous fp32 or bf16 (upcast to fp32 first).
+ * Masks: causal -> complete = p < q, local = the local_window_blocks blocks
+ * before q; non-causal -> every block complete, local = p < local_window_blocks.
+ * top_p / k_min / k_max apply to every row unless the matching *_rows array
+ * (B*Qb values, device memory) is given; with k_max_rows, k_max_bound must be
+ * >= every value in it.
+ * out_indices (B, Qb, capacity) int32: remote blocks in rank order, then the
+ * non-remote blocks in index order, then zeros past Nb (core.py:121-123).
+ * out_counts (B, Qb) int32; out_mass (optional, B*Qb fp32) = local mass +
+ * cumulative remote mass of the selected blocks. */
+FSI_API int fsi_route_from_scores(const void* scores, int dtype, int64_t B, int64_t Qb, int64_t Nb, int causal,
+                                  int local_window_blocks, float top_p, int k_min, int k_max, int capacity,
+                                  const float* top_p_rows, const int32_t* k_min_rows, const int32_t* k_max_rows,
+                                  int k_max_bound, int32_t* out_indices, int32_t* out_counts, float* out_mass,
+                                  void* stream);
+
+/* Fused cosine scoring + select_blocks: scores = normalize(q) . normalize(k) /
+ * sqrt(index_dim), all in fp32 (the fp32 form of FovealIndexer.compute_block_scores,
+ * foveal_indexer/core.py:254-266), never materialised.  q: (B, Q, 16) and k: (N, 16)
+ * per batch entry at element offset b * k_batch_stride (0 = shared keys), both
+ * of `dtype`, k 16-byte aligned.  Outputs as fsi_route_from_scores; the query
+ * row index is the query block index of the causal mask. */
+FSI_API int fsi_score_and_route(const void* q, const void* k, int dtype, int64_t B, int64_t Q,
+                                int64_t N, int64_t index_dim, int64_t k_batch_stride, int causal,
+                                int local_window_blocks, float top_p, int k_min, int k_max, int capacity,
+                                int32_t* out_indices, int32_t* out_counts, float* out_mass, void* stream);
+
+/* decode_step remote-page routing and additive-stream context
+ * (foveal_indexer/attention.py:313-337,369-376), one sequence per row.
+ * qi: (B, 16) in dtype; kp: (B, P, 16) fp32 page keys; vp: (B, P, 16) in dtype.
+ * Position per sequence: pos_rows[b] (device int32) or pos for all.
+ * first_local_page = max(0, pos + 1 - window) / page_size; routes only when
+ * completed_pages > first_local_page > 0, over pages [0, first_local_page):
+ * count = min(max(K_min, min(#(cum < top_p) + 1, min(K_max, first_local_page))),
+ * first_local_page).  out_pages (B, capacity) int32: page ids in rank order, -1
+ * past count (capacity >= max(K_max, K_min) returns every selected page).
+ * out_context (optional, (B, 16) in dtype): softmax over all completed pages
+ * (probabilities cast to dtype) times vp. */
+FSI_API int fsi_decode_route(const void* qi, const float* kp, const void* vp, int dtype, int64_t B, int64_t P,
+                             int64_t index_dim, const int32_t* pos_rows, int64_t pos, int64_t page_size,
+                             int64_t window, int64_t completed_pages, float top_p, int k_min, int k_max,
+                             int capacity, int32_t* out_pages, int32_t* out_counts, void* out_context,
+                             void* stream);
+
+/* ------------------------------------------------------------------------- *
+ * FovealIndexer representations (foveal_indexer/core.py:214-312), index_dim 16.
+ * The D -> 16 projections are plain GEMMs done by the caller; these entry
+ * points apply everything after them with the reference's bf16 rounding points.
+ * All tensors contiguous and of `dtype`.
+ * ------------------------------------------------------------------------- */
+/* F.rms_norm over the 16 components (eps = FLT_EPSILON), x/out: (M, 16).
+ * Replaces the norm of compute_query_16d (core.py:221-222) and of decode_step's
+ * index key (attention.py:305). */
+FSI_API int fsi_index_rms_norm(const void* x, int dtype, int64_t M, int64_t index_dim, void* out, void* stream);
+
+/* compute_kv_blocks_16d after the projections (core.py:241-250):
+ * k_blocks = normalize(mean_block(rms_norm(k_lin))), v_blocks = mean_block(v_lin).
+ * k_lin/v_lin: (B, N, 16); k_blocks/v_blocks: (B, N / block_size, 16). */
+FSI_API int fsi_index_pool_kv(const void* k_lin, const void* v_lin, int dtype, int64_t B, int64_t N,
+                              int64_t index_dim, int64_t block_size, void* k_blocks, void* v_blocks, void* stream);
+
+/* compute_block_scores (core.py:254-266): normalize(q) . normalize(k) / sqrt(16)
+ * with the operands rounded to dtype after normalising and the product rounded
+ * before the division.  q: (B, Q, 16); k: (B, N, 16); out: (B, Q, N). */
+FSI_API int fsi_block_scores(const void* q, const void* k, int dtype, int64_t B, int64_t Q, int64_t N,
+                             int64_t index_dim, void* out, void* stream);
+
+/* additive_stream up to the output projection (core.py:288-310):
+ * context = masked_softmax(scores, causal ? p < q : all) . v_blocks, probabilities
+ * rounded to dtype.  scores: (B, Q, N); v_blocks: (B, N, 16); context: (B, Q, 16). */
+FSI_API int fsi_additive_context(const void* scores, const void* v_blocks, int dtype, int64_t B, int64_t Q,
+                                 int64_t N, int64_t index_dim, int causal, void* context, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

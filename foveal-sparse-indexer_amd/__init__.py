@@ -25,7 +25,7 @@ from .core import (
     score_and_route,
     select_blocks,
 )
-from .attention import decode_route
+from .attention import FovealKVCache, FovealSparseAttention, decode_attention, decode_route
 from .foveal_pattention import (
     FovealPattentionMLP,
     mlp_pooled_route,
@@ -41,6 +41,9 @@ __all__ = [
     "index_rms_norm",
     "FovealIndexer",
     "decode_route",
+    "decode_attention",
+    "FovealKVCache",
+    "FovealSparseAttention",
     "FovealPattentionMLP",
     "sparsify_model_with_foveal_pattention",
     "mlp_pooled_route",

@@ -8,12 +8,15 @@ a host sync per sequence).
 """
 from __future__ import annotations
 
-from typing import Optional
+import math
+from typing import Any, Dict, List, Optional, Tuple
 
 import torch
-from torch import Tensor
+import torch.nn.functional as F
+from torch import Tensor, nn
 
 from . import _lib
+from .core import FovealIndexer, index_rms_norm
 
 
 def decode_route(
@@ -76,3 +79,291 @@ def decode_route(
     if return_context:
         return pages, counts, ctx
     return pages, counts
+
+
+PAGE_SIZE = 64
+
+
+class FovealKVCache:
+    """Paged KV cache for foveal decoding (drop-in for attention.py:22-94).
+
+    Same constructor, `update` and public state (`kp_cache`, `vp_cache`,
+    `partial_kp`, `partial_vp`, `seq_len`, `completed_pages`) as the reference.
+    The full-rank cache is paged instead of contiguous: `k_cache` / `v_cache`
+    are physical page pools in the MFMA-tile layouts of include/fsi.h, and
+    `page_table` (B, max_pages) maps each sequence's logical pages to them
+    (sequence b owns pages [b * max_pages, (b + 1) * max_pages) unless a
+    caller-built table is installed).  `to_dense()` / `load_dense()` convert
+    to and from the reference's (B, Hkv, S, hd) layout.  bf16 only; page_size 64.
+    """
+
+    def __init__(
+        self,
+        batch_size: int,
+        max_seq_len: int,
+        num_kv_heads: int,
+        head_dim: int,
+        index_dim: int,
+        page_size: int,
+        device: torch.device,
+        dtype: torch.dtype = torch.bfloat16,
+        n_phys_pages: Optional[int] = None,
+        page_table: Optional[Tensor] = None,
+    ):
+        if page_size != PAGE_SIZE:
+            raise ValueError(f"FovealKVCache: page_size {page_size} unsupported (the HIP path uses {PAGE_SIZE})")
+        if dtype != torch.bfloat16:
+            raise TypeError(f"FovealKVCache: dtype {dtype} unsupported (bfloat16 only on the MI355X path)")
+        if head_dim not in (64, 128):
+            raise ValueError(f"FovealKVCache: head_dim {head_dim} unsupported (64 or 128)")
+        self.batch_size = batch_size
+        self.max_seq_len = max_seq_len
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.index_dim = index_dim
+        self.page_size = page_size
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.max_pages = -(-max_seq_len // page_size)
+        if page_table is None:
+            page_table = torch.arange(batch_size * self.max_pages, dtype=torch.int32).view(batch_size, self.max_pages)
+        self.page_table = page_table.to(device=self.device, dtype=torch.int32).contiguous()
+        if tuple(self.page_table.shape) != (batch_size, self.max_pages):
+            raise ValueError(f"FovealKVCache: page table {tuple(self.page_table.shape)} != "
+                             f"{(batch_size, self.max_pages)}")
+        self.n_phys_pages = int(n_phys_pages) if n_phys_pages is not None else batch_size * self.max_pages
+        per_page = num_kv_heads * page_size * head_dim
+        self.k_cache = torch.zeros(self.n_phys_pages, per_page, device=self.device, dtype=dtype)
+        self.v_cache = torch.zeros(self.n_phys_pages, per_page, device=self.device, dtype=dtype)
+        self.kp_cache = torch.zeros(batch_size, self.max_pages, index_dim, device=self.device, dtype=torch.float32)
+        self.vp_cache = torch.zeros(batch_size, self.max_pages, index_dim, device=self.device, dtype=dtype)
+        self.partial_kp = torch.zeros(batch_size, page_size, index_dim, device=self.device, dtype=dtype)
+        self.partial_vp = torch.zeros(batch_size, page_size, index_dim, device=self.device, dtype=dtype)
+        self.seq_len = 0
+        self.completed_pages = 0
+
+    def _write(self, k: Tensor, v: Tensor, start: int) -> None:
+        what = "FovealKVCache"
+        B, H, n, hd = k.shape
+        if (B, H, hd) != (self.batch_size, self.num_kv_heads, self.head_dim) or v.shape != k.shape:
+            raise ValueError(f"{what}: K {tuple(k.shape)} / V {tuple(v.shape)} do not match the cache")
+        if k.dtype != self.dtype or v.dtype != self.dtype:
+            raise TypeError(f"{what}: K/V dtype {k.dtype}/{v.dtype} != {self.dtype}")
+        if k.stride(-1) != 1:
+            k = k.contiguous()
+        if v.stride(-1) != 1:
+            v = v.contiguous()
+        dev = _lib.require_gpu(k, v, self.k_cache, what=what)
+        err = _lib.error_word(dev)
+        st = _lib.lib().fsi_kv_write(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2), v.stride(0),
+                                     v.stride(1), v.stride(2), B, H, n, hd, None, start, self.page_table.data_ptr(),
+                                     self.max_pages, self.n_phys_pages, self.k_cache.data_ptr(),
+                                     self.v_cache.data_ptr(), err.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        if _lib.checks_enabled():
+            _lib.raise_device_errors(dev, what)
+
+    def update(self, k_step: Tensor, v_step: Tensor, ki_step: Tensor, vi_step: Tensor) -> int:
+        """Append one token's KV and 16-D index representation (attention.py:62-94)."""
+        pos = self.seq_len
+        if pos >= self.max_seq_len:
+            raise RuntimeError(f"KV cache capacity {self.max_seq_len} exceeded.")
+        self._write(k_step, v_step, pos)
+        offset = pos % self.page_size
+        page = pos // self.page_size
+        self.partial_kp[:, offset] = ki_step.reshape(self.batch_size, self.index_dim)
+        self.partial_vp[:, offset] = vi_step.reshape(self.batch_size, self.index_dim)
+        if offset == self.page_size - 1:
+            dev = self.kp_cache.device
+            st = _lib.lib().fsi_kv_page_pool(
+                self.partial_kp.data_ptr(), self.partial_vp.data_ptr(), _lib.dtype_code(self.dtype, "kv_page_pool"),
+                self.batch_size, self.page_size, self.index_dim, self.kp_cache[:, page].data_ptr(),
+                self.vp_cache[:, page].data_ptr(), self.max_pages * self.index_dim, _lib.stream_handle(dev))
+            _lib.check(st, "FovealKVCache.update")
+            self.completed_pages += 1
+        self.seq_len += 1
+        return pos
+
+    def load_dense(self, k: Tensor, v: Tensor, start: int = 0) -> None:
+        """Write (B, Hkv, n, hd) K/V at positions start .. start + n - 1 (the
+        reference layout) without touching the 16-D page state."""
+        self._write(k, v, start)
+
+    def to_dense(self, n_tok: Optional[int] = None):
+        """(K, V) of positions [0, n_tok) in the reference layout (B, Hkv, n, hd)."""
+        n = self.seq_len if n_tok is None else int(n_tok)
+        shape = (self.batch_size, self.num_kv_heads, n, self.head_dim)
+        k = torch.empty(shape, dtype=self.dtype, device=self.k_cache.device)
+        v = torch.empty_like(k)
+        st = _lib.lib().fsi_kv_read(self.k_cache.data_ptr(), self.v_cache.data_ptr(), self.batch_size,
+                                    self.num_kv_heads, n, self.head_dim, self.page_table.data_ptr(), self.max_pages,
+                                    self.n_phys_pages, k.data_ptr(), v.data_ptr(),
+                                    _lib.stream_handle(self.k_cache.device))
+        _lib.check(st, "FovealKVCache.to_dense")
+        return k, v
+
+
+def decode_attention(
+    q: Tensor,
+    cache: FovealKVCache,
+    *,
+    pos: int | Tensor,
+    window: int,
+    remote_pages: Optional[Tensor],
+    remote_counts: Optional[Tensor],
+    scale: float,
+    out: Optional[Tensor] = None,
+) -> Tensor:
+    """softmax(scale q K^T) V over [max(0, pos + 1 - window), pos] plus the
+    selected remote pages, for every sequence and query head (attention.py:339-365).
+    q: (B, Hq, hd) or (B, Hq, 1, hd) bf16.  Returns (B, Hq, hd) bf16."""
+    what = "decode_attention"
+    dev = _lib.require_gpu(q, cache.k_cache, what=what)
+    B = q.shape[0]
+    Hq, hd = q.shape[1], q.shape[-1]
+    q3 = q.reshape(B, Hq, hd).contiguous()
+    if q3.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: q dtype {q3.dtype} unsupported (bfloat16)")
+    if B != cache.batch_size or hd != cache.head_dim:
+        raise ValueError(f"{what}: q {tuple(q.shape)} does not match the cache")
+    pos_rows, pos_val = None, 0
+    if isinstance(pos, Tensor):
+        pos_rows = pos.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+    else:
+        pos_val = int(pos)
+    cap = 0
+    if remote_pages is not None and remote_pages.numel():
+        remote_pages = remote_pages.to(device=dev, dtype=torch.int32).contiguous()
+        remote_counts = remote_counts.to(device=dev, dtype=torch.int32).contiguous()
+        cap = remote_pages.shape[-1]
+    if out is None:
+        out = torch.empty((B, Hq, hd), dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    ws = _lib.workspace(dev, L.fsi_decode_attn_workspace_size(B, Hq, cache.num_kv_heads, hd, window, cap,
+                                                               cache.max_pages), stream)
+    err = _lib.error_word(dev)
+    st = L.fsi_decode_attn(q3.data_ptr(), cache.k_cache.data_ptr(), cache.v_cache.data_ptr(),
+                           cache.page_table.data_ptr(), cache.max_pages, cache.n_phys_pages, _lib.ptr(pos_rows),
+                           pos_val, int(window), _lib.ptr(remote_pages) if cap else None,
+                           _lib.ptr(remote_counts) if cap else None, cap, B, Hq, cache.num_kv_heads, hd, float(scale),
+                           out.data_ptr(), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+    return out
+
+
+class FovealSparseAttention(nn.Module):
+    """Causal foveal sparse attention (attention.py:97-379): same constructor,
+    parameters (state_dict compatible), `init_kv_cache` and `decode_step`.
+
+    decode_step runs on the MI355X path: 16-D index projections + norm, paged
+    cache append, page routing + additive-stream context in one launch, and
+    split-K paged attention over the local window plus the selected pages.
+    Every sequence attends its own selected pages; the reference attends
+    sequence 0's pages for all sequences (attention.py:348) and
+    `reference_batch0_pages = True` reproduces that.  `selected_remote_pages`
+    reports each sequence's own selection in both modes, as the reference does.
+    The prefill `forward` is not on the MI355X path yet and raises.
+    """
+
+    def __init__(
+        self,
+        hidden_size: int,
+        num_heads: int,
+        num_kv_heads: Optional[int] = None,
+        head_dim: Optional[int] = None,
+        page_size: int = 64,
+        local_window_blocks: int = 4,
+        index_dim: int = 16,
+        top_p: float = 0.95,
+        min_remote_pages: int = 0,
+        max_remote_pages: int = 8,
+        remote_capacity: int = 8,
+        use_additive_stream: bool = True,
+    ):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads if num_kv_heads is not None else num_heads
+        self.head_dim = head_dim if head_dim is not None else hidden_size // num_heads
+        self.page_size = page_size
+        self.local_window_blocks = local_window_blocks
+        self.local_window = local_window_blocks * page_size
+        self.use_additive_stream = use_additive_stream
+        self.groups = self.num_heads // self.num_kv_heads
+        self.scale = 1.0 / math.sqrt(self.head_dim)
+        self.reference_batch0_pages = False
+
+        self.q_proj = nn.Linear(hidden_size, self.num_heads * self.head_dim, bias=False)
+        self.k_proj = nn.Linear(hidden_size, self.num_kv_heads * self.head_dim, bias=False)
+        self.v_proj = nn.Linear(hidden_size, self.num_kv_heads * self.head_dim, bias=False)
+        self.out_proj = nn.Linear(self.num_heads * self.head_dim, hidden_size, bias=False)
+        self.indexer = FovealIndexer(
+            hidden_size=hidden_size,
+            index_dim=index_dim,
+            block_size=page_size,
+            local_window_blocks=local_window_blocks,
+            top_p=top_p,
+            min_remote_blocks=min_remote_pages,
+            max_remote_blocks=max_remote_pages,
+            remote_capacity=remote_capacity,
+            causal=True,
+            use_additive_stream=use_additive_stream,
+        )
+
+    def forward(self, x: Tensor, compute_teacher_loss: bool = False) -> Tuple[Tensor, Dict[str, Any]]:
+        raise NotImplementedError(
+            "FovealSparseAttention.forward (prefill) is not on the MI355X path; decode_step is"
+        )
+
+    def init_kv_cache(self, batch_size: int, max_seq_len: int, device: torch.device) -> FovealKVCache:
+        """A paged cache for decoding (attention.py:271-282)."""
+        return FovealKVCache(
+            batch_size=batch_size,
+            max_seq_len=max_seq_len,
+            num_kv_heads=self.num_kv_heads,
+            head_dim=self.head_dim,
+            index_dim=self.indexer.index_dim,
+            page_size=self.page_size,
+            device=device,
+            dtype=self.q_proj.weight.dtype,
+        )
+
+    def decode_step(self, x_step: Tensor, kv_cache: FovealKVCache) -> Tuple[Tensor, Dict[str, Any]]:
+        """One autoregressive step for every sequence (attention.py:284-379)."""
+        batch, seq_one, _ = x_step.shape
+        if seq_one != 1:
+            raise ValueError("decode_step processes one token at a time")
+        pos = kv_cache.seq_len
+        q = self.q_proj(x_step).view(batch, self.num_heads, self.head_dim)
+        k = self.k_proj(x_step).view(batch, self.num_kv_heads, 1, self.head_dim)
+        v = self.v_proj(x_step).view(batch, self.num_kv_heads, 1, self.head_dim)
+        x_detach = x_step.detach()
+        qi = self.indexer.compute_query_16d(x_detach)
+        ki = index_rms_norm(self.indexer.k_proj(x_detach), "decode_step")
+        vi = self.indexer.v_proj(x_detach)
+        kv_cache.update(k, v, ki, vi)
+
+        completed = kv_cache.completed_pages
+        want_ctx = self.use_additive_stream and completed > 0
+        routed = decode_route(
+            qi, kv_cache.kp_cache, kv_cache.vp_cache, pos=pos, page_size=self.page_size,
+            local_window=self.local_window, completed_pages=completed, top_p=self.indexer.top_p,
+            min_remote_blocks=self.indexer.min_remote_blocks, max_remote_blocks=self.indexer.max_remote_blocks,
+            return_context=want_ctx)
+        pages, counts = routed[0], routed[1]
+        att_pages, att_counts = pages, counts
+        if self.reference_batch0_pages:
+            att_pages = pages[:1].expand(batch, -1).contiguous()
+            att_counts = counts[:1].expand(batch).contiguous()
+        attn = decode_attention(q, kv_cache, pos=pos, window=self.local_window, remote_pages=att_pages,
+                                remote_counts=att_counts, scale=self.scale)
+        out = self.out_proj(attn.reshape(batch, 1, self.num_heads * self.head_dim))
+        if want_ctx:
+            out = out + self.indexer.out_proj(routed[2].view(batch, 1, -1))
+        cnt = counts.tolist()
+        rows = pages.tolist()
+        selected: List[List[int]] = [rows[b][:cnt[b]] for b in range(batch)]
+        return out, {"selected_remote_pages": selected}

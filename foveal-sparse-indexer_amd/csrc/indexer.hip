@@ -69,36 +69,51 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const void* __restri
 }
 
 // One thread per (batch, block): pooled normalised key and mean value.
-template <bool BF16>
+//   RMS: rms-normalise (and round) every token's key first (compute_kv_blocks_16d);
+//        off for FovealKVCache pages, whose keys arrive normalised (attention.py:305).
+//   KF32: write the normalised key in fp32 without rounding (FovealKVCache.kp_cache
+//        is fp32, attention.py:52,89-90); otherwise round to the input dtype.
+// Outputs are written at row stride out_stride (elements) per pooled row.
+template <bool BF16, bool RMS, bool KF32>
 __global__ __launch_bounds__(256) void pool_kv_kernel(const void* __restrict__ k_lin, const void* __restrict__ v_lin,
-                                                     int64_t n_pool, int block, void* __restrict__ k_out,
-                                                     void* __restrict__ v_out) {
+                                                     int64_t n_pool, int block, int64_t in_group_stride,
+                                                     int64_t groups_per_batch, int64_t out_batch_stride,
+                                                     void* __restrict__ k_out, void* __restrict__ v_out) {
   const int64_t pb = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // flat (batch, block)
   if (pb >= n_pool) return;
+  const int64_t bb = pb / groups_per_batch, gi = pb % groups_per_batch;
+  const int64_t t0 = (bb * groups_per_batch + gi) * in_group_stride;  // element offset of the first token
+  const int64_t o = bb * out_batch_stride + gi * IX_D;
   float ks[IX_D], vs[IX_D];
 #pragma unroll
   for (int c = 0; c < IX_D; ++c) ks[c] = vs[c] = 0.f;
-  const int64_t t0 = pb * block;
   for (int t = 0; t < block; ++t) {
     float kv[IX_D];
 #pragma unroll
-    for (int c = 0; c < IX_D; ++c) kv[c] = ld<BF16>(k_lin, (t0 + t) * IX_D + c);
-    rms_norm16(kv);
+    for (int c = 0; c < IX_D; ++c) kv[c] = ld<BF16>(k_lin, t0 + t * IX_D + c);
+    if (RMS) {
+      rms_norm16(kv);
+#pragma unroll
+      for (int c = 0; c < IX_D; ++c) kv[c] = rnd<BF16>(kv[c]);
+    }
 #pragma unroll
     for (int c = 0; c < IX_D; ++c) {
-      ks[c] += rnd<BF16>(kv[c]);
-      vs[c] += ld<BF16>(v_lin, (t0 + t) * IX_D + c);
+      ks[c] += kv[c];
+      vs[c] += ld<BF16>(v_lin, t0 + t * IX_D + c);
     }
   }
   const float n = static_cast<float>(block);
 #pragma unroll
   for (int c = 0; c < IX_D; ++c) {
     ks[c] = rnd<BF16>(ks[c] / n);
-    st<BF16>(v_out, pb * IX_D + c, vs[c] / n);
+    st<BF16>(v_out, o + c, vs[c] / n);
   }
   l2_normalize16(ks);
 #pragma unroll
-  for (int c = 0; c < IX_D; ++c) st<BF16>(k_out, pb * IX_D + c, ks[c]);
+  for (int c = 0; c < IX_D; ++c) {
+    if (KF32) static_cast<float*>(k_out)[o + c] = ks[c];
+    else st<BF16>(k_out, o + c, ks[c]);
+  }
 }
 
 // Block scores: workgroup = (batch, 32-query tile, 256-key tile); each thread
@@ -223,16 +238,43 @@ FSI_API int fsi_index_pool_kv(const void* k_lin, const void* v_lin, int dtype, i
                 "index_pool_kv: bad sizes");
   FSI_CHECK_ARG(N % block_size == 0, FSI_ERR_SHAPE, "index_pool_kv: length %lld not divisible by block_size %lld",
                 (long long)N, (long long)block_size);
-  const int64_t n_pool = B * (N / block_size);
+  const int64_t nb = N / block_size;
+  const int64_t n_pool = B * nb;
   if (n_pool == 0) return FSI_OK;
   FSI_CHECK_ARG(k_lin && v_lin && k_blocks && v_blocks, FSI_ERR_INVALID_ARG, "index_pool_kv: null pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned grid = static_cast<unsigned>((n_pool + 255) / 256);
+  const int64_t gs = block_size * IX_D;
   if (dtype == FSI_DTYPE_BF16)
-    pool_kv_kernel<true><<<grid, 256, 0, st>>>(k_lin, v_lin, n_pool, (int)block_size, k_blocks, v_blocks);
+    pool_kv_kernel<true, true, false><<<grid, 256, 0, st>>>(k_lin, v_lin, n_pool, (int)block_size, gs, nb, nb * IX_D,
+                                                            k_blocks, v_blocks);
   else
-    pool_kv_kernel<false><<<grid, 256, 0, st>>>(k_lin, v_lin, n_pool, (int)block_size, k_blocks, v_blocks);
+    pool_kv_kernel<false, true, false><<<grid, 256, 0, st>>>(k_lin, v_lin, n_pool, (int)block_size, gs, nb, nb * IX_D,
+                                                             k_blocks, v_blocks);
   FSI_HIP_LAUNCH_CHECK("index_pool_kv");
+  return FSI_OK;
+}
+
+FSI_API int fsi_kv_page_pool(const void* partial_k, const void* partial_v, int dtype, int64_t B, int64_t page_size,
+                             int64_t index_dim, float* kp_out, void* vp_out, int64_t out_batch_stride,
+                             void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "kv_page_pool: dtype %d", dtype);
+  FSI_CHECK_ARG(index_dim == IX_D, FSI_ERR_SHAPE, "kv_page_pool: index_dim %lld != %d", (long long)index_dim, IX_D);
+  FSI_CHECK_ARG(B >= 0 && page_size > 0 && page_size <= 0x7fffffff && out_batch_stride >= IX_D, FSI_ERR_SHAPE,
+                "kv_page_pool: bad sizes");
+  if (B == 0) return FSI_OK;
+  FSI_CHECK_ARG(partial_k && partial_v && kp_out && vp_out, FSI_ERR_INVALID_ARG, "kv_page_pool: null pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned grid = static_cast<unsigned>((B + 255) / 256);
+  const int64_t gs = page_size * IX_D;
+  if (dtype == FSI_DTYPE_BF16)
+    pool_kv_kernel<true, false, true><<<grid, 256, 0, st>>>(partial_k, partial_v, B, (int)page_size, gs, 1,
+                                                            out_batch_stride, kp_out, vp_out);
+  else
+    pool_kv_kernel<false, false, true><<<grid, 256, 0, st>>>(partial_k, partial_v, B, (int)page_size, gs, 1,
+                                                             out_batch_stride, kp_out, vp_out);
+  FSI_HIP_LAUNCH_CHECK("kv_page_pool");
   return FSI_OK;
 }
 

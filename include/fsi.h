@@ -213,6 +213,14 @@ FSI_API int fsi_index_rms_norm(const void* x, int dtype, int64_t M, int64_t inde
 FSI_API int fsi_index_pool_kv(const void* k_lin, const void* v_lin, int dtype, int64_t B, int64_t N,
                               int64_t index_dim, int64_t block_size, void* k_blocks, void* v_blocks, void* stream);
 
+/* FovealKVCache page pooling at the end of a page (attention.py:84-91):
+ * kp = normalize(mean(partial_k)) in fp32, vp = mean(partial_v) in dtype.
+ * partial_k/partial_v: (B, page_size, 16) contiguous; kp_out (fp32) and vp_out
+ * (dtype) rows are written at element offset b * out_batch_stride. */
+FSI_API int fsi_kv_page_pool(const void* partial_k, const void* partial_v, int dtype, int64_t B, int64_t page_size,
+                             int64_t index_dim, float* kp_out, void* vp_out, int64_t out_batch_stride,
+                             void* stream);
+
 /* compute_block_scores (core.py:254-266): normalize(q) . normalize(k) / sqrt(16)
  * with the operands rounded to dtype after normalising and the product rounded
  * before the division.  q: (B, Q, 16); k: (B, N, 16); out: (B, Q, N). */
@@ -224,6 +232,48 @@ FSI_API int fsi_block_scores(const void* q, const void* k, int dtype, int64_t B,
  * rounded to dtype.  scores: (B, Q, N); v_blocks: (B, N, 16); context: (B, Q, 16). */
 FSI_API int fsi_additive_context(const void* scores, const void* v_blocks, int dtype, int64_t B, int64_t Q,
                                  int64_t N, int64_t index_dim, int causal, void* context, void* stream);
+
+/* ------------------------------------------------------------------------- *
+ * Foveal paged-KV decode attention (foveal_indexer/attention.py:284-367).
+ * Paged pools (bf16), page = 64 tokens of one sequence for all KV heads:
+ *   K pool: [n_phys_pages][Hkv][head_dim/32][64][32]
+ *   V pool: [n_phys_pages][Hkv][2][head_dim][32], each 32-token half stored
+ *           dim-major with token tau at slot 8*((tau%16)/4) + 4*(tau/16) + tau%4
+ * page_table: (B, max_pages) int32 logical page -> physical page.
+ * head_dim: 64 or 128.
+ * ------------------------------------------------------------------------- */
+/* Write tokens start .. start + n_tok - 1 (start_rows[b] per sequence, or start)
+ * of K and V given as (B, Hkv, n_tok, head_dim) bf16 with element strides
+ * (16-byte aligned rows) into the pools.  Replaces the slice writes of
+ * FovealKVCache.update (attention.py:72-73).  Positions outside the page table
+ * or pages outside the pool are skipped and reported through err. */
+FSI_API int fsi_kv_write(const void* k, const void* v, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                         int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t, int64_t B, int64_t Hkv,
+                         int64_t n_tok, int64_t head_dim, const int32_t* start_rows, int64_t start,
+                         const int32_t* page_table, int64_t max_pages, int64_t n_phys_pages, void* k_pool,
+                         void* v_pool, int* err, void* stream);
+
+/* Read tokens [0, n_tok) of every sequence back to contiguous (B, Hkv, n_tok,
+ * head_dim) K and V (the reference cache layout, attention.py:48-49). */
+FSI_API int fsi_kv_read(const void* k_pool, const void* v_pool, int64_t B, int64_t Hkv, int64_t n_tok,
+                        int64_t head_dim, const int32_t* page_table, int64_t max_pages, int64_t n_phys_pages,
+                        void* k_out, void* v_out, void* stream);
+
+FSI_API size_t fsi_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, int64_t window,
+                                              int64_t capacity, int64_t max_pages);
+
+/* out (B, Hq, head_dim) bf16 = softmax(scale * q K^T) V over each sequence's
+ * support: tokens [max(0, pos + 1 - window), pos] followed by the pages
+ * remote_pages[b, :remote_counts[b]] (logical ids, as fsi_decode_route returns
+ * them).  Query head h uses KV head h / (Hq / Hkv); Hq / Hkv <= 16.
+ * Replaces the gather + repeat_interleave + SDPA of decode_step
+ * (attention.py:339-365).  remote_pages/remote_counts may be NULL when
+ * capacity == 0.  Invalid page ids are skipped and reported through err. */
+FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
+                            int64_t max_pages, int64_t n_phys_pages, const int32_t* pos_rows, int64_t pos,
+                            int64_t window, const int32_t* remote_pages, const int32_t* remote_counts,
+                            int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale,
+                            void* out, void* workspace, size_t workspace_bytes, int* err, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,131 @@
+"""GPU parity of the paged KV cache and foveal decode attention.
+
+KV pool writes/reads are bit-exact.  Attention outputs: bf16 rel-L2 <= 2e-3
+against fp64 textbook attention over the same support (probabilities are
+rounded to bf16 before the PV product, as flash-style kernels do)."""
+import copy
+import math
+
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import pattention as Pt
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _cache(fsi, dev, B, Hkv, hd, max_seq, seed, n_phys=None):
+    g = torch.Generator().manual_seed(seed)
+    P = -(-max_seq // 64)
+    n_phys = n_phys or B * P + 3
+    table = torch.randperm(n_phys, generator=g)[:B * P].view(B, P).to(torch.int32)
+    c = fsi.FovealKVCache(B, max_seq, Hkv, hd, 16, 64, dev, torch.bfloat16, n_phys_pages=n_phys, page_table=table)
+    k = torch.randn(B, Hkv, max_seq, hd, generator=g).bfloat16()
+    v = torch.randn(B, Hkv, max_seq, hd, generator=g).bfloat16()
+    c.load_dense(k.to(dev), v.to(dev))
+    return c, k, v
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_kv_pool_round_trip(fsi, dev, hd):
+    print(f"[case] kv round trip hd={hd}", flush=True)
+    c, k, v = _cache(fsi, dev, 3, 2, hd, 300, seed=hd)
+    kk, vv = c.to_dense(300)
+    assert torch.equal(kk.cpu(), k) and torch.equal(vv.cpu(), v)
+    # a strided (non-contiguous) source and an offset start
+    k2 = torch.randn(3, 2, 5, hd).bfloat16()
+    v2 = torch.randn(3, 5, 2, hd).bfloat16().transpose(1, 2)
+    c.load_dense(k2.to(dev), v2.to(dev), start=100)
+    kk, vv = c.to_dense(300)
+    assert torch.equal(kk.cpu()[:, :, 100:105], k2) and torch.equal(vv.cpu()[:, :, 100:105], v2)
+    assert torch.equal(kk.cpu()[:, :, :100], k[:, :, :100])
+
+
+CASES = [
+    # B, Hq, Hkv, hd, max_seq, pos, window, pages per seq
+    (2, 8, 2, 128, 1024, 700, 100, [[0, 5, 3], [2]]),
+    (3, 4, 4, 64, 512, 511, 64, [[1], [0, 2, 4], []]),
+    (1, 16, 1, 128, 640, 33, 1024, [[]]),
+    (2, 32, 8, 128, 4096, 4000, 1024, [[0, 10, 20, 30, 40, 44], [7]]),
+    (2, 8, 1, 64, 2048, 1500, 77, [[3, 1, 22], [0]]),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
+def test_decode_attention_parity(fsi, dev, case):
+    B, Hq, Hkv, hd, max_seq, pos, W, pages = case
+    print(f"[case] decode_attention {case[:7]}", flush=True)
+    c, k, v = _cache(fsi, dev, B, Hkv, hd, max_seq, seed=B * 100 + Hq)
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(B, Hq, hd, generator=g).bfloat16()
+    cap = max(1, max(len(p) for p in pages))
+    rp = torch.full((B, cap), -1, dtype=torch.int32)
+    for b, p in enumerate(pages):
+        rp[b, :len(p)] = torch.tensor(p, dtype=torch.int32)
+    cnt = torch.tensor([len(p) for p in pages], dtype=torch.int32)
+    scale = 1.0 / math.sqrt(hd)
+    out = fsi.decode_attention(q.to(dev), c, pos=pos, window=W, remote_pages=rp.to(dev), remote_counts=cnt.to(dev),
+                               scale=scale).cpu()
+    ref = A.decode_attention_f64(q.float(), k, v, pos, W, pages, 64, scale)
+    assert Pt.rel_l2(out.float(), ref.float()) <= TOL
+
+
+def test_decode_attention_per_sequence_positions(fsi, dev):
+    B, Hq, Hkv, hd = 4, 8, 2, 128
+    c, k, v = _cache(fsi, dev, B, Hkv, hd, 1024, seed=7)
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(B, Hq, hd, generator=g).bfloat16()
+    pos = [1023, 64, 500, 0]
+    pages = [[1, 2], [], [0, 3], []]
+    rp = torch.tensor([[1, 2], [-1, -1], [0, 3], [-1, -1]], dtype=torch.int32)
+    cnt = torch.tensor([2, 0, 2, 0], dtype=torch.int32)
+    out = fsi.decode_attention(q.to(dev), c, pos=torch.tensor(pos).to(dev), window=128, remote_pages=rp.to(dev),
+                               remote_counts=cnt.to(dev), scale=0.1).cpu()
+    ref = A.decode_attention_f64(q.float(), k, v, pos, 128, pages, 64, 0.1)
+    assert Pt.rel_l2(out.float(), ref.float()) <= TOL
+
+
+def test_decode_attention_invalid_page_reported(fsi, dev, monkeypatch):
+    c, k, v = _cache(fsi, dev, 1, 1, 64, 256, seed=3)
+    q = torch.randn(1, 1, 64).bfloat16().to(dev)
+    rp = torch.tensor([[9]], dtype=torch.int32, device=dev)  # beyond the 4-page table
+    cnt = torch.tensor([1], dtype=torch.int32, device=dev)
+    monkeypatch.setenv("FSI_CHECK", "1")
+    with pytest.raises(IndexError):
+        fsi.decode_attention(q, c, pos=200, window=64, remote_pages=rp, remote_counts=cnt, scale=0.125)
+
+
+def test_decode_step_module(fsi, dev):
+    """FovealSparseAttention.decode_step over several pages against the CPU
+    restatement with the same weights: selected pages (near-tie tolerant) and
+    outputs.  The module output also passes through four bf16 library GEMMs
+    (q/k/v/out projections) on each side, so its bar is rel-L2 1e-2."""
+    torch.manual_seed(0)
+    m = fsi.FovealSparseAttention(hidden_size=256, num_heads=8, num_kv_heads=2, head_dim=64, page_size=64,
+                                  local_window_blocks=2, top_p=0.8, min_remote_pages=1, max_remote_pages=3,
+                                  remote_capacity=3).to(torch.bfloat16)
+    ora = A.DecodeStepOracle(copy.deepcopy(m), batch=2, max_seq_len=640)
+    md = m.to(dev)
+    cache = md.init_kv_cache(2, 640, dev)
+    g = torch.Generator().manual_seed(4)
+    xs = torch.randn(400, 2, 1, 256, generator=g).bfloat16()
+    worst = 0.0
+    with torch.no_grad():
+        for t in range(400):
+            out, aux = md.decode_step(xs[t].to(dev), cache)
+            ref, pages, r = ora.step(xs[t])
+            if aux["selected_remote_pages"] != pages:
+                # only a near-tie may reorder or resize the selection
+                for b in range(2):
+                    got, exp = aux["selected_remote_pages"][b], pages[b]
+                    if got != exp:
+                        pr = r["probs"][b]
+                        n = min(len(got), len(exp))
+                        assert torch.allclose(pr[got[:n]], pr[exp[:n]], rtol=1e-5), (t, b, got, exp)
+                continue
+            worst = max(worst, Pt.rel_l2(out.cpu().float(), ref.float()))
+    assert cache.completed_pages == 6 and cache.seq_len == 400
+    assert worst <= 1e-2, worst

@@ -13,7 +13,11 @@ the active weights are not served from the 256 MB MALL of one repeated layer.
 The K timed steps are captured once in a HIP graph and replayed; HIP events on
 the replay stream bracket the timed region.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-prefill]
+Other workloads (one JSON line each, for the profiles; not the headline line):
+  --workload routing      C2: fused 16-D cosine scoring + top-p selection, 8192 queries x 4096 keys
+  --workload decode_attn  C4: foveal paged-KV decode attention, 32 sequences x 131072 context
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-prefill] [--workload W]
 """
 from __future__ import annotations
 
@@ -111,6 +115,141 @@ def cpu_baseline(layer_cpu, x_cpu, active, reps: int):
     return ts[len(ts) // 2], cores
 
 
+def _result(metric, value, unit, steps, warmup, ms, dtype, data, config, higher=True):
+    return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": ms, "higher_is_better": higher, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+            "data": data, "config": config}
+
+
+def c2_inputs(Q: int, N: int, dev, seed: int = 0):
+    """Queries = Dirichlet(0.3)-weighted mixes of 4 random keys + N(0, 0.1) noise;
+    keys N(0,1) then L2-normalised; both bf16."""
+    g = torch.Generator().manual_seed(seed)
+    keys = torch.nn.functional.normalize(torch.randn(N, 16, generator=g), dim=-1)
+    j = torch.argsort(torch.rand(Q, N, generator=g), dim=1)[:, :4]
+    w = torch.distributions.Dirichlet(torch.full((4,), 0.3)).sample((Q,))
+    q = (w[..., None] * keys[j]).sum(1) + 0.1 * torch.randn(Q, 16, generator=g)
+    return q.bfloat16().to(dev), keys.bfloat16().to(dev)
+
+
+def bench_routing(fsi, args, dev):
+    Q, N, KMIN, KMAX, CAP, TOP_P = 8192, 4096, 4, 64, 64, 0.9
+    q, k = c2_inputs(Q, N, dev)
+    outs = {}
+
+    def step(i):
+        outs["r"] = fsi.score_and_route(q, k, causal=False, top_p=TOP_P, min_remote_blocks=KMIN,
+                                        max_remote_blocks=KMAX, remote_capacity=CAP, return_mass=True)
+
+    t, _ = time_graph(step, args.steps, args.warmup, dev)
+    per = t / args.steps
+    counts = outs["r"][1].float()
+    algo = Q * 16 * 2 + N * 16 * 2 + Q * CAP * 4 + Q * 4 * 2
+    res = _result("indexer routing queries/s (fused 16-D cosine scoring + top-p selection)", round(Q / per, 1),
+                  "queries/s", args.steps, args.warmup, round(per * 1e3, 6), "fp32",
+                  "synthetic (seeded Dirichlet(0.3) mixes of 4 N(0,1)-normalised keys + N(0,0.1) noise, bf16)",
+                  {"workload": "C2: 8192 queries x 4096 block keys, index_dim 16, top-p 0.9, K_min 4, K_max 64, "
+                               "capacity 64, non-causal", "mean_selected": round(float(counts.mean()), 2)})
+    res["roofline"] = {"bound": "valu", "achieved": round(algo / per / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(algo / per / 1e9 / HBM_PEAK_GBS, 6), "traffic": None,
+                       "kernel": "score_route_kernel (1 launch)", "bytes_per_launch": algo,
+                       "note": "not HBM-bound: 33.5 M scores, exps and a top-64 rank per launch"}
+    if not args.no_cpu_baseline:
+        from oracle import routing as R
+
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        qs, ks = q[:1024].cpu(), k.cpu()
+        R.select_route(R.cosine_scores_f32(qs[None], ks[None]), causal=False, top_p=TOP_P, min_remote_blocks=KMIN,
+                       max_remote_blocks=KMAX, remote_capacity=CAP)
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            R.select_route(R.cosine_scores_f32(qs[None], ks[None]), causal=False, top_p=TOP_P,
+                           min_remote_blocks=KMIN, max_remote_blocks=KMAX, remote_capacity=CAP)
+            ts.append(time.perf_counter() - t0)
+        med = sorted(ts)[1]
+        res["cpu_baseline"] = {"value": round(1024 / med, 1), "unit": "queries/s", "cores": cores, "kind": "port",
+                               "sample": f"oracle torch-CPU cosine scores + select_blocks on the first 1024 of the "
+                                         f"8192 queries, median of 3, {med * 1e3:.1f} ms"}
+    return res
+
+
+def bench_decode_attn(fsi, args, dev):
+    B, HQ, HKV, HD, CTX, PAGE, W, KMAX, TOP_P = 32, 32, 8, 128, 131072, 64, 1024, 32, 0.9
+    P = CTX // PAGE
+    n_phys = 65536
+    g = torch.Generator(device=dev).manual_seed(0)
+    table = torch.randperm(n_phys, device=dev, generator=g)[:B * P].view(B, P).to(torch.int32)
+    cache = fsi.FovealKVCache(B, CTX, HKV, HD, 16, PAGE, dev, torch.bfloat16, n_phys_pages=n_phys, page_table=table)
+    # pools filled in place: every page holds N(0,1) keys and values
+    cache.k_cache.normal_(generator=g)
+    cache.v_cache.normal_(generator=g)
+    cache.kp_cache.copy_(torch.nn.functional.normalize(torch.randn(B, P, 16, device=dev, generator=g), dim=-1))
+    cache.vp_cache.normal_(generator=g)
+    cache.seq_len, cache.completed_pages = CTX, P
+    pos = CTX - 1
+    q = torch.randn(B, HQ, HD, device=dev, generator=g).bfloat16()
+    qi = torch.nn.functional.rms_norm(torch.randn(B, 16, device=dev, generator=g), (16,)).bfloat16()
+    scale = 1.0 / (HD ** 0.5)
+    outs = {}
+
+    def step(i):
+        pages, counts, ctx = fsi.decode_route(qi, cache.kp_cache, cache.vp_cache, pos=pos, page_size=PAGE,
+                                              local_window=W, completed_pages=P, top_p=TOP_P, min_remote_blocks=0,
+                                              max_remote_blocks=KMAX, return_context=True)
+        outs["o"] = fsi.decode_attention(q, cache, pos=pos, window=W, remote_pages=pages, remote_counts=counts,
+                                         scale=scale)
+        outs["c"] = counts
+
+    t, _ = time_graph(step, args.steps, args.warmup, dev)
+    per = t / args.steps
+    k_sel = float(outs["c"].float().mean())
+    flp = (pos + 1 - W) // PAGE
+    kv_bytes = int(B * (W + PAGE * k_sel) * HKV * HD * 2 * 2)
+    algo = kv_bytes + B * flp * 16 * 4 + B * P * 16 * 2 + 2 * B * HQ * HD * 2
+    gbs = algo / per / 1e9
+    res = _result("foveal decode attention tok/s (32 sequences x 131072 context, local 1024 + top-p pages)",
+                  round(B / per, 1), "tok/s", args.steps, args.warmup, round(per * 1e3, 6), "bf16",
+                  "synthetic (seeded N(0,1) K/V pool of 65536 pages, random page table, normalised page keys)",
+                  {"workload": "C4: Llama-3-8B attention shape (32 q heads, 8 KV heads, head_dim 128), batch 32, "
+                               "context 131072, page 64, local window 1024, top-p 0.9, K_max 32",
+                   "mean_selected_pages": round(k_sel, 2)})
+    res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                       "kernel": "decode_route + decode_attn_partial + decode_attn_merge (3 launches)",
+                       "bytes_per_launch": algo}
+    if not args.no_cpu_baseline:
+        from oracle import attention as A
+
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        # the reference's dense-layout decode attention on 4 sequences' supports, gathered on the host
+        pages, counts = fsi.decode_route(qi, cache.kp_cache, None, pos=pos, page_size=PAGE, local_window=W,
+                                         completed_pages=P, top_p=TOP_P, min_remote_blocks=0,
+                                         max_remote_blocks=KMAX)
+        nb = 4
+        kd, vd = cache.to_dense(CTX, batch=slice(0, nb))
+        kc, vc = kd.cpu(), vd.cpu()
+        del kd, vd
+        pl = [pages[b, :int(counts[b])].tolist() for b in range(nb)]
+        qc = q[:nb].cpu()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for b in range(nb):
+                toks = torch.tensor(A.support_tokens(pos, W, pl[b], PAGE))
+                kk = kc[b][:, toks].repeat_interleave(HQ // HKV, dim=0)
+                vv = vc[b][:, toks].repeat_interleave(HQ // HKV, dim=0)
+                torch.nn.functional.scaled_dot_product_attention(qc[b][:, None], kk, vv, scale=scale)
+            ts.append(time.perf_counter() - t0)
+        med = sorted(ts)[1]
+        res["cpu_baseline"] = {"value": round(nb / med, 1), "unit": "tok/s", "cores": cores, "kind": "port",
+                               "sample": f"gather + repeat_interleave + bf16 SDPA on the host for 4 of the 32 "
+                                         f"sequences (attention.py:339-365 order), median of 3, {med * 1e3:.1f} ms"}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +259,7 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=16)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="pattention", choices=["pattention", "routing", "decode_attn"])
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 512 MiB device copy (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -133,6 +273,11 @@ def main():
     fsi = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
+    if args.workload != "pattention":
+        fn = {"routing": bench_routing, "decode_attn": bench_decode_attn}[args.workload]
+        with torch.no_grad():
+            print(json.dumps(fn(fsi, args, dev)), flush=True)
+        return
     layers = make_layers(fsi, args.layers, dev)
 
     gx = torch.Generator(device=dev).manual_seed(1)

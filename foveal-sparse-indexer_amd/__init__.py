@@ -26,6 +26,13 @@ from .core import (
     select_blocks,
 )
 from .attention import FovealKVCache, FovealSparseAttention, decode_attention, decode_route
+from .block_matmul import (
+    BlockSparseLinear,
+    BlockwiseMatMul2D,
+    block_sparse_linear,
+    blockwise_matmul,
+    triton_block_sparse_linear,
+)
 from .foveal_pattention import (
     FovealPattentionMLP,
     mlp_pooled_route,
@@ -41,6 +48,11 @@ __all__ = [
     "index_rms_norm",
     "FovealIndexer",
     "decode_route",
+    "BlockSparseLinear",
+    "BlockwiseMatMul2D",
+    "block_sparse_linear",
+    "blockwise_matmul",
+    "triton_block_sparse_linear",
     "decode_attention",
     "FovealKVCache",
     "FovealSparseAttention",

@@ -97,6 +97,18 @@ SIGNATURES: dict[str, tuple] = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_ptr, _c_size, _c_ptr, _c_ptr],
     ),
+    "fsi_block_sparse_linear_workspace_size": (_c_size, [_c_i64, _c_i64]),
+    "fsi_block_sparse_linear": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr,
+         _c_i64, _c_ptr, _c_size, _c_ptr, _c_ptr],
+    ),
+    "fsi_blockwise_matmul_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "fsi_blockwise_matmul": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+         _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr],
+    ),
 }
 
 ROUTE_MAX_BLOCKS = 4096

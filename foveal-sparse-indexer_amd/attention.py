@@ -189,14 +189,17 @@ class FovealKVCache:
         reference layout) without touching the 16-D page state."""
         self._write(k, v, start)
 
-    def to_dense(self, n_tok: Optional[int] = None):
-        """(K, V) of positions [0, n_tok) in the reference layout (B, Hkv, n, hd)."""
+    def to_dense(self, n_tok: Optional[int] = None, batch: Optional[slice] = None):
+        """(K, V) of positions [0, n_tok) in the reference layout (b, Hkv, n, hd)
+        for the sequences in `batch` (a slice; all by default)."""
         n = self.seq_len if n_tok is None else int(n_tok)
-        shape = (self.batch_size, self.num_kv_heads, n, self.head_dim)
+        rows = self.page_table[batch] if batch is not None else self.page_table
+        rows = rows.contiguous()
+        shape = (rows.shape[0], self.num_kv_heads, n, self.head_dim)
         k = torch.empty(shape, dtype=self.dtype, device=self.k_cache.device)
         v = torch.empty_like(k)
-        st = _lib.lib().fsi_kv_read(self.k_cache.data_ptr(), self.v_cache.data_ptr(), self.batch_size,
-                                    self.num_kv_heads, n, self.head_dim, self.page_table.data_ptr(), self.max_pages,
+        st = _lib.lib().fsi_kv_read(self.k_cache.data_ptr(), self.v_cache.data_ptr(), rows.shape[0],
+                                    self.num_kv_heads, n, self.head_dim, rows.data_ptr(), self.max_pages,
                                     self.n_phys_pages, k.data_ptr(), v.data_ptr(),
                                     _lib.stream_handle(self.k_cache.device))
         _lib.check(st, "FovealKVCache.to_dense")

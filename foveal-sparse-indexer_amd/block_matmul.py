@@ -1,0 +1,369 @@
+"""Block-sparse linear layers on MI355X: drop-in for foveal_indexer/block_matmul.py
+and triton_block_sparse_linear (foveal_indexer/triton_ops.py:316-370).
+
+The GEMMs run on the HIP block-sparse MFMA engine (csrc/bsgemm.hip): active
+column blocks (BlockSparseLinear) or active 2-D tiles (BlockwiseMatMul2D) are
+read straight from the full weight, no gathered copies.  BlockSparseLinear's
+routing (16-D scores, per-token top-p, union of blocks) runs in the HIP routing
+kernels; BlockwiseMatMul2D's tile routing is evaluated with torch ops on the
+GPU.  bf16 only; inference only (the HIP ops have no backward).
+"""
+from __future__ import annotations
+
+import math
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from . import _lib
+from .core import FovealIndexer, Route, _forward_only, select_blocks
+
+
+def block_sparse_linear(x2d: Tensor, weight: Tensor, bias: Optional[Tensor], active_blocks: Tensor,
+                        block_size: int, out: Optional[Tensor] = None) -> Tensor:
+    """out = zeros; out[:, blk] = x w[blk]^T (+ bias[blk]) for the active column blocks."""
+    what = "block_sparse_linear"
+    dev = _lib.require_gpu(x2d, weight, bias, what=what)
+    _forward_only(what, x2d, weight, bias)
+    if x2d.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or (bias is not None and bias.dtype != torch.bfloat16):
+        raise TypeError(f"{what}: bfloat16 only (x {x2d.dtype}, weight {weight.dtype})")
+    x2d = x2d.contiguous()
+    weight = weight.contiguous()
+    M, K = x2d.shape
+    N, K2 = weight.shape
+    if K2 != K:
+        raise ValueError(f"{what}: K mismatch {K} vs {K2}")
+    idx = torch.as_tensor(active_blocks).reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
+    if out is None:
+        out = torch.empty((M, N), dtype=x2d.dtype, device=dev)
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    ws = _lib.workspace(dev, L.fsi_block_sparse_linear_workspace_size(N, block_size), stream)
+    err = _lib.error_word(dev)
+    st = L.fsi_block_sparse_linear(x2d.data_ptr(), x2d.stride(0), weight.data_ptr(), weight.stride(0),
+                                   _lib.ptr(bias.contiguous() if bias is not None else None),
+                                   idx.data_ptr() if idx.numel() else None, idx.numel(), block_size, M, N, K,
+                                   _lib.DTYPE_BF16, out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(),
+                                   err.data_ptr(), stream)
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+    return out
+
+
+def triton_block_sparse_linear(x: Tensor, weight: Tensor, bias: Optional[Tensor], active_block_indices: Tensor,
+                               block_size: int = 32) -> Tensor:
+    """Block-sparse linear Y = X W_active^T (+ bias) (triton_ops.py:316-370); the
+    `triton_` name is kept for compatibility, the kernel is HIP."""
+    if not x.is_cuda:
+        raise RuntimeError("Block-Sparse Linear requires a ROCm GPU (no CPU path).")
+    M, K = x.shape
+    N, K_w = weight.shape
+    assert K == K_w, f"K mismatch: {K} vs {K_w}"
+    return block_sparse_linear(x, weight, bias, active_block_indices, block_size)
+
+
+def blockwise_matmul(x2d: Tensor, weight: Tensor, tile_mask: Tensor, block_k: int, block_n: int,
+                     rows_per_group: Optional[int] = None, out: Optional[Tensor] = None) -> Tensor:
+    """out = x (weight o expand(tile_mask))^T.  tile_mask: bool (T,) or (groups, T)
+    with tile id k_b * (N / block_n) + n_b (block_matmul.py:384-385); with
+    groups > 1, row group g covers rows [g rows_per_group, (g+1) rows_per_group)."""
+    what = "blockwise_matmul"
+    dev = _lib.require_gpu(x2d, weight, tile_mask, what=what)
+    _forward_only(what, x2d, weight)
+    if x2d.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: bfloat16 only (x {x2d.dtype}, weight {weight.dtype})")
+    x2d = x2d.contiguous()
+    weight = weight.contiguous()
+    M, K = x2d.shape
+    N = weight.shape[0]
+    mask = tile_mask.to(device=dev)
+    if mask.dim() == 1:
+        mask = mask[None]
+    groups = mask.shape[0]
+    rpg = rows_per_group if rows_per_group is not None else max(M, 1)
+    m8 = mask.to(torch.uint8).contiguous()
+    if out is None:
+        out = torch.empty((M, N), dtype=x2d.dtype, device=dev)
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    ws = _lib.workspace(dev, L.fsi_blockwise_matmul_workspace_size(M, N, K, block_k), stream)
+    st = L.fsi_blockwise_matmul(x2d.data_ptr(), x2d.stride(0), weight.data_ptr(), weight.stride(0), m8.data_ptr(),
+                                groups, rpg, block_k, block_n, M, N, K, _lib.DTYPE_BF16, out.data_ptr(), out.stride(0),
+                                ws.data_ptr(), ws.numel(), stream)
+    _lib.check(st, what)
+    return out
+
+
+def _eval_active_blocks(block_scores: Tensor, base_blocks: int, top_p: float, max_remote: int, num_blocks: int):
+    """BlockSparseLinear's inference selection (block_matmul.py:168-185): per token,
+    softmax over the remote blocks, needed = clamp(#(cum < top_p) + 1, 0, K_max)
+    top blocks; the active set is the base blocks plus the union over tokens.
+    Returns (sorted active block ids int32, mean needed)."""
+    dev = block_scores.device
+    B, T, nb = block_scores.shape
+    mask = torch.zeros(num_blocks, dtype=torch.bool, device=dev)
+    mask[:base_blocks] = True
+    remote = block_scores[..., base_blocks:]
+    mean_needed = 0.0
+    if remote.shape[-1] > 0:
+        r = select_blocks(remote.contiguous(), causal=False, local_window_blocks=0, top_p=top_p,
+                          min_remote_blocks=0, max_remote_blocks=max_remote, remote_capacity=max(max_remote, 1))
+        cap = r.remote_indices.shape[-1]
+        valid = torch.arange(cap, device=dev).view(1, 1, cap) < r.remote_counts[..., None]
+        sel = r.remote_indices[valid].long() + base_blocks
+        if sel.numel():
+            mask[sel] = True
+        mean_needed = float(r.remote_counts.float().mean())
+    return torch.where(mask)[0].to(torch.int32), mean_needed
+
+
+class BlockSparseLinear(nn.Module):
+    """Linear projection with blockwise dynamic sparsity (block_matmul.py:26-282)."""
+
+    def __init__(
+        self,
+        in_features: int,
+        out_features: int,
+        block_size: int = 64,
+        base_blocks: int = 2,
+        index_dim: int = 16,
+        top_p: float = 0.95,
+        min_remote_blocks: int = 0,
+        max_remote_blocks: int = 8,
+        remote_capacity: int = 8,
+        use_additive_stream: bool = True,
+        bias: bool = False,
+        dtype: torch.dtype = torch.bfloat16,
+    ):
+        super().__init__()
+        if out_features % block_size != 0:
+            raise ValueError(f"out_features ({out_features}) must be divisible by block_size ({block_size})")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.block_size = block_size
+        self.num_blocks = out_features // block_size
+        self.base_blocks = min(base_blocks, self.num_blocks)
+        self.use_additive_stream = use_additive_stream
+        self.weight = nn.Parameter(torch.empty(out_features, in_features, dtype=dtype))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(out_features, dtype=dtype))
+        else:
+            self.register_parameter("bias", None)
+        self.reset_parameters()
+        self.indexer = FovealIndexer(
+            hidden_size=in_features, index_dim=index_dim, block_size=block_size,
+            local_window_blocks=self.base_blocks, top_p=top_p, min_remote_blocks=min_remote_blocks,
+            max_remote_blocks=max_remote_blocks, remote_capacity=remote_capacity, causal=False,
+            use_additive_stream=use_additive_stream,
+        ).to(dtype)
+        self.weight_to_k = nn.Linear(in_features, index_dim, bias=False, dtype=dtype)
+        self.weight_to_v = nn.Linear(in_features, index_dim, bias=False, dtype=dtype)
+        self.indexer.out_proj = nn.Linear(index_dim, out_features, bias=False, dtype=dtype)
+        nn.init.normal_(self.weight_to_k.weight, std=in_features ** -0.5)
+        nn.init.normal_(self.weight_to_v.weight, std=in_features ** -0.5)
+        nn.init.normal_(self.indexer.out_proj.weight, std=1e-3)
+        self._cached_kp: Optional[Tensor] = None
+        self._cached_vp: Optional[Tensor] = None
+
+    def reset_parameters(self) -> None:
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+        if self.bias is not None:
+            fan_in = self.weight.shape[1]
+            bound = 1 / math.sqrt(fan_in) if fan_in > 0 else 0
+            nn.init.uniform_(self.bias, -bound, bound)
+
+    def refresh_block_cache(self) -> None:
+        with torch.no_grad():
+            self._cached_kp, self._cached_vp = self.get_block_keys_and_values()
+
+    def get_block_keys_and_values(self) -> Tuple[Tensor, Tensor]:
+        """Pooled 16-D key and value per weight block (block_matmul.py:109-128)."""
+        what = "get_block_keys_and_values"
+        k_lin = self.weight_to_k(self.weight).contiguous()
+        v_lin = self.weight_to_v(self.weight).contiguous()
+        dev = _lib.require_gpu(k_lin, v_lin, what=what)
+        _forward_only(what, k_lin, v_lin)
+        d = self.indexer.index_dim
+        kb = torch.empty((1, self.num_blocks, d), dtype=k_lin.dtype, device=dev)
+        vb = torch.empty_like(kb)
+        st = _lib.lib().fsi_index_pool_kv(k_lin.data_ptr(), v_lin.data_ptr(), _lib.dtype_code(k_lin.dtype, what), 1,
+                                          self.out_features, d, self.block_size, kb.data_ptr(), vb.data_ptr(),
+                                          _lib.stream_handle(dev))
+        _lib.check(st, what)
+        return kb, vb
+
+    def forward(self, x: Tensor, compute_teacher_loss: bool = False) -> Tuple[Tensor, Dict[str, Any]]:
+        orig_ndim = x.ndim
+        if orig_ndim == 2:
+            x = x.unsqueeze(1)
+        batch, seq_len, in_feat = x.shape
+        device = x.device
+        q_16d = self.indexer.compute_query_16d(x.detach())
+        if not self.training and self._cached_kp is not None:
+            kp_16d, vp_16d = self._cached_kp, self._cached_vp
+        else:
+            kp_16d, vp_16d = self.get_block_keys_and_values()
+            if not self.training:
+                self._cached_kp, self._cached_vp = kp_16d, vp_16d
+        kp_16d = kp_16d.expand(batch, -1, -1)
+        vp_16d = vp_16d.expand(batch, -1, -1)
+        block_scores = self.indexer.compute_block_scores(q_16d, kp_16d)
+
+        route: Optional[Route] = None
+        if not self.training and not torch.is_grad_enabled():
+            active, mean_remote = _eval_active_blocks(block_scores, self.base_blocks, self.indexer.top_p,
+                                                      self.indexer.max_remote_blocks, self.num_blocks)
+        else:
+            route = self.indexer.route(block_scores)
+            mask = torch.zeros(self.num_blocks, dtype=torch.bool, device=device)
+            mask[: self.base_blocks] = True
+            cap = route.remote_indices.shape[-1]
+            valid = torch.arange(cap, device=device).view(1, 1, cap) < route.remote_counts[..., None]
+            sel = route.remote_indices[valid]
+            sel = sel[sel >= self.base_blocks]
+            if sel.numel() > 0:
+                mask[sel.long()] = True
+            active = torch.where(mask)[0].to(torch.int32)
+            mean_remote = float(route.mean_remote_blocks)
+        num_active = int(active.numel())
+
+        out = block_sparse_linear(x.reshape(batch * seq_len, in_feat), self.weight, self.bias, active,
+                                  self.block_size).view(batch, seq_len, self.out_features)
+        additive_out = None
+        if self.use_additive_stream:
+            ctx = _additive_context(block_scores, vp_16d)
+            additive_out = self.indexer.out_proj(ctx).to(out.dtype)
+            out = out + additive_out
+        if orig_ndim == 2:
+            out = out.squeeze(1)
+        mean_active = self.base_blocks + mean_remote
+        aux: Dict[str, Any] = {
+            "route": route,
+            "additive_out": additive_out,
+            "active_blocks_union": num_active,
+            "mean_active_blocks": mean_active,
+            "total_blocks": self.num_blocks,
+            "sparsity": 1.0 - (mean_active / self.num_blocks),
+            "distill_loss": torch.tensor(0.0, device=device),
+        }
+        if compute_teacher_loss:
+            with torch.no_grad():
+                dense_out = F.linear(x, self.weight, self.bias)
+                energy = torch.norm(dense_out.view(batch, seq_len, self.num_blocks, self.block_size), p=2, dim=-1)
+                teacher = F.softmax(energy, dim=-1)
+            aux["distill_loss"] = self.indexer.distillation_loss(block_scores, teacher)
+        return out, aux
+
+
+def _additive_context(scores: Tensor, v_blocks: Tensor) -> Tensor:
+    """softmax over every block (probabilities in the values' dtype) times the
+    block values (block_matmul.py:257-260)."""
+    what = "additive_stream"
+    dev = _lib.require_gpu(scores, v_blocks, what=what)
+    s = scores.to(v_blocks.dtype).contiguous() if scores.dtype != v_blocks.dtype else scores.contiguous()
+    v = v_blocks.contiguous()
+    B, Q, N = s.shape
+    d = v.shape[-1]
+    ctx = torch.empty((B, Q, d), dtype=v.dtype, device=dev)
+    st = _lib.lib().fsi_additive_context(s.data_ptr(), v.data_ptr(), _lib.dtype_code(v.dtype, what), B, Q, N, d, 0,
+                                         ctx.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return ctx
+
+
+class BlockwiseMatMul2D(nn.Module):
+    """2-D tile-sparse matmul (block_matmul.py:285-419)."""
+
+    def __init__(
+        self,
+        in_features: int,
+        out_features: int,
+        block_k: int = 64,
+        block_n: int = 64,
+        base_tiles_ratio: float = 0.25,
+        index_dim: int = 16,
+        top_p: float = 0.95,
+        dtype: torch.dtype = torch.bfloat16,
+    ):
+        super().__init__()
+        if in_features % block_k != 0 or out_features % block_n != 0:
+            raise ValueError(f"Shapes ({in_features}, {out_features}) must be divisible by "
+                             f"tile sizes ({block_k}, {block_n})")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.block_k = block_k
+        self.block_n = block_n
+        self.num_k_blocks = in_features // block_k
+        self.num_n_blocks = out_features // block_n
+        self.total_tiles = self.num_k_blocks * self.num_n_blocks
+        self.base_tiles = max(1, int(self.total_tiles * base_tiles_ratio))
+        self.weight = nn.Parameter(torch.empty(out_features, in_features, dtype=dtype))
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+        self.tile_q = nn.Linear(block_k, index_dim, bias=False, dtype=dtype)
+        self.tile_k = nn.Linear(block_k * block_n, index_dim, bias=False, dtype=dtype)
+        self.tile_v = nn.Linear(block_k * block_n, index_dim, bias=False, dtype=dtype)
+        self.out_proj = nn.Linear(index_dim, out_features, bias=False, dtype=dtype)
+        nn.init.normal_(self.tile_q.weight, std=block_k ** -0.5)
+        nn.init.normal_(self.tile_k.weight, std=(block_k * block_n) ** -0.5)
+        nn.init.normal_(self.tile_v.weight, std=(block_k * block_n) ** -0.5)
+        nn.init.normal_(self.out_proj.weight, std=1e-3)
+        self.top_p = top_p
+        self.index_dim = index_dim
+
+    def tile_keys_and_values(self) -> Tuple[Tensor, Tensor]:
+        """16-D key (normalised) and value of every tile (block_matmul.py:341-353)."""
+        w_tiles = (self.weight.view(self.num_n_blocks, self.block_n, self.num_k_blocks, self.block_k)
+                   .permute(2, 0, 1, 3).contiguous().view(self.total_tiles, self.block_n * self.block_k))
+        tile_k = F.normalize(F.rms_norm(self.tile_k(w_tiles), (self.index_dim,)), dim=-1)
+        tile_v = self.tile_v(w_tiles)
+        return tile_k, tile_v
+
+    def route_tiles(self, x: Tensor):
+        """Per-token top-p over all tiles, union with the base tiles
+        (block_matmul.py:355-379).  Returns (tile mask, probs, scores)."""
+        batch, seq_len, _ = x.shape
+        tile_k, tile_v = self.tile_keys_and_values()
+        x_k = x.view(batch, seq_len, self.num_k_blocks, self.block_k).mean(dim=2)
+        q_16d = F.normalize(F.rms_norm(self.tile_q(x_k), (self.index_dim,)), dim=-1)
+        # plain 2-D products with contiguous operands (no batched bf16 product on a transposed view)
+        scores = (q_16d.reshape(-1, self.index_dim) @ tile_k.t().contiguous()).view(batch, seq_len, -1)
+        scores = scores / math.sqrt(self.index_dim)
+        probs = F.softmax(scores, dim=-1)
+        sorted_probs, sorted_indices = probs.sort(dim=-1, descending=True)
+        cumulative = sorted_probs.cumsum(dim=-1)
+        needed = ((cumulative < self.top_p).sum(dim=-1) + 1).clamp_max(self.total_tiles)
+        slot = torch.arange(self.total_tiles, device=x.device).view(1, 1, -1)
+        chosen = sorted_indices[slot < needed[..., None]]
+        mask = torch.zeros(self.total_tiles, dtype=torch.bool, device=x.device)
+        mask[: self.base_tiles] = True
+        mask[chosen] = True
+        return mask, probs, scores, tile_v
+
+    def forward(self, x: Tensor, compute_teacher_loss: bool = False) -> Tuple[Tensor, Dict[str, Any]]:
+        batch, seq_len, _ = x.shape
+        device = x.device
+        mask, probs, scores, tile_v = self.route_tiles(x)
+        n_active = int(mask.sum())
+        out = blockwise_matmul(x.reshape(batch * seq_len, self.in_features), self.weight, mask, self.block_k,
+                               self.block_n).view(batch, seq_len, self.out_features)
+        context = (probs.to(tile_v.dtype).reshape(-1, self.total_tiles) @ tile_v.contiguous()).view(
+            batch, seq_len, self.index_dim)
+        out = out + self.out_proj(context)
+        aux: Dict[str, Any] = {
+            "active_tiles": n_active,
+            "total_tiles": self.total_tiles,
+            "tile_sparsity": 1.0 - (n_active / self.total_tiles),
+            "distill_loss": torch.tensor(0.0, device=device),
+        }
+        if compute_teacher_loss:
+            with torch.no_grad():
+                dense_out = F.linear(x, self.weight)
+                energy = torch.norm(dense_out.view(batch, seq_len, self.num_n_blocks, self.block_n), p=2, dim=-1)
+                # tile (k_b, n_b) takes the energy of its output block n_b (block_matmul.py:404-410)
+                tile_energy = energy.repeat(1, 1, self.num_k_blocks)
+                teacher = F.softmax(tile_energy, dim=-1)
+            aux["distill_loss"] = -(teacher * F.log_softmax(scores, dim=-1)).sum(dim=-1).mean()
+        return out, aux

@@ -1,0 +1,577 @@
+// Gather-driven block-sparse bf16 GEMM engine for MI355X (gfx950).
+//
+// One workgroup (4 waves) computes a 128 x 128 tile of C[M, N] = A[M, K] B[N, K]^T
+// (both operands K-contiguous, the F.linear layout) with fp32 accumulation on
+// v_mfma_f32_16x16x32_bf16.  What makes it block-sparse is how a tile finds its
+// operands:
+//   * N is gathered in 32-column sub-blocks: each of the tile's four
+//     sub-blocks has its own B pointer and row base and its own C column base
+//     (active column blocks of BlockSparseLinear, gate/up rows of the active
+//     Pattention blocks);
+//   * K advances in 64-wide steps, each with its own A and B column offset
+//     (dense K, K gathered by active blocks for the Pattention down
+//     projection, or a per-tile list of active 2-D tiles).
+// Per K-step the workgroup stages A and B (16 KiB each) through a double-
+// buffered, XOR-swizzled LDS tile: the global loads are 1 KiB contiguous per
+// wave instruction and the MFMA fragment reads are free of bank conflicts.
+// Wave (wm, wn) owns rows 64 wm .. +64 and tile columns {32 wn .. +32} of both
+// 64-column halves, so a gate column and its up column land in the same lane.
+#include <algorithm>
+
+#include "fsi_common.h"
+
+using namespace fsi;
+
+namespace {
+
+constexpr int TM = 128, TN = 128, TK = 64;
+constexpr int GT = 256;  // threads per workgroup
+constexpr int SUB = 32;  // N gather granularity
+
+enum NMode { N_DIRECT = 0, N_GATHER = 1, N_DUAL = 2 };
+enum KMode { K_DENSE = 0, K_GATHER_B = 1, K_LIST = 2 };
+enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1 };
+
+struct GemmArgs {
+  const bf16_t* A;  // [M, lda]
+  const bf16_t* B0; // [rows, ldb]
+  const bf16_t* B1; // second B (up projection) for N_DUAL
+  const bf16_t* bias;
+  bf16_t* C;
+  int64_t lda, ldb, ldc;
+  int M, N, K;                 // N: logical columns of the gathered problem, K: reduction length
+  const int32_t* blocks;       // N_GATHER / N_DUAL: active block ids; K_GATHER_B: active blocks along K
+  int n_blocks;                // entries in `blocks`
+  int block;                   // block size in columns (multiple of 32)
+  int n_rows_total;            // rows of B (bounds for gathered ids)
+  int scatter_c;               // N_GATHER: write C at the gathered column (1) or compactly (0)
+  const int32_t* tile_n;       // K_LIST: per work item, n tile index
+  const int32_t* tile_m;       // K_LIST: per work item, m tile index
+  const int32_t* klist_off;    // K_LIST: per work item, offset into klist
+  const int32_t* klist;        // K_LIST: k offsets (elements, multiple of 64)
+  int n_items;                 // K_LIST: work items
+  const uint8_t* tmask;        // K_LIST: [groups][nkb * nnb] tile mask (k-major tile ids)
+  int tgroups, rows_per_group, nkb, nnb, block_k, block_n;
+  int m_tiles, n_tiles;        // dense grid (non-list modes)
+  int act, rounding;           // EPI_SWIGLU
+  int* err;
+};
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+template <int NM, int KM, int EPI>
+__global__ __launch_bounds__(GT, 2) void bsgemm_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TM * TK];  // [buf][A/B][row * 64 + k]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- which tile ----------------------------------------------------------
+  int mt, nt, kcount, koff = 0;
+  if (KM == K_LIST) {
+    const int item = blockIdx.x;
+    mt = g.tile_m[item];
+    nt = g.tile_n[item];
+    koff = g.klist_off[item];
+    kcount = g.klist_off[item + 1] - koff;
+  } else {
+    // consecutive workgroups walk down M for one N tile: the B tile stays hot in L2
+    mt = blockIdx.x % g.m_tiles;
+    nt = blockIdx.x / g.m_tiles;
+    kcount = KM == K_GATHER_B ? g.n_blocks * (g.block / TK) : (g.K + TK - 1) / TK;
+  }
+  const int m0 = mt * TM;
+
+  // ---- per 32-column sub-block: B row base (and pointer) and C column base --
+  // (computed by every thread for all four sub-blocks; cheap scalar work)
+  int64_t brow[4];
+  int ccol[4];
+  bool bval[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (NM == N_DUAL) {
+      // tile nt covers channel block half: 64 channels = [gate 64 | up 64]
+      const int ch = nt * 64 + (s & 1) * SUB;  // compact channel index
+      const int bi = ch / g.block;
+      const int blk = bi < g.n_blocks ? (g.blocks ? g.blocks[bi] : bi) : -1;
+      const int64_t row = static_cast<int64_t>(blk) * g.block + ch % g.block;
+      bval[s] = blk >= 0 && row + SUB <= g.n_rows_total;
+      brow[s] = bval[s] ? row : 0;
+      ccol[s] = ch;
+    } else if (NM == N_GATHER) {
+      const int col = nt * TN + s * SUB;  // compact column
+      const int bi = col / g.block;
+      const int blk = bi < g.n_blocks ? (g.blocks ? g.blocks[bi] : bi) : -1;
+      const int64_t row = static_cast<int64_t>(blk) * g.block + col % g.block;
+      bval[s] = blk >= 0 && row + SUB <= g.n_rows_total;
+      brow[s] = bval[s] ? row : 0;
+      ccol[s] = g.scatter_c ? static_cast<int>(row) : col;
+    } else {
+      const int col = nt * TN + s * SUB;
+      bval[s] = col < g.N;
+      brow[s] = bval[s] ? col : 0;
+      ccol[s] = col;
+    }
+    if (NM != N_DIRECT && !bval[s] && g.err && ((NM == N_DUAL ? nt * 64 + (s & 1) * SUB : nt * TN + s * SUB) < g.N))
+      set_error(g.err, FSI_ERR_INDEX_RANGE);
+  }
+
+  // K_LIST: the tile mask row of this tile's row group and each sub-block's n block
+  const uint8_t* gmask = nullptr;
+  int nbs[4] = {0, 0, 0, 0};
+  if (KM == K_LIST) {
+    int grp = m0 / g.rows_per_group;
+    grp = grp < g.tgroups ? grp : g.tgroups - 1;
+    gmask = g.tmask + static_cast<int64_t>(grp) * g.nkb * g.nnb;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) nbs[s] = (nt * TN + s * SUB) / g.block_n;
+  }
+
+  // ---- global -> register staging: thread loads 4 A chunks and 4 B chunks ----
+  // chunk q = tid + 256 i: row q / 8, k chunk q % 8 (16 B)
+  const int lrow0 = tid >> 3, lchunk = tid & 7;
+  // K_GATHER_B: kb_rows = columns of B (bounds for the gathered blocks)
+  auto k_cols = [&](int step, int64_t& a_k, int64_t& b_k) -> bool {
+    if (KM == K_LIST) {
+      a_k = b_k = g.klist[koff + step];
+    } else if (KM == K_GATHER_B) {
+      const int per = g.block / TK;
+      const int bi = step / per;
+      const int blk = g.blocks ? g.blocks[bi] : bi;
+      a_k = static_cast<int64_t>(step) * TK;
+      if (blk < 0 || static_cast<int64_t>(blk + 1) * g.block > g.n_rows_total) {
+        b_k = 0;
+        return false;
+      }
+      b_k = static_cast<int64_t>(blk) * g.block + (step % per) * TK;
+    } else {
+      a_k = b_k = static_cast<int64_t>(step) * TK;
+    }
+    return true;
+  };
+  u32x4_t ra[4], rb[4];
+  auto load_step = [&](int step) {
+    int64_t a_k, b_k;
+    const bool kval = k_cols(step, a_k, b_k);
+    if (!kval && g.err) set_error(g.err, FSI_ERR_INDEX_RANGE);
+    const int kk = static_cast<int>((KM == K_DENSE ? a_k : 0) + lchunk * 8);  // element k within the problem
+    bool tile_on[4] = {true, true, true, true};
+    if (KM == K_LIST) {  // (k block, n block) tiles outside the mask contribute nothing
+      const int kb = static_cast<int>(a_k / g.block_k);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) tile_on[s] = nbs[s] < g.nnb && gmask[kb * g.nnb + nbs[s]] != 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = lrow0 + 32 * i;
+      const int m = m0 + r;
+      const bool kin = KM == K_DENSE ? (kk < g.K) : true;
+      if (m < g.M && kin) ra[i] = *reinterpret_cast<const u32x4_t*>(g.A + m * g.lda + a_k + lchunk * 8);
+      else ra[i] = u32x4_t{0u, 0u, 0u, 0u};
+      const int s = r / SUB;  // sub-block of this tile row
+      const bf16_t* bp = (NM == N_DUAL && s >= 2) ? g.B1 : g.B0;
+      const int64_t row = brow[s] + (r % SUB);
+      const bool rin = NM != N_DIRECT || row < g.N;  // direct N: rows past N (N % 32 != 0) are not read
+      if (bval[s] && rin && kin && kval && tile_on[s])
+        rb[i] = *reinterpret_cast<const u32x4_t*>(bp + row * g.ldb + b_k + lchunk * 8);
+      else rb[i] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = lrow0 + 32 * i;
+      const int off = r * TK + swz(r, lchunk) * 8;
+      *reinterpret_cast<u32x4_t*>(&lds[buf][0][off]) = ra[i];
+      *reinterpret_cast<u32x4_t*>(&lds[buf][1][off]) = rb[i];
+    }
+  };
+
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // wave's B fragment rows: tile columns {32 wn + 16 f} (f = 0, 1) and {64 + 32 wn + 16 (f - 2)}
+  const int frow = lane & 15, fchunk = lane >> 4;
+  if (kcount > 0) {
+    load_step(0);
+    store_step(0);
+  }
+  __syncthreads();
+  for (int step = 0; step < kcount; ++step) {
+    const int buf = step & 1;
+    const int nxt = step + 1 < kcount ? step + 1 : step;  // straight-line prefetch; the last one is redundant
+    load_step(nxt);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4_t fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 64 * wm + 16 * i + frow;
+        fa[i] = *reinterpret_cast<const u32x4_t*>(&lds[buf][0][r * TK + swz(r, ks * 4 + fchunk) * 8]);
+      }
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const int c = (f < 2 ? 32 * wn + 16 * f : 64 + 32 * wn + 16 * (f - 2)) + frow;
+        fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[buf][1][c * TK + swz(c, ks * 4 + fchunk) * 8]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fa[i], fb[f], acc[i][f]);
+    }
+    if (step + 1 < kcount) store_step(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds C[row 4 (lane / 16) + j][col lane % 16] of each fragment ----
+  const int crow0 = m0 + 64 * wm + 4 * (lane >> 4);
+  if (EPI == EPI_SWIGLU) {
+    // gate fragments f = 0, 1 pair with up fragments f = 2, 3 (same channel)
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int ch = ccol[0] + 32 * wn + 16 * f + frow;  // ccol[0] = first channel of the tile
+      if (ch >= g.N) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = crow0 + 16 * i + j;
+          if (m >= g.M) continue;
+          float gv = acc[i][f][j], uv = acc[i][f + 2][j];
+          float h;
+          if (g.act == ACT_SWIGLU) h = pattention_act<ACT_SWIGLU>(gv, uv, g.rounding);
+          else h = 0.f;
+          g.C[m * g.ldc + ch] = f32_to_bf16(h);
+        }
+    }
+  } else {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int tc = f < 2 ? 32 * wn + 16 * f : 64 + 32 * wn + 16 * (f - 2);  // tile column of the fragment
+      const int s = tc / SUB;
+      if (NM != N_DIRECT && !bval[s]) continue;
+      const int col = ccol[s] + (tc % SUB) + frow;
+      if (NM == N_DIRECT && col >= g.N) continue;
+      const float bv = g.bias ? bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + frow : col]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = crow0 + 16 * i + j;
+          if (m >= g.M) continue;
+          g.C[m * g.ldc + col] = f32_to_bf16(acc[i][f][j] + bv);
+        }
+    }
+  }
+}
+
+// Zero the columns of C whose column block is inactive (BlockSparseLinear's
+// torch.zeros + scatter); mask[b] != 0 marks active block b.
+__global__ __launch_bounds__(256) void zero_inactive_kernel(bf16_t* __restrict__ C, int64_t ldc, int M, int N,
+                                                            int block, const uint8_t* __restrict__ mask) {
+  const int64_t total = static_cast<int64_t>(M) * (N / 8);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int m = static_cast<int>(i / (N / 8));
+    const int c = static_cast<int>(i % (N / 8)) * 8;
+    if (!mask[c / block]) *reinterpret_cast<u32x4_t*>(C + m * ldc + c) = u32x4_t{0u, 0u, 0u, 0u};
+  }
+}
+
+__global__ __launch_bounds__(256) void block_mask_kernel(const int32_t* __restrict__ blocks, int n, int n_blocks,
+                                                         uint8_t* __restrict__ mask, int* __restrict__ err) {
+  // mask was cleared by a fill kernel before this launch
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+    const int b = blocks[i];
+    if (b >= 0 && b < n_blocks) mask[b] = 1;
+    else if (err) set_error(err, FSI_ERR_INDEX_RANGE);
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t* __restrict__ p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    p[i] = 0;
+}
+
+// Work list of a 2-D tile mask: one item per (128-row tile, 128-column tile).
+// mask: [groups][num_k_blocks * num_n_blocks] uint8, tile id k_b * num_n_blocks + n_b
+// (block_matmul.py:384-385).  Item (mt, nt) gathers the 64-wide k steps of
+// every k block at which any n block of column tile nt is active; the GEMM
+// loader zeroes the weight rows of (k block, n block) tiles outside the mask,
+// so a column tile holding several n blocks with different masks stays exact.
+__global__ __launch_bounds__(256) void tile_list_kernel(const uint8_t* __restrict__ mask, int groups, int rows_per_group,
+                                                        int m_tiles, int n_tiles, int nkb, int nnb, int block_k,
+                                                        int block_n, int32_t* __restrict__ item_m,
+                                                        int32_t* __restrict__ item_n, int32_t* __restrict__ counts) {
+  const int item = blockIdx.x * 256 + threadIdx.x;
+  if (item >= m_tiles * n_tiles) return;
+  const int mt = item / n_tiles, nt = item % n_tiles;
+  const int grp = (mt * TM) / rows_per_group;
+  const uint8_t* gm = mask + static_cast<int64_t>(grp < groups ? grp : groups - 1) * nkb * nnb;
+  const int nb0 = (nt * TN) / block_n, nb1 = ((nt + 1) * TN - 1) / block_n;
+  int cnt = 0;
+  for (int kb = 0; kb < nkb; ++kb) {
+    bool any = false;
+    for (int nb = nb0; nb <= nb1 && nb < nnb; ++nb) any |= gm[kb * nnb + nb] != 0;
+    if (any) cnt += block_k / TK;
+  }
+  item_m[item] = mt;
+  item_n[item] = nt;
+  counts[item] = cnt;
+}
+
+__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ counts, int n,
+                                                     int32_t* __restrict__ offsets) {
+  // single workgroup exclusive scan (n items), offsets[n] = total
+  __shared__ int32_t part[1024];
+  const int t = threadIdx.x;
+  const int per = (n + 1023) / 1024;
+  int s = 0;
+  for (int i = t * per; i < (t + 1) * per && i < n; ++i) s += counts[i];
+  part[t] = s;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int run = t > 0 ? part[t - 1] : 0;
+  for (int i = t * per; i < (t + 1) * per && i < n; ++i) {
+    offsets[i] = run;
+    run += counts[i];
+  }
+  if (t == 1023) offsets[n] = part[1023];
+}
+
+__global__ __launch_bounds__(256) void tile_klist_kernel(const uint8_t* __restrict__ mask, int groups,
+                                                         int rows_per_group, int n_tiles, int nkb, int nnb,
+                                                         int block_k, int block_n, const int32_t* __restrict__ offsets,
+                                                         int n_items, int32_t* __restrict__ klist) {
+  const int item = blockIdx.x * 256 + threadIdx.x;
+  if (item >= n_items) return;
+  const int mt = item / n_tiles, nt = item % n_tiles;
+  const int grp = (mt * TM) / rows_per_group;
+  const uint8_t* gm = mask + static_cast<int64_t>(grp < groups ? grp : groups - 1) * nkb * nnb;
+  const int nb0 = (nt * TN) / block_n, nb1 = ((nt + 1) * TN - 1) / block_n;
+  int o = offsets[item];
+  for (int kb = 0; kb < nkb; ++kb) {
+    bool any = false;
+    for (int nb = nb0; nb <= nb1 && nb < nnb; ++nb) any |= gm[kb * nnb + nb] != 0;
+    if (any)
+      for (int s = 0; s < block_k / TK; ++s) klist[o++] = kb * block_k + s * TK;
+  }
+}
+
+template <int NM, int KM, int EPI>
+hipError_t launch(const GemmArgs& a, unsigned grid, hipStream_t st) {
+  bsgemm_kernel<NM, KM, EPI><<<grid, GT, 0, st>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+namespace fsi_gemm {
+
+// Pattention prefill building blocks, used by fsi_pattention_fwd.
+// H[M, 64 n_active] = act(x K_gate[S]^T, x K_up[S]^T), S = active blocks of block_n (multiple of 32)
+int gateup_swiglu(const bf16_t* x, int64_t ldx, const bf16_t* kg, const bf16_t* ku, int64_t ldk, int N_p,
+                  const int32_t* blocks, int n_active, int block_n, int M, int K, int rounding, bf16_t* H,
+                  int64_t ldh, int* err, hipStream_t st) {
+  GemmArgs a{};
+  a.A = x;
+  a.B0 = kg;
+  a.B1 = ku;
+  a.C = H;
+  a.lda = ldx;
+  a.ldb = ldk;
+  a.ldc = ldh;
+  a.M = M;
+  a.N = n_active * block_n;
+  a.K = K;
+  a.blocks = blocks;
+  a.n_blocks = n_active;
+  a.block = block_n;
+  a.n_rows_total = N_p;
+  a.m_tiles = (M + TM - 1) / TM;
+  a.n_tiles = (a.N + 63) / 64;
+  a.act = ACT_SWIGLU;
+  a.rounding = rounding;
+  a.err = err;
+  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
+  return launch<N_DUAL, K_DENSE, EPI_SWIGLU>(a, grid, st) == hipSuccess ? 0 : -1;
+}
+
+// out[M, D] = H[M, 64 n_active] W_down[:, S]^T with W_down [D, N_p] (row stride ldw)
+int down_gather(const bf16_t* H, int64_t ldh, const bf16_t* wd, int64_t ldw, int N_p, const int32_t* blocks,
+                int n_active, int block_n, int M, int D, bf16_t* out, int64_t ldo, int* err, hipStream_t st) {
+  GemmArgs a{};
+  a.A = H;
+  a.B0 = a.B1 = wd;
+  a.C = out;
+  a.lda = ldh;
+  a.ldb = ldw;
+  a.ldc = ldo;
+  a.M = M;
+  a.N = D;
+  a.K = n_active * block_n;
+  a.blocks = blocks;
+  a.n_blocks = n_active;
+  a.block = block_n;
+  a.n_rows_total = N_p;
+  a.m_tiles = (M + TM - 1) / TM;
+  a.n_tiles = (D + TN - 1) / TN;
+  a.err = err;
+  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
+  return launch<N_DIRECT, K_GATHER_B, EPI_STORE>(a, grid, st) == hipSuccess ? 0 : -1;
+}
+
+}  // namespace fsi_gemm
+
+extern "C" {
+
+FSI_API size_t fsi_block_sparse_linear_workspace_size(int64_t N, int64_t block_size) {
+  if (block_size <= 0) return FSI_WORKSPACE_COUNTER_BYTES;
+  return FSI_WORKSPACE_COUNTER_BYTES + static_cast<size_t>((N / block_size + 255) / 256 * 256);
+}
+
+FSI_API int fsi_block_sparse_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                                    const int32_t* active_blocks, int64_t n_active, int64_t block_size, int64_t M,
+                                    int64_t N, int64_t K, int dtype, void* out, int64_t ldo, void* workspace,
+                                    size_t workspace_bytes, int* err, void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "block_sparse_linear: dtype %d (bf16 only)", dtype);
+  FSI_CHECK_ARG(M >= 0 && N >= 0 && K > 0 && n_active >= 0, FSI_ERR_SHAPE, "block_sparse_linear: bad sizes");
+  FSI_CHECK_ARG(block_size > 0 && block_size % SUB == 0 && N % block_size == 0, FSI_ERR_SHAPE,
+                "block_sparse_linear: block_size %lld must be a multiple of %d dividing N %lld", (long long)block_size,
+                SUB, (long long)N);
+  FSI_CHECK_ARG(K % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldo % 8 == 0 && N % 8 == 0, FSI_ERR_ALIGN,
+                "block_sparse_linear: K, N and leading dimensions must be multiples of 8");
+  FSI_CHECK_ARG(ldx >= K && ldw >= K && ldo >= N, FSI_ERR_SHAPE, "block_sparse_linear: leading dimension too small");
+  FSI_CHECK_ARG(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, FSI_ERR_SHAPE,
+                "block_sparse_linear: sizes beyond int32");
+  if (M == 0 || N == 0) return FSI_OK;
+  FSI_CHECK_ARG(x && w && out && (active_blocks || n_active == 0), FSI_ERR_INVALID_ARG,
+                "block_sparse_linear: null pointer");
+  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(out) % 16 == 0,
+                FSI_ERR_ALIGN, "block_sparse_linear: x, w and out must be 16-byte aligned");
+  const int64_t nb = N / block_size;
+  const size_t need = fsi_block_sparse_linear_workspace_size(N, block_size);
+  FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE,
+                "block_sparse_linear: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* mask = static_cast<uint8_t*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES;
+  fill_u8_kernel<<<1, 256, 0, st>>>(mask, nb);
+  if (n_active > 0)
+    block_mask_kernel<<<static_cast<unsigned>((n_active + 255) / 256), 256, 0, st>>>(active_blocks, (int)n_active,
+                                                                                    (int)nb, mask, err);
+  const int64_t zero_items = M * (N / 8);
+  zero_inactive_kernel<<<static_cast<unsigned>(std::min<int64_t>((zero_items + 255) / 256, 1 << 16)), 256, 0, st>>>(
+      static_cast<bf16_t*>(out), ldo, (int)M, (int)N, (int)block_size, mask);
+  FSI_HIP_LAUNCH_CHECK("block_sparse_linear zero");
+  if (n_active == 0) return FSI_OK;
+  GemmArgs a{};
+  a.A = static_cast<const bf16_t*>(x);
+  a.B0 = a.B1 = static_cast<const bf16_t*>(w);
+  a.bias = static_cast<const bf16_t*>(bias);
+  a.C = static_cast<bf16_t*>(out);
+  a.lda = ldx;
+  a.ldb = ldw;
+  a.ldc = ldo;
+  a.M = (int)M;
+  a.N = (int)(n_active * block_size);
+  a.K = (int)K;
+  a.blocks = active_blocks;
+  a.n_blocks = (int)n_active;
+  a.block = (int)block_size;
+  a.n_rows_total = (int)N;
+  a.scatter_c = 1;
+  a.m_tiles = (int)((M + TM - 1) / TM);
+  a.n_tiles = (int)((a.N + TN - 1) / TN);
+  a.err = err;
+  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
+  const hipError_t e = launch<N_GATHER, K_DENSE, EPI_STORE>(a, grid, st);
+  FSI_CHECK_ARG(e == hipSuccess, FSI_ERR_HIP, "block_sparse_linear: launch failed: %s", hipGetErrorString(e));
+  return FSI_OK;
+}
+
+FSI_API size_t fsi_blockwise_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int64_t block_k) {
+  (void)block_k;
+  const int64_t items = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+  const int64_t ksteps = (K + TK - 1) / TK;
+  return FSI_WORKSPACE_COUNTER_BYTES + static_cast<size_t>(4 * (3 * items + 1) + 4 * items * ksteps) + 256;
+}
+
+FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                 const uint8_t* tile_mask, int64_t groups, int64_t rows_per_group, int64_t block_k,
+                                 int64_t block_n, int64_t M, int64_t N, int64_t K, int dtype, void* out, int64_t ldo,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "blockwise_matmul: dtype %d (bf16 only)", dtype);
+  FSI_CHECK_ARG(M >= 0 && N > 0 && K > 0 && groups > 0 && rows_per_group > 0, FSI_ERR_SHAPE,
+                "blockwise_matmul: bad sizes");
+  FSI_CHECK_ARG(block_k % TK == 0 && block_k > 0 && K % block_k == 0 && block_n > 0 && N % block_n == 0 &&
+                    (block_n % TN == 0 || TN % block_n == 0),
+                FSI_ERR_SHAPE, "blockwise_matmul: tiles %lldx%lld must be multiples of %d (K) and divide or be "
+                "multiples of %d (N)", (long long)block_k, (long long)block_n, TK, TN);
+  FSI_CHECK_ARG(rows_per_group % TM == 0 || groups == 1, FSI_ERR_SHAPE,
+                "blockwise_matmul: rows_per_group %lld must be a multiple of %d", (long long)rows_per_group, TM);
+  FSI_CHECK_ARG(ldx % 8 == 0 && ldw % 8 == 0 && ldo % 8 == 0 && ldx >= K && ldw >= K && ldo >= N, FSI_ERR_ALIGN,
+                "blockwise_matmul: leading dimensions");
+  FSI_CHECK_ARG(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, FSI_ERR_SHAPE,
+                "blockwise_matmul: sizes beyond int32");
+  if (M == 0) return FSI_OK;
+  FSI_CHECK_ARG(x && w && tile_mask && out, FSI_ERR_INVALID_ARG, "blockwise_matmul: null pointer");
+  const size_t need = fsi_blockwise_matmul_workspace_size(M, N, K, block_k);
+  FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE, "blockwise_matmul: workspace %zu < %zu",
+                workspace_bytes, need);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int m_tiles = (int)((M + TM - 1) / TM), n_tiles = (int)((N + TN - 1) / TN);
+  const int items = m_tiles * n_tiles;
+  const int nkb = (int)(K / block_k), nnb = (int)(N / block_n);
+  int32_t* base = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES);
+  int32_t* item_m = base;
+  int32_t* item_n = item_m + items;
+  int32_t* counts = item_n + items;
+  int32_t* offsets = counts + items;  // items + 1
+  int32_t* klist = offsets + items + 1;
+  const unsigned g1 = static_cast<unsigned>((items + 255) / 256);
+  tile_list_kernel<<<g1, 256, 0, st>>>(tile_mask, (int)groups, (int)rows_per_group, m_tiles, n_tiles, nkb, nnb,
+                                       (int)block_k, (int)block_n, item_m, item_n, counts);
+  scan_kernel<<<1, 1024, 0, st>>>(counts, items, offsets);
+  tile_klist_kernel<<<g1, 256, 0, st>>>(tile_mask, (int)groups, (int)rows_per_group, n_tiles, nkb, nnb,
+                                        (int)block_k, (int)block_n, offsets, items, klist);
+  FSI_HIP_LAUNCH_CHECK("blockwise_matmul lists");
+  GemmArgs a{};
+  a.A = static_cast<const bf16_t*>(x);
+  a.B0 = a.B1 = static_cast<const bf16_t*>(w);
+  a.C = static_cast<bf16_t*>(out);
+  a.lda = ldx;
+  a.ldb = ldw;
+  a.ldc = ldo;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.tile_m = item_m;
+  a.tile_n = item_n;
+  a.klist_off = offsets;
+  a.klist = klist;
+  a.n_items = items;
+  a.tmask = tile_mask;
+  a.tgroups = (int)groups;
+  a.rows_per_group = (int)rows_per_group;
+  a.nkb = nkb;
+  a.nnb = nnb;
+  a.block_k = (int)block_k;
+  a.block_n = (int)block_n;
+  const unsigned grid = static_cast<unsigned>(items);
+  const hipError_t e = launch<N_DIRECT, K_LIST, EPI_STORE>(a, grid, st);
+  FSI_CHECK_ARG(e == hipSuccess, FSI_ERR_HIP, "blockwise_matmul: launch failed: %s", hipGetErrorString(e));
+  return FSI_OK;
+}
+
+}  // extern "C"

@@ -20,6 +20,8 @@
 //                                             P as a bf16 hi + lo pair, two MFMAs)
 // Per-wave partials (max, sum, O) are merged by a second kernel; nothing is
 // synchronised across workgroups.
+#include <algorithm>
+
 #include "fsi_common.h"
 
 using namespace fsi;
@@ -49,9 +51,9 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const bf16_t* __restrict_
                                                       int64_t n_phys, bf16_t* __restrict__ k_pool,
                                                       bf16_t* __restrict__ v_pool, int* __restrict__ err) {
   constexpr int PIECES = HD / 8;
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t total = static_cast<int64_t>(B) * Hkv * n_tok * PIECES;
-  if (gid >= total) return;
+  for (int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; gid < total;
+       gid += static_cast<int64_t>(gridDim.x) * 256) {
   const int piece = static_cast<int>(gid % PIECES);
   int64_t r = gid / PIECES;
   const int t = static_cast<int>(r % n_tok);
@@ -62,12 +64,12 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const bf16_t* __restrict_
   const int lp = p / PAGE, off = p % PAGE;
   if (p < 0 || lp >= max_pages) {
     if (err) set_error(err, FSI_ERR_INDEX_RANGE);
-    return;
+    continue;
   }
   const int64_t phys = page_table[static_cast<int64_t>(b) * max_pages + lp];
   if (phys < 0 || phys >= n_phys) {
     if (err) set_error(err, FSI_ERR_INDEX_RANGE);
-    return;
+    continue;
   }
   const int64_t page_base = (phys * Hkv + g) * PAGE * HD;
   const int d0 = piece * 8;
@@ -82,6 +84,7 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const bf16_t* __restrict_
     vb[(d0 + 2 * w) * CHUNK] = static_cast<bf16_t>(vv[w] & 0xffffu);
     vb[(d0 + 2 * w + 1) * CHUNK] = static_cast<bf16_t>(vv[w] >> 16);
   }
+  }
 }
 
 // Reader for tests and cache export: pooled tokens [0, n_tok) of every
@@ -92,9 +95,9 @@ __global__ __launch_bounds__(256) void kv_read_kernel(const bf16_t* __restrict__
                                                      const int32_t* __restrict__ page_table, int max_pages,
                                                      int64_t n_phys, bf16_t* __restrict__ k_out,
                                                      bf16_t* __restrict__ v_out) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t total = static_cast<int64_t>(B) * Hkv * n_tok * HD;
-  if (gid >= total) return;
+  for (int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; gid < total;
+       gid += static_cast<int64_t>(gridDim.x) * 256) {
   const int d = static_cast<int>(gid % HD);
   int64_t r = gid / HD;
   const int t = static_cast<int>(r % n_tok);
@@ -111,6 +114,7 @@ __global__ __launch_bounds__(256) void kv_read_kernel(const bf16_t* __restrict__
   }
   k_out[gid] = kk;
   v_out[gid] = vv;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -333,29 +337,53 @@ __global__ __launch_bounds__(64 * DA_WAVES) void decode_attn_partial_kernel(Deco
   }
 }
 
-// One workgroup per (sequence, query head); thread d merges dimension d.
+// One wave per (sequence, query head): lanes read the split maxima and sums in
+// parallel, then every lane merges HD / 64 dimensions over the splits.
+constexpr int MG_WAVES = 4;
+
 template <int HD>
-__global__ __launch_bounds__(HD) void decode_attn_merge_kernel(const float* __restrict__ m_part,
-                                                              const float* __restrict__ l_part,
-                                                              const float* __restrict__ o_part, int Hq, int Hkv,
-                                                              int G, int S, bf16_t* __restrict__ out) {
-  const int b = blockIdx.x / Hq, hq = blockIdx.x % Hq;
+__global__ __launch_bounds__(64 * MG_WAVES) void decode_attn_merge_kernel(const float* __restrict__ m_part,
+                                                                         const float* __restrict__ l_part,
+                                                                         const float* __restrict__ o_part, int B,
+                                                                         int Hq, int Hkv, int G, int S,
+                                                                         bf16_t* __restrict__ out) {
+  constexpr int DPL = HD / 64;  // dimensions per lane
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * MG_WAVES + (threadIdx.x >> 6);
+  if (item >= B * Hq) return;
+  const int b = item / Hq, hq = item % Hq;
   const int g = hq / G, h = hq % G;
-  const int d = threadIdx.x;
   const int64_t part0 = (static_cast<int64_t>(b) * Hkv + g) * S;
   float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, m_part[(part0 + s) * 16 + h]);
-  float L = 0.f, o = 0.f;
+  for (int s = lane; s < S; s += 64) M = fmaxf(M, m_part[(part0 + s) * 16 + h]);
+  M = wave_max(M);
+  float o[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) o[i] = 0.f;
+  float L = 0.f;
   if (M != -INFINITY) {
-    for (int s = 0; s < S; ++s) {
-      const float ms = m_part[(part0 + s) * 16 + h];
-      if (ms == -INFINITY) continue;
-      const float w = exp2f(ms - M);
-      L += l_part[(part0 + s) * 16 + h] * w;
-      o += o_part[((part0 + s) * G + h) * HD + d] * w;
+    for (int s0 = 0; s0 < S; s0 += 64) {
+      const int s = s0 + lane;
+      float w = 0.f, lw = 0.f;
+      if (s < S) {
+        const float ms = m_part[(part0 + s) * 16 + h];
+        w = ms == -INFINITY ? 0.f : exp2f(ms - M);
+        lw = l_part[(part0 + s) * 16 + h] * w;
+      }
+      L += wave_sum(lw);
+      const int n = S - s0 < 64 ? S - s0 : 64;
+#pragma unroll 4
+      for (int k = 0; k < n; ++k) {
+        const float wk = __shfl(w, k, 64);
+        const float* src = o_part + ((part0 + s0 + k) * G + h) * HD + lane * DPL;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) o[i] = fmaf(src[i], wk, o[i]);
+      }
     }
   }
-  out[(static_cast<int64_t>(b) * Hq + hq) * HD + d] = f32_to_bf16(L > 0.f ? o / L : 0.f);
+  bf16_t* dst = out + (static_cast<int64_t>(b) * Hq + hq) * HD + lane * DPL;
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) dst[i] = f32_to_bf16(L > 0.f ? o[i] / L : 0.f);
 }
 
 int split_count(int64_t B, int64_t Hkv, int64_t max_chunks) {
@@ -399,7 +427,7 @@ FSI_API int fsi_kv_write(const void* k, const void* v, int64_t k_stride_b, int64
                 FSI_ERR_ALIGN, "kv_write: K/V rows must be 16-byte aligned");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t total = B * Hkv * n_tok * (head_dim / 8);
-  const unsigned grid = static_cast<unsigned>((total + 255) / 256);
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 1 << 20));
 #define KVW(HDV)                                                                                                   \
   kv_write_kernel<HDV><<<grid, 256, 0, st>>>(                                                                      \
       static_cast<const bf16_t*>(k), static_cast<const bf16_t*>(v), k_stride_b, k_stride_h, k_stride_t,             \
@@ -424,7 +452,7 @@ FSI_API int fsi_kv_read(const void* k_pool, const void* v_pool, int64_t B, int64
   FSI_CHECK_ARG(k_pool && v_pool && page_table && k_out && v_out, FSI_ERR_INVALID_ARG, "kv_read: null pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t total = B * Hkv * n_tok * head_dim;
-  const unsigned grid = static_cast<unsigned>((total + 255) / 256);
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 1 << 20));
 #define KVR(HDV)                                                                                                  \
   kv_read_kernel<HDV><<<grid, 256, 0, st>>>(static_cast<const bf16_t*>(k_pool), static_cast<const bf16_t*>(v_pool), \
                                             (int)B, (int)Hkv, (int)n_tok, page_table, (int)max_pages,              \
@@ -502,16 +530,19 @@ FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_poo
   P.scale_log2 = scale * LOG2E;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned grid = static_cast<unsigned>((parts + DA_WAVES - 1) / DA_WAVES);
+  const unsigned merge_grid = static_cast<unsigned>((B * Hq + MG_WAVES - 1) / MG_WAVES);
   if (head_dim == 128) {
     decode_attn_partial_kernel<128><<<grid, 64 * DA_WAVES, 0, st>>>(P);
     FSI_HIP_LAUNCH_CHECK("decode_attn partial");
-    decode_attn_merge_kernel<128><<<(unsigned)(B * Hq), 128, 0, st>>>(P.m_part, P.l_part, P.o_part, (int)Hq,
-                                                                      (int)Hkv, P.G, S, static_cast<bf16_t*>(out));
+    decode_attn_merge_kernel<128><<<merge_grid, 64 * MG_WAVES, 0, st>>>(P.m_part, P.l_part, P.o_part, (int)B,
+                                                                        (int)Hq, (int)Hkv, P.G, S,
+                                                                        static_cast<bf16_t*>(out));
   } else {
     decode_attn_partial_kernel<64><<<grid, 64 * DA_WAVES, 0, st>>>(P);
     FSI_HIP_LAUNCH_CHECK("decode_attn partial");
-    decode_attn_merge_kernel<64><<<(unsigned)(B * Hq), 64, 0, st>>>(P.m_part, P.l_part, P.o_part, (int)Hq,
-                                                                    (int)Hkv, P.G, S, static_cast<bf16_t*>(out));
+    decode_attn_merge_kernel<64><<<merge_grid, 64 * MG_WAVES, 0, st>>>(P.m_part, P.l_part, P.o_part, (int)B,
+                                                                       (int)Hq, (int)Hkv, P.G, S,
+                                                                       static_cast<bf16_t*>(out));
   }
   FSI_HIP_LAUNCH_CHECK("decode_attn merge");
   return FSI_OK;

@@ -26,6 +26,17 @@
 
 #include "fsi_common.h"
 
+namespace fsi_gemm {
+int gateup_swiglu(const fsi::bf16_t* x, int64_t ldx, const fsi::bf16_t* kg, const fsi::bf16_t* ku, int64_t ldk,
+                  int N_p, const int32_t* blocks, int n_active, int block_n, int M, int K, int rounding,
+                  fsi::bf16_t* H, int64_t ldh, int* err, hipStream_t st);
+int down_gather(const fsi::bf16_t* H, int64_t ldh, const fsi::bf16_t* wd, int64_t ldw, int N_p, const int32_t* blocks,
+                int n_active, int block_n, int M, int D, fsi::bf16_t* out, int64_t ldo, int* err, hipStream_t st);
+}  // namespace fsi_gemm
+
+// Token count from which the tiled MFMA GEMM path replaces the skinny kernels.
+constexpr int64_t GEMM_MIN_M = 256;
+
 using namespace fsi;
 
 namespace {
@@ -629,6 +640,24 @@ int fsi_pattention_fwd(const void* x, int64_t ldx, const void* k_gate, const voi
   const bf16_t* xb = static_cast<const bf16_t*>(x);
   const bf16_t* kgb = static_cast<const bf16_t*>(k_gate);
   const bf16_t* kub = static_cast<const bf16_t*>(k_up);
+
+  // Many tokens: tiled MFMA GEMMs (gathered gate/up with the SwiGLU fused in the
+  // epilogue, then the down projection gathered along K).
+  if (M >= GEMM_MIN_M && activation == FSI_ACT_SWIGLU && kub && block_n % 64 == 0 && N_p % block_n == 0 &&
+      v_transposed && ldv % 8 == 0 && (uintptr_t)v % 16 == 0 && ldo % 8 == 0 && (uintptr_t)out % 16 == 0) {
+    const int n_act = active_blocks ? (int)n_active : (int)(N_p / block_n);
+    if (fsi_gemm::gateup_swiglu(xb, ldx, kgb, kub, ldk, (int)N_p, active_blocks, n_act, (int)block_n, (int)M,
+                                (int)K, rounding, h, ldh, err, st) != 0) {
+      fsi_host::set_last_error("pattention: gate/up GEMM launch failed: %s", hipGetErrorString(hipGetLastError()));
+      return FSI_ERR_HIP;
+    }
+    if (fsi_gemm::down_gather(h, ldh, static_cast<const bf16_t*>(v), ldv, (int)N_p, active_blocks, n_act,
+                              (int)block_n, (int)M, (int)D_out, static_cast<bf16_t*>(out), ldo, err, st) != 0) {
+      fsi_host::set_last_error("pattention: down GEMM launch failed: %s", hipGetErrorString(hipGetLastError()));
+      return FSI_ERR_HIP;
+    }
+    return FSI_OK;
+  }
   const dim3 g1((unsigned)p.n_groups, (unsigned)p.m_tiles);
   const bf16_t* kub2 = kub ? kub : kgb;
   switch (activation) {

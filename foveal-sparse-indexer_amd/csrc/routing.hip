@@ -83,13 +83,14 @@ __device__ __forceinline__ void bitonic_desc(uint64_t (&v)[E]) {
   }
 }
 
-// Number of keys >= t in the row.
+// Number of keys >= t in the row: one compare mask and scalar popcount per
+// register slot, no cross-lane data movement.
 template <int PL>
 __device__ __forceinline__ int count_ge(const uint32_t (&key)[PL], uint32_t t) {
   int c = 0;
 #pragma unroll
-  for (int i = 0; i < PL; ++i) c += key[i] >= t;
-  return wave_sum_i(c);
+  for (int i = 0; i < PL; ++i) c += __popcll(__ballot(key[i] >= t));
+  return c;
 }
 
 // The R largest keys (0 < R <= min(64 E, #candidates)), sorted descending into
@@ -176,7 +177,7 @@ __device__ __forceinline__ void running_mass(const uint64_t (&sorted)[E], int n,
     cum[e] = 0.f;
     const int m = n - e * 64 < 64 ? n - e * 64 : 64;
     for (int l = 0; l < m; ++l) {
-      const float pl = __shfl(p, l, 64);
+      const float pl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), l));
       float c;
       if (RB) {
         accf += pl;
@@ -487,24 +488,57 @@ __global__ __launch_bounds__(64 * SR_WAVES) void score_route_kernel(const void* 
 
 // ---------------------------------------------------------------------------
 // decode_step page routing (attention.py:313-337) and additive-stream context
-// (attention.py:369-376), one sequence per wave.
+// (attention.py:369-376), one 16-wave workgroup per sequence.
 //   qi: (B, d) 16-D query (dtype), kp: (B, P, d) fp32 page keys,
 //   vp: (B, P, d) page values (dtype); pages [0, completed) are complete.
-// Routing runs when completed > flp > 0 (flp = first local page): softmax over
-// pages [0, flp), count = max(K_min, min(#(cum < top_p) + 1, min(K_max, flp))),
-// at most flp.  The context is softmax over every completed page (probabilities
-// cast to vp's dtype) contracted with vp, in vp's dtype.
+// Every thread scores pages t, t + 1024, ... into LDS; the context is the
+// softmax over all completed pages (probabilities cast to vp's dtype)
+// contracted with vp; routing runs when completed > flp > 0 (flp = first local
+// page) over pages [0, flp): count = max(K_min, min(#(cum < top_p) + 1,
+// min(K_max, flp))), at most flp, ranked by wave 0 from the LDS scores.
 // ---------------------------------------------------------------------------
+constexpr int DR_THREADS = 1024;
+constexpr int DR_WAVES = DR_THREADS / 64;
+
+__device__ __forceinline__ float dr_block_max(float v, float* red) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < DR_WAVES; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+
+__device__ __forceinline__ float dr_block_sum(float v, float* red) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < DR_WAVES; ++w) r += red[w];
+  return r;
+}
+
 template <int PL, int E, bool BF16>
-__global__ __launch_bounds__(64) void decode_route_kernel(const void* __restrict__ qi, const float* __restrict__ kp,
-                                                          const void* __restrict__ vp, int P,
-                                                          const int32_t* __restrict__ pos_rows, int pos, int page,
-                                                          int window, int completed, float top_p, int k_min,
-                                                          int k_max, int cap, float sqrt_d,
-                                                          int32_t* __restrict__ out_pages,
-                                                          int32_t* __restrict__ out_cnt, void* __restrict__ out_ctx) {
+__global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __restrict__ qi,
+                                                                  const float* __restrict__ kp,
+                                                                  const void* __restrict__ vp, int P,
+                                                                  const int32_t* __restrict__ pos_rows, int pos,
+                                                                  int page, int window, int completed, float top_p,
+                                                                  int k_min, int k_max, int cap, float sqrt_d,
+                                                                  int32_t* __restrict__ out_pages,
+                                                                  int32_t* __restrict__ out_cnt,
+                                                                  void* __restrict__ out_ctx) {
+  __shared__ float sc[64 * PL];
+  __shared__ float red[DR_WAVES];
+  __shared__ float ctx_part[DR_WAVES][SR_D];
   __shared__ uint32_t lk[64 * E], li[64 * E];
-  const int lane = lane_id();
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
   const int b = blockIdx.x;
   const int mypos = pos_rows ? pos_rows[b] : pos;
   const int local_start = mypos + 1 - window > 0 ? mypos + 1 - window : 0;
@@ -522,106 +556,100 @@ __global__ __launch_bounds__(64) void decode_route_kernel(const void* __restrict
 #pragma unroll
   for (int c = 0; c < SR_D; ++c) qv[c] = qv[c] / nrm;
 
-  float s[PL];
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const int j = i * 64 + lane;
+  for (int j = threadIdx.x; j < completed; j += DR_THREADS) {
+    const float4* kr = reinterpret_cast<const float4*>(kp + (static_cast<int64_t>(b) * P + j) * SR_D);
     float acc = 0.f;
-    if (j < completed) {
-      const float4* kr = reinterpret_cast<const float4*>(kp + (static_cast<int64_t>(b) * P + j) * SR_D);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float4 f = kr[w];
-        acc = fmaf(qv[4 * w], f.x, acc);
-        acc = fmaf(qv[4 * w + 1], f.y, acc);
-        acc = fmaf(qv[4 * w + 2], f.z, acc);
-        acc = fmaf(qv[4 * w + 3], f.w, acc);
-      }
+    for (int w = 0; w < 4; ++w) {
+      const float4 f = kr[w];
+      acc = fmaf(qv[4 * w], f.x, acc);
+      acc = fmaf(qv[4 * w + 1], f.y, acc);
+      acc = fmaf(qv[4 * w + 2], f.z, acc);
+      acc = fmaf(qv[4 * w + 3], f.w, acc);
     }
-    s[i] = acc / sqrt_d;
+    sc[j] = acc / sqrt_d;
   }
+  __syncthreads();
 
-  if (out_ctx) {
-    float ctx = 0.f;  // lane c < 16 accumulates context component c
+  if (out_ctx) {  // uniform across the workgroup
+    float ctx = 0.f;
     if (completed > 0) {
       float mx = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < PL; ++i)
-        if (i * 64 + lane < completed) mx = fmaxf(mx, s[i]);
-      mx = wave_max(mx);
-      float e[PL], z = 0.f;
-#pragma unroll
-      for (int i = 0; i < PL; ++i) {
-        e[i] = i * 64 + lane < completed ? expf(s[i] - mx) : 0.f;
-        z += e[i];
-      }
-      z = wave_sum(z);
+      for (int j = threadIdx.x; j < completed; j += DR_THREADS) mx = fmaxf(mx, sc[j]);
+      mx = dr_block_max(mx, red);
+      float z = 0.f;
+      for (int j = threadIdx.x; j < completed; j += DR_THREADS) z += expf(sc[j] - mx);
+      z = dr_block_sum(z, red);
       float part[SR_D];
 #pragma unroll
       for (int c = 0; c < SR_D; ++c) part[c] = 0.f;
+      for (int j = threadIdx.x; j < completed; j += DR_THREADS) {
+        float pj = expf(sc[j] - mx) / z;
+        const int64_t off = (static_cast<int64_t>(b) * P + j) * SR_D;
+        if (BF16) {
+          pj = round_bf16(pj);
+          const u32x4_t* vr = reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(vp) + off);
+          const u32x4_t a = vr[0], c2 = vr[1];
 #pragma unroll
-      for (int i = 0; i < PL; ++i) {
-        const int j = i * 64 + lane;
-        if (j < completed) {
-          float p = e[i] / z;
-          const int64_t off = (static_cast<int64_t>(b) * P + j) * SR_D;
-          if (BF16) {
-            p = round_bf16(p);
-            const u32x4_t* vr = reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(vp) + off);
-            const u32x4_t a = vr[0], c2 = vr[1];
+          for (int w = 0; w < 4; ++w) {
+            part[2 * w] = fmaf(pj, lo_bf16(a[w]), part[2 * w]);
+            part[2 * w + 1] = fmaf(pj, hi_bf16(a[w]), part[2 * w + 1]);
+            part[8 + 2 * w] = fmaf(pj, lo_bf16(c2[w]), part[8 + 2 * w]);
+            part[9 + 2 * w] = fmaf(pj, hi_bf16(c2[w]), part[9 + 2 * w]);
+          }
+        } else {
+          const float4* vr = reinterpret_cast<const float4*>(static_cast<const float*>(vp) + off);
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              part[2 * w] = fmaf(p, lo_bf16(a[w]), part[2 * w]);
-              part[2 * w + 1] = fmaf(p, hi_bf16(a[w]), part[2 * w + 1]);
-              part[8 + 2 * w] = fmaf(p, lo_bf16(c2[w]), part[8 + 2 * w]);
-              part[9 + 2 * w] = fmaf(p, hi_bf16(c2[w]), part[9 + 2 * w]);
-            }
-          } else {
-            const float4* vr = reinterpret_cast<const float4*>(static_cast<const float*>(vp) + off);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              const float4 f = vr[w];
-              part[4 * w] = fmaf(p, f.x, part[4 * w]);
-              part[4 * w + 1] = fmaf(p, f.y, part[4 * w + 1]);
-              part[4 * w + 2] = fmaf(p, f.z, part[4 * w + 2]);
-              part[4 * w + 3] = fmaf(p, f.w, part[4 * w + 3]);
-            }
+          for (int w = 0; w < 4; ++w) {
+            const float4 f = vr[w];
+            part[4 * w] = fmaf(pj, f.x, part[4 * w]);
+            part[4 * w + 1] = fmaf(pj, f.y, part[4 * w + 1]);
+            part[4 * w + 2] = fmaf(pj, f.z, part[4 * w + 2]);
+            part[4 * w + 3] = fmaf(pj, f.w, part[4 * w + 3]);
           }
         }
       }
 #pragma unroll
       for (int c = 0; c < SR_D; ++c) {
         const float t = wave_sum(part[c]);
-        if (lane == c) ctx = t;
+        if (lane == 0) ctx_part[wave][c] = t;
+      }
+      __syncthreads();
+      if (threadIdx.x < SR_D) {
+#pragma unroll
+        for (int w = 0; w < DR_WAVES; ++w) ctx += ctx_part[w][threadIdx.x];
       }
     }
-    if (lane < SR_D) {
-      const int64_t off = static_cast<int64_t>(b) * SR_D + lane;
+    if (threadIdx.x < SR_D) {
+      const int64_t off = static_cast<int64_t>(b) * SR_D + threadIdx.x;
       if (BF16) static_cast<bf16_t*>(out_ctx)[off] = f32_to_bf16(ctx);
       else static_cast<float*>(out_ctx)[off] = ctx;
     }
   }
 
+  const bool route = completed > flp && flp > 0;
+  float z = 1.f, mx = 0.f;
+  if (route) {  // uniform
+    float m = -INFINITY;
+    for (int j = threadIdx.x; j < flp; j += DR_THREADS) m = fmaxf(m, sc[j]);
+    mx = dr_block_max(m, red);
+    float zz = 0.f;
+    for (int j = threadIdx.x; j < flp; j += DR_THREADS) zz += expf(sc[j] - mx);
+    z = dr_block_sum(zz, red);
+  }
+  if (wave != 0) return;  // ranking and output by wave 0 only; no workgroup barrier follows
+
   int count = 0;
   uint64_t sorted[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) sorted[e] = 0;
-  if (completed > flp && flp > 0) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PL; ++i)
-      if (i * 64 + lane < flp) mx = fmaxf(mx, s[i]);
-    mx = wave_max(mx);
-    float z = 0.f;
-#pragma unroll
-    for (int i = 0; i < PL; ++i) {
-      s[i] = i * 64 + lane < flp ? expf(s[i] - mx) : 0.f;
-      z += s[i];
-    }
-    z = wave_sum(z);
+  if (route) {
     uint32_t key[PL];
 #pragma unroll
-    for (int i = 0; i < PL; ++i) key[i] = i * 64 + lane < flp ? __float_as_uint(s[i] / z) + 1u : 0u;
+    for (int i = 0; i < PL; ++i) {
+      const int j = i * 64 + lane;
+      key[i] = j < flp ? __float_as_uint(expf(sc[j] - mx) / z) + 1u : 0u;
+    }
     const int kcap = k_max < flp ? k_max : flp;  // k_max = min(K_max, first_local_page)
     int R = kcap > k_min ? kcap : k_min;
     R = R < flp ? R : flp;
@@ -845,11 +873,11 @@ FSI_API int fsi_decode_route(const void* qi, const float* kp, const void* vp, in
   const int win = static_cast<int>(window < 0x7fffffff ? window : 0x7fffffff);
   FSI_DISPATCH_PL(pick_pl(completed_pages), FSI_DISPATCH_E(pick_e(want), {
     if (dtype == FSI_DTYPE_BF16)
-      decode_route_kernel<PL, E, true><<<(unsigned)B, 64, 0, st>>>(
+      decode_route_kernel<PL, E, true><<<(unsigned)B, DR_THREADS, 0, st>>>(
           qi, kp, vp, (int)P, pos_rows, (int)pos, (int)page_size, win, (int)completed_pages, top_p, k_min, k_max,
           capacity, sqrt_d, out_pages, out_counts, out_context);
     else
-      decode_route_kernel<PL, E, false><<<(unsigned)B, 64, 0, st>>>(
+      decode_route_kernel<PL, E, false><<<(unsigned)B, DR_THREADS, 0, st>>>(
           qi, kp, vp, (int)P, pos_rows, (int)pos, (int)page_size, win, (int)completed_pages, top_p, k_min, k_max,
           capacity, sqrt_d, out_pages, out_counts, out_context);
   }))

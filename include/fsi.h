@@ -275,6 +275,37 @@ FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_poo
                             int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale,
                             void* out, void* workspace, size_t workspace_bytes, int* err, void* stream);
 
+/* ------------------------------------------------------------------------- *
+ * Block-sparse GEMMs (bf16 in, fp32 accumulate, bf16 out) on 128 x 128 MFMA
+ * tiles.  x: (M, K) row stride ldx; w: (N, K) row stride ldw (the nn.Linear
+ * weight layout); out: (M, N) row stride ldo.  K, N and leading dimensions
+ * multiples of 8, base pointers 16-byte aligned.
+ * ------------------------------------------------------------------------- */
+FSI_API size_t fsi_block_sparse_linear_workspace_size(int64_t N, int64_t block_size);
+
+/* Column-block sparse linear (triton_block_sparse_linear, foveal_indexer/triton_ops.py:316-370):
+ * out[:, b*bs:(b+1)*bs] = x w[b*bs:(b+1)*bs]^T (+ bias[b*bs:(b+1)*bs]) for every
+ * active block b, all other columns 0.  block_size: multiple of 32 dividing N.
+ * Block ids outside [0, N / block_size) are skipped and reported through err. */
+FSI_API int fsi_block_sparse_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                                    const int32_t* active_blocks, int64_t n_active, int64_t block_size, int64_t M,
+                                    int64_t N, int64_t K, int dtype, void* out, int64_t ldo, void* workspace,
+                                    size_t workspace_bytes, int* err, void* stream);
+
+FSI_API size_t fsi_blockwise_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int64_t block_k);
+
+/* 2-D tile-sparse matmul (BlockwiseMatMul2D, foveal_indexer/block_matmul.py:335-392):
+ * out = x (w o T)^T where T expands tile_mask to elements: tile (k_b, n_b) of
+ * size block_k x block_n is active iff tile_mask[g][k_b * (N / block_n) + n_b],
+ * with g the row group of the output row (rows_per_group rows each; groups = 1
+ * applies one mask to every row).  block_k multiple of 64 dividing K; block_n
+ * divides N and divides or is a multiple of 128; rows_per_group a multiple of
+ * 128 when groups > 1.  Rows of a group whose tiles are all inactive get 0. */
+FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                 const uint8_t* tile_mask, int64_t groups, int64_t rows_per_group, int64_t block_k,
+                                 int64_t block_n, int64_t M, int64_t N, int64_t K, int dtype, void* out, int64_t ldo,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

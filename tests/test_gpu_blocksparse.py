@@ -1,0 +1,118 @@
+"""GPU parity of the block-sparse MFMA GEMM engine: column-block sparse linear,
+2-D tile-sparse matmul, the Pattention prefill path, and the BlockSparseLinear /
+BlockwiseMatMul2D modules.  bf16 bar: rel-L2 <= 2e-3 against fp64."""
+import pytest
+import torch
+
+from oracle import blocksparse as BS
+from oracle import pattention as P
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _rel(got, ref):
+    return P.rel_l2(got.float().cpu(), ref.float())
+
+
+@pytest.mark.parametrize("M,K,N,bs,active,bias", [
+    (1, 64, 256, 64, [3, 0], False),
+    (100, 256, 512, 32, [15, 2, 7, 9], True),
+    (300, 1000, 384, 128, [1, 2], True),
+    (257, 128, 1024, 64, list(range(16)), False),
+    (64, 512, 256, 64, [], True),
+])
+def test_block_sparse_linear(fsi, dev, M, K, N, bs, active, bias):
+    print(f"[case] block_sparse_linear M={M} K={K} N={N} bs={bs} n_active={len(active)}", flush=True)
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    b = torch.randn(N, generator=g).bfloat16() if bias else None
+    act = torch.tensor(active, dtype=torch.int32)
+    out = fsi.triton_block_sparse_linear(x.to(dev), w.to(dev), None if b is None else b.to(dev), act.to(dev),
+                                         block_size=bs).cpu()
+    ref = BS.block_sparse_linear_f64(x, w, b, active, bs)
+    inactive = torch.ones(N, dtype=torch.bool)
+    for a in active:
+        inactive[a * bs:(a + 1) * bs] = False
+    assert torch.all(out[:, inactive] == 0)
+    if active:
+        assert _rel(out, ref) <= TOL
+
+
+def test_block_sparse_linear_bad_block_reported(fsi, dev, monkeypatch):
+    x = torch.randn(8, 64).bfloat16().to(dev)
+    w = torch.randn(128, 64).bfloat16().to(dev)
+    monkeypatch.setenv("FSI_CHECK", "1")
+    with pytest.raises(IndexError):
+        fsi.triton_block_sparse_linear(x, w, None, torch.tensor([5], dtype=torch.int32, device=dev), block_size=64)
+
+
+@pytest.mark.parametrize("M,K,N,bk,bn,density,groups", [
+    (256, 512, 512, 128, 128, 0.25, 1),
+    (384, 512, 256, 64, 64, 0.3, 3),
+    (200, 256, 512, 64, 128, 0.5, 1),
+    (512, 1024, 1024, 128, 128, 0.1, 4),
+])
+def test_blockwise_matmul(fsi, dev, M, K, N, bk, bn, density, groups):
+    print(f"[case] blockwise_matmul M={M} K={K} N={N} tile={bk}x{bn} d={density} groups={groups}", flush=True)
+    g = torch.Generator().manual_seed(K + N)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    T = (K // bk) * (N // bn)
+    masks = torch.rand(groups, T, generator=g) < density
+    rpg = -(-M // groups) if groups > 1 else M
+    rpg = -(-rpg // 128) * 128 if groups > 1 else rpg
+    out = fsi.blockwise_matmul(x.to(dev), w.to(dev), masks.to(dev), bk, bn, rows_per_group=rpg).cpu()
+    ref = BS.blockwise_matmul_f64(x, w, masks, bk, bn, rpg)
+    assert _rel(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,rounding", [(300, "fused"), (512, "eager"), (256, "fp32")])
+def test_pattention_prefill_gemm_path(fsi, dev, M, rounding):
+    """M >= 256 with SwiGLU and down_proj-layout V takes the MFMA GEMM path."""
+    print(f"[case] prefill gemm M={M} {rounding}", flush=True)
+    g = torch.Generator().manual_seed(M)
+    D, N_p = 512, 2048
+    x = torch.randn(M, D, generator=g).bfloat16()
+    kg = (torch.randn(N_p, D, generator=g) * 0.02).bfloat16()
+    ku = (torch.randn(N_p, D, generator=g) * 0.02).bfloat16()
+    wd = (torch.randn(D, N_p, generator=g) * 0.02).bfloat16()  # down_proj layout; v = wd.t()
+    active = torch.tensor([5, 0, 31, 7, 12, 3], dtype=torch.int32)
+    vt = wd.to(dev).t()
+    got = fsi.pattention_forward(x.to(dev), kg.to(dev), ku.to(dev), vt, active.to(dev), 64, "swiglu", rounding).cpu()
+    if rounding == "fp32":
+        ref = P.pattention_fp32_act(x, kg, wd.t().contiguous(), ku, active, "swiglu", 64)
+    else:
+        ref = P.mlp_eval_forward(x, kg, ku, wd.t().contiguous(), active, 64, fused=(rounding == "fused"))
+    assert _rel(got, ref) <= TOL
+
+
+def test_block_sparse_linear_module(fsi, dev):
+    torch.manual_seed(0)
+    m = fsi.BlockSparseLinear(256, 1024, block_size=64, base_blocks=2, top_p=0.9, max_remote_blocks=4, bias=True)
+    m.eval()
+    x = torch.randn(2, 5, 256).bfloat16()
+    with torch.no_grad():
+        ref, active_ref = BS.block_sparse_forward(m, x)
+        md = m.to(dev)
+        out, aux = md(x.to(dev))
+    assert aux["active_blocks_union"] == active_ref.numel() or abs(aux["active_blocks_union"] - active_ref.numel()) <= 1
+    assert _rel(out, ref) <= 1e-2
+
+
+def test_blockwise_matmul_module(fsi, dev):
+    torch.manual_seed(1)
+    m = fsi.BlockwiseMatMul2D(256, 512, block_k=64, block_n=64, base_tiles_ratio=0.1, top_p=0.5).eval()
+    x = torch.randn(2, 3, 256).bfloat16()
+    with torch.no_grad():
+        md = m.to(dev)
+        xd = x.to(dev)
+        out, aux = md(xd)
+        mask, probs, scores, tile_v = md.route_tiles(xd)
+        ref = BS.blockwise_matmul_f64(x.reshape(-1, 256), m.weight.detach().cpu(), mask.cpu(), 64, 64, 6)
+        ctx = (probs.to(tile_v.dtype).reshape(-1, m.total_tiles) @ tile_v).view(2, 3, 16)
+        ref = ref.view(2, 3, 512) + md.out_proj(ctx).double().cpu()
+    assert aux["active_tiles"] == int(mask.sum())
+    assert _rel(out, ref) <= 1e-2

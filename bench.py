@@ -16,6 +16,7 @@ the replay stream bracket the timed region.
 Other workloads (one JSON line each, for the profiles; not the headline line):
   --workload routing      C2: fused 16-D cosine scoring + top-p selection, 8192 queries x 4096 keys
   --workload decode_attn  C4: foveal paged-KV decode attention, 32 sequences x 131072 context
+  --workload block_sparse C5: 2-D tile-sparse matmul, 4096 x 8192 by 8192 x 8192, 128 x 128 tiles
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-prefill] [--workload W]
 """
@@ -250,6 +251,67 @@ def bench_decode_attn(fsi, args, dev):
     return res
 
 
+def bench_block_sparse(fsi, args, dev):
+    M, K, N, T = 4096, 8192, 8192, 128
+    groups, nkb, nnb = M // T, K // T, N // T
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(M, K, device=dev, generator=g).bfloat16()
+    w = (torch.randn(N, K, device=dev, generator=g) * 0.01).bfloat16()
+    scores = torch.rand(groups, nkb * nnb, device=dev, generator=g)
+    lines = {}
+    for d in (0.10, 0.25, 0.50):
+        n_tiles = int(-(-d * nkb * nnb // 1))
+        top = scores.topk(n_tiles, dim=1).indices
+        mask = torch.zeros(groups, nkb * nnb, dtype=torch.bool, device=dev)
+        mask.scatter_(1, top, True)
+        outs = {}
+
+        def step(i):
+            outs["o"] = fsi.blockwise_matmul(x, w, mask, T, T, rows_per_group=T)
+
+        t, _ = time_graph(step, args.steps, args.warmup, dev)
+        per = t / args.steps
+        flops = groups * n_tiles * 2 * T * T * T
+        lines[d] = (per, flops, n_tiles)
+    per, flops, n_tiles = lines[0.25]
+    tf = flops / per / 1e12
+    res = _result("2-D tile-sparse matmul TFLOP/s (per-row-group 128x128 tile masks)", round(tf, 2), "TFLOP/s",
+                  args.steps, args.warmup, round(per * 1e3, 6), "bf16",
+                  "synthetic (seeded N(0,1) X, N(0,0.01) W, per-row-group top-d tiles of seeded uniform scores)",
+                  {"workload": "C5: X 4096 x 8192, W 8192 x 8192 in 128 x 128 tiles (4096), one mask per 128-row "
+                               "group (32 groups), density 25% (1024 tiles per group)",
+                   "densities": {f"{d:.2f}": {"ms_per_step": round(v[0] * 1e3, 4), "tiles_per_group": v[2],
+                                             "tflops": round(v[1] / v[0] / 1e12, 2),
+                                             "frac_mfma": round(v[1] / v[0] / 1e12 / BF16_PEAK_TFLOPS, 4)}
+                                 for d, v in lines.items()}})
+    res["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                       "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                       "kernel": "bsgemm_kernel<N_DIRECT, K_LIST> (+3 small list-building launches)",
+                       "flops_per_launch": flops}
+    if not args.no_cpu_baseline:
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        from oracle import blocksparse as BS
+
+        # masked dense matmul on the host for one 128-row group at 25% density
+        top = scores.topk(n_tiles, dim=1).indices
+        mask = torch.zeros(groups, nkb * nnb, dtype=torch.bool, device=dev)
+        mask.scatter_(1, top, True)
+        xc, wc = x[:T].cpu(), w.cpu()
+        em = BS.expand_tile_mask(mask[0].cpu(), N, K, T, T)
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            torch.nn.functional.linear(xc, wc * em)
+            ts.append(time.perf_counter() - t0)
+        med = sorted(ts)[1]
+        gflop = n_tiles * 2 * T ** 3
+        res["cpu_baseline"] = {"value": round(gflop / med / 1e12, 4), "unit": "TFLOP/s", "cores": cores,
+                               "kind": "port", "sample": f"masked dense F.linear on the host for one 128-row group "
+                                                         f"at 25% density (bf16), median of 3, {med * 1e3:.1f} ms"}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -259,7 +321,8 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=16)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", default="pattention", choices=["pattention", "routing", "decode_attn"])
+    ap.add_argument("--workload", default="pattention",
+                    choices=["pattention", "routing", "decode_attn", "block_sparse"])
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 512 MiB device copy (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -274,7 +337,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
     if args.workload != "pattention":
-        fn = {"routing": bench_routing, "decode_attn": bench_decode_attn}[args.workload]
+        fn = {"routing": bench_routing, "decode_attn": bench_decode_attn,
+              "block_sparse": bench_block_sparse}[args.workload]
         with torch.no_grad():
             print(json.dumps(fn(fsi, args, dev)), flush=True)
         return

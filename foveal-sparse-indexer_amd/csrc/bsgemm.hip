@@ -25,6 +25,15 @@ using namespace fsi;
 namespace {
 
 constexpr int TM = 128, TN = 128, TK = 64;
+
+// Global-load lead of the software pipeline in K-steps (1: loads for step s + 1
+// issued at the start of step s, two workgroups per CU; 2: two register stages,
+// one workgroup per CU with the full register file).
+#ifndef FSI_GEMM_DEPTH
+#define FSI_GEMM_DEPTH 1
+#endif
+constexpr int GEMM_DEPTH = FSI_GEMM_DEPTH;
+constexpr int GEMM_WG_PER_CU = GEMM_DEPTH == 1 ? 2 : 1;
 constexpr int GT = 256;  // threads per workgroup
 constexpr int SUB = 32;  // N gather granularity
 
@@ -60,7 +69,7 @@ struct GemmArgs {
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 template <int NM, int KM, int EPI>
-__global__ __launch_bounds__(GT, 2) void bsgemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TM * TK];  // [buf][A/B][row * 64 + k]
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -149,8 +158,7 @@ __global__ __launch_bounds__(GT, 2) void bsgemm_kernel(GemmArgs g) {
     }
     return true;
   };
-  u32x4_t ra[4], rb[4];
-  auto load_step = [&](int step) {
+  auto load_step = [&](int step, u32x4_t (&ra)[4], u32x4_t (&rb)[4]) {
     int64_t a_k, b_k;
     const bool kval = k_cols(step, a_k, b_k);
     if (!kval && g.err) set_error(g.err, FSI_ERR_INDEX_RANGE);
@@ -177,7 +185,7 @@ __global__ __launch_bounds__(GT, 2) void bsgemm_kernel(GemmArgs g) {
       else rb[i] = u32x4_t{0u, 0u, 0u, 0u};
     }
   };
-  auto store_step = [&](int buf) {
+  auto store_step = [&](int buf, const u32x4_t (&ra)[4], const u32x4_t (&rb)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = lrow0 + 32 * i;
@@ -195,15 +203,10 @@ __global__ __launch_bounds__(GT, 2) void bsgemm_kernel(GemmArgs g) {
 
   // wave's B fragment rows: tile columns {32 wn + 16 f} (f = 0, 1) and {64 + 32 wn + 16 (f - 2)}
   const int frow = lane & 15, fchunk = lane >> 4;
-  if (kcount > 0) {
-    load_step(0);
-    store_step(0);
-  }
-  __syncthreads();
-  for (int step = 0; step < kcount; ++step) {
-    const int buf = step & 1;
-    const int nxt = step + 1 < kcount ? step + 1 : step;  // straight-line prefetch; the last one is redundant
-    load_step(nxt);
+  // Software pipeline: LDS holds steps s and s + 1 (double buffer); with depth 2
+  // registers hold step s + 2, issued two compute steps before it is written to
+  // LDS, so the global-load latency is covered by two steps of MFMA work.
+  auto compute = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       u32x4_t fa[4], fb[4];
@@ -222,8 +225,41 @@ __global__ __launch_bounds__(GT, 2) void bsgemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fa[i], fb[f], acc[i][f]);
     }
-    if (step + 1 < kcount) store_step(buf ^ 1);
+  };
+  auto clampk = [&](int st) { return st < kcount ? st : (kcount > 0 ? kcount - 1 : 0); };
+  if (GEMM_DEPTH == 1) {
+    u32x4_t ra[4], rb[4];
+    if (kcount > 0) {
+      load_step(0, ra, rb);
+      store_step(0, ra, rb);
+    }
     __syncthreads();
+    for (int step = 0; step < kcount; ++step) {
+      load_step(clampk(step + 1), ra, rb);  // straight-line prefetch; the last one is redundant
+      compute(step & 1);
+      if (step + 1 < kcount) store_step((step & 1) ^ 1, ra, rb);
+      __syncthreads();
+    }
+  } else {
+    u32x4_t ra0[4], rb0[4], ra1[4], rb1[4];
+    if (kcount > 0) {
+      load_step(0, ra0, rb0);
+      store_step(0, ra0, rb0);
+      load_step(clampk(1), ra1, rb1);
+    }
+    __syncthreads();
+    // one iteration = two K-steps: regs1 hold step + 1, regs0 receive step + 2, and so on
+    for (int step = 0; step < kcount; step += 2) {
+      load_step(clampk(step + 2), ra0, rb0);  // redundant past the end (straight-line code)
+      compute(0);
+      if (step + 1 < kcount) store_step(1, ra1, rb1);
+      __syncthreads();
+      if (step + 1 >= kcount) break;
+      load_step(clampk(step + 3), ra1, rb1);
+      compute(1);
+      if (step + 2 < kcount) store_step(0, ra0, rb0);
+      __syncthreads();
+    }
   }
 
   // ---- epilogue: lane holds C[row 4 (lane / 16) + j][col lane % 16] of each fragment ----

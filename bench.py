@@ -41,6 +41,12 @@ D_MODEL, N_PARAM, BLOCK, BASE, REMOTE = 4096, 14336, 64, 8, 56
 DECODE_BATCH, PREFILL_TOKENS = 64, 4096
 
 
+# HBM bytes of one decode step (both kernels) measured with rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes, scaled by a 512 MiB copy (profiles/pattention_decode_prefill_8b.md):
+# (34883.8 + 18524.5) KiB x 2.000 read + 1024 KiB x 1.000 written.
+DECODE_TRAFFIC_BYTES = int(107840.6 * 1024)
+
+
 def decode_bytes(n_active: int, batch: int) -> int:
     """Algorithmic HBM bytes of one decode forward: the active rows of k_gate,
     k_up and v (3 x 64 x 4096 x 2 B per block) plus x in and y out."""
@@ -69,12 +75,26 @@ def make_layers(fsi, n_layers: int, dev):
     return layers
 
 
+EAGER = False  # --eager: launch every step directly (per-dispatch profiler counters), no graph
+
+
 def time_graph(fn_steps, steps: int, warmup: int, dev):
     """Warm up eagerly, capture `steps` steps in one graph, replay once untimed,
     then time one replay with events on the capture stream."""
     for i in range(warmup):
         fn_steps(i)
     torch.cuda.synchronize(dev)
+    if EAGER:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        s = torch.cuda.current_stream(dev)
+        t0 = time.perf_counter()
+        start.record(s)
+        for i in range(steps):
+            fn_steps(i)
+        end.record(s)
+        torch.cuda.synchronize(dev)
+        return start.elapsed_time(end) / 1e3, time.perf_counter() - t0
     graph = torch.cuda.CUDAGraph()
     stream = torch.cuda.Stream(dev)
     stream.wait_stream(torch.cuda.current_stream(dev))
@@ -323,9 +343,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="pattention",
                     choices=["pattention", "routing", "decode_attn", "block_sparse"])
+    ap.add_argument("--eager", action="store_true", help="no graph capture (for per-dispatch counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 512 MiB device copy (reference kernel for HBM counters)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the multi-GPU sharding of this path is described in DESIGN.md, not run)", file=sys.stderr)
@@ -401,8 +424,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "decode forward = patt_gateup_bf16 + patt_down_bf16 (2 launches, graph-replayed)",
+            "traffic": DECODE_TRAFFIC_BYTES if n_active == BASE + REMOTE else None,
+            "kernel": "decode forward = patt_skinny<GATEUP> + patt_skinny<DOWNT> (2 launches, graph-replayed); "
+                      "achieved = algorithmic bytes of the forward / forward duration",
             "bytes_per_launch": bytes_step,
         },
     }

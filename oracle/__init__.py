@@ -19,8 +19,13 @@ How each function is pinned (see tests/test_oracle_*.py):
   routing.cosine_scores_f32   closed form: cos(q, k) / sqrt(d) in fp64
   routing.mlp_pooled_route    fp64 recomputation of the pooled score + brute-force top-k
   routing.decode_route        brute force per sequence + reference invariant (tests/test_attention.py:37-62)
+  indexer.*                   brute-force loops (rms_norm, block pooling, additive context) and
+                              the cos / sqrt(d) closed form
   pattention.*                identity with dense SwiGLU in fp64 when every block is active, and
                               masked-dense SwiGLU for any active set
-  attention.*                 textbook softmax attention in fp64 over the gathered support
-  block_sparse.*              masked dense matmul X (W * M)^T in fp64
+  attention.decode_attention_f64
+                              single-token and equal-score closed forms, torch SDPA in fp64
+  attention.DecodeStepOracle  page pooling against an fp64 recomputation
+  blocksparse.*               brute-force loops, the dense special case (F.linear), tile ids and
+                              row groups, closed forms of the eval block selection
 """

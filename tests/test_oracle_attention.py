@@ -45,3 +45,30 @@ def test_matches_sdpa_with_gqa():
         vv = v[b][:, toks].double().repeat_interleave(2, dim=0)
         ref = F.scaled_dot_product_attention(q[b][:, None].double(), kk, vv, scale=0.25)[:, 0]
         assert torch.allclose(out[b], ref, atol=1e-12)
+
+
+def test_decode_step_oracle_page_pooling_brute_force():
+    """After a full page the oracle's page key is normalize(mean of the page's
+    rms-normed index keys) in fp32 and its page value the mean of the index
+    values (attention.py:84-91), checked against a plain fp64 recomputation."""
+    import math
+
+    import __graft_entry__
+
+    fsi = __graft_entry__.load_package()  # module classes only; no GPU work
+    torch.manual_seed(0)
+    m = fsi.FovealSparseAttention(hidden_size=32, num_heads=2, num_kv_heads=1, head_dim=64, page_size=64,
+                                  local_window_blocks=1, max_remote_pages=1, remote_capacity=1)
+    ora = A.DecodeStepOracle(m, batch=1, max_seq_len=128)
+    xs = torch.randn(64, 1, 1, 32)
+    kis, vis = [], []
+    for t in range(64):
+        ora.step(xs[t])
+        with torch.no_grad():
+            kis.append(F.rms_norm(m.indexer.k_proj(xs[t]), (16,))[0, 0].double())
+            vis.append(m.indexer.v_proj(xs[t])[0, 0].double())
+    km = sum(kis) / 64
+    assert ora.completed == 1
+    assert torch.allclose(ora.kp[0, 0].double(), km / km.norm(), atol=1e-6)
+    assert torch.allclose(ora.vp[0, 0].double(), sum(vis) / 64, atol=1e-6)
+    assert math.isclose(float(ora.kp[0, 0].norm()), 1.0, rel_tol=1e-6)

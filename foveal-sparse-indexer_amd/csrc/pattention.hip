@@ -34,6 +34,14 @@ int down_gather(const fsi::bf16_t* H, int64_t ldh, const fsi::bf16_t* wd, int64_
                 int n_active, int block_n, int M, int D, fsi::bf16_t* out, int64_t ldo, int* err, hipStream_t st);
 }  // namespace fsi_gemm
 
+namespace fsi_dec {
+size_t workspace_bytes(int64_t M, int64_t K, int64_t D, int64_t n_ch, int log2bn);
+int run(const fsi::bf16_t* x, int64_t ldx, const fsi::bf16_t* kg, const fsi::bf16_t* ku, int64_t ldk,
+        const fsi::bf16_t* vt, int64_t ldv, const int32_t* active, int64_t n_blocks_valid, int log2bn, int64_t N_p,
+        int M, int K, int64_t n_ch, int D, int activation, int rounding, fsi::bf16_t* out, int64_t ldo,
+        void* workspace, size_t ws_bytes, int* err, hipStream_t st);
+}  // namespace fsi_dec
+
 // Token count from which the tiled MFMA GEMM path replaces the skinny kernels.
 constexpr int64_t GEMM_MIN_M = 256;
 
@@ -542,7 +550,10 @@ extern "C" {
 size_t fsi_pattention_workspace_size(int64_t M, int64_t K, int64_t D_out, int64_t n_channels, int dtype) {
   if (M <= 0 || K <= 0 || D_out <= 0 || n_channels <= 0) return FSI_WORKSPACE_COUNTER_BYTES;
   if (dtype == FSI_DTYPE_F32) return workspace_f32(M, n_channels);
-  return make_plan_bf16(M, D_out, n_channels).total;
+  const size_t skinny = make_plan_bf16(M, D_out, n_channels).total;
+  // the decode path (M <= 64) needs its split partials too; block sizes >= 32 only
+  const size_t dec = fsi_dec::workspace_bytes(M, K, D_out, n_channels, 5);
+  return skinny > dec ? skinny : dec;
 }
 
 int fsi_pattention_fwd(const void* x, int64_t ldx, const void* k_gate, const void* k_up, int64_t ldk,
@@ -640,6 +651,19 @@ int fsi_pattention_fwd(const void* x, int64_t ldx, const void* k_gate, const voi
   const bf16_t* xb = static_cast<const bf16_t*>(x);
   const bf16_t* kgb = static_cast<const bf16_t*>(k_gate);
   const bf16_t* kub = static_cast<const bf16_t*>(k_up);
+
+  // Decode (up to 64 tokens): split-K MFMA kernels with every operand loaded
+  // straight into registers; falls through when its shape conditions do not hold.
+  if (M <= 64 && v_transposed && cm.log2bn >= 5) {
+    const int r = fsi_dec::run(xb, ldx, kgb, kub, ldk, static_cast<const bf16_t*>(v), ldv, active_blocks,
+                               cm.n_blocks, cm.log2bn, N_p, (int)M, (int)K, n_channels, (int)D_out, activation,
+                               rounding, static_cast<bf16_t*>(out), ldo, workspace, workspace_bytes, err, st);
+    if (r < 0) {
+      fsi_host::set_last_error("pattention: decode launch failed: %s", hipGetErrorString(hipGetLastError()));
+      return FSI_ERR_HIP;
+    }
+    if (r == 0) return FSI_OK;
+  }
 
   // Many tokens: tiled MFMA GEMMs (gathered gate/up with the SwiGLU fused in the
   // epilogue, then the down projection gathered along K).

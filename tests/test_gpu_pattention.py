@@ -106,6 +106,61 @@ def test_transposed_v_layout(fsi, dev, case):
         assert P.rel_l2(got, ref) <= BF16_TOL, rounding
 
 
+# Shapes that take the decode kernels (M <= 64, V in down_proj layout, K % 256 == 0,
+# block_n >= 32): every k-range variant (4 / 8 / 16 k-steps per gate/up wave, 4 / 8
+# per down wave), 1-4 token tiles, with and without an up projection.
+@pytest.mark.parametrize("case", [
+    (1, 256, 1024, 48, 64, 5, "swiglu"),        # one token tile, shortest ranges
+    (17, 512, 2048, 300, 32, 21, "swiglu"),     # D_out not a multiple of 32, 32-wide blocks
+    (40, 1024, 4096, 256, 64, 19, "silu"),      # no up projection
+    (64, 4096, 4096, 200, 64, 32, "gelu"),      # 8 k-steps per gate/up wave
+    (64, 2048, 16384, 2048, 64, 128, "swiglu"),  # 16 per gate/up wave, 8 per down wave
+    (33, 256, 640, 64, 64, 10, "relu2"),
+    (48, 768, 1536, 96, 128, 7, "relu"),
+])
+def test_decode_kernel_variants(fsi, dev, case):
+    M, K, N_p, D_out, block_n, n_act, act = case
+    print(f"[case] decode variant {case}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    kg = (torch.randn(N_p, K, generator=g) * 0.03).bfloat16()
+    ku = (torch.randn(N_p, K, generator=g) * 0.03).bfloat16() if act == "swiglu" else None
+    vt = (torch.randn(D_out, N_p, generator=g) * 0.03).bfloat16()
+    active = torch.randperm(N_p // block_n, generator=g)[:n_act].to(torch.int32)
+    roundings = ("eager", "fused", "fp32") if act == "swiglu" else ("fp32",)
+    for rounding in roundings:
+        got = fsi.pattention_forward(x.to(dev), kg.to(dev), None if ku is None else ku.to(dev), vt.to(dev).t(),
+                                     active.to(dev), block_n, act, rounding).cpu()
+        if rounding == "fp32":
+            ref = P.pattention_fp32_act(x, kg, vt.t().contiguous(), ku, active, act, block_n)
+        else:
+            ref = P.mlp_eval_forward(x, kg, ku, vt.t().contiguous(), active, block_n, fused=rounding == "fused")
+        err = P.rel_l2(got, ref)
+        assert got.shape == (M, D_out)
+        assert err <= BF16_TOL, (rounding, err)
+
+
+def test_decode_kernels_mask_bad_block(fsi, dev):
+    """An out-of-range block id on the decode kernels contributes nothing and is
+    reported in the error word (pattention_triton.py:151 masks rows past N_p)."""
+    from foveal_sparse_indexer_amd import _lib
+
+    M, K, N_p, D_out, block_n = 8, 512, 1024, 128, 64
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    kg = (torch.randn(N_p, K, generator=g) * 0.03).bfloat16()
+    ku = (torch.randn(N_p, K, generator=g) * 0.03).bfloat16()
+    vt = (torch.randn(D_out, N_p, generator=g) * 0.03).bfloat16()
+    _lib.error_word(dev).zero_()
+    bad = torch.tensor([3, 99, 7], dtype=torch.int32)
+    got = fsi.pattention_forward(x.to(dev), kg.to(dev), ku.to(dev), vt.to(dev).t(), bad.to(dev), block_n,
+                                 "swiglu", "fp32").cpu()
+    ref = P.pattention_fp32_act(x, kg, vt.t().contiguous(), ku, torch.tensor([3, 7]), "swiglu", block_n)
+    assert P.rel_l2(got, ref) <= BF16_TOL
+    assert int(_lib.error_word(dev)[0]) == _lib.FSI_ERR_INDEX_RANGE
+    _lib.error_word(dev).zero_()
+
+
 def test_empty_active_set_gives_zeros(fsi, dev):
     x, kg, ku, v = _mk(64, 256, 4, torch.bfloat16, seed=1)
     got = fsi.triton_pattention(x.to(dev), kg.to(dev), v.to(dev), k_up=ku.to(dev),

@@ -6,19 +6,18 @@
 // PyTorch fallback) and the eval body of FovealPattentionMLP.forward
 // (foveal_indexer/foveal_pattention.py:278-288,328-335).
 //
-// bf16 design (token counts up to a few hundred, the decode regime):
-//   phase 1  (gateup kernel): one workgroup per (64-token tile, 64-channel tile,
-//            K split).  Weights are streamed once from HBM with 16-byte loads
-//            straight into MFMA operand registers (x and K rows are both
-//            K-contiguous).  Split partial sums go to a workspace; the last
-//            workgroup to arrive on a tile (arrival counter) adds the splits in
-//            a fixed order, applies the activation with the requested rounding
-//            points and writes H = act(...) as bf16.
-//   phase 2  (down kernel): one workgroup per (64-token tile, 64-column tile of
-//            D_out, channel split).  V rows are D-contiguous, so each lane loads
-//            8-byte pieces of 16 consecutive V rows and transposes them in
-//            registers into K-contiguous MFMA operands.  Split partials are
-//            reduced the same deterministic way and rounded once to bf16.
+// bf16 has three paths, chosen per call:
+//   decode   (up to 64 tokens, V in down_proj layout, K % 256 == 0): split-K
+//            kernels of pattention_decode.hip (LDS-shared token tile, weight
+//            rows streamed once through a register ring).
+//   GEMM     (256+ tokens, SwiGLU): the tiled MFMA engine of bsgemm.hip, with
+//            the gather of active blocks in its loaders and SwiGLU fused in
+//            the gate/up epilogue.
+//   skinny   (everything else, below): one workgroup per (16 weight rows,
+//            64-token tile) stages x and the weight rows through LDS and
+//            splits K across its own waves, combined in LDS in a fixed order;
+//            the down kernel reads V or V^T the same way.  H = act(...) is
+//            written once as bf16 with the requested rounding points.
 // Gate/up are computed exactly once per (token, channel); the reference fused
 // kernel recomputes them for every 64-wide output tile
 // (pattention_triton.py:127-169).

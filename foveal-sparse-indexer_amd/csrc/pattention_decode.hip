@@ -10,7 +10,7 @@
 //      the range (tokens x K range) is staged once into LDS, so x costs one
 //      L2 read per workgroup instead of one per wave; each wave streams the
 //      16 B-per-lane gate and up rows of its tile from HBM through a
-//      register ring of 4 k-steps and feeds the 16x16x32 bf16 MFMA with x
+//      register ring of 8 k-steps and feeds the 16x16x32 bf16 MFMA with x
 //      from LDS.  The two halves are summed through LDS and one fp32 partial
 //      per K range goes to a workspace slab.
 //   2. activation: H = act(sum of gate partials, sum of up partials) with the
@@ -29,7 +29,17 @@ using namespace fsi;
 namespace {
 
 constexpr int KSTEP = 32;  // MFMA k per step
-constexpr int RING = 4;    // k-steps of weight loads in flight per wave
+#ifndef FSI_DEC_RING
+#define FSI_DEC_RING 8
+#endif
+constexpr int RING = FSI_DEC_RING;
+// Fewest workgroups (one per CU) the split choice below aims for.
+#ifndef FSI_DEC_MIN_WGS1
+#define FSI_DEC_MIN_WGS1 256
+#endif
+#ifndef FSI_DEC_MIN_WGS2
+#define FSI_DEC_MIN_WGS2 256
+#endif  // k-steps of weight loads in flight per wave (at most)
 constexpr int NKH = 2;     // waves along the k range of a workgroup (summed through LDS)
 constexpr int NCT = 4;     // 16-channel tiles per gate/up workgroup
 constexpr int DT = 2;      // 16-dim tiles per down wave
@@ -68,16 +78,24 @@ struct DecArgs {
   int* err;
 };
 
-__device__ __forceinline__ int64_t row_of(const DecArgs& a, int c) {
-  if (c >= a.n_ch) return -1;
-  if (a.active == nullptr) return c;
-  const int32_t blk = a.active[c >> a.log2bn];
-  if (blk < 0 || blk >= a.n_blocks_valid) {
-    if (a.err) set_error(a.err, FSI_ERR_INDEX_RANGE);
-    return -1;
+// Weight rows of NG channel groups c[0..NG) (16 or 32 channels each, inside
+// one block since bn >= 32): row of the group's first channel, or -1 when the
+// group is past n_ch or its block id is out of range (*bad is set then).  The
+// c[] are wave-uniform, so the block ids are scalar loads, all issued before
+// the first wait and independent of the vector loads already in flight.
+// A dense call (no block list) runs on an identity list the host writes first.
+template <int NG>
+__device__ __forceinline__ void group_rows(const DecArgs& a, const int* c, int64_t* row, bool* bad) {
+  int32_t blk[NG];
+#pragma unroll
+  for (int j = 0; j < NG; ++j) blk[j] = a.active[(c[j] < a.n_ch ? c[j] : 0) >> a.log2bn];
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    const bool in = c[j] < a.n_ch;
+    const bool ok = blk[j] >= 0 && blk[j] < a.n_blocks_valid;
+    *bad |= in && !ok;
+    row[j] = in && ok ? (static_cast<int64_t>(blk[j]) << a.log2bn) | (c[j] & ((1 << a.log2bn) - 1)) : -1;
   }
-  const int64_t r = (static_cast<int64_t>(blk) << a.log2bn) | (c & ((1 << a.log2bn) - 1));
-  return r < a.N_p ? r : -1;
 }
 
 // A [ROWS][COLS] bf16 tile (rows >= valid read row 0) staged from global memory
@@ -147,7 +165,7 @@ __global__ __launch_bounds__(GU_THREADS) void dec_gateup_kernel(DecArgs a) {
   using XTile = LdsTile<TT * 16, KR, GU_THREADS>;
   constexpr int RED_BYTES = (NKH - 1) * NCT * NACC * 4 * 64 * 4;
   __shared__ __attribute__((aligned(16))) char lds[XTile::BYTES > RED_BYTES ? XTile::BYTES : RED_BYTES];
-  static_assert(NS >= RING, "ring deeper than the k steps of a wave");
+  constexpr int RG = NS < RING ? NS : RING;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -157,23 +175,27 @@ __global__ __launch_bounds__(GU_THREADS) void dec_gateup_kernel(DecArgs a) {
   const int kw0 = s * KR;
   const int kk0 = kh * NS * KSTEP;  // this wave's first k inside the range
   const int r = lane & 15, q = lane >> 4;
-  const int64_t row = row_of(a, ct * 16 + r);
-  const bool rv = row >= 0;
-  // Loaded data is never masked (a select right after a load would wait for
-  // it): rows of invalid channels read row 0 and their outputs are zeroed.
-  const bf16_t* gp = a.kg + (rv ? row : 0) * a.ldk + kw0 + kk0 + 8 * q;
-  const bf16_t* up = HAS_UP ? a.ku + (rv ? row : 0) * a.ldk + kw0 + kk0 + 8 * q : gp;
 
   XTile xt;
   xt.load(a.x, a.ldx, a.M, kw0);
   DEC_SCHED_FENCE();
-  u32x4_t rg[RING], ru[RING];
+  bool bad = false;
+  const int cg = ct * 16;
+  int64_t row0;
+  group_rows<1>(a, &cg, &row0, &bad);
+  const int64_t row = row0 + r;
+  const bool rv = row0 >= 0 && cg + r < a.n_ch && row < a.N_p;
+  // Loaded data is never masked (a select right after a load would wait for
+  // it): rows of invalid channels read row 0 and their outputs are zeroed.
+  const bf16_t* gp = a.kg + (rv ? row : 0) * a.ldk + kw0 + kk0 + 8 * q;
+  const bf16_t* up = HAS_UP ? a.ku + (rv ? row : 0) * a.ldk + kw0 + kk0 + 8 * q : gp;
+  u32x4_t rg[RG], ru[RG];
   auto load = [&](int slot, int step) {
     rg[slot] = ld16g(gp + step * KSTEP);
     if (HAS_UP) ru[slot] = ld16g(up + step * KSTEP);
   };
 #pragma unroll
-  for (int d = 0; d < RING; ++d) load(d, d);
+  for (int d = 0; d < RG; ++d) load(d, d);
   DEC_SCHED_FENCE();
   xt.store(lds);
   __syncthreads();
@@ -195,14 +217,15 @@ __global__ __launch_bounds__(GU_THREADS) void dec_gateup_kernel(DecArgs a) {
     if (j + 1 < NS) rdx((j + 1) & 1, j + 1);
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      acc[t] = mfma16x16x32(xr[j & 1][t], rg[j % RING], acc[t]);
-      if (HAS_UP) acc[TT + t] = mfma16x16x32(xr[j & 1][t], ru[j % RING], acc[TT + t]);
+      acc[t] = mfma16x16x32(xr[j & 1][t], rg[j % RG], acc[t]);
+      if (HAS_UP) acc[TT + t] = mfma16x16x32(xr[j & 1][t], ru[j % RG], acc[TT + t]);
     }
-    if (j + RING < NS) load(j % RING, j + RING);  // resolved at compile time
+    if (j + RG < NS) load(j % RG, j + RG);  // resolved at compile time
     DEC_SCHED_FENCE();
   }
   reduce_k_halves<NACC, NCT>(lds, acc, ctl, kh, lane);
   if (kh > 0) return;
+  if (bad && lane == 0 && a.err) set_error(a.err, FSI_ERR_INDEX_RANGE);
 
   const float keep = rv ? 1.f : 0.f;
   // lane holds C[token 4 q + j][channel r] of each tile
@@ -219,38 +242,42 @@ __global__ __launch_bounds__(GU_THREADS) void dec_gateup_kernel(DecArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. H = act(sum_s G_s, sum_s U_s), four channels per thread
+// 2. H = act(sum_s G_s, sum_s U_s).  Workgroup = one 64-channel group x 16
+//    tokens, four channels per thread.  Its linear id is congruent mod 8 with
+//    the ids of the gate/up workgroups that wrote the group's partials
+//    (n_ch_pad / 64 is a multiple of 8 at the sizes that matter), so on
+//    MI355X's round-robin XCD dispatch it reads them from its own XCD's L2.
 // ---------------------------------------------------------------------------
 template <int ACT, bool HAS_UP>
 __global__ __launch_bounds__(256) void dec_act_kernel(DecArgs a) {
-  const int per_row = a.n_ch_pad / 4;
-  const int total = a.M * per_row;
-  for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
-    const int tok = i / per_row, c = (i % per_row) * 4;
-    float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
+  const int ncg = a.n_ch_pad / 64;
+  const int cg = blockIdx.x % ncg, tg = blockIdx.x / ncg;
+  const int tok = tg * 16 + (threadIdx.x >> 4);
+  if (tok >= a.M) return;
+  const int c = cg * 64 + (threadIdx.x & 15) * 4;
+  float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
 #pragma unroll 4
-    for (int s = 0; s < a.S; ++s) {
-      const int64_t off = (static_cast<int64_t>(s) * 64 + tok) * a.n_ch_pad + c;
-      const float4 gs = *reinterpret_cast<const float4*>(a.pg + off);
-      g.x += gs.x;
-      g.y += gs.y;
-      g.z += gs.z;
-      g.w += gs.w;
-      if (HAS_UP) {
-        const float4 us = *reinterpret_cast<const float4*>(a.pu + off);
-        u.x += us.x;
-        u.y += us.y;
-        u.z += us.z;
-        u.w += us.w;
-      }
+  for (int s = 0; s < a.S; ++s) {
+    const int64_t off = (static_cast<int64_t>(s) * 64 + tok) * a.n_ch_pad + c;
+    const float4 gs = *reinterpret_cast<const float4*>(a.pg + off);
+    g.x += gs.x;
+    g.y += gs.y;
+    g.z += gs.z;
+    g.w += gs.w;
+    if (HAS_UP) {
+      const float4 us = *reinterpret_cast<const float4*>(a.pu + off);
+      u.x += us.x;
+      u.y += us.y;
+      u.z += us.z;
+      u.w += us.w;
     }
-    const float h0 = pattention_act<ACT>(g.x, u.x, a.rounding);
-    const float h1 = pattention_act<ACT>(g.y, u.y, a.rounding);
-    const float h2 = pattention_act<ACT>(g.z, u.z, a.rounding);
-    const float h3 = pattention_act<ACT>(g.w, u.w, a.rounding);
-    *reinterpret_cast<u32x2_t*>(a.h + static_cast<int64_t>(tok) * a.n_ch_pad + c) =
-        u32x2_t{pack_bf16x2(h0, h1), pack_bf16x2(h2, h3)};
   }
+  const float h0 = pattention_act<ACT>(g.x, u.x, a.rounding);
+  const float h1 = pattention_act<ACT>(g.y, u.y, a.rounding);
+  const float h2 = pattention_act<ACT>(g.z, u.z, a.rounding);
+  const float h3 = pattention_act<ACT>(g.w, u.w, a.rounding);
+  *reinterpret_cast<u32x2_t*>(a.h + static_cast<int64_t>(tok) * a.n_ch_pad + c) =
+      u32x2_t{pack_bf16x2(h0, h1), pack_bf16x2(h2, h3)};
 }
 
 // ---------------------------------------------------------------------------
@@ -263,7 +290,7 @@ __global__ __launch_bounds__(DN_THREADS) void dec_down_kernel(DecArgs a) {
   using HTile = LdsTile<TT * 16, CR, DN_THREADS>;
   constexpr int RED_BYTES = (NKH - 1) * NDG * NACC * 4 * 64 * 4;
   __shared__ __attribute__((aligned(16))) char lds[HTile::BYTES > RED_BYTES ? HTile::BYTES : RED_BYTES];
-  static_assert(NS >= RING, "ring deeper than the k steps of a wave");
+  constexpr int RG = NS < RING ? NS : RING;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -280,30 +307,26 @@ __global__ __launch_bounds__(DN_THREADS) void dec_down_kernel(DecArgs a) {
     const int dim = (dt0 + d) * 16 + r;
     vp[d] = a.vt + static_cast<int64_t>(dim < a.D ? dim : 0) * a.ldv + 8 * q;
   }
-  const int bn = 1 << a.log2bn;
-  // The 32 channels of a step lie in one block (bn >= 32): one row base per
-  // step.  Channels of invalid blocks have H == 0 (their gate/up partials were
-  // zeroed), so they read row 0 of V and contribute nothing.
-  auto row_base = [&](int c) -> int64_t {
-    if (c >= a.n_ch) return 0;
-    if (a.active == nullptr) return c;
-    const int32_t blk = a.active[c >> a.log2bn];
-    if (blk < 0 || blk >= a.n_blocks_valid) return 0;
-    const int64_t rr = static_cast<int64_t>(blk) * bn + (c & (bn - 1));
-    return rr + KSTEP <= a.N_p ? rr : 0;
-  };
-
   HTile ht;
   ht.load(a.h, a.n_ch_pad, a.M, c0);
   DEC_SCHED_FENCE();
-  u32x4_t rv[RING][DT];
-  auto load = [&](int slot, int step) {
-    const int64_t rb = row_base(c0 + cc0 + step * KSTEP);
+  // Row base of each 32-channel step.  Channels of invalid blocks have H == 0
+  // (their gate/up partials were zeroed), so they read row 0 of V and add nothing.
+  int cs[NS];
+  int64_t rbs[NS];
+  bool bad = false;
 #pragma unroll
-    for (int d = 0; d < DT; ++d) rv[slot][d] = ld16g(vp[d] + rb);
+  for (int j = 0; j < NS; ++j) cs[j] = c0 + cc0 + j * KSTEP;
+  group_rows<NS>(a, cs, rbs, &bad);
+#pragma unroll
+  for (int j = 0; j < NS; ++j) rbs[j] = rbs[j] >= 0 && rbs[j] + KSTEP <= a.N_p ? rbs[j] : 0;
+  u32x4_t rv[RG][DT];
+  auto load = [&](int slot, int step) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d) rv[slot][d] = ld16g(vp[d] + rbs[step]);
   };
 #pragma unroll
-  for (int d = 0; d < RING; ++d) load(d, d);
+  for (int d = 0; d < RG; ++d) load(d, d);
   DEC_SCHED_FENCE();
   ht.store(lds);
   __syncthreads();
@@ -325,8 +348,8 @@ __global__ __launch_bounds__(DN_THREADS) void dec_down_kernel(DecArgs a) {
 #pragma unroll
     for (int t = 0; t < TT; ++t)
 #pragma unroll
-      for (int d = 0; d < DT; ++d) acc[d * TT + t] = mfma16x16x32(hr[j & 1][t], rv[j % RING][d], acc[d * TT + t]);
-    if (j + RING < NS) load(j % RING, j + RING);
+      for (int d = 0; d < DT; ++d) acc[d * TT + t] = mfma16x16x32(hr[j & 1][t], rv[j % RG][d], acc[d * TT + t]);
+    if (j + RG < NS) load(j % RG, j + RG);
     DEC_SCHED_FENCE();
   }
   reduce_k_halves<NACC, NDG>(lds, acc, dgl, kh, lane);
@@ -344,28 +367,35 @@ __global__ __launch_bounds__(DN_THREADS) void dec_down_kernel(DecArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 4. out = bf16(sum_s2 Y_s2), four dims per thread
+// 4. out = bf16(sum_s2 Y_s2).  Workgroup = one 128-dim group x 8 tokens, four
+//    dims per thread, on the XCD of the down workgroups of that dim group
+//    (as for the activation kernel).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void dec_reduce_kernel(DecArgs a) {
-  const int per_row = (a.D + 3) / 4;
-  const int total = a.M * per_row;
-  for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
-    const int tok = i / per_row, d = (i % per_row) * 4;
-    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int ndg = (a.D + 127) / 128;
+  const int dg = blockIdx.x % ndg, tg = blockIdx.x / ndg;
+  const int tok = tg * 8 + (threadIdx.x >> 5);
+  const int d = dg * 128 + (threadIdx.x & 31) * 4;
+  if (tok >= a.M || d >= a.D) return;
+  float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 8
-    for (int s = 0; s < a.S2; ++s) {
-      const float4 v = *reinterpret_cast<const float4*>(a.py + (static_cast<int64_t>(s) * 64 + tok) * a.D_pad + d);
-      y.x += v.x;
-      y.y += v.y;
-      y.z += v.z;
-      y.w += v.w;
-    }
-    bf16_t* o = a.out + static_cast<int64_t>(tok) * a.ldo + d;
-    const float vals[4] = {y.x, y.y, y.z, y.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (d + e < a.D) o[e] = f32_to_bf16(vals[e]);
+  for (int s = 0; s < a.S2; ++s) {
+    const float4 v = *reinterpret_cast<const float4*>(a.py + (static_cast<int64_t>(s) * 64 + tok) * a.D_pad + d);
+    y.x += v.x;
+    y.y += v.y;
+    y.z += v.z;
+    y.w += v.w;
   }
+  bf16_t* o = a.out + static_cast<int64_t>(tok) * a.ldo + d;
+  const float vals[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (d + e < a.D) o[e] = f32_to_bf16(vals[e]);
+}
+
+__global__ __launch_bounds__(256) void dec_iota_kernel(int32_t* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = i;
 }
 
 }  // namespace
@@ -376,7 +406,7 @@ namespace fsi_dec {
 struct Layout {
   int S, S2, n_ch_pad, D_pad;
   int NS1, NS2;  // k-steps per wave of the gate/up and down kernels
-  size_t off_pg, off_pu, off_h, off_py, total;
+  size_t off_pg, off_pu, off_h, off_py, off_ids, total;
 };
 
 bool layout(int64_t M, int64_t K, int64_t D, int64_t n_ch, int log2bn, Layout* L) {
@@ -391,7 +421,7 @@ bool layout(int64_t M, int64_t K, int64_t D, int64_t n_ch, int log2bn, Layout* L
   l.NS1 = 4;
   for (int ns : {16, 8}) {
     const int64_t kr = int64_t(ns) * NKH * KSTEP;
-    if (K % kr == 0 && wgs_per_range1 * (K / kr) >= 256) {
+    if (K % kr == 0 && wgs_per_range1 * (K / kr) >= FSI_DEC_MIN_WGS1) {
       l.NS1 = ns;
       break;
     }
@@ -399,7 +429,7 @@ bool layout(int64_t M, int64_t K, int64_t D, int64_t n_ch, int log2bn, Layout* L
   l.NS2 = 4;
   {
     const int64_t cr = 8 * NKH * KSTEP;
-    if (l.n_ch_pad % cr == 0 && wgs_per_range2 * (l.n_ch_pad / cr) >= 256) l.NS2 = 8;
+    if (l.n_ch_pad % cr == 0 && wgs_per_range2 * (l.n_ch_pad / cr) >= FSI_DEC_MIN_WGS2) l.NS2 = 8;
   }
   const int64_t S = K / (int64_t(l.NS1) * NKH * KSTEP);
   const int64_t S2 = l.n_ch_pad / (int64_t(l.NS2) * NKH * KSTEP);
@@ -416,6 +446,7 @@ bool layout(int64_t M, int64_t K, int64_t D, int64_t n_ch, int log2bn, Layout* L
   l.off_pu = take(sizeof(float) * static_cast<size_t>(S) * 64 * l.n_ch_pad);
   l.off_h = take(sizeof(bf16_t) * 64 * static_cast<size_t>(l.n_ch_pad));
   l.off_py = take(sizeof(float) * static_cast<size_t>(S2) * 64 * l.D_pad);
+  l.off_ids = take(sizeof(int32_t) * static_cast<size_t>((n_ch >> log2bn) + 1));  // identity block list
   l.total = o;
   *L = l;
   return true;
@@ -449,6 +480,12 @@ int run(const bf16_t* x, int64_t ldx, const bf16_t* kg, const bf16_t* ku, int64_
   a.ldk = ldk;
   a.vt = vt;
   a.ldv = ldv;
+  if (active == nullptr) {
+    const int nb = static_cast<int>((n_ch + (1 << log2bn) - 1) >> log2bn);
+    int32_t* ids = reinterpret_cast<int32_t*>(ws + l.off_ids);
+    dec_iota_kernel<<<static_cast<unsigned>((nb + 255) / 256), 256, 0, st>>>(ids, nb);
+    active = ids;
+  }
   a.active = active;
   a.n_blocks_valid = static_cast<int>(n_blocks_valid);
   a.log2bn = log2bn;
@@ -490,8 +527,7 @@ int run(const bf16_t* x, int64_t ldx, const bf16_t* kg, const bf16_t* ku, int64_
   }
 #undef GU
 #undef GU_NS
-  const int act_items = M * (l.n_ch_pad / 4);
-  const unsigned g2 = static_cast<unsigned>((act_items + 255) / 256);
+  const unsigned g2 = static_cast<unsigned>((l.n_ch_pad / 64) * ((M + 15) / 16));
   switch (activation) {
     case FSI_ACT_SWIGLU: dec_act_kernel<ACT_SWIGLU, true><<<g2, 256, 0, st>>>(a); break;
     case FSI_ACT_SILU: dec_act_kernel<ACT_SILU, false><<<g2, 256, 0, st>>>(a); break;
@@ -512,8 +548,8 @@ int run(const bf16_t* x, int64_t ldx, const bf16_t* kg, const bf16_t* ku, int64_
     default: DN(4); break;
   }
 #undef DN
-  const int red_items = M * ((D + 3) / 4);
-  dec_reduce_kernel<<<static_cast<unsigned>((red_items + 255) / 256), 256, 0, st>>>(a);
+  const unsigned g4 = static_cast<unsigned>(((D + 127) / 128) * ((M + 7) / 8));
+  dec_reduce_kernel<<<g4, 256, 0, st>>>(a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -41,10 +41,10 @@ D_MODEL, N_PARAM, BLOCK, BASE, REMOTE = 4096, 14336, 64, 8, 56
 DECODE_BATCH, PREFILL_TOKENS = 64, 4096
 
 
-# HBM bytes of one decode step (both kernels) measured with rocprofv3 FETCH_SIZE and
-# WRITE_SIZE passes, scaled by a 512 MiB copy (profiles/pattention_decode_prefill_8b.md):
-# (34883.8 + 18524.5) KiB x 2.000 read + 1024 KiB x 1.000 written.
-DECODE_TRAFFIC_BYTES = int(107840.6 * 1024)
+# HBM bytes of one decode step (all four kernels) measured with rocprofv3 FETCH_SIZE
+# and WRITE_SIZE passes, scaled by a 512 MiB copy (profiles/pattention_decode_prefill_8b.md):
+# (34872.4 + 4129.5 + 18477.7 + 4109.0) KiB x 1.9997 read + 17408 KiB x 1.000 written.
+DECODE_TRAFFIC_BYTES = int(140566.8 * 1024)
 
 
 def decode_bytes(n_active: int, batch: int) -> int:
@@ -425,7 +425,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": DECODE_TRAFFIC_BYTES if n_active == BASE + REMOTE else None,
-            "kernel": "decode forward = patt_skinny<GATEUP> + patt_skinny<DOWNT> (2 launches, graph-replayed); "
+            "kernel": "decode forward = dec_gateup + dec_act + dec_down + dec_reduce (4 launches, graph-replayed); "
                       "achieved = algorithmic bytes of the forward / forward duration",
             "bytes_per_launch": bytes_step,
         },

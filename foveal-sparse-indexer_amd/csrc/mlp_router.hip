@@ -6,8 +6,8 @@
 //   top    = topk(s[base:], remote_blocks)                      (descending; ties -> lower index)
 //   active = [0, 1, ..., base-1] ++ (top + base)
 //
-// Rounding points mirror torch's CPU bf16 ops: the token mean accumulates
-// sequentially in fp32 (torch's outer-dim reduction order) and rounds once;
+// Rounding points mirror torch's CPU bf16 ops: the token mean accumulates in
+// fp32 (chunked, fixed order) and rounds once;
 // the projection and scores accumulate in fp32 and round once; rms_norm runs in
 // fp32 with eps = FLT_EPSILON and rounds once.
 #include "fsi_common.h"
@@ -18,21 +18,38 @@ namespace {
 
 constexpr int MAX_INDEX_DIM = 64;
 
-// Sequential-over-tokens mean of x[:, d], rounded to the storage dtype.
+// Mean of x[:, d] over the tokens, rounded to the storage dtype.  The tokens
+// are cut into at most MEAN_CHUNKS chunks; each chunk is summed sequentially in
+// fp32 (one thread per column, coalesced across the wave), then the chunk sums
+// are added in chunk order (deterministic).  The order differs from torch's
+// CPU reduction only in fp32 rounding, below one bf16 ulp of the mean.
+constexpr int MEAN_CHUNKS = 64;
+
 template <bool BF16>
-__global__ void token_mean(const void* __restrict__ x, int64_t ldx, int M, int D, float* __restrict__ xm) {
-  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void token_partial(const void* __restrict__ x, int64_t ldx, int M, int D,
+                                                     int rows_per_chunk, float* __restrict__ part) {
+  const int d = blockIdx.x * 256 + threadIdx.x;
+  if (d >= D) return;
+  const int m0 = blockIdx.y * rows_per_chunk;
+  const int m1 = min(M, m0 + rows_per_chunk);
+  float acc = 0.f;
+#pragma unroll 16
+  for (int m = m0; m < m1; ++m) {
+    const int64_t i = static_cast<int64_t>(m) * ldx + d;
+    acc += BF16 ? bf16_to_f32(static_cast<const bf16_t*>(x)[i]) : static_cast<const float*>(x)[i];
+  }
+  part[static_cast<int64_t>(blockIdx.y) * D + d] = acc;
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void token_mean(const float* __restrict__ part, int n_chunks, int M, int D,
+                                                  float* __restrict__ xm) {
+  const int d = blockIdx.x * 256 + threadIdx.x;
   if (d >= D) return;
   float acc = 0.f;
-  if (BF16) {
-    const bf16_t* p = static_cast<const bf16_t*>(x) + d;
-    for (int m = 0; m < M; ++m) acc += bf16_to_f32(p[static_cast<int64_t>(m) * ldx]);
-    xm[d] = round_bf16(acc / static_cast<float>(M));
-  } else {
-    const float* p = static_cast<const float*>(x) + d;
-    for (int m = 0; m < M; ++m) acc += p[static_cast<int64_t>(m) * ldx];
-    xm[d] = acc / static_cast<float>(M);
-  }
+  for (int c = 0; c < n_chunks; ++c) acc += part[static_cast<int64_t>(c) * D + d];
+  const float mean = acc / static_cast<float>(M);
+  xm[d] = BF16 ? round_bf16(mean) : mean;
 }
 
 template <bool BF16>
@@ -96,7 +113,8 @@ __global__ __launch_bounds__(256) void pooled_route(const float* __restrict__ xm
 extern "C" {
 
 FSI_API size_t fsi_mlp_router_workspace_size(int64_t D, int64_t n_blocks) {
-  return FSI_WORKSPACE_COUNTER_BYTES + fsi_host::align_up(sizeof(float) * D, 256) + fsi_host::align_up(sizeof(float) * n_blocks, 256);
+  return FSI_WORKSPACE_COUNTER_BYTES + fsi_host::align_up(sizeof(float) * D, 256) +
+         fsi_host::align_up(sizeof(float) * n_blocks, 256) + fsi_host::align_up(sizeof(float) * MEAN_CHUNKS * D, 256);
 }
 
 FSI_API int fsi_mlp_router(const void* x, int64_t ldx, int64_t M, int64_t D, const void* q_proj_w, int64_t index_dim,
@@ -121,15 +139,21 @@ FSI_API int fsi_mlp_router(const void* x, int64_t ldx, int64_t M, int64_t D, con
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   float* xm = reinterpret_cast<float*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES);
   float* scratch = reinterpret_cast<float*>(reinterpret_cast<char*>(xm) + fsi_host::align_up(sizeof(float) * D, 256));
-  const dim3 g1((unsigned)((D + 63) / 64));
+  float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + fsi_host::align_up(sizeof(float) * n_blocks, 256));
+  const int rows = static_cast<int>((M + MEAN_CHUNKS - 1) / MEAN_CHUNKS);
+  const int n_chunks = static_cast<int>((M + rows - 1) / rows);
+  const dim3 gp((unsigned)((D + 255) / 256), (unsigned)n_chunks);
+  const dim3 g1((unsigned)((D + 255) / 256));
   if (dtype == FSI_DTYPE_BF16) {
-    token_mean<true><<<g1, 64, 0, st>>>(x, ldx, (int)M, (int)D, xm);
+    token_partial<true><<<gp, 256, 0, st>>>(x, ldx, (int)M, (int)D, rows, part);
+    token_mean<true><<<g1, 256, 0, st>>>(part, n_chunks, (int)M, (int)D, xm);
     FSI_HIP_LAUNCH_CHECK("mlp_router mean");
     pooled_route<true><<<1, 256, 0, st>>>(xm, (int)D, q_proj_w, (int)index_dim, block_keys, (int)n_blocks,
                                           (int)base_blocks, (int)remote_blocks, score_scale, out_active, out_scores,
                                           scratch);
   } else {
-    token_mean<false><<<g1, 64, 0, st>>>(x, ldx, (int)M, (int)D, xm);
+    token_partial<false><<<gp, 256, 0, st>>>(x, ldx, (int)M, (int)D, rows, part);
+    token_mean<false><<<g1, 256, 0, st>>>(part, n_chunks, (int)M, (int)D, xm);
     FSI_HIP_LAUNCH_CHECK("mlp_router mean");
     pooled_route<false><<<1, 256, 0, st>>>(xm, (int)D, q_proj_w, (int)index_dim, block_keys, (int)n_blocks,
                                            (int)base_blocks, (int)remote_blocks, score_scale, out_active, out_scores,

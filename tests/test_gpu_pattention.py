@@ -117,6 +117,7 @@ def test_transposed_v_layout(fsi, dev, case):
     (64, 2048, 16384, 2048, 64, 128, "swiglu"),  # 16 per gate/up wave, 8 per down wave
     (33, 256, 640, 64, 64, 10, "relu2"),
     (48, 768, 1536, 96, 128, 7, "relu"),
+    (16, 512, 1024, 200, 64, None, "swiglu"),   # dense: no block list
 ])
 def test_decode_kernel_variants(fsi, dev, case):
     M, K, N_p, D_out, block_n, n_act, act = case
@@ -126,15 +127,16 @@ def test_decode_kernel_variants(fsi, dev, case):
     kg = (torch.randn(N_p, K, generator=g) * 0.03).bfloat16()
     ku = (torch.randn(N_p, K, generator=g) * 0.03).bfloat16() if act == "swiglu" else None
     vt = (torch.randn(D_out, N_p, generator=g) * 0.03).bfloat16()
-    active = torch.randperm(N_p // block_n, generator=g)[:n_act].to(torch.int32)
+    active = None if n_act is None else torch.randperm(N_p // block_n, generator=g)[:n_act].to(torch.int32)
     roundings = ("eager", "fused", "fp32") if act == "swiglu" else ("fp32",)
     for rounding in roundings:
         got = fsi.pattention_forward(x.to(dev), kg.to(dev), None if ku is None else ku.to(dev), vt.to(dev).t(),
-                                     active.to(dev), block_n, act, rounding).cpu()
+                                     None if active is None else active.to(dev), block_n, act, rounding).cpu()
         if rounding == "fp32":
             ref = P.pattention_fp32_act(x, kg, vt.t().contiguous(), ku, active, act, block_n)
         else:
-            ref = P.mlp_eval_forward(x, kg, ku, vt.t().contiguous(), active, block_n, fused=rounding == "fused")
+            all_blocks = torch.arange(N_p // block_n) if active is None else active
+            ref = P.mlp_eval_forward(x, kg, ku, vt.t().contiguous(), all_blocks, block_n, fused=rounding == "fused")
         err = P.rel_l2(got, ref)
         assert got.shape == (M, D_out)
         assert err <= BF16_TOL, (rounding, err)

@@ -36,6 +36,9 @@ constexpr int GEMM_DEPTH = FSI_GEMM_DEPTH;
 constexpr int GEMM_WG_PER_CU = GEMM_DEPTH == 1 ? 2 : 1;
 constexpr int GT = 256;  // threads per workgroup
 constexpr int SUB = 32;  // N gather granularity
+// K-gathered problems keep the column offset of every active K block in LDS
+// (a per-step global lookup would make each step wait for all loads in flight).
+constexpr int KTAB_MAX = 2048;
 
 enum NMode { N_DIRECT = 0, N_GATHER = 1, N_DUAL = 2 };
 enum KMode { K_DENSE = 0, K_GATHER_B = 1, K_LIST = 2 };
@@ -68,10 +71,23 @@ struct GemmArgs {
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
+// ktab[i] = first B column of active K block i, or -1 when its id is out of range.
+__device__ __forceinline__ void fill_ktab(const GemmArgs& g, int32_t* ktab, int nthreads) {
+  for (int i = threadIdx.x; i < g.n_blocks; i += nthreads) {
+    const int blk = g.blocks ? g.blocks[i] : i;
+    ktab[i] = (blk < 0 || static_cast<int64_t>(blk + 1) * g.block > g.n_rows_total) ? -1 : blk * g.block;
+  }
+}
+
 template <int NM, int KM, int EPI>
 __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][TM * TK];  // [buf][A/B][row * 64 + k]
+  __shared__ int32_t ktab[KM == K_GATHER_B ? KTAB_MAX : 1];
   const int tid = threadIdx.x;
+  if (KM == K_GATHER_B) {
+    fill_ktab(g, ktab, GT);
+    __syncthreads();
+  }
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
@@ -145,14 +161,13 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
       a_k = b_k = g.klist[koff + step];
     } else if (KM == K_GATHER_B) {
       const int per = g.block / TK;
-      const int bi = step / per;
-      const int blk = g.blocks ? g.blocks[bi] : bi;
+      const int col = ktab[step / per];
       a_k = static_cast<int64_t>(step) * TK;
-      if (blk < 0 || static_cast<int64_t>(blk + 1) * g.block > g.n_rows_total) {
+      if (col < 0) {
         b_k = 0;
         return false;
       }
-      b_k = static_cast<int64_t>(blk) * g.block + (step % per) * TK;
+      b_k = col + (step % per) * TK;
     } else {
       a_k = b_k = static_cast<int64_t>(step) * TK;
     }
@@ -304,6 +319,256 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile variant for many-row problems (prefill): 256 x 256 tile, 4 waves
+// of 128 x 128 (one wave per SIMD, accumulators in AGPRs), K in 32-wide
+// steps.  A wave reads 16 fragments per 64 MFMAs from LDS (vs. 8 per 16 in the
+// 128 x 128 kernel), and a tile re-reads A and B half as often from L2.
+// LDS: 2 stages x (A + B) x 16 KiB.
+// Workgroups with consecutive logical ids share an XCD (and its L2); a
+// logical id walks down M first, so the B tile of an XCD's group stays hot.
+// ---------------------------------------------------------------------------
+#ifndef FSI_GEMM_BIG_WAVES
+#define FSI_GEMM_BIG_WAVES 8
+#endif
+#ifndef FSI_GEMM_BIG_PIPE
+#define FSI_GEMM_BIG_PIPE 1
+#endif
+#ifndef FSI_GEMM_BIG_BK
+#define FSI_GEMM_BIG_BK 64
+#endif
+constexpr int BM = 256, BN = 256, BK = FSI_GEMM_BIG_BK;
+constexpr int BCPR = BK / 8;                 // 16-byte chunks per LDS row
+constexpr int BWN = FSI_GEMM_BIG_WAVES / 2;  // waves along N (2 along M)
+constexpr int BT = 64 * 2 * BWN;             // threads per workgroup
+constexpr int BHW = 128 / BWN;               // columns of each tile half per wave
+constexpr int BNF = 2 * BHW / 16;            // B fragments per wave
+constexpr int BLPT = BM * BCPR / BT;        // 16-byte A (and B) chunks per thread and step
+
+// Conflict-free fragment reads: 32-wide rows XOR the chunk with row bits 2-3,
+// 64-wide rows with row bits 1-3.
+__device__ __forceinline__ int swzb(int row, int chunk) {
+  return BCPR == 4 ? chunk ^ ((row >> 2) & 3) : chunk ^ ((row >> 1) & 7);
+}
+
+__device__ __forceinline__ int xcd_group_id(int w, int n) {
+  if ((n & 7) != 0) return w;
+  return (w & 7) * (n >> 3) + (w >> 3);
+}
+
+template <int NM, int KM, int EPI>
+__global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
+  static_assert(KM != K_LIST, "tile lists run on the 128 x 128 kernel");
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][BM * BK];  // [stage][A/B][row * 32 + k]
+  __shared__ int32_t ktab[KM == K_GATHER_B ? KTAB_MAX : 1];
+  const int tid = threadIdx.x;
+  if (KM == K_GATHER_B) {
+    fill_ktab(g, ktab, BT);
+    __syncthreads();
+  }
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / BWN, wn = wave % BWN;
+
+  const int lid = xcd_group_id(blockIdx.x, gridDim.x);
+  const int mt = lid % g.m_tiles, nt = lid / g.m_tiles;
+  const int kcount = KM == K_GATHER_B ? g.n_blocks * (g.block / BK) : (g.K + BK - 1) / BK;
+  const int m0 = mt * BM;
+
+  // ---- per 32-column sub-block: B row base and C column base ----------------
+  int64_t brow[8];
+  int ccol[8];
+  bool bval[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    if (NM == N_DUAL) {
+      // tile nt covers 128 channels: tile columns [gate 128 | up 128]
+      const int ch = nt * 128 + (s & 3) * SUB;
+      const int bi = ch / g.block;
+      const int blk = bi < g.n_blocks ? (g.blocks ? g.blocks[bi] : bi) : -1;
+      const int64_t row = static_cast<int64_t>(blk) * g.block + ch % g.block;
+      bval[s] = blk >= 0 && row + SUB <= g.n_rows_total;
+      brow[s] = bval[s] ? row : 0;
+      ccol[s] = ch;
+    } else if (NM == N_GATHER) {
+      const int col = nt * BN + s * SUB;
+      const int bi = col / g.block;
+      const int blk = bi < g.n_blocks ? (g.blocks ? g.blocks[bi] : bi) : -1;
+      const int64_t row = static_cast<int64_t>(blk) * g.block + col % g.block;
+      bval[s] = blk >= 0 && row + SUB <= g.n_rows_total;
+      brow[s] = bval[s] ? row : 0;
+      ccol[s] = g.scatter_c ? static_cast<int>(row) : col;
+    } else {
+      const int col = nt * BN + s * SUB;
+      bval[s] = col < g.N;
+      brow[s] = bval[s] ? col : 0;
+      ccol[s] = col;
+    }
+    if (NM != N_DIRECT && !bval[s] && g.err && ((NM == N_DUAL ? nt * 128 + (s & 3) * SUB : nt * BN + s * SUB) < g.N))
+      set_error(g.err, FSI_ERR_INDEX_RANGE);
+  }
+
+  // ---- global -> register staging: chunk q = tid + BT i: row q / BCPR, 16-byte chunk q % BCPR
+  const int lrow0 = tid / BCPR, lchunk = tid % BCPR;
+  auto k_cols = [&](int step, int64_t& a_k, int64_t& b_k) -> bool {
+    if (KM == K_GATHER_B) {
+      const int per = g.block / BK;
+      const int col = ktab[step / per];
+      a_k = static_cast<int64_t>(step) * BK;
+      if (col < 0) {
+        b_k = 0;
+        return false;
+      }
+      b_k = col + (step % per) * BK;
+    } else {
+      a_k = b_k = static_cast<int64_t>(step) * BK;
+    }
+    return true;
+  };
+  auto load_step = [&](int step, u32x4_t (&ra)[BLPT], u32x4_t (&rb)[BLPT]) {
+    int64_t a_k, b_k;
+    const bool kval = k_cols(step, a_k, b_k);
+    if (!kval && g.err) set_error(g.err, FSI_ERR_INDEX_RANGE);
+    const int kk = static_cast<int>((KM == K_DENSE ? a_k : 0) + lchunk * 8);
+    const bool kin = KM == K_DENSE ? (kk < g.K) : true;
+#pragma unroll
+    for (int i = 0; i < BLPT; ++i) {
+      const int r = lrow0 + (BT / BCPR) * i;
+      const int m = m0 + r;
+      if (m < g.M && kin) ra[i] = *reinterpret_cast<const u32x4_t*>(g.A + static_cast<int64_t>(m) * g.lda + a_k + lchunk * 8);
+      else ra[i] = u32x4_t{0u, 0u, 0u, 0u};
+      const int s = r / SUB;
+      const bf16_t* bp = (NM == N_DUAL && s >= 4) ? g.B1 : g.B0;
+      const int64_t row = brow[s] + (r % SUB);
+      const bool rin = NM != N_DIRECT || row < g.N;
+      if (bval[s] && rin && kin && kval)
+        rb[i] = *reinterpret_cast<const u32x4_t*>(bp + row * g.ldb + b_k + lchunk * 8);
+      else rb[i] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_step = [&](int buf, const u32x4_t (&ra)[BLPT], const u32x4_t (&rb)[BLPT]) {
+#pragma unroll
+    for (int i = 0; i < BLPT; ++i) {
+      const int r = lrow0 + (BT / BCPR) * i;
+      const int off = r * BK + swzb(r, lchunk) * 8;
+      *reinterpret_cast<u32x4_t*>(&lds[buf][0][off]) = ra[i];
+      *reinterpret_cast<u32x4_t*>(&lds[buf][1][off]) = rb[i];
+    }
+  };
+
+  f32x4_t acc[8][BNF];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < BNF; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // wave fragments: A rows 128 wm + 16 i; B tile columns {BHW wn + 16 f} (f < BNF / 2)
+  // and {128 + BHW wn + 16 (f - BNF / 2)}: a gate column and its up column share a lane
+  const int frow = lane & 15, fchunk = lane >> 4;
+  auto bcol = [&](int f) { return f < BNF / 2 ? BHW * wn + 16 * f : 128 + BHW * wn + 16 * (f - BNF / 2); };
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      u32x4_t fa[8], fb[BNF];
+#pragma unroll
+      for (int f = 0; f < BNF; ++f) {
+        const int c = bcol(f) + frow;
+        fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[buf][1][c * BK + swzb(c, 4 * ks + fchunk) * 8]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 128 * wm + 16 * i + frow;
+        fa[i] = *reinterpret_cast<const u32x4_t*>(&lds[buf][0][r * BK + swzb(r, 4 * ks + fchunk) * 8]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int f = 0; f < BNF; ++f) acc[i][f] = mfma16x16x32(fa[i], fb[f], acc[i][f]);
+    }
+  };
+
+#if FSI_GEMM_BIG_PIPE == 2
+  // Loads run three K-steps ahead: at iteration s the registers of step s + 1
+  // go to the free LDS stage, step s + 3 is issued into them, then step s is
+  // computed.  A load has two steps of MFMA work to arrive.
+  u32x4_t ra0[BLPT], rb0[BLPT], ra1[BLPT], rb1[BLPT];
+  if (kcount > 0) {
+    load_step(0, ra0, rb0);
+    store_step(0, ra0, rb0);
+  }
+  if (kcount > 1) load_step(1, ra1, rb1);
+  if (kcount > 2) load_step(2, ra0, rb0);
+  __syncthreads();
+  int step = 0;
+  for (; step + 1 < kcount; step += 2) {
+    store_step(1, ra1, rb1);
+    if (step + 3 < kcount) load_step(step + 3, ra1, rb1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    if (step + 2 < kcount) store_step(0, ra0, rb0);
+    if (step + 4 < kcount) load_step(step + 4, ra0, rb0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+  }
+  if (step < kcount) compute(0);  // odd step count: the last step sits in stage 0
+#else
+  // loads for step s + 1 are issued before step s is computed and written to
+  // the other LDS stage after it
+  u32x4_t ra0[BLPT], rb0[BLPT];
+  if (kcount > 0) {
+    load_step(0, ra0, rb0);
+    store_step(0, ra0, rb0);
+  }
+  __syncthreads();
+  for (int step = 0; step < kcount; ++step) {
+    if (step + 1 < kcount) load_step(step + 1, ra0, rb0);
+    compute(step & 1);
+    if (step + 1 < kcount) store_step((step & 1) ^ 1, ra0, rb0);
+    __syncthreads();
+  }
+#endif
+
+  // ---- epilogue: lane holds C[row 4 (lane / 16) + j][col lane % 16] of each fragment ----
+  const int crow0 = m0 + 128 * wm + 4 * (lane >> 4);
+  if (EPI == EPI_SWIGLU) {
+#pragma unroll
+    for (int f = 0; f < BNF / 2; ++f) {
+      const int ch = ccol[0] + BHW * wn + 16 * f + frow;  // ccol[0] = first channel of the tile
+      if (ch >= g.N) continue;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = crow0 + 16 * i + j;
+          if (m >= g.M) continue;
+          const float h = pattention_act<ACT_SWIGLU>(acc[i][f][j], acc[i][f + BNF / 2][j], g.rounding);
+          g.C[static_cast<int64_t>(m) * g.ldc + ch] = f32_to_bf16(h);
+        }
+    }
+  } else {
+#pragma unroll
+    for (int f = 0; f < BNF; ++f) {
+      const int tc = bcol(f);
+      const int s = tc / SUB;
+      if (NM != N_DIRECT && !bval[s]) continue;
+      const int col = ccol[s] + (tc % SUB) + frow;
+      if (NM == N_DIRECT && col >= g.N) continue;
+      const float bv = g.bias ? bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + frow : col]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = crow0 + 16 * i + j;
+          if (m >= g.M) continue;
+          g.C[static_cast<int64_t>(m) * g.ldc + col] = f32_to_bf16(acc[i][f][j] + bv);
+        }
+    }
+  }
+}
+
 // Zero the columns of C whose column block is inactive (BlockSparseLinear's
 // torch.zeros + scatter); mask[b] != 0 marks active block b.
 __global__ __launch_bounds__(256) void zero_inactive_kernel(bf16_t* __restrict__ C, int64_t ldc, int M, int N,
@@ -408,6 +673,27 @@ hipError_t launch(const GemmArgs& a, unsigned grid, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Rows from which the 256 x 256 kernel replaces the 128 x 128 one.
+#ifndef FSI_GEMM_BIG_MIN_M
+#define FSI_GEMM_BIG_MIN_M 256
+#endif
+constexpr int BIG_MIN_M = FSI_GEMM_BIG_MIN_M;
+
+// Sets the tile grid for the kernel `big` selects and launches it.
+template <int NM, int KM, int EPI>
+hipError_t launch_tiled(GemmArgs& a, bool big, hipStream_t st) {
+  const int tm = big ? BM : TM;
+  const int tn = NM == N_DUAL ? (big ? BN / 2 : TN / 2) : (big ? BN : TN);
+  a.m_tiles = (a.M + tm - 1) / tm;
+  a.n_tiles = (a.N + tn - 1) / tn;
+  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
+  if (big) {
+    bsgemm_big_kernel<NM, KM, EPI><<<grid, BT, 0, st>>>(a);
+    return hipGetLastError();
+  }
+  return launch<NM, KM, EPI>(a, grid, st);
+}
+
 }  // namespace
 
 namespace fsi_gemm {
@@ -432,18 +718,16 @@ int gateup_swiglu(const bf16_t* x, int64_t ldx, const bf16_t* kg, const bf16_t* 
   a.n_blocks = n_active;
   a.block = block_n;
   a.n_rows_total = N_p;
-  a.m_tiles = (M + TM - 1) / TM;
-  a.n_tiles = (a.N + 63) / 64;
   a.act = ACT_SWIGLU;
   a.rounding = rounding;
   a.err = err;
-  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
-  return launch<N_DUAL, K_DENSE, EPI_SWIGLU>(a, grid, st) == hipSuccess ? 0 : -1;
+  return launch_tiled<N_DUAL, K_DENSE, EPI_SWIGLU>(a, M >= BIG_MIN_M, st) == hipSuccess ? 0 : -1;
 }
 
 // out[M, D] = H[M, 64 n_active] W_down[:, S]^T with W_down [D, N_p] (row stride ldw)
 int down_gather(const bf16_t* H, int64_t ldh, const bf16_t* wd, int64_t ldw, int N_p, const int32_t* blocks,
                 int n_active, int block_n, int M, int D, bf16_t* out, int64_t ldo, int* err, hipStream_t st) {
+  if (n_active > KTAB_MAX) return 1;  // more active blocks than the LDS table holds
   GemmArgs a{};
   a.A = H;
   a.B0 = a.B1 = wd;
@@ -458,11 +742,8 @@ int down_gather(const bf16_t* H, int64_t ldh, const bf16_t* wd, int64_t ldw, int
   a.n_blocks = n_active;
   a.block = block_n;
   a.n_rows_total = N_p;
-  a.m_tiles = (M + TM - 1) / TM;
-  a.n_tiles = (D + TN - 1) / TN;
   a.err = err;
-  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
-  return launch<N_DIRECT, K_GATHER_B, EPI_STORE>(a, grid, st) == hipSuccess ? 0 : -1;
+  return launch_tiled<N_DIRECT, K_GATHER_B, EPI_STORE>(a, M >= BIG_MIN_M, st) == hipSuccess ? 0 : -1;
 }
 
 }  // namespace fsi_gemm
@@ -526,11 +807,8 @@ FSI_API int fsi_block_sparse_linear(const void* x, int64_t ldx, const void* w, i
   a.block = (int)block_size;
   a.n_rows_total = (int)N;
   a.scatter_c = 1;
-  a.m_tiles = (int)((M + TM - 1) / TM);
-  a.n_tiles = (int)((a.N + TN - 1) / TN);
   a.err = err;
-  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
-  const hipError_t e = launch<N_GATHER, K_DENSE, EPI_STORE>(a, grid, st);
+  const hipError_t e = launch_tiled<N_GATHER, K_DENSE, EPI_STORE>(a, M >= BIG_MIN_M, st);
   FSI_CHECK_ARG(e == hipSuccess, FSI_ERR_HIP, "block_sparse_linear: launch failed: %s", hipGetErrorString(e));
   return FSI_OK;
 }

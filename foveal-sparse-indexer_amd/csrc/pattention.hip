@@ -43,6 +43,8 @@ int run(const fsi::bf16_t* x, int64_t ldx, const fsi::bf16_t* kg, const fsi::bf1
 
 // Token count from which the tiled MFMA GEMM path replaces the skinny kernels.
 constexpr int64_t GEMM_MIN_M = 256;
+// Most active blocks the K-gathered down GEMM keeps in its LDS table.
+constexpr int64_t GEMM_MAX_BLOCKS = 2048;
 
 using namespace fsi;
 
@@ -667,6 +669,7 @@ int fsi_pattention_fwd(const void* x, int64_t ldx, const void* k_gate, const voi
   // Many tokens: tiled MFMA GEMMs (gathered gate/up with the SwiGLU fused in the
   // epilogue, then the down projection gathered along K).
   if (M >= GEMM_MIN_M && activation == FSI_ACT_SWIGLU && kub && block_n % 64 == 0 && N_p % block_n == 0 &&
+      (active_blocks ? n_active : N_p / block_n) <= GEMM_MAX_BLOCKS &&
       v_transposed && ldv % 8 == 0 && (uintptr_t)v % 16 == 0 && ldo % 8 == 0 && (uintptr_t)out % 16 == 0) {
     const int n_act = active_blocks ? (int)n_active : (int)(N_p / block_n);
     if (fsi_gemm::gateup_swiglu(xb, ldx, kgb, kub, ldk, (int)N_p, active_blocks, n_act, (int)block_n, (int)M,

@@ -569,6 +569,219 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS variant of the 256 x 256 kernel.  Operands go from global
+// memory straight into LDS with global_load_lds_dwordx4 (lane l's 16 bytes
+// land at M0 + 16 l), so the pipeline holds four LDS stages without staging
+// registers and loads run three 32-wide K-steps ahead of the MFMAs.  Each wave
+// loads whole KiB of a stage: 16 rows x 64 bytes, the lanes' source chunks
+// permuted so that the LDS image carries the conflict-free XOR swizzle.
+// Rows that must read as zero (past M, past N, inactive blocks) are never
+// masked on the load side: they read a valid row, and the epilogue drops or
+// zeroes what they produce.  Dense K only, K % 32 == 0.
+// ---------------------------------------------------------------------------
+// Direct-to-LDS loads for the 256 x 256 tiles (0: register-staged kernel).
+#ifndef FSI_GEMM_DMA
+#define FSI_GEMM_DMA 1
+#endif
+#ifndef FSI_GEMM_DMA_SCHED
+#define FSI_GEMM_DMA_SCHED 1
+#endif
+constexpr int DK = 32, DSTAGES = 4, DTHREADS = 512;
+constexpr int DLOADS = 4;  // global_load_lds per wave and K-step: 2 KiB of A, 2 KiB of B
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+// s_waitcnt vmcnt(N) leaving expcnt and lgkmcnt alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier without the release fence of __syncthreads(), which would
+// wait for every direct-to-LDS load in flight.  The caller has waited for the
+// loads the next step reads; the memory clobber keeps the compiler from moving
+// LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int NM, int KM, int EPI>
+__global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
+  static_assert(KM != K_LIST, "tile lists run on the 128 x 128 kernel");
+  __shared__ __attribute__((aligned(1024))) bf16_t lds[DSTAGES][2][BM * DK];  // [stage][A/B][row * 32 + k]
+  __shared__ int32_t ktab[KM == K_GATHER_B ? KTAB_MAX : 1];
+  const int tid = threadIdx.x;
+  if (KM == K_GATHER_B) {
+    fill_ktab(g, ktab, DTHREADS);
+    __syncthreads();
+  }
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves of 128 x 64
+
+  const int lid = xcd_group_id(blockIdx.x, gridDim.x);
+  const int mt = lid % g.m_tiles, nt = lid / g.m_tiles;
+  const int kcount = KM == K_GATHER_B ? g.n_blocks * (g.block / DK) : g.K / DK;
+  const int m0 = mt * BM;
+
+  // ---- per 32-column sub-block: B row base and C column base ----------------
+  int64_t brow[8];
+  int ccol[8];
+  bool bval[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    if (NM == N_DUAL) {
+      const int ch = nt * 128 + (s & 3) * SUB;  // tile columns [gate 128 | up 128]
+      const int bi = ch / g.block;
+      const int blk = bi < g.n_blocks ? (g.blocks ? g.blocks[bi] : bi) : -1;
+      const int64_t row = static_cast<int64_t>(blk) * g.block + ch % g.block;
+      bval[s] = blk >= 0 && row + SUB <= g.n_rows_total;
+      brow[s] = bval[s] ? row : 0;
+      ccol[s] = ch;
+    } else if (NM == N_GATHER) {
+      const int col = nt * BN + s * SUB;
+      const int bi = col / g.block;
+      const int blk = bi < g.n_blocks ? (g.blocks ? g.blocks[bi] : bi) : -1;
+      const int64_t row = static_cast<int64_t>(blk) * g.block + col % g.block;
+      bval[s] = blk >= 0 && row + SUB <= g.n_rows_total;
+      brow[s] = bval[s] ? row : 0;
+      ccol[s] = g.scatter_c ? static_cast<int>(row) : col;
+    } else {
+      const int col = nt * BN + s * SUB;
+      bval[s] = col < g.N;
+      brow[s] = bval[s] ? col : 0;
+      ccol[s] = col;
+    }
+    if (NM != N_DIRECT && !bval[s] && g.err && ((NM == N_DUAL ? nt * 128 + (s & 3) * SUB : nt * BN + s * SUB) < g.N))
+      set_error(g.err, FSI_ERR_INDEX_RANGE);
+  }
+
+  // ---- this lane's source rows: KiB j of the wave holds tile rows 16 (2 wave + j) .. +16
+  const bf16_t* asrc[2];
+  const bf16_t* bsrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 16 * (2 * wave + j) + (lane >> 2);
+    const int lc = (lane & 3) ^ ((r >> 2) & 3);  // logical chunk landing at physical chunk lane & 3
+    const int m = m0 + r < g.M ? m0 + r : g.M - 1;
+    asrc[j] = g.A + static_cast<int64_t>(m) * g.lda + lc * 8;
+    const int s = r / SUB;
+    const bf16_t* bp = (NM == N_DUAL && s >= 4) ? g.B1 : g.B0;
+    int64_t brw = brow[s] + (r % SUB);
+    if (NM == N_DIRECT && brw >= g.N) brw = g.N - 1;
+    bsrc[j] = bp + brw * g.ldb + lc * 8;
+  }
+  auto issue = [&](int step, int stage) {
+    int64_t a_k, b_k;
+    if (KM == K_GATHER_B) {
+      const int per = g.block / DK;
+      const int col = ktab[step / per];
+      a_k = static_cast<int64_t>(step) * DK;
+      b_k = col < 0 ? 0 : col + (step % per) * DK;  // an inactive block's H columns are zero
+    } else {
+      a_k = b_k = static_cast<int64_t>(step) * DK;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bf16_t* da = &lds[stage][0][(2 * wave + j) * 512];
+      bf16_t* db = &lds[stage][1][(2 * wave + j) * 512];
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(asrc[j] + a_k), (lds_void_t*)da, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(bsrc[j] + b_k), (lds_void_t*)db, 16, 0, 0);
+    }
+  };
+
+  f32x4_t acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // wave fragments: A rows 128 wm + 16 i; B tile columns {32 wn + 16 f} (f < 2) and
+  // {128 + 32 wn + 16 (f - 2)}: a gate column and its up column share a lane
+  const int frow = lane & 15, fchunk = lane >> 4;
+  auto bcol = [&](int f) { return f < 2 ? 32 * wn + 16 * f : 128 + 32 * wn + 16 * (f - 2); };
+  // All twelve fragment reads are issued before the first MFMA, so their
+  // latency overlaps instead of being paid pair by pair.
+  auto compute = [&](int stage) {
+    u32x4_t fa[8], fb[4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int c = bcol(f) + frow;
+      fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[stage][1][c * DK + (fchunk ^ ((c >> 2) & 3)) * 8]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 128 * wm + 16 * i + frow;
+      fa[i] = *reinterpret_cast<const u32x4_t*>(&lds[stage][0][r * DK + (fchunk ^ ((r >> 2) & 3)) * 8]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fa[i], fb[f], acc[i][f]);
+#if FSI_GEMM_DMA_SCHED
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);  // MFMAs
+#endif
+  };
+
+  // prologue: steps 0 .. 2 into stages 0 .. 2, then wait for step 0
+  const int pre = kcount < DSTAGES - 1 ? kcount : DSTAGES - 1;
+  for (int p = 0; p < pre; ++p) issue(p, p);
+  if (pre == 3) wait_vmcnt<2 * DLOADS>();
+  else if (pre == 2) wait_vmcnt<DLOADS>();
+  else wait_vmcnt<0>();
+  stage_barrier();
+  for (int step = 0; step < kcount; ++step) {
+    // the stage of step + 3 was last read by step - 1, which every wave has finished
+    if (step + DSTAGES - 1 < kcount) issue(step + DSTAGES - 1, (step + DSTAGES - 1) % DSTAGES);
+    compute(step % DSTAGES);
+    // step + 1 must have landed; steps + 2 and + 3 may still be in flight
+    const int after = (kcount - 1 < step + 3 ? kcount - 1 : step + 3) - (step + 1);
+    if (after >= 2) wait_vmcnt<2 * DLOADS>();
+    else if (after == 1) wait_vmcnt<DLOADS>();
+    else wait_vmcnt<0>();
+    stage_barrier();
+  }
+
+  // ---- epilogue: lane holds C[row 4 (lane / 16) + j][col lane % 16] of each fragment ----
+  const int crow0 = m0 + 128 * wm + 4 * (lane >> 4);
+  if (EPI == EPI_SWIGLU) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int tc = 32 * wn + 16 * f;          // gate tile column of the fragment
+      const int ch = ccol[0] + tc + frow;       // ccol[0] = first channel of the tile
+      if (ch >= g.N) continue;
+      const bool live = bval[tc / SUB] && bval[4 + tc / SUB];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = crow0 + 16 * i + j;
+          if (m >= g.M) continue;
+          const float h = live ? pattention_act<ACT_SWIGLU>(acc[i][f][j], acc[i][f + 2][j], g.rounding) : 0.f;
+          g.C[static_cast<int64_t>(m) * g.ldc + ch] = f32_to_bf16(h);
+        }
+    }
+  } else {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int tc = bcol(f);
+      const int s = tc / SUB;
+      if (NM != N_DIRECT && !bval[s]) continue;
+      const int col = ccol[s] + (tc % SUB) + frow;
+      if (NM == N_DIRECT && col >= g.N) continue;
+      const float bv = g.bias ? bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + frow : col]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = crow0 + 16 * i + j;
+          if (m >= g.M) continue;
+          g.C[static_cast<int64_t>(m) * g.ldc + col] = f32_to_bf16(acc[i][f][j] + bv);
+        }
+    }
+  }
+}
+
 // Zero the columns of C whose column block is inactive (BlockSparseLinear's
 // torch.zeros + scatter); mask[b] != 0 marks active block b.
 __global__ __launch_bounds__(256) void zero_inactive_kernel(bf16_t* __restrict__ C, int64_t ldc, int M, int N,
@@ -687,6 +900,12 @@ hipError_t launch_tiled(GemmArgs& a, bool big, hipStream_t st) {
   a.m_tiles = (a.M + tm - 1) / tm;
   a.n_tiles = (a.N + tn - 1) / tn;
   const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
+  // Direct-to-LDS for dense K (measured faster there); the K-gathered down
+  // projection reads half lines per 32-wide step and runs better on 64-wide steps.
+  if (big && FSI_GEMM_DMA && KM == K_DENSE && a.K % DK == 0) {
+    bsgemm_dma_kernel<NM, KM, EPI><<<grid, DTHREADS, 0, st>>>(a);
+    return hipGetLastError();
+  }
   if (big) {
     bsgemm_big_kernel<NM, KM, EPI><<<grid, BT, 0, st>>>(a);
     return hipGetLastError();

@@ -57,20 +57,37 @@ __device__ __forceinline__ float ldval(const void* p, int64_t i) {
   return BF16 ? bf16_to_f32(static_cast<const bf16_t*>(p)[i]) : static_cast<const float*>(p)[i];
 }
 
-// One workgroup: projection, rms_norm, scores and top-k selection.
+// One workgroup of 16 waves: projection, rms_norm, scores and top-k selection.
+constexpr int PR_THREADS = 1024;
+constexpr int PR_LDS_SCORES = 8192;
+
 template <bool BF16>
-__global__ __launch_bounds__(256) void pooled_route(const float* __restrict__ xm, int D,
-                                                    const void* __restrict__ wq, int index_dim,
-                                                    const void* __restrict__ keys, int n_blocks,
-                                                    int base_blocks, int remote_blocks, float score_scale,
-                                                    int32_t* __restrict__ active, float* __restrict__ scores_out,
-                                                    float* __restrict__ scratch) {
+__global__ __launch_bounds__(PR_THREADS) void pooled_route(const float* __restrict__ xm, int D,
+                                                           const void* __restrict__ wq, int index_dim,
+                                                           const void* __restrict__ keys, int n_blocks,
+                                                           int base_blocks, int remote_blocks, float score_scale,
+                                                           int32_t* __restrict__ active,
+                                                           float* __restrict__ scores_out,
+                                                           float* __restrict__ scratch) {
   __shared__ float q[MAX_INDEX_DIM];
+  __shared__ float lds_scores[PR_LDS_SCORES];
+  // the ranking re-reads every score once per candidate: keep them in LDS
+  float* sc = n_blocks <= PR_LDS_SCORES ? lds_scores : scratch;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // q_j = x_mean . Wq[j]  (wave w handles j = w, w + 4, ...)
-  for (int j = wave; j < index_dim; j += 4) {
+  // q_j = x_mean . Wq[j]  (wave w handles j = w, w + 16, ...); eight independent
+  // partial sums per lane keep eight loads in flight
+  for (int j = wave; j < index_dim; j += PR_THREADS / 64) {
+    float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int64_t row = static_cast<int64_t>(j) * D;
+    int d = lane;
+    for (; d + 7 * 64 < D; d += 8 * 64) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[e] = fmaf(xm[d + 64 * e], ldval<BF16>(wq, row + d + 64 * e), part[e]);
+    }
+    for (; d < D; d += 64) part[0] = fmaf(xm[d], ldval<BF16>(wq, row + d), part[0]);
     float acc = 0.f;
-    for (int d = lane; d < D; d += 64) acc = fmaf(xm[d], ldval<BF16>(wq, static_cast<int64_t>(j) * D + d), acc);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += part[e];
     acc = wave_sum(acc);
     if (lane == 0) q[j] = BF16 ? round_bf16(acc) : acc;
   }
@@ -83,7 +100,7 @@ __global__ __launch_bounds__(256) void pooled_route(const float* __restrict__ xm
   }
   __syncthreads();
   // scores
-  for (int b = tid; b < n_blocks; b += 256) {
+  for (int b = tid; b < n_blocks; b += PR_THREADS) {
     float acc = 0.f;
     for (int j = 0; j < index_dim; ++j) acc = fmaf(q[j], ldval<BF16>(keys, static_cast<int64_t>(b) * index_dim + j), acc);
     if (score_scale != 1.0f) {
@@ -91,21 +108,21 @@ __global__ __launch_bounds__(256) void pooled_route(const float* __restrict__ xm
       acc = acc * score_scale;
     }
     const float s = BF16 ? round_bf16(acc) : acc;
-    scratch[b] = s;
+    sc[b] = s;
     if (scores_out) scores_out[b] = s;
   }
   __syncthreads();
   // Rank among remote candidates: larger score first, ties broken by lower index.
-  for (int b = base_blocks + tid; b < n_blocks; b += 256) {
-    const float s = scratch[b];
+  for (int b = base_blocks + tid; b < n_blocks; b += PR_THREADS) {
+    const float s = sc[b];
     int rank = 0;
     for (int o = base_blocks; o < n_blocks; ++o) {
-      const float t = scratch[o];
+      const float t = sc[o];
       rank += (t > s) || (t == s && o < b);
     }
     if (rank < remote_blocks) active[base_blocks + rank] = b;
   }
-  for (int b = tid; b < base_blocks; b += 256) active[b] = b;
+  for (int b = tid; b < base_blocks; b += PR_THREADS) active[b] = b;
 }
 
 }  // namespace
@@ -148,14 +165,14 @@ FSI_API int fsi_mlp_router(const void* x, int64_t ldx, int64_t M, int64_t D, con
     token_partial<true><<<gp, 256, 0, st>>>(x, ldx, (int)M, (int)D, rows, part);
     token_mean<true><<<g1, 256, 0, st>>>(part, n_chunks, (int)M, (int)D, xm);
     FSI_HIP_LAUNCH_CHECK("mlp_router mean");
-    pooled_route<true><<<1, 256, 0, st>>>(xm, (int)D, q_proj_w, (int)index_dim, block_keys, (int)n_blocks,
+    pooled_route<true><<<1, PR_THREADS, 0, st>>>(xm, (int)D, q_proj_w, (int)index_dim, block_keys, (int)n_blocks,
                                           (int)base_blocks, (int)remote_blocks, score_scale, out_active, out_scores,
                                           scratch);
   } else {
     token_partial<false><<<gp, 256, 0, st>>>(x, ldx, (int)M, (int)D, rows, part);
     token_mean<false><<<g1, 256, 0, st>>>(part, n_chunks, (int)M, (int)D, xm);
     FSI_HIP_LAUNCH_CHECK("mlp_router mean");
-    pooled_route<false><<<1, 256, 0, st>>>(xm, (int)D, q_proj_w, (int)index_dim, block_keys, (int)n_blocks,
+    pooled_route<false><<<1, PR_THREADS, 0, st>>>(xm, (int)D, q_proj_w, (int)index_dim, block_keys, (int)n_blocks,
                                            (int)base_blocks, (int)remote_blocks, score_scale, out_active, out_scores,
                                            scratch);
   }

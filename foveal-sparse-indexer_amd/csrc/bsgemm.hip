@@ -356,6 +356,24 @@ __device__ __forceinline__ int xcd_group_id(int w, int n) {
   return (w & 7) * (n >> 3) + (w >> 3);
 }
 
+// Logical id -> (m tile, n tile) in groups of GEMM_GROUP_M m tiles: the workgroups an
+// XCD runs at once cover a few m tiles x several n tiles, so both operands' tiles
+// are shared in its L2 (a plain walk down M shares only the B tile).
+#ifndef FSI_GEMM_GROUP_M
+#define FSI_GEMM_GROUP_M 4
+#endif
+__device__ __forceinline__ void grouped_tile(int lid, int m_tiles, int n_tiles, int& mt, int& nt) {
+  constexpr int G = FSI_GEMM_GROUP_M;
+  if (G <= 1 || m_tiles % G != 0) {
+    mt = lid % m_tiles;
+    nt = lid / m_tiles;
+    return;
+  }
+  const int group = lid / (G * n_tiles), within = lid % (G * n_tiles);
+  mt = group * G + within % G;
+  nt = within / G;
+}
+
 template <int NM, int KM, int EPI>
 __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
   static_assert(KM != K_LIST, "tile lists run on the 128 x 128 kernel");
@@ -370,7 +388,8 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
   const int wm = wave / BWN, wn = wave % BWN;
 
   const int lid = xcd_group_id(blockIdx.x, gridDim.x);
-  const int mt = lid % g.m_tiles, nt = lid / g.m_tiles;
+  int mt, nt;
+  grouped_tile(lid, g.m_tiles, g.n_tiles, mt, nt);
   const int kcount = KM == K_GATHER_B ? g.n_blocks * (g.block / BK) : (g.K + BK - 1) / BK;
   const int m0 = mt * BM;
 
@@ -573,9 +592,8 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
 // Direct-to-LDS variant of the 256 x 256 kernel.  Operands go from global
 // memory straight into LDS with global_load_lds_dwordx4 (lane l's 16 bytes
 // land at M0 + 16 l), so the pipeline holds four LDS stages without staging
-// registers and loads run three 32-wide K-steps ahead of the MFMAs.  Each wave
-// loads whole KiB of a stage: 16 rows x 64 bytes, the lanes' source chunks
-// permuted so that the LDS image carries the conflict-free XOR swizzle.
+// registers and loads run three 32-wide K-steps ahead of the MFMAs.  Each load
+// fills one MFMA fragment (16 rows x 64 bytes) in lane order.
 // Rows that must read as zero (past M, past N, inactive blocks) are never
 // masked on the load side: they read a valid row, and the epilogue drops or
 // zeroes what they produce.  Dense K only, K % 32 == 0.
@@ -587,7 +605,19 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
 #ifndef FSI_GEMM_DMA_SCHED
 #define FSI_GEMM_DMA_SCHED 1
 #endif
-constexpr int DK = 32, DSTAGES = 4, DTHREADS = 512;
+#ifndef FSI_GEMM_DMA_STAGES
+#define FSI_GEMM_DMA_STAGES 4
+#endif
+#ifndef FSI_GEMM_DMA_PREFETCH
+#define FSI_GEMM_DMA_PREFETCH 1
+#endif
+constexpr int DK = 32, DSTAGES = FSI_GEMM_DMA_STAGES, DTHREADS = 512;
+
+// Chunk swizzle of 64-byte LDS rows.  Rows r and r + 4 share banks (256-byte bank
+// period); the swizzle (bit-reversed r / 4) gives distinct 16-byte slots both to the
+// 16 rows of one fragment column (lanes 0-15) and to 8 rows x 2 chunks (lanes 0-7
+// with 16-23), the two lane groupings a 128-bit LDS read may be served in.
+__device__ __forceinline__ int dswz(int r) { return ((r >> 1) & 2) | ((r >> 3) & 1); }
 constexpr int DLOADS = 4;  // global_load_lds per wave and K-step: 2 KiB of A, 2 KiB of B
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
@@ -606,21 +636,17 @@ __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "
 
 template <int NM, int KM, int EPI>
 __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
-  static_assert(KM != K_LIST, "tile lists run on the 128 x 128 kernel");
-  __shared__ __attribute__((aligned(1024))) bf16_t lds[DSTAGES][2][BM * DK];  // [stage][A/B][row * 32 + k]
-  __shared__ int32_t ktab[KM == K_GATHER_B ? KTAB_MAX : 1];
+  static_assert(KM == K_DENSE, "K-gathered and tile-list problems run on the register-staged kernels");
+  __shared__ __attribute__((aligned(1024))) bf16_t lds[DSTAGES][2][BM * DK];  // [stage][A/B][fragment][lane]
   const int tid = threadIdx.x;
-  if (KM == K_GATHER_B) {
-    fill_ktab(g, ktab, DTHREADS);
-    __syncthreads();
-  }
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves of 128 x 64
 
   const int lid = xcd_group_id(blockIdx.x, gridDim.x);
-  const int mt = lid % g.m_tiles, nt = lid / g.m_tiles;
-  const int kcount = KM == K_GATHER_B ? g.n_blocks * (g.block / DK) : g.K / DK;
+  int mt, nt;
+  grouped_tile(lid, g.m_tiles, g.n_tiles, mt, nt);
+  const int kcount = g.K / DK;
   const int m0 = mt * BM;
 
   // ---- per 32-column sub-block: B row base and C column base ----------------
@@ -655,13 +681,16 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
       set_error(g.err, FSI_ERR_INDEX_RANGE);
   }
 
-  // ---- this lane's source rows: KiB j of the wave holds tile rows 16 (2 wave + j) .. +16
+  // ---- this lane's source rows.  A stage holds each operand row-major, 64 bytes
+  // (4 chunks of 16) per row, the chunk of row r at physical slot chunk ^ dswz(r).
+  // Wave w loads KiB 2 w and 2 w + 1 of A and of B (16 rows each): lane l lands at
+  // row 16 KiB + l / 4, slot l % 4, so it loads the logical chunk (l % 4) ^ dswz(row).
   const bf16_t* asrc[2];
   const bf16_t* bsrc[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int r = 16 * (2 * wave + j) + (lane >> 2);
-    const int lc = (lane & 3) ^ ((r >> 2) & 3);  // logical chunk landing at physical chunk lane & 3
+    const int lc = (lane & 3) ^ dswz(r);
     const int m = m0 + r < g.M ? m0 + r : g.M - 1;
     asrc[j] = g.A + static_cast<int64_t>(m) * g.lda + lc * 8;
     const int s = r / SUB;
@@ -671,15 +700,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
     bsrc[j] = bp + brw * g.ldb + lc * 8;
   }
   auto issue = [&](int step, int stage) {
-    int64_t a_k, b_k;
-    if (KM == K_GATHER_B) {
-      const int per = g.block / DK;
-      const int col = ktab[step / per];
-      a_k = static_cast<int64_t>(step) * DK;
-      b_k = col < 0 ? 0 : col + (step % per) * DK;  // an inactive block's H columns are zero
-    } else {
-      a_k = b_k = static_cast<int64_t>(step) * DK;
-    }
+    const int64_t a_k = static_cast<int64_t>(step) * DK, b_k = a_k;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       bf16_t* da = &lds[stage][0][(2 * wave + j) * 512];
@@ -695,52 +716,92 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // wave fragments: A rows 128 wm + 16 i; B tile columns {32 wn + 16 f} (f < 2) and
-  // {128 + 32 wn + 16 (f - 2)}: a gate column and its up column share a lane
-  const int frow = lane & 15, fchunk = lane >> 4;
+  // wave fragments: A fragments 8 wm + i; B fragments of tile columns {32 wn + 16 f}
+  // (f < 2) and {128 + 32 wn + 16 (f - 2)}: a gate column and its up column share a lane
+  const int frow = lane & 15;
   auto bcol = [&](int f) { return f < 2 ? 32 * wn + 16 * f : 128 + 32 * wn + 16 * (f - 2); };
-  // All twelve fragment reads are issued before the first MFMA, so their
-  // latency overlaps instead of being paid pair by pair.
-  auto compute = [&](int stage) {
-    u32x4_t fa[8], fb[4];
+  const int fchunk = lane >> 4;
+  auto read_frags = [&](int stage, u32x4_t (&fa)[8], u32x4_t (&fb)[4]) {
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
       const int c = bcol(f) + frow;
-      fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[stage][1][c * DK + (fchunk ^ ((c >> 2) & 3)) * 8]);
+      fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[stage][1][c * DK + (fchunk ^ dswz(c)) * 8]);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 128 * wm + 16 * i + frow;
-      fa[i] = *reinterpret_cast<const u32x4_t*>(&lds[stage][0][r * DK + (fchunk ^ ((r >> 2) & 3)) * 8]);
+      fa[i] = *reinterpret_cast<const u32x4_t*>(&lds[stage][0][r * DK + (fchunk ^ dswz(r)) * 8]);
     }
+  };
+  auto mfmas = [&](const u32x4_t (&fa)[8], const u32x4_t (&fb)[4]) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fa[i], fb[f], acc[i][f]);
-#if FSI_GEMM_DMA_SCHED
-    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // DS reads
-    __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);  // MFMAs
-#endif
+  };
+#if FSI_GEMM_DMA_PREFETCH
+  // Step s + 2 must have landed at the end of iteration s (its fragments are read
+  // during iteration s + 1); later steps may still be in flight.
+  auto wait_through = [&](int s) {
+    const int last = kcount - 1 < s + DSTAGES - 1 ? kcount - 1 : s + DSTAGES - 1;  // last step issued
+    const int after = last - (s + 2);
+    if (DSTAGES >= 5 && after >= 2) wait_vmcnt<2 * DLOADS>();
+    else if (after >= 1) wait_vmcnt<DLOADS>();
+    else wait_vmcnt<0>();
+  };
+  // One K-step: issue step + DSTAGES - 1, read step + 1's fragments while step's
+  // MFMAs run.
+  auto iteration = [&](int step, const u32x4_t (&ca)[8], const u32x4_t (&cb)[4], u32x4_t (&na)[8],
+                       u32x4_t (&nb)[4]) {
+    // the stage of step + DSTAGES - 1 was last read during iteration step - 2
+    if (step + DSTAGES - 1 < kcount) issue(step + DSTAGES - 1, (step + DSTAGES - 1) % DSTAGES);
+    // unconditional (past the last step it reads a stale stage that is never
+    // used), so the compiler's wait before the MFMAs counts only older reads
+    read_frags((step + 1) % DSTAGES, na, nb);
+    mfmas(ca, cb);
+    wait_through(step);
+    stage_barrier();
   };
 
-  // prologue: steps 0 .. 2 into stages 0 .. 2, then wait for step 0
+  // prologue: steps 0 .. DSTAGES - 2 into their stages; steps 0 and 1 must land first
   const int pre = kcount < DSTAGES - 1 ? kcount : DSTAGES - 1;
   for (int p = 0; p < pre; ++p) issue(p, p);
-  if (pre == 3) wait_vmcnt<2 * DLOADS>();
-  else if (pre == 2) wait_vmcnt<DLOADS>();
+  if (DSTAGES >= 5 && pre >= 4) wait_vmcnt<2 * DLOADS>();
+  else if (pre >= 3) wait_vmcnt<DLOADS>();
+  else wait_vmcnt<0>();
+  stage_barrier();
+  u32x4_t fa0[8], fb0[4], fa1[8], fb1[4];
+  if (kcount > 0) read_frags(0, fa0, fb0);
+  int step = 0;
+  for (; step + 1 < kcount; step += 2) {
+    iteration(step, fa0, fb0, fa1, fb1);
+    iteration(step + 1, fa1, fb1, fa0, fb0);
+  }
+  if (step < kcount) mfmas(fa0, fb0);  // odd step count: the last step's fragments are in set 0
+#else
+  // Each iteration reads its own step's fragments; step s + 1 must have landed at
+  // the end of iteration s.
+  const int pre = kcount < DSTAGES - 1 ? kcount : DSTAGES - 1;
+  for (int p = 0; p < pre; ++p) issue(p, p);
+  if (DSTAGES >= 5 && pre >= 4) wait_vmcnt<3 * DLOADS>();
+  else if (pre >= 3) wait_vmcnt<2 * DLOADS>();
+  else if (pre >= 2) wait_vmcnt<DLOADS>();
   else wait_vmcnt<0>();
   stage_barrier();
   for (int step = 0; step < kcount; ++step) {
-    // the stage of step + 3 was last read by step - 1, which every wave has finished
     if (step + DSTAGES - 1 < kcount) issue(step + DSTAGES - 1, (step + DSTAGES - 1) % DSTAGES);
-    compute(step % DSTAGES);
-    // step + 1 must have landed; steps + 2 and + 3 may still be in flight
-    const int after = (kcount - 1 < step + 3 ? kcount - 1 : step + 3) - (step + 1);
-    if (after >= 2) wait_vmcnt<2 * DLOADS>();
-    else if (after == 1) wait_vmcnt<DLOADS>();
+    u32x4_t fa[8], fb[4];
+    read_frags(step % DSTAGES, fa, fb);
+    mfmas(fa, fb);
+    const int last = kcount - 1 < step + DSTAGES - 1 ? kcount - 1 : step + DSTAGES - 1;
+    const int after = last - (step + 1);
+    if (DSTAGES >= 5 && after >= 3) wait_vmcnt<3 * DLOADS>();
+    else if (after >= 2) wait_vmcnt<2 * DLOADS>();
+    else if (after >= 1) wait_vmcnt<DLOADS>();
     else wait_vmcnt<0>();
     stage_barrier();
   }
+#endif
 
   // ---- epilogue: lane holds C[row 4 (lane / 16) + j][col lane % 16] of each fragment ----
   const int crow0 = m0 + 128 * wm + 4 * (lane >> 4);
@@ -902,9 +963,11 @@ hipError_t launch_tiled(GemmArgs& a, bool big, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
   // Direct-to-LDS for dense K (measured faster there); the K-gathered down
   // projection reads half lines per 32-wide step and runs better on 64-wide steps.
-  if (big && FSI_GEMM_DMA && KM == K_DENSE && a.K % DK == 0) {
-    bsgemm_dma_kernel<NM, KM, EPI><<<grid, DTHREADS, 0, st>>>(a);
-    return hipGetLastError();
+  if constexpr (KM == K_DENSE) {
+    if (big && FSI_GEMM_DMA && a.K % DK == 0) {
+      bsgemm_dma_kernel<NM, KM, EPI><<<grid, DTHREADS, 0, st>>>(a);
+      return hipGetLastError();
+    }
   }
   if (big) {
     bsgemm_big_kernel<NM, KM, EPI><<<grid, BT, 0, st>>>(a);

@@ -596,7 +596,7 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
 // fills one MFMA fragment (16 rows x 64 bytes) in lane order.
 // Rows that must read as zero (past M, past N, inactive blocks) are never
 // masked on the load side: they read a valid row, and the epilogue drops or
-// zeroes what they produce.  Dense K only, K % 32 == 0.
+// zeroes what they produce.  Dense K needs K % 32 == 0.
 // ---------------------------------------------------------------------------
 // Direct-to-LDS loads for the 256 x 256 tiles (0: register-staged kernel).
 #ifndef FSI_GEMM_DMA
@@ -610,6 +610,11 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
 #endif
 #ifndef FSI_GEMM_DMA_PREFETCH
 #define FSI_GEMM_DMA_PREFETCH 1
+#endif
+// K-gathered problems (the Pattention down projection) on the DMA kernel: 174 vs
+// 168 us for the register-staged 64-wide-step kernel at the 8B prefill shape.
+#ifndef FSI_GEMM_DMA_KGATHER
+#define FSI_GEMM_DMA_KGATHER 0
 #endif
 constexpr int DK = 32, DSTAGES = FSI_GEMM_DMA_STAGES, DTHREADS = 512;
 
@@ -636,9 +641,14 @@ __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "
 
 template <int NM, int KM, int EPI>
 __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
-  static_assert(KM == K_DENSE, "K-gathered and tile-list problems run on the register-staged kernels");
-  __shared__ __attribute__((aligned(1024))) bf16_t lds[DSTAGES][2][BM * DK];  // [stage][A/B][fragment][lane]
+  static_assert(KM != K_LIST, "tile lists run on the 128 x 128 kernel");
+  __shared__ __attribute__((aligned(1024))) bf16_t lds[DSTAGES][2][BM * DK];  // [stage][A/B][row * 32 + k]
+  __shared__ int32_t ktab[KM == K_GATHER_B ? KTAB_MAX : 1];
   const int tid = threadIdx.x;
+  if (KM == K_GATHER_B) {
+    fill_ktab(g, ktab, DTHREADS);
+    __syncthreads();
+  }
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves of 128 x 64
@@ -646,7 +656,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   const int lid = xcd_group_id(blockIdx.x, gridDim.x);
   int mt, nt;
   grouped_tile(lid, g.m_tiles, g.n_tiles, mt, nt);
-  const int kcount = g.K / DK;
+  const int kcount = KM == K_GATHER_B ? g.n_blocks * (g.block / DK) : g.K / DK;
   const int m0 = mt * BM;
 
   // ---- per 32-column sub-block: B row base and C column base ----------------
@@ -700,7 +710,13 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
     bsrc[j] = bp + brw * g.ldb + lc * 8;
   }
   auto issue = [&](int step, int stage) {
-    const int64_t a_k = static_cast<int64_t>(step) * DK, b_k = a_k;
+    const int64_t a_k = static_cast<int64_t>(step) * DK;
+    int64_t b_k = a_k;
+    if (KM == K_GATHER_B) {
+      const int per = g.block / DK;
+      const int col = ktab[step / per];
+      b_k = col < 0 ? 0 : col + (step % per) * DK;  // an inactive block's H columns are zero
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       bf16_t* da = &lds[stage][0][(2 * wave + j) * 512];
@@ -961,10 +977,10 @@ hipError_t launch_tiled(GemmArgs& a, bool big, hipStream_t st) {
   a.m_tiles = (a.M + tm - 1) / tm;
   a.n_tiles = (a.N + tn - 1) / tn;
   const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
-  // Direct-to-LDS for dense K (measured faster there); the K-gathered down
-  // projection reads half lines per 32-wide step and runs better on 64-wide steps.
-  if constexpr (KM == K_DENSE) {
-    if (big && FSI_GEMM_DMA && a.K % DK == 0) {
+  // Direct-to-LDS for dense K; the K-gathered down projection reads half lines
+  // per 32-wide step and runs better on the 64-wide-step kernel.
+  if constexpr (KM != K_LIST) {
+    if (big && FSI_GEMM_DMA && (KM == K_GATHER_B ? FSI_GEMM_DMA_KGATHER != 0 : a.K % DK == 0)) {
       bsgemm_dma_kernel<NM, KM, EPI><<<grid, DTHREADS, 0, st>>>(a);
       return hipGetLastError();
     }

@@ -495,7 +495,8 @@ __global__ __launch_bounds__(64 * SR_WAVES) void score_route_kernel(const void* 
 // softmax over all completed pages (probabilities cast to vp's dtype)
 // contracted with vp; routing runs when completed > flp > 0 (flp = first local
 // page) over pages [0, flp): count = max(K_min, min(#(cum < top_p) + 1,
-// min(K_max, flp))), at most flp, ranked by wave 0 from the LDS scores.
+// min(K_max, flp))), at most flp.  The top candidates are selected by all 16
+// waves from the LDS scores and sorted by wave 0.
 // ---------------------------------------------------------------------------
 constexpr int DR_THREADS = 1024;
 constexpr int DR_WAVES = DR_THREADS / 64;
@@ -524,6 +525,118 @@ __device__ __forceinline__ float dr_block_sum(float v, float* red) {
   return r;
 }
 
+// Sum of the DR_WAVES per-wave words at w (16-byte aligned), read as four
+// 16-byte vectors (every lane reads the same words: broadcast reads).
+__device__ __forceinline__ int dr_sum16(const int* w) {
+  const int4* v = reinterpret_cast<const int4*>(w);
+  int total = 0;
+#pragma unroll
+  for (int q = 0; q < DR_WAVES / 4; ++q) {
+    const int4 a = v[q];
+    total += a.x + a.y + a.z + a.w;
+  }
+  return total;
+}
+
+// Candidates >= t in the workgroup (thread t holds candidates t + DR_THREADS i):
+// one ballot per key slot, one LDS word per wave, one barrier.  cnt holds two
+// banks of DR_WAVES words used alternately, so a bank is rewritten only after
+// every wave has passed the barrier that followed its last read.
+template <int NPT>
+__device__ __forceinline__ int dr_count_ge(const uint32_t (&key)[NPT], uint32_t t, int* cnt, int& bank) {
+  int c = 0;
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) c += __popcll(__ballot(key[i] >= t));
+  if (lane_id() == 0) cnt[bank * DR_WAVES + (threadIdx.x >> 6)] = c;
+  __syncthreads();
+  const int total = dr_sum16(cnt + bank * DR_WAVES);
+  bank ^= 1;
+  return total;
+}
+
+// Workgroup-wide form of rank_top's selection: the R largest keys (R > 0) are
+// found by the same bisection, with every wave counting its own keys, and are
+// compacted in candidate order (ties at the threshold by lower index) into
+// lds_k / lds_i.  Every thread of the workgroup calls it; sorting is left to
+// the caller.
+template <int NPT>
+__device__ void dr_select_top(const uint32_t (&key)[NPT], int R, uint32_t* lds_k, uint32_t* lds_i, int* cnt) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  int bank = 0;
+  uint32_t mx = 0;
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) mx = key[i] > mx ? key[i] : mx;
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t o = __shfl_xor(mx, off, 64);
+    mx = o > mx ? o : mx;
+  }
+  if (lane == 0) cnt[wave] = static_cast<int>(mx);
+  __syncthreads();
+  {
+    const int4* v = reinterpret_cast<const int4*>(cnt);
+    mx = 0;
+#pragma unroll
+    for (int q = 0; q < DR_WAVES / 4; ++q) {
+      const int4 a = v[q];
+      const uint32_t m0 = static_cast<uint32_t>(a.x) > static_cast<uint32_t>(a.y) ? a.x : a.y;
+      const uint32_t m1 = static_cast<uint32_t>(a.z) > static_cast<uint32_t>(a.w) ? a.z : a.w;
+      const uint32_t m2 = m0 > m1 ? m0 : m1;
+      mx = m2 > mx ? m2 : mx;
+    }
+  }
+  bank = 1;
+  // Invariant: count_ge(lo) >= R > count_ge(hi).  All values are uniform.
+  uint32_t lo = 1, hi = mx + 1;
+  int clo = dr_count_ge<NPT>(key, lo, cnt, bank);
+  while (clo != R && hi - lo > 1) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    const int c = dr_count_ge<NPT>(key, mid, cnt, bank);
+    if (c >= R) {
+      lo = mid;
+      clo = c;
+    } else {
+      hi = mid;
+    }
+  }
+  const uint32_t T = lo;
+  const uint32_t strict = clo == R ? T : T + 1;
+  // two passes (keys > T, then keys == T while fewer than R), each in candidate
+  // order: slot i, then wave, then lane; the counts use their own two banks
+  int* cc = cnt + 2 * DR_WAVES;
+  bank = 0;
+  int base = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass == 1 && (strict == T || base >= R)) break;  // uniform
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      const bool take = pass == 0 ? key[i] >= strict : key[i] == T;
+      const uint64_t b = __ballot(take);
+      if (lane == 0) cc[bank * DR_WAVES + wave] = __popcll(b);
+      __syncthreads();
+      int before = 0, total = 0;
+      const int4* v4 = reinterpret_cast<const int4*>(cc + bank * DR_WAVES);
+#pragma unroll
+      for (int q = 0; q < DR_WAVES / 4; ++q) {
+        const int4 a = v4[q];
+        const int vals[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          before += 4 * q + e < wave ? vals[e] : 0;
+          total += vals[e];
+        }
+      }
+      bank ^= 1;
+      const int pos = base + before + lanes_below(b);
+      if (take && pos < R) {
+        lds_k[pos] = key[i];
+        lds_i[pos] = static_cast<uint32_t>(threadIdx.x + DR_THREADS * i);
+      }
+      base += total;
+    }
+  }
+  __syncthreads();
+}
+
 template <int PL, int E, bool BF16>
 __global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __restrict__ qi,
                                                                   const float* __restrict__ kp,
@@ -538,6 +651,7 @@ __global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __
   __shared__ float red[DR_WAVES];
   __shared__ float ctx_part[DR_WAVES][SR_D];
   __shared__ uint32_t lk[64 * E], li[64 * E];
+  __shared__ __attribute__((aligned(16))) int dr_cnt[4 * DR_WAVES];
   const int lane = lane_id(), wave = threadIdx.x >> 6;
   const int b = blockIdx.x;
   const int mypos = pos_rows ? pos_rows[b] : pos;
@@ -556,12 +670,34 @@ __global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __
 #pragma unroll
   for (int c = 0; c < SR_D; ++c) qv[c] = qv[c] / nrm;
 
-  for (int j = threadIdx.x; j < completed; j += DR_THREADS) {
-    const float4* kr = reinterpret_cast<const float4*>(kp + (static_cast<int64_t>(b) * P + j) * SR_D);
+  // Every load this thread needs (page keys and, for the context, page values
+  // of pages t + DR_THREADS i) is issued up front, so the kernel pays one
+  // memory latency instead of one per pass.
+  constexpr int NPT = (64 * PL + DR_THREADS - 1) / DR_THREADS;
+  float4 kreg[NPT][4];
+  u32x4_t vreg[NPT][2];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const int j = threadIdx.x + DR_THREADS * i;
+    const int jj = j < completed ? j : 0;
+    const float4* kr = reinterpret_cast<const float4*>(kp + (static_cast<int64_t>(b) * P + jj) * SR_D);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) kreg[i][w] = kr[w];
+    if (BF16 && out_ctx) {
+      const u32x4_t* vr = reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(vp) +
+                                                           (static_cast<int64_t>(b) * P + jj) * SR_D);
+      vreg[i][0] = vr[0];
+      vreg[i][1] = vr[1];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const int j = threadIdx.x + DR_THREADS * i;
+    if (j >= completed) continue;
     float acc = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float4 f = kr[w];
+      const float4 f = kreg[i][w];
       acc = fmaf(qv[4 * w], f.x, acc);
       acc = fmaf(qv[4 * w + 1], f.y, acc);
       acc = fmaf(qv[4 * w + 2], f.z, acc);
@@ -583,13 +719,15 @@ __global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __
       float part[SR_D];
 #pragma unroll
       for (int c = 0; c < SR_D; ++c) part[c] = 0.f;
-      for (int j = threadIdx.x; j < completed; j += DR_THREADS) {
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) {
+        const int j = threadIdx.x + DR_THREADS * i;
+        if (j >= completed) continue;
         float pj = expf(sc[j] - mx) / z;
         const int64_t off = (static_cast<int64_t>(b) * P + j) * SR_D;
         if (BF16) {
           pj = round_bf16(pj);
-          const u32x4_t* vr = reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(vp) + off);
-          const u32x4_t a = vr[0], c2 = vr[1];
+          const u32x4_t a = vreg[i][0], c2 = vreg[i][1];
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             part[2 * w] = fmaf(pj, lo_bf16(a[w]), part[2 * w]);
@@ -637,24 +775,31 @@ __global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __
     for (int j = threadIdx.x; j < flp; j += DR_THREADS) zz += expf(sc[j] - mx);
     z = dr_block_sum(zz, red);
   }
-  if (wave != 0) return;  // ranking and output by wave 0 only; no workgroup barrier follows
-
   int count = 0;
   uint64_t sorted[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) sorted[e] = 0;
-  if (route) {
-    uint32_t key[PL];
+  const int kcap = k_max < flp ? k_max : flp;  // k_max = min(K_max, first_local_page)
+  int R = kcap > k_min ? kcap : k_min;
+  R = R < flp ? R : flp;
+  R = R < cap ? R : cap;
+  if (route && R > 0) {  // uniform: every thread takes part in the selection
+    uint32_t key[NPT];
 #pragma unroll
-    for (int i = 0; i < PL; ++i) {
-      const int j = i * 64 + lane;
+    for (int i = 0; i < NPT; ++i) {
+      const int j = threadIdx.x + DR_THREADS * i;
       key[i] = j < flp ? __float_as_uint(expf(sc[j] - mx) / z) + 1u : 0u;
     }
-    const int kcap = k_max < flp ? k_max : flp;  // k_max = min(K_max, first_local_page)
-    int R = kcap > k_min ? kcap : k_min;
-    R = R < flp ? R : flp;
-    R = R < cap ? R : cap;
-    rank_top<PL, E>(key, R, sorted, lk, li);
+    dr_select_top<NPT>(key, R, lk, li, dr_cnt);
+  }
+  if (wave != 0) return;  // sorting and output by wave 0 only; no workgroup barrier follows
+  if (route && R > 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int k = e * 64 + lane;
+      sorted[e] = k < R ? comp_key(lk[k], li[k]) : 0;
+    }
+    bitonic_desc<E>(sorted);
     float cum[E];
     running_mass<E, false>(sorted, R, cum);
     const int first = first_reaching<E>(cum, R, top_p);

@@ -25,7 +25,14 @@ from .core import (
     score_and_route,
     select_blocks,
 )
-from .attention import FovealKVCache, FovealSparseAttention, decode_attention, decode_route
+from .attention import (
+    FovealKVCache,
+    FovealSparseAttention,
+    decode_attention,
+    decode_route,
+    sparse_attention,
+    triton_foveal_sparse_attention,
+)
 from .block_matmul import (
     BlockSparseLinear,
     BlockwiseMatMul2D,
@@ -54,6 +61,8 @@ __all__ = [
     "blockwise_matmul",
     "triton_block_sparse_linear",
     "decode_attention",
+    "sparse_attention",
+    "triton_foveal_sparse_attention",
     "FovealKVCache",
     "FovealSparseAttention",
     "FovealPattentionMLP",

@@ -1,10 +1,15 @@
-"""Foveal sparse attention decode path on MI355X: drop-in pieces of
-foveal_indexer/attention.py.
+"""Foveal sparse attention on MI355X: drop-in pieces of
+foveal_indexer/attention.py and of triton_foveal_sparse_attention
+(foveal_indexer/triton_ops.py:256-313).
 
 decode_route: the per-step remote-page routing and additive-stream context of
 FovealSparseAttention.decode_step (attention.py:313-337,369-376) as one HIP
 launch over the whole batch (the reference loops over sequences in Python with
 a host sync per sequence).
+
+sparse_attention: block-sparse prefill attention (the local window plus routed
+pages of FovealSparseAttention.forward, attention.py:148-227, or the block lists
+of the Triton kernel) in one HIP launch that never forms the (T, T) mask.
 """
 from __future__ import annotations
 
@@ -16,7 +21,7 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import _lib
-from .core import FovealIndexer, index_rms_norm
+from .core import FovealIndexer, _forward_only, index_rms_norm
 
 
 def decode_route(
@@ -257,6 +262,111 @@ def decode_attention(
     return out
 
 
+SATTN_LOCAL_REMOTE = 0  # FSI_SATTN_LOCAL_REMOTE
+SATTN_BLOCK_LIST = 1  # FSI_SATTN_BLOCK_LIST
+
+
+def _attn_operand(t: Tensor, what: str, name: str) -> Tensor:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: {name} dtype {t.dtype} unsupported (bfloat16)")
+    if t.dim() != 4:
+        raise ValueError(f"{what}: {name} must be (B, H, T, head_dim), got {tuple(t.shape)}")
+    if t.stride(3) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def sparse_attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    lists: Optional[Tensor],
+    counts: Tensor,
+    *,
+    block: int,
+    mode: int = SATTN_LOCAL_REMOTE,
+    window: int = 0,
+    scale: Optional[float] = None,
+    out: Optional[Tensor] = None,
+) -> Tensor:
+    """Block-sparse attention of q (B, Hq, T, hd) over k, v (B, Hkv, T, hd), bf16.
+
+    mode SATTN_LOCAL_REMOTE (attention.py:148-218): query t sees keys s with
+    t - window < s <= t plus every key of the pages lists[b, t // block, :counts]
+    (a union).  mode SATTN_BLOCK_LIST (triton_ops.py:26-93): query block qb sees
+    every key of the listed key blocks.  lists: (B, ceil(T / block), capacity)
+    int32; counts: (B, ceil(T / block)).  Views with unit stride over head_dim
+    (such as proj(x).view(B, T, H, hd).transpose(1, 2)) are read in place; `out`
+    may be such a view too.  Returns (B, Hq, T, hd) bf16."""
+    what = "sparse_attention"
+    dev = _lib.require_gpu(q, k, v, counts, lists, what=what)
+    _forward_only(what, q, k, v)
+    q, k, v = (_attn_operand(t, what, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    B, Hq, T, hd = q.shape
+    Hkv = k.shape[1]
+    if tuple(k.shape) != (B, Hkv, T, hd) or tuple(v.shape) != (B, Hkv, T, hd) or Hq % Hkv:
+        raise ValueError(f"{what}: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
+    Qb = -(-T // block)
+    counts = counts.to(device=dev, dtype=torch.int32)
+    if tuple(counts.shape) != (B, Qb):
+        raise ValueError(f"{what}: counts {tuple(counts.shape)} != {(B, Qb)}")
+    cap = 0
+    if lists is not None and lists.numel():
+        lists = lists.to(device=dev, dtype=torch.int32)
+        if lists.dim() != 3 or tuple(lists.shape[:2]) != (B, Qb) or lists.stride(2) != 1:
+            lists = lists.contiguous()
+        if lists.dim() != 3 or tuple(lists.shape[:2]) != (B, Qb):
+            raise ValueError(f"{what}: lists {tuple(lists.shape)} != {(B, Qb)} + (capacity,)")
+        cap = lists.shape[2]
+    else:
+        lists = None
+    if out is None:
+        out = torch.empty((B, T, Hq, hd), dtype=torch.bfloat16, device=dev).transpose(1, 2)
+    elif tuple(out.shape) != (B, Hq, T, hd) or out.dtype != torch.bfloat16 or out.stride(3) != 1:
+        raise ValueError(f"{what}: out must be a (B, Hq, T, hd) bf16 tensor with unit stride over hd")
+    if scale is None:
+        scale = 1.0 / math.sqrt(hd)
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    ws = _lib.workspace(dev, L.fsi_sparse_attn_workspace_size(B, Hkv, T, hd), stream)
+    err = _lib.error_word(dev)
+    st = L.fsi_sparse_attn(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), B, Hq, Hkv, T, hd, int(block), int(mode), int(window),
+        _lib.ptr(lists), lists.stride(0) if cap else 0, lists.stride(1) if cap else 0, cap, counts.data_ptr(),
+        counts.stride(0), counts.stride(1), float(scale), 1, out.data_ptr(), out.stride(0), out.stride(1),
+        out.stride(2), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+    return out
+
+
+def triton_foveal_sparse_attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    block_indices: Tensor,
+    active_counts: Tensor,
+    scale: Optional[float] = None,
+    block_size: int = 16,
+) -> Tensor:
+    """Block-sparse attention (triton_ops.py:256-313): query block m of
+    block_size queries attends every key of block_indices[b, m, :active_counts[b, m]],
+    with no causal mask; a query block with no active block gets 0.  q, k, v:
+    (B, H, N, D) bf16 with N % block_size == 0.  The `triton_` name is kept for
+    compatibility; the kernel is HIP (block_size a multiple of 16; D 16, 32, 64
+    or 128; bfloat16)."""
+    B, H, N, D = q.shape
+    if N % block_size != 0:
+        raise ValueError(f"N ({N}) must be divisible by block_size ({block_size})")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    return sparse_attention(q, k, v, block_indices, active_counts, block=block_size, mode=SATTN_BLOCK_LIST,
+                            scale=scale, out=out)
+
+
 class FovealSparseAttention(nn.Module):
     """Causal foveal sparse attention (attention.py:97-379): same constructor,
     parameters (state_dict compatible), `init_kv_cache` and `decode_step`.
@@ -268,7 +378,8 @@ class FovealSparseAttention(nn.Module):
     sequence 0's pages for all sequences (attention.py:348) and
     `reference_batch0_pages = True` reproduces that.  `selected_remote_pages`
     reports each sequence's own selection in both modes, as the reference does.
-    The prefill `forward` is not on the MI355X path yet and raises.
+    The prefill `forward` routes with the HIP indexer ops and runs one
+    block-sparse attention launch (`sparse_attention`); inference only.
     """
 
     def __init__(
@@ -317,9 +428,66 @@ class FovealSparseAttention(nn.Module):
         )
 
     def forward(self, x: Tensor, compute_teacher_loss: bool = False) -> Tuple[Tensor, Dict[str, Any]]:
-        raise NotImplementedError(
-            "FovealSparseAttention.forward (prefill) is not on the MI355X path; decode_step is"
-        )
+        """Prefill forward pass (attention.py:180-269).  x: (B, T, D), T a
+        multiple of page_size.  Returns (out (B, T, D), aux with 'route',
+        'additive_out', 'distill_loss').
+
+        The attention runs as one block-sparse HIP launch over the local window
+        plus each query block's routed pages (the reference builds a (B, T, T)
+        boolean mask and calls dense SDPA).  The teacher for the distillation loss
+        (attention.py:243-267) needs only the softmax rows of the query-block
+        anchors, which are computed in fp32 for those rows alone."""
+        batch, seq_len, _ = x.shape
+        if seq_len % self.page_size != 0:
+            raise ValueError(f"Sequence length {seq_len} must be multiple of page_size {self.page_size}")
+        num_pages = seq_len // self.page_size
+
+        x_detach = x.detach()
+        q_16d = self.indexer.compute_query_16d(x_detach)
+        kp_16d, vp_16d = self.indexer.compute_kv_blocks_16d(x_detach)
+        q_block_16d = q_16d[:, :: self.page_size]
+        block_scores = self.indexer.compute_block_scores(q_block_16d, kp_16d)
+        route = self.indexer.route(block_scores)
+
+        q = self.q_proj(x).view(batch, seq_len, self.num_heads, self.head_dim).transpose(1, 2)
+        k = self.k_proj(x).view(batch, seq_len, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        v = self.v_proj(x).view(batch, seq_len, self.num_kv_heads, self.head_dim).transpose(1, 2)
+
+        attn = torch.empty((batch, seq_len, self.num_heads, self.head_dim), dtype=q.dtype, device=q.device)
+        sparse_attention(q, k, v, route.remote_indices, route.remote_counts, block=self.page_size,
+                         mode=SATTN_LOCAL_REMOTE, window=self.local_window, scale=self.scale,
+                         out=attn.transpose(1, 2))
+        out = self.out_proj(attn.view(batch, seq_len, self.num_heads * self.head_dim))
+
+        additive_out = None
+        if self.use_additive_stream:
+            additive_out = self.indexer.additive_stream(block_scores, vp_16d)
+            out = out + additive_out
+
+        aux: Dict[str, Any] = {
+            "route": route,
+            "additive_out": additive_out,
+            "distill_loss": torch.tensor(0.0, device=x.device),
+        }
+        if compute_teacher_loss:
+            with torch.no_grad():
+                teacher_mass = self._teacher_page_mass(q, k, num_pages)
+            aux["distill_loss"] = self.indexer.distillation_loss(block_scores, teacher_mass)
+        return out, aux
+
+    def _teacher_page_mass(self, q: Tensor, k: Tensor, num_pages: int) -> Tensor:
+        """Dense causal attention mass per key page for the first query of each
+        query block, averaged over heads (attention.py:243-265): (B, Q_blocks, pages)."""
+        batch, _, seq_len, hd = q.shape
+        qa = q[:, :, :: self.page_size].float().reshape(batch, self.num_kv_heads, self.groups * num_pages, hd)
+        s = torch.matmul(qa.contiguous(), k.float().transpose(-2, -1).contiguous()) * self.scale
+        s = s.view(batch, self.num_heads, num_pages, seq_len)
+        anchors = torch.arange(0, seq_len, self.page_size, device=q.device)
+        keys = torch.arange(seq_len, device=q.device)
+        s = s.masked_fill(keys[None, :] > anchors[:, None], -float("inf"))
+        probs = torch.softmax(s, dim=-1)
+        page_mass = probs.view(batch, self.num_heads, num_pages, num_pages, self.page_size).sum(dim=-1)
+        return page_mass.mean(dim=1)
 
     def init_kv_cache(self, batch_size: int, max_seq_len: int, device: torch.device) -> FovealKVCache:
         """A paged cache for decoding (attention.py:271-282)."""

@@ -1,0 +1,388 @@
+// Block-sparse prefill attention on MI355X (gfx950).
+//
+//   FSI_SATTN_LOCAL_REMOTE (FovealSparseAttention.forward with _build_sparse_mask,
+//     foveal_indexer/attention.py:148-269): query q of query block qb attends the
+//     keys k with k <= q and k > q - window, plus every key of the remote pages
+//     listed for (b, qb) (a boolean union: keys in both count once);
+//   FSI_SATTN_BLOCK_LIST (triton_foveal_sparse_attention,
+//     foveal_indexer/triton_ops.py:26-93,256-313): query block qb attends every key
+//     of each listed key block (a block listed twice is summed twice, as the
+//     Triton kernel does).
+//
+// Work: one wave per (sequence, query head, 16 queries).  A workgroup holds up
+// to four query heads of one KV head (a GQA group) at the same 16 queries, so
+// their K and V reads hit the CU's L1.  The wave walks a list of 32-key chunks
+// (local window chunks, then the chunks of the listed pages) with an online
+// softmax:
+//   S^T[t][q] = sum_d K[t][d] Q[q][d]       (A = K tile straight from k,
+//                                            B = Q^T kept in registers)
+//   O^T[d][q] += sum_t V^T[d][t] P^T[t][q]   (A = V^T tile, B = P^T taken from
+//                                            S^T's accumulators, as a bf16 hi + lo
+//                                            pair so P keeps ~16 bits)
+// V^T comes from a workspace copy of v, dim-major per 32-token chunk with the
+// chunk's tokens in the MFMA k order of P^T, written by a first kernel.
+#include <algorithm>
+#include <type_traits>
+
+#include "fsi_common.h"
+
+using namespace fsi;
+
+namespace {
+
+constexpr int SA_WAVES = 4;   // query heads per workgroup
+constexpr int SA_CHUNK = 32;  // keys per chunk
+constexpr float SA_LOG2E = 1.4426950408889634f;
+
+// storage position (MFMA k index) of token tau within a 32-token chunk: lane
+// group g of the P^T operand holds tokens 4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3
+__host__ __device__ __forceinline__ int sa_slot(int tau) { return 8 * ((tau & 15) >> 2) + 4 * (tau >> 4) + (tau & 3); }
+
+// ---------------------------------------------------------------------------
+// V^T copy: vt[((b Hkv + g) n32 + c) HD 32 + d 32 + sa_slot(tau)] = v[b][g][32 c + tau][d],
+// zero past T.  One thread per (b, g, token, 8 dims).
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void sa_vt_kernel(const bf16_t* __restrict__ v, int64_t vs_b, int64_t vs_g,
+                                                    int64_t vs_t, int B, int Hkv, int T, int n32,
+                                                    bf16_t* __restrict__ vt) {
+  constexpr int PIECES = HD / 8;
+  const int64_t total = static_cast<int64_t>(B) * Hkv * n32 * SA_CHUNK * PIECES;
+  for (int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; gid < total;
+       gid += static_cast<int64_t>(gridDim.x) * 256) {
+    const int piece = static_cast<int>(gid % PIECES);
+    int64_t r = gid / PIECES;
+    const int t = static_cast<int>(r % (static_cast<int64_t>(n32) * SA_CHUNK));
+    r /= static_cast<int64_t>(n32) * SA_CHUNK;
+    const int g = static_cast<int>(r % Hkv);
+    const int b = static_cast<int>(r / Hkv);
+    u32x4_t val = u32x4_t{0u, 0u, 0u, 0u};
+    if (t < T) val = *reinterpret_cast<const u32x4_t*>(v + b * vs_b + g * vs_g + t * vs_t + 8 * piece);
+    const int c = t / SA_CHUNK, tau = t % SA_CHUNK;
+    bf16_t* o = vt + ((static_cast<int64_t>(b) * Hkv + g) * n32 + c) * HD * SA_CHUNK + sa_slot(tau);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t w = val[e >> 1];
+      o[(8 * piece + e) * SA_CHUNK] = static_cast<bf16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+    }
+  }
+}
+
+struct SAParams {
+  const bf16_t* q;
+  int64_t qs_b, qs_h, qs_t;
+  const bf16_t* k;
+  int64_t ks_b, ks_h, ks_t;
+  const bf16_t* vt;  // workspace copy of v
+  int B, Hq, Hkv, G, T, n32, block, mode, window;
+  const int32_t* lists;  // (B, Qb, cap) page / block ids, strides ls_b, ls_q
+  int64_t ls_b, ls_q;
+  const int32_t* counts;  // (B, Qb), strides cs_b, cs_q
+  int64_t cs_b, cs_q;
+  int cap, n_blocks;  // list capacity; key blocks in [0, n_blocks)
+  float scale_log2;
+  bf16_t* out;
+  int64_t os_b, os_h, os_t;
+  int* err;
+};
+
+// chunk descriptor: absolute chunk index << 16 | local << 12 | hi << 6 | lo, with
+// [lo, hi) the chunk's keys taken (a chunk whose range is empty is skipped)
+__device__ __forceinline__ int64_t sa_desc(int64_t c, int lo, int hi, int local) {
+  return (c << 16) | (static_cast<int64_t>(local) << 12) | (static_cast<int64_t>(hi) << 6) | lo;
+}
+
+template <int HD>
+__global__ __launch_bounds__(64 * SA_WAVES) void sparse_attn_kernel(SAParams P) {
+  constexpr int KS = (HD + 31) / 32;  // k-steps of S^T (head_dim 16 pads dims 16..31 with 0)
+  constexpr int DT = HD / 16;         // dim tiles of O^T
+  constexpr int KL = 2 * KS;          // K loads per chunk
+  constexpr bool NARROW = HD < 32;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q0 = blockIdx.x * 16;
+  const int per_g = (P.G + SA_WAVES - 1) / SA_WAVES;
+  int y = blockIdx.y;
+  const int hsub = y % per_g;
+  y /= per_g;
+  const int g = y % P.Hkv;
+  const int b = y / P.Hkv;
+  const int hg = hsub * SA_WAVES + wave;
+  if (hg >= P.G) return;  // whole wave; no barriers in this kernel
+  const int h = g * P.G + hg;
+  const int r = lane & 15, grp = lane >> 4;
+  const bool dims_live = !NARROW || grp < 2;  // this lane's 8 dims of each k-step exist
+  const int qb = q0 / P.block;
+  const int myq = q0 + r;  // this lane's query column
+
+  // ---- chunk list: local window chunks, then the chunks of the listed blocks ----
+  int cnt = P.counts[b * P.cs_b + qb * P.cs_q];
+  cnt = cnt < 0 ? 0 : (cnt > P.cap ? P.cap : cnt);
+  int n_local = 0, c_lo = 0;
+  if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
+    const int klo = q0 - P.window + 1 > 0 ? q0 - P.window + 1 : 0;
+    const int khi = q0 + 15 < P.T - 1 ? q0 + 15 : P.T - 1;
+    c_lo = klo / SA_CHUNK;
+    n_local = khi / SA_CHUNK - c_lo + 1;
+  }
+  const int per_block = (P.block + SA_CHUNK - 1) / SA_CHUNK + 1;  // chunk slots per listed block
+  const int n_chunks = n_local + cnt * per_block;
+
+  const int32_t* list = P.lists + b * P.ls_b + qb * P.ls_q;
+
+  // Q^T operand: lane supplies Q[q0 + r][32 ks + 8 grp .. +8] (rows past T read row T - 1)
+  u32x4_t qop[KS];
+  {
+    const int qq = myq < P.T ? myq : P.T - 1;
+    const bf16_t* qp = P.q + b * P.qs_b + h * P.qs_h + static_cast<int64_t>(qq) * P.qs_t + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qop[ks] = dims_live ? *reinterpret_cast<const u32x4_t*>(qp + 32 * ks) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  const bf16_t* kbase = P.k + b * P.ks_b + g * P.ks_h + 8 * grp;
+  const bf16_t* vtbase = P.vt + (static_cast<int64_t>(b) * P.Hkv + g) * P.n32 * HD * SA_CHUNK + 8 * grp;
+
+  f32x4_t acc[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  for (int pass0 = 0; pass0 < n_chunks; pass0 += 64) {
+    // lane i describes chunk pass0 + i
+    int64_t desc = 0;  // empty range: skipped
+    {
+      const int i = pass0 + lane;
+      if (i < n_local) {
+        desc = sa_desc(c_lo + i, 0, SA_CHUNK, 1);
+      } else if (i < n_chunks) {
+        const int slot = (i - n_local) / per_block, part = (i - n_local) % per_block;
+        const int blk = list[slot];
+        bool ok = blk >= 0 && blk < P.n_blocks;
+        if (!ok && P.err) set_error(P.err, FSI_ERR_INDEX_RANGE);
+        if (ok && P.mode == FSI_SATTN_LOCAL_REMOTE) {
+          // the mask is a union: a page listed twice counts once
+          for (int s2 = 0; s2 < slot; ++s2) ok = ok && list[s2] != blk;
+        }
+        if (ok) {
+          const int k0 = blk * P.block;
+          const int k1 = k0 + P.block < P.T ? k0 + P.block : P.T;
+          const int c = k0 / SA_CHUNK + part;
+          const int lo = k0 - c * SA_CHUNK > 0 ? k0 - c * SA_CHUNK : 0;
+          const int hi = k1 - c * SA_CHUNK < SA_CHUNK ? k1 - c * SA_CHUNK : SA_CHUNK;
+          if (hi > lo) desc = sa_desc(c, lo, hi, 0);
+        }
+      }
+    }
+    const int n_here = n_chunks - pass0 < 64 ? n_chunks - pass0 : 64;
+
+    u32x4_t kc[KL], vc[DT];
+    auto load_chunk = [&](int64_t d, u32x4_t (&kr)[KL], u32x4_t (&vr)[DT]) {
+      const int64_t c = d >> 16;
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile) {
+        int key = static_cast<int>(c * SA_CHUNK) + 16 * tile + r;
+        key = key < P.T ? key : P.T - 1;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          kr[tile * KS + ks] = dims_live ? *reinterpret_cast<const u32x4_t*>(kbase + static_cast<int64_t>(key) * P.ks_t +
+                                                                                32 * ks)
+                                         : u32x4_t{0u, 0u, 0u, 0u};
+      }
+      const bf16_t* vp = vtbase + c * HD * SA_CHUNK;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) vr[dt] = *reinterpret_cast<const u32x4_t*>(vp + (16 * dt + r) * SA_CHUNK);
+    };
+
+    for (int i = 0; i < n_here; ++i) {
+      const uint32_t dlo = __builtin_amdgcn_readlane(static_cast<uint32_t>(desc), i);
+      const uint32_t dhi = __builtin_amdgcn_readlane(static_cast<uint32_t>(desc >> 32), i);
+      const int64_t d = static_cast<int64_t>((static_cast<uint64_t>(dhi) << 32) | dlo);
+      const int lo = static_cast<int>(d & 63), hi = static_cast<int>((d >> 6) & 63);
+      if (hi <= lo) continue;  // uniform
+      const bool local = ((d >> 12) & 1) != 0;
+      const int kc0 = static_cast<int>((d >> 16) * SA_CHUNK);
+      load_chunk(d, kc, vc);
+
+      f32x4_t st[2];
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile) {
+        st[tile] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) st[tile] = mfma16x16x32(kc[tile * KS + ks], qop[ks], st[tile]);
+      }
+      // lane holds keys kc0 + 16 tile + 4 grp + j for query myq
+      float sv[8];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tau = 16 * tile + 4 * grp + j;
+          const int key = kc0 + tau;
+          bool ok = tau >= lo && tau < hi && key < P.T;
+          if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
+            const bool in_win = key <= myq && key > myq - P.window;
+            ok = ok && (local ? in_win : !in_win);
+          }
+          const float v = ok ? st[tile][j] * P.scale_log2 : -INFINITY;
+          sv[tile * 4 + j] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx);
+      float alpha = 1.f, psum = 0.f;
+      uint32_t pk_hi[4], pk_lo[4];
+      if (m_new == -INFINITY) {  // nothing valid yet for this query
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pk_hi[w] = pk_lo[w] = 0u;
+      } else {
+        alpha = exp2f(m_run - m_new);
+        float phi[8], plo[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pe = exp2f(sv[e] - m_new);
+          psum += pe;
+          phi[e] = round_bf16(pe);
+          plo[e] = pe - phi[e];
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          pk_hi[w] = pack_bf16x2(phi[2 * w], phi[2 * w + 1]);
+          pk_lo[w] = pack_bf16x2(plo[2 * w], plo[2 * w + 1]);
+        }
+      }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+      const u32x4_t pbh = u32x4_t{pk_hi[0], pk_hi[1], pk_hi[2], pk_hi[3]};
+      const u32x4_t pbl = u32x4_t{pk_lo[0], pk_lo[1], pk_lo[2], pk_lo[3]};
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[dt][j] *= alpha;
+        acc[dt] = mfma16x16x32(vc[dt], pbh, acc[dt]);
+        acc[dt] = mfma16x16x32(vc[dt], pbl, acc[dt]);
+      }
+    }
+  }
+
+  // lane holds O^T[16 dt + 4 grp + j][query r]
+  if (myq < P.T) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    bf16_t* o = P.out + b * P.os_b + h * P.os_h + static_cast<int64_t>(myq) * P.os_t + 4 * grp;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const u32x2_t w = u32x2_t{pack_bf16x2(acc[dt][0] * inv, acc[dt][1] * inv),
+                                pack_bf16x2(acc[dt][2] * inv, acc[dt][3] * inv)};
+      *reinterpret_cast<u32x2_t*>(o + 16 * dt) = w;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+FSI_API size_t fsi_sparse_attn_workspace_size(int64_t B, int64_t Hkv, int64_t T, int64_t head_dim) {
+  if (B <= 0 || Hkv <= 0 || T <= 0 || head_dim <= 0) return FSI_WORKSPACE_COUNTER_BYTES;
+  const int64_t n32 = (T + SA_CHUNK - 1) / SA_CHUNK;
+  return FSI_WORKSPACE_COUNTER_BYTES +
+         fsi_host::align_up(sizeof(bf16_t) * static_cast<size_t>(B * Hkv * n32 * SA_CHUNK * head_dim), 256);
+}
+
+FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, const void* k, int64_t ks_b,
+                            int64_t ks_h, int64_t ks_t, const void* v, int64_t vs_b, int64_t vs_h, int64_t vs_t,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t head_dim, int64_t block, int mode,
+                            int64_t window, const int32_t* lists, int64_t ls_b, int64_t ls_q, int64_t capacity,
+                            const int32_t* counts, int64_t cs_b, int64_t cs_q, float scale, int dtype, void* out,
+                            int64_t os_b, int64_t os_h, int64_t os_t, void* workspace, size_t workspace_bytes,
+                            int* err, void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "sparse_attn: dtype %d (bf16 only)", dtype);
+  FSI_CHECK_ARG(mode == FSI_SATTN_LOCAL_REMOTE || mode == FSI_SATTN_BLOCK_LIST, FSI_ERR_INVALID_ARG,
+                "sparse_attn: mode %d", mode);
+  FSI_CHECK_ARG(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, FSI_ERR_SHAPE,
+                "sparse_attn: head_dim %lld (16, 32, 64 or 128)", (long long)head_dim);
+  FSI_CHECK_ARG(B > 0 && T > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, FSI_ERR_SHAPE,
+                "sparse_attn: B=%lld T=%lld Hq=%lld Hkv=%lld", (long long)B, (long long)T, (long long)Hq,
+                (long long)Hkv);
+  FSI_CHECK_ARG(block > 0 && block % 16 == 0, FSI_ERR_SHAPE, "sparse_attn: block %lld must be a multiple of 16",
+                (long long)block);
+  FSI_CHECK_ARG(capacity >= 0 && capacity <= 4096, FSI_ERR_CAPACITY, "sparse_attn: capacity %lld",
+                (long long)capacity);
+  FSI_CHECK_ARG(mode != FSI_SATTN_LOCAL_REMOTE || window > 0, FSI_ERR_SHAPE, "sparse_attn: window %lld",
+                (long long)window);
+  FSI_CHECK_ARG(T <= (int64_t(1) << 30) && B * Hkv * ((Hq / Hkv + SA_WAVES - 1) / SA_WAVES) <= 65535, FSI_ERR_SHAPE,
+                "sparse_attn: sizes beyond range");
+  FSI_CHECK_ARG(q && k && v && out && counts && (lists || capacity == 0), FSI_ERR_INVALID_ARG,
+                "sparse_attn: null pointer");
+  FSI_CHECK_ARG(qs_t % 8 == 0 && qs_h % 8 == 0 && qs_b % 8 == 0 && ks_t % 8 == 0 && ks_h % 8 == 0 &&
+                    ks_b % 8 == 0 && vs_t % 8 == 0 && vs_h % 8 == 0 && vs_b % 8 == 0 && os_t % 4 == 0 &&
+                    os_h % 4 == 0 && os_b % 4 == 0,
+                FSI_ERR_ALIGN, "sparse_attn: strides must be multiples of 8 elements (out: 4)");
+  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(v) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0,
+                FSI_ERR_ALIGN, "sparse_attn: q, k, v 16-byte and out 8-byte aligned");
+  const size_t need = fsi_sparse_attn_workspace_size(B, Hkv, T, head_dim);
+  FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE, "sparse_attn: workspace %zu < %zu",
+                workspace_bytes, need);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int n32 = static_cast<int>((T + SA_CHUNK - 1) / SA_CHUNK);
+  bf16_t* vt = reinterpret_cast<bf16_t*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES);
+  const int64_t vt_items = B * Hkv * static_cast<int64_t>(n32) * SA_CHUNK * (head_dim / 8);
+  const unsigned g1 = static_cast<unsigned>(std::min<int64_t>((vt_items + 255) / 256, 1 << 20));
+
+  SAParams P{};
+  P.q = static_cast<const bf16_t*>(q);
+  P.qs_b = qs_b;
+  P.qs_h = qs_h;
+  P.qs_t = qs_t;
+  P.k = static_cast<const bf16_t*>(k);
+  P.ks_b = ks_b;
+  P.ks_h = ks_h;
+  P.ks_t = ks_t;
+  P.vt = vt;
+  P.B = static_cast<int>(B);
+  P.Hq = static_cast<int>(Hq);
+  P.Hkv = static_cast<int>(Hkv);
+  P.G = static_cast<int>(Hq / Hkv);
+  P.T = static_cast<int>(T);
+  P.n32 = n32;
+  P.block = static_cast<int>(block);
+  P.mode = mode;
+  P.window = static_cast<int>(window);
+  P.lists = lists;
+  P.ls_b = ls_b;
+  P.ls_q = ls_q;
+  P.counts = counts;
+  P.cs_b = cs_b;
+  P.cs_q = cs_q;
+  P.cap = static_cast<int>(capacity);
+  P.n_blocks = static_cast<int>((T + block - 1) / block);
+  P.scale_log2 = scale * SA_LOG2E;
+  P.out = static_cast<bf16_t*>(out);
+  P.os_b = os_b;
+  P.os_h = os_h;
+  P.os_t = os_t;
+  P.err = err;
+  const dim3 grid(static_cast<unsigned>((T + 15) / 16),
+                  static_cast<unsigned>(B * Hkv * ((P.G + SA_WAVES - 1) / SA_WAVES)));
+  auto launch = [&](auto hd_tag) -> int {
+    constexpr int HD = decltype(hd_tag)::value;
+    sa_vt_kernel<HD><<<g1, 256, 0, st>>>(static_cast<const bf16_t*>(v), vs_b, vs_h, vs_t, P.B, P.Hkv, P.T, n32, vt);
+    FSI_HIP_LAUNCH_CHECK("sparse_attn v copy");
+    sparse_attn_kernel<HD><<<grid, 64 * SA_WAVES, 0, st>>>(P);
+    FSI_HIP_LAUNCH_CHECK("sparse_attn");
+    return FSI_OK;
+  };
+  switch (head_dim) {
+    case 16: return launch(std::integral_constant<int, 16>{});
+    case 32: return launch(std::integral_constant<int, 32>{});
+    case 64: return launch(std::integral_constant<int, 64>{});
+    default: return launch(std::integral_constant<int, 128>{});
+  }
+}
+
+}  // extern "C"

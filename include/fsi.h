@@ -276,6 +276,43 @@ FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_poo
                             void* out, void* workspace, size_t workspace_bytes, int* err, void* stream);
 
 /* ------------------------------------------------------------------------- *
+ * Block-sparse prefill attention (bf16 in, fp32 softmax and accumulate, bf16 out).
+ * q: (B, Hq, T, head_dim), k and v: (B, Hkv, T, head_dim), out: (B, Hq, T,
+ * head_dim), each given by element strides (s_b, s_h, s_t; unit stride over
+ * head_dim).  Query head h uses KV head h / (Hq / Hkv).  Query block qb holds
+ * queries [qb * block, (qb + 1) * block); lists: (B, ceil(T / block), capacity)
+ * int32 key-block ids (strides ls_b, ls_q), counts: (B, ceil(T / block)) int32
+ * (strides cs_b, cs_q; values clamped to [0, capacity]).  Key block j holds keys
+ * [j * block, min((j + 1) * block, T)).  Ids outside [0, ceil(T / block)) are
+ * skipped and reported through err.  A query with no key gets 0.
+ * ------------------------------------------------------------------------- */
+typedef enum fsi_sattn_mode {
+  /* FovealSparseAttention.forward with _build_sparse_mask (attention.py:148-227):
+   * query t sees keys s with t - window < s <= t, plus every key of the listed
+   * remote pages of its block (a union: a key in both, or in a page listed
+   * twice, counts once). */
+  FSI_SATTN_LOCAL_REMOTE = 0,
+  /* triton_foveal_sparse_attention (foveal_indexer/triton_ops.py:26-93,256-313):
+   * query block qb sees every key of each listed block, no causal mask (a block
+   * listed twice counts twice). */
+  FSI_SATTN_BLOCK_LIST = 1
+} fsi_sattn_mode;
+
+FSI_API size_t fsi_sparse_attn_workspace_size(int64_t B, int64_t Hkv, int64_t T, int64_t head_dim);
+
+/* head_dim 16, 32, 64 or 128; block a multiple of 16; capacity <= 4096; window > 0 for
+ * FSI_SATTN_LOCAL_REMOTE.  Strides multiples of 8 elements (out: 4), q, k, v
+ * 16-byte aligned.  Replaces the dense masked SDPA of attention.py:211-218 and
+ * the Triton kernel launch of triton_ops.py:298-312. */
+FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, const void* k, int64_t ks_b,
+                            int64_t ks_h, int64_t ks_t, const void* v, int64_t vs_b, int64_t vs_h, int64_t vs_t,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t head_dim, int64_t block, int mode,
+                            int64_t window, const int32_t* lists, int64_t ls_b, int64_t ls_q, int64_t capacity,
+                            const int32_t* counts, int64_t cs_b, int64_t cs_q, float scale, int dtype, void* out,
+                            int64_t os_b, int64_t os_h, int64_t os_t, void* workspace, size_t workspace_bytes,
+                            int* err, void* stream);
+
+/* ------------------------------------------------------------------------- *
  * Block-sparse GEMMs (bf16 in, fp32 accumulate, bf16 out) on 128 x 128 MFMA
  * tiles.  x: (M, K) row stride ldx; w: (N, K) row stride ldw (the nn.Linear
  * weight layout); out: (M, N) row stride ldo.  K, N and leading dimensions

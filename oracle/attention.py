@@ -8,6 +8,17 @@
                            CPU ops in the reference's order (attention.py:284-379),
                            fed by the same module weights; per-sequence pages by
                            default, the reference's sequence-0 pages with batch0=True
+  * sparse_mask            _build_sparse_mask (attention.py:148-178): causal local
+                           window OR the query block's listed remote pages
+  * block_list_weights     the key multiplicities of triton_foveal_sparse_attention
+                           (triton_ops.py:26-93): query block m counts each key of
+                           every listed block once per listing
+  * weighted_attention_f64 softmax attention in fp64 with per-key weights
+                           (0 / 1 for a boolean mask: the SDPA of attention.py:211-216;
+                           counts for the Triton kernel); a row with no weight gives 0
+                           (the Triton kernel's clamp of l at 1e-6)
+  * prefill_forward        FovealSparseAttention.forward (attention.py:180-269) with
+                           a given route, and its teacher page mass (:243-265)
 """
 from __future__ import annotations
 
@@ -103,3 +114,88 @@ class DecodeStepOracle:
             ctx = torch.einsum("btp,bpr->btr", pr, self.vp[:, :self.completed])
             out = out + m.indexer.out_proj(ctx)
         return out, pages, r
+
+
+def sparse_mask(batch: int, seq_len: int, window: int, page_size: int, remote_indices: Tensor,
+                remote_counts: Tensor) -> Tensor:
+    """(B, T, T) bool: key s visible to query t (attention.py:148-178)."""
+    q = torch.arange(seq_len)
+    k = torch.arange(seq_len)
+    allowed = (k[None, :] <= q[:, None]) & (k[None, :] > q[:, None] - window)
+    allowed = allowed[None].expand(batch, -1, -1).clone()
+    for b in range(batch):
+        for qb in range(remote_counts.shape[1]):
+            q0, q1 = qb * page_size, min((qb + 1) * page_size, seq_len)
+            for slot in range(int(remote_counts[b, qb])):
+                page = int(remote_indices[b, qb, slot])
+                allowed[b, q0:q1, page * page_size:min((page + 1) * page_size, seq_len)] = True
+    return allowed
+
+
+def block_list_weights(batch: int, seq_len: int, block: int, block_indices: Tensor, counts: Tensor) -> Tensor:
+    """(B, T, T) float64: how many times key s is listed for query t's block
+    (triton_ops.py:67-88: one pass over the block per listing)."""
+    w = torch.zeros(batch, seq_len, seq_len, dtype=torch.float64)
+    for b in range(batch):
+        for m in range(counts.shape[1]):
+            q0, q1 = m * block, min((m + 1) * block, seq_len)
+            for j in range(int(counts[b, m])):
+                kb = int(block_indices[b, m, j])
+                w[b, q0:q1, kb * block:min((kb + 1) * block, seq_len)] += 1.0
+    return w
+
+
+def weighted_attention_f64(q: Tensor, k: Tensor, v: Tensor, weights: Tensor, scale: float) -> Tensor:
+    """out[b, h, t] = sum_s w[b, t, s] exp(scale q.k_s) v_s / sum_s w[b, t, s] exp(scale q.k_s)
+    in fp64, KV head h // (Hq / Hkv); q: (B, Hq, T, hd), k, v: (B, Hkv, T, hd),
+    weights: (B, T, T) bool or float.  Rows with no weight give 0."""
+    B, Hq, T, hd = q.shape
+    Hkv = k.shape[1]
+    groups = Hq // Hkv
+    w = weights.double()
+    kk = k.double().repeat_interleave(groups, dim=1)
+    vv = v.double().repeat_interleave(groups, dim=1)
+    s = torch.matmul(q.double(), kk.transpose(-2, -1)) * scale
+    s = s.masked_fill(w[:, None] == 0, float("-inf"))
+    mx = s.amax(dim=-1, keepdim=True)
+    mx = torch.where(torch.isfinite(mx), mx, torch.zeros_like(mx))
+    e = torch.exp(s - mx) * w[:, None]
+    z = e.sum(dim=-1, keepdim=True)
+    p = torch.where(z > 0, e / z.clamp_min(1e-300), torch.zeros_like(e))
+    return torch.matmul(p, vv)
+
+
+@torch.no_grad()
+def prefill_forward(m, x: Tensor, remote_indices: Tensor, remote_counts: Tensor):
+    """FovealSparseAttention.forward (attention.py:180-269) on the CPU with the
+    module's weights and a given route: projections in the module dtype, the
+    masked SDPA (attention.py:211-216) as fp64 attention under sparse_mask,
+    out_proj, additive stream.  Also returns the teacher page mass of
+    attention.py:243-265 (dense causal softmax over all T keys, anchor rows,
+    summed per page, averaged over heads), computed in fp32 as written there.
+    Returns (out (B, T, D), teacher_mass (B, Qb, pages))."""
+    B, T, _ = x.shape
+    ps = m.page_size
+    pages = T // ps
+    q = m.q_proj(x).view(B, T, m.num_heads, m.head_dim).transpose(1, 2)
+    k = m.k_proj(x).view(B, T, m.num_kv_heads, m.head_dim).transpose(1, 2)
+    v = m.v_proj(x).view(B, T, m.num_kv_heads, m.head_dim).transpose(1, 2)
+    mask = sparse_mask(B, T, m.local_window, ps, remote_indices, remote_counts)
+    attn = weighted_attention_f64(q, k, v, mask, m.scale).to(x.dtype)
+    out = m.out_proj(attn.transpose(1, 2).reshape(B, T, m.num_heads * m.head_dim))
+    if m.use_additive_stream:
+        from . import indexer as IX
+
+        qi = IX.rms_norm16(m.indexer.q_proj(x))
+        kb, vb = IX.pool_kv(m.indexer.k_proj(x), m.indexer.v_proj(x), ps)
+        scores = IX.block_scores(qi[:, ::ps], kb)
+        ctx = IX.additive_context(scores, vb, True)
+        out = out + m.indexer.out_proj(ctx).repeat_interleave(ps, dim=1)
+    groups = m.num_heads // m.num_kv_heads
+    kf = k.float().repeat_interleave(groups, dim=1)
+    s = torch.matmul(q.float(), kf.transpose(-2, -1)) * m.scale
+    causal = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    s = s.masked_fill(~causal[None, None], -float("inf"))
+    probs = torch.softmax(s, dim=-1)[:, :, ::ps]
+    teacher = probs.view(B, m.num_heads, pages, pages, ps).sum(dim=-1).mean(dim=1)
+    return out, teacher

@@ -1,0 +1,163 @@
+"""GPU parity of block-sparse prefill attention (fsi_sparse_attn).
+
+Both modes are compared with fp64 softmax attention under the oracle's key
+weights: sparse_mask (FovealSparseAttention's local window OR listed pages,
+attention.py:148-218) and block_list_weights (triton_foveal_sparse_attention,
+triton_ops.py:26-93).  bf16 outputs: rel-L2 <= 2e-3.  The module forward also
+passes through the bf16 library GEMMs of the four projections on each side, so
+its bar is rel-L2 1e-2, as for decode_step."""
+import math
+
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import pattention as Pt
+from oracle import routing as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _qkv(B, Hq, Hkv, T, hd, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, T, hd, generator=g).bfloat16()
+    k = torch.randn(B, Hkv, T, hd, generator=g).bfloat16()
+    v = torch.randn(B, Hkv, T, hd, generator=g).bfloat16()
+    return q, k, v, g
+
+
+LR_CASES = [
+    # B, Hq, Hkv, hd, T, block, window, capacity
+    (2, 8, 2, 128, 512, 64, 128, 3),
+    (1, 4, 4, 64, 256, 64, 64, 4),
+    (2, 8, 1, 64, 320, 64, 1, 2),      # window of one key: the query itself
+    (1, 32, 8, 128, 1024, 64, 256, 8),
+    (2, 4, 2, 32, 100, 16, 24, 3),     # T not a multiple of 16 or 32
+    (1, 2, 1, 16, 96, 32, 40, 2),      # head_dim 16
+    (1, 6, 1, 64, 192, 64, 1000, 2),   # window beyond T; 6 heads per KV head (two workgroups)
+    (2, 4, 2, 128, 256, 64, 64, 0),    # no remote pages at all
+]
+
+
+@pytest.mark.parametrize("case", LR_CASES, ids=[f"c{i}" for i in range(len(LR_CASES))])
+def test_local_remote_parity(fsi, dev, case):
+    B, Hq, Hkv, hd, T, blk, W, cap = case
+    print(f"[case] sparse_attention local_remote {case}", flush=True)
+    q, k, v, g = _qkv(B, Hq, Hkv, T, hd, seed=sum(case))
+    Qb = -(-T // blk)
+    idx = torch.randint(0, Qb, (B, Qb, max(cap, 1)), generator=g, dtype=torch.int32)[:, :, :cap]
+    cnt = torch.randint(0, cap + 1, (B, Qb), generator=g, dtype=torch.int32)
+    if cap >= 2:
+        idx[0, Qb - 1, :2] = torch.tensor([0, 0], dtype=torch.int32)  # a page listed twice counts once
+        cnt[0, Qb - 1] = 2
+    scale = 1.0 / math.sqrt(hd)
+    out = fsi.sparse_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev) if cap else None, cnt.to(dev), block=blk,
+                               mode=0, window=W, scale=scale)
+    mask = A.sparse_mask(B, T, W, blk, idx, cnt)
+    ref = A.weighted_attention_f64(q, k, v, mask, scale)
+    err = Pt.rel_l2(out.cpu().float(), ref.float())
+    assert err <= TOL, err
+
+
+BL_CASES = [
+    # B, H, N, D, block_size, max_active
+    (2, 4, 128, 64, 16, 4),
+    (1, 2, 256, 128, 32, 5),
+    (2, 3, 192, 16, 64, 2),
+    (1, 8, 512, 128, 64, 8),
+    (1, 2, 64, 32, 16, 6),
+]
+
+
+@pytest.mark.parametrize("case", BL_CASES, ids=[f"c{i}" for i in range(len(BL_CASES))])
+def test_block_list_parity(fsi, dev, case):
+    """triton_foveal_sparse_attention: every key of each listed block, no causal
+    mask, a block listed twice counts twice, an empty list gives 0."""
+    B, H, N, D, bs, mx = case
+    print(f"[case] triton_foveal_sparse_attention {case}", flush=True)
+    q, k, v, g = _qkv(B, H, H, N, D, seed=7 * sum(case))
+    M = N // bs
+    idx = torch.randint(0, M, (B, M, mx), generator=g, dtype=torch.int32)
+    cnt = torch.randint(0, mx + 1, (B, M), generator=g, dtype=torch.int32)
+    cnt[0, 0] = 0
+    idx[0, 1, :2] = 1
+    cnt[0, 1] = max(int(cnt[0, 1]), 2)
+    out = fsi.triton_foveal_sparse_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), cnt.to(dev),
+                                             block_size=bs).cpu()
+    assert out.is_contiguous() and out.shape == q.shape
+    w = A.block_list_weights(B, N, bs, idx, cnt)
+    ref = A.weighted_attention_f64(q, k, v, w, 1.0 / math.sqrt(D))
+    assert torch.equal(out[0, :, :bs], torch.zeros(H, bs, D, dtype=torch.bfloat16))
+    err = Pt.rel_l2(out.float(), ref.float())
+    assert err <= TOL, err
+
+
+def test_strided_views_in_place(fsi, dev):
+    """q, k, v as (B, T, H, hd) projections viewed (B, H, T, hd), output written
+    into such a view."""
+    B, Hq, Hkv, T, hd, blk = 2, 8, 2, 256, 64, 64
+    g = torch.Generator().manual_seed(11)
+    qs = torch.randn(B, T, Hq, hd, generator=g).bfloat16()
+    ks = torch.randn(B, T, Hkv, hd, generator=g).bfloat16()
+    vs = torch.randn(B, T, Hkv, hd, generator=g).bfloat16()
+    idx = torch.tensor([[[0, 1], [0, 2], [1, 0], [2, 0]]] * B, dtype=torch.int32)
+    cnt = torch.tensor([[0, 1, 2, 1]] * B, dtype=torch.int32)
+    outs = torch.zeros(B, T, Hq, hd, dtype=torch.bfloat16, device=dev)
+    fsi.sparse_attention(qs.to(dev).transpose(1, 2), ks.to(dev).transpose(1, 2), vs.to(dev).transpose(1, 2),
+                         idx.to(dev), cnt.to(dev), block=blk, mode=0, window=70, scale=0.1,
+                         out=outs.transpose(1, 2))
+    mask = A.sparse_mask(B, T, 70, blk, idx, cnt)
+    ref = A.weighted_attention_f64(qs.transpose(1, 2), ks.transpose(1, 2), vs.transpose(1, 2), mask, 0.1)
+    err = Pt.rel_l2(outs.cpu().transpose(1, 2).float(), ref.float())
+    assert err <= TOL, err
+
+
+def test_invalid_block_reported(fsi, dev, monkeypatch):
+    q, k, v, _ = _qkv(1, 2, 1, 128, 64, seed=5)
+    idx = torch.tensor([[[0], [5]]], dtype=torch.int32, device=dev)  # 2 blocks exist
+    cnt = torch.tensor([[0, 1]], dtype=torch.int32, device=dev)
+    monkeypatch.setenv("FSI_CHECK", "1")
+    with pytest.raises(IndexError):
+        fsi.sparse_attention(q.to(dev), k.to(dev), v.to(dev), idx, cnt, block=64, mode=0, window=64)
+
+
+def test_prefill_forward_module(fsi, dev):
+    """FovealSparseAttention.forward: route against the routing oracle on the
+    module's own block scores, output against the CPU restatement of
+    attention.py:180-269 under that route, distillation loss against the loss
+    of the oracle's dense teacher mass."""
+    from route_check import check_rows
+
+    torch.manual_seed(0)
+    B, T, D = 2, 1024, 256
+    m = fsi.FovealSparseAttention(hidden_size=D, num_heads=8, num_kv_heads=2, head_dim=32, page_size=64,
+                                  local_window_blocks=2, top_p=0.8, min_remote_pages=1, max_remote_pages=3,
+                                  remote_capacity=4).to(torch.bfloat16)
+    cpu = {kk: vv.clone() for kk, vv in m.state_dict().items()}
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, T, D, generator=g).bfloat16()
+    md = m.to(dev)
+    with torch.no_grad():
+        out, aux = md(x.to(dev), compute_teacher_loss=True)
+        xd = x.to(dev)
+        qb = md.indexer.compute_query_16d(xd)[:, ::64]
+        kb, _ = md.indexer.compute_kv_blocks_16d(xd)
+        scores = md.indexer.compute_block_scores(qb, kb).cpu()
+    route = aux["route"]
+    ora = R.select_route(scores, causal=True, local_window_blocks=2, top_p=0.8, min_remote_blocks=1,
+                         max_remote_blocks=3, remote_capacity=4)
+    _, _, remote = R.route_masks(T // 64, T // 64, True, 2)
+    assert not check_rows(route.remote_indices, route.remote_counts, ora, remote, 1e-6, 1e-5)
+
+    mc = fsi.FovealSparseAttention(hidden_size=D, num_heads=8, num_kv_heads=2, head_dim=32, page_size=64,
+                                   local_window_blocks=2, top_p=0.8, min_remote_pages=1, max_remote_pages=3,
+                                   remote_capacity=4).to(torch.bfloat16)
+    mc.load_state_dict(cpu)
+    ref, teacher = A.prefill_forward(mc, x, route.remote_indices.cpu(), route.remote_counts.cpu())
+    err = Pt.rel_l2(out.cpu().float(), ref.float())
+    assert err <= 1e-2, err
+    assert aux["additive_out"] is not None and out.shape == (B, T, D)
+    ref_loss = mc.indexer.distillation_loss(scores, teacher)
+    assert math.isclose(float(aux["distill_loss"]), float(ref_loss), rel_tol=1e-2, abs_tol=1e-5)

@@ -16,6 +16,7 @@ the replay stream bracket the timed region.
 Other workloads (one JSON line each, for the profiles; not the headline line):
   --workload routing      C2: fused 16-D cosine scoring + top-p selection, 8192 queries x 4096 keys
   --workload decode_attn  C4: foveal paged-KV decode attention, 32 sequences x 131072 context
+  --workload prefill_attn block-sparse prefill attention, 16384 tokens, Llama-3-8B attention heads
   --workload block_sparse C5: 2-D tile-sparse matmul, 4096 x 8192 by 8192 x 8192, 128 x 128 tiles
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-prefill] [--workload W]
@@ -41,10 +42,12 @@ D_MODEL, N_PARAM, BLOCK, BASE, REMOTE = 4096, 14336, 64, 8, 56
 DECODE_BATCH, PREFILL_TOKENS = 64, 4096
 
 
-# HBM bytes of one decode step (all four kernels) measured with rocprofv3 FETCH_SIZE
-# and WRITE_SIZE passes, scaled by a 512 MiB copy (profiles/pattention_decode_prefill_8b.md):
-# (34872.4 + 4129.5 + 18477.7 + 4109.0) KiB x 1.9997 read + 17408 KiB x 1.000 written.
-DECODE_TRAFFIC_BYTES = int(140566.8 * 1024)
+# HBM bytes of one decode step measured with rocprofv3 FETCH_SIZE and WRITE_SIZE
+# passes, scaled by a 512 MiB copy (profiles/pattention_decode_prefill_8b.md):
+#   packed path  : (34911.25 + 18549.35) KiB x 1.99979 read + (512 + 512) KiB written
+#   --no-pack    : (34872.4 + 4129.5 + 18477.7 + 4109.0) KiB x 1.9997 read + 17408 KiB written
+DECODE_TRAFFIC_BYTES = int(107933.9 * 1024)
+DECODE_TRAFFIC_BYTES_UNPACKED = int(140566.8 * 1024)
 
 
 def decode_bytes(n_active: int, batch: int) -> int:
@@ -271,6 +274,85 @@ def bench_decode_attn(fsi, args, dev):
     return res
 
 
+def prefill_attn_flops(lists, counts, T: int, W: int, page: int, hq: int, hd: int) -> int:
+    """Algorithmic FLOPs of block-sparse prefill attention: for every query, its
+    attended keys (the causal window of W keys plus the keys of its block's
+    listed pages outside that window) x 4 hd FLOPs (QK^T and PV) x heads."""
+    B, Qb, _ = lists.shape
+    t = torch.arange(T, device=lists.device)
+    keys = torch.clamp(t + 1, max=W).to(torch.int64).expand(B, T).clone()
+    slot = torch.arange(lists.shape[2], device=lists.device)
+    valid = slot[None, None] < counts[..., None]
+    first = (lists.to(torch.int64) * page).masked_fill(~valid, T)       # (B, Qb, cap)
+    first_t = first.repeat_interleave(page, dim=1)[:, :T]                # (B, T, cap)
+    outside = torch.clamp(t[None, :, None] - W + 1 - first_t, min=0, max=page)
+    keys += outside.sum(-1)
+    return int(keys.sum()) * hq * hd * 4
+
+
+def bench_prefill_attn(fsi, args, dev):
+    B, HQ, HKV, HD, T, PAGE, WB, KMAX, TOP_P = 1, 32, 8, 128, 16384, 64, 16, 32, 0.9
+    W = WB * PAGE
+    Qb = T // PAGE
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, HQ, T, HD, device=dev, generator=g).bfloat16()
+    k = torch.randn(B, HKV, T, HD, device=dev, generator=g).bfloat16()
+    v = torch.randn(B, HKV, T, HD, device=dev, generator=g).bfloat16()
+    # pages routed as FovealSparseAttention.forward does: cosine/4 block scores of
+    # the block-anchor 16-D queries against normalised 16-D page keys, causal top-p
+    qi = torch.nn.functional.normalize(torch.randn(B, Qb, 16, device=dev, generator=g), dim=-1)
+    kp = torch.nn.functional.normalize(torch.randn(B, Qb, 16, device=dev, generator=g), dim=-1)
+    scores = torch.bmm(qi, kp.transpose(1, 2).contiguous()) / 4.0
+    route = fsi.select_blocks(scores, causal=True, block_size=PAGE, local_window_blocks=WB, top_p=TOP_P,
+                              min_remote_blocks=0, max_remote_blocks=KMAX, remote_capacity=KMAX)
+    lists, counts = route.remote_indices, route.remote_counts
+    out = torch.empty(B, T, HQ, HD, dtype=torch.bfloat16, device=dev)
+    scale = 1.0 / HD ** 0.5
+
+    def step(i):
+        fsi.sparse_attention(q, k, v, lists, counts, block=PAGE, mode=0, window=W, scale=scale,
+                             out=out.transpose(1, 2))
+
+    t, _ = time_graph(step, args.steps, args.warmup, dev)
+    per = t / args.steps
+    flops = prefill_attn_flops(lists, counts, T, W, PAGE, HQ, HD)
+    tfs = flops / per / 1e12
+    res = _result("foveal prefill attention tok/s (16384 tokens, local 1024 + top-p pages)", round(B * T / per, 1),
+                  "tok/s", args.steps, args.warmup, round(per * 1e3, 6), "bf16",
+                  "synthetic (seeded N(0,1) q/k/v; pages routed by select_blocks on cosine/4 scores of random "
+                  "normalised 16-D anchors and page keys)",
+                  {"workload": "FovealSparseAttention.forward attention core at the Llama-3-8B attention shape "
+                               "(32 q heads, 8 KV heads, head_dim 128), batch 1 x 16384 tokens, page 64, local "
+                               "window 1024, top-p 0.9, K_max 32",
+                   "mean_remote_pages": round(float(counts.float().mean()), 2)})
+    res["roofline"] = {"bound": "mfma", "achieved": round(tfs, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                       "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                       "kernel": "sa_vt_kernel + sparse_attn_kernel (2 launches)", "flops_per_launch": flops}
+    if not args.no_cpu_baseline:
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        # the reference's dense masked SDPA (attention.py:199-216) for the last query block only
+        nq = PAGE
+        qc = q[:, :, T - nq:].cpu()
+        kc = k.cpu().repeat_interleave(HQ // HKV, dim=1)
+        vc = v.cpu().repeat_interleave(HQ // HKV, dim=1)
+        tq = torch.arange(T - nq, T)
+        ks = torch.arange(T)
+        mask = (ks[None] <= tq[:, None]) & (ks[None] > tq[:, None] - W)
+        for p in lists[0, Qb - 1, :int(counts[0, Qb - 1])].tolist():
+            mask[:, p * PAGE:(p + 1) * PAGE] = True
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            torch.nn.functional.scaled_dot_product_attention(qc, kc, vc, attn_mask=mask[None, None], scale=scale)
+            ts.append(time.perf_counter() - t0)
+        med = sorted(ts)[1]
+        res["cpu_baseline"] = {"value": round(nq / med, 1), "unit": "tok/s", "cores": cores, "kind": "port",
+                               "sample": f"the reference's dense bool-masked bf16 SDPA over all 16384 keys for the "
+                                         f"last 64-query block (32 heads), median of 3, {med * 1e3:.1f} ms"}
+    return res
+
+
 def bench_block_sparse(fsi, args, dev):
     M, K, N, T = 4096, 8192, 8192, 128
     groups, nkb, nnb = M // T, K // T, N // T
@@ -342,8 +424,10 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="pattention",
-                    choices=["pattention", "routing", "decode_attn", "block_sparse"])
+                    choices=["pattention", "routing", "decode_attn", "prefill_attn", "block_sparse"])
     ap.add_argument("--eager", action="store_true", help="no graph capture (for per-dispatch counter runs)")
+    ap.add_argument("--no-pack", action="store_true",
+                    help="decode from the parameters in place (4-kernel split-K path) instead of packed weights")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 512 MiB device copy (reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -360,7 +444,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
     if args.workload != "pattention":
-        fn = {"routing": bench_routing, "decode_attn": bench_decode_attn,
+        fn = {"routing": bench_routing, "decode_attn": bench_decode_attn, "prefill_attn": bench_prefill_attn,
               "block_sparse": bench_block_sparse}[args.workload]
         with torch.no_grad():
             print(json.dumps(fn(fsi, args, dev)), flush=True)
@@ -371,10 +455,14 @@ def main():
     x_dec = torch.randn(DECODE_BATCH, 1, D_MODEL, device=dev, generator=gx).bfloat16()
     x_pre = torch.randn(1, PREFILL_TOKENS, D_MODEL, device=dev, generator=gx).bfloat16()
     # Routing once per layer (the eval cache fill), then cached blocks for every step.
+    # One decode call per layer packs its weights into the MFMA operand layout (a
+    # once-per-weight-version transform, outside the timed region).
     with torch.no_grad():
         for m in layers:
+            m.pack_decode_weights = not args.no_pack
             m.clear_cache()
             m(x_pre)
+            m(x_dec)
     n_active = int(layers[0]._cached_active_blocks.numel())
 
     if args.copy_calibration:
@@ -424,9 +512,11 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": DECODE_TRAFFIC_BYTES if n_active == BASE + REMOTE else None,
-            "kernel": "decode forward = dec_gateup + dec_act + dec_down + dec_reduce (4 launches, graph-replayed); "
-                      "achieved = algorithmic bytes of the forward / forward duration",
+            "traffic": (DECODE_TRAFFIC_BYTES_UNPACKED if args.no_pack else DECODE_TRAFFIC_BYTES)
+                       if n_active == BASE + REMOTE else None,
+            "kernel": ("decode forward = dec_gateup + dec_act + dec_down + dec_reduce (4 launches" if args.no_pack else
+                       "decode forward = ws_gateup_kernel + ws_down_kernel over packed weights (2 launches")
+                      + ", graph-replayed); achieved = algorithmic bytes of the forward / forward duration",
             "bytes_per_launch": bytes_step,
         },
     }

@@ -11,7 +11,10 @@ from .pattention import (
     HAS_TRITON,
     TritonSwiGLUPattentionMLP,
     convert_llm_mlp_to_pattention,
+    PackedPattentionWeights,
     fused_swiglu,
+    pack_pattention_weights,
+    pattention_decode_packed,
     pattention_forward,
     triton_fused_swiglu,
     triton_pattention,
@@ -72,6 +75,9 @@ __all__ = [
     "triton_fused_swiglu",
     "fused_swiglu",
     "pattention_forward",
+    "pattention_decode_packed",
+    "pack_pattention_weights",
+    "PackedPattentionWeights",
     "TritonSwiGLUPattentionMLP",
     "convert_llm_mlp_to_pattention",
     "HAS_HIP",

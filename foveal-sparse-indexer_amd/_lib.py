@@ -49,6 +49,18 @@ SIGNATURES: dict[str, tuple] = {
         [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr, _c_ptr],
     ),
+    "fsi_pattention_packed_size": (_c_size, [_c_i64, _c_i64, _c_i64]),
+    "fsi_pattention_pack": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_size,
+         _c_ptr],
+    ),
+    "fsi_pattention_packed_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "fsi_pattention_fwd_packed": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr,
+         _c_i64, _c_ptr, _c_size, _c_ptr, _c_ptr],
+    ),
     "fsi_swiglu": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
     "fsi_mlp_router_workspace_size": (_c_size, [_c_i64, _c_i64]),
     "fsi_mlp_router": (

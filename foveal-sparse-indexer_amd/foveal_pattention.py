@@ -22,7 +22,14 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import _lib
-from .pattention import pattention_forward
+from .pattention import (
+    PackedPattentionWeights,
+    _weights_key,
+    pack_pattention_weights,
+    packed_decode_supported,
+    pattention_decode_packed,
+    pattention_forward,
+)
 
 
 def mlp_pooled_route(
@@ -108,6 +115,12 @@ class FovealPattentionMLP(nn.Module):
         self.register_buffer("offsets", torch.arange(block_size, dtype=torch.int64))
 
         self._cached_active_blocks: Optional[Tensor] = None
+        # Decode calls (up to 64 tokens, bf16) stream a copy of k_gate, k_up and v
+        # repacked into the MFMA operand layout, rebuilt whenever a weight tensor is
+        # replaced or modified in place.  It holds as many bytes as the three weights;
+        # set pack_decode_weights = False to decode from the parameters directly.
+        self.pack_decode_weights = True
+        self._packed: Optional[PackedPattentionWeights] = None
         self.reset_parameters()
 
     # -- cache state machine (foveal_pattention.py:108-122) -----------------
@@ -169,6 +182,20 @@ class FovealPattentionMLP(nn.Module):
         q_16 = F.rms_norm(self.q_proj_16d(x), (self.index_dim,))
         return torch.matmul(q_16, self.block_keys_16d.t()) / math.sqrt(self.index_dim)
 
+    def _decode_packed(self, x_2d: Tensor, active_blocks: Tensor) -> bool:
+        return (self.pack_decode_weights and x_2d.dtype == torch.bfloat16 and self.k_gate.dtype == torch.bfloat16
+                and packed_decode_supported(x_2d.shape[0], self.hidden_dim, self.v.shape[1], self.intermediate_dim,
+                                            self.block_size, active_blocks.numel() * self.block_size))
+
+    def _packed_weights(self) -> PackedPattentionWeights:
+        key = _weights_key(self.k_gate, self.k_up, self.v)
+        if self._packed is None or self._packed.key != key:
+            self._packed = None
+            self._packed = pack_pattention_weights(self.k_gate.detach(), self.k_up.detach(), self.v.detach(),
+                                                   self.block_size)
+            self._packed.key = key
+        return self._packed
+
     def _rounding(self) -> str:
         return "fused" if self.use_fused_kernel else "eager"
 
@@ -189,8 +216,12 @@ class FovealPattentionMLP(nn.Module):
                                       self.remote_blocks)
             self._cached_active_blocks = active
         active_blocks = self._cached_active_blocks
-        out = pattention_forward(x_2d, self.k_gate, self.k_up, self.v, active_blocks, self.block_size,
-                                 activation="swiglu", rounding=self._rounding()).reshape(*orig_shape)
+        if self._decode_packed(x_2d, active_blocks):
+            out = pattention_decode_packed(x_2d, self._packed_weights(), active_blocks,
+                                           rounding=self._rounding()).reshape(*orig_shape)
+        else:
+            out = pattention_forward(x_2d, self.k_gate, self.k_up, self.v, active_blocks, self.block_size,
+                                     activation="swiglu", rounding=self._rounding()).reshape(*orig_shape)
         if return_router_info:
             if fast:
                 return out, {"active_blocks": active_blocks}

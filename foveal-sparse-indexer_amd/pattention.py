@@ -124,6 +124,100 @@ def pattention_forward(
     return out
 
 
+class PackedPattentionWeights:
+    """k_gate, k_up and v repacked into the MFMA operand layout of the decode
+    path (fsi_pattention_pack): one uint8 device buffer plus the shapes and the
+    identity of the tensors it was built from."""
+
+    def __init__(self, buf: Tensor, N_p: int, K: int, D_out: int, block_n: int, key: tuple):
+        self.buf, self.N_p, self.K, self.D_out, self.block_n, self.key = buf, N_p, K, D_out, block_n, key
+
+
+def _weights_key(*ts: Tensor) -> tuple:
+    return tuple((t.data_ptr(), t._version, tuple(t.shape), tuple(t.stride())) for t in ts)
+
+
+def packed_decode_supported(M: int, K: int, D_out: int, N_p: int, block_n: int, n_channels: int) -> bool:
+    """Shapes the packed decode kernels take (include/fsi.h, fsi_pattention_fwd_packed)."""
+    nc = K // 256
+    return (1 <= M <= 64 and K % 256 == 0 and nc in (1, 2, 4, 8, 16, 32) and D_out % 16 == 0 and block_n >= 32
+            and block_n & (block_n - 1) == 0 and N_p % block_n == 0 and 1 <= n_channels <= 8192)
+
+
+def pack_pattention_weights(k_gate: Tensor, k_up: Tensor, v: Tensor, block_n: int) -> PackedPattentionWeights:
+    """Repack bf16 k_gate / k_up (N_p, K) and v (N_p, D_out), in either storage
+    order, for pattention_decode_packed.  One pass over the weights."""
+    what = "pack_pattention_weights"
+    dev = _lib.require_gpu(k_gate, k_up, v, what=what)
+    if not (k_gate.dtype == k_up.dtype == v.dtype == torch.bfloat16):
+        raise TypeError(f"{what}: bfloat16 weights required")
+    key = _weights_key(k_gate, k_up, v)
+    k_gate, k_up = _rows_contig(k_gate), _rows_contig(k_up)
+    if k_up.stride(0) != k_gate.stride(0) or k_gate.stride(0) % 8:
+        k_gate, k_up = k_gate.contiguous(), k_up.contiguous()
+    v_transposed = v.stride(0) == 1 and v.stride(1) >= v.shape[0] and v.shape[1] > 1
+    if not v_transposed:
+        v = _rows_contig(v)
+    ldv = v.stride(1) if v_transposed else v.stride(0)
+    N_p, K = k_gate.shape
+    D_out = v.shape[1]
+    if tuple(k_up.shape) != (N_p, K) or v.shape[0] != N_p:
+        raise ValueError(f"{what}: k_gate {tuple(k_gate.shape)}, k_up {tuple(k_up.shape)}, v {tuple(v.shape)}")
+    L = _lib.lib()
+    nbytes = L.fsi_pattention_packed_size(N_p, K, D_out)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    st = L.fsi_pattention_pack(k_gate.data_ptr(), k_up.data_ptr(), k_gate.stride(0), v.data_ptr(), ldv,
+                               int(v_transposed), N_p, K, D_out, block_n, _lib.DTYPE_BF16, buf.data_ptr(), nbytes,
+                               _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return PackedPattentionWeights(buf, N_p, K, D_out, block_n, key)
+
+
+def pattention_decode_packed(
+    x2d: Tensor,
+    packed: PackedPattentionWeights,
+    active_blocks: Optional[Tensor],
+    rounding: str = "fused",
+    out: Optional[Tensor] = None,
+) -> Tensor:
+    """SwiGLU Pattention of up to 64 bf16 tokens over packed weights: the same
+    result as pattention_forward(x2d, k_gate, k_up, v, active_blocks, block_n,
+    "swiglu", rounding) up to fp32 summation order."""
+    what = "pattention_decode_packed"
+    dev = _lib.require_gpu(x2d, packed.buf, what=what)
+    if x2d.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: x dtype {x2d.dtype} (bfloat16 only)")
+    x2d = _rows_contig(x2d)
+    if x2d.stride(0) % 8 or x2d.data_ptr() % 16:
+        x2d = x2d.contiguous()
+    M, K = x2d.shape
+    if K != packed.K:
+        raise ValueError(f"{what}: x has K={K}, weights {packed.K}")
+    if active_blocks is not None:
+        idx = _as_index_tensor(active_blocks, dev)
+        n_active = idx.numel()
+    else:
+        idx, n_active = None, 0
+    n_ch = packed.N_p if idx is None else n_active * packed.block_n
+    if out is None:
+        out = torch.empty((M, packed.D_out), dtype=torch.bfloat16, device=dev)
+    if idx is not None and n_active == 0:
+        return out.zero_()
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    ws = _lib.workspace(dev, L.fsi_pattention_packed_workspace_size(M, K, packed.D_out, n_ch, packed.block_n),
+                        stream)
+    err = _lib.error_word(dev)
+    st = L.fsi_pattention_fwd_packed(
+        x2d.data_ptr(), x2d.stride(0), packed.buf.data_ptr(), _lib.ptr(idx), n_active, packed.block_n, M, K,
+        packed.N_p, packed.D_out, _lib.DTYPE_BF16, _lib.ROUNDING[rounding], out.data_ptr(), out.stride(0),
+        ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+    return out
+
+
 def triton_pattention(
     x: Tensor,
     k_gate: Tensor,

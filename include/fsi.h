@@ -104,6 +104,39 @@ FSI_API int fsi_pattention_fwd(const void* x, int64_t ldx, const void* k_gate, c
                        int activation, int rounding, void* out, int64_t ldo, void* workspace,
                        size_t workspace_bytes, int* err, void* stream);
 
+/* ------------------------------------------------------------------------- *
+ * Decode Pattention over weights repacked into the MFMA operand layout (bf16,
+ * SwiGLU).  The reference streams k_gate / k_up / v rows of the active blocks
+ * after copying them (foveal_pattention.py:115-122, 278-288); here the three
+ * weights are repacked once per weight version, and each decode step streams
+ * the active blocks' 1 KiB operand tiles.
+ *
+ * fsi_pattention_pack: k_gate, k_up [N_p, K] (row stride ldk); v as in
+ * fsi_pattention_fwd ([N_p, D_out], or [D_out, N_p] storage with v_transposed).
+ * packed: fsi_pattention_packed_size(N_p, K, D_out) bytes, 256-byte aligned.
+ * Requires block_n a power of two >= 32 dividing N_p, K % 32 == 0,
+ * D_out % 16 == 0.
+ *
+ * fsi_pattention_fwd_packed: out[M, D_out] = (silu(x K_g,S^T) * (x K_u,S^T)) V_S
+ * for 1 <= M <= 64 tokens, K = 256 * {1, 2, 4, 8, 16, 32}, at most 8192 active
+ * channels; rounding as fsi_pattention_fwd.  Out-of-range block ids contribute
+ * zero and are reported through err.  Workspace:
+ * fsi_pattention_packed_workspace_size(M, K, D_out, n_channels, block_n).
+ * ------------------------------------------------------------------------- */
+FSI_API size_t fsi_pattention_packed_size(int64_t N_p, int64_t K, int64_t D_out);
+
+FSI_API int fsi_pattention_pack(const void* k_gate, const void* k_up, int64_t ldk, const void* v, int64_t ldv,
+                                int v_transposed, int64_t N_p, int64_t K, int64_t D_out, int64_t block_n, int dtype,
+                                void* packed, size_t packed_bytes, void* stream);
+
+FSI_API size_t fsi_pattention_packed_workspace_size(int64_t M, int64_t K, int64_t D_out, int64_t n_channels,
+                                                    int64_t block_n);
+
+FSI_API int fsi_pattention_fwd_packed(const void* x, int64_t ldx, const void* packed, const int32_t* active_blocks,
+                                      int64_t n_active, int64_t block_n, int64_t M, int64_t K, int64_t N_p,
+                                      int64_t D_out, int dtype, int rounding, void* out, int64_t ldo,
+                                      void* workspace, size_t workspace_bytes, int* err, void* stream);
+
 /* Elementwise SwiGLU: out = silu(g) * u, computed in fp32 and rounded once to
  * the storage dtype (rounding = FUSED) or with torch-eager rounding points
  * (rounding = EAGER).  Replaces triton_fused_swiglu / _swiglu_fwd_kernel

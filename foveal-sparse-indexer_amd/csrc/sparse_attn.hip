@@ -281,6 +281,355 @@ __global__ __launch_bounds__(64 * SA_WAVES) void sparse_attn_kernel(SAParams P) 
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// LDS variant for query blocks of a multiple of 64 (FovealSparseAttention's
+// pages; power-of-two block, at most 64 listed pages, positive scale).  A
+// workgroup is the GQA group's query heads (up to 4) at 64 queries: 8 waves,
+// each one head x SAL_QT query tiles (32 queries at SAL_QT = 2, two waves per
+// SIMD; 4 tiles at one wave per SIMD measured 2.53 vs 1.63 ms at 16K tokens).
+// Every 32-key chunk (K rows and the V^T copy) is moved once per workgroup
+// into a ring of LDS stages with direct-to-LDS loads, SAL_AHEAD chunks ahead,
+// and read from there by all 8 waves: a chunk serves 4 heads x 64 queries.  The
+// 16-byte pieces of each LDS row are XOR-swizzled so the 16 rows of a fragment
+// read fall on 16 different bank groups.  Q^T operands are parked in LDS.  The
+// block's remote pages are checked, de-duplicated and compacted once; chunks
+// are described by wave-uniform scalar code.  Per chunk the S^T tiles of all
+// query tiles are formed first, then their softmax, then the P V products, so
+// consecutive MFMAs are independent.  The softmax skips the per-key mask for
+// chunks every query sees, moves its running max only by jumps above 2^8
+// (rescaling the accumulators rarely), and builds the bf16 hi + lo halves of P
+// with v_cvt_pk_bf16_f32.  Query blocks run from the last (most keys) to the
+// first.
+// ---------------------------------------------------------------------------
+// Two fp32 values to a packed bf16 pair (round to nearest even) with gfx950's
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+#ifndef FSI_SAL_QT
+#define FSI_SAL_QT 2
+#endif
+constexpr int SAL_QT = FSI_SAL_QT;           // query tiles per wave
+constexpr int SAL_HALVES = 4 / SAL_QT;       // waves per query head (64 queries split)
+constexpr int SAL_WAVES = 4 * SAL_HALVES;    // 4 query heads per workgroup
+constexpr int SAL_MAX_CAP = 64;  // listed pages per query block
+constexpr int SAL_AHEAD = 3;     // chunks in flight ahead of the one computed
+constexpr int SAL_STAGES = SAL_AHEAD + 1;
+typedef __attribute__((address_space(3))) void sal_lds_t;
+typedef __attribute__((address_space(1))) void sal_glb_t;
+
+template <int N>
+__device__ __forceinline__ void sal_wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void sal_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int HD>
+__global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParams P) {
+  constexpr int KS = HD / 32;
+  constexpr int DT = HD / 16;
+  constexpr int KROW = HD * 2;                  // bytes of one key row
+  constexpr int KBYTES = SA_CHUNK * KROW;       // K rows of a chunk
+  constexpr int VBYTES = HD * SA_CHUNK * 2;     // V^T of a chunk: HD rows of 64 B
+  constexpr int STAGE = KBYTES + VBYTES;
+  constexpr int LOADS = STAGE / 1024;           // 1 KiB direct loads per chunk
+  constexpr int LPW = LOADS / SAL_WAVES;        // per wave
+  static_assert(LOADS % SAL_WAVES == 0, "chunk loads must split over the waves");
+  constexpr int KPR = KROW / 16;                // 16-byte pieces per key row
+  __shared__ __attribute__((aligned(1024))) char ring[SAL_STAGES][STAGE];
+  // Q^T operand tiles of each wave, (query tile, k-step) KiB in lane order
+  __shared__ __attribute__((aligned(1024))) char qlds[SAL_WAVES][SAL_QT * KS * 1024];
+  __shared__ int wl[SAL_MAX_CAP];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qblk0 = (gridDim.x - 1 - blockIdx.x) * 64;  // the workgroup's 64 queries
+  const int half = wave / 4;                               // this wave's part of them
+  const int q0 = qblk0 + half * 16 * SAL_QT;
+  const int per_g = (P.G + 3) / 4;
+  int y = blockIdx.y;
+  const int hsub = y % per_g;
+  y /= per_g;
+  const int g = y % P.Hkv;
+  const int b = y / P.Hkv;
+  const int hg = hsub * 4 + (wave & 3);
+  const bool head_live = hg < P.G;  // idle waves still load and meet the barriers
+  const int h = g * P.G + (head_live ? hg : 0);
+  const int r = lane & 15, grp = lane >> 4;
+  const int qb = qblk0 / P.block;
+
+  // ---- listed pages: validity, first-listing de-duplication, compaction ----
+  int cnt = P.counts[b * P.cs_b + qb * P.cs_q];
+  cnt = cnt < 0 ? 0 : (cnt > P.cap ? P.cap : cnt);
+  const int32_t* list = P.lists + b * P.ls_b + qb * P.ls_q;
+  const int myblk = lane < cnt ? list[lane] : -1;
+  bool okl = lane < cnt && myblk >= 0 && myblk < P.n_blocks;
+  if (wave == 0 && lane < cnt && !okl && P.err) set_error(P.err, FSI_ERR_INDEX_RANGE);
+  if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
+    // the mask is a union: a page listed twice counts once
+    for (int s2 = 0; s2 < SAL_MAX_CAP; ++s2) {
+      if (s2 >= cnt) break;  // uniform
+      const int other = __builtin_amdgcn_readlane(myblk, s2);
+      okl = okl && !(s2 < lane && other == myblk);
+    }
+  }
+  const uint64_t vmask = __ballot(okl);
+  if (wave == 0 && okl) wl[__popcll(vmask & ((uint64_t(1) << lane) - 1))] = myblk;
+  const int n_remote = __popcll(vmask);
+
+  int n_local = 0, c_lo = 0;
+  if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
+    const int klo = qblk0 - P.window + 1 > 0 ? qblk0 - P.window + 1 : 0;
+    const int khi = qblk0 + 63 < P.T - 1 ? qblk0 + 63 : P.T - 1;
+    c_lo = klo / SA_CHUNK;
+    n_local = khi / SA_CHUNK - c_lo + 1;
+  }
+  const int per_block = P.block / SA_CHUNK;  // a power of two (host-checked)
+  const int pb_shift = __builtin_ctz(per_block);
+  const int n_chunks = n_local + n_remote * per_block;
+  __syncthreads();  // wl is written
+
+  // chunk i: absolute chunk c, keys [0, hi) of it, local-window chunk or page chunk
+  auto describe = [&](int i, int& c, int& hi, bool& local) {
+    if (i < n_local) {
+      c = c_lo + i;
+      hi = SA_CHUNK;
+      local = true;
+    } else {
+      const int j = i - n_local;
+      const int blk = __builtin_amdgcn_readfirstlane(wl[j >> pb_shift]);
+      const int k0 = blk * P.block;
+      const int k1 = k0 + P.block < P.T ? k0 + P.block : P.T;
+      c = k0 / SA_CHUNK + (j & (per_block - 1));
+      hi = k1 - c * SA_CHUNK;
+      hi = hi > SA_CHUNK ? SA_CHUNK : hi;
+      if (hi <= 0) {  // past the end of the sequence: load the page's first chunk, use nothing
+        c = k0 / SA_CHUNK;
+        hi = 0;
+      }
+      local = false;
+    }
+  };
+
+  // ---- direct loads of chunk c into stage st: this wave's LPW KiB of it ----
+  const bf16_t* kbase = P.k + b * P.ks_b + g * P.ks_h;
+  const bf16_t* vtbase = P.vt + (static_cast<int64_t>(b) * P.Hkv + g) * P.n32 * HD * SA_CHUNK;
+  // Per-lane parts of the addresses, fixed for the whole kernel: load i of this
+  // wave is K row krow[i] / 16-byte piece, or V^T row / piece of the chunk.
+  int64_t loff[LPW];
+  int krow[LPW];
+  bool isk[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int inst = wave * LPW + i;
+    const int off = inst * 1024 + lane * 16;  // byte offset in the stage
+    isk[i] = off < KBYTES;
+    if (isk[i]) {
+      const int row = off / KROW, slot = (off % KROW) / 16;  // key row, 16-byte slot
+      krow[i] = row;
+      loff[i] = static_cast<int64_t>(row) * P.ks_t + 8 * (slot ^ (row & (KPR - 1) & 15));
+    } else {
+      const int vo = off - KBYTES;
+      const int row = vo / 64, slot = (vo % 64) / 16;  // V^T row (dim), 16-byte slot
+      krow[i] = 0;
+      loff[i] = row * SA_CHUNK + 8 * (slot ^ ((row >> 2) & 3));
+    }
+  }
+  auto issue = [&](int c, int st) {
+    const bf16_t* kc = kbase + static_cast<int64_t>(c) * SA_CHUNK * P.ks_t;
+    const bf16_t* vc = vtbase + static_cast<int64_t>(c) * HD * SA_CHUNK;
+    const bool tail = (c + 1) * SA_CHUNK > P.T;  // uniform: rows past T read row T - 1
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const bf16_t* src = isk[i] ? kc + loff[i] : vc + loff[i];
+      if (tail && isk[i] && c * SA_CHUNK + krow[i] >= P.T)
+        src = kbase + static_cast<int64_t>(P.T - 1) * P.ks_t + (loff[i] - static_cast<int64_t>(krow[i]) * P.ks_t);
+      __builtin_amdgcn_global_load_lds((sal_glb_t*)src, (sal_lds_t*)(&ring[st][(wave * LPW + i) * 1024]), 16, 0, 0);
+    }
+  };
+
+  // Q^T operands (lane (r, grp) holds Q[query 16 qt + r][32 ks + 8 grp .. +8]) parked in LDS
+#pragma unroll
+  for (int qt = 0; qt < SAL_QT; ++qt) {
+    const int myq = q0 + 16 * qt + r;
+    const int qq = myq < P.T ? myq : P.T - 1;
+    const bf16_t* qp = P.q + b * P.qs_b + h * P.qs_h + static_cast<int64_t>(qq) * P.qs_t + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      *reinterpret_cast<u32x4_t*>(&qlds[wave][(qt * KS + ks) * 1024 + lane * 16]) =
+          *reinterpret_cast<const u32x4_t*>(qp + 32 * ks);
+  }
+  f32x4_t acc[SAL_QT][DT];
+  float m_run[SAL_QT], l_run[SAL_QT];
+#pragma unroll
+  for (int qt = 0; qt < SAL_QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int i = 0; i < DT; ++i) acc[qt][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // the Q loads above are this wave's only other vector loads: let them land
+  // before the ring's vmcnt accounting starts
+  sal_wait_vmcnt<0>();
+  for (int i = 0; i < SAL_AHEAD; ++i) {
+    if (i >= n_chunks) break;
+    int c, hi;
+    bool lc;
+    describe(i, c, hi, lc);
+    issue(c, i % SAL_STAGES);
+  }
+
+  for (int i = 0; i < n_chunks; ++i) {
+    // chunk i landed: at most the loads of chunks i + 1 .. i + AHEAD - 1 remain
+    const int later = (i + SAL_AHEAD - 1 < n_chunks - 1 ? i + SAL_AHEAD - 1 : n_chunks - 1) - i;
+    if (later >= 2) sal_wait_vmcnt<2 * LPW>();
+    else if (later == 1) sal_wait_vmcnt<LPW>();
+    else sal_wait_vmcnt<0>();
+    sal_barrier();
+    if (i + SAL_AHEAD < n_chunks) {  // into the stage chunk i - 1 used
+      int c, hi;
+      bool lc;
+      describe(i + SAL_AHEAD, c, hi, lc);
+      issue(c, (i + SAL_AHEAD) % SAL_STAGES);
+    }
+    int c, hi;
+    bool local;
+    describe(i, c, hi, local);
+    if (hi <= 0 || !head_live) continue;  // uniform: an empty chunk or an idle wave
+    const char* stg = ring[i % SAL_STAGES];
+    // K fragments: lane (r, grp) reads key 16 tile + r, dims 32 ks + 8 grp .. +8
+    u32x4_t kf[2 * KS];
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int row = 16 * tile + r;
+        kf[tile * KS + ks] = *reinterpret_cast<const u32x4_t*>(
+            stg + row * KROW + 16 * ((4 * ks + grp) ^ (row & (KPR - 1) & 15)));
+      }
+    // V^T fragments: lane (r, grp) reads dim 16 dt + r, slots 8 grp .. +8
+    u32x4_t vf[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int row = 16 * dt + r;
+      vf[dt] = *reinterpret_cast<const u32x4_t*>(stg + KBYTES + row * 64 + 16 * (grp ^ ((row >> 2) & 3)));
+    }
+    const int kc0 = c * SA_CHUNK;
+    // phase 1: S^T tiles of the 4 query tiles (8 independent accumulator chains)
+    f32x4_t st[SAL_QT][2];
+#pragma unroll
+    for (int qt = 0; qt < SAL_QT; ++qt) st[qt][0] = st[qt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int qt = 0; qt < SAL_QT; ++qt) {
+        const u32x4_t qop = *reinterpret_cast<const u32x4_t*>(&qlds[wave][(qt * KS + ks) * 1024 + lane * 16]);
+#pragma unroll
+        for (int tile = 0; tile < 2; ++tile) st[qt][tile] = mfma16x16x32(kf[tile * KS + ks], qop, st[qt][tile]);
+      }
+    // phase 2: online softmax of the 4 query tiles.  Chunks whose keys every
+    // query of the wave sees (inside all windows, or a page wholly before them)
+    // skip the per-key mask.
+    const bool nomask = local ? (kc0 + SA_CHUNK - 1 <= q0 && kc0 > q0 + 16 * SAL_QT - 1 - P.window &&
+                                 kc0 + SA_CHUNK <= P.T)
+                              : (hi == SA_CHUNK && kc0 + SA_CHUNK - 1 <= q0 - P.window);
+    float alpha[SAL_QT];
+    u32x4_t pbh[SAL_QT], pbl[SAL_QT];
+#pragma unroll
+    for (int qt = 0; qt < SAL_QT; ++qt) {
+      const int myq = q0 + 16 * qt + r;
+      float sv[8];  // raw scores, -inf where masked
+      if (nomask) {
+#pragma unroll
+        for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sv[tile * 4 + j] = st[qt][tile][j];
+      } else {
+#pragma unroll
+        for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int tau = 16 * tile + 4 * grp + j;
+            const int key = kc0 + tau;
+            bool ok = tau < hi && key < P.T;
+            if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
+              const bool in_win = key <= myq && key > myq - P.window;
+              ok = ok && (local ? in_win : !in_win);
+            }
+            sv[tile * 4 + j] = ok ? st[qt][tile][j] : -INFINITY;
+          }
+      }
+      float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // The running max (log2 units) moves only when a score exceeds it by more
+      // than 8: P then stays below 2^8 and the accumulators are rescaled rarely.
+      const float m_cand = mx * P.scale_log2;
+      const bool bump = m_cand > m_run[qt] + 8.f;
+      const float m_new = bump ? m_cand : m_run[qt];
+      alpha[qt] = bump ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;  // exp2(-inf) = 0 on the first bump
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // no valid key yet: every p is exp2(-inf) = 0
+      float psum = 0.f;
+      uint32_t pk_hi[4], pk_lo[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        // P as a bf16 hi + lo pair, converted with v_cvt_pk_bf16_f32 (round to nearest even)
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w], P.scale_log2, -m_use));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w + 1], P.scale_log2, -m_use));
+        psum += p0 + p1;
+        pk_hi[w] = cvt_pk_bf16(p0, p1);
+        pk_lo[w] = cvt_pk_bf16(p0 - lo_bf16(pk_hi[w]), p1 - hi_bf16(pk_hi[w]));
+      }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      l_run[qt] = l_run[qt] * alpha[qt] + psum;
+      m_run[qt] = m_new;
+      pbh[qt] = u32x4_t{pk_hi[0], pk_hi[1], pk_hi[2], pk_hi[3]};
+      pbl[qt] = u32x4_t{pk_lo[0], pk_lo[1], pk_lo[2], pk_lo[3]};
+    }
+    // phase 3: rescale (skipped while no query's running max moved) and P V
+    // (hi then lo halves; consecutive MFMAs independent)
+#pragma unroll
+    for (int qt = 0; qt < SAL_QT; ++qt) {
+      if (__ballot(alpha[qt] != 1.f) != 0) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[qt][dt][j] *= alpha[qt];
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int qt = 0; qt < SAL_QT; ++qt) acc[qt][dt] = mfma16x16x32(vf[dt], pbh[qt], acc[qt][dt]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int qt = 0; qt < SAL_QT; ++qt) acc[qt][dt] = mfma16x16x32(vf[dt], pbl[qt], acc[qt][dt]);
+  }
+
+  if (!head_live) return;
+#pragma unroll
+  for (int qt = 0; qt < SAL_QT; ++qt) {
+    const int myq = q0 + 16 * qt + r;
+    if (myq < P.T) {
+      const float inv = l_run[qt] > 0.f ? 1.f / l_run[qt] : 0.f;
+      bf16_t* o = P.out + b * P.os_b + h * P.os_h + static_cast<int64_t>(myq) * P.os_t + 4 * grp;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const u32x2_t w = u32x2_t{pack_bf16x2(acc[qt][dt][0] * inv, acc[qt][dt][1] * inv),
+                                  pack_bf16x2(acc[qt][dt][2] * inv, acc[qt][dt][3] * inv)};
+        *reinterpret_cast<u32x2_t*>(o + 16 * dt) = w;
+      }
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -369,11 +718,17 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
   P.err = err;
   const dim3 grid(static_cast<unsigned>((T + 15) / 16),
                   static_cast<unsigned>(B * Hkv * ((P.G + SA_WAVES - 1) / SA_WAVES)));
+  // 64 queries per wave when a query block holds whole 64-query tiles and its list fits one wave
+  const bool wide = block % 64 == 0 && fsi_host::is_pow2(block) && capacity <= SAL_MAX_CAP && scale > 0.f;
+  const dim3 grid_w(static_cast<unsigned>((T + 63) / 64), grid.y);
   auto launch = [&](auto hd_tag) -> int {
     constexpr int HD = decltype(hd_tag)::value;
     sa_vt_kernel<HD><<<g1, 256, 0, st>>>(static_cast<const bf16_t*>(v), vs_b, vs_h, vs_t, P.B, P.Hkv, P.T, n32, vt);
     FSI_HIP_LAUNCH_CHECK("sparse_attn v copy");
-    sparse_attn_kernel<HD><<<grid, 64 * SA_WAVES, 0, st>>>(P);
+    if (wide && HD >= 64)
+      sparse_attn_lds_kernel<(HD >= 64 ? HD : 64)><<<grid_w, 64 * SAL_WAVES, 0, st>>>(P);
+    else
+      sparse_attn_kernel<HD><<<grid, 64 * SA_WAVES, 0, st>>>(P);
     FSI_HIP_LAUNCH_CHECK("sparse_attn");
     return FSI_OK;
   };

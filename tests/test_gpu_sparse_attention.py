@@ -38,6 +38,10 @@ LR_CASES = [
     (1, 2, 1, 16, 96, 32, 40, 2),      # head_dim 16
     (1, 6, 1, 64, 192, 64, 1000, 2),   # window beyond T; 6 heads per KV head (two workgroups)
     (2, 4, 2, 128, 256, 64, 64, 0),    # no remote pages at all
+    (1, 8, 2, 128, 200, 64, 100, 3),   # T not a multiple of the 64-query block
+    (2, 16, 2, 64, 384, 64, 128, 5),   # 8 query heads per KV head (two workgroups)
+    (1, 4, 4, 128, 256, 64, 64, 70),   # more than 64 listed pages per block
+    (1, 4, 1, 128, 512, 128, 200, 3),  # 128-token blocks: 4 chunks per listed block
 ]
 
 

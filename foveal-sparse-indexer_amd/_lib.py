@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple] = {
          _c_i64, _c_ptr, _c_size, _c_ptr, _c_ptr],
     ),
     "fsi_swiglu": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
+    "fsi_swiglu_bwd": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_int, _c_ptr]),
     "fsi_mlp_router_workspace_size": (_c_size, [_c_i64, _c_i64]),
     "fsi_mlp_router": (
         _c_int,

@@ -502,6 +502,31 @@ __global__ void swiglu_f32(const float* __restrict__ g, const float* __restrict_
     out[i] = silu_f32(g[i]) * u[i];
 }
 
+// SwiGLU backward (pattention_triton.py:49-71): with s = sigmoid(g),
+//   du = dout * g s,   dg = dout * u * s (1 + g (1 - s)),
+// in fp32, each rounded once to the storage dtype.
+template <typename T>
+__device__ __forceinline__ float ld_as_f32(const T* p, int64_t i) {
+  if constexpr (sizeof(T) == 2) return bf16_to_f32(reinterpret_cast<const bf16_t*>(p)[i]);
+  else return reinterpret_cast<const float*>(p)[i];
+}
+template <typename T>
+__device__ __forceinline__ void st_from_f32(T* p, int64_t i, float v) {
+  if constexpr (sizeof(T) == 2) reinterpret_cast<bf16_t*>(p)[i] = f32_to_bf16(v);
+  else reinterpret_cast<float*>(p)[i] = v;
+}
+template <typename T>
+__global__ void swiglu_bwd_kernel(const T* __restrict__ dout, const T* __restrict__ g, const T* __restrict__ u,
+                                  T* __restrict__ dg, T* __restrict__ du, int64_t n) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float d = ld_as_f32(dout, i), gv = ld_as_f32(g, i), uv = ld_as_f32(u, i);
+    const float s = 1.0f / (1.0f + expf(-gv));
+    st_from_f32(du, i, d * (gv * s));
+    st_from_f32(dg, i, d * uv * (s * (1.0f + gv * (1.0f - s))));
+  }
+}
+
 // Byte-wise zero fill of `rows` rows of `row_bytes` bytes (stride `ld_bytes`).
 // A kernel rather than hipMemsetAsync so the call stays safe inside graph capture.
 __global__ void zero_rows(char* __restrict__ p, int64_t ld_bytes, int64_t row_bytes) {
@@ -732,6 +757,27 @@ int fsi_swiglu(const void* g, const void* u, void* out, int64_t n, int dtype, in
     swiglu_f32<<<blocks, 256, 0, st>>>(static_cast<const float*>(g), static_cast<const float*>(u),
                                        static_cast<float*>(out), n);
   FSI_HIP_LAUNCH_CHECK("swiglu");
+  return FSI_OK;
+}
+
+int fsi_swiglu_bwd(const void* dout, const void* g, const void* u, void* dg, void* du, int64_t n, int dtype,
+                   void* stream) {
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16 || dtype == FSI_DTYPE_F32, FSI_ERR_DTYPE, "swiglu_bwd: dtype %d", dtype);
+  FSI_CHECK_ARG(n >= 0, FSI_ERR_SHAPE, "swiglu_bwd: n < 0");
+  if (n == 0) return FSI_OK;
+  FSI_CHECK_ARG(dout && g && u && dg && du, FSI_ERR_INVALID_ARG, "swiglu_bwd: null pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t blocks64 = (n + 255) / 256;
+  const unsigned blocks = (unsigned)(blocks64 > 16384 ? 16384 : blocks64);
+  if (dtype == FSI_DTYPE_BF16)
+    swiglu_bwd_kernel<bf16_t><<<blocks, 256, 0, st>>>(
+        static_cast<const bf16_t*>(dout), static_cast<const bf16_t*>(g), static_cast<const bf16_t*>(u),
+        static_cast<bf16_t*>(dg), static_cast<bf16_t*>(du), n);
+  else
+    swiglu_bwd_kernel<float><<<blocks, 256, 0, st>>>(static_cast<const float*>(dout), static_cast<const float*>(g),
+                                                     static_cast<const float*>(u), static_cast<float*>(dg),
+                                                     static_cast<float*>(du), n);
+  FSI_HIP_LAUNCH_CHECK("swiglu_bwd");
   return FSI_OK;
 }
 

@@ -10,7 +10,8 @@ active-block cache and forward signature as the reference
   * bf16 rounding follows the reference's GPU path when use_fused_kernel=True
     (fused SwiGLU, one rounding of silu(g)*u; :281-282) and its eager path
     otherwise (silu(g) and the product rounded separately; :283-284).
-  * Inference only: training-mode forward raises NotImplementedError.
+  * Training mode follows the reference's per-token routing and additive stream
+    with library GEMMs around the HIP SwiGLU forward / backward kernels.
 """
 from __future__ import annotations
 
@@ -29,6 +30,7 @@ from .pattention import (
     packed_decode_supported,
     pattention_decode_packed,
     pattention_forward,
+    triton_fused_swiglu,
 )
 
 
@@ -199,11 +201,47 @@ class FovealPattentionMLP(nn.Module):
     def _rounding(self) -> str:
         return "fused" if self.use_fused_kernel else "eager"
 
+    def _train_forward(self, x_2d: Tensor, orig_shape, return_router_info: bool):
+        """Training forward (foveal_pattention.py:292-307, 328-342): per-token
+        router scores, top-k of their token mean over the remote blocks, the
+        active rows gathered from the parameters, three library GEMMs with the
+        HIP SwiGLU (forward and backward kernels) between them, and the additive
+        16-D stream softmax(scores / T) @ block_keys -> out_proj_16d.  Gradients
+        reach k_gate, k_up, v (active rows), q_proj_16d, block_keys_16d and
+        out_proj_16d as in the reference."""
+        _lib.require_gpu(x_2d, what="FovealPattentionMLP training forward")
+        scores = self.compute_router_scores(x_2d)
+        mean_scores = scores.mean(dim=0)
+        _, top_remote = torch.topk(mean_scores[self.base_blocks:], k=self.remote_blocks)
+        if self.base_blocks > 0:
+            active_blocks = torch.cat([
+                torch.arange(self.base_blocks, device=x_2d.device, dtype=torch.int32),
+                (top_remote + self.base_blocks).to(torch.int32),
+            ])
+        else:
+            active_blocks = top_remote.to(torch.int32)
+        indices = (active_blocks.view(-1, 1).to(torch.int64) * self.block_size + self.offsets).flatten()
+        kg_proj = F.linear(x_2d, self.k_gate[indices])
+        ku_proj = F.linear(x_2d, self.k_up[indices])
+        if self.use_fused_kernel:
+            act = triton_fused_swiglu(kg_proj, ku_proj)
+        else:
+            act = F.silu(kg_proj) * ku_proj
+        out_patt = F.linear(act, self.v[indices].t())
+        soft = F.softmax(scores / self.temperature, dim=-1)
+        context_16d = torch.matmul(soft, self.block_keys_16d)
+        out = (out_patt + self.out_proj_16d(context_16d)).reshape(*orig_shape)
+        if return_router_info:
+            return out, {
+                "scores": scores,
+                "active_blocks": active_blocks,
+                "sparsity": (1.0 - self.total_active_blocks / self.num_blocks) * 100.0,
+            }
+        return out
+
     def forward(self, x: Tensor, return_router_info: bool = False):
         if self.training:
-            raise NotImplementedError(
-                "FovealPattentionMLP training forward is not implemented on the MI355X path; call .eval()"
-            )
+            return self._train_forward(x.reshape(-1, x.shape[-1]), x.shape, return_router_info)
         orig_shape = x.shape
         D = orig_shape[-1]
         x_2d = x.reshape(-1, D)

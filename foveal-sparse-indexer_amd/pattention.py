@@ -244,19 +244,11 @@ def triton_pattention(
     return out
 
 
-def triton_fused_swiglu(g: Tensor, u: Tensor) -> Tensor:
-    """silu(g) * u in fp32, rounded once (pattention_triton.py:30-47, 98-104).
-    Forward only: the HIP build targets inference."""
-    return fused_swiglu(g, u, rounding="fused")
-
-
-def fused_swiglu(g: Tensor, u: Tensor, rounding: str = "fused") -> Tensor:
+def _swiglu_launch(g: Tensor, u: Tensor, rounding: str) -> Tensor:
     what = "swiglu"
     dev = _lib.require_gpu(g, u, what=what)
     if g.shape != u.shape or g.dtype != u.dtype:
         raise ValueError(f"{what}: g {tuple(g.shape)}/{g.dtype} vs u {tuple(u.shape)}/{u.dtype}")
-    if torch.is_grad_enabled() and (g.requires_grad or u.requires_grad):
-        raise NotImplementedError(f"{what}: backward is not implemented on the MI355X inference path")
     code = _lib.dtype_code(g.dtype, what)
     g_c, u_c = g.contiguous(), u.contiguous()
     out = torch.empty_like(g_c)
@@ -264,6 +256,49 @@ def fused_swiglu(g: Tensor, u: Tensor, rounding: str = "fused") -> Tensor:
                                _lib.ROUNDING[rounding], _lib.stream_handle(dev))
     _lib.check(st, what)
     return out
+
+
+class FusedSwiGLUFunction(torch.autograd.Function):
+    """silu(g) * u with its exact backward on the HIP kernels
+    (TritonFusedSwiGLUFunction, pattention_triton.py:73-96): the forward rounds
+    silu(g) * u once from fp32, the backward computes du = dout * silu(g) and
+    dg = dout * u * s (1 + g (1 - s)), s = sigmoid(g), in fp32."""
+
+    @staticmethod
+    def forward(ctx, g: Tensor, u: Tensor) -> Tensor:
+        g_c, u_c = g.contiguous(), u.contiguous()
+        ctx.save_for_backward(g_c, u_c)
+        return _swiglu_launch(g_c, u_c, "fused")
+
+    @staticmethod
+    def backward(ctx, dout: Tensor):
+        g, u = ctx.saved_tensors
+        what = "swiglu backward"
+        dev = _lib.require_gpu(dout, g, u, what=what)
+        code = _lib.dtype_code(g.dtype, what)
+        d = dout.to(g.dtype).contiguous()
+        dg, du = torch.empty_like(g), torch.empty_like(u)
+        st = _lib.lib().fsi_swiglu_bwd(d.data_ptr(), g.data_ptr(), u.data_ptr(), dg.data_ptr(), du.data_ptr(),
+                                       g.numel(), code, _lib.stream_handle(dev))
+        _lib.check(st, what)
+        return dg, du
+
+
+def triton_fused_swiglu(g: Tensor, u: Tensor) -> Tensor:
+    """silu(g) * u in fp32, rounded once, with exact gradients
+    (pattention_triton.py:30-104).  The `triton_` name is kept; the kernels are HIP."""
+    return FusedSwiGLUFunction.apply(g, u)
+
+
+def fused_swiglu(g: Tensor, u: Tensor, rounding: str = "fused") -> Tensor:
+    """silu(g) * u with the given bf16 rounding points ("fused": one rounding;
+    "eager": silu(g) rounded first, as torch's eager F.silu(g) * u).  The fused
+    form is differentiable (FusedSwiGLUFunction); the eager form is forward-only."""
+    if rounding == "fused":
+        return FusedSwiGLUFunction.apply(g, u)
+    if torch.is_grad_enabled() and (g.requires_grad or u.requires_grad):
+        raise NotImplementedError("swiglu: the eager-rounding form has no backward; use rounding='fused'")
+    return _swiglu_launch(g, u, rounding)
 
 
 class TritonSwiGLUPattentionMLP(nn.Module):

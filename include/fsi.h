@@ -143,6 +143,13 @@ FSI_API int fsi_pattention_fwd_packed(const void* x, int64_t ldx, const void* pa
  * (foveal_indexer/pattention_triton.py:30-47,98-104). */
 FSI_API int fsi_swiglu(const void* g, const void* u, void* out, int64_t n, int dtype, int rounding, void* stream);
 
+/* SwiGLU backward: with s = sigmoid(g), du = dout * g * s and
+ * dg = dout * u * s * (1 + g * (1 - s)), computed in fp32 and rounded once to the
+ * storage dtype.  Replaces _swiglu_bwd_kernel / TritonFusedSwiGLUFunction.backward
+ * (foveal_indexer/pattention_triton.py:49-71, 86-96). */
+FSI_API int fsi_swiglu_bwd(const void* dout, const void* g, const void* u, void* dg, void* du, int64_t n, int dtype,
+                           void* stream);
+
 /* ------------------------------------------------------------------------- *
  * Pooled 16-D router of FovealPattentionMLP in eval mode
  * (foveal_indexer/foveal_pattention.py:310-322):

@@ -8,8 +8,12 @@ lands at the same points as the reference):
   * _pattention_fused_kernel numerics   foveal_indexer/pattention_triton.py:153-201
                                         (fp32 accumulation, act cast to V dtype, fp32 acc)
   * _swiglu_fwd_kernel numerics         foveal_indexer/pattention_triton.py:40-47
+  * _swiglu_bwd_kernel                  foveal_indexer/pattention_triton.py:49-71 (closed form, fp64)
+  * FovealPattentionMLP training forward foveal_indexer/foveal_pattention.py:292-307, 328-342
 """
 from __future__ import annotations
+
+import math
 
 import torch
 import torch.nn.functional as F
@@ -112,3 +116,35 @@ def dense_swiglu_f64(x2d: Tensor, k_gate: Tensor, k_up: Tensor, v: Tensor, chann
     if channel_mask is not None:
         h = h * channel_mask.double()
     return h @ v.double()
+
+
+def swiglu_bwd_f64(dout: Tensor, g: Tensor, u: Tensor):
+    """(dg, du) of silu(g) * u in fp64 (pattention_triton.py:63-71):
+    s = sigmoid(g); du = dout * g s; dg = dout * u * s (1 + g (1 - s))."""
+    d, gg, uu = dout.double(), g.double(), u.double()
+    sg = torch.sigmoid(gg)
+    return d * uu * sg * (1.0 + gg * (1.0 - sg)), d * gg * sg
+
+
+def train_forward(m, x: Tensor, active: Tensor | None = None):
+    """FovealPattentionMLP.forward in training mode (foveal_pattention.py:292-307,
+    328-342) with torch CPU ops in the reference's order, on the module's own
+    parameters (autograd-capable): returns (out, active_blocks).  `active`, when
+    given, replaces the top-k selection (to check the arithmetic after routing
+    on its own)."""
+    D = x.shape[-1]
+    x_2d = x.reshape(-1, D)
+    q_16 = F.rms_norm(m.q_proj_16d(x_2d), (m.index_dim,))
+    scores = torch.matmul(q_16, m.block_keys_16d.t()) / math.sqrt(m.index_dim)
+    _, top_remote = torch.topk(scores.mean(dim=0)[m.base_blocks:], k=m.remote_blocks)
+    if active is None:
+        active = torch.cat([torch.arange(m.base_blocks, dtype=torch.int32),
+                            (top_remote + m.base_blocks).to(torch.int32)])
+    indices = (active.view(-1, 1).to(torch.int64) * m.block_size + m.offsets).flatten()
+    kg_proj = F.linear(x_2d, m.k_gate[indices])
+    ku_proj = F.linear(x_2d, m.k_up[indices])
+    act = F.silu(kg_proj) * ku_proj
+    out_patt = F.linear(act, m.v[indices].t())
+    soft = F.softmax(scores / m.temperature, dim=-1)
+    add = m.out_proj_16d(torch.matmul(soft, m.block_keys_16d))
+    return (out_patt + add).reshape(x.shape), active

@@ -72,3 +72,65 @@ def test_activations_closed_form():
         out = P.pattention_eager(x, kg, v, None, None, act, 64)
         ref = fn(x.double() @ kg.double().t()) @ v.double()
         assert P.rel_l2(out, ref) < 1e-6, act
+
+
+def test_swiglu_bwd_matches_autograd_fp64():
+    """The closed-form SwiGLU gradient of the reference's Triton backward
+    (pattention_triton.py:63-71) equals autograd through F.silu(g) * u."""
+    from oracle import pattention as P
+
+    g = torch.randn(257, dtype=torch.float64, requires_grad=True)
+    u = torch.randn(257, dtype=torch.float64, requires_grad=True)
+    dout = torch.randn(257, dtype=torch.float64)
+    (torch.nn.functional.silu(g) * u).backward(dout)
+    dg, du = P.swiglu_bwd_f64(dout, g.detach(), u.detach())
+    assert torch.allclose(dg, g.grad, rtol=1e-12, atol=1e-14)
+    assert torch.allclose(du, u.grad, rtol=1e-12, atol=1e-14)
+    # special cases: g = 0 -> dg = dout * u / 2, du = 0
+    z = torch.zeros(3, dtype=torch.float64)
+    dg0, du0 = P.swiglu_bwd_f64(torch.ones(3), z, torch.tensor([2.0, -4.0, 1.0]))
+    assert torch.allclose(dg0, torch.tensor([1.0, -2.0, 0.5], dtype=torch.float64)) and torch.all(du0 == 0)
+
+
+@pytest.mark.parametrize("base,remote,temp", [(2, 6, 1.0), (1, 3, 0.5), (0, 4, 2.0)])
+def test_train_forward_closed_form(base, remote, temp):
+    """train_forward (foveal_pattention.py:292-307, 328-342) against brute force:
+    per-token rms-normed 16-D queries, the active set = base blocks + the top
+    `remote` token-mean scores, dense SwiGLU in fp64 with the inactive channels
+    zeroed, plus softmax(scores / T) @ block_keys through out_proj."""
+    import math
+
+    import __graft_entry__
+
+    fi = __graft_entry__.load_package()
+    torch.manual_seed(base * 10 + remote)
+    H, I, bs, T = 64, 512, 64, 5
+    m = fi.FovealPattentionMLP(hidden_dim=H, intermediate_dim=I, block_size=bs, base_blocks=base,
+                               remote_blocks=remote, temperature=temp, dtype=torch.float64).train()
+    with torch.no_grad():
+        m.block_keys_16d.normal_()
+    x = torch.randn(T, H, dtype=torch.float64)
+    out, active = P.train_forward(m, x)
+
+    Wq, K16, Wo = m.q_proj_16d.weight.detach(), m.block_keys_16d.detach(), m.out_proj_16d.weight.detach()
+    nb = I // bs
+    scores = torch.zeros(T, nb, dtype=torch.float64)
+    add = torch.zeros(T, H, dtype=torch.float64)
+    for t in range(T):
+        q = [sum(Wq[i, d].item() * x[t, d].item() for d in range(H)) for i in range(16)]
+        r = math.sqrt(sum(v * v for v in q) / 16)
+        q = [v / r for v in q]
+        s = [sum(q[i] * K16[j, i].item() for i in range(16)) / 4.0 for j in range(nb)]
+        scores[t] = torch.tensor(s, dtype=torch.float64)
+        e = [math.exp((v - max(s)) / temp) for v in s]
+        p = [v / sum(e) for v in e]
+        c = [sum(p[j] * K16[j, i].item() for j in range(nb)) for i in range(16)]
+        add[t] = torch.tensor([sum(Wo[h, i].item() * c[i] for i in range(16)) for h in range(H)], dtype=torch.float64)
+    mean = scores.mean(0)
+    rem = sorted(range(base, nb), key=lambda j: -mean[j].item())[:remote]
+    assert active[:base].tolist() == list(range(base)) and sorted(active[base:].tolist()) == sorted(rem)
+    mask = torch.zeros(I, dtype=torch.float64)
+    for b in active.tolist():
+        mask[b * bs:(b + 1) * bs] = 1
+    want = P.dense_swiglu_f64(x, m.k_gate.detach(), m.k_up.detach(), m.v.detach(), mask) + add
+    assert torch.allclose(out.detach(), want, rtol=1e-10, atol=1e-10)

@@ -72,6 +72,9 @@ SIGNATURES: dict[str, tuple] = {
     "fsi_masked_softmax": (
         _c_int, [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
+    "fsi_masked_softmax_bwd": (
+        _c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
     "fsi_route_from_scores": (
         _c_int,
         [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, ctypes.c_float, _c_int, _c_int, _c_int, _c_ptr,
@@ -95,6 +98,19 @@ SIGNATURES: dict[str, tuple] = {
     "fsi_block_scores": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "fsi_additive_context": (
         _c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_ptr],
+    ),
+    "fsi_index_rms_norm_bwd": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_ptr]),
+    "fsi_index_pool_kv_bwd": (
+        _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr],
+    ),
+    "fsi_block_scores_bwd": (
+        _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr],
+    ),
+    "fsi_additive_context_bwd_workspace_size": (_c_size, [_c_i64, _c_i64]),
+    "fsi_additive_context_bwd": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_size,
+         _c_ptr],
     ),
     "fsi_kv_write": (
         _c_int,

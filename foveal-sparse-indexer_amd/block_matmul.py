@@ -18,7 +18,7 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import _lib
-from .core import FovealIndexer, Route, _forward_only, select_blocks
+from .core import FovealIndexer, Route, _forward_only, _PoolKVFn, select_blocks
 
 
 def block_sparse_linear(x2d: Tensor, weight: Tensor, bias: Optional[Tensor], active_blocks: Tensor,
@@ -180,20 +180,14 @@ class BlockSparseLinear(nn.Module):
             self._cached_kp, self._cached_vp = self.get_block_keys_and_values()
 
     def get_block_keys_and_values(self) -> Tuple[Tensor, Tensor]:
-        """Pooled 16-D key and value per weight block (block_matmul.py:109-128)."""
+        """Pooled 16-D key and value per weight block (block_matmul.py:109-128);
+        differentiable in the weight and the two 16-D projections."""
         what = "get_block_keys_and_values"
         k_lin = self.weight_to_k(self.weight).contiguous()
         v_lin = self.weight_to_v(self.weight).contiguous()
-        dev = _lib.require_gpu(k_lin, v_lin, what=what)
-        _forward_only(what, k_lin, v_lin)
-        d = self.indexer.index_dim
-        kb = torch.empty((1, self.num_blocks, d), dtype=k_lin.dtype, device=dev)
-        vb = torch.empty_like(kb)
-        st = _lib.lib().fsi_index_pool_kv(k_lin.data_ptr(), v_lin.data_ptr(), _lib.dtype_code(k_lin.dtype, what), 1,
-                                          self.out_features, d, self.block_size, kb.data_ptr(), vb.data_ptr(),
-                                          _lib.stream_handle(dev))
-        _lib.check(st, what)
-        return kb, vb
+        _lib.require_gpu(k_lin, v_lin, what=what)
+        _lib.dtype_code(k_lin.dtype, what)
+        return _PoolKVFn.apply(k_lin.unsqueeze(0), v_lin.unsqueeze(0), self.block_size)
 
     def forward(self, x: Tensor, compute_teacher_loss: bool = False) -> Tuple[Tensor, Dict[str, Any]]:
         orig_ndim = x.ndim

@@ -5,8 +5,11 @@ Same names, signatures, defaults and return structures as the reference
 `FovealIndexer` :163-353).  Softmax, ranking, prefix mass, counts, scoring,
 pooling and the additive-stream contraction run in the HIP library
 (csrc/routing.hip, csrc/indexer.hip); the D -> 16 projections are library
-GEMMs (nn.Linear).  Inference only: the HIP ops have no backward and refuse
-inputs that require grad while autograd is recording.
+GEMMs (nn.Linear).  masked_softmax and the FovealIndexer representations
+(compute_query_16d, compute_kv_blocks_16d, compute_block_scores,
+additive_stream) are differentiable through HIP backward kernels, as the
+reference's dual-gradient training needs (tests/test_indexer.py:63-101);
+select_blocks / route take no gradient (the reference detaches the scores).
 
 Differences by design:
   * equal probabilities are ranked lower index first (torch.sort leaves their
@@ -56,14 +59,46 @@ def _as_3d(scores: Tensor, what: str) -> Tensor:
     return scores.contiguous()
 
 
+class _MaskedSoftmaxFn(torch.autograd.Function):
+    """fsi_masked_softmax with fsi_masked_softmax_bwd as its gradient.
+    s3: contiguous (B, Q, N) scores; m8: uint8 mask view over (B, Q, N)."""
+
+    @staticmethod
+    def forward(ctx, s3: Tensor, m8: Tensor) -> Tensor:
+        what = "masked_softmax"
+        dev = s3.device
+        code = _lib.dtype_code(s3.dtype, what)
+        out = torch.empty_like(s3)
+        B, Q, N = s3.shape
+        st = _lib.lib().fsi_masked_softmax(s3.data_ptr(), code, B, Q, N, m8.data_ptr(), m8.stride(0), m8.stride(1),
+                                           m8.stride(2), out.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        ctx.save_for_backward(s3, m8)
+        return out
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        what = "masked_softmax backward"
+        s3, m8 = ctx.saved_tensors
+        dev = _lib.require_gpu(g, s3, what=what)
+        gc = g.to(s3.dtype).contiguous()
+        ds = torch.empty_like(s3)
+        B, Q, N = s3.shape
+        st = _lib.lib().fsi_masked_softmax_bwd(s3.data_ptr(), gc.data_ptr(), _lib.dtype_code(s3.dtype, what), B, Q, N,
+                                               m8.data_ptr(), m8.stride(0), m8.stride(1), m8.stride(2), ds.data_ptr(),
+                                               _lib.stream_handle(dev))
+        _lib.check(st, what)
+        return ds, None
+
+
 def masked_softmax(scores: Tensor, mask: Tensor) -> Tensor:
     """Softmax over `mask` with masked entries and all-masked rows exactly zero,
     computed in fp32 and returned in the scores' dtype (core.py:36-43).
-    scores: (..., N); mask: bool, broadcastable to scores."""
+    scores: (..., N); mask: bool, broadcastable to scores.  Differentiable in
+    the scores."""
     what = "masked_softmax"
     dev = _lib.require_gpu(scores, mask, what=what)
-    _forward_only(what, scores)
-    code = _lib.dtype_code(scores.dtype, what)
+    _lib.dtype_code(scores.dtype, what)
     shape = scores.shape
     if scores.dim() == 0:
         raise ValueError(f"{what}: scores must have at least one dimension")
@@ -75,12 +110,7 @@ def masked_softmax(scores: Tensor, mask: Tensor) -> Tensor:
         s3 = scores.contiguous().reshape(-1, 1, N)
         m = m.reshape(-1, 1, N)
     m8 = m.view(torch.uint8)  # bool and uint8 share the element size; strides carry over
-    out = torch.empty_like(s3)
-    B, Q, _ = s3.shape
-    st = _lib.lib().fsi_masked_softmax(s3.data_ptr(), code, B, Q, N, m8.data_ptr(), m8.stride(0), m8.stride(1),
-                                       m8.stride(2), out.data_ptr(), _lib.stream_handle(dev))
-    _lib.check(st, what)
-    return out.reshape(shape)
+    return _MaskedSoftmaxFn.apply(s3, m8).reshape(shape)
 
 
 def _per_row(value, B: int, Qb: int, dtype: torch.dtype, dev: torch.device):
@@ -250,18 +280,9 @@ class FovealIndexer(nn.Module):
             raise ValueError(f"Element length {n_elements} must be divisible by block_size={self.block_size}")
         k_lin = self.k_proj(x)
         v_lin = self.v_proj(x)
-        dev = _lib.require_gpu(k_lin, v_lin, what=what)
-        _forward_only(what, k_lin, v_lin)
-        code = _lib.dtype_code(k_lin.dtype, what)
-        k_lin, v_lin = k_lin.contiguous(), v_lin.contiguous()
-        nb = n_elements // self.block_size
-        k_blocks = torch.empty((batch, nb, self.index_dim), dtype=k_lin.dtype, device=dev)
-        v_blocks = torch.empty_like(k_blocks)
-        st = _lib.lib().fsi_index_pool_kv(k_lin.data_ptr(), v_lin.data_ptr(), code, batch, n_elements,
-                                          self.index_dim, self.block_size, k_blocks.data_ptr(), v_blocks.data_ptr(),
-                                          _lib.stream_handle(dev))
-        _lib.check(st, what)
-        return k_blocks, v_blocks
+        _lib.require_gpu(k_lin, v_lin, what=what)
+        _lib.dtype_code(k_lin.dtype, what)
+        return _PoolKVFn.apply(k_lin.contiguous(), v_lin.contiguous(), self.block_size)
 
     def compute_block_scores(self, q_blocks: Tensor, k_blocks: Tensor) -> Tensor:
         """Cosine / sqrt(index_dim) block scores (core.py:254-266)."""
@@ -290,20 +311,16 @@ class FovealIndexer(nn.Module):
         """Soft 16-D read over the valid blocks, projected to hidden_size and
         repeated over each block's elements (core.py:288-312)."""
         what = "additive_stream"
-        dev = _lib.require_gpu(block_scores, v_blocks, what=what)
-        _forward_only(what, block_scores, v_blocks)
+        _lib.require_gpu(block_scores, v_blocks, what=what)
         if block_scores.dtype != v_blocks.dtype:
             raise TypeError(f"{what}: scores {block_scores.dtype} and values {v_blocks.dtype} differ")
-        code = _lib.dtype_code(v_blocks.dtype, what)
+        _lib.dtype_code(v_blocks.dtype, what)
         s = _as_3d(block_scores, what)
         v = v_blocks.contiguous()
         B, Qb, Nb = s.shape
         if tuple(v.shape) != (B, Nb, self.index_dim):
             raise ValueError(f"{what}: values {tuple(v.shape)} != {(B, Nb, self.index_dim)}")
-        context = torch.empty((B, Qb, self.index_dim), dtype=v.dtype, device=dev)
-        st = _lib.lib().fsi_additive_context(s.data_ptr(), v.data_ptr(), code, B, Qb, Nb, self.index_dim,
-                                             int(bool(self.causal)), context.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
+        context = _AdditiveContextFn.apply(s, v, self.causal)
         out_blocks = self.out_proj(context)
         return out_blocks.repeat_interleave(self.block_size, dim=1)
 
@@ -337,37 +354,152 @@ class FovealIndexer(nn.Module):
         return student_scores.sum() * 0.0
 
 
+class _IndexRmsNormFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, xc: Tensor, what: str) -> Tensor:
+        dev = xc.device
+        code = _lib.dtype_code(xc.dtype, what)
+        d = xc.shape[-1]
+        out = torch.empty_like(xc)
+        st = _lib.lib().fsi_index_rms_norm(xc.data_ptr(), code, xc.numel() // max(d, 1), d, out.data_ptr(),
+                                           _lib.stream_handle(dev))
+        _lib.check(st, what)
+        ctx.save_for_backward(xc)
+        ctx.what = what
+        return out
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        (xc,) = ctx.saved_tensors
+        what = ctx.what + " backward"
+        dev = _lib.require_gpu(g, xc, what=what)
+        gc = g.to(xc.dtype).contiguous()
+        dx = torch.empty_like(xc)
+        d = xc.shape[-1]
+        st = _lib.lib().fsi_index_rms_norm_bwd(xc.data_ptr(), gc.data_ptr(), _lib.dtype_code(xc.dtype, what),
+                                               xc.numel() // max(d, 1), d, dx.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        return dx, None
+
+
 def index_rms_norm(x: Tensor, what: str = "index_rms_norm") -> Tensor:
-    """F.rms_norm over the last (16-wide) dimension, eps = FLT_EPSILON."""
-    dev = _lib.require_gpu(x, what=what)
-    _forward_only(what, x)
-    code = _lib.dtype_code(x.dtype, what)
-    xc = x.contiguous()
-    d = xc.shape[-1]
-    out = torch.empty_like(xc)
-    st = _lib.lib().fsi_index_rms_norm(xc.data_ptr(), code, xc.numel() // max(d, 1), d, out.data_ptr(),
-                                       _lib.stream_handle(dev))
-    _lib.check(st, what)
-    return out
+    """F.rms_norm over the last (16-wide) dimension, eps = FLT_EPSILON; differentiable."""
+    _lib.require_gpu(x, what=what)
+    _lib.dtype_code(x.dtype, what)
+    return _IndexRmsNormFn.apply(x.contiguous(), what)
+
+
+class _PoolKVFn(torch.autograd.Function):
+    """fsi_index_pool_kv with fsi_index_pool_kv_bwd as its gradient (B, N, 16) inputs."""
+
+    @staticmethod
+    def forward(ctx, k_lin: Tensor, v_lin: Tensor, block_size: int):
+        what = "compute_kv_blocks_16d"
+        dev = k_lin.device
+        code = _lib.dtype_code(k_lin.dtype, what)
+        batch, n_elements, d = k_lin.shape
+        nb = n_elements // block_size
+        k_blocks = torch.empty((batch, nb, d), dtype=k_lin.dtype, device=dev)
+        v_blocks = torch.empty_like(k_blocks)
+        st = _lib.lib().fsi_index_pool_kv(k_lin.data_ptr(), v_lin.data_ptr(), code, batch, n_elements, d, block_size,
+                                          k_blocks.data_ptr(), v_blocks.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        ctx.save_for_backward(k_lin)
+        ctx.block_size = block_size
+        return k_blocks, v_blocks
+
+    @staticmethod
+    def backward(ctx, gk: Optional[Tensor], gv: Optional[Tensor]):
+        what = "compute_kv_blocks_16d backward"
+        (k_lin,) = ctx.saved_tensors
+        dev = _lib.require_gpu(k_lin, what=what)
+        batch, n_elements, d = k_lin.shape
+        nb = n_elements // ctx.block_size
+        zeros = lambda: torch.zeros((batch, nb, d), dtype=k_lin.dtype, device=dev)  # noqa: E731
+        gk = zeros() if gk is None else gk.to(k_lin.dtype).contiguous()
+        gv = zeros() if gv is None else gv.to(k_lin.dtype).contiguous()
+        dk, dv = torch.empty_like(k_lin), torch.empty_like(k_lin)
+        st = _lib.lib().fsi_index_pool_kv_bwd(k_lin.data_ptr(), gk.data_ptr(), gv.data_ptr(),
+                                              _lib.dtype_code(k_lin.dtype, what), batch, n_elements, d, ctx.block_size,
+                                              dk.data_ptr(), dv.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        return dk, dv, None
+
+
+class _BlockScoresFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q: Tensor, k: Tensor) -> Tensor:
+        what = "compute_block_scores"
+        dev = q.device
+        B, Q, d = q.shape
+        N = k.shape[1]
+        out = torch.empty((B, Q, N), dtype=q.dtype, device=dev)
+        st = _lib.lib().fsi_block_scores(q.data_ptr(), k.data_ptr(), _lib.dtype_code(q.dtype, what), B, Q, N, d,
+                                         out.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        ctx.save_for_backward(q, k)
+        return out
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        what = "compute_block_scores backward"
+        q, k = ctx.saved_tensors
+        dev = _lib.require_gpu(g, q, k, what=what)
+        gc = g.to(q.dtype).contiguous()
+        B, Q, d = q.shape
+        N = k.shape[1]
+        dq, dk = torch.empty_like(q), torch.empty_like(k)
+        st = _lib.lib().fsi_block_scores_bwd(q.data_ptr(), k.data_ptr(), gc.data_ptr(), _lib.dtype_code(q.dtype, what),
+                                             B, Q, N, d, dq.data_ptr(), dk.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        return dq, dk
+
+
+class _AdditiveContextFn(torch.autograd.Function):
+    """context = masked_softmax(scores, causal ? p < q : all).to(v) @ v (core.py:296-309)."""
+
+    @staticmethod
+    def forward(ctx, s: Tensor, v: Tensor, causal: bool) -> Tensor:
+        what = "additive_stream"
+        dev = s.device
+        B, Qb, Nb = s.shape
+        d = v.shape[-1]
+        context = torch.empty((B, Qb, d), dtype=v.dtype, device=dev)
+        st = _lib.lib().fsi_additive_context(s.data_ptr(), v.data_ptr(), _lib.dtype_code(v.dtype, what), B, Qb, Nb, d,
+                                             int(bool(causal)), context.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        ctx.save_for_backward(s, v)
+        ctx.causal = bool(causal)
+        return context
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        what = "additive_stream backward"
+        s, v = ctx.saved_tensors
+        dev = _lib.require_gpu(g, s, v, what=what)
+        gc = g.to(v.dtype).contiguous()
+        B, Qb, Nb = s.shape
+        d = v.shape[-1]
+        ds, dv = torch.empty_like(s), torch.empty_like(v)
+        lib = _lib.lib()
+        ws = torch.empty(max(1, lib.fsi_additive_context_bwd_workspace_size(B, Qb)), dtype=torch.uint8, device=dev)
+        st = lib.fsi_additive_context_bwd(s.data_ptr(), v.data_ptr(), gc.data_ptr(), _lib.dtype_code(v.dtype, what),
+                                          B, Qb, Nb, d, int(ctx.causal), ds.data_ptr(), dv.data_ptr(), ws.data_ptr(),
+                                          ws.numel(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        return ds, dv, None
 
 
 def block_scores(q_blocks: Tensor, k_blocks: Tensor) -> Tensor:
     """normalize(q) . normalize(k)^T / sqrt(d) with the reference's rounding
-    points (core.py:254-266).  q: (B, Q, 16); k: (B, N, 16)."""
+    points (core.py:254-266); differentiable.  q: (B, Q, 16); k: (B, N, 16)."""
     what = "compute_block_scores"
-    dev = _lib.require_gpu(q_blocks, k_blocks, what=what)
-    _forward_only(what, q_blocks, k_blocks)
+    _lib.require_gpu(q_blocks, k_blocks, what=what)
     if q_blocks.dtype != k_blocks.dtype:
         raise TypeError(f"{what}: q {q_blocks.dtype} and k {k_blocks.dtype} differ")
-    code = _lib.dtype_code(q_blocks.dtype, what)
+    _lib.dtype_code(q_blocks.dtype, what)
     q = q_blocks.contiguous()
     k = k_blocks.contiguous()
     if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
         raise ValueError(f"{what}: q {tuple(q.shape)} and k {tuple(k.shape)} do not match")
-    B, Q, d = q.shape
-    N = k.shape[1]
-    out = torch.empty((B, Q, N), dtype=q.dtype, device=dev)
-    st = _lib.lib().fsi_block_scores(q.data_ptr(), k.data_ptr(), code, B, Q, N, d, out.data_ptr(),
-                                     _lib.stream_handle(dev))
-    _lib.check(st, what)
-    return out
+    return _BlockScoresFn.apply(q, k)

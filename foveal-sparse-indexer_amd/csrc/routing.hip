@@ -867,6 +867,42 @@ __global__ __launch_bounds__(MS_THREADS) void masked_softmax_kernel(const void* 
   }
 }
 
+// Backward of masked_softmax (autograd of core.py:36-43): with p the fp32
+// softmax over the mask, dscores = p * (dp - sum_k p_k dp_k) on masked-in
+// entries and 0 elsewhere (all-masked rows: 0).  p is recomputed from the scores
+// in fp32, as the reference's autograd keeps fp32 intermediates; dscores is
+// rounded once to the scores' dtype.
+template <bool BF16>
+__global__ __launch_bounds__(MS_THREADS) void masked_softmax_bwd_kernel(
+    const void* __restrict__ scores, const void* __restrict__ dprobs, int Q, int N, const uint8_t* __restrict__ mask,
+    int64_t msb, int64_t msq, int64_t msn, void* __restrict__ dscores) {
+  __shared__ float red[MS_THREADS / 64];
+  const int q = blockIdx.x, b = blockIdx.y;
+  const int64_t row = static_cast<int64_t>(b) * Q + q;
+  const uint8_t* mrow = mask + b * msb + q * msq;
+  auto load = [&](const void* p, int j) -> float {
+    return BF16 ? bf16_to_f32(static_cast<const bf16_t*>(p)[row * N + j]) : static_cast<const float*>(p)[row * N + j];
+  };
+  float mx = -INFINITY;
+  for (int j = threadIdx.x; j < N; j += MS_THREADS)
+    if (mrow[j * msn]) mx = fmaxf(mx, load(scores, j));
+  mx = block_reduce(mx, red, true);
+  if (!isfinite(mx)) mx = 0.0f;
+  float z = 0.f;
+  for (int j = threadIdx.x; j < N; j += MS_THREADS)
+    if (mrow[j * msn]) z += expf(load(scores, j) - mx);
+  z = fmaxf(block_reduce(z, red, false), 1e-20f);
+  float dot = 0.f;
+  for (int j = threadIdx.x; j < N; j += MS_THREADS)
+    if (mrow[j * msn]) dot = fmaf(expf(load(scores, j) - mx) / z, load(dprobs, j), dot);
+  dot = block_reduce(dot, red, false);
+  for (int j = threadIdx.x; j < N; j += MS_THREADS) {
+    const float g = mrow[j * msn] ? expf(load(scores, j) - mx) / z * (load(dprobs, j) - dot) : 0.0f;
+    if (BF16) static_cast<bf16_t*>(dscores)[row * N + j] = f32_to_bf16(g);
+    else static_cast<float*>(dscores)[row * N + j] = g;
+  }
+}
+
 int pick_pl(int64_t n) {
   const int pl = static_cast<int>((n + 63) / 64);
   if (pl <= 4) return 4;
@@ -1049,6 +1085,29 @@ FSI_API int fsi_masked_softmax(const void* scores, int dtype, int64_t B, int64_t
     masked_softmax_kernel<false><<<grid, MS_THREADS, 0, st>>>(scores, (int)Q, (int)N, mask, mask_stride_b,
                                                               mask_stride_q, mask_stride_n, out);
   FSI_HIP_LAUNCH_CHECK("masked_softmax");
+  return FSI_OK;
+}
+
+FSI_API int fsi_masked_softmax_bwd(const void* scores, const void* dprobs, int dtype, int64_t B, int64_t Q, int64_t N,
+                                   const uint8_t* mask, int64_t mask_stride_b, int64_t mask_stride_q,
+                                   int64_t mask_stride_n, void* dscores, void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "masked_softmax_bwd: dtype %d",
+                dtype);
+  FSI_CHECK_ARG(B >= 0 && Q >= 0 && N >= 0, FSI_ERR_SHAPE, "masked_softmax_bwd: negative size");
+  if (B == 0 || Q == 0 || N == 0) return FSI_OK;
+  FSI_CHECK_ARG(B <= 65535 && Q <= (int64_t)0x7fffffff && N <= (int64_t)0x7fffffff, FSI_ERR_SHAPE,
+                "masked_softmax_bwd: grid too large");
+  FSI_CHECK_ARG(scores && dprobs && mask && dscores, FSI_ERR_INVALID_ARG, "masked_softmax_bwd: null pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(Q), static_cast<unsigned>(B));
+  if (dtype == FSI_DTYPE_BF16)
+    masked_softmax_bwd_kernel<true><<<grid, MS_THREADS, 0, st>>>(scores, dprobs, (int)Q, (int)N, mask, mask_stride_b,
+                                                                 mask_stride_q, mask_stride_n, dscores);
+  else
+    masked_softmax_bwd_kernel<false><<<grid, MS_THREADS, 0, st>>>(scores, dprobs, (int)Q, (int)N, mask, mask_stride_b,
+                                                                  mask_stride_q, mask_stride_n, dscores);
+  FSI_HIP_LAUNCH_CHECK("masked_softmax_bwd");
   return FSI_OK;
 }
 

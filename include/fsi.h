@@ -190,6 +190,13 @@ FSI_API int fsi_masked_softmax(const void* scores, int dtype, int64_t B, int64_t
                                int64_t mask_stride_b, int64_t mask_stride_q, int64_t mask_stride_n, void* out,
                                void* stream);
 
+/* Backward of masked_softmax (autograd of core.py:36-43): dscores = p (dp - sum p dp)
+ * on masked-in entries, 0 elsewhere, with p recomputed in fp32 from scores.
+ * scores/dprobs/dscores: contiguous (B, Q, N); mask as in fsi_masked_softmax. */
+FSI_API int fsi_masked_softmax_bwd(const void* scores, const void* dprobs, int dtype, int64_t B, int64_t Q, int64_t N,
+                                   const uint8_t* mask, int64_t mask_stride_b, int64_t mask_stride_q,
+                                   int64_t mask_stride_n, void* dscores, void* stream);
+
 /* select_blocks on materialised scores
  * (foveal_indexer/core.py:46-160, via FovealIndexer.route core.py:268-286).
  * scores: (B, Qb, Nb) contiguous fp32 or bf16 (upcast to fp32 first).
@@ -272,6 +279,27 @@ FSI_API int fsi_block_scores(const void* q, const void* k, int dtype, int64_t B,
  * rounded to dtype.  scores: (B, Q, N); v_blocks: (B, N, 16); context: (B, Q, 16). */
 FSI_API int fsi_additive_context(const void* scores, const void* v_blocks, int dtype, int64_t B, int64_t Q,
                                  int64_t N, int64_t index_dim, int causal, void* context, void* stream);
+
+/* Backward passes of the four entry points above: the autograd of
+ * compute_query_16d, compute_kv_blocks_16d, compute_block_scores and
+ * additive_stream (core.py:214-310, exercised by tests/test_indexer.py:63-101).
+ * Gradients are computed in fp32 from the forward inputs (intermediates
+ * recomputed) and rounded to dtype where the reference's graph holds a tensor
+ * of that dtype.  Shapes as in the forward; gradient tensors have the shapes
+ * of the tensors they belong to. */
+FSI_API int fsi_index_rms_norm_bwd(const void* x, const void* dy, int dtype, int64_t M, int64_t index_dim, void* dx,
+                                   void* stream);
+FSI_API int fsi_index_pool_kv_bwd(const void* k_lin, const void* dk_blocks, const void* dv_blocks, int dtype, int64_t B,
+                                  int64_t N, int64_t index_dim, int64_t block_size, void* dk_lin, void* dv_lin,
+                                  void* stream);
+FSI_API int fsi_block_scores_bwd(const void* q, const void* k, const void* dscores, int dtype, int64_t B, int64_t Q,
+                                 int64_t N, int64_t index_dim, void* dq, void* dk, void* stream);
+/* Workspace: per-row softmax statistics, written before they are read (need
+ * not be zeroed), 8-byte aligned. */
+FSI_API size_t fsi_additive_context_bwd_workspace_size(int64_t B, int64_t Q);
+FSI_API int fsi_additive_context_bwd(const void* scores, const void* v_blocks, const void* dcontext, int dtype,
+                                     int64_t B, int64_t Q, int64_t N, int64_t index_dim, int causal, void* dscores,
+                                     void* dv_blocks, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------- *
  * Foveal paged-KV decode attention (foveal_indexer/attention.py:284-367).

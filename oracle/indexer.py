@@ -7,6 +7,9 @@ Restates with torch CPU ops, in the reference's order and dtypes:
   * additive_stream context    foveal_indexer/core.py:288-310 (up to out_proj)
 The projections themselves (nn.Linear) are inputs here: the HIP path runs them
 as library GEMMs and these functions start from their outputs.
+Backward passes: torch autograd of these functions, as in the reference's
+training (tests/test_indexer.py:63-101); with fp64 inputs and acc=float64 they
+are exact fp64 gradients, pinned by finite differences (gradcheck).
 """
 from __future__ import annotations
 
@@ -24,30 +27,30 @@ def rms_norm16(x_lin: Tensor) -> Tensor:
     return F.rms_norm(x_lin, (x_lin.shape[-1],))
 
 
-def pool_kv(k_lin: Tensor, v_lin: Tensor, block_size: int):
+def pool_kv(k_lin: Tensor, v_lin: Tensor, block_size: int, acc: torch.dtype = torch.float32):
     """(k_blocks, v_blocks) from the k/v projections (core.py:241-250)."""
     B, N, d = k_lin.shape
     nb = N // block_size
     k_elem = F.rms_norm(k_lin, (d,))
     k_blocks = k_elem.view(B, nb, block_size, d).mean(dim=2)
     v_blocks = v_lin.view(B, nb, block_size, d).mean(dim=2)
-    k_blocks = F.normalize(k_blocks.float(), dim=-1).to(k_lin.dtype)
+    k_blocks = F.normalize(k_blocks.to(acc), dim=-1).to(k_lin.dtype)
     return k_blocks, v_blocks
 
 
-def block_scores(q_blocks: Tensor, k_blocks: Tensor) -> Tensor:
+def block_scores(q_blocks: Tensor, k_blocks: Tensor, acc: torch.dtype = torch.float32) -> Tensor:
     """cosine / sqrt(d) with the operands cast back to their dtype (core.py:263-265)."""
-    qn = F.normalize(q_blocks.float(), dim=-1).to(q_blocks.dtype)
-    kn = F.normalize(k_blocks.float(), dim=-1).to(k_blocks.dtype)
+    qn = F.normalize(q_blocks.to(acc), dim=-1).to(q_blocks.dtype)
+    kn = F.normalize(k_blocks.to(acc), dim=-1).to(k_blocks.dtype)
     return torch.bmm(qn, kn.transpose(-2, -1).contiguous()) / math.sqrt(q_blocks.shape[-1])
 
 
-def additive_context(block_scores: Tensor, v_blocks: Tensor, causal: bool) -> Tensor:
+def additive_context(block_scores: Tensor, v_blocks: Tensor, causal: bool, acc: torch.dtype = torch.float32) -> Tensor:
     """masked_softmax(scores, valid).to(v dtype) @ v_blocks (core.py:296-310)."""
     B, Qb, Nb = block_scores.shape
     if causal:
         valid = torch.arange(Nb).view(1, Nb) < torch.arange(Qb).view(Qb, 1)
     else:
         valid = torch.ones(Qb, Nb, dtype=torch.bool)
-    probs = masked_probs(block_scores, valid[None].expand(B, -1, -1)).to(v_blocks.dtype)
+    probs = masked_probs(block_scores, valid[None].expand(B, -1, -1), acc).to(v_blocks.dtype)
     return torch.bmm(probs, v_blocks)

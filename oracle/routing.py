@@ -22,10 +22,11 @@ import torch.nn.functional as F
 from torch import Tensor
 
 
-def masked_probs(scores: Tensor, mask: Tensor) -> Tensor:
+def masked_probs(scores: Tensor, mask: Tensor, acc: torch.dtype = torch.float32) -> Tensor:
     """fp32 softmax over `mask`, masked entries exactly 0, all-masked rows 0,
-    returned in the scores' dtype (core.py:36-43)."""
-    s = scores.float().masked_fill(~mask, float("-inf"))
+    returned in the scores' dtype (core.py:36-43).  `acc` = float64 gives the
+    exact (fp64) value and gradient for fp64 scores."""
+    s = scores.to(acc).masked_fill(~mask, float("-inf"))
     mx = s.amax(dim=-1, keepdim=True)
     mx = torch.where(torch.isfinite(mx), mx, torch.zeros_like(mx))
     e = torch.exp(s - mx) * mask

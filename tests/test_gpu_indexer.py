@@ -119,6 +119,9 @@ def test_foveal_indexer_module(fsi, dev):
 
 
 def test_forward_only_guard(fsi, dev):
-    m = fsi.FovealIndexer(hidden_size=32, block_size=8).to(dev)
+    """Ops without a backward refuse to record autograd (the indexer
+    representations are differentiable: test_gpu_indexer_backward)."""
+    w = torch.randn(128, 64, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    x = torch.randn(4, 64, device=dev, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError, match="inference-only"):
-        m.compute_query_16d(torch.randn(1, 8, 32, device=dev))
+        fsi.block_sparse_linear(x, w, None, torch.tensor([0], dtype=torch.int32, device=dev), 64)

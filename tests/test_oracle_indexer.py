@@ -2,6 +2,7 @@
 forms (CPU only)."""
 import math
 
+import pytest
 import torch
 
 from oracle import indexer as IX
@@ -67,3 +68,28 @@ def test_additive_context_brute_force():
     full = IX.additive_context(s, v, causal=False)
     w = torch.softmax(s[0].double(), -1)
     assert torch.allclose(full[0].double(), w @ v[0].double(), atol=1e-6)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_indexer_gradients_match_finite_differences(causal):
+    """The backward oracle is autograd of the fp64 restatement; gradcheck pins
+    it against central differences for every differentiable input."""
+    from oracle import indexer as IX
+    from oracle import routing as R
+
+    g = torch.Generator().manual_seed(3)
+    f64 = dict(dtype=torch.float64)
+    x = torch.randn(2, 5, 16, generator=g, **f64).requires_grad_()
+    assert torch.autograd.gradcheck(lambda t: IX.rms_norm16(t), (x,))
+    k = torch.randn(2, 12, 16, generator=g, **f64).requires_grad_()
+    v = torch.randn(2, 12, 16, generator=g, **f64).requires_grad_()
+    assert torch.autograd.gradcheck(lambda a, b: IX.pool_kv(a, b, 4, torch.float64), (k, v))
+    q = torch.randn(2, 4, 16, generator=g, **f64).requires_grad_()
+    kb = torch.randn(2, 3, 16, generator=g, **f64).requires_grad_()
+    assert torch.autograd.gradcheck(lambda a, b: IX.block_scores(a, b, torch.float64), (q, kb))
+    s = torch.randn(2, 4, 3, generator=g, **f64).requires_grad_()
+    vb = torch.randn(2, 3, 16, generator=g, **f64).requires_grad_()
+    assert torch.autograd.gradcheck(lambda a, b: IX.additive_context(a, b, causal, torch.float64), (s, vb))
+    mask = torch.rand(2, 4, 3, generator=g) > 0.4
+    mask[0, 1] = False  # an all-masked row
+    assert torch.autograd.gradcheck(lambda a: R.masked_probs(a, mask, torch.float64), (s,))

@@ -18,6 +18,7 @@ Other workloads (one JSON line each, for the profiles; not the headline line):
   --workload decode_attn  C4: foveal paged-KV decode attention, 32 sequences x 131072 context
   --workload prefill_attn block-sparse prefill attention, 16384 tokens, Llama-3-8B attention heads
   --workload block_sparse C5: 2-D tile-sparse matmul, 4096 x 8192 by 8192 x 8192, 128 x 128 tiles
+  --workload teacher_targets dense block-energy distillation targets, Llama-3-8B MLP, 4096 tokens
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-prefill] [--workload W]
 """
@@ -414,6 +415,55 @@ def bench_block_sparse(fsi, args, dev):
     return res
 
 
+def bench_teacher_targets(fsi, args, dev):
+    """Dense block-energy teacher targets (compute_teacher_dense_block_targets) for
+    one Llama-3-8B MLP over 4096 tokens: the fused gate/up GEMM with the |act|
+    block-sum epilogue plus the column-norm and softmax kernels."""
+    M, D, I, BS, T = 4096, D_MODEL, N_PARAM, 64, 1.0
+    g = torch.Generator(device=dev).manual_seed(0)
+    h = torch.randn(M, D, device=dev, generator=g).bfloat16()
+    gw = (torch.randn(I, D, device=dev, generator=g) * 0.02).bfloat16()
+    uw = (torch.randn(I, D, device=dev, generator=g) * 0.02).bfloat16()
+    dw = (torch.randn(D, I, device=dev, generator=g) * 0.02).bfloat16()
+    out = {}
+
+    def step(i):
+        out["p"] = fsi.dense_block_targets(h, gw, uw, dw, BS, T)
+
+    t, _ = time_graph(step, args.steps, args.warmup, dev)
+    per = t / args.steps
+    flops = 2 * M * D * 2 * I
+    tfs = flops / per / 1e12
+    res = _result("dense teacher block targets tok/s (Llama-3-8B MLP, 4096 tokens)", round(M / per, 1), "tok/s",
+                  args.steps, args.warmup, round(per * 1e3, 6), "bf16",
+                  "synthetic (seeded N(0,1) hidden states, N(0,0.02) gate/up/down weights)",
+                  {"workload": "compute_teacher_dense_block_targets per layer: h (4096, 4096), gate/up (14336, 4096), "
+                               "down (4096, 14336), block 64 (224 blocks), T = 1"})
+    res["roofline"] = {"bound": "mfma", "achieved": round(tfs, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                       "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                       "kernel": "bsgemm_dma_kernel<N_DUAL, K_DENSE, EPI_ENERGY> (+ column_sumsq_kernel, "
+                                 "column_norms_kernel, block_mean_kernel, block_softmax_kernel: 5 launches)",
+                       "flops_per_launch": flops}
+    if not args.no_cpu_baseline:
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        from oracle import pattention as OP
+
+        n = 64
+        hc, gc, uc, dc = h[:n].cpu(), gw.cpu(), uw.cpu(), dw.cpu()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            OP.dense_block_targets(hc, gc, uc, dc, BS, T)
+            ts.append(time.perf_counter() - t0)
+        med = sorted(ts)[1]
+        res["cpu_baseline"] = {"value": round(n / med, 1), "unit": "tok/s", "cores": cores, "kind": "port",
+                               "sample": f"the reference's torch ops (bf16, train_foveal_pattention_speedrun.py:"
+                                         f"176-185) on the host for 64 of the 4096 tokens, median of 3, "
+                                         f"{med * 1e3:.1f} ms"}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -424,7 +474,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="pattention",
-                    choices=["pattention", "routing", "decode_attn", "prefill_attn", "block_sparse"])
+                    choices=["pattention", "routing", "decode_attn", "prefill_attn", "block_sparse",
+                             "teacher_targets"])
     ap.add_argument("--eager", action="store_true", help="no graph capture (for per-dispatch counter runs)")
     ap.add_argument("--no-pack", action="store_true",
                     help="decode from the parameters in place (4-kernel split-K path) instead of packed weights")
@@ -445,7 +496,7 @@ def main():
     torch.manual_seed(0)
     if args.workload != "pattention":
         fn = {"routing": bench_routing, "decode_attn": bench_decode_attn, "prefill_attn": bench_prefill_attn,
-              "block_sparse": bench_block_sparse}[args.workload]
+              "block_sparse": bench_block_sparse, "teacher_targets": bench_teacher_targets}[args.workload]
         with torch.no_grad():
             print(json.dumps(fn(fsi, args, dev)), flush=True)
         return

@@ -12,6 +12,7 @@ from .pattention import (
     TritonSwiGLUPattentionMLP,
     convert_llm_mlp_to_pattention,
     PackedPattentionWeights,
+    dense_block_targets,
     fused_swiglu,
     pack_pattention_weights,
     pattention_decode_packed,
@@ -45,6 +46,7 @@ from .block_matmul import (
 )
 from .foveal_pattention import (
     FovealPattentionMLP,
+    compute_teacher_dense_block_targets,
     mlp_pooled_route,
     sparsify_model_with_foveal_pattention,
 )
@@ -78,6 +80,8 @@ __all__ = [
     "pattention_decode_packed",
     "pack_pattention_weights",
     "PackedPattentionWeights",
+    "dense_block_targets",
+    "compute_teacher_dense_block_targets",
     "TritonSwiGLUPattentionMLP",
     "convert_llm_mlp_to_pattention",
     "HAS_HIP",

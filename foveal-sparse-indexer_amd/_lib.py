@@ -99,6 +99,12 @@ SIGNATURES: dict[str, tuple] = {
     "fsi_additive_context": (
         _c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_ptr],
     ),
+    "fsi_dense_block_targets_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "fsi_dense_block_targets": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
+         _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr],
+    ),
     "fsi_index_rms_norm_bwd": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_ptr]),
     "fsi_index_pool_kv_bwd": (
         _c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr],

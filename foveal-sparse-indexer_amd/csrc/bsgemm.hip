@@ -42,7 +42,7 @@ constexpr int KTAB_MAX = 2048;
 
 enum NMode { N_DIRECT = 0, N_GATHER = 1, N_DUAL = 2 };
 enum KMode { K_DENSE = 0, K_GATHER_B = 1, K_LIST = 2 };
-enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1 };
+enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_ENERGY = 2 };
 
 struct GemmArgs {
   const bf16_t* A;  // [M, lda]
@@ -50,6 +50,7 @@ struct GemmArgs {
   const bf16_t* B1; // second B (up projection) for N_DUAL
   const bf16_t* bias;
   bf16_t* C;
+  float* E;         // EPI_ENERGY: [M, N / 32] per-row sums of |act| over 32-channel groups (row stride ldc)
   int64_t lda, ldb, ldc;
   int M, N, K;                 // N: logical columns of the gathered problem, K: reduction length
   const int32_t* blocks;       // N_GATHER / N_DUAL: active block ids; K_GATHER_B: active blocks along K
@@ -70,6 +71,22 @@ struct GemmArgs {
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+// Sum over the 16 lanes that hold one row of a 16 x 16 MFMA result (lanes 16 q .. 16 q + 15).
+__device__ __forceinline__ float sum16(float v) {
+  v += __shfl_xor(v, 8, 16);
+  v += __shfl_xor(v, 4, 16);
+  v += __shfl_xor(v, 2, 16);
+  v += __shfl_xor(v, 1, 16);
+  return v;
+}
+
+// |act(g, u)| of one gate/up accumulator pair, rounded as the stored activation
+// would be unless the rounding mode is fp32 (EPI_ENERGY).
+__device__ __forceinline__ float energy_term(float gv, float uv, int rounding) {
+  const float h = pattention_act<ACT_SWIGLU>(gv, uv, rounding);
+  return fabsf(rounding == FSI_ROUND_FP32 ? h : round_bf16(h));
+}
 
 // ktab[i] = first B column of active K block i, or -1 when its id is out of range.
 __device__ __forceinline__ void fill_ktab(const GemmArgs& g, int32_t* ktab, int nthreads) {
@@ -296,6 +313,22 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
           if (g.act == ACT_SWIGLU) h = pattention_act<ACT_SWIGLU>(gv, uv, g.rounding);
           else h = 0.f;
           g.C[m * g.ldc + ch] = f32_to_bf16(h);
+        }
+    }
+  } else if (EPI == EPI_ENERGY) {
+    // wave wn holds the tile's channels 32 wn .. 32 wn + 31 (gate fragments f = 0, 1)
+    const int grp_ch = ccol[0] + 32 * wn;
+    if (grp_ch < g.N) {
+      const bool live = bval[wn] && bval[2 + wn];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float e = 0.f;
+          if (live) e = energy_term(acc[i][0][j], acc[i][2][j], g.rounding) + energy_term(acc[i][1][j], acc[i][3][j], g.rounding);
+          e = sum16(e);
+          const int m = crow0 + 16 * i + j;
+          if (frow == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
         }
     }
   } else {
@@ -850,6 +883,22 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
           g.C[static_cast<int64_t>(m) * g.ldc + ch] = f32_to_bf16(h);
         }
     }
+  } else if (EPI == EPI_ENERGY) {
+    // wave wn holds the tile's channels 32 wn .. 32 wn + 31 (gate fragments f = 0, 1)
+    const int grp_ch = ccol[0] + 32 * wn;
+    if (grp_ch < g.N) {
+      const bool live = bval[wn] && bval[4 + wn];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float e = 0.f;
+          if (live) e = energy_term(acc[i][0][j], acc[i][2][j], g.rounding) + energy_term(acc[i][1][j], acc[i][3][j], g.rounding);
+          e = sum16(e);
+          const int m = crow0 + 16 * i + j;
+          if (frow == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
+        }
+    }
   } else {
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
@@ -997,9 +1046,11 @@ hipError_t launch_tiled(GemmArgs& a, bool big, hipStream_t st) {
       return hipGetLastError();
     }
   }
-  if (big) {
-    bsgemm_big_kernel<NM, KM, EPI><<<grid, BT, 0, st>>>(a);
-    return hipGetLastError();
+  if constexpr (EPI != EPI_ENERGY) {
+    if (big) {
+      bsgemm_big_kernel<NM, KM, EPI><<<grid, BT, 0, st>>>(a);
+      return hipGetLastError();
+    }
   }
   return launch<NM, KM, EPI>(a, grid, st);
 }
@@ -1032,6 +1083,33 @@ int gateup_swiglu(const bf16_t* x, int64_t ldx, const bf16_t* kg, const bf16_t* 
   a.rounding = rounding;
   a.err = err;
   return launch_tiled<N_DUAL, K_DENSE, EPI_SWIGLU>(a, M >= BIG_MIN_M, st) == hipSuccess ? 0 : -1;
+}
+
+// E[M, N / 32] = per-row sums over 32-channel groups of |act(x K_gate^T, x K_up^T)| for all N
+// channels (dense; N % 32 == 0).  The 256 x 256 direct-to-LDS kernel needs K % 32 == 0;
+// otherwise the 128 x 128 kernel runs.
+int gateup_energy(const bf16_t* x, int64_t ldx, const bf16_t* kg, const bf16_t* ku, int64_t ldk, int N, int M, int K,
+                  int rounding, float* E, int64_t lde, int* err, hipStream_t st) {
+  GemmArgs a{};
+  a.A = x;
+  a.B0 = kg;
+  a.B1 = ku;
+  a.E = E;
+  a.lda = ldx;
+  a.ldb = ldk;
+  a.ldc = lde;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.blocks = nullptr;
+  a.n_blocks = N / SUB;
+  a.block = SUB;
+  a.n_rows_total = N;
+  a.act = ACT_SWIGLU;
+  a.rounding = rounding;
+  a.err = err;
+  const bool big = M >= BIG_MIN_M && K % DK == 0;
+  return launch_tiled<N_DUAL, K_DENSE, EPI_ENERGY>(a, big, st) == hipSuccess ? 0 : -1;
 }
 
 // out[M, D] = H[M, 64 n_active] W_down[:, S]^T with W_down [D, N_p] (row stride ldw)

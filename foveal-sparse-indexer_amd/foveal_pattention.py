@@ -25,6 +25,7 @@ from torch import Tensor, nn
 from . import _lib
 from .pattention import (
     PackedPattentionWeights,
+    dense_block_targets,
     _weights_key,
     pack_pattention_weights,
     packed_decode_supported,
@@ -294,3 +295,30 @@ def sparsify_model_with_foveal_pattention(
     if torch.cuda.is_available():
         torch.cuda.empty_cache()
     return model
+
+
+def compute_teacher_dense_block_targets(
+    teacher: nn.Module,
+    b_ids: Tensor,
+    target_layers: list,
+    block_size: int = 64,
+    temperature: float = 1.0,
+) -> Tuple[Tensor, Tensor, List[Tensor]]:
+    """Teacher representations and dense block-energy targets for KL
+    distillation (archive/hy_mt2/llm_pattention/train_foveal_pattention_speedrun.py:154-189):
+    one no-grad teacher forward with hidden states, then for every target
+    layer the block targets of its MLP input (post_attention_layernorm of the
+    layer's input hidden state) on the fused HIP kernel.  Returns
+    (last hidden state, hidden state 16, [P_target per layer]) as the reference."""
+    with torch.no_grad():
+        t_out = teacher.model(b_ids, output_hidden_states=True)
+        t_rep = t_out.last_hidden_state
+        t_mid = t_out.hidden_states[16]
+        targets = []
+        for l_idx in target_layers:
+            layer = teacher.model.layers[l_idx]
+            mlp = layer.mlp
+            norm_h = layer.post_attention_layernorm(t_out.hidden_states[l_idx])
+            targets.append(dense_block_targets(norm_h, mlp.gate_proj.weight, mlp.up_proj.weight,
+                                               mlp.down_proj.weight, block_size, temperature))
+    return t_rep, t_mid, targets

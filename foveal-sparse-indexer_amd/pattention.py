@@ -301,6 +301,61 @@ def fused_swiglu(g: Tensor, u: Tensor, rounding: str = "fused") -> Tensor:
     return _swiglu_launch(g, u, rounding)
 
 
+def _aligned_rows(t: Tensor) -> Tensor:
+    """Contiguous rows whose start is 16-byte aligned (the GEMM's direct loads)."""
+    t = _rows_contig(t)
+    if t.data_ptr() % 16 or t.stride(0) % 8:
+        t = t.contiguous()
+        if t.data_ptr() % 16:
+            t = t.clone()
+    return t
+
+
+def dense_block_targets(norm_h: Tensor, gate_w: Tensor, up_w: Tensor, down_w: Tensor, block_size: int = 64,
+                        temperature: float = 1.0) -> Tensor:
+    """Block-energy distillation targets of a dense SwiGLU MLP
+    (archive/hy_mt2/llm_pattention/train_foveal_pattention_speedrun.py:176-185):
+    act = silu(h W_gate^T) * (h W_up^T) over all channels, block energy =
+    mean over the block of |act| times the block mean of W_down's column norms,
+    P = softmax(energy / temperature) in fp32.
+
+    norm_h: (..., D) bf16 (the MLP input after post_attention_layernorm);
+    gate_w, up_w: (I, D) bf16; down_w: (D, I) bf16 (nn.Linear layouts).
+    Returns (..., I // block_size) float32.  One fused GEMM whose epilogue
+    reduces |act| in registers: the (tokens, I) activation is never stored.
+    """
+    what = "dense_block_targets"
+    dev = _lib.require_gpu(norm_h, gate_w, up_w, down_w, what=what)
+    for name, t in (("norm_h", norm_h), ("gate_w", gate_w), ("up_w", up_w), ("down_w", down_w)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{what}: {name} must be bfloat16, got {t.dtype}")
+    D = norm_h.shape[-1]
+    I = gate_w.shape[0]
+    if gate_w.shape != (I, D) or up_w.shape != (I, D) or down_w.shape != (D, I):
+        raise ValueError(f"{what}: gate {tuple(gate_w.shape)}, up {tuple(up_w.shape)}, down {tuple(down_w.shape)} "
+                         f"do not match hidden size {D}")
+    if block_size < 32 or block_size % 32 or I % block_size:
+        raise ValueError(f"{what}: block_size {block_size} must be a multiple of 32 dividing {I}")
+    lead = norm_h.shape[:-1]
+    h = _aligned_rows(norm_h.reshape(-1, D))
+    gw, uw, dw = _aligned_rows(gate_w), _aligned_rows(up_w), _aligned_rows(down_w)
+    M = h.shape[0]
+    nb = I // block_size
+    out = torch.empty((M, nb), dtype=torch.float32, device=dev)
+    if M == 0:
+        return out.reshape(*lead, nb)
+    if gw.stride(0) != uw.stride(0):
+        uw = uw.contiguous()
+        gw = gw.contiguous()
+    lib = _lib.lib()
+    ws = torch.empty(lib.fsi_dense_block_targets_workspace_size(M, D, I, block_size), dtype=torch.uint8, device=dev)
+    st = lib.fsi_dense_block_targets(h.data_ptr(), h.stride(0), gw.data_ptr(), uw.data_ptr(), gw.stride(0),
+                                     dw.data_ptr(), dw.stride(0), M, D, I, block_size, float(temperature),
+                                     out.data_ptr(), nb, ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return out.reshape(*lead, nb)
+
+
 class TritonSwiGLUPattentionMLP(nn.Module):
     """Drop-in SwiGLU MLP via fused Pattention (pattention_triton.py:314-375)."""
 

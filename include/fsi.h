@@ -280,6 +280,23 @@ FSI_API int fsi_block_scores(const void* q, const void* k, int dtype, int64_t B,
 FSI_API int fsi_additive_context(const void* scores, const void* v_blocks, int dtype, int64_t B, int64_t Q,
                                  int64_t N, int64_t index_dim, int causal, void* context, void* stream);
 
+/* ------------------------------------------------------------------------- *
+ * Dense teacher block targets for KL distillation
+ * (archive/hy_mt2/llm_pattention/train_foveal_pattention_speedrun.py:154-189,
+ * compute_teacher_dense_block_targets): with act = silu(h W_gate^T) * (h W_up^T)
+ * over all I channels (bf16 roundings of eager SwiGLU), dw[b] = block mean of
+ * W_down's column norms, out[m, b] = softmax_b(bf16(bf16(mean_b |act[m]|) * dw[b]) / T).
+ * h: (M, D) bf16 rows (stride ldh); w_gate, w_up: (I, D) bf16 (stride ld_gu);
+ * w_down: (D, I) bf16 (stride ld_down); out: (M, I / block_size) fp32 (stride ldo).
+ * block_size a multiple of 32 dividing I; D % 8 == 0; 16-byte aligned h and
+ * gate/up rows.  Workspace (256-byte aligned, need not be zeroed) from
+ * fsi_dense_block_targets_workspace_size. */
+FSI_API size_t fsi_dense_block_targets_workspace_size(int64_t M, int64_t D, int64_t I, int64_t block_size);
+FSI_API int fsi_dense_block_targets(const void* h, int64_t ldh, const void* w_gate, const void* w_up, int64_t ld_gu,
+                                    const void* w_down, int64_t ld_down, int64_t M, int64_t D, int64_t I,
+                                    int64_t block_size, float temperature, float* out, int64_t ldo, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
 /* Backward passes of the four entry points above: the autograd of
  * compute_query_16d, compute_kv_blocks_16d, compute_block_scores and
  * additive_stream (core.py:214-310, exercised by tests/test_indexer.py:63-101).

@@ -10,6 +10,7 @@ lands at the same points as the reference):
   * _swiglu_fwd_kernel numerics         foveal_indexer/pattention_triton.py:40-47
   * _swiglu_bwd_kernel                  foveal_indexer/pattention_triton.py:49-71 (closed form, fp64)
   * FovealPattentionMLP training forward foveal_indexer/foveal_pattention.py:292-307, 328-342
+  * dense block-energy teacher targets  archive/hy_mt2/llm_pattention/train_foveal_pattention_speedrun.py:176-185
 """
 from __future__ import annotations
 
@@ -148,3 +149,18 @@ def train_forward(m, x: Tensor, active: Tensor | None = None):
     soft = F.softmax(scores / m.temperature, dim=-1)
     add = m.out_proj_16d(torch.matmul(soft, m.block_keys_16d))
     return (out_patt + add).reshape(x.shape), active
+
+
+def dense_block_targets(norm_h: Tensor, gate_w: Tensor, up_w: Tensor, down_w: Tensor, block_size: int,
+                        temperature: float) -> Tensor:
+    """P_target of compute_teacher_dense_block_targets
+    (train_foveal_pattention_speedrun.py:176-185) with torch CPU ops in the
+    inputs' dtype (bf16 models: the same rounding points as the reference)."""
+    g = F.silu(F.linear(norm_h, gate_w))
+    u = F.linear(norm_h, up_w)
+    act = g * u
+    nb = act.shape[-1] // block_size
+    dw_norms = down_w.norm(dim=0).view(nb, block_size).mean(dim=-1)
+    act_blocks = act.abs().view(*act.shape[:-1], nb, block_size).mean(dim=-1)
+    energy = act_blocks * dw_norms
+    return F.softmax(energy.float() / temperature, dim=-1)

@@ -134,3 +134,34 @@ def test_train_forward_closed_form(base, remote, temp):
         mask[b * bs:(b + 1) * bs] = 1
     want = P.dense_swiglu_f64(x, m.k_gate.detach(), m.k_up.detach(), m.v.detach(), mask) + add
     assert torch.allclose(out.detach(), want, rtol=1e-10, atol=1e-10)
+
+
+def test_dense_block_targets_brute_force():
+    """The teacher-target oracle (train_foveal_pattention_speedrun.py:176-185)
+    against explicit loops in fp64: |silu(g) u| block means times the block
+    mean of W_down's column norms, softmax over blocks / T."""
+    import math
+
+    g0 = torch.Generator().manual_seed(11)
+    M, D, I, bs, T = 3, 8, 64, 32, 0.05
+    h = torch.randn(M, D, generator=g0, dtype=torch.float64)
+    gw = torch.randn(I, D, generator=g0, dtype=torch.float64) * 0.3
+    uw = torch.randn(I, D, generator=g0, dtype=torch.float64) * 0.3
+    dw = torch.randn(D, I, generator=g0, dtype=torch.float64)
+    P_ = P.dense_block_targets(h, gw, uw, dw, bs, T)
+    nb = I // bs
+    for m in range(M):
+        e = []
+        for b in range(nb):
+            a = n = 0.0
+            for i in range(b * bs, (b + 1) * bs):
+                gv = sum(h[m, d].item() * gw[i, d].item() for d in range(D))
+                uv = sum(h[m, d].item() * uw[i, d].item() for d in range(D))
+                a += abs(gv / (1 + math.exp(-gv)) * uv)
+                n += math.sqrt(sum(dw[d, i].item() ** 2 for d in range(D)))
+            e.append(a / bs * n / bs / T)
+        mx = max(e)
+        z = sum(math.exp(v - mx) for v in e)
+        want = torch.tensor([math.exp(v - mx) / z for v in e])
+        assert torch.allclose(P_[m].double(), want.double(), rtol=1e-5, atol=1e-7)
+    assert torch.allclose(P_.sum(-1), torch.ones(M), atol=1e-6)

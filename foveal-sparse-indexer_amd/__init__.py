@@ -47,6 +47,7 @@ from .block_matmul import (
 from .foveal_pattention import (
     FovealPattentionMLP,
     compute_teacher_dense_block_targets,
+    load_foveal_pattention_mlps,
     mlp_pooled_route,
     sparsify_model_with_foveal_pattention,
 )
@@ -82,6 +83,7 @@ __all__ = [
     "PackedPattentionWeights",
     "dense_block_targets",
     "compute_teacher_dense_block_targets",
+    "load_foveal_pattention_mlps",
     "TritonSwiGLUPattentionMLP",
     "convert_llm_mlp_to_pattention",
     "HAS_HIP",

@@ -15,8 +15,10 @@ active-block cache and forward signature as the reference
 """
 from __future__ import annotations
 
+import json
 import math
-from typing import Any, Dict, List, Optional, Tuple
+from pathlib import Path
+from typing import Any, Dict, Iterable, List, Optional, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -176,8 +178,64 @@ class FovealPattentionMLP(nn.Module):
             nn.init.zeros_(patt.out_proj_16d.weight)
         return patt
 
-    def calibrate_offline_svd(self, features: Tensor, ridge_lambda: float = 1e-2) -> Dict[str, float]:
-        raise NotImplementedError("offline SVD calibration is outside the MI355X inference path")
+    @torch.no_grad()
+    def _dense_block_mass_f32(self, X: Tensor, chunk: int = 4096) -> Tensor:
+        """E[t, b] = mean_{j in b} |silu(x_t k_gate_j) (x_t k_up_j)| * ||V_b||_F in fp32
+        (foveal_pattention.py:201-213), token chunks bounding the (tokens, I)
+        activation to `chunk` rows."""
+        nb, bs = self.num_blocks, self.block_size
+        kg, ku = self.k_gate.float(), self.k_up.float()
+        v_norm = self.v.float().reshape(nb, bs, -1).norm(dim=(1, 2))
+        out = torch.empty(X.shape[0], nb, dtype=torch.float32, device=X.device)
+        for t0 in range(0, X.shape[0], chunk):
+            xc = X[t0:t0 + chunk]
+            a = F.silu(xc @ kg.t()) * (xc @ ku.t())
+            out[t0:t0 + chunk] = a.abs().reshape(xc.shape[0], nb, bs).mean(dim=-1) * v_norm
+        return out
+
+    @torch.no_grad()
+    def calibrate_offline_svd(self, features: Tensor, ridge_lambda: float = 1e-2) -> Dict[str, Any]:
+        """Offline router calibration (foveal_pattention.py:175-255), in fp32 on the
+        module's device: q_proj_16d = top-16 right singular vectors of the
+        calibration tokens, teacher block energies of the dense SwiGLU, block keys
+        by closed-form ridge regression of the rms-normed 16-D projections onto
+        the teacher softmax, then the calibration top-k set as the active blocks.
+        The SVD, the fp32 products and the solve are library calls (torch.linalg,
+        hipBLASLt): this is a one-time conversion step.  Singular vectors carry an
+        arbitrary sign per component; the router scores do not depend on it."""
+        _lib.require_gpu(self.k_gate, what="calibrate_offline_svd")
+        device = self.k_gate.device
+        orig_dtype = self.k_gate.dtype
+        X = features.to(device=device, dtype=torch.float32).reshape(-1, self.hidden_dim)
+        _, S, Vh = torch.linalg.svd(X, full_matrices=False)
+        if Vh.shape[0] < self.index_dim:
+            pad = torch.randn(self.index_dim - Vh.shape[0], self.hidden_dim, device=device)
+            Vh = torch.cat([Vh, pad], dim=0)
+        V16 = Vh[: self.index_dim, :].T
+        self.q_proj_16d.weight.data.copy_(V16.T.to(dtype=orig_dtype))
+        Z = F.rms_norm(X @ V16, (self.index_dim,))
+        teacher_target = F.softmax(self._dense_block_mass_f32(X) / self.temperature, dim=-1)
+        reg = ridge_lambda * torch.eye(self.index_dim, device=device)
+        block_keys = torch.linalg.solve(Z.T @ Z + reg, Z.T @ teacher_target).T
+        self.block_keys_16d.data.copy_(block_keys.to(dtype=orig_dtype))
+
+        scores = (Z @ block_keys.T) / math.sqrt(self.index_dim)
+        student_probs = F.softmax(scores / self.temperature, dim=-1)
+        kl = F.kl_div(student_probs.log(), teacher_target, reduction="batchmean").item()
+        _, top_rem = torch.topk(scores.mean(dim=0)[self.base_blocks:], k=self.remote_blocks)
+        calib_active = torch.cat([torch.arange(self.base_blocks, device=device, dtype=torch.int32),
+                                  (top_rem + self.base_blocks).to(torch.int32)])
+        self.set_active_blocks(calib_active)
+        total_var = (S ** 2).sum().item()
+        top16_var = (S[: self.index_dim] ** 2).sum().item()
+        return {
+            "top16_explained_variance": top16_var / max(total_var, 1e-12),
+            "initial_kl_divergence": kl,
+            "num_blocks": self.num_blocks,
+            "active_blocks": self.total_active_blocks,
+            "calib_active_blocks": calib_active.tolist(),
+            "sparsity_pct": (1.0 - self.total_active_blocks / self.num_blocks) * 100.0,
+        }
 
     def compute_router_scores(self, x: Tensor) -> Tensor:
         """Per-token router scores rms_norm(q_proj(x)) @ K_16^T / sqrt(16)
@@ -322,3 +380,79 @@ def compute_teacher_dense_block_targets(
             targets.append(dense_block_targets(norm_h, mlp.gate_proj.weight, mlp.up_proj.weight,
                                                mlp.down_proj.weight, block_size, temperature))
     return t_rep, t_mid, targets
+
+
+def load_foveal_pattention_mlps(
+    checkpoint_dir,
+    layers: Optional[Iterable[int]] = None,
+    block_size: int = 64,
+    base_blocks: int = 4,
+    remote_blocks: int = 20,
+    index_dim: int = 16,
+    temperature: float = 1.0,
+    use_fused_kernel: bool = True,
+    device=None,
+    layer_prefix: str = "model.layers.",
+) -> Dict[int, FovealPattentionMLP]:
+    """FovealPattentionMLP modules for the MLPs of a local Llama-style Hugging
+    Face checkpoint (config.json + *.safetensors, optionally sharded with
+    model.safetensors.index.json), built the way from_dense_mlp
+    (foveal_pattention.py:133-173) and sparsify_model_with_foveal_pattention
+    (:355-387) build them from a loaded model, without instantiating the model:
+    each layer's gate_proj / up_proj / down_proj tensors are read with
+    safetensors straight onto `device` and become k_gate, k_up and v (v keeps
+    down_proj's (hidden, intermediate) storage, the layout the kernels stream).
+    The router's q_proj_16d and block_keys_16d get the module's random
+    initialisation and out_proj_16d is zero, as in from_dense_mlp."""
+    from safetensors import safe_open
+
+    path = Path(checkpoint_dir)
+    cfg = json.loads((path / "config.json").read_text())
+    hidden, inter, n_layers = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
+    index = path / "model.safetensors.index.json"
+    if index.exists():
+        weight_map = json.loads(index.read_text())["weight_map"]
+    else:
+        weight_map = {}
+        for f in sorted(path.glob("*.safetensors")):
+            with safe_open(str(f), framework="pt") as h:
+                weight_map.update({k: f.name for k in h.keys()})
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    targets = list(range(n_layers)) if layers is None else list(layers)
+    handles: Dict[str, Any] = {}
+    out: Dict[int, FovealPattentionMLP] = {}
+    try:
+        for i in targets:
+            if not 0 <= i < n_layers:
+                raise IndexError(f"layer {i} outside [0, {n_layers})")
+            w = {}
+            for p in ("gate", "up", "down"):
+                name = f"{layer_prefix}{i}.mlp.{p}_proj.weight"
+                if name not in weight_map:
+                    raise KeyError(f"{name} not found in {path}")
+                f = weight_map[name]
+                if f not in handles:
+                    handles[f] = safe_open(str(path / f), framework="pt", device=str(dev))
+                w[p] = handles[f].get_tensor(name)
+            if (tuple(w["gate"].shape) != (inter, hidden) or tuple(w["up"].shape) != (inter, hidden)
+                    or tuple(w["down"].shape) != (hidden, inter)):
+                raise ValueError(f"layer {i}: gate {tuple(w['gate'].shape)}, up {tuple(w['up'].shape)}, "
+                                 f"down {tuple(w['down'].shape)} do not match config ({hidden}, {inter})")
+            with torch.device("meta"):
+                m = FovealPattentionMLP(hidden_dim=hidden, intermediate_dim=inter, block_size=block_size,
+                                        base_blocks=base_blocks, remote_blocks=remote_blocks, index_dim=index_dim,
+                                        temperature=temperature, dtype=w["gate"].dtype,
+                                        use_fused_kernel=use_fused_kernel)
+            m = m.to_empty(device=dev)
+            with torch.no_grad():
+                m.k_gate = nn.Parameter(w["gate"])
+                m.k_up = nn.Parameter(w["up"])
+                m.v = nn.Parameter(w["down"].t())
+                m.offsets.copy_(torch.arange(block_size, dtype=torch.int64))
+                nn.init.normal_(m.q_proj_16d.weight, std=hidden ** -0.5)
+                nn.init.normal_(m.block_keys_16d, std=index_dim ** -0.5)
+                nn.init.zeros_(m.out_proj_16d.weight)
+            out[i] = m
+    finally:
+        handles.clear()
+    return out

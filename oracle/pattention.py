@@ -11,6 +11,7 @@ lands at the same points as the reference):
   * _swiglu_bwd_kernel                  foveal_indexer/pattention_triton.py:49-71 (closed form, fp64)
   * FovealPattentionMLP training forward foveal_indexer/foveal_pattention.py:292-307, 328-342
   * dense block-energy teacher targets  archive/hy_mt2/llm_pattention/train_foveal_pattention_speedrun.py:176-185
+  * calibrate_offline_svd               foveal_indexer/foveal_pattention.py:175-255 (fp64)
 """
 from __future__ import annotations
 
@@ -164,3 +165,30 @@ def dense_block_targets(norm_h: Tensor, gate_w: Tensor, up_w: Tensor, down_w: Te
     act_blocks = act.abs().view(*act.shape[:-1], nb, block_size).mean(dim=-1)
     energy = act_blocks * dw_norms
     return F.softmax(energy.float() / temperature, dim=-1)
+
+
+def calibrate_offline_svd(k_gate: Tensor, k_up: Tensor, v: Tensor, X: Tensor, index_dim: int, block_size: int,
+                          base_blocks: int, remote_blocks: int, temperature: float, ridge_lambda: float):
+    """FovealPattentionMLP.calibrate_offline_svd (foveal_pattention.py:175-255)
+    in fp64: returns (q_proj weight (16, D), block keys (nb, 16), metrics).
+    v is the logical (intermediate, hidden) V = W_down^T."""
+    X = X.double().reshape(-1, k_gate.shape[1])
+    _, S, Vh = torch.linalg.svd(X, full_matrices=False)
+    V16 = Vh[:index_dim].T
+    Z = F.rms_norm(X @ V16, (index_dim,))
+    kg, ku, vv = k_gate.double(), k_up.double(), v.double()
+    A = F.silu(X @ kg.T) * (X @ ku.T)
+    nb = kg.shape[0] // block_size
+    energies = [A[:, b * block_size:(b + 1) * block_size].abs().mean(dim=-1)
+                * vv[b * block_size:(b + 1) * block_size].norm() for b in range(nb)]
+    target = F.softmax(torch.stack(energies, dim=-1) / temperature, dim=-1)
+    reg = ridge_lambda * torch.eye(index_dim, dtype=torch.float64)
+    keys = torch.linalg.solve(Z.T @ Z + reg, Z.T @ target).T
+    scores = Z @ keys.T / math.sqrt(index_dim)
+    kl = F.kl_div(F.softmax(scores / temperature, dim=-1).log(), target, reduction="batchmean").item()
+    _, top = torch.topk(scores.mean(dim=0)[base_blocks:], k=remote_blocks)
+    active = torch.cat([torch.arange(base_blocks), top + base_blocks]).to(torch.int32)
+    metrics = {"top16_explained_variance": ((S[:index_dim] ** 2).sum() / (S ** 2).sum()).item(),
+               "initial_kl_divergence": kl, "calib_active_blocks": active.tolist(), "Z": Z, "target": target,
+               "scores": scores}
+    return V16.T, keys, metrics

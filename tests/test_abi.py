@@ -107,3 +107,43 @@ def test_module_matches_reference_interface(fsi):
     m.train()
     with pytest.raises(RuntimeError, match="ROCm GPU"):  # no CPU path, training included
         m(torch.randn(2, 3, 128))
+
+
+def test_load_foveal_pattention_mlps_from_safetensors(fsi, tmp_path):
+    """A local Llama-style checkpoint (sharded safetensors + index) becomes one
+    FovealPattentionMLP per layer with the exact dense weights (K_gate = W_gate,
+    K_up = W_up, V = W_down^T over down_proj's storage) and the reference's
+    from_dense_mlp router initialisation (zero out_proj)."""
+    import json
+
+    import torch
+    from safetensors.torch import save_file
+
+    g = torch.Generator().manual_seed(0)
+    t = {}
+    for i in range(3):
+        t[f"model.layers.{i}.mlp.gate_proj.weight"] = torch.randn(256, 64, generator=g).bfloat16()
+        t[f"model.layers.{i}.mlp.up_proj.weight"] = torch.randn(256, 64, generator=g).bfloat16()
+        t[f"model.layers.{i}.mlp.down_proj.weight"] = torch.randn(64, 256, generator=g).bfloat16()
+    names = sorted(t)
+    shard = {n: ("model-00001-of-00002.safetensors" if "layers.0" in n or "layers.1.mlp.up" in n
+                 else "model-00002-of-00002.safetensors") for n in names}
+    for f in set(shard.values()):
+        save_file({n: t[n] for n in names if shard[n] == f}, str(tmp_path / f))
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": shard}))
+    (tmp_path / "config.json").write_text(json.dumps({"hidden_size": 64, "intermediate_size": 256,
+                                                      "num_hidden_layers": 3}))
+    ms = fsi.load_foveal_pattention_mlps(tmp_path, layers=[0, 2], block_size=64, base_blocks=1, remote_blocks=2,
+                                         device="cpu")
+    assert sorted(ms) == [0, 2]
+    for i, m in ms.items():
+        assert torch.equal(m.k_gate, t[f"model.layers.{i}.mlp.gate_proj.weight"])
+        assert torch.equal(m.k_up, t[f"model.layers.{i}.mlp.up_proj.weight"])
+        assert torch.equal(m.v, t[f"model.layers.{i}.mlp.down_proj.weight"].t()) and m.v.t().is_contiguous()
+        assert torch.equal(m.offsets, torch.arange(64)) and not m.out_proj_16d.weight.any()
+        assert m.q_proj_16d.weight.dtype == torch.bfloat16 and m.q_proj_16d.weight.std() > 0
+        assert m.num_blocks == 4 and m.total_active_blocks == 3
+    with pytest.raises(IndexError):
+        fsi.load_foveal_pattention_mlps(tmp_path, layers=[3], device="cpu")
+    with pytest.raises(KeyError):
+        fsi.load_foveal_pattention_mlps(tmp_path, layers=[0], device="cpu", layer_prefix="transformer.h.")

@@ -165,3 +165,33 @@ def test_dense_block_targets_brute_force():
         want = torch.tensor([math.exp(v - mx) / z for v in e])
         assert torch.allclose(P_[m].double(), want.double(), rtol=1e-5, atol=1e-7)
     assert torch.allclose(P_.sum(-1), torch.ones(M), atol=1e-6)
+
+
+def test_calibrate_offline_svd_oracle_invariants():
+    """The calibration oracle (foveal_pattention.py:175-255) against facts the
+    mathematics fixes: orthonormal q rows spanning the top eigenvectors of X^T X,
+    explained variance from the eigenvalues, the ridge normal equations, and the
+    teacher targets against brute-force block energies."""
+    g0 = torch.Generator().manual_seed(4)
+    D, I, bs = 24, 128, 32
+    X = torch.randn(200, D, generator=g0, dtype=torch.float64) * torch.linspace(3, 0.2, D, dtype=torch.float64)
+    kg = torch.randn(I, D, generator=g0, dtype=torch.float64) * 0.2
+    ku = torch.randn(I, D, generator=g0, dtype=torch.float64) * 0.2
+    v = torch.randn(I, D, generator=g0, dtype=torch.float64) * 0.2
+    q, keys, met = P.calibrate_offline_svd(kg, ku, v, X, 16, bs, 1, 2, 0.5, 1e-2)
+    assert torch.allclose(q @ q.T, torch.eye(16, dtype=torch.float64), atol=1e-10)
+    evals, evecs = torch.linalg.eigh(X.T @ X)
+    top = evecs[:, -16:]
+    assert torch.allclose(q.T @ (q @ top), top, atol=1e-8)  # same subspace
+    assert abs(met["top16_explained_variance"] - (evals[-16:].sum() / evals.sum()).item()) < 1e-10
+    Z, target = met["Z"], met["target"]
+    resid = (Z.T @ Z + 1e-2 * torch.eye(16, dtype=torch.float64)) @ keys.T - Z.T @ target
+    assert resid.abs().max() < 1e-9
+    t, b = 7, 2  # one target entry by brute force
+    e = []
+    for blk in range(I // bs):
+        a = sum(abs(torch.nn.functional.silu(X[t] @ kg[j]) * (X[t] @ ku[j])) for j in range(blk * bs, (blk + 1) * bs))
+        e.append(a / bs * v[blk * bs:(blk + 1) * bs].pow(2).sum().sqrt())
+    e = torch.stack(e) / 0.5
+    assert torch.allclose(target[t], torch.softmax(e, 0), atol=1e-12)
+    assert met["calib_active_blocks"][0] == 0 and len(met["calib_active_blocks"]) == 3

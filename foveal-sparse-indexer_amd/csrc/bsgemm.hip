@@ -88,6 +88,21 @@ __device__ __forceinline__ float energy_term(float gv, float uv, int rounding) {
   return fabsf(rounding == FSI_ROUND_FP32 ? h : round_bf16(h));
 }
 
+// Four consecutive bf16 outputs C[off .. off + 3] (n of them inside the matrix): one
+// 8-byte store when all four exist and `vec` (8-byte aligned rows) holds.
+__device__ __forceinline__ void store4_bf16(bf16_t* C, int64_t off, const float (&v)[4], int n, bool vec) {
+  if (vec && n >= 4) {
+    uint2 w;
+    w.x = pack_bf16x2(v[0], v[1]);
+    w.y = pack_bf16x2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(C + off) = w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j < n) C[off + j] = f32_to_bf16(v[j]);
+  }
+}
+
 // ktab[i] = first B column of active K block i, or -1 when its id is out of range.
 __device__ __forceinline__ void fill_ktab(const GemmArgs& g, int32_t* ktab, int nthreads) {
   for (int i = threadIdx.x; i < g.n_blocks; i += nthreads) {
@@ -534,7 +549,7 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int f = 0; f < BNF; ++f) acc[i][f] = mfma16x16x32(fa[i], fb[f], acc[i][f]);
+        for (int f = 0; f < BNF; ++f) acc[i][f] = mfma16x16x32(fb[f], fa[i], acc[i][f]);  // C^T fragment
     }
   };
 
@@ -583,22 +598,27 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
   }
 #endif
 
-  // ---- epilogue: lane holds C[row 4 (lane / 16) + j][col lane % 16] of each fragment ----
-  const int crow0 = m0 + 128 * wm + 4 * (lane >> 4);
+  // ---- epilogue: the fragments hold C^T, so lane (q = lane / 16, r = lane % 16) of
+  // fragment (i, f) holds row 16 i + r of the wave's rows and the four consecutive
+  // columns 4 q .. 4 q + 3 of the fragment: one 8-byte store per fragment
+  const int crow = m0 + 128 * wm + frow;
+  const int cq = 4 * fchunk;
+  const bool vec = (reinterpret_cast<uintptr_t>(g.C) & 7) == 0 && (g.ldc & 3) == 0;
   if (EPI == EPI_SWIGLU) {
 #pragma unroll
     for (int f = 0; f < BNF / 2; ++f) {
-      const int ch = ccol[0] + BHW * wn + 16 * f + frow;  // ccol[0] = first channel of the tile
+      const int ch = ccol[0] + BHW * wn + 16 * f + cq;  // ccol[0] = first channel of the tile
       if (ch >= g.N) continue;
+      const int n = g.N - ch;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 8; ++i) {
+        const int m = crow + 16 * i;
+        if (m >= g.M) continue;
+        float h[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = crow0 + 16 * i + j;
-          if (m >= g.M) continue;
-          const float h = pattention_act<ACT_SWIGLU>(acc[i][f][j], acc[i][f + BNF / 2][j], g.rounding);
-          g.C[static_cast<int64_t>(m) * g.ldc + ch] = f32_to_bf16(h);
-        }
+        for (int j = 0; j < 4; ++j) h[j] = pattention_act<ACT_SWIGLU>(acc[i][f][j], acc[i][f + BNF / 2][j], g.rounding);
+        store4_bf16(g.C, static_cast<int64_t>(m) * g.ldc + ch, h, n, vec);
+      }
     }
   } else {
 #pragma unroll
@@ -606,17 +626,22 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
       const int tc = bcol(f);
       const int s = tc / SUB;
       if (NM != N_DIRECT && !bval[s]) continue;
-      const int col = ccol[s] + (tc % SUB) + frow;
+      const int col = ccol[s] + (tc % SUB) + cq;
       if (NM == N_DIRECT && col >= g.N) continue;
-      const float bv = g.bias ? bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + frow : col]) : 0.f;
+      const int n = NM == N_DIRECT ? g.N - col : 4;
+      float bv[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int j = 0; j < 4; ++j)
+        bv[j] = g.bias && j < n ? bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + cq + j : col + j]) : 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = crow0 + 16 * i + j;
-          if (m >= g.M) continue;
-          g.C[static_cast<int64_t>(m) * g.ldc + col] = f32_to_bf16(acc[i][f][j] + bv);
-        }
+      for (int i = 0; i < 8; ++i) {
+        const int m = crow + 16 * i;
+        if (m >= g.M) continue;
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = acc[i][f][j] + bv[j];
+        store4_bf16(g.C, static_cast<int64_t>(m) * g.ldc + col, o, n, vec);
+      }
     }
   }
 }

@@ -18,6 +18,8 @@
 // 64-column halves, so a gate column and its up column land in the same lane.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "fsi_common.h"
 
 using namespace fsi;
@@ -86,6 +88,36 @@ __device__ __forceinline__ float sum16(float v) {
 __device__ __forceinline__ float energy_term(float gv, float uv, int rounding) {
   const float h = pattention_act<ACT_SWIGLU>(gv, uv, rounding);
   return fabsf(rounding == FSI_ROUND_FP32 ? h : round_bf16(h));
+}
+
+// Two fp32 values to a packed bf16 pair with v_cvt_pk_bf16_f32 (round to nearest even).
+__device__ __forceinline__ uint32_t hw_pack_bf16x2(float a, float b) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// SwiGLU of the GEMM epilogue with the rounding mode R fixed at compile time:
+// silu from the hardware exp2 and reciprocal (about 1 ulp each in fp32; the result
+// is rounded to bf16).  The library expf / IEEE divide expand to ~25 instructions
+// per element, and the epilogue runs once per tile from a cold instruction cache.
+template <int R>
+__device__ __forceinline__ float swiglu_epi(float gv, float uv) {
+  if (R != FSI_ROUND_FP32) {
+    gv = round_bf16(gv);
+    uv = round_bf16(uv);
+  }
+  float s = gv * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * gv));
+  if (R == FSI_ROUND_EAGER) s = round_bf16(s);
+  return s * uv;
+}
+
+// Epilogue fast path: four outputs known to be inside the matrix, 8-byte aligned.
+__device__ __forceinline__ void store4_fast(bf16_t* C, int64_t off, const float (&v)[4]) {
+  uint2 w;
+  w.x = hw_pack_bf16x2(v[0], v[1]);
+  w.y = hw_pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<uint2*>(C + off) = w;
 }
 
 // Four consecutive bf16 outputs C[off .. off + 3] (n of them inside the matrix): one
@@ -270,7 +302,7 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fa[i], fb[f], acc[i][f]);
+        for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fb[f], fa[i], acc[i][f]);  // C^T fragment
     }
   };
   auto clampk = [&](int st) { return st < kcount ? st : (kcount > 0 ? kcount - 1 : 0); };
@@ -309,60 +341,128 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
     }
   }
 
-  // ---- epilogue: lane holds C[row 4 (lane / 16) + j][col lane % 16] of each fragment ----
-  const int crow0 = m0 + 64 * wm + 4 * (lane >> 4);
+  // ---- epilogue: the fragments hold C^T, so lane (q = lane / 16, r = lane % 16) of
+  // fragment (i, f) holds row 16 i + r of the wave's rows and the four consecutive
+  // columns 4 q .. 4 q + 3 of the fragment: one 8-byte store per fragment; interior
+  // tiles take a branch-free path (see the 256 x 256 kernels)
+  const int crow = m0 + 64 * wm + frow;
+  const int cq = 4 * fchunk;
+  const bool vec = (reinterpret_cast<uintptr_t>(g.C) & 7) == 0 && (g.ldc & 3) == 0;
+  const bool rows_in = m0 + TM <= g.M;
   if (EPI == EPI_SWIGLU) {
-    // gate fragments f = 0, 1 pair with up fragments f = 2, 3 (same channel)
+    // gate fragments f = 0, 1 pair with up fragments f = 2, 3 (same channel); both
+    // gate fragments of wave wn lie in sub-block wn
+    const bool live = g.act == ACT_SWIGLU && bval[wn] && bval[2 + wn];
+    const int ch0 = ccol[0] + 32 * wn + cq;
+    auto interior = [&](auto rnd) {
+      constexpr int R = decltype(rnd)::value;
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      const int ch = ccol[0] + 32 * wn + 16 * f + frow;  // ccol[0] = first channel of the tile
-      if (ch >= g.N) continue;
+      for (int f = 0; f < 2; ++f)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+          float h[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = crow0 + 16 * i + j;
-          if (m >= g.M) continue;
-          float gv = acc[i][f][j], uv = acc[i][f + 2][j];
-          float h;
-          if (g.act == ACT_SWIGLU) h = pattention_act<ACT_SWIGLU>(gv, uv, g.rounding);
-          else h = 0.f;
-          g.C[m * g.ldc + ch] = f32_to_bf16(h);
+          for (int j = 0; j < 4; ++j) h[j] = swiglu_epi<R>(acc[i][f][j], acc[i][f + 2][j]);
+          store4_fast(g.C, static_cast<int64_t>(crow + 16 * i) * g.ldc + ch0 + 16 * f, h);
         }
+    };
+    if (vec && rows_in && live && ccol[0] + 64 <= g.N) {
+      if (g.rounding == FSI_ROUND_FP32) interior(std::integral_constant<int, FSI_ROUND_FP32>{});
+      else if (g.rounding == FSI_ROUND_FUSED) interior(std::integral_constant<int, FSI_ROUND_FUSED>{});
+      else interior(std::integral_constant<int, FSI_ROUND_EAGER>{});
+    } else {
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const int ch = ch0 + 16 * f;
+        if (ch >= g.N) continue;
+        const int n = g.N - ch;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = crow + 16 * i;
+          if (m >= g.M) continue;
+          float h[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            h[j] = live ? pattention_act<ACT_SWIGLU>(acc[i][f][j], acc[i][f + 2][j], g.rounding) : 0.f;
+          store4_bf16(g.C, static_cast<int64_t>(m) * g.ldc + ch, h, n, vec);
+        }
+      }
     }
   } else if (EPI == EPI_ENERGY) {
-    // wave wn holds the tile's channels 32 wn .. 32 wn + 31 (gate fragments f = 0, 1)
+    // wave wn holds the tile's channels 32 wn .. 32 wn + 31 (gate fragments f = 0, 1):
+    // each lane sums its 8 channels of row 16 i + r, then the four lanes r, r + 16,
+    // r + 32, r + 48 of the row are added
     const int grp_ch = ccol[0] + 32 * wn;
     if (grp_ch < g.N) {
       const bool live = bval[wn] && bval[2 + wn];
+      auto sums = [&](auto rnd) {
+        constexpr int R = decltype(rnd)::value;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int i = 0; i < 4; ++i) {
           float e = 0.f;
-          if (live) e = energy_term(acc[i][0][j], acc[i][2][j], g.rounding) + energy_term(acc[i][1][j], acc[i][3][j], g.rounding);
-          e = sum16(e);
-          const int m = crow0 + 16 * i + j;
-          if (frow == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
+          if (live) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              e += energy_term(acc[i][0][j], acc[i][2][j], R) + energy_term(acc[i][1][j], acc[i][3][j], R);
+          }
+          e += __shfl_xor(e, 16);
+          e += __shfl_xor(e, 32);
+          const int m = crow + 16 * i;
+          if (fchunk == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
         }
+      };
+      if (g.rounding == FSI_ROUND_FP32) sums(std::integral_constant<int, FSI_ROUND_FP32>{});
+      else if (g.rounding == FSI_ROUND_FUSED) sums(std::integral_constant<int, FSI_ROUND_FUSED>{});
+      else sums(std::integral_constant<int, FSI_ROUND_EAGER>{});
     }
   } else {
+    auto tcol = [&](int f) { return f < 2 ? 32 * wn + 16 * f : 64 + 32 * wn + 16 * (f - 2); };
+    bool all = vec && rows_in;
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const int tc = f < 2 ? 32 * wn + 16 * f : 64 + 32 * wn + 16 * (f - 2);  // tile column of the fragment
-      const int s = tc / SUB;
-      if (NM != N_DIRECT && !bval[s]) continue;
-      const int col = ccol[s] + (tc % SUB) + frow;
-      if (NM == N_DIRECT && col >= g.N) continue;
-      const float bv = g.bias ? bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + frow : col]) : 0.f;
+    for (int sb = 0; sb < 4; ++sb) all = all && (NM == N_DIRECT ? ccol[sb] + SUB <= g.N : bval[sb]);
+    if (all) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int f = 0; f < 4; ++f) {
+        const int tc = tcol(f);
+        const int s = tc / SUB;
+        const int col = ccol[s] + (tc % SUB) + cq;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (g.bias) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = crow0 + 16 * i + j;
-          if (m >= g.M) continue;
-          g.C[m * g.ldc + col] = f32_to_bf16(acc[i][f][j] + bv);
+          for (int j = 0; j < 4; ++j)
+            bv[j] = bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + cq + j : col + j]);
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = acc[i][f][j] + bv[j];
+          store4_fast(g.C, static_cast<int64_t>(crow + 16 * i) * g.ldc + col, o);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const int tc = tcol(f);
+        const int s = tc / SUB;
+        if (NM != N_DIRECT && !bval[s]) continue;
+        const int col = ccol[s] + (tc % SUB) + cq;
+        if (NM == N_DIRECT && col >= g.N) continue;
+        const int n = NM == N_DIRECT ? g.N - col : 4;
+        float bv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bv[j] = g.bias && j < n ? bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + cq + j : col + j]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = crow + 16 * i;
+          if (m >= g.M) continue;
+          float o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = acc[i][f][j] + bv[j];
+          store4_bf16(g.C, static_cast<int64_t>(m) * g.ldc + col, o, n, vec);
+        }
+      }
     }
   }
 }
@@ -621,6 +721,31 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
       }
     }
   } else {
+    bool all = vec && m0 + BM <= g.M;
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) all = all && (NM == N_DIRECT ? ccol[sb] + SUB <= g.N : bval[sb]);
+    if (all) {  // interior tile: no per-element checks (the epilogue's code size is its cost)
+#pragma unroll
+      for (int f = 0; f < BNF; ++f) {
+        const int tc = bcol(f);
+        const int s = tc / SUB;
+        const int col = ccol[s] + (tc % SUB) + cq;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (g.bias) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            bv[j] = bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + cq + j : col + j]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = acc[i][f][j] + bv[j];
+          store4_fast(g.C, static_cast<int64_t>(crow + 16 * i) * g.ldc + col, o);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int f = 0; f < BNF; ++f) {
       const int tc = bcol(f);
@@ -814,7 +939,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fa[i], fb[f], acc[i][f]);
+      for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fb[f], fa[i], acc[i][f]);  // C^T fragment
   };
 #if FSI_GEMM_DMA_PREFETCH
   // Step s + 2 must have landed at the end of iteration s (its fragments are read
@@ -889,58 +1014,127 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   }
 #endif
 
-  // ---- epilogue: lane holds C[row 4 (lane / 16) + j][col lane % 16] of each fragment ----
-  const int crow0 = m0 + 128 * wm + 4 * (lane >> 4);
+  // ---- epilogue: the fragments hold C^T, so lane (q = lane / 16, r = lane % 16) of
+  // fragment (i, f) holds row 16 i + r of the wave's rows and the four consecutive
+  // columns 4 q .. 4 q + 3 of the fragment: one 8-byte store per fragment.  Interior
+  // tiles take a branch-free path with the rounding mode fixed at compile time: the
+  // epilogue runs once per tile from a cold instruction cache, so its code size is
+  // its cost.
+  const int crow = m0 + 128 * wm + frow;
+  const int cq = 4 * fchunk;
+  const bool vec = (reinterpret_cast<uintptr_t>(g.C) & 7) == 0 && (g.ldc & 3) == 0;
+  const bool rows_in = m0 + BM <= g.M;
   if (EPI == EPI_SWIGLU) {
+    const bool live = bval[wn] && bval[4 + wn];  // both gate fragments lie in sub-block wn
+    const int ch0 = ccol[0] + 32 * wn + cq;
+    auto interior = [&](auto rnd) {
+      constexpr int R = decltype(rnd)::value;
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      const int tc = 32 * wn + 16 * f;          // gate tile column of the fragment
-      const int ch = ccol[0] + tc + frow;       // ccol[0] = first channel of the tile
-      if (ch >= g.N) continue;
-      const bool live = bval[tc / SUB] && bval[4 + tc / SUB];
+      for (int f = 0; f < 2; ++f)
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < 8; ++i) {
+          float h[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = crow0 + 16 * i + j;
-          if (m >= g.M) continue;
-          const float h = live ? pattention_act<ACT_SWIGLU>(acc[i][f][j], acc[i][f + 2][j], g.rounding) : 0.f;
-          g.C[static_cast<int64_t>(m) * g.ldc + ch] = f32_to_bf16(h);
+          for (int j = 0; j < 4; ++j) h[j] = swiglu_epi<R>(acc[i][f][j], acc[i][f + 2][j]);
+          store4_fast(g.C, static_cast<int64_t>(crow + 16 * i) * g.ldc + ch0 + 16 * f, h);
         }
+    };
+    if (vec && rows_in && live && ccol[0] + 128 <= g.N) {
+      if (g.rounding == FSI_ROUND_FP32) interior(std::integral_constant<int, FSI_ROUND_FP32>{});
+      else if (g.rounding == FSI_ROUND_FUSED) interior(std::integral_constant<int, FSI_ROUND_FUSED>{});
+      else interior(std::integral_constant<int, FSI_ROUND_EAGER>{});
+    } else {
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const int ch = ch0 + 16 * f;
+        if (ch >= g.N) continue;
+        const int n = g.N - ch;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int m = crow + 16 * i;
+          if (m >= g.M) continue;
+          float h[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            h[j] = live ? pattention_act<ACT_SWIGLU>(acc[i][f][j], acc[i][f + 2][j], g.rounding) : 0.f;
+          store4_bf16(g.C, static_cast<int64_t>(m) * g.ldc + ch, h, n, vec);
+        }
+      }
     }
   } else if (EPI == EPI_ENERGY) {
-    // wave wn holds the tile's channels 32 wn .. 32 wn + 31 (gate fragments f = 0, 1)
+    // wave wn holds the tile's channels 32 wn .. 32 wn + 31 (gate fragments f = 0, 1):
+    // each lane sums its 8 channels of row 16 i + r, then the four lanes r, r + 16,
+    // r + 32, r + 48 of the row are added
     const int grp_ch = ccol[0] + 32 * wn;
     if (grp_ch < g.N) {
       const bool live = bval[wn] && bval[4 + wn];
+      auto sums = [&](auto rnd) {
+        constexpr int R = decltype(rnd)::value;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int i = 0; i < 8; ++i) {
           float e = 0.f;
-          if (live) e = energy_term(acc[i][0][j], acc[i][2][j], g.rounding) + energy_term(acc[i][1][j], acc[i][3][j], g.rounding);
-          e = sum16(e);
-          const int m = crow0 + 16 * i + j;
-          if (frow == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
+          if (live) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              e += energy_term(acc[i][0][j], acc[i][2][j], R) + energy_term(acc[i][1][j], acc[i][3][j], R);
+          }
+          e += __shfl_xor(e, 16);
+          e += __shfl_xor(e, 32);
+          const int m = crow + 16 * i;
+          if (fchunk == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
         }
+      };
+      if (g.rounding == FSI_ROUND_FP32) sums(std::integral_constant<int, FSI_ROUND_FP32>{});
+      else if (g.rounding == FSI_ROUND_FUSED) sums(std::integral_constant<int, FSI_ROUND_FUSED>{});
+      else sums(std::integral_constant<int, FSI_ROUND_EAGER>{});
     }
   } else {
+    bool all = vec && rows_in;
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const int tc = bcol(f);
-      const int s = tc / SUB;
-      if (NM != N_DIRECT && !bval[s]) continue;
-      const int col = ccol[s] + (tc % SUB) + frow;
-      if (NM == N_DIRECT && col >= g.N) continue;
-      const float bv = g.bias ? bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + frow : col]) : 0.f;
+    for (int sb = 0; sb < 8; ++sb) all = all && (NM == N_DIRECT ? ccol[sb] + SUB <= g.N : bval[sb]);
+    if (all) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int f = 0; f < 4; ++f) {
+        const int tc = bcol(f);
+        const int s = tc / SUB;
+        const int col = ccol[s] + (tc % SUB) + cq;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (g.bias) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = crow0 + 16 * i + j;
-          if (m >= g.M) continue;
-          g.C[static_cast<int64_t>(m) * g.ldc + col] = f32_to_bf16(acc[i][f][j] + bv);
+          for (int j = 0; j < 4; ++j)
+            bv[j] = bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + cq + j : col + j]);
         }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = acc[i][f][j] + bv[j];
+          store4_fast(g.C, static_cast<int64_t>(crow + 16 * i) * g.ldc + col, o);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const int tc = bcol(f);
+        const int s = tc / SUB;
+        if (NM != N_DIRECT && !bval[s]) continue;
+        const int col = ccol[s] + (tc % SUB) + cq;
+        if (NM == N_DIRECT && col >= g.N) continue;
+        const int n = NM == N_DIRECT ? g.N - col : 4;
+        float bv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bv[j] = g.bias && j < n ? bf16_to_f32(g.bias[NM == N_GATHER ? brow[s] + (tc % SUB) + cq + j : col + j]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int m = crow + 16 * i;
+          if (m >= g.M) continue;
+          float o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = acc[i][f][j] + bv[j];
+          store4_bf16(g.C, static_cast<int64_t>(m) * g.ldc + col, o, n, vec);
+        }
+      }
     }
   }
 }

@@ -70,6 +70,13 @@ struct GemmArgs {
   int m_tiles, n_tiles;        // dense grid (non-list modes)
   int act, rounding;           // EPI_SWIGLU
   int* err;
+  // Packed B (the decode weight layout: 16 x 32 MFMA operand tiles of 1 KiB in lane
+  // order).  N_DUAL / K_DENSE: tile (ct, s) of 16 rows at (ct pk_S + s) KiB of Bp0
+  // (gate) / Bp1 (up).  N_DIRECT / K_GATHER_B: tile (b, dt, cl) of block b, 16 output
+  // dims dt, 32-channel slice cl at ((b pk_DT + dt) pk_CB + cl) KiB of Bp0.
+  const bf16_t* Bp0;
+  const bf16_t* Bp1;
+  int pk_S, pk_DT, pk_CB;
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
@@ -800,6 +807,7 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
 #define FSI_GEMM_DMA_KGATHER 0
 #endif
 constexpr int DK = 32, DSTAGES = FSI_GEMM_DMA_STAGES, DTHREADS = 512;
+constexpr int PK_TILE_ELEMS = 512;  // bf16 elements of one packed 16 x 32 operand tile
 
 // Chunk swizzle of 64-byte LDS rows.  A 128-bit LDS read is served eight lanes at a
 // time over a 128-byte bank period, so the eight rows r .. r + 7 of one fragment
@@ -825,8 +833,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // LDS accesses across it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <int NM, int KM, int EPI>
+template <int NM, int KM, int EPI, bool PB = false>
 __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
+  static_assert(!PB || (NM == N_DUAL && KM == K_DENSE) || (NM == N_DIRECT && KM == K_GATHER_B),
+                "packed B: gate/up (dual, dense K) or down (direct, gathered K)");
   static_assert(KM != K_LIST, "tile lists run on the 128 x 128 kernel");
   __shared__ __attribute__((aligned(1024))) bf16_t lds[DSTAGES][2][BM * DK];  // [stage][A/B][row * 32 + k]
   __shared__ int32_t ktab[KM == K_GATHER_B ? KTAB_MAX : 1];
@@ -881,6 +891,9 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   // (4 chunks of 16) per row, the chunk of row r at physical slot chunk ^ dswz(r).
   // Wave w loads KiB 2 w and 2 w + 1 of A and of B (16 rows each): lane l lands at
   // row 16 KiB + l / 4, slot l % 4, so it loads the logical chunk (l % 4) ^ dswz(row).
+  // Packed B: the stage holds B as 16 fragments of 1 KiB in lane order (fragment
+  // fi = tile columns 16 fi .. 16 fi + 15) and wave w loads fragments 2 w, 2 w + 1
+  // straight from their packed tiles: one contiguous KiB per load.
   const bf16_t* asrc[2];
   const bf16_t* bsrc[2];
 #pragma unroll
@@ -889,19 +902,60 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
     const int lc = (lane & 3) ^ dswz(r);
     const int m = m0 + r < g.M ? m0 + r : g.M - 1;
     asrc[j] = g.A + static_cast<int64_t>(m) * g.lda + lc * 8;
-    const int s = r / SUB;
-    const bf16_t* bp = (NM == N_DUAL && s >= 4) ? g.B1 : g.B0;
-    int64_t brw = brow[s] + (r % SUB);
-    if (NM == N_DIRECT && brw >= g.N) brw = g.N - 1;
-    bsrc[j] = bp + brw * g.ldb + lc * 8;
+    if (PB) {
+      const int fi = 2 * wave + j;
+      if (NM == N_DUAL) {
+        const int sb = fi >> 1;                                     // 32-row sub-block
+        const int64_t ct = (brow[sb] >> 4) + (fi & 1);              // 16-row packed tile
+        bsrc[j] = (sb >= 4 ? g.Bp1 : g.Bp0) + ct * g.pk_S * PK_TILE_ELEMS + lane * 8;
+      } else {
+        int dt = (nt * BN) / 16 + fi;
+        if (dt >= g.pk_DT) dt = g.pk_DT - 1;                        // columns past N: never stored
+        bsrc[j] = g.Bp0 + static_cast<int64_t>(dt) * g.pk_CB * PK_TILE_ELEMS + lane * 8;
+      }
+    } else {
+      const int s = r / SUB;
+      const bf16_t* bp = (NM == N_DUAL && s >= 4) ? g.B1 : g.B0;
+      int64_t brw = brow[s] + (r % SUB);
+      if (NM == N_DIRECT && brw >= g.N) brw = g.N - 1;
+      bsrc[j] = bp + brw * g.ldb + lc * 8;
+    }
+  }
+  // K-gathered B: steps are issued in order, so the block and 32-wide sub-step of the
+  // next issue are counters, and the block's first column (block id for packed B)
+  // comes from a register copy of 64 ktab entries (lane i holds entry 64 c + i) read
+  // with v_readlane.  The copy of the next 64 entries is loaded one chunk ahead, so
+  // an issue never waits on an LDS read (a wait on it would also hold back the
+  // global loads behind the fragment reads in flight).
+  const int per = KM == K_GATHER_B ? g.block / DK : 1;
+  auto kt_load = [&](int c) {
+    const int e = 64 * c + lane;
+    const int col = e < g.n_blocks ? ktab[e] : -1;
+    return PB ? (col < 0 ? -1 : col / g.block) : col;
+  };
+  int iss_blk = 0, iss_sub = 0, kt_cur = 0, kt_next = 0;
+  if (KM == K_GATHER_B) {
+    kt_cur = kt_load(0);
+    kt_next = kt_load(1);
   }
   auto issue = [&](int step, int stage) {
     const int64_t a_k = static_cast<int64_t>(step) * DK;
     int64_t b_k = a_k;
     if (KM == K_GATHER_B) {
-      const int per = g.block / DK;
-      const int col = ktab[step / per];
-      b_k = col < 0 ? 0 : col + (step % per) * DK;  // an inactive block's H columns are zero
+      const int col = __builtin_amdgcn_readlane(kt_cur, iss_blk & 63);
+      if (PB)  // tile (b, dt, cl) at ((b DT + dt) CB + cl) KiB; a dead block reads block 0 (its H is zero)
+        b_k = (static_cast<int64_t>(col < 0 ? 0 : col) * g.pk_DT * g.pk_CB + iss_sub) * PK_TILE_ELEMS;
+      else
+        b_k = col < 0 ? 0 : col + iss_sub * DK;  // an inactive block's H columns are zero
+      if (++iss_sub == per) {
+        iss_sub = 0;
+        if ((++iss_blk & 63) == 0) {
+          kt_cur = kt_next;
+          kt_next = kt_load((iss_blk >> 6) + 1);
+        }
+      }
+    } else if (PB) {
+      b_k = static_cast<int64_t>(step) * PK_TILE_ELEMS;  // k-step s of every row tile
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -926,8 +980,12 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   auto read_frags = [&](int stage, u32x4_t (&fa)[8], u32x4_t (&fb)[4]) {
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
-      const int c = bcol(f) + frow;
-      fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[stage][1][c * DK + (fchunk ^ dswz(c)) * 8]);
+      if (PB) {
+        fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[stage][1][(bcol(f) >> 4) * PK_TILE_ELEMS + lane * 8]);
+      } else {
+        const int c = bcol(f) + frow;
+        fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[stage][1][c * DK + (fchunk ^ dswz(c)) * 8]);
+      }
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -1329,6 +1387,63 @@ int gateup_energy(const bf16_t* x, int64_t ldx, const bf16_t* kg, const bf16_t* 
   a.err = err;
   const bool big = M >= BIG_MIN_M && K % DK == 0;
   return launch_tiled<N_DUAL, K_DENSE, EPI_ENERGY>(a, big, st) == hipSuccess ? 0 : -1;
+}
+
+// Prefill GEMMs over the packed decode weights (B operands as contiguous 1 KiB MFMA
+// tiles).  Need M >= 256 rows' worth of work to pay for the 256 x 256 tiles, K % 32 == 0.
+int gateup_swiglu_packed(const bf16_t* x, int64_t ldx, const bf16_t* kgp, const bf16_t* kup, int S, int N_p,
+                         const int32_t* blocks, int n_active, int block_n, int M, int K, int rounding, bf16_t* H,
+                         int64_t ldh, int* err, hipStream_t st) {
+  GemmArgs a{};
+  a.A = x;
+  a.Bp0 = kgp;
+  a.Bp1 = kup;
+  a.pk_S = S;
+  a.C = H;
+  a.lda = ldx;
+  a.ldc = ldh;
+  a.M = M;
+  a.N = n_active * block_n;
+  a.K = K;
+  a.blocks = blocks;
+  a.n_blocks = n_active;
+  a.block = block_n;
+  a.n_rows_total = N_p;
+  a.act = ACT_SWIGLU;
+  a.rounding = rounding;
+  a.err = err;
+  a.m_tiles = (M + BM - 1) / BM;
+  a.n_tiles = (a.N + BN / 2 - 1) / (BN / 2);
+  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
+  bsgemm_dma_kernel<N_DUAL, K_DENSE, EPI_SWIGLU, true><<<grid, DTHREADS, 0, st>>>(a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int down_gather_packed(const bf16_t* H, int64_t ldh, const bf16_t* vp, int DT, int CB, int N_p,
+                       const int32_t* blocks, int n_active, int block_n, int M, int D, bf16_t* out, int64_t ldo,
+                       int* err, hipStream_t st) {
+  if (n_active > KTAB_MAX) return 1;
+  GemmArgs a{};
+  a.A = H;
+  a.Bp0 = vp;
+  a.pk_DT = DT;
+  a.pk_CB = CB;
+  a.C = out;
+  a.lda = ldh;
+  a.ldc = ldo;
+  a.M = M;
+  a.N = D;
+  a.K = n_active * block_n;
+  a.blocks = blocks;
+  a.n_blocks = n_active;
+  a.block = block_n;
+  a.n_rows_total = N_p;
+  a.err = err;
+  a.m_tiles = (M + BM - 1) / BM;
+  a.n_tiles = (D + BN - 1) / BN;
+  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
+  bsgemm_dma_kernel<N_DIRECT, K_GATHER_B, EPI_STORE, true><<<grid, DTHREADS, 0, st>>>(a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // out[M, D] = H[M, 64 n_active] W_down[:, S]^T with W_down [D, N_p] (row stride ldw)

@@ -38,6 +38,15 @@
 
 using namespace fsi;
 
+namespace fsi_gemm {
+int gateup_swiglu_packed(const bf16_t* x, int64_t ldx, const bf16_t* kgp, const bf16_t* kup, int S, int N_p,
+                         const int32_t* blocks, int n_active, int block_n, int M, int K, int rounding, bf16_t* H,
+                         int64_t ldh, int* err, hipStream_t st);
+int down_gather_packed(const bf16_t* H, int64_t ldh, const bf16_t* vp, int DT, int CB, int N_p,
+                       const int32_t* blocks, int n_active, int block_n, int M, int D, bf16_t* out, int64_t ldo,
+                       int* err, hipStream_t st);
+}  // namespace fsi_gemm
+
 namespace {
 
 constexpr int PK_TILE = 512;  // bf16 elements of one 16 x 32 operand tile
@@ -424,6 +433,16 @@ PkLayout pk_layout(int64_t N_p, int64_t K, int64_t D) {
   return l;
 }
 
+// Prefill (M >= PK_PREFILL_MIN_M tokens) runs the two 256 x 256 direct-to-LDS GEMMs
+// over the packed tiles with a row-major H [M, n_ch] in the workspace.
+constexpr int64_t PK_PREFILL_MIN_M = 256;
+constexpr int64_t PK_PREFILL_MAX_BLOCKS = 2048;
+
+size_t pk_prefill_workspace(int64_t M, int64_t n_ch, int64_t n_blocks) {
+  return FSI_WORKSPACE_COUNTER_BYTES + fsi_host::align_up(sizeof(bf16_t) * static_cast<size_t>(M) * n_ch, 256) +
+         fsi_host::align_up(sizeof(int32_t) * static_cast<size_t>(n_blocks + 1), 256);
+}
+
 size_t pk_workspace(int64_t n_ch, int64_t n_blocks) {
   const int ns = down_steps(n_ch);
   const int64_t n_ch_pad = int64_t(PK_WAVES) * 32 * (ns ? ns : 32);
@@ -486,6 +505,7 @@ size_t fsi_pattention_packed_workspace_size(int64_t M, int64_t K, int64_t D_out,
                                             int64_t block_n) {
   if (M <= 0 || K <= 0 || D_out <= 0 || n_channels <= 0 || block_n <= 0) return FSI_WORKSPACE_COUNTER_BYTES;
   const int64_t nb = (n_channels + block_n - 1) / block_n;
+  if (M >= PK_PREFILL_MIN_M) return pk_prefill_workspace(M, n_channels, nb);
   return pk_workspace(n_channels, nb);
 }
 
@@ -500,7 +520,9 @@ int fsi_pattention_fwd_packed(const void* x, int64_t ldx, const void* packed, co
   FSI_CHECK_ARG(x && packed && out, FSI_ERR_INVALID_ARG, "pattention_packed: null pointer");
   FSI_CHECK_ARG(active_blocks != nullptr || n_active == 0, FSI_ERR_INVALID_ARG,
                 "pattention_packed: n_active > 0 with null active_blocks");
-  FSI_CHECK_ARG(M >= 1 && M <= 64, FSI_ERR_SHAPE, "pattention_packed: M=%lld (1..64 tokens)", (long long)M);
+  FSI_CHECK_ARG((M >= 1 && M <= 64) || M >= PK_PREFILL_MIN_M, FSI_ERR_SHAPE,
+                "pattention_packed: M=%lld (1..64 tokens, or >= %lld)", (long long)M, (long long)PK_PREFILL_MIN_M);
+  FSI_CHECK_ARG(M <= 0x7fffffff, FSI_ERR_SHAPE, "pattention_packed: M beyond int32");
   const int64_t nc = K / KC;
   FSI_CHECK_ARG(K % KC == 0 && (nc == 1 || nc == 2 || nc == 4 || nc == 8 || nc == 16 || nc == 32), FSI_ERR_SHAPE,
                 "pattention_packed: K=%lld (256 x 1, 2, 4, ..., 32)", (long long)K);
@@ -510,9 +532,10 @@ int fsi_pattention_fwd_packed(const void* x, int64_t ldx, const void* packed, co
                 (long long)D_out, (long long)block_n);
   const int64_t n_ch = active_blocks ? n_active * block_n : N_p;
   FSI_CHECK_ARG(n_active >= 0 && n_ch >= 1, FSI_ERR_SHAPE, "pattention_packed: no active channel");
+  const bool prefill = M >= PK_PREFILL_MIN_M;
   const int ns = down_steps(n_ch);
-  FSI_CHECK_ARG(ns > 0, FSI_ERR_SHAPE, "pattention_packed: %lld active channels (at most %d)", (long long)n_ch,
-                PK_WAVES * 32 * 32);
+  FSI_CHECK_ARG(prefill || ns > 0, FSI_ERR_SHAPE, "pattention_packed: %lld active channels (at most %d)",
+                (long long)n_ch, PK_WAVES * 32 * 32);
   FSI_CHECK_ARG(ldx >= K && ldx % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldo >= D_out,
                 FSI_ERR_ALIGN, "pattention_packed: x must be 16-byte aligned with ldx %% 8 == 0");
   FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(packed) % 256 == 0 && reinterpret_cast<uintptr_t>(out) % 2 == 0,
@@ -521,11 +544,40 @@ int fsi_pattention_fwd_packed(const void* x, int64_t ldx, const void* packed, co
                 FSI_ERR_SHAPE, "pattention_packed: V too large");
   const int64_t n_blocks = N_p / block_n;
   const int64_t n_list = active_blocks ? n_active : n_blocks;
-  const size_t need = pk_workspace(n_ch, n_list);
+  FSI_CHECK_ARG(!prefill || n_list <= PK_PREFILL_MAX_BLOCKS, FSI_ERR_CAPACITY,
+                "pattention_packed: %lld blocks (prefill: at most %lld)", (long long)n_list,
+                (long long)PK_PREFILL_MAX_BLOCKS);
+  const size_t need = prefill ? pk_prefill_workspace(M, n_ch, n_list) : pk_workspace(n_ch, n_list);
   FSI_CHECK_ARG(workspace && workspace_bytes >= need && reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
                 FSI_ERR_WORKSPACE, "pattention_packed: workspace %zu < %zu (or misaligned)", workspace_bytes, need);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const PkLayout l = pk_layout(N_p, K, D_out);
+  if (prefill) {
+    char* ws = static_cast<char*>(workspace);
+    bf16_t* h = reinterpret_cast<bf16_t*>(ws + FSI_WORKSPACE_COUNTER_BYTES);
+    int32_t* ids = reinterpret_cast<int32_t*>(ws + FSI_WORKSPACE_COUNTER_BYTES +
+                                              align_up(sizeof(bf16_t) * static_cast<size_t>(M) * n_ch, 256));
+    if (active_blocks == nullptr) {
+      pk_iota_kernel<<<static_cast<unsigned>((n_blocks + 255) / 256), 256, 0, st>>>(ids, static_cast<int>(n_blocks));
+      active_blocks = ids;
+    }
+    const char* pbase = static_cast<const char*>(packed);
+    const bf16_t* pg = reinterpret_cast<const bf16_t*>(pbase + l.gate);
+    const bf16_t* pu = reinterpret_cast<const bf16_t*>(pbase + l.up);
+    const bf16_t* pd = reinterpret_cast<const bf16_t*>(pbase + l.down);
+    if (fsi_gemm::gateup_swiglu_packed(static_cast<const bf16_t*>(x), ldx, pg, pu, static_cast<int>(K / 32),
+                                       static_cast<int>(N_p), active_blocks, static_cast<int>(n_list),
+                                       static_cast<int>(block_n), static_cast<int>(M), static_cast<int>(K), rounding,
+                                       h, n_ch, err, st) != 0 ||
+        fsi_gemm::down_gather_packed(h, n_ch, pd, static_cast<int>(D_out / 16), static_cast<int>(block_n / 32),
+                                     static_cast<int>(N_p), active_blocks, static_cast<int>(n_list),
+                                     static_cast<int>(block_n), static_cast<int>(M), static_cast<int>(D_out),
+                                     static_cast<bf16_t*>(out), ldo, err, st) != 0) {
+      set_last_error("pattention_packed: prefill GEMM launch failed: %s", hipGetErrorString(hipGetLastError()));
+      return FSI_ERR_HIP;
+    }
+    return FSI_OK;
+  }
   const int64_t n_ch_pad = int64_t(PK_WAVES) * 32 * ns;
   char* ws = static_cast<char*>(workspace);
   bf16_t* hp = reinterpret_cast<bf16_t*>(ws + FSI_WORKSPACE_COUNTER_BYTES);

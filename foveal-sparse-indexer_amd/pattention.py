@@ -137,11 +137,21 @@ def _weights_key(*ts: Tensor) -> tuple:
     return tuple((t.data_ptr(), t._version, tuple(t.shape), tuple(t.stride())) for t in ts)
 
 
+PACKED_PREFILL_MIN_M = 256
+
+
 def packed_decode_supported(M: int, K: int, D_out: int, N_p: int, block_n: int, n_channels: int) -> bool:
-    """Shapes the packed decode kernels take (include/fsi.h, fsi_pattention_fwd_packed)."""
+    """Shapes fsi_pattention_fwd_packed takes (include/fsi.h): decode (1..64 tokens,
+    at most 8192 active channels) and prefill (256 tokens and more, at most 2048
+    active blocks)."""
     nc = K // 256
-    return (1 <= M <= 64 and K % 256 == 0 and nc in (1, 2, 4, 8, 16, 32) and D_out % 16 == 0 and block_n >= 32
-            and block_n & (block_n - 1) == 0 and N_p % block_n == 0 and 1 <= n_channels <= 8192)
+    common = (K % 256 == 0 and nc in (1, 2, 4, 8, 16, 32) and D_out % 16 == 0 and block_n >= 32
+              and block_n & (block_n - 1) == 0 and N_p % block_n == 0 and n_channels >= 1)
+    if not common:
+        return False
+    if 1 <= M <= 64:
+        return n_channels <= 8192
+    return M >= PACKED_PREFILL_MIN_M and n_channels // block_n <= 2048
 
 
 def pack_pattention_weights(k_gate: Tensor, k_up: Tensor, v: Tensor, block_n: int) -> PackedPattentionWeights:
@@ -180,9 +190,10 @@ def pattention_decode_packed(
     rounding: str = "fused",
     out: Optional[Tensor] = None,
 ) -> Tensor:
-    """SwiGLU Pattention of up to 64 bf16 tokens over packed weights: the same
-    result as pattention_forward(x2d, k_gate, k_up, v, active_blocks, block_n,
-    "swiglu", rounding) up to fp32 summation order."""
+    """SwiGLU Pattention of bf16 tokens over packed weights: the same result as
+    pattention_forward(x2d, k_gate, k_up, v, active_blocks, block_n, "swiglu",
+    rounding) up to fp32 summation order.  1..64 tokens run the decode kernels,
+    256 and more the prefill GEMMs reading the same packed tiles."""
     what = "pattention_decode_packed"
     dev = _lib.require_gpu(x2d, packed.buf, what=what)
     if x2d.dtype != torch.bfloat16:

@@ -58,6 +58,38 @@ def test_packed_decode_parity(fsi, dev, case):
         assert err <= BF16_TOL, (rounding, err)
 
 
+# prefill (>= 256 tokens): the 256 x 256 GEMMs over the packed tiles
+PREFILL_CASES = [
+    (256, 512, 2048, 304, 32, 21, True),      # 32-wide blocks, D_out not a multiple of 256
+    (300, 1024, 4096, 256, 64, 19, False),    # V row-major [N_p, D_out], partial row tile
+    (257, 256, 8192, 48, 64, 100, True),      # 6400 channels, one row past a tile
+    (1024, 1024, 4096, 512, 64, None, True),  # dense: no block list
+    (512, 2048, 16384, 640, 128, 40, True),   # 128-wide blocks
+]
+
+
+@pytest.mark.parametrize("case", PREFILL_CASES, ids=[f"p{i}" for i in range(len(PREFILL_CASES))])
+def test_packed_prefill_parity(fsi, dev, case):
+    test_packed_decode_parity(fsi, dev, case)
+
+
+def test_packed_prefill_bad_block_masked_and_reported(fsi, dev):
+    from foveal_sparse_indexer_amd import _lib
+
+    M, K, N_p, D_out, block_n = 300, 512, 1024, 256, 64
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    kg, ku, v = _weights(N_p, K, D_out, g, True)
+    pk = fsi.pack_pattention_weights(kg.to(dev), ku.to(dev), v.to(dev), block_n)
+    _lib.error_word(dev).zero_()
+    bad = torch.tensor([3, 99, 7, -1], dtype=torch.int32)
+    got = fsi.pattention_decode_packed(x.to(dev), pk, bad.to(dev), rounding="fp32").cpu()
+    ref = P.pattention_fp32_act(x, kg, v.contiguous(), ku, torch.tensor([3, 7]), "swiglu", block_n)
+    assert P.rel_l2(got, ref) <= BF16_TOL
+    assert int(_lib.error_word(dev)[0]) == _lib.FSI_ERR_INDEX_RANGE
+    _lib.error_word(dev).zero_()
+
+
 def test_packed_8b_decode_shape(fsi, dev):
     """C3a at full size: d_model 4096, 14336 parameter tokens, 8 base + 56 remote, batch 64."""
     print("[case] packed 8b decode shape", flush=True)
@@ -100,8 +132,9 @@ def test_packed_rejects_unsupported_shapes(fsi, dev):
         fsi.pattention_decode_packed(torch.randn(4, 320).bfloat16().to(dev), pk, None)
     kg, ku, v = _weights(1024, 256, 64, g, True)
     pk = fsi.pack_pattention_weights(kg.to(dev), ku.to(dev), v.to(dev), 64)
-    with pytest.raises(ValueError):  # more than 64 tokens
+    with pytest.raises(ValueError):  # between the decode (<= 64) and prefill (>= 256) ranges
         fsi.pattention_decode_packed(torch.randn(65, 256).bfloat16().to(dev), pk, None)
+    assert fsi.pattention_decode_packed(torch.randn(256, 256).bfloat16().to(dev), pk, None).shape == (256, 64)
 
 
 def test_module_decode_uses_packed_weights_and_repacks(fsi, dev):

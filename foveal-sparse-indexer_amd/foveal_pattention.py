@@ -120,10 +120,11 @@ class FovealPattentionMLP(nn.Module):
         self.register_buffer("offsets", torch.arange(block_size, dtype=torch.int64))
 
         self._cached_active_blocks: Optional[Tensor] = None
-        # Decode calls (up to 64 tokens, bf16) stream a copy of k_gate, k_up and v
-        # repacked into the MFMA operand layout, rebuilt whenever a weight tensor is
-        # replaced or modified in place.  It holds as many bytes as the three weights;
-        # set pack_decode_weights = False to decode from the parameters directly.
+        # Decode (up to 64 tokens) and prefill (256 tokens and more) calls in bf16
+        # stream a copy of k_gate, k_up and v repacked into the MFMA operand layout,
+        # rebuilt whenever a weight tensor is replaced or modified in place.  It holds
+        # as many bytes as the three weights; set pack_decode_weights = False to run
+        # from the parameters directly.
         self.pack_decode_weights = True
         self._packed: Optional[PackedPattentionWeights] = None
         self.reset_parameters()

@@ -118,10 +118,12 @@ FSI_API int fsi_pattention_fwd(const void* x, int64_t ldx, const void* k_gate, c
  * D_out % 16 == 0.
  *
  * fsi_pattention_fwd_packed: out[M, D_out] = (silu(x K_g,S^T) * (x K_u,S^T)) V_S
- * for 1 <= M <= 64 tokens, K = 256 * {1, 2, 4, 8, 16, 32}, at most 8192 active
- * channels; rounding as fsi_pattention_fwd.  Out-of-range block ids contribute
- * zero and are reported through err.  Workspace:
- * fsi_pattention_packed_workspace_size(M, K, D_out, n_channels, block_n).
+ * for K = 256 * {1, 2, 4, 8, 16, 32} and either 1 <= M <= 64 tokens (decode
+ * kernels, at most 8192 active channels) or M >= 256 (prefill: the 256 x 256
+ * GEMMs reading the same packed tiles, at most 2048 active blocks); rounding as
+ * fsi_pattention_fwd.  Out-of-range block ids contribute zero and are reported
+ * through err.  Workspace: fsi_pattention_packed_workspace_size(M, K, D_out,
+ * n_channels, block_n) (for prefill it holds H [M, n_channels]).
  * ------------------------------------------------------------------------- */
 FSI_API size_t fsi_pattention_packed_size(int64_t N_p, int64_t K, int64_t D_out);
 

@@ -841,7 +841,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) bf16_t lds[DSTAGES][2][BM * DK];  // [stage][A/B][row * 32 + k]
   __shared__ int32_t ktab[KM == K_GATHER_B ? KTAB_MAX : 1];
   const int tid = threadIdx.x;
-  if (KM == K_GATHER_B) {
+  if (KM == K_GATHER_B && !PB) {  // packed B reads the block ids from global memory
     fill_ktab(g, ktab, DTHREADS);
     __syncthreads();
   }
@@ -930,8 +930,12 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   const int per = KM == K_GATHER_B ? g.block / DK : 1;
   auto kt_load = [&](int c) {
     const int e = 64 * c + lane;
-    const int col = e < g.n_blocks ? ktab[e] : -1;
-    return PB ? (col < 0 ? -1 : col / g.block) : col;
+    if (PB) {  // block ids straight from global memory: an LDS read here would make the
+               // compiler wait for every direct-to-LDS load before each fragment read
+      const int blk = e < g.n_blocks ? (g.blocks ? g.blocks[e] : e) : -1;
+      return blk >= 0 && static_cast<int64_t>(blk + 1) * g.block <= g.n_rows_total ? blk : -1;
+    }
+    return e < g.n_blocks ? ktab[e] : -1;
   };
   int iss_blk = 0, iss_sub = 0, kt_cur = 0, kt_next = 0;
   if (KM == K_GATHER_B) {

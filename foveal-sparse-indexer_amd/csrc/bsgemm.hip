@@ -412,8 +412,7 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
             for (int j = 0; j < 4; ++j)
               e += energy_term(acc[i][0][j], acc[i][2][j], R) + energy_term(acc[i][1][j], acc[i][3][j], R);
           }
-          e += __shfl_xor(e, 16);
-          e += __shfl_xor(e, 32);
+          e = sum_rows4(e);
           const int m = crow + 16 * i;
           if (fchunk == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
         }
@@ -1140,8 +1139,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
             for (int j = 0; j < 4; ++j)
               e += energy_term(acc[i][0][j], acc[i][2][j], R) + energy_term(acc[i][1][j], acc[i][3][j], R);
           }
-          e += __shfl_xor(e, 16);
-          e += __shfl_xor(e, 32);
+          e = sum_rows4(e);
           const int m = crow + 16 * i;
           if (fchunk == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
         }

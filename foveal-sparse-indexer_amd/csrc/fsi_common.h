@@ -94,6 +94,27 @@ __device__ __forceinline__ float pattention_act(float g, float u, int rounding) 
 }
 
 // ---------------------------------------------------------------------------
+// Sum / max over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four row groups of a
+// 16 x 16 MFMA result column) with gfx950's v_permlane16_swap / v_permlane32_swap.
+// Each swap leaves a lane's own value in one output and its partner's in the
+// other, so combining the two outputs reduces a pair.  VALU only: a shuffle that
+// compiles to ds_bpermute is an LDS instruction, and in a kernel with
+// direct-to-LDS loads in flight the compiler waits for all of them before it.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sum_rows4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float max_rows4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// ---------------------------------------------------------------------------
 // Wave-level reductions (64 lanes).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {

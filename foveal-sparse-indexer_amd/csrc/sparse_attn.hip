@@ -228,8 +228,7 @@ __global__ __launch_bounds__(64 * SA_WAVES) void sparse_attn_kernel(SAParams P) 
           sv[tile * 4 + j] = v;
           mx = fmaxf(mx, v);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = max_rows4(mx);
       const float m_new = fmaxf(m_run, mx);
       float alpha = 1.f, psum = 0.f;
       uint32_t pk_hi[4], pk_lo[4];
@@ -252,8 +251,7 @@ __global__ __launch_bounds__(64 * SA_WAVES) void sparse_attn_kernel(SAParams P) 
           pk_lo[w] = pack_bf16x2(plo[2 * w], plo[2 * w + 1]);
         }
       }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
+      psum = sum_rows4(psum);
       l_run = l_run * alpha + psum;
       m_run = m_new;
       const u32x4_t pbh = u32x4_t{pk_hi[0], pk_hi[1], pk_hi[2], pk_hi[3]};
@@ -340,10 +338,17 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   constexpr int LPW = LOADS / SAL_WAVES;        // per wave
   static_assert(LOADS % SAL_WAVES == 0, "chunk loads must split over the waves");
   constexpr int KPR = KROW / 16;                // 16-byte pieces per key row
-  __shared__ __attribute__((aligned(1024))) char ring[SAL_STAGES][STAGE];
-  // Q^T operand tiles of each wave, (query tile, k-step) KiB in lane order
-  __shared__ __attribute__((aligned(1024))) char qlds[SAL_WAVES][SAL_QT * KS * 1024];
-  __shared__ int wl[SAL_MAX_CAP];
+  // One LDS array holds the chunk ring, the Q^T operand tiles of each wave
+  // ((query tile, k-step) KiB in lane order) and the block list.  Separate
+  // __shared__ arrays would get alias scopes, and the compiler would then make
+  // every ring read wait for all direct loads in flight (vmcnt(0)), including the
+  // chunks issued ahead; with one array the explicit waits below order the ring.
+  constexpr int QBYTES = SAL_QT * KS * 1024;
+  __shared__ __attribute__((aligned(1024))) char smem[SAL_STAGES * STAGE + SAL_WAVES * QBYTES +
+                                                      SAL_MAX_CAP * 4];
+  char (*ring)[STAGE] = reinterpret_cast<char (*)[STAGE]>(smem);
+  char (*qlds)[QBYTES] = reinterpret_cast<char (*)[QBYTES]>(smem + SAL_STAGES * STAGE);
+  int* wl = reinterpret_cast<int*>(smem + SAL_STAGES * STAGE + SAL_WAVES * QBYTES);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -392,6 +397,10 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   const int pb_shift = __builtin_ctz(per_block);
   const int n_chunks = n_local + n_remote * per_block;
   __syncthreads();  // wl is written
+  // Each wave keeps the page list in a register (lane i holds entry i) and reads it
+  // with v_readlane: an LDS read inside the chunk loop would make the compiler wait
+  // for every direct-to-LDS chunk load in flight before the loop's LDS reads.
+  const int wl_reg = wl[lane < SAL_MAX_CAP ? lane : 0];
 
   // chunk i: absolute chunk c, keys [0, hi) of it, local-window chunk or page chunk
   auto describe = [&](int i, int& c, int& hi, bool& local) {
@@ -401,7 +410,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
       local = true;
     } else {
       const int j = i - n_local;
-      const int blk = __builtin_amdgcn_readfirstlane(wl[j >> pb_shift]);
+      const int blk = __builtin_amdgcn_readlane(wl_reg, j >> pb_shift);
       const int k0 = blk * P.block;
       const int k1 = k0 + P.block < P.T ? k0 + P.block : P.T;
       c = k0 / SA_CHUNK + (j & (per_block - 1));
@@ -565,8 +574,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
           }
       }
       float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = max_rows4(mx);
       // The running max (log2 units) moves only when a score exceeds it by more
       // than 8: P then stays below 2^8 and the accumulators are rescaled rarely.
       const float m_cand = mx * P.scale_log2;
@@ -585,8 +593,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
         pk_hi[w] = cvt_pk_bf16(p0, p1);
         pk_lo[w] = cvt_pk_bf16(p0 - lo_bf16(pk_hi[w]), p1 - hi_bf16(pk_hi[w]));
       }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
+      psum = sum_rows4(psum);
       l_run[qt] = l_run[qt] * alpha[qt] + psum;
       m_run[qt] = m_new;
       pbh[qt] = u32x4_t{pk_hi[0], pk_hi[1], pk_hi[2], pk_hi[3]};

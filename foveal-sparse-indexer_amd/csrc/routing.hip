@@ -525,6 +525,58 @@ __device__ __forceinline__ float dr_block_sum(float v, float* red) {
   return r;
 }
 
+// Wave sums of 16 per-lane values, scattered over the lanes: lane l returns the
+// sum over the wave of v[which], and the four lanes of each quad share one
+// `which`.  Cross-lane steps are VALU permutes (permlane32 / permlane16 swaps,
+// then DPP row mirrors and quad permutes), each halving the values a lane
+// carries: 17 exchanges in all instead of 16 butterfly sums of 6 LDS permutes.
+// The channel each lane ends up with is found by passing labels through the
+// same swaps.
+__device__ __forceinline__ float dpp_f(float x, int ctrl) {
+  switch (ctrl) {  // the DPP control must be a compile-time constant
+    case 0x140: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF, false));
+    case 0x141: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, false));
+    case 0xB1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+    default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));
+  }
+}
+__device__ __forceinline__ float dr_wave_sum16_scatter(const float (&v)[16], int& which) {
+  const int lane = lane_id();
+  // lanes l and l ^ 32: value c stays in one half, c + 8 in the other
+  float a[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[c]), __float_as_uint(v[c + 8]), false, false);
+    a[c] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  }
+  const int l32 = static_cast<int>(__builtin_amdgcn_permlane32_swap(0u, 8u, false, false)[0]);
+  // lanes l and l ^ 16: c and c + 4
+  float b[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[c]), __float_as_uint(a[c + 4]), false, false);
+    b[c] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  }
+  const int l16 = static_cast<int>(__builtin_amdgcn_permlane16_swap(0u, 4u, false, false)[0]);
+  // row mirror (i <-> 15 - i): lanes with bit 3 set keep c + 2
+  const bool up8 = (lane & 8) != 0;
+  float d[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const float keep = up8 ? b[c + 2] : b[c];
+    const float give = up8 ? b[c] : b[c + 2];
+    d[c] = keep + dpp_f(give, 0x140);
+  }
+  // half-row mirror (i <-> 7 - i): lanes with bit 2 set keep c + 1
+  const bool up4 = (lane & 4) != 0;
+  float e = (up4 ? d[1] : d[0]) + dpp_f(up4 ? d[0] : d[1], 0x141);
+  // the four lanes of a quad hold parts of the same value
+  e += dpp_f(e, 0xB1);
+  e += dpp_f(e, 0x4E);
+  which = l32 + l16 + (up8 ? 2 : 0) + (up4 ? 1 : 0);
+  return e;
+}
+
 // Sum of the DR_WAVES per-wave words at w (16-byte aligned), read as four
 // 16-byte vectors (every lane reads the same words: broadcast reads).
 __device__ __forceinline__ int dr_sum16(const int* w) {
@@ -747,11 +799,9 @@ __global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __
           }
         }
       }
-#pragma unroll
-      for (int c = 0; c < SR_D; ++c) {
-        const float t = wave_sum(part[c]);
-        if (lane == 0) ctx_part[wave][c] = t;
-      }
+      int which;
+      const float t = dr_wave_sum16_scatter(part, which);
+      if ((lane & 3) == 0) ctx_part[wave][which] = t;
       __syncthreads();
       if (threadIdx.x < SR_D) {
 #pragma unroll

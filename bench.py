@@ -200,22 +200,35 @@ def bench_routing(fsi, args, dev):
     return res
 
 
-def bench_decode_attn(fsi, args, dev):
-    B, HQ, HKV, HD, CTX, PAGE, W, KMAX, TOP_P = 32, 32, 8, 128, 131072, 64, 1024, 32, 0.9
-    P = CTX // PAGE
-    n_phys = 65536
+C4 = dict(B=32, HQ=32, HKV=8, HD=128, CTX=131072, PAGE=64, W=1024, KMAX=32, TOP_P=0.9, N_PHYS=65536)
+
+
+def c4_inputs(fsi, dev):
+    """C4 decode attention inputs: a 65536-page K/V pool (N(0,1), 16 GiB), a seeded
+    random page table, normalised fp32 page keys, bf16 q and rms-normed 16-D query."""
+    c = C4
+    B, P = c["B"], c["CTX"] // c["PAGE"]
     g = torch.Generator(device=dev).manual_seed(0)
-    table = torch.randperm(n_phys, device=dev, generator=g)[:B * P].view(B, P).to(torch.int32)
-    cache = fsi.FovealKVCache(B, CTX, HKV, HD, 16, PAGE, dev, torch.bfloat16, n_phys_pages=n_phys, page_table=table)
+    table = torch.randperm(c["N_PHYS"], device=dev, generator=g)[:B * P].view(B, P).to(torch.int32)
+    cache = fsi.FovealKVCache(B, c["CTX"], c["HKV"], c["HD"], 16, c["PAGE"], dev, torch.bfloat16,
+                              n_phys_pages=c["N_PHYS"], page_table=table)
     # pools filled in place: every page holds N(0,1) keys and values
     cache.k_cache.normal_(generator=g)
     cache.v_cache.normal_(generator=g)
     cache.kp_cache.copy_(torch.nn.functional.normalize(torch.randn(B, P, 16, device=dev, generator=g), dim=-1))
     cache.vp_cache.normal_(generator=g)
-    cache.seq_len, cache.completed_pages = CTX, P
-    pos = CTX - 1
-    q = torch.randn(B, HQ, HD, device=dev, generator=g).bfloat16()
+    cache.seq_len, cache.completed_pages = c["CTX"], P
+    q = torch.randn(B, c["HQ"], c["HD"], device=dev, generator=g).bfloat16()
     qi = torch.nn.functional.rms_norm(torch.randn(B, 16, device=dev, generator=g), (16,)).bfloat16()
+    return cache, q, qi
+
+
+def bench_decode_attn(fsi, args, dev):
+    B, HQ, HKV, HD, CTX, PAGE, W, KMAX, TOP_P = (C4[k] for k in ("B", "HQ", "HKV", "HD", "CTX", "PAGE", "W", "KMAX",
+                                                                 "TOP_P"))
+    P = CTX // PAGE
+    cache, q, qi = c4_inputs(fsi, dev)
+    pos = CTX - 1
     scale = 1.0 / (HD ** 0.5)
     outs = {}
 
@@ -354,19 +367,36 @@ def bench_prefill_attn(fsi, args, dev):
     return res
 
 
-def bench_block_sparse(fsi, args, dev):
-    M, K, N, T = 4096, 8192, 8192, 128
-    groups, nkb, nnb = M // T, K // T, N // T
+C5 = dict(M=4096, K=8192, N=8192, T=128, DENSITIES=(0.10, 0.25, 0.50))
+
+
+def c5_inputs(dev):
+    """C5 inputs: X N(0,1) (4096, 8192) and W N(0, 0.01^2) (8192, 8192) bf16, plus
+    seeded uniform tile scores per 128-row group (32 x 4096 tiles)."""
+    M, K, N, T = C5["M"], C5["K"], C5["N"], C5["T"]
     g = torch.Generator(device=dev).manual_seed(0)
     x = torch.randn(M, K, device=dev, generator=g).bfloat16()
     w = (torch.randn(N, K, device=dev, generator=g) * 0.01).bfloat16()
-    scores = torch.rand(groups, nkb * nnb, device=dev, generator=g)
+    scores = torch.rand(M // T, (K // T) * (N // T), device=dev, generator=g)
+    return x, w, scores
+
+
+def c5_mask(scores, density: float):
+    """Per-row-group tile masks: the top ceil(density x tiles) tiles of each group's scores."""
+    groups, tiles = scores.shape
+    n_tiles = int(-(-density * tiles // 1))
+    mask = torch.zeros(groups, tiles, dtype=torch.bool, device=scores.device)
+    mask.scatter_(1, scores.topk(n_tiles, dim=1).indices, True)
+    return mask, n_tiles
+
+
+def bench_block_sparse(fsi, args, dev):
+    M, K, N, T = C5["M"], C5["K"], C5["N"], C5["T"]
+    groups, nkb, nnb = M // T, K // T, N // T
+    x, w, scores = c5_inputs(dev)
     lines = {}
-    for d in (0.10, 0.25, 0.50):
-        n_tiles = int(-(-d * nkb * nnb // 1))
-        top = scores.topk(n_tiles, dim=1).indices
-        mask = torch.zeros(groups, nkb * nnb, dtype=torch.bool, device=dev)
-        mask.scatter_(1, top, True)
+    for d in C5["DENSITIES"]:
+        mask, n_tiles = c5_mask(scores, d)
         outs = {}
 
         def step(i):
@@ -375,18 +405,27 @@ def bench_block_sparse(fsi, args, dev):
         t, _ = time_graph(step, args.steps, args.warmup, dev)
         per = t / args.steps
         flops = groups * n_tiles * 2 * T * T * T
-        lines[d] = (per, flops, n_tiles)
-    per, flops, n_tiles = lines[0.25]
+        # HBM floor: X and Y once plus every weight tile some group uses
+        hbm = 2 * M * K * 2 + int(mask.any(dim=0).sum()) * T * T * 2
+        lines[d] = (per, flops, n_tiles, hbm)
+    per, flops, n_tiles, _ = lines[0.25]
     tf = flops / per / 1e12
+
+    def grade(v):
+        per_d, fl, nt, hbm = v
+        tfs, gbs = fl / per_d / 1e12, hbm / per_d / 1e9
+        # the bound is whichever floor is longer: MFMA time or HBM time
+        bound = "mfma" if fl / (BF16_PEAK_TFLOPS * 1e12) >= hbm / (HBM_PEAK_GBS * 1e9) else "hbm"
+        return {"ms_per_step": round(per_d * 1e3, 4), "tiles_per_group": nt, "tflops": round(tfs, 2),
+                "hbm_bytes": hbm, "gbs": round(gbs, 1), "bound": bound,
+                "frac": round(tfs / BF16_PEAK_TFLOPS if bound == "mfma" else gbs / HBM_PEAK_GBS, 4)}
+
     res = _result("2-D tile-sparse matmul TFLOP/s (per-row-group 128x128 tile masks)", round(tf, 2), "TFLOP/s",
                   args.steps, args.warmup, round(per * 1e3, 6), "bf16",
                   "synthetic (seeded N(0,1) X, N(0,0.01) W, per-row-group top-d tiles of seeded uniform scores)",
                   {"workload": "C5: X 4096 x 8192, W 8192 x 8192 in 128 x 128 tiles (4096), one mask per 128-row "
                                "group (32 groups), density 25% (1024 tiles per group)",
-                   "densities": {f"{d:.2f}": {"ms_per_step": round(v[0] * 1e3, 4), "tiles_per_group": v[2],
-                                             "tflops": round(v[1] / v[0] / 1e12, 2),
-                                             "frac_mfma": round(v[1] / v[0] / 1e12 / BF16_PEAK_TFLOPS, 4)}
-                                 for d, v in lines.items()}})
+                   "densities": {f"{d:.2f}": grade(v) for d, v in lines.items()}})
     res["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                        "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
                        "kernel": "bsgemm_kernel<N_DIRECT, K_LIST> (+3 small list-building launches)",
@@ -397,9 +436,7 @@ def bench_block_sparse(fsi, args, dev):
         from oracle import blocksparse as BS
 
         # masked dense matmul on the host for one 128-row group at 25% density
-        top = scores.topk(n_tiles, dim=1).indices
-        mask = torch.zeros(groups, nkb * nnb, dtype=torch.bool, device=dev)
-        mask.scatter_(1, top, True)
+        mask, n_tiles = c5_mask(scores, 0.25)
         xc, wc = x[:T].cpu(), w.cpu()
         em = BS.expand_tile_mask(mask[0].cpu(), N, K, T, T)
         ts = []
@@ -473,6 +510,8 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=16)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="only the C3 line (skip the C2 / C4 / C5 / prefill-attention sub-objects)")
     ap.add_argument("--workload", default="pattention",
                     choices=["pattention", "routing", "decode_attn", "prefill_attn", "block_sparse",
                              "teacher_targets"])
@@ -603,6 +642,28 @@ def main():
             "sample": f"oracle torch-CPU restatement of the eval forward (gather + 3 F.linear + fused SwiGLU), "
                       f"decode batch 64 on layer 0, median of 7 after 2 warm-ups, {med * 1e3:.1f} ms/step",
         }
+        if "prefill" in result:
+            med_p, _ = cpu_baseline(layer_cpu, x_pre.reshape(-1, D_MODEL).cpu(), act, reps=3)
+            result["prefill"]["cpu_baseline"] = {
+                "value": round(PREFILL_TOKENS / med_p, 1), "unit": "tok/s", "cores": cores, "kind": "port",
+                "sample": f"oracle torch-CPU restatement of the eval forward on the full 4096-token prefill of layer "
+                          f"0, median of 3 after 2 warm-ups, {med_p * 1e3:.1f} ms/step"}
+    del layers, outs
+    torch.cuda.empty_cache()
+
+    if not args.no_workloads:
+        # The other SURVEY configs, each one JSON sub-object with its own roofline and CPU baseline.
+        sub_args = argparse.Namespace(**vars(args))
+        sub_args.steps, sub_args.warmup = max(1, min(args.steps, 20)), max(1, min(args.warmup, 3))
+        result["workloads"] = {}
+        for name, fn in (("C2_routing", bench_routing), ("C4_decode_attention", bench_decode_attn),
+                         ("C5_block_sparse", bench_block_sparse), ("prefill_attention", bench_prefill_attn)):
+            with torch.no_grad():
+                r = fn(fsi, sub_args, dev)
+            result["workloads"][name] = {k: r[k] for k in ("metric", "value", "unit", "steps", "ms_per_step",
+                                                           "dtype", "config", "roofline", "cpu_baseline") if k in r}
+            torch.cuda.empty_cache()
+            print(f"bench: {name} {r['value']} {r['unit']}", file=sys.stderr, flush=True)
     print(json.dumps(result), flush=True)
 
 

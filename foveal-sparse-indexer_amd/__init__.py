@@ -14,6 +14,7 @@ from .pattention import (
     PackedPattentionWeights,
     dense_block_targets,
     fused_swiglu,
+    is_triton_available,
     pack_pattention_weights,
     pattention_decode_packed,
     pattention_forward,
@@ -42,6 +43,7 @@ from .block_matmul import (
     BlockwiseMatMul2D,
     block_sparse_linear,
     blockwise_matmul,
+    tile_route,
     triton_block_sparse_linear,
 )
 from .foveal_pattention import (
@@ -65,6 +67,7 @@ __all__ = [
     "BlockwiseMatMul2D",
     "block_sparse_linear",
     "blockwise_matmul",
+    "tile_route",
     "triton_block_sparse_linear",
     "decode_attention",
     "sparse_attention",
@@ -88,4 +91,5 @@ __all__ = [
     "convert_llm_mlp_to_pattention",
     "HAS_HIP",
     "HAS_TRITON",
+    "is_triton_available",
 ]

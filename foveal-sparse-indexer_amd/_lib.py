@@ -118,6 +118,17 @@ SIGNATURES: dict[str, tuple] = {
         [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_size,
          _c_ptr],
     ),
+    "fsi_distill_kl_workspace_size": (_c_size, [_c_i64, _c_i64]),
+    "fsi_distill_kl_fwd": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_i64, _c_i64, _c_i64,
+         ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr],
+    ),
+    "fsi_distill_kl_bwd": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_i64, _c_i64, _c_i64,
+         ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
+    ),
     "fsi_kv_write": (
         _c_int,
         [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr,
@@ -151,6 +162,10 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
          _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr],
+    ),
+    "fsi_tile_route": (
+        _c_int,
+        [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
     ),
 }
 

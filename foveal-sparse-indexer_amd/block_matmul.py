@@ -5,8 +5,8 @@ The GEMMs run on the HIP block-sparse MFMA engine (csrc/bsgemm.hip): active
 column blocks (BlockSparseLinear) or active 2-D tiles (BlockwiseMatMul2D) are
 read straight from the full weight, no gathered copies.  BlockSparseLinear's
 routing (16-D scores, per-token top-p, union of blocks) runs in the HIP routing
-kernels; BlockwiseMatMul2D's tile routing is evaluated with torch ops on the
-GPU.  bf16 only; inference only (the HIP ops have no backward).
+kernels; BlockwiseMatMul2D's tile routing (per-token top-p over all tiles, union
+mask) runs in the HIP tile router (csrc/tile_route.hip).
 """
 from __future__ import annotations
 
@@ -95,6 +95,36 @@ def blockwise_matmul(x2d: Tensor, weight: Tensor, tile_mask: Tensor, block_k: in
                                 ws.data_ptr(), ws.numel(), stream)
     _lib.check(st, what)
     return out
+
+
+def tile_route(scores: Tensor, top_p: float, base_tiles: int, rows_per_group: Optional[int] = None):
+    """BlockwiseMatMul2D's tile selection (block_matmul.py:364-377) on the HIP
+    router (fsi_tile_route): per token row, softmax over all tiles, the tiles
+    whose sorted running mass stays below top_p plus the one that crosses it
+    (no K_min, no K_max), and the union over rows with tiles [0, base_tiles).
+
+    scores: (rows, T) fp32 or bf16.  rows_per_group: one union per group of that
+    many consecutive rows (None: one union over all rows, as the reference).
+    Returns (mask (groups, T) bool, probs (rows, T) in the scores' dtype,
+    needed (rows,) int32)."""
+    what = "tile_route"
+    dev = _lib.require_gpu(scores, what=what)
+    code = _lib.dtype_code(scores.dtype, what)
+    if scores.dim() != 2:
+        raise ValueError(f"{what}: scores must be (rows, tiles), got {tuple(scores.shape)}")
+    if scores.stride(1) != 1:
+        scores = scores.contiguous()
+    rows, T = scores.shape
+    rpg = max(rows, 1) if rows_per_group is None else int(rows_per_group)
+    groups = max(1, -(-rows // rpg)) if rows else 1
+    mask = torch.empty((groups, T), dtype=torch.uint8, device=dev)
+    probs = torch.empty((rows, T), dtype=scores.dtype, device=dev)
+    needed = torch.empty((rows,), dtype=torch.int32, device=dev)
+    st = _lib.lib().fsi_tile_route(scores.data_ptr() if rows else None, code, rows, T, max(scores.stride(0), T), rpg,
+                                   int(base_tiles), float(top_p), mask.data_ptr(), needed.data_ptr() if rows else None,
+                                   probs.data_ptr() if rows else None, _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return mask.view(torch.bool), probs, needed
 
 
 def _eval_active_blocks(block_scores: Tensor, base_blocks: int, top_p: float, max_remote: int, num_blocks: int):
@@ -325,16 +355,8 @@ class BlockwiseMatMul2D(nn.Module):
         # plain 2-D products with contiguous operands (no batched bf16 product on a transposed view)
         scores = (q_16d.reshape(-1, self.index_dim) @ tile_k.t().contiguous()).view(batch, seq_len, -1)
         scores = scores / math.sqrt(self.index_dim)
-        probs = F.softmax(scores, dim=-1)
-        sorted_probs, sorted_indices = probs.sort(dim=-1, descending=True)
-        cumulative = sorted_probs.cumsum(dim=-1)
-        needed = ((cumulative < self.top_p).sum(dim=-1) + 1).clamp_max(self.total_tiles)
-        slot = torch.arange(self.total_tiles, device=x.device).view(1, 1, -1)
-        chosen = sorted_indices[slot < needed[..., None]]
-        mask = torch.zeros(self.total_tiles, dtype=torch.bool, device=x.device)
-        mask[: self.base_tiles] = True
-        mask[chosen] = True
-        return mask, probs, scores, tile_v
+        mask, probs, _ = tile_route(scores.detach().reshape(-1, self.total_tiles), self.top_p, self.base_tiles)
+        return mask[0], probs.view(batch, seq_len, -1), scores, tile_v
 
     def forward(self, x: Tensor, compute_teacher_loss: bool = False) -> Tuple[Tensor, Dict[str, Any]]:
         batch, seq_len, _ = x.shape

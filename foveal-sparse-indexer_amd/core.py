@@ -25,7 +25,6 @@ from dataclasses import dataclass
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import _lib
@@ -330,28 +329,73 @@ class FovealIndexer(nn.Module):
         teacher_block_mass: Tensor,
         valid_mask: Optional[Tensor] = None,
     ) -> Tensor:
-        """Block-level KL loss against teacher mass (core.py:314-353).  A
-        training objective, evaluated with autograd-capable torch ops."""
+        """Block-level KL loss of the student scores against the teacher block
+        mass (core.py:315-353), on the fused HIP kernels of csrc/distill.hip:
+        a masked log-softmax cross-entropy against the teacher mass renormalised
+        over the valid blocks (uniform when that mass vanishes), averaged over
+        the rows that have a valid block.  Without `valid_mask` the valid set is
+        the causal set (key block < query block) or every block.  Differentiable
+        in the student scores (the teacher is a constant target)."""
+        what = "distillation_loss"
+        s = student_scores
+        if s.dim() != 3:
+            raise ValueError(f"{what}: expected (B, Q_blocks, total_blocks) scores, got {tuple(s.shape)}")
+        dev = _lib.require_gpu(s, teacher_block_mass, valid_mask, what=what)
+        t = teacher_block_mass
+        if t.dtype not in (torch.float32, torch.bfloat16):
+            t = t.float()
+        t = torch.broadcast_to(t, s.shape).contiguous()
         if valid_mask is None:
-            if self.causal:
-                _, qb_len, pb_len = student_scores.shape
-                qb = torch.arange(qb_len, device=student_scores.device)
-                pb = torch.arange(pb_len, device=student_scores.device)
-                valid_mask = (pb.view(1, pb_len) < qb.view(qb_len, 1))[None].expand_as(student_scores)
-            else:
-                valid_mask = torch.ones_like(student_scores, dtype=torch.bool)
-        masked = student_scores.masked_fill(~valid_mask, -float("inf"))
-        log_student = F.log_softmax(masked.float() / self.distill_temperature, dim=-1)
-        log_student = torch.where(valid_mask, log_student, torch.zeros_like(log_student))
-        teacher = teacher_block_mass.float().clamp_min(0.0).masked_fill(~valid_mask, 0.0)
-        denom = teacher.sum(dim=-1, keepdim=True)
-        uniform = valid_mask.float() / valid_mask.float().sum(dim=-1, keepdim=True).clamp_min(1.0)
-        target = torch.where(denom > 1e-12, teacher / denom.clamp_min(1e-12), uniform)
-        kl = -(target.detach() * log_student).sum(dim=-1)
-        has_valid = valid_mask.any(dim=-1)
-        if has_valid.any():
-            return kl[has_valid].mean()
-        return student_scores.sum() * 0.0
+            mode, m8 = (1 if self.causal else 0), None
+            no_rows = self.causal and s.shape[1] <= 1
+        else:
+            mode = 2
+            m8 = torch.broadcast_to(valid_mask.to(device=dev, dtype=torch.bool), s.shape).view(torch.uint8)
+            no_rows = False
+        loss = _DistillKLFn.apply(s.contiguous(), t, mode, m8, float(self.distill_temperature))
+        if no_rows:
+            # no query block has a candidate: the reference returns scores.sum() * 0
+            return loss.to(s.dtype)
+        return loss
+
+
+class _DistillKLFn(torch.autograd.Function):
+    """fsi_distill_kl_fwd with fsi_distill_kl_bwd as the gradient in the scores."""
+
+    @staticmethod
+    def forward(ctx, s: Tensor, t: Tensor, mode: int, m8: Optional[Tensor], temperature: float) -> Tensor:
+        what = "distillation_loss"
+        dev = s.device
+        B, Q, N = s.shape
+        L = _lib.lib()
+        stream = _lib.stream_handle(dev)
+        loss = torch.empty((), dtype=torch.float32, device=dev)
+        n_rows = torch.empty(1, dtype=torch.int32, device=dev)
+        ws = _lib.workspace(dev, L.fsi_distill_kl_workspace_size(B, Q), stream)
+        ms = m8.stride() if m8 is not None else (0, 0, 0)
+        st = L.fsi_distill_kl_fwd(s.data_ptr(), _lib.dtype_code(s.dtype, what), t.data_ptr(),
+                                  _lib.dtype_code(t.dtype, what), B, Q, N, mode, _lib.ptr(m8), ms[0], ms[1], ms[2],
+                                  temperature, loss.data_ptr(), n_rows.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        _lib.check(st, what)
+        ctx.save_for_backward(s, t, m8, n_rows)
+        ctx.mode, ctx.temperature = mode, temperature
+        return loss
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        what = "distillation_loss backward"
+        s, t, m8, n_rows = ctx.saved_tensors
+        dev = s.device
+        B, Q, N = s.shape
+        ds = torch.empty_like(s)
+        g32 = g.detach().to(device=dev, dtype=torch.float32).reshape(1).contiguous()
+        ms = m8.stride() if m8 is not None else (0, 0, 0)
+        st = _lib.lib().fsi_distill_kl_bwd(s.data_ptr(), _lib.dtype_code(s.dtype, what), t.data_ptr(),
+                                           _lib.dtype_code(t.dtype, what), B, Q, N, ctx.mode, _lib.ptr(m8), ms[0],
+                                           ms[1], ms[2], ctx.temperature, g32.data_ptr(), n_rows.data_ptr(),
+                                           ds.data_ptr(), _lib.stream_handle(dev))
+        _lib.check(st, what)
+        return ds, None, None, None, None
 
 
 class _IndexRmsNormFn(torch.autograd.Function):

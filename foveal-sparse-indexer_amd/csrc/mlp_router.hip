@@ -61,6 +61,15 @@ __device__ __forceinline__ float ldval(const void* p, int64_t i) {
 constexpr int PR_THREADS = 1024;
 constexpr int PR_LDS_SCORES = 8192;
 
+// Order-preserving 32-bit key of a float for ranking: NaN -> 0xffffffff (above
+// +inf), -0 -> the key of +0, otherwise larger floats get larger keys.
+__device__ __forceinline__ uint32_t rank_key(float f) {
+  if (f != f) return 0xffffffffu;
+  if (f == 0.0f) f = 0.0f;
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 template <bool BF16>
 __global__ __launch_bounds__(PR_THREADS) void pooled_route(const float* __restrict__ xm, int D,
                                                            const void* __restrict__ wq, int index_dim,
@@ -113,11 +122,14 @@ __global__ __launch_bounds__(PR_THREADS) void pooled_route(const float* __restri
   }
   __syncthreads();
   // Rank among remote candidates: larger score first, ties broken by lower index.
+  // Scores compare through an order-preserving integer key in which NaN sorts
+  // above +inf (torch.topk ranks NaN largest) and -0 equals +0, so the ranks
+  // are a permutation and every output slot is written.
   for (int b = base_blocks + tid; b < n_blocks; b += PR_THREADS) {
-    const float s = sc[b];
+    const uint32_t s = rank_key(sc[b]);
     int rank = 0;
     for (int o = base_blocks; o < n_blocks; ++o) {
-      const float t = sc[o];
+      const uint32_t t = rank_key(sc[o]);
       rank += (t > s) || (t == s && o < b);
     }
     if (rank < remote_blocks) active[base_blocks + rank] = b;

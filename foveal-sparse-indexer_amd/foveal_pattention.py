@@ -26,6 +26,7 @@ from torch import Tensor, nn
 
 from . import _lib
 from .pattention import (
+    FusedSwiGLUFunction,
     PackedPattentionWeights,
     dense_block_targets,
     _weights_key,
@@ -80,6 +81,46 @@ def mlp_pooled_route(
     return active
 
 
+class _EvalPattentionFn(torch.autograd.Function):
+    """The eval-mode forward of FovealPattentionMLP with a gradient for its input.
+
+    The reference's eval path runs F.linear on detached copies of the active
+    rows (foveal_pattention.py:115-122, 278-288), so autograd reaches x but no
+    weight.  Forward: the HIP decode / prefill kernels.  Backward, for
+    h = act(g, u), g = x K_g,S^T, u = x K_u,S^T, y = h V_S:
+        dh = dy V_S^T;  (dg, du) = swiglu_bwd(dh, g, u);  dx = dg K_g,S + du K_u,S
+    with g, u recomputed, library GEMMs on the active rows and the HIP SwiGLU
+    backward kernel."""
+
+    @staticmethod
+    def forward(ctx, x_2d: Tensor, module: "FovealPattentionMLP", active_blocks: Tensor) -> Tensor:
+        ctx.module = module
+        ctx.save_for_backward(x_2d, active_blocks)
+        return module._eval_compute(x_2d, active_blocks)
+
+    @staticmethod
+    def backward(ctx, dy: Tensor):
+        m = ctx.module
+        x_2d, active_blocks = ctx.saved_tensors
+        idx = (active_blocks.view(-1, 1).to(torch.int64) * m.block_size + m.offsets).flatten()
+        kg = m.k_gate.detach().index_select(0, idx)
+        ku = m.k_up.detach().index_select(0, idx)
+        v = m.v.detach().index_select(0, idx)
+        g = F.linear(x_2d, kg)
+        u = F.linear(x_2d, ku)
+        dh = F.linear(dy.to(x_2d.dtype), v.t().contiguous())
+        dg, du = FusedSwiGLUFunction.backward(_SavedGU(g, u), dh)
+        dx = F.linear(dg, kg.t().contiguous()) + F.linear(du, ku.t().contiguous())
+        return dx, None, None
+
+
+class _SavedGU:
+    """Stand-in autograd context holding (g, u) for FusedSwiGLUFunction.backward."""
+
+    def __init__(self, g: Tensor, u: Tensor):
+        self.saved_tensors = (g.contiguous(), u.contiguous())
+
+
 class FovealPattentionMLP(nn.Module):
     """Foveal block-sparse SwiGLU Pattention layer (foveal_pattention.py:54-352)."""
 
@@ -120,6 +161,7 @@ class FovealPattentionMLP(nn.Module):
         self.register_buffer("offsets", torch.arange(block_size, dtype=torch.int64))
 
         self._cached_active_blocks: Optional[Tensor] = None
+        self._gathered: Optional[tuple] = None
         # Decode (up to 64 tokens) and prefill (256 tokens and more) calls in bf16
         # stream a copy of k_gate, k_up and v repacked into the MFMA operand layout,
         # rebuilt whenever a weight tensor is replaced or modified in place.  It holds
@@ -132,6 +174,52 @@ class FovealPattentionMLP(nn.Module):
     # -- cache state machine (foveal_pattention.py:108-122) -----------------
     def clear_cache(self) -> None:
         self._cached_active_blocks = None
+        self._gathered = None
+
+    def _gathered_rows(self, which: int) -> Optional[Tensor]:
+        """Contiguous detached copies of the active rows of (k_gate, k_up, v), made
+        only when a caller reads _cached_kg / _cached_ku / _cached_v (the kernels
+        never use them), memoised for the current active set."""
+        blocks = self._cached_active_blocks
+        if blocks is None:
+            return None
+        g = getattr(self, "_gathered", None)
+        if g is None or g[0] is not blocks:
+            idx = (blocks.view(-1, 1).to(torch.int64) * self.block_size + self.offsets).flatten()
+            g = (blocks, self.k_gate[idx].detach().contiguous(), self.k_up[idx].detach().contiguous(),
+                 self.v[idx].detach().contiguous())
+            self._gathered = g
+        return g[1 + which]
+
+    def _cache_attr_set(self, value) -> None:
+        # The reference's caches are plain attributes that callers reset with None
+        # to force re-routing (foveal_pattention.py:101-112); anything else is refused.
+        if value is not None:
+            raise AttributeError("the active-row caches are derived from the active block list; "
+                                 "use set_active_blocks() to change them")
+        self.clear_cache()
+
+    _cached_kg = property(lambda self: self._gathered_rows(0), _cache_attr_set)
+    _cached_ku = property(lambda self: self._gathered_rows(1), _cache_attr_set)
+    _cached_v = property(lambda self: self._gathered_rows(2), _cache_attr_set)
+
+    def invalidate_packed_weights(self) -> None:
+        """Drop the packed copy of k_gate / k_up / v; the next bf16 eval call repacks.
+        Needed after writing the weights through `.data` (such writes do not bump
+        the tensors' version counters, which is how in-place changes through the
+        parameters themselves are detected).  load_state_dict and module moves
+        call it."""
+        self._packed = None
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self.invalidate_packed_weights()
+        self._gathered = None
+        return super()._load_from_state_dict(*args, **kwargs)
+
+    def _apply(self, fn, *args, **kwargs):
+        self.invalidate_packed_weights()
+        self._gathered = None
+        return super()._apply(fn, *args, **kwargs)
 
     def set_active_blocks(self, active_blocks: Tensor) -> None:
         """Fix the active block list used by later eval calls until clear_cache()."""
@@ -142,6 +230,7 @@ class FovealPattentionMLP(nn.Module):
                 raise IndexError(f"active block index out of range [0, {self.num_blocks}): min {lo}, max {hi}")
         self._cached_active_blocks = active_blocks.reshape(-1).to(device=self.k_gate.device,
                                                                   dtype=torch.int32).contiguous()
+        self._gathered = None
 
     def reset_parameters(self) -> None:
         std = self.hidden_dim ** -0.5
@@ -261,6 +350,17 @@ class FovealPattentionMLP(nn.Module):
     def _rounding(self) -> str:
         return "fused" if self.use_fused_kernel else "eager"
 
+    def _eval_compute(self, x_2d: Tensor, active_blocks: Tensor) -> Tensor:
+        """y = (silu(x K_g,S^T) * (x K_u,S^T)) V_S over the active blocks S on the
+        HIP kernels: packed weights for bf16 decode / prefill shapes, the
+        parameters in place otherwise."""
+        with torch.no_grad():
+            if self._decode_packed(x_2d, active_blocks):
+                return pattention_decode_packed(x_2d, self._packed_weights(), active_blocks,
+                                                rounding=self._rounding())
+            return pattention_forward(x_2d, self.k_gate, self.k_up, self.v, active_blocks, self.block_size,
+                                      activation="swiglu", rounding=self._rounding())
+
     def _train_forward(self, x_2d: Tensor, orig_shape, return_router_info: bool):
         """Training forward (foveal_pattention.py:292-307, 328-342): per-token
         router scores, top-k of their token mean over the remote blocks, the
@@ -314,12 +414,10 @@ class FovealPattentionMLP(nn.Module):
                                       self.remote_blocks)
             self._cached_active_blocks = active
         active_blocks = self._cached_active_blocks
-        if self._decode_packed(x_2d, active_blocks):
-            out = pattention_decode_packed(x_2d, self._packed_weights(), active_blocks,
-                                           rounding=self._rounding()).reshape(*orig_shape)
+        if torch.is_grad_enabled() and x_2d.requires_grad:
+            out = _EvalPattentionFn.apply(x_2d, self, active_blocks).reshape(*orig_shape)
         else:
-            out = pattention_forward(x_2d, self.k_gate, self.k_up, self.v, active_blocks, self.block_size,
-                                     activation="swiglu", rounding=self._rounding()).reshape(*orig_shape)
+            out = self._eval_compute(x_2d, active_blocks).reshape(*orig_shape)
         if return_router_info:
             if fast:
                 return out, {"active_blocks": active_blocks}

@@ -21,6 +21,12 @@ HAS_HIP = _lib.LIB_PATH.exists()
 HAS_TRITON = HAS_HIP
 
 
+def is_triton_available() -> bool:
+    """The reference's GPU-kernel predicate (triton_ops.py:252-253): True when the
+    kernel library is built and a GPU is visible.  The kernels are HIP, not Triton."""
+    return HAS_HIP and torch.cuda.is_available()
+
+
 def _as_index_tensor(active_blocks, device: torch.device) -> Tensor:
     if isinstance(active_blocks, Tensor):
         t = active_blocks

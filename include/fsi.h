@@ -320,6 +320,29 @@ FSI_API int fsi_additive_context_bwd(const void* scores, const void* v_blocks, c
                                      int64_t B, int64_t Q, int64_t N, int64_t index_dim, int causal, void* dscores,
                                      void* dv_blocks, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Block-level KL distillation loss, FovealIndexer.distillation_loss
+ * (foveal_indexer/core.py:315-353).  Per row (b, q) with valid set V
+ * (mask_mode 0: every entry; 1: the causal set p < q; 2: mask[b, q, p] != 0,
+ * uint8 with element strides, 0 = broadcast):
+ *   target = max(t, 0) / sum_V max(t, 0) if that sum > 1e-12, else 1 / |V|;
+ *   row loss = -sum_V target * log_softmax_V(s / temperature).
+ * loss[0] (fp32, device) = mean of the row losses over rows with |V| > 0 (0 if
+ * none); n_rows[0] (device) = that row count.  scores, teacher: contiguous
+ * (B, Q, N) fp32 or bf16.  Workspace: fsi_distill_kl_workspace_size(B, Q) bytes. */
+FSI_API size_t fsi_distill_kl_workspace_size(int64_t B, int64_t Q);
+FSI_API int fsi_distill_kl_fwd(const void* scores, int s_dtype, const void* teacher, int t_dtype, int64_t B,
+                               int64_t Q, int64_t N, int mask_mode, const uint8_t* mask, int64_t mask_stride_b,
+                               int64_t mask_stride_q, int64_t mask_stride_n, float temperature, float* loss,
+                               int32_t* n_rows, void* workspace, size_t workspace_bytes, void* stream);
+/* Gradient of that loss with respect to the scores (the teacher takes none):
+ * dscores = dloss[0] / n_rows[0] * (softmax_V(z) * sum_V target - target) / temperature
+ * on valid entries of valid rows, 0 elsewhere, written in the scores' dtype.
+ * dloss and n_rows are device scalars (n_rows as the forward wrote it). */
+FSI_API int fsi_distill_kl_bwd(const void* scores, int s_dtype, const void* teacher, int t_dtype, int64_t B,
+                               int64_t Q, int64_t N, int mask_mode, const uint8_t* mask, int64_t mask_stride_b,
+                               int64_t mask_stride_q, int64_t mask_stride_n, float temperature, const float* dloss,
+                               const int32_t* n_rows, void* dscores, void* stream);
+
 /* ------------------------------------------------------------------------- *
  * Foveal paged-KV decode attention (foveal_indexer/attention.py:284-367).
  * Paged pools (bf16), page = 64 tokens of one sequence for all KV heads:
@@ -429,6 +452,21 @@ FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int6
                                  const uint8_t* tile_mask, int64_t groups, int64_t rows_per_group, int64_t block_k,
                                  int64_t block_n, int64_t M, int64_t N, int64_t K, int dtype, void* out, int64_t ldo,
                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* 2-D tile routing of BlockwiseMatMul2D (foveal_indexer/block_matmul.py:355-377).
+ * Per row r of scores (rows x n_tiles, row stride ld_scores, fp32 or bf16):
+ * p = softmax(row) (rounded to bf16 for bf16 rows), tiles ranked by p
+ * descending (equal p: lower tile id first), running mass summed in fp64 and
+ * compared after rounding to the row dtype, needed = min(#(cum < top_p) + 1,
+ * n_tiles) (no K_min, no K_max).  out_mask (groups x n_tiles uint8,
+ * groups = ceil(rows / rows_per_group)): 1 for tiles [0, base_tiles) and for
+ * every tile some row of the group selects, 0 elsewhere (rows_per_group >= rows
+ * gives the reference's single union mask).  out_needed (optional, rows
+ * int32) and out_probs (optional, rows x n_tiles contiguous, row dtype).
+ * n_tiles <= 4096. */
+FSI_API int fsi_tile_route(const void* scores, int dtype, int64_t rows, int64_t n_tiles, int64_t ld_scores,
+                           int64_t rows_per_group, int64_t base_tiles, float top_p, uint8_t* out_mask,
+                           int32_t* out_needed, void* out_probs, void* stream);
 
 #ifdef __cplusplus
 }

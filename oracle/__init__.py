@@ -21,6 +21,8 @@ How each function is pinned (see tests/test_oracle_*.py):
   routing.decode_route        brute force per sequence + reference invariant (tests/test_attention.py:37-62)
   indexer.*                   brute-force loops (rms_norm, block pooling, additive context) and
                               the cos / sqrt(d) closed form
+  indexer.distillation_loss   pure-Python brute force (oracle/brute.py), closed forms (teacher =
+                              student softmax -> entropy; zero teacher -> uniform target), gradcheck
   pattention.*                identity with dense SwiGLU in fp64 when every block is active, and
                               masked-dense SwiGLU for any active set
   attention.decode_attention_f64

@@ -72,3 +72,48 @@ def masks(qb, nb, causal, local_window_blocks):
 def topk_desc(values, k):
     """Indices of the k largest values, ties to the lower index."""
     return sorted(range(len(values)), key=lambda i: (-values[i], i))[:k]
+
+
+def distill_loss_rows(student, teacher, valid, temperature):
+    """Brute-force block KL loss (foveal_indexer/core.py:315-353) on nested
+    lists [row][block]: fp64 log-softmax of student / T over the valid blocks,
+    target = clamped teacher mass renormalised over them (uniform if it sums to
+    <= 1e-12), loss = mean over rows with a valid block of -sum target * logp.
+    Returns (loss, per-row losses or None for rows without a valid block)."""
+    rows = []
+    for s_row, t_row, v_row in zip(student, teacher, valid):
+        ids = [i for i, ok in enumerate(v_row) if ok]
+        if not ids:
+            rows.append(None)
+            continue
+        z = [s_row[i] / temperature for i in ids]
+        m = max(z)
+        lse = m + math.log(sum(math.exp(v - m) for v in z))
+        t = [max(t_row[i], 0.0) for i in ids]
+        mass = sum(t)
+        if mass > 1e-12:
+            tgt = [v / mass for v in t]
+        else:
+            tgt = [1.0 / len(ids)] * len(ids)
+        rows.append(-sum(w * (v - lse) for w, v in zip(tgt, z)))
+    kept = [r for r in rows if r is not None]
+    loss = sum(kept) / len(kept) if kept else 0.0
+    return loss, rows
+
+
+def tile_route_row(scores, top_p):
+    """Tiles one token row of BlockwiseMatMul2D selects (foveal_indexer/block_matmul.py:364-377),
+    spelled out: fp64 softmax, tiles ranked by (probability desc, tile asc), running
+    fp64 mass, count = #(running mass < top_p) + 1, capped at the tile count.
+    Returns the selected tile ids in rank order."""
+    m = max(scores)
+    e = [math.exp(s - m) for s in scores]
+    z = sum(e)
+    probs = [v / z for v in e]
+    ranked = sorted(range(len(scores)), key=lambda i: (-probs[i], i))
+    running, below = 0.0, 0
+    for i in ranked:
+        running += probs[i]
+        if running < top_p:
+            below += 1
+    return ranked[: min(below + 1, len(scores))]

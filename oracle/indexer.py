@@ -5,6 +5,7 @@ Restates with torch CPU ops, in the reference's order and dtypes:
   * compute_kv_blocks_16d      foveal_indexer/core.py:224-250
   * compute_block_scores       foveal_indexer/core.py:254-266
   * additive_stream context    foveal_indexer/core.py:288-310 (up to out_proj)
+  * distillation_loss          foveal_indexer/core.py:315-353
 The projections themselves (nn.Linear) are inputs here: the HIP path runs them
 as library GEMMs and these functions start from their outputs.
 Backward passes: torch autograd of these functions, as in the reference's
@@ -54,3 +55,33 @@ def additive_context(block_scores: Tensor, v_blocks: Tensor, causal: bool, acc: 
         valid = torch.ones(Qb, Nb, dtype=torch.bool)
     probs = masked_probs(block_scores, valid[None].expand(B, -1, -1), acc).to(v_blocks.dtype)
     return torch.bmm(probs, v_blocks)
+
+
+def distillation_loss(student: Tensor, teacher: Tensor, valid_mask: Tensor | None = None, causal: bool = True,
+                      temperature: float = 1.0, acc: torch.dtype = torch.float32) -> Tensor:
+    """FovealIndexer.distillation_loss (core.py:315-353): cross-entropy of the
+    teacher block mass (clamped at 0, zeroed outside the valid set, renormalised,
+    uniform over the valid set when its mass is <= 1e-12) against
+    log_softmax(student / T) over the valid set, averaged over query rows that
+    have a valid block.  valid_mask defaults to key block < query block (causal)
+    or everything.  Autograd of this restatement is the oracle gradient."""
+    B, Q, N = student.shape
+    if valid_mask is None:
+        if causal:
+            valid = torch.arange(N).view(1, N) < torch.arange(Q).view(Q, 1)
+        else:
+            valid = torch.ones(Q, N, dtype=torch.bool)
+        valid = valid[None].expand(B, Q, N)
+    else:
+        valid = torch.broadcast_to(valid_mask.bool(), (B, Q, N))
+    z = (student.to(acc) / temperature).masked_fill(~valid, float("-inf"))
+    logp = torch.where(valid, torch.log_softmax(z, dim=-1), torch.zeros((), dtype=acc))
+    t = torch.where(valid, teacher.to(acc).clamp(min=0.0), torch.zeros((), dtype=acc))
+    mass = t.sum(dim=-1, keepdim=True)
+    n_valid = valid.to(acc).sum(dim=-1, keepdim=True)
+    target = torch.where(mass > 1e-12, t / mass.clamp(min=1e-12), valid.to(acc) / n_valid.clamp(min=1.0))
+    per_row = -(target.detach() * logp).sum(dim=-1)
+    rows = valid.any(dim=-1)
+    if bool(rows.any()):
+        return per_row[rows].mean()
+    return student.sum() * 0.0

@@ -180,3 +180,28 @@ def decode_route(qi: Tensor, kp_cache: Tensor, pos: int, page_size: int, local_w
         out["pages"][b] = order[b, :need].tolist()
     out.update(probs=probs, sorted_probs=sp, cumulative=cum, scores=scores)
     return out
+
+
+def tile_route(scores: Tensor, top_p: float, base_tiles: int, rows_per_group: int | None = None) -> dict:
+    """BlockwiseMatMul2D tile selection (block_matmul.py:364-377) over token rows.
+
+    scores: (rows, T) in the module dtype.  probs = softmax (in that dtype), tiles
+    sorted by probability descending (stable: equal probabilities keep tile
+    order), cumulative mass with ATen's CPU cumsum, needed = #(cum < top_p) + 1
+    capped at T (no K_min / K_max), and the union of every row's first `needed`
+    tiles with tiles [0, base_tiles).  With rows_per_group, one union per group
+    of consecutive rows (the reference has a single group).
+    Returns mask (groups, T) bool, needed (rows,), probs, sorted_probs,
+    cumulative and order."""
+    R, T = scores.shape
+    probs = F.softmax(scores, dim=-1)
+    sp, order = probs.sort(dim=-1, descending=True, stable=True)
+    cum = sp.cumsum(dim=-1)
+    needed = ((cum < top_p).sum(dim=-1) + 1).clamp_max(T)
+    rpg = R if rows_per_group is None else rows_per_group
+    groups = max(1, -(-R // max(rpg, 1)))
+    mask = torch.zeros(groups, T, dtype=torch.bool)
+    mask[:, :base_tiles] = True
+    for r in range(R):
+        mask[r // max(rpg, 1), order[r, : int(needed[r])]] = True
+    return {"mask": mask, "needed": needed, "probs": probs, "sorted_probs": sp, "cumulative": cum, "order": order}

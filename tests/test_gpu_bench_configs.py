@@ -1,0 +1,141 @@
+"""Parity at the exact configurations the benchmark times (BASELINE.json configs
+C1-C5, built by the same constructors bench.py uses), against the CPU oracle:
+
+  C1  fp32 FovealPattentionMLP, D 512, 2048 parameter tokens, base 2, K_max 8,
+      x 4 x 128 (foveal_pattention.py:264-352): routing bit-exact, output vs
+      fp64 within 1e-5 rel-L2 (fp32 accumulation over K = 512 puts the kernel
+      at ~1e-6 from the exact value, the same distance as CPU fp32 GEMMs);
+  C3b 8B prefill, 4096 tokens x 4096, 64 of 224 blocks, packed weights
+      (foveal_pattention.py:278-288) vs the oracle eval forward, bf16 rel-L2 <= 2e-3;
+  C4  32 sequences x 131072 context, 32 routed pages each, 16 GiB paged pool
+      (attention.py:339-367): routing vs the oracle, attention of 3 sequences vs
+      fp64 over supports gathered on the device;
+  C5  4096 x 8192 x 8192, 128 x 128 tiles, per-row-group masks at 10/25/50%
+      (block_matmul.py:381-392): 2 row groups per density vs fp64.
+"""
+import math
+
+import pytest
+import torch
+
+import bench
+from oracle import attention as A
+from oracle import pattention as P
+from oracle import routing as R
+from route_check import check_rows, tolerances
+
+pytestmark = pytest.mark.gpu
+
+
+def test_c1_fp32_module_exact_config(fsi, dev):
+    print("[case] C1 fp32 module", flush=True)
+    g = torch.Generator().manual_seed(0)
+    D, N_p, base, kmax, kmin, top_p = 512, 2048, 2, 8, 2, 0.9
+    kg = torch.randn(N_p, D, generator=g) * 0.02
+    ku = torch.randn(N_p, D, generator=g) * 0.02
+    v = torch.randn(N_p, D, generator=g) * 0.02
+    qmat = torch.linalg.qr(torch.randn(D, 16, generator=g))[0]
+    keys = torch.randn(N_p // 64, 16, generator=g) * 0.25
+    x = torch.randn(4, 128, D, generator=g)
+    m = fsi.FovealPattentionMLP(hidden_dim=D, intermediate_dim=N_p, block_size=64, base_blocks=base,
+                                remote_blocks=kmax, temperature=1.0, dtype=torch.float32)
+    with torch.no_grad():
+        m.k_gate.copy_(kg)
+        m.k_up.copy_(ku)
+        m.v.copy_(v)
+        m.q_proj_16d.weight.copy_(qmat.t())
+        m.block_keys_16d.copy_(keys)
+    m = m.to(dev).eval()
+    with torch.no_grad():
+        out = m(x.to(dev)).cpu()
+    active = m._cached_active_blocks.cpu()
+    x2 = x.reshape(-1, D)
+    ref_active = R.mlp_pooled_route(x2, qmat.t().contiguous(), keys, base, kmax)
+    assert torch.equal(active, ref_active), (active.tolist(), ref_active.tolist())
+    # The top-p form of the same routing (select_blocks on the pooled row, local = base blocks):
+    s = R.mlp_router_scores(x2, qmat.t().contiguous(), keys).float()[None, None]
+    kw = dict(causal=False, local_window_blocks=base, top_p=top_p, min_remote_blocks=kmin, max_remote_blocks=kmax,
+              remote_capacity=kmax)
+    got = fsi.select_blocks(s.to(dev), **kw)
+    ref = R.select_route(s, **kw)
+    remote = R.route_masks(1, N_p // 64, False, base)[2]
+    assert check_rows(got.remote_indices, got.remote_counts, ref, remote, *tolerances(torch.float32)) == []
+    assert int(got.remote_counts[0, 0]) == kmax  # K_max binds at this config (flat cosine-free scores)
+    assert sorted(got.remote_indices[0, 0].tolist()) == sorted((ref_active[base:]).tolist())
+    mask = torch.zeros(N_p, dtype=torch.bool)
+    mask[P.channel_index(active, 64)] = True
+    exact = P.dense_swiglu_f64(x2, kg, ku, v, mask)
+    err = P.rel_l2(out.reshape(-1, D), exact)
+    print(f"C1 fp32 rel-L2 vs fp64: {err:.3e}", flush=True)
+    assert err <= 1e-5
+
+
+def test_c3b_prefill_full_size(fsi, dev):
+    print("[case] C3b prefill 4096 tokens", flush=True)
+    layers = bench.make_layers(fsi, 1, dev)
+    m = layers[0]
+    gx = torch.Generator(device=dev).manual_seed(1)
+    torch.randn(bench.DECODE_BATCH, 1, bench.D_MODEL, device=dev, generator=gx)  # bench draws x_dec first
+    x_pre = torch.randn(1, bench.PREFILL_TOKENS, bench.D_MODEL, device=dev, generator=gx).bfloat16()
+    with torch.no_grad():
+        out = m(x_pre)
+    active = m._cached_active_blocks.cpu()
+    assert active.numel() == bench.BASE + bench.REMOTE and m._packed is not None  # packed prefill path
+    x2 = x_pre.reshape(-1, bench.D_MODEL).cpu()
+    ref = P.mlp_eval_forward(x2, m.k_gate.detach().cpu(), m.k_up.detach().cpu(), m.v.detach().cpu(), active, 64,
+                             fused=True)
+    err = P.rel_l2(out.reshape(-1, bench.D_MODEL).cpu(), ref)
+    print(f"C3b rel-L2: {err:.3e}", flush=True)
+    assert err <= 2e-3
+
+
+def test_c4_decode_attention_full_size(fsi, dev):
+    print("[case] C4 decode attention 32 x 131072", flush=True)
+    c = bench.C4
+    cache, q, qi = bench.c4_inputs(fsi, dev)
+    B, CTX, PAGE, W = c["B"], c["CTX"], c["PAGE"], c["W"]
+    pos = CTX - 1
+    scale = 1.0 / math.sqrt(c["HD"])
+    with torch.no_grad():
+        pages, counts = fsi.decode_route(qi, cache.kp_cache, None, pos=pos, page_size=PAGE, local_window=W,
+                                         completed_pages=CTX // PAGE, top_p=c["TOP_P"], min_remote_blocks=0,
+                                         max_remote_blocks=c["KMAX"])
+        out = fsi.decode_attention(q, cache, pos=pos, window=W, remote_pages=pages, remote_counts=counts,
+                                   scale=scale).cpu()
+    ref_r = R.decode_route(qi.cpu()[:, None], cache.kp_cache.cpu(), pos, PAGE, W, CTX // PAGE, c["TOP_P"], 0,
+                           c["KMAX"])
+    cnt = counts.cpu().tolist()
+    assert cnt == [len(p) for p in ref_r["pages"]] and min(cnt) == c["KMAX"]  # K_max binds: 32 pages each
+    for b in range(B):
+        assert sorted(pages[b, :cnt[b]].tolist()) == sorted(ref_r["pages"][b])
+    for b in (0, 13, B - 1):
+        sel = pages[b, :cnt[b]].tolist()
+        toks = torch.tensor(A.support_tokens(pos, W, sel, PAGE), device=dev)
+        kd, vd = cache.to_dense(CTX, batch=slice(b, b + 1))
+        ks, vs = kd[:, :, toks].cpu(), vd[:, :, toks].cpu()  # (1, Hkv, 3072, hd): the support only
+        del kd, vd
+        n = ks.shape[2]
+        ref = A.decode_attention_f64(q[b:b + 1].cpu().float(), ks, vs, n - 1, n, [[]], PAGE, scale)
+        err = P.rel_l2(out[b:b + 1].float(), ref.float())
+        print(f"C4 seq {b} support {n} rel-L2 {err:.3e}", flush=True)
+        assert n == W + PAGE * c["KMAX"] and err <= 2e-3
+
+
+@pytest.mark.parametrize("density", bench.C5["DENSITIES"])
+def test_c5_block_sparse_full_size(fsi, dev, density):
+    print(f"[case] C5 density {density}", flush=True)
+    x, w, scores = bench.c5_inputs(dev)
+    mask, n_tiles = bench.c5_mask(scores, density)
+    T = bench.C5["T"]
+    with torch.no_grad():
+        out = fsi.blockwise_matmul(x, w, mask, T, T, rows_per_group=T)
+    from oracle import blocksparse as BS
+
+    N, K = w.shape
+    wc = w.cpu().double()
+    for grp in (0, 21):
+        em = BS.expand_tile_mask(mask[grp].cpu(), N, K, T, T)
+        ref = x[grp * T:(grp + 1) * T].cpu().double() @ (wc * em).t()
+        err = P.rel_l2(out[grp * T:(grp + 1) * T].cpu().float(), ref.float())
+        print(f"C5 d={density} group {grp}: {n_tiles} tiles rel-L2 {err:.3e}", flush=True)
+        assert err <= 2e-3

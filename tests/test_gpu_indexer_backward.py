@@ -168,7 +168,7 @@ def test_foveal_indexer_gradients(fsi, dev, hidden, seq, block):
     rk, rv = IX.pool_kv(mr.k_proj(xr), mr.v_proj(xr), block, F64)
     rs = IX.block_scores(rq[:, ::block], rk, F64)
     radd = mr.out_proj(IX.additive_context(rs, rv, True, F64)).repeat_interleave(block, dim=1)
-    rdist = mr.distillation_loss(rs, teacher.double())
+    rdist = IX.distillation_loss(rs, teacher.double(), causal=True, temperature=mr.distill_temperature, acc=F64)
     (radd.sum() + rdist).backward()
 
     assert _rel(add_out, radd) <= 1e-4

@@ -93,3 +93,67 @@ def test_indexer_gradients_match_finite_differences(causal):
     mask = torch.rand(2, 4, 3, generator=g) > 0.4
     mask[0, 1] = False  # an all-masked row
     assert torch.autograd.gradcheck(lambda a: R.masked_probs(a, mask, torch.float64), (s,))
+
+
+def _distill_case(g, B, Q, N, kind):
+    s = torch.randn(B, Q, N, generator=g, dtype=torch.float64) * 2
+    t = torch.rand(B, Q, N, generator=g, dtype=torch.float64) - 0.2  # some negative teacher mass
+    t[0, -1] = 0.0  # a row whose teacher mass vanishes -> uniform target
+    if kind == "explicit":
+        mask = torch.rand(B, Q, N, generator=g) > 0.4
+        mask[0, 0] = False  # a row without a valid block
+        return s, t, mask, False
+    return s, t, None, kind == "causal"
+
+
+@pytest.mark.parametrize("kind", ["causal", "full", "explicit"])
+@pytest.mark.parametrize("temperature", [0.5, 1.0, 2.0])
+def test_distillation_loss_brute_force(kind, temperature):
+    from oracle import brute
+
+    g = torch.Generator().manual_seed(7)
+    B, Q, N = 2, 6, 9
+    s, t, mask, causal = _distill_case(g, B, Q, N, kind)
+    got = IX.distillation_loss(s, t, mask, causal=causal, temperature=temperature, acc=torch.float64)
+    if mask is None:
+        valid = (torch.arange(N)[None] < torch.arange(Q)[:, None]) if causal else torch.ones(Q, N, dtype=torch.bool)
+        valid = valid[None].expand(B, Q, N)
+    else:
+        valid = mask
+    rows_s = s.reshape(B * Q, N).tolist()
+    rows_t = t.reshape(B * Q, N).tolist()
+    rows_v = valid.reshape(B * Q, N).tolist()
+    ref, per_row = brute.distill_loss_rows(rows_s, rows_t, rows_v, temperature)
+    assert abs(float(got) - ref) <= 1e-12 * max(1.0, abs(ref))
+    if kind != "full":
+        assert any(r is None for r in per_row)  # the empty rows are excluded, not averaged as 0
+
+
+def test_distillation_loss_closed_forms():
+    g = torch.Generator().manual_seed(3)
+    s = torch.randn(1, 4, 11, generator=g, dtype=torch.float64)
+    p = torch.softmax(s, dim=-1)
+    # teacher = student distribution: the loss is the mean entropy of the rows
+    ent = -(p * p.log()).sum(-1).mean()
+    got = IX.distillation_loss(s, p * 3.0, causal=False, acc=torch.float64)  # unnormalised teacher mass
+    assert abs(float(got) - float(ent)) <= 1e-12
+    # zero teacher: uniform target, loss = logsumexp(z) - mean(z)
+    z = s / 0.7
+    ref = (torch.logsumexp(z, -1) - z.mean(-1)).mean()
+    got = IX.distillation_loss(s, torch.zeros_like(s), causal=False, temperature=0.7, acc=torch.float64)
+    assert abs(float(got) - float(ref)) <= 1e-12
+    # one query block, causal: no valid row, zero loss with zero gradient
+    s1 = torch.randn(1, 1, 5, dtype=torch.float64, requires_grad=True)
+    loss = IX.distillation_loss(s1, torch.rand(1, 1, 5, dtype=torch.float64), causal=True, acc=torch.float64)
+    loss.backward()
+    assert float(loss) == 0.0 and not s1.grad.any()
+
+
+def test_distillation_loss_gradcheck():
+    g = torch.Generator().manual_seed(5)
+    s = torch.randn(2, 4, 6, generator=g, dtype=torch.float64, requires_grad=True)
+    t = torch.rand(2, 4, 6, generator=g, dtype=torch.float64)
+    t[1, 2] = 0.0
+    for causal in (True, False):
+        assert torch.autograd.gradcheck(
+            lambda x: IX.distillation_loss(x, t, causal=causal, temperature=1.3, acc=torch.float64), (s,))

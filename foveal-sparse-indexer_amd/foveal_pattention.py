@@ -108,7 +108,7 @@ class _EvalPattentionFn(torch.autograd.Function):
         v = m.v.detach().index_select(0, idx)
         g = F.linear(x_2d, kg)
         u = F.linear(x_2d, ku)
-        dh = F.linear(dy.to(x_2d.dtype), v.t().contiguous())
+        dh = F.linear(dy.to(x_2d.dtype), v)
         dg, du = FusedSwiGLUFunction.backward(_SavedGU(g, u), dh)
         dx = F.linear(dg, kg.t().contiguous()) + F.linear(du, ku.t().contiguous())
         return dx, None, None

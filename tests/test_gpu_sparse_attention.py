@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from oracle import attention as A
+from oracle import indexer as IX
 from oracle import pattention as Pt
 from oracle import routing as R
 
@@ -163,5 +164,5 @@ def test_prefill_forward_module(fsi, dev):
     err = Pt.rel_l2(out.cpu().float(), ref.float())
     assert err <= 1e-2, err
     assert aux["additive_out"] is not None and out.shape == (B, T, D)
-    ref_loss = mc.indexer.distillation_loss(scores, teacher)
+    ref_loss = IX.distillation_loss(scores, teacher, causal=True, temperature=mc.indexer.distill_temperature)
     assert math.isclose(float(aux["distill_loss"]), float(ref_loss), rel_tol=1e-2, abs_tol=1e-5)

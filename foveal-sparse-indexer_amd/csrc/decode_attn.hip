@@ -21,6 +21,8 @@
 // Per-wave partials (max, sum, O) are merged by a second kernel; nothing is
 // synchronised across workgroups.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "fsi_common.h"
 
@@ -464,22 +466,16 @@ FSI_API int fsi_kv_read(const void* k_pool, const void* v_pool, int64_t B, int64
   return FSI_OK;
 }
 
-FSI_API size_t fsi_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, int64_t window,
-                                              int64_t capacity, int64_t max_pages) {
-  if (B <= 0 || Hkv <= 0 || Hq <= 0 || head_dim <= 0 || max_pages <= 0 || window < 0 || capacity < 0)
-    return FSI_WORKSPACE_COUNTER_BYTES;
-  const int64_t S = split_count(B, Hkv, max_chunks_of(window, capacity, max_pages));
-  const int64_t G = Hq / Hkv;
-  const int64_t parts = B * Hkv * S;
-  return FSI_WORKSPACE_COUNTER_BYTES + static_cast<size_t>(parts) * (2 * 16 + G * head_dim) * sizeof(float) + 256;
-}
+}  // extern "C"
 
-FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
-                            int64_t max_pages, int64_t n_phys_pages, const int32_t* pos_rows, int64_t pos,
-                            int64_t window, const int32_t* remote_pages, const int32_t* remote_counts,
-                            int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale,
-                            void* out, void* workspace, size_t workspace_bytes, int* err, void* stream) {
-  using namespace fsi_host;
+namespace {
+
+// Checks shared by fsi_decode_attn and fsi_decode_attn_noalloc that do not
+// involve the partials buffer.  Returns FSI_OK or a status with the message set.
+int decode_attn_check(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
+                      int64_t max_pages, int64_t n_phys_pages, const int32_t* pos_rows, int64_t pos, int64_t window,
+                      const int32_t* remote_pages, const int32_t* remote_counts, int64_t capacity, int64_t B,
+                      int64_t Hq, int64_t Hkv, int64_t head_dim, void* out) {
   FSI_CHECK_ARG(head_dim == 64 || head_dim == 128, FSI_ERR_SHAPE, "decode_attn: head_dim %lld not 64 or 128",
                 (long long)head_dim);
   FSI_CHECK_ARG(B >= 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16, FSI_ERR_SHAPE,
@@ -495,16 +491,31 @@ FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_poo
   FSI_CHECK_ARG(q && k_pool && v_pool && page_table && out, FSI_ERR_INVALID_ARG, "decode_attn: null pointer");
   FSI_CHECK_ARG(capacity == 0 || (remote_pages && remote_counts), FSI_ERR_INVALID_ARG,
                 "decode_attn: remote page list or counts missing");
+  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k_pool) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(v_pool) % 16 == 0,
+                FSI_ERR_ALIGN, "decode_attn: q and pools must be 16-byte aligned");
+  return FSI_OK;
+}
+
+// Bytes of per-wave partials (max, sum, O) the partial and merge kernels exchange.
+size_t decode_attn_partials_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, int64_t window,
+                                  int64_t capacity, int64_t max_pages) {
+  const int64_t S = split_count(B, Hkv, max_chunks_of(window, capacity, max_pages));
+  const int64_t parts = B * Hkv * S;
+  return static_cast<size_t>(parts) * (2 * 16 + (Hq / Hkv) * head_dim) * sizeof(float);
+}
+
+// The partial and merge kernels with the partials at `ws` (16-byte aligned,
+// decode_attn_partials_bytes long; every byte read is written first in the
+// same call, so it needs no clearing).
+int decode_attn_launch(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
+                       int64_t max_pages, int64_t n_phys_pages, const int32_t* pos_rows, int64_t pos, int64_t window,
+                       const int32_t* remote_pages, const int32_t* remote_counts, int64_t capacity, int64_t B,
+                       int64_t Hq, int64_t Hkv, int64_t head_dim, float scale, void* out, char* ws, int* err,
+                       void* stream) {
   const int64_t max_chunks = max_chunks_of(window, capacity, max_pages);
   const int S = split_count(B, Hkv, max_chunks);
-  const size_t need = fsi_decode_attn_workspace_size(B, Hq, Hkv, head_dim, window, capacity, max_pages);
-  FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE, "decode_attn: workspace %zu < %zu bytes",
-                workspace_bytes, need);
-  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k_pool) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(v_pool) % 16 == 0 && reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
-                FSI_ERR_ALIGN, "decode_attn: q, pools and workspace must be 16-byte aligned");
   const int64_t parts = B * Hkv * S;
-  char* ws = static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES;
   DecodeParams P;
   P.q = static_cast<const bf16_t*>(q);
   P.k_pool = static_cast<const bf16_t*>(k_pool);
@@ -546,6 +557,91 @@ FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_poo
   }
   FSI_HIP_LAUNCH_CHECK("decode_attn merge");
   return FSI_OK;
+}
+
+// Scratch of fsi_decode_attn_noalloc: the per-wave partials live in this
+// file-scope device array, one copy per GPU, held until the process ends.  Host
+// code never passes the symbol itself to a kernel: the array's device address
+// is looked up once per device with hipGetSymbolAddress.
+constexpr size_t NOALLOC_SCRATCH_BYTES = FSI_DECODE_ATTN_NOALLOC_MAX_BYTES;
+__device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::atomic<char*> g_scratch_ptr[MAX_DEVICES];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on the first call
+// there, with that device current), or null with the last-error message set.
+char* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+    fsi_host::set_last_error("decode_attn_noalloc: no current HIP device (or index >= %d)", MAX_DEVICES);
+    return nullptr;
+  }
+  char* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+  if (p) return p;
+  void* addr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || addr == nullptr) {
+    fsi_host::set_last_error("decode_attn_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                             hipGetErrorString(e));
+    return nullptr;
+  }
+  p = static_cast<char*>(addr);
+  g_scratch_ptr[dev].store(p, std::memory_order_release);
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+FSI_API size_t fsi_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, int64_t window,
+                                              int64_t capacity, int64_t max_pages) {
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || head_dim <= 0 || max_pages <= 0 || window < 0 || capacity < 0)
+    return FSI_WORKSPACE_COUNTER_BYTES;
+  return FSI_WORKSPACE_COUNTER_BYTES + decode_attn_partials_bytes(B, Hq, Hkv, head_dim, window, capacity, max_pages) +
+         256;
+}
+
+FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
+                            int64_t max_pages, int64_t n_phys_pages, const int32_t* pos_rows, int64_t pos,
+                            int64_t window, const int32_t* remote_pages, const int32_t* remote_counts,
+                            int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale,
+                            void* out, void* workspace, size_t workspace_bytes, int* err, void* stream) {
+  const int c = decode_attn_check(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
+                                  remote_pages, remote_counts, capacity, B, Hq, Hkv, head_dim, out);
+  if (c != FSI_OK || B == 0) return c;
+  const size_t need = fsi_decode_attn_workspace_size(B, Hq, Hkv, head_dim, window, capacity, max_pages);
+  FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE, "decode_attn: workspace %zu < %zu bytes",
+                workspace_bytes, need);
+  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, FSI_ERR_ALIGN,
+                "decode_attn: workspace must be 16-byte aligned");
+  return decode_attn_launch(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
+                            remote_pages, remote_counts, capacity, B, Hq, Hkv, head_dim, scale, out,
+                            static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES, err, stream);
+}
+
+FSI_API int fsi_decode_attn_noalloc(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
+                                    int64_t max_pages, int64_t n_phys_pages, const int32_t* pos_rows, int64_t pos,
+                                    int64_t window, const int32_t* remote_pages, const int32_t* remote_counts,
+                                    int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim,
+                                    float scale, void* out, int* err, void* stream) {
+  const int c = decode_attn_check(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
+                                  remote_pages, remote_counts, capacity, B, Hq, Hkv, head_dim, out);
+  if (c != FSI_OK || B == 0) return c;
+  const size_t need = decode_attn_partials_bytes(B, Hq, Hkv, head_dim, window, capacity, max_pages);
+  FSI_CHECK_ARG(need <= NOALLOC_SCRATCH_BYTES, FSI_ERR_CAPACITY,
+                "decode_attn_noalloc: %zu bytes of partials exceed the %zu-byte device scratch "
+                "(use fsi_decode_attn with a workspace)",
+                need, NOALLOC_SCRATCH_BYTES);
+  char* ws = scratch_on_current_device();
+  if (!ws) return FSI_ERR_HIP;
+  return decode_attn_launch(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
+                            remote_pages, remote_counts, capacity, B, Hq, Hkv, head_dim, scale, out, ws, err, stream);
 }
 
 }  // extern "C"

@@ -385,6 +385,24 @@ FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_poo
                             int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale,
                             void* out, void* workspace, size_t workspace_bytes, int* err, void* stream);
 
+/* fsi_decode_attn without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The partials live in a file-scope device array of
+ * FSI_DECODE_ATTN_NOALLOC_MAX_BYTES per GPU, held until the process ends; a
+ * call needing more (fsi_decode_attn_workspace_size(...) -
+ * FSI_WORKSPACE_COUNTER_BYTES - 256 bytes, about 4.5 MB for 32 sequences x 32
+ * heads x head_dim 128) returns FSI_ERR_CAPACITY.  Every call on one GPU shares
+ * that array: calls that overlap in time on one GPU (different streams, or
+ * different host threads without ordering) race and must not be issued.
+ * Arguments and results are those of fsi_decode_attn. */
+#define FSI_DECODE_ATTN_NOALLOC_MAX_BYTES (16u << 20)
+FSI_API int fsi_decode_attn_noalloc(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
+                                    int64_t max_pages, int64_t n_phys_pages, const int32_t* pos_rows, int64_t pos,
+                                    int64_t window, const int32_t* remote_pages, const int32_t* remote_counts,
+                                    int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim,
+                                    float scale, void* out, int* err, void* stream);
+
 /* ------------------------------------------------------------------------- *
  * Block-sparse prefill attention (bf16 in, fp32 softmax and accumulate, bf16 out).
  * q: (B, Hq, T, head_dim), k and v: (B, Hkv, T, head_dim), out: (B, Hq, T,

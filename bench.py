@@ -13,12 +13,16 @@ the active weights are not served from the 256 MB MALL of one repeated layer.
 The K timed steps are captured once in a HIP graph and replayed; HIP events on
 the replay stream bracket the timed region.
 
-Other workloads (one JSON line each, for the profiles; not the headline line):
+The default line also carries, under "workloads", one sub-object per other
+config (each with its own roofline and CPU baseline, 20 graph-replayed steps):
+C2 routing, C4 decode attention, C5 block-sparse GEMM and prefill attention
+(skip them with --no-workloads).  Each can also run alone as its own line:
   --workload routing      C2: fused 16-D cosine scoring + top-p selection, 8192 queries x 4096 keys
   --workload decode_attn  C4: foveal paged-KV decode attention, 32 sequences x 131072 context
   --workload prefill_attn block-sparse prefill attention, 16384 tokens, Llama-3-8B attention heads
   --workload block_sparse C5: 2-D tile-sparse matmul, 4096 x 8192 by 8192 x 8192, 128 x 128 tiles
   --workload teacher_targets dense block-energy distillation targets, Llama-3-8B MLP, 4096 tokens
+  --workload hbm_stream   the HBM read ceiling (fsi_stream_read probe; torch copy and sum beside it)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-prefill] [--workload W]
 """
@@ -49,6 +53,16 @@ DECODE_BATCH, PREFILL_TOKENS = 64, 4096
 #   --no-pack    : (34872.4 + 4129.5 + 18477.7 + 4109.0) KiB x 1.9997 read + 17408 KiB written
 DECODE_TRAFFIC_BYTES = int(107933.9 * 1024)
 DECODE_TRAFFIC_BYTES_UNPACKED = int(140566.8 * 1024)
+# Same method for the other workloads (KiB read after the x 1.99979 scale + KiB written;
+# profiles/pattention_decode_prefill_8b.md, decode_attention_c4.md, indexer_routing_c2.md,
+# block_sparse_gemm_c5.md).
+PREFILL_TRAFFIC_BYTES = int((393549 + 33260 + 196761 + 34494) * 1024)
+C4_TRAFFIC_BYTES = int((407891 + 4617) * 1024)
+C2_TRAFFIC_BYTES = int((2335 + 2112) * 1024)
+C5_TRAFFIC_BYTES = {0.10: (714 + 64) << 20, 0.25: (1665 + 64) << 20, 0.50: (2910 + 64) << 20}
+# C2: wave-level VALU instructions of one score_route_kernel launch (rocprofv3 SQ_INSTS_VALU)
+C2_VALU_INSTS = 84_080_701
+VALU_PEAK_GIPS = 256 * 4 * 2.4 / 4  # G wave64 VALU instructions/s: 256 CUs x 4 SIMDs x 2.4 GHz / 4 cycles
 
 
 def decode_bytes(n_active: int, batch: int) -> int:
@@ -175,9 +189,15 @@ def bench_routing(fsi, args, dev):
                   "synthetic (seeded Dirichlet(0.3) mixes of 4 N(0,1)-normalised keys + N(0,0.1) noise, bf16)",
                   {"workload": "C2: 8192 queries x 4096 block keys, index_dim 16, top-p 0.9, K_min 4, K_max 64, "
                                "capacity 64, non-causal", "mean_selected": round(float(counts.mean()), 2)})
-    res["roofline"] = {"bound": "valu", "achieved": round(algo / per / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(algo / per / 1e9 / HBM_PEAK_GBS, 6), "traffic": None,
-                       "kernel": "score_route_kernel (1 launch)", "bytes_per_launch": algo,
+    # VALU issue roofline: the launch's wave-level VALU instruction count (rocprofv3
+    # SQ_INSTS_VALU, profiles/indexer_routing_c2.md) over the issue peak of 256 CUs x
+    # 4 SIMDs x 2.4 GHz / 4 cycles per wave64 instruction.
+    gips = C2_VALU_INSTS / per / 1e9
+    res["roofline"] = {"bound": "valu", "achieved": round(gips, 1), "peak": VALU_PEAK_GIPS,
+                       "unit": "G VALU wave-instructions/s", "frac": round(gips / VALU_PEAK_GIPS, 4),
+                       "traffic": C2_TRAFFIC_BYTES, "kernel": "score_route_kernel (1 launch)",
+                       "valu_insts_per_launch": C2_VALU_INSTS, "bytes_per_launch": algo,
+                       "hbm_gbs": round(algo / per / 1e9, 2),
                        "note": "not HBM-bound: 33.5 M scores, exps and a top-64 rank per launch"}
     if not args.no_cpu_baseline:
         from oracle import routing as R
@@ -254,7 +274,7 @@ def bench_decode_attn(fsi, args, dev):
                                "context 131072, page 64, local window 1024, top-p 0.9, K_max 32",
                    "mean_selected_pages": round(k_sel, 2)})
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                       "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C4_TRAFFIC_BYTES,
                        "kernel": "decode_route + decode_attn_partial + decode_attn_merge (3 launches)",
                        "bytes_per_launch": algo}
     if not args.no_cpu_baseline:
@@ -425,9 +445,10 @@ def bench_block_sparse(fsi, args, dev):
                   "synthetic (seeded N(0,1) X, N(0,0.01) W, per-row-group top-d tiles of seeded uniform scores)",
                   {"workload": "C5: X 4096 x 8192, W 8192 x 8192 in 128 x 128 tiles (4096), one mask per 128-row "
                                "group (32 groups), density 25% (1024 tiles per group)",
-                   "densities": {f"{d:.2f}": grade(v) for d, v in lines.items()}})
+                   "densities": {f"{d:.2f}": dict(grade(v), traffic=C5_TRAFFIC_BYTES.get(d))
+                                 for d, v in lines.items()}})
     res["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                       "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                       "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": C5_TRAFFIC_BYTES[0.25],
                        "kernel": "bsgemm_kernel<N_DIRECT, K_LIST> (+3 small list-building launches)",
                        "flops_per_launch": flops}
     if not args.no_cpu_baseline:
@@ -501,6 +522,52 @@ def bench_teacher_targets(fsi, args, dev):
     return res
 
 
+def bench_hbm_stream(fsi, args, dev):
+    """The practical HBM ceiling the HBM-bound kernels are measured against: a
+    plain device copy (read + write) and a read-only sum, 4 GiB each, timed with
+    events over graph replays like every other workload."""
+    n = 4 << 30
+    a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    av = a.view(torch.float32)
+    outs = {}
+
+    def copy_step(i):
+        b.copy_(a)
+
+    def read_step(i):
+        outs["s"] = av.sum()
+
+    t_c, _ = time_graph(copy_step, args.steps, args.warmup, dev)
+    t_r, _ = time_graph(read_step, args.steps, args.warmup, dev)
+    copy_gbs = 2 * n / (t_c / args.steps) / 1e9
+    read_gbs = n / (t_r / args.steps) / 1e9
+    # the library's stream-read probe over launch shapes: the best is the read ceiling
+    from foveal_sparse_indexer_amd import _lib
+
+    L = _lib.lib()
+    sink = torch.empty(16384 * 256, dtype=torch.int32, device=dev)
+    probe = {}
+    for wgs in (1024, 2048, 4096, 8192, 16384):
+        for unroll in (4, 8, 16):
+            def probe_step(i, wgs=wgs, unroll=unroll):
+                _lib.check(L.fsi_stream_read(a.data_ptr(), n, wgs, unroll, sink.data_ptr(),
+                                             torch.cuda.current_stream(dev).cuda_stream), "stream_read")
+
+            t_p, _ = time_graph(probe_step, args.steps, args.warmup, dev)
+            probe[f"{wgs}x256/u{unroll}"] = round(n / (t_p / args.steps) / 1e9, 1)
+    best = max(probe, key=probe.get)
+    res = _result("HBM stream bandwidth GB/s (best stream-read probe shape)", probe[best], "GB/s", args.steps,
+                  args.warmup, round(n / probe[best] / 1e6, 6), "u8", "synthetic (4 GiB buffers)",
+                  {"workload": "fsi_stream_read over 4 GiB at several launch shapes; torch copy_ of 4 GiB (read + "
+                               "write); torch sum over 4 GiB of fp32 (read)",
+                   "probe_gbs": probe, "best_shape": best, "torch_copy_gbs": round(copy_gbs, 1),
+                   "torch_sum_gbs": round(read_gbs, 1)})
+    res["roofline"] = {"bound": "hbm", "achieved": probe[best], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(probe[best] / HBM_PEAK_GBS, 4), "traffic": None}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -514,7 +581,7 @@ def main():
                     help="only the C3 line (skip the C2 / C4 / C5 / prefill-attention sub-objects)")
     ap.add_argument("--workload", default="pattention",
                     choices=["pattention", "routing", "decode_attn", "prefill_attn", "block_sparse",
-                             "teacher_targets"])
+                             "teacher_targets", "hbm_stream"])
     ap.add_argument("--eager", action="store_true", help="no graph capture (for per-dispatch counter runs)")
     ap.add_argument("--no-pack", action="store_true",
                     help="decode from the parameters in place (4-kernel split-K path) instead of packed weights")
@@ -533,9 +600,17 @@ def main():
     fsi = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
+    if args.copy_calibration:
+        # reference dispatch for the HBM counters: one plain 512 MiB device copy
+        a = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize(dev)
+        del a, b
     if args.workload != "pattention":
         fn = {"routing": bench_routing, "decode_attn": bench_decode_attn, "prefill_attn": bench_prefill_attn,
-              "block_sparse": bench_block_sparse, "teacher_targets": bench_teacher_targets}[args.workload]
+              "block_sparse": bench_block_sparse, "teacher_targets": bench_teacher_targets,
+              "hbm_stream": bench_hbm_stream}[args.workload]
         with torch.no_grad():
             print(json.dumps(fn(fsi, args, dev)), flush=True)
         return
@@ -554,13 +629,6 @@ def main():
             m(x_pre)
             m(x_dec)
     n_active = int(layers[0]._cached_active_blocks.numel())
-
-    if args.copy_calibration:
-        a = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
-        b = torch.empty_like(a)
-        b.copy_(a)
-        torch.cuda.synchronize(dev)
-        del a, b
 
     outs = {}
 
@@ -626,7 +694,9 @@ def main():
             "ms_per_step": round(t_pre / args.prefill_steps * 1e3, 4),
             "config": "C3b: 1 x 4096 tokens, same layers and active blocks",
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None, "flops_per_launch": flops},
+                         "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                         "traffic": PREFILL_TRAFFIC_BYTES if n_active == BASE + REMOTE else None,
+                         "flops_per_launch": flops},
         }
 
     if not args.no_cpu_baseline:

@@ -486,6 +486,13 @@ FSI_API int fsi_tile_route(const void* scores, int dtype, int64_t rows, int64_t 
                            int64_t rows_per_group, int64_t base_tiles, float top_p, uint8_t* out_mask,
                            int32_t* out_needed, void* out_probs, void* stream);
 
+/* HBM read-bandwidth probe (measurement only; no counterpart in the reference):
+ * reads `bytes` (multiple of 16, 16-byte aligned src) once with `workgroups` x 256
+ * lanes, `unroll` (1, 4, 8 or 16) 16-byte loads in flight per lane; sink receives
+ * workgroups * 256 dwords.  bench.py uses it as the practical HBM ceiling. */
+FSI_API int fsi_stream_read(const void* src, int64_t bytes, int64_t workgroups, int unroll, uint32_t* sink,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,7 +21,7 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import _lib
-from .core import FovealIndexer, _forward_only, index_rms_norm
+from .core import FovealIndexer, index_rms_norm
 
 
 def decode_route(
@@ -90,16 +90,21 @@ PAGE_SIZE = 64
 
 
 class FovealKVCache:
-    """Paged KV cache for foveal decoding (drop-in for attention.py:22-94).
+    """KV cache for foveal decoding (drop-in for attention.py:22-94).
 
-    Same constructor, `update` and public state (`kp_cache`, `vp_cache`,
-    `partial_kp`, `partial_vp`, `seq_len`, `completed_pages`) as the reference.
-    The full-rank cache is paged instead of contiguous: `k_cache` / `v_cache`
-    are physical page pools in the MFMA-tile layouts of include/fsi.h, and
-    `page_table` (B, max_pages) maps each sequence's logical pages to them
-    (sequence b owns pages [b * max_pages, (b + 1) * max_pages) unless a
-    caller-built table is installed).  `to_dense()` / `load_dense()` convert
-    to and from the reference's (B, Hkv, S, hd) layout.  bf16 only; page_size 64.
+    Same constructor, `update` and public state (`k_cache`, `v_cache`,
+    `kp_cache`, `vp_cache`, `partial_kp`, `partial_vp`, `seq_len`,
+    `completed_pages`) as the reference, including its default dtype (fp32).
+    Two layouts of the full-rank K/V:
+      * paged (bf16, page_size 64, head_dim 64 or 128, unless paged=False):
+        `k_cache` / `v_cache` are physical page pools in the MFMA-tile layouts
+        of include/fsi.h, and `page_table` (B, max_pages) maps each sequence's
+        logical pages to them (sequence b owns pages [b * max_pages,
+        (b + 1) * max_pages) unless a caller-built table is installed);
+        `to_dense()` / `load_dense()` convert to and from the reference layout;
+      * contiguous (every other dtype / page size / head_dim, or paged=False):
+        `k_cache` / `v_cache` are (B, Hkv, max_seq_len, head_dim) exactly as in
+        the reference, so callers may read and write them directly.
     """
 
     def __init__(
@@ -111,16 +116,21 @@ class FovealKVCache:
         index_dim: int,
         page_size: int,
         device: torch.device,
-        dtype: torch.dtype = torch.bfloat16,
+        dtype: torch.dtype = torch.float32,
         n_phys_pages: Optional[int] = None,
         page_table: Optional[Tensor] = None,
+        paged: Optional[bool] = None,
     ):
-        if page_size != PAGE_SIZE:
-            raise ValueError(f"FovealKVCache: page_size {page_size} unsupported (the HIP path uses {PAGE_SIZE})")
-        if dtype != torch.bfloat16:
-            raise TypeError(f"FovealKVCache: dtype {dtype} unsupported (bfloat16 only on the MI355X path)")
-        if head_dim not in (64, 128):
-            raise ValueError(f"FovealKVCache: head_dim {head_dim} unsupported (64 or 128)")
+        if dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"FovealKVCache: dtype {dtype} unsupported (float32 or bfloat16)")
+        if page_size <= 0 or head_dim <= 0 or head_dim > 256:
+            raise ValueError(f"FovealKVCache: page_size {page_size} / head_dim {head_dim} unsupported")
+        pageable = dtype == torch.bfloat16 and page_size == PAGE_SIZE and head_dim in (64, 128)
+        if paged and not pageable:
+            raise ValueError("FovealKVCache: the paged layout needs bfloat16, page_size 64 and head_dim 64 or 128")
+        self.paged = pageable if paged is None else bool(paged)
+        if not self.paged and (page_table is not None or n_phys_pages is not None):
+            raise ValueError("FovealKVCache: page_table / n_phys_pages apply to the paged layout only")
         self.batch_size = batch_size
         self.max_seq_len = max_seq_len
         self.num_kv_heads = num_kv_heads
@@ -130,16 +140,24 @@ class FovealKVCache:
         self.device = torch.device(device)
         self.dtype = dtype
         self.max_pages = -(-max_seq_len // page_size)
-        if page_table is None:
-            page_table = torch.arange(batch_size * self.max_pages, dtype=torch.int32).view(batch_size, self.max_pages)
-        self.page_table = page_table.to(device=self.device, dtype=torch.int32).contiguous()
-        if tuple(self.page_table.shape) != (batch_size, self.max_pages):
-            raise ValueError(f"FovealKVCache: page table {tuple(self.page_table.shape)} != "
-                             f"{(batch_size, self.max_pages)}")
-        self.n_phys_pages = int(n_phys_pages) if n_phys_pages is not None else batch_size * self.max_pages
-        per_page = num_kv_heads * page_size * head_dim
-        self.k_cache = torch.zeros(self.n_phys_pages, per_page, device=self.device, dtype=dtype)
-        self.v_cache = torch.zeros(self.n_phys_pages, per_page, device=self.device, dtype=dtype)
+        if self.paged:
+            if page_table is None:
+                page_table = torch.arange(batch_size * self.max_pages, dtype=torch.int32).view(batch_size,
+                                                                                               self.max_pages)
+            self.page_table = page_table.to(device=self.device, dtype=torch.int32).contiguous()
+            if tuple(self.page_table.shape) != (batch_size, self.max_pages):
+                raise ValueError(f"FovealKVCache: page table {tuple(self.page_table.shape)} != "
+                                 f"{(batch_size, self.max_pages)}")
+            self.n_phys_pages = int(n_phys_pages) if n_phys_pages is not None else batch_size * self.max_pages
+            per_page = num_kv_heads * page_size * head_dim
+            self.k_cache = torch.zeros(self.n_phys_pages, per_page, device=self.device, dtype=dtype)
+            self.v_cache = torch.zeros(self.n_phys_pages, per_page, device=self.device, dtype=dtype)
+        else:
+            self.page_table = None
+            self.n_phys_pages = 0
+            shape = (batch_size, num_kv_heads, max_seq_len, head_dim)
+            self.k_cache = torch.zeros(shape, device=self.device, dtype=dtype)
+            self.v_cache = torch.zeros(shape, device=self.device, dtype=dtype)
         self.kp_cache = torch.zeros(batch_size, self.max_pages, index_dim, device=self.device, dtype=torch.float32)
         self.vp_cache = torch.zeros(batch_size, self.max_pages, index_dim, device=self.device, dtype=dtype)
         self.partial_kp = torch.zeros(batch_size, page_size, index_dim, device=self.device, dtype=dtype)
@@ -152,6 +170,14 @@ class FovealKVCache:
         B, H, n, hd = k.shape
         if (B, H, hd) != (self.batch_size, self.num_kv_heads, self.head_dim) or v.shape != k.shape:
             raise ValueError(f"{what}: K {tuple(k.shape)} / V {tuple(v.shape)} do not match the cache")
+        if start < 0 or start + n > self.max_seq_len:
+            raise RuntimeError(f"KV cache capacity {self.max_seq_len} exceeded.")
+        if not self.paged:
+            # the reference layout: a slice copy (attention.py:72-73), cast to the cache dtype
+            with torch.no_grad():
+                self.k_cache[:, :, start:start + n] = k
+                self.v_cache[:, :, start:start + n] = v
+            return
         if k.dtype != self.dtype or v.dtype != self.dtype:
             raise TypeError(f"{what}: K/V dtype {k.dtype}/{v.dtype} != {self.dtype}")
         if k.stride(-1) != 1:
@@ -176,8 +202,9 @@ class FovealKVCache:
         self._write(k_step, v_step, pos)
         offset = pos % self.page_size
         page = pos // self.page_size
-        self.partial_kp[:, offset] = ki_step.reshape(self.batch_size, self.index_dim)
-        self.partial_vp[:, offset] = vi_step.reshape(self.batch_size, self.index_dim)
+        with torch.no_grad():  # cache state, as the kernels read it: no autograd history
+            self.partial_kp[:, offset] = ki_step.reshape(self.batch_size, self.index_dim)
+            self.partial_vp[:, offset] = vi_step.reshape(self.batch_size, self.index_dim)
         if offset == self.page_size - 1:
             dev = self.kp_cache.device
             st = _lib.lib().fsi_kv_page_pool(
@@ -198,6 +225,9 @@ class FovealKVCache:
         """(K, V) of positions [0, n_tok) in the reference layout (b, Hkv, n, hd)
         for the sequences in `batch` (a slice; all by default)."""
         n = self.seq_len if n_tok is None else int(n_tok)
+        if not self.paged:
+            sel = batch if batch is not None else slice(None)
+            return self.k_cache[sel, :, :n].clone(), self.v_cache[sel, :, :n].clone()
         rows = self.page_table[batch] if batch is not None else self.page_table
         rows = rows.contiguous()
         shape = (rows.shape[0], self.num_kv_heads, n, self.head_dim)
@@ -209,6 +239,86 @@ class FovealKVCache:
                                     _lib.stream_handle(self.k_cache.device))
         _lib.check(st, "FovealKVCache.to_dense")
         return k, v
+
+
+def _decode_attention_launch(q3: Tensor, cache: FovealKVCache, pos_rows: Optional[Tensor], pos_val: int,
+                             window: int, remote_pages: Optional[Tensor], remote_counts: Optional[Tensor], cap: int,
+                             scale: float, out: Tensor) -> Tensor:
+    what = "decode_attention"
+    dev = q3.device
+    B, Hq, hd = q3.shape
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    err = _lib.error_word(dev)
+    rp = _lib.ptr(remote_pages) if cap else None
+    rc = _lib.ptr(remote_counts) if cap else None
+    if cache.paged:
+        ws = _lib.workspace(dev, L.fsi_decode_attn_workspace_size(B, Hq, cache.num_kv_heads, hd, window, cap,
+                                                                   cache.max_pages), stream)
+        st = L.fsi_decode_attn(q3.data_ptr(), cache.k_cache.data_ptr(), cache.v_cache.data_ptr(),
+                               cache.page_table.data_ptr(), cache.max_pages, cache.n_phys_pages, _lib.ptr(pos_rows),
+                               pos_val, int(window), rp, rc, cap, B, Hq, cache.num_kv_heads, hd, float(scale),
+                               out.data_ptr(), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
+    else:
+        k, v = cache.k_cache, cache.v_cache
+        st = L.fsi_decode_attn_dense(q3.data_ptr(), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+                                     k.stride(2), v.stride(0), v.stride(1), v.stride(2), cache.max_seq_len,
+                                     _lib.ptr(pos_rows), pos_val, int(window), cache.page_size, rp, rc, cap, B, Hq,
+                                     cache.num_kv_heads, hd, float(scale), _lib.dtype_code(q3.dtype, what),
+                                     out.data_ptr(), err.data_ptr(), stream)
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+    return out
+
+
+def _decode_support(cache: FovealKVCache, b: int, pos: int, window: int, pages: List[int]):
+    """(K, V) of one sequence's support, (Hkv, n, hd), in the order the kernels and
+    the reference (attention.py:341-352) attend it."""
+    ls = max(0, pos + 1 - window)
+    toks = list(range(ls, pos + 1))
+    for p in pages:
+        toks.extend(range(p * cache.page_size, (p + 1) * cache.page_size))
+    idx = torch.tensor(toks, dtype=torch.long, device=cache.k_cache.device)
+    k, v = cache.to_dense(max(idx.max().item() + 1, 1) if toks else 1, batch=slice(b, b + 1))
+    return k[0].index_select(1, idx), v[0].index_select(1, idx)
+
+
+class _DecodeAttnFn(torch.autograd.Function):
+    """Decode attention with a gradient for the query.  The cached keys and values
+    are inference state (the kernels read them in place), so they are constants
+    here; the backward recomputes each sequence's softmax over its gathered
+    support in fp32: dq = scale * sum_t p_t (dO . v_t - dO . o) k_t."""
+
+    @staticmethod
+    def forward(ctx, q3, cache, pos_rows, pos_val, window, remote_pages, remote_counts, cap, scale):
+        out = torch.empty_like(q3)
+        _decode_attention_launch(q3, cache, pos_rows, pos_val, window, remote_pages, remote_counts, cap, scale, out)
+        ctx.cache, ctx.meta = cache, (pos_val, window, cap, scale)
+        ctx.save_for_backward(q3, pos_rows, remote_pages, remote_counts)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q3, pos_rows, remote_pages, remote_counts = ctx.saved_tensors
+        cache = ctx.cache
+        pos_val, window, cap, scale = ctx.meta
+        B, Hq, hd = q3.shape
+        G = Hq // cache.num_kv_heads
+        dq = torch.empty_like(q3, dtype=torch.float32)
+        pos_list = pos_rows.tolist() if pos_rows is not None else [pos_val] * B
+        cnts = remote_counts.tolist() if cap else [0] * B
+        pages_all = remote_pages.tolist() if cap else [[] for _ in range(B)]
+        for b in range(B):
+            k, v = _decode_support(cache, b, int(pos_list[b]), window, pages_all[b][:max(0, min(cnts[b], cap))])
+            k = k.float().repeat_interleave(G, dim=0)  # (Hq, n, hd)
+            v = v.float().repeat_interleave(G, dim=0)
+            qb, gb = q3[b].float(), dout[b].float()
+            p = torch.softmax(torch.bmm(k, qb[:, :, None]).squeeze(-1) * scale, dim=-1)  # (Hq, n)
+            o = torch.bmm(p[:, None], v).squeeze(1)
+            dp = torch.bmm(v, gb[:, :, None]).squeeze(-1) - (gb * o).sum(-1, keepdim=True)
+            dq[b] = torch.bmm((p * dp)[:, None], k).squeeze(1) * scale
+        return dq.to(q3.dtype), None, None, None, None, None, None, None, None
 
 
 def decode_attention(
@@ -224,14 +334,16 @@ def decode_attention(
 ) -> Tensor:
     """softmax(scale q K^T) V over [max(0, pos + 1 - window), pos] plus the
     selected remote pages, for every sequence and query head (attention.py:339-365).
-    q: (B, Hq, hd) or (B, Hq, 1, hd) bf16.  Returns (B, Hq, hd) bf16."""
+    q: (B, Hq, hd) or (B, Hq, 1, hd) in the cache's dtype.  Returns (B, Hq, hd).
+    Paged caches run the split-K MFMA kernels, contiguous ones the generic
+    kernel.  Differentiable in q (the cached keys and values are constants)."""
     what = "decode_attention"
     dev = _lib.require_gpu(q, cache.k_cache, what=what)
     B = q.shape[0]
     Hq, hd = q.shape[1], q.shape[-1]
-    q3 = q.reshape(B, Hq, hd).contiguous()
-    if q3.dtype != torch.bfloat16:
-        raise TypeError(f"{what}: q dtype {q3.dtype} unsupported (bfloat16)")
+    q3 = q.reshape(B, Hq, hd)
+    if q3.dtype != cache.dtype:
+        raise TypeError(f"{what}: q dtype {q3.dtype} != cache dtype {cache.dtype}")
     if B != cache.batch_size or hd != cache.head_dim:
         raise ValueError(f"{what}: q {tuple(q.shape)} does not match the cache")
     pos_rows, pos_val = None, 0
@@ -244,22 +356,18 @@ def decode_attention(
         remote_pages = remote_pages.to(device=dev, dtype=torch.int32).contiguous()
         remote_counts = remote_counts.to(device=dev, dtype=torch.int32).contiguous()
         cap = remote_pages.shape[-1]
+    else:
+        remote_pages = remote_counts = None
+    if torch.is_grad_enabled() and q3.requires_grad:
+        res = _DecodeAttnFn.apply(q3.contiguous(), cache, pos_rows, pos_val, int(window), remote_pages,
+                                  remote_counts, cap, float(scale))
+        if out is not None:
+            out.copy_(res.detach())
+        return res
     if out is None:
-        out = torch.empty((B, Hq, hd), dtype=torch.bfloat16, device=dev)
-    L = _lib.lib()
-    stream = _lib.stream_handle(dev)
-    ws = _lib.workspace(dev, L.fsi_decode_attn_workspace_size(B, Hq, cache.num_kv_heads, hd, window, cap,
-                                                               cache.max_pages), stream)
-    err = _lib.error_word(dev)
-    st = L.fsi_decode_attn(q3.data_ptr(), cache.k_cache.data_ptr(), cache.v_cache.data_ptr(),
-                           cache.page_table.data_ptr(), cache.max_pages, cache.n_phys_pages, _lib.ptr(pos_rows),
-                           pos_val, int(window), _lib.ptr(remote_pages) if cap else None,
-                           _lib.ptr(remote_counts) if cap else None, cap, B, Hq, cache.num_kv_heads, hd, float(scale),
-                           out.data_ptr(), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
-    _lib.check(st, what)
-    if _lib.checks_enabled():
-        _lib.raise_device_errors(dev, what)
-    return out
+        out = torch.empty((B, Hq, hd), dtype=q3.dtype, device=dev)
+    return _decode_attention_launch(q3.detach().contiguous(), cache, pos_rows, pos_val, int(window), remote_pages,
+                                    remote_counts, cap, float(scale), out)
 
 
 SATTN_LOCAL_REMOTE = 0  # FSI_SATTN_LOCAL_REMOTE
@@ -267,13 +375,96 @@ SATTN_BLOCK_LIST = 1  # FSI_SATTN_BLOCK_LIST
 
 
 def _attn_operand(t: Tensor, what: str, name: str) -> Tensor:
-    if t.dtype != torch.bfloat16:
-        raise TypeError(f"{what}: {name} dtype {t.dtype} unsupported (bfloat16)")
+    if t.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{what}: {name} dtype {t.dtype} unsupported (bfloat16 or float32)")
     if t.dim() != 4:
         raise ValueError(f"{what}: {name} must be (B, H, T, head_dim), got {tuple(t.shape)}")
     if t.stride(3) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
         t = t.contiguous()
     return t
+
+
+def _sparse_attention_launch(q, k, v, lists, counts, cap, block, mode, window, scale, out):
+    what = "sparse_attention"
+    dev = q.device
+    B, Hq, T, hd = q.shape
+    Hkv = k.shape[1]
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    ws = _lib.workspace(dev, L.fsi_sparse_attn_workspace_size(B, Hkv, T, hd), stream)
+    err = _lib.error_word(dev)
+    st = L.fsi_sparse_attn(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), B, Hq, Hkv, T, hd, int(block), int(mode), int(window),
+        _lib.ptr(lists), lists.stride(0) if cap else 0, lists.stride(1) if cap else 0, cap, counts.data_ptr(),
+        counts.stride(0), counts.stride(1), float(scale), _lib.dtype_code(q.dtype, what), out.data_ptr(),
+        out.stride(0), out.stride(1), out.stride(2), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+    return out
+
+
+def _sparse_logit_bias(lists, counts, cap, B, T, block, mode, window, dev):
+    """(B, 1, T, T) additive logit bias of a sparse pattern: 0 for an allowed key
+    (log of its multiplicity for block lists), -inf elsewhere.  The dense form of
+    what the kernels walk, for the recompute in the backward (the reference
+    builds the same boolean mask, attention.py:148-176)."""
+    nb = -(-T // block)
+    mult = torch.zeros(B, nb, nb + 1, dtype=torch.float32, device=dev)  # last column: ids out of range
+    if cap:
+        slot = torch.arange(cap, device=dev)
+        valid = slot[None, None] < counts.clamp(0, cap)[..., None]
+        ids = lists.long().clamp(-1, nb)
+        ids = torch.where(valid & (ids >= 0) & (ids < nb), ids, torch.full_like(ids, nb))
+        mult.scatter_add_(2, ids, valid.float())
+    mult = mult[..., :nb]
+    tb = torch.arange(T, device=dev) // block
+    page = mult[:, tb][:, :, tb]  # (B, T, T): multiplicity of key s's block for query t's block
+    if mode == SATTN_LOCAL_REMOTE:
+        t = torch.arange(T, device=dev)
+        win = (t[None, :] <= t[:, None]) & (t[None, :] > t[:, None] - window)
+        allowed = win[None] | (page > 0)
+        bias = torch.zeros(B, T, T, device=dev).masked_fill_(~allowed, float("-inf"))
+    else:
+        bias = torch.where(page > 0, page.log(), torch.full_like(page, float("-inf")))
+    return bias[:, None]
+
+
+class _SparseAttnFn(torch.autograd.Function):
+    """sparse_attention with gradients for q, k and v.  The forward is the HIP
+    kernel; the backward recomputes the attention densely in fp32 over the same
+    pattern (library matmuls and softmax, B x Hq x T x T memory, as the
+    reference's own masked SDPA) and differentiates it."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, lists, counts, cap, block, mode, window, scale):
+        B, Hq, T, hd = q.shape
+        out = torch.empty((B, T, Hq, hd), dtype=q.dtype, device=q.device).transpose(1, 2)
+        _sparse_attention_launch(q, k, v, lists, counts, cap, block, mode, window, scale, out)
+        ctx.save_for_backward(q, k, v, lists, counts)
+        ctx.meta = (cap, block, mode, window, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, lists, counts = ctx.saved_tensors
+        cap, block, mode, window, scale = ctx.meta
+        B, Hq, T, hd = q.shape
+        G = Hq // k.shape[1]
+        bias = _sparse_logit_bias(lists, counts, cap, B, T, block, mode, window, q.device)
+        with torch.enable_grad():
+            qf = q.detach().float().requires_grad_()
+            kf = k.detach().float().requires_grad_()
+            vf = v.detach().float().requires_grad_()
+            ke = kf.repeat_interleave(G, dim=1)
+            ve = vf.repeat_interleave(G, dim=1)
+            s = torch.matmul(qf, ke.transpose(-1, -2).contiguous()) * scale + bias
+            empty = torch.isneginf(s).all(dim=-1, keepdim=True)  # rows with no key give 0
+            p = torch.softmax(s.masked_fill(empty, 0.0), dim=-1).masked_fill(empty, 0.0)
+            o = torch.matmul(p, ve)
+            dq, dk, dv = torch.autograd.grad(o, (qf, kf, vf), dout.float())
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None, None, None)
 
 
 def sparse_attention(
@@ -289,7 +480,8 @@ def sparse_attention(
     scale: Optional[float] = None,
     out: Optional[Tensor] = None,
 ) -> Tensor:
-    """Block-sparse attention of q (B, Hq, T, hd) over k, v (B, Hkv, T, hd), bf16.
+    """Block-sparse attention of q (B, Hq, T, hd) over k, v (B, Hkv, T, hd), bf16
+    or fp32 (fp32 softmax and accumulation either way).
 
     mode SATTN_LOCAL_REMOTE (attention.py:148-218): query t sees keys s with
     t - window < s <= t plus every key of the pages lists[b, t // block, :counts]
@@ -297,14 +489,15 @@ def sparse_attention(
     every key of the listed key blocks.  lists: (B, ceil(T / block), capacity)
     int32; counts: (B, ceil(T / block)).  Views with unit stride over head_dim
     (such as proj(x).view(B, T, H, hd).transpose(1, 2)) are read in place; `out`
-    may be such a view too.  Returns (B, Hq, T, hd) bf16."""
+    may be such a view too.  Differentiable in q, k and v.  Returns (B, Hq, T, hd)."""
     what = "sparse_attention"
     dev = _lib.require_gpu(q, k, v, counts, lists, what=what)
-    _forward_only(what, q, k, v)
-    q, k, v = (_attn_operand(t, what, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
-    B, Hq, T, hd = q.shape
-    Hkv = k.shape[1]
-    if tuple(k.shape) != (B, Hkv, T, hd) or tuple(v.shape) != (B, Hkv, T, hd) or Hq % Hkv:
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"{what}: q, k, v dtypes {q.dtype}, {k.dtype}, {v.dtype} differ")
+    qa, ka, va = (_attn_operand(t, what, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    B, Hq, T, hd = qa.shape
+    Hkv = ka.shape[1]
+    if tuple(ka.shape) != (B, Hkv, T, hd) or tuple(va.shape) != (B, Hkv, T, hd) or Hq % Hkv:
         raise ValueError(f"{what}: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
     Qb = -(-T // block)
     counts = counts.to(device=dev, dtype=torch.int32)
@@ -320,26 +513,19 @@ def sparse_attention(
         cap = lists.shape[2]
     else:
         lists = None
-    if out is None:
-        out = torch.empty((B, T, Hq, hd), dtype=torch.bfloat16, device=dev).transpose(1, 2)
-    elif tuple(out.shape) != (B, Hq, T, hd) or out.dtype != torch.bfloat16 or out.stride(3) != 1:
-        raise ValueError(f"{what}: out must be a (B, Hq, T, hd) bf16 tensor with unit stride over hd")
     if scale is None:
         scale = 1.0 / math.sqrt(hd)
-    L = _lib.lib()
-    stream = _lib.stream_handle(dev)
-    ws = _lib.workspace(dev, L.fsi_sparse_attn_workspace_size(B, Hkv, T, hd), stream)
-    err = _lib.error_word(dev)
-    st = L.fsi_sparse_attn(
-        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
-        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), B, Hq, Hkv, T, hd, int(block), int(mode), int(window),
-        _lib.ptr(lists), lists.stride(0) if cap else 0, lists.stride(1) if cap else 0, cap, counts.data_ptr(),
-        counts.stride(0), counts.stride(1), float(scale), 1, out.data_ptr(), out.stride(0), out.stride(1),
-        out.stride(2), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
-    _lib.check(st, what)
-    if _lib.checks_enabled():
-        _lib.raise_device_errors(dev, what)
-    return out
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        res = _SparseAttnFn.apply(qa, ka, va, lists, counts, cap, int(block), int(mode), int(window), float(scale))
+        if out is not None:
+            out.copy_(res.detach())
+        return res
+    if out is None:
+        out = torch.empty((B, T, Hq, hd), dtype=qa.dtype, device=dev).transpose(1, 2)
+    elif tuple(out.shape) != (B, Hq, T, hd) or out.dtype != qa.dtype or out.stride(3) != 1:
+        raise ValueError(f"{what}: out must be a (B, Hq, T, hd) {qa.dtype} tensor with unit stride over hd")
+    return _sparse_attention_launch(qa.detach(), ka.detach(), va.detach(), lists, counts, cap, block, mode, window,
+                                    scale, out)
 
 
 def triton_foveal_sparse_attention(
@@ -354,17 +540,17 @@ def triton_foveal_sparse_attention(
     """Block-sparse attention (triton_ops.py:256-313): query block m of
     block_size queries attends every key of block_indices[b, m, :active_counts[b, m]],
     with no causal mask; a query block with no active block gets 0.  q, k, v:
-    (B, H, N, D) bf16 with N % block_size == 0.  The `triton_` name is kept for
-    compatibility; the kernel is HIP (block_size a multiple of 16; D 16, 32, 64
-    or 128; bfloat16)."""
+    (B, H, N, D) bf16 or fp32 with N % block_size == 0.  The `triton_` name is
+    kept for compatibility; the kernels are HIP (MFMA for bf16 with block_size a
+    multiple of 16 and D 16, 32, 64 or 128; the generic kernel otherwise)."""
     B, H, N, D = q.shape
     if N % block_size != 0:
         raise ValueError(f"N ({N}) must be divisible by block_size ({block_size})")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    return sparse_attention(q, k, v, block_indices, active_counts, block=block_size, mode=SATTN_BLOCK_LIST,
-                            scale=scale, out=out)
+    res = sparse_attention(q, k, v, block_indices, active_counts, block=block_size, mode=SATTN_BLOCK_LIST,
+                           scale=scale)
+    return res.contiguous()
 
 
 class FovealSparseAttention(nn.Module):
@@ -379,7 +565,10 @@ class FovealSparseAttention(nn.Module):
     `reference_batch0_pages = True` reproduces that.  `selected_remote_pages`
     reports each sequence's own selection in both modes, as the reference does.
     The prefill `forward` routes with the HIP indexer ops and runs one
-    block-sparse attention launch (`sparse_attention`); inference only.
+    block-sparse attention launch (`sparse_attention`).  Both paths take the
+    reference's dtypes (fp32 by default, bf16) and are differentiable: the
+    attention backward recomputes the sparse pattern densely (as the reference's
+    forward does), decode's gradient reaches q (the cache is inference state).
     """
 
     def __init__(
@@ -453,11 +642,10 @@ class FovealSparseAttention(nn.Module):
         k = self.k_proj(x).view(batch, seq_len, self.num_kv_heads, self.head_dim).transpose(1, 2)
         v = self.v_proj(x).view(batch, seq_len, self.num_kv_heads, self.head_dim).transpose(1, 2)
 
-        attn = torch.empty((batch, seq_len, self.num_heads, self.head_dim), dtype=q.dtype, device=q.device)
-        sparse_attention(q, k, v, route.remote_indices, route.remote_counts, block=self.page_size,
-                         mode=SATTN_LOCAL_REMOTE, window=self.local_window, scale=self.scale,
-                         out=attn.transpose(1, 2))
-        out = self.out_proj(attn.view(batch, seq_len, self.num_heads * self.head_dim))
+        # (B, Hq, T, hd) view of a (B, T, Hq, hd) buffer: the heads merge without a copy
+        attn = sparse_attention(q, k, v, route.remote_indices, route.remote_counts, block=self.page_size,
+                                mode=SATTN_LOCAL_REMOTE, window=self.local_window, scale=self.scale)
+        out = self.out_proj(attn.transpose(1, 2).reshape(batch, seq_len, self.num_heads * self.head_dim))
 
         additive_out = None
         if self.use_additive_stream:

@@ -18,39 +18,88 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import _lib
-from .core import FovealIndexer, Route, _forward_only, _PoolKVFn, select_blocks
+from .core import FovealIndexer, Route, _AdditiveContextFn, _PoolKVFn, masked_softmax, select_blocks
 
 
-def block_sparse_linear(x2d: Tensor, weight: Tensor, bias: Optional[Tensor], active_blocks: Tensor,
-                        block_size: int, out: Optional[Tensor] = None) -> Tensor:
-    """out = zeros; out[:, blk] = x w[blk]^T (+ bias[blk]) for the active column blocks."""
+def _linear_launch(x2d: Tensor, weight: Tensor, bias: Optional[Tensor], idx: Tensor, block_size: int,
+                   out: Tensor) -> Tensor:
     what = "block_sparse_linear"
-    dev = _lib.require_gpu(x2d, weight, bias, what=what)
-    _forward_only(what, x2d, weight, bias)
-    if x2d.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or (bias is not None and bias.dtype != torch.bfloat16):
-        raise TypeError(f"{what}: bfloat16 only (x {x2d.dtype}, weight {weight.dtype})")
-    x2d = x2d.contiguous()
-    weight = weight.contiguous()
+    dev = x2d.device
     M, K = x2d.shape
-    N, K2 = weight.shape
-    if K2 != K:
-        raise ValueError(f"{what}: K mismatch {K} vs {K2}")
-    idx = torch.as_tensor(active_blocks).reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
-    if out is None:
-        out = torch.empty((M, N), dtype=x2d.dtype, device=dev)
+    N = weight.shape[0]
     L = _lib.lib()
     stream = _lib.stream_handle(dev)
     ws = _lib.workspace(dev, L.fsi_block_sparse_linear_workspace_size(N, block_size), stream)
     err = _lib.error_word(dev)
     st = L.fsi_block_sparse_linear(x2d.data_ptr(), x2d.stride(0), weight.data_ptr(), weight.stride(0),
-                                   _lib.ptr(bias.contiguous() if bias is not None else None),
-                                   idx.data_ptr() if idx.numel() else None, idx.numel(), block_size, M, N, K,
-                                   _lib.DTYPE_BF16, out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(),
-                                   err.data_ptr(), stream)
+                                   _lib.ptr(bias), idx.data_ptr() if idx.numel() else None, idx.numel(), block_size,
+                                   M, N, K, _lib.dtype_code(x2d.dtype, what), out.data_ptr(), out.stride(0),
+                                   ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
     _lib.check(st, what)
     if _lib.checks_enabled():
         _lib.raise_device_errors(dev, what)
     return out
+
+
+def _column_mask(idx: Tensor, n_blocks: int, block_size: int) -> Tensor:
+    """(N,) float mask of the active column blocks' output columns."""
+    m = torch.zeros(n_blocks, dtype=torch.float32, device=idx.device)
+    if idx.numel():
+        m[idx.long()] = 1.0
+    return m.repeat_interleave(block_size)
+
+
+class _BlockSparseLinearFn(torch.autograd.Function):
+    """Column-block sparse linear on the HIP kernels with the gradients of the
+    reference's gather -> F.linear -> scatter (block_matmul.py:215-232):
+    dy restricted to the active columns, dx = dy_S W_S, dW_S = dy_S^T x,
+    dbias_S = sum(dy_S) — library GEMMs on the restricted dy."""
+
+    @staticmethod
+    def forward(ctx, x2d, weight, bias, idx, block_size):
+        out = torch.empty((x2d.shape[0], weight.shape[0]), dtype=x2d.dtype, device=x2d.device)
+        _linear_launch(x2d, weight, bias, idx, block_size, out)
+        ctx.save_for_backward(x2d, weight, idx)
+        ctx.block_size, ctx.has_bias = block_size, bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2d, weight, idx = ctx.saved_tensors
+        cm = _column_mask(idx, weight.shape[0] // ctx.block_size, ctx.block_size).to(dy.dtype)
+        dys = dy * cm
+        dx = dys @ weight
+        dw = dys.t() @ x2d
+        db = dys.sum(0) if ctx.has_bias else None
+        return dx, dw, db, None, None
+
+
+def block_sparse_linear(x2d: Tensor, weight: Tensor, bias: Optional[Tensor], active_blocks: Tensor,
+                        block_size: int, out: Optional[Tensor] = None) -> Tensor:
+    """out = zeros; out[:, blk] = x w[blk]^T (+ bias[blk]) for the active column
+    blocks.  fp32 or bf16 (fp32 accumulation); differentiable in x, weight and
+    bias."""
+    what = "block_sparse_linear"
+    dev = _lib.require_gpu(x2d, weight, bias, what=what)
+    if x2d.dtype != weight.dtype or (bias is not None and bias.dtype != x2d.dtype):
+        raise TypeError(f"{what}: x {x2d.dtype}, weight {weight.dtype} and bias dtypes differ")
+    _lib.dtype_code(x2d.dtype, what)
+    x2d = x2d.contiguous()
+    weight = weight.contiguous()
+    bias = bias.contiguous() if bias is not None else None
+    M, K = x2d.shape
+    N, K2 = weight.shape
+    if K2 != K:
+        raise ValueError(f"{what}: K mismatch {K} vs {K2}")
+    idx = torch.as_tensor(active_blocks).reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x2d, weight, bias)):
+        res = _BlockSparseLinearFn.apply(x2d, weight, bias, idx, int(block_size))
+        if out is not None:
+            out.copy_(res.detach())
+        return res
+    if out is None:
+        out = torch.empty((M, N), dtype=x2d.dtype, device=dev)
+    return _linear_launch(x2d, weight, bias, idx, int(block_size), out)
 
 
 def triton_block_sparse_linear(x: Tensor, weight: Tensor, bias: Optional[Tensor], active_block_indices: Tensor,
@@ -72,29 +121,76 @@ def blockwise_matmul(x2d: Tensor, weight: Tensor, tile_mask: Tensor, block_k: in
     groups > 1, row group g covers rows [g rows_per_group, (g+1) rows_per_group)."""
     what = "blockwise_matmul"
     dev = _lib.require_gpu(x2d, weight, tile_mask, what=what)
-    _forward_only(what, x2d, weight)
-    if x2d.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
-        raise TypeError(f"{what}: bfloat16 only (x {x2d.dtype}, weight {weight.dtype})")
+    if x2d.dtype != weight.dtype:
+        raise TypeError(f"{what}: x {x2d.dtype} and weight {weight.dtype} differ")
+    _lib.dtype_code(x2d.dtype, what)
     x2d = x2d.contiguous()
     weight = weight.contiguous()
     M, K = x2d.shape
-    N = weight.shape[0]
     mask = tile_mask.to(device=dev)
     if mask.dim() == 1:
         mask = mask[None]
-    groups = mask.shape[0]
     rpg = rows_per_group if rows_per_group is not None else max(M, 1)
     m8 = mask.to(torch.uint8).contiguous()
+    if torch.is_grad_enabled() and (x2d.requires_grad or weight.requires_grad):
+        res = _BlockwiseMatmulFn.apply(x2d, weight, m8, int(block_k), int(block_n), int(rpg))
+        if out is not None:
+            out.copy_(res.detach())
+        return res
     if out is None:
-        out = torch.empty((M, N), dtype=x2d.dtype, device=dev)
+        out = torch.empty((M, weight.shape[0]), dtype=x2d.dtype, device=dev)
+    return _blockwise_launch(x2d, weight, m8, int(block_k), int(block_n), int(rpg), out)
+
+
+def _blockwise_launch(x2d: Tensor, weight: Tensor, m8: Tensor, block_k: int, block_n: int, rpg: int,
+                      out: Tensor) -> Tensor:
+    what = "blockwise_matmul"
+    dev = x2d.device
+    M, K = x2d.shape
+    N = weight.shape[0]
     L = _lib.lib()
     stream = _lib.stream_handle(dev)
     ws = _lib.workspace(dev, L.fsi_blockwise_matmul_workspace_size(M, N, K, block_k), stream)
     st = L.fsi_blockwise_matmul(x2d.data_ptr(), x2d.stride(0), weight.data_ptr(), weight.stride(0), m8.data_ptr(),
-                                groups, rpg, block_k, block_n, M, N, K, _lib.DTYPE_BF16, out.data_ptr(), out.stride(0),
-                                ws.data_ptr(), ws.numel(), stream)
+                                m8.shape[0], rpg, block_k, block_n, M, N, K, _lib.dtype_code(x2d.dtype, what),
+                                out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), stream)
     _lib.check(st, what)
     return out
+
+
+def _expand_tiles(m: Tensor, N: int, K: int, block_k: int, block_n: int) -> Tensor:
+    """(nkb * nnb,) k-major tile mask -> (N, K) element mask of the weight."""
+    nkb, nnb = K // block_k, N // block_n
+    return m.view(nkb, nnb).t().repeat_interleave(block_n, 0).repeat_interleave(block_k, 1)
+
+
+class _BlockwiseMatmulFn(torch.autograd.Function):
+    """2-D tile-sparse matmul on the HIP kernels with the gradients of the
+    reference's per-tile F.linear sum (block_matmul.py:381-392), i.e. of
+    x (W o M)^T: dx = dy (W o M), dW = (dy^T x) o M, row group by row group —
+    library GEMMs in the backward."""
+
+    @staticmethod
+    def forward(ctx, x2d, weight, m8, block_k, block_n, rpg):
+        out = torch.empty((x2d.shape[0], weight.shape[0]), dtype=x2d.dtype, device=x2d.device)
+        _blockwise_launch(x2d, weight, m8, block_k, block_n, rpg, out)
+        ctx.save_for_backward(x2d, weight, m8)
+        ctx.meta = (block_k, block_n, rpg)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2d, weight, m8 = ctx.saved_tensors
+        block_k, block_n, rpg = ctx.meta
+        N, K = weight.shape
+        dx = torch.empty_like(x2d)
+        dw = torch.zeros_like(weight)
+        for g in range(m8.shape[0]):
+            rows = slice(g * rpg, min((g + 1) * rpg, x2d.shape[0]))
+            em = _expand_tiles(m8[g].bool(), N, K, block_k, block_n).to(weight.dtype)
+            dx[rows] = dy[rows] @ (weight * em)
+            dw += (dy[rows].t() @ x2d[rows]) * em
+        return dx, dw, None, None, None, None
 
 
 def tile_route(scores: Tensor, top_p: float, base_tiles: int, rows_per_group: Optional[int] = None):
@@ -166,7 +262,7 @@ class BlockSparseLinear(nn.Module):
         remote_capacity: int = 8,
         use_additive_stream: bool = True,
         bias: bool = False,
-        dtype: torch.dtype = torch.bfloat16,
+        dtype: Optional[torch.dtype] = None,
     ):
         super().__init__()
         if out_features % block_size != 0:
@@ -188,7 +284,7 @@ class BlockSparseLinear(nn.Module):
             local_window_blocks=self.base_blocks, top_p=top_p, min_remote_blocks=min_remote_blocks,
             max_remote_blocks=max_remote_blocks, remote_capacity=remote_capacity, causal=False,
             use_additive_stream=use_additive_stream,
-        ).to(dtype)
+        ).to(dtype if dtype is not None else torch.get_default_dtype())
         self.weight_to_k = nn.Linear(in_features, index_dim, bias=False, dtype=dtype)
         self.weight_to_v = nn.Linear(in_features, index_dim, bias=False, dtype=dtype)
         self.indexer.out_proj = nn.Linear(index_dim, out_features, bias=False, dtype=dtype)
@@ -286,16 +382,10 @@ def _additive_context(scores: Tensor, v_blocks: Tensor) -> Tensor:
     """softmax over every block (probabilities in the values' dtype) times the
     block values (block_matmul.py:257-260)."""
     what = "additive_stream"
-    dev = _lib.require_gpu(scores, v_blocks, what=what)
+    _lib.require_gpu(scores, v_blocks, what=what)
     s = scores.to(v_blocks.dtype).contiguous() if scores.dtype != v_blocks.dtype else scores.contiguous()
-    v = v_blocks.contiguous()
-    B, Q, N = s.shape
-    d = v.shape[-1]
-    ctx = torch.empty((B, Q, d), dtype=v.dtype, device=dev)
-    st = _lib.lib().fsi_additive_context(s.data_ptr(), v.data_ptr(), _lib.dtype_code(v.dtype, what), B, Q, N, d, 0,
-                                         ctx.data_ptr(), _lib.stream_handle(dev))
-    _lib.check(st, what)
-    return ctx
+    # differentiable in the scores and the block values (HIP backward kernels)
+    return _AdditiveContextFn.apply(s, v_blocks.contiguous(), False)
 
 
 class BlockwiseMatMul2D(nn.Module):
@@ -310,7 +400,7 @@ class BlockwiseMatMul2D(nn.Module):
         base_tiles_ratio: float = 0.25,
         index_dim: int = 16,
         top_p: float = 0.95,
-        dtype: torch.dtype = torch.bfloat16,
+        dtype: Optional[torch.dtype] = None,
     ):
         super().__init__()
         if in_features % block_k != 0 or out_features % block_n != 0:
@@ -365,6 +455,9 @@ class BlockwiseMatMul2D(nn.Module):
         n_active = int(mask.sum())
         out = blockwise_matmul(x.reshape(batch * seq_len, self.in_features), self.weight, mask, self.block_k,
                                self.block_n).view(batch, seq_len, self.out_features)
+        if torch.is_grad_enabled() and scores.requires_grad:
+            # the additive stream trains tile_q / tile_k through the softmax (block_matmul.py:395)
+            probs = masked_softmax(scores, torch.ones((), dtype=torch.bool, device=device))
         context = (probs.to(tile_v.dtype).reshape(-1, self.total_tiles) @ tile_v.contiguous()).view(
             batch, seq_len, self.index_dim)
         out = out + self.out_proj(context)

@@ -44,14 +44,6 @@ class Route:
     base_only_rate: Tensor
 
 
-def _forward_only(what: str, *tensors: Optional[Tensor]) -> None:
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
-        raise NotImplementedError(
-            f"{what}: the MI355X path is inference-only (no backward); "
-            "call it under torch.no_grad() or torch.inference_mode()"
-        )
-
-
 def _as_3d(scores: Tensor, what: str) -> Tensor:
     if scores.dim() != 3:
         raise ValueError(f"{what}: expected (B, Q_blocks, total_blocks) scores, got {tuple(scores.shape)}")

@@ -24,6 +24,15 @@
 
 using namespace fsi;
 
+namespace fsi_bs_generic {  // csrc/bsgemm_generic.hip: fp32 and the bf16 tilings below do not take
+int tile_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, const uint8_t* mask,
+              int64_t groups, int64_t rows_per_group, int64_t block_k, int64_t block_n, int64_t M, int64_t N,
+              int64_t K, int dtype, void* out, int64_t ldo, hipStream_t st);
+int column_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                const int32_t* active_blocks, int64_t n_active, int64_t block_size, int64_t M, int64_t N, int64_t K,
+                int dtype, void* out, int64_t ldo, uint8_t* mask_ws, int* err, hipStream_t st);
+}  // namespace fsi_bs_generic
+
 namespace {
 
 constexpr int TM = 128, TN = 128, TK = 64;
@@ -1484,8 +1493,25 @@ FSI_API int fsi_block_sparse_linear(const void* x, int64_t ldx, const void* w, i
                                     int64_t N, int64_t K, int dtype, void* out, int64_t ldo, void* workspace,
                                     size_t workspace_bytes, int* err, void* stream) {
   using namespace fsi_host;
-  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "block_sparse_linear: dtype %d (bf16 only)", dtype);
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16 || dtype == FSI_DTYPE_F32, FSI_ERR_DTYPE, "block_sparse_linear: dtype %d",
+                dtype);
   FSI_CHECK_ARG(M >= 0 && N >= 0 && K > 0 && n_active >= 0, FSI_ERR_SHAPE, "block_sparse_linear: bad sizes");
+  if (dtype == FSI_DTYPE_F32 || block_size % SUB != 0 || K % 8 || ldx % 8 || ldw % 8 || ldo % 8 || N % 8 ||
+      reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w) % 16 ||
+      reinterpret_cast<uintptr_t>(out) % 16) {
+    // fp32, and bf16 shapes the MFMA engine does not tile: the generic kernel
+    if (M == 0 || N == 0) return FSI_OK;
+    FSI_CHECK_ARG(x && w && out && (active_blocks || n_active == 0), FSI_ERR_INVALID_ARG,
+                  "block_sparse_linear: null pointer");
+    FSI_CHECK_ARG(block_size > 0 && N % block_size == 0, FSI_ERR_SHAPE,
+                  "block_sparse_linear: block_size %lld must divide N %lld", (long long)block_size, (long long)N);
+    const size_t need = fsi_block_sparse_linear_workspace_size(N, block_size);
+    FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE,
+                  "block_sparse_linear: workspace %zu < %zu bytes", workspace_bytes, need);
+    return fsi_bs_generic::column_gemm(x, ldx, w, ldw, bias, active_blocks, n_active, block_size, M, N, K, dtype, out,
+                                       ldo, static_cast<uint8_t*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES, err,
+                                       reinterpret_cast<hipStream_t>(stream));
+  }
   FSI_CHECK_ARG(block_size > 0 && block_size % SUB == 0 && N % block_size == 0, FSI_ERR_SHAPE,
                 "block_sparse_linear: block_size %lld must be a multiple of %d dividing N %lld", (long long)block_size,
                 SUB, (long long)N);
@@ -1549,9 +1575,18 @@ FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int6
                                  int64_t block_n, int64_t M, int64_t N, int64_t K, int dtype, void* out, int64_t ldo,
                                  void* workspace, size_t workspace_bytes, void* stream) {
   using namespace fsi_host;
-  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "blockwise_matmul: dtype %d (bf16 only)", dtype);
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16 || dtype == FSI_DTYPE_F32, FSI_ERR_DTYPE, "blockwise_matmul: dtype %d",
+                dtype);
   FSI_CHECK_ARG(M >= 0 && N > 0 && K > 0 && groups > 0 && rows_per_group > 0, FSI_ERR_SHAPE,
                 "blockwise_matmul: bad sizes");
+  if (dtype == FSI_DTYPE_F32 || block_k % TK != 0 || !(block_n % TN == 0 || TN % block_n == 0) ||
+      !(rows_per_group % TM == 0 || groups == 1) || ldx % 8 || ldw % 8 || ldo % 8) {
+    // fp32, and bf16 tilings the MFMA engine does not take: the generic kernel
+    if (M == 0) return FSI_OK;
+    FSI_CHECK_ARG(x && w && tile_mask && out, FSI_ERR_INVALID_ARG, "blockwise_matmul: null pointer");
+    return fsi_bs_generic::tile_gemm(x, ldx, w, ldw, nullptr, tile_mask, groups, rows_per_group, block_k, block_n,
+                                     M, N, K, dtype, out, ldo, reinterpret_cast<hipStream_t>(stream));
+  }
   FSI_CHECK_ARG(block_k % TK == 0 && block_k > 0 && K % block_k == 0 && block_n > 0 && N % block_n == 0 &&
                     (block_n % TN == 0 || TN % block_n == 0),
                 FSI_ERR_SHAPE, "blockwise_matmul: tiles %lldx%lld must be multiples of %d (K) and divide or be "

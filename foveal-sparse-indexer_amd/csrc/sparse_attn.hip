@@ -28,6 +28,15 @@
 
 using namespace fsi;
 
+namespace fsi_attn_generic {  // csrc/attn_generic.hip
+int sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, const void* k, int64_t ks_b, int64_t ks_h,
+                int64_t ks_t, const void* v, int64_t vs_b, int64_t vs_h, int64_t vs_t, int64_t B, int64_t Hq,
+                int64_t Hkv, int64_t T, int64_t head_dim, int64_t block, int mode, int64_t window,
+                const int32_t* lists, int64_t ls_b, int64_t ls_q, int64_t capacity, const int32_t* counts,
+                int64_t cs_b, int64_t cs_q, float scale, int dtype, void* out, int64_t os_b, int64_t os_h,
+                int64_t os_t, int* err, void* stream);
+}  // namespace fsi_attn_generic
+
 namespace {
 
 constexpr int SA_WAVES = 4;   // query heads per workgroup
@@ -656,9 +665,31 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
                             int64_t os_b, int64_t os_h, int64_t os_t, void* workspace, size_t workspace_bytes,
                             int* err, void* stream) {
   using namespace fsi_host;
-  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "sparse_attn: dtype %d (bf16 only)", dtype);
   FSI_CHECK_ARG(mode == FSI_SATTN_LOCAL_REMOTE || mode == FSI_SATTN_BLOCK_LIST, FSI_ERR_INVALID_ARG,
                 "sparse_attn: mode %d", mode);
+  // fp32, blocks that are not multiples of 16, other head dims and unaligned
+  // operands run the generic kernel (csrc/attn_generic.hip)
+  const bool mfma_path =
+      dtype == FSI_DTYPE_BF16 && block > 0 && block % 16 == 0 &&
+      (head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128) && qs_t % 8 == 0 && qs_h % 8 == 0 &&
+      qs_b % 8 == 0 && ks_t % 8 == 0 && ks_h % 8 == 0 && ks_b % 8 == 0 && vs_t % 8 == 0 && vs_h % 8 == 0 &&
+      vs_b % 8 == 0 && os_t % 4 == 0 && os_h % 4 == 0 && os_b % 4 == 0 &&
+      reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(v) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0;
+  if (!mfma_path) {
+    FSI_CHECK_ARG(B > 0 && T > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, FSI_ERR_SHAPE,
+                  "sparse_attn: B=%lld T=%lld Hq=%lld Hkv=%lld", (long long)B, (long long)T, (long long)Hq,
+                  (long long)Hkv);
+    FSI_CHECK_ARG(capacity >= 0 && capacity <= 4096, FSI_ERR_CAPACITY, "sparse_attn: capacity %lld",
+                  (long long)capacity);
+    FSI_CHECK_ARG(mode != FSI_SATTN_LOCAL_REMOTE || window > 0, FSI_ERR_SHAPE, "sparse_attn: window %lld",
+                  (long long)window);
+    FSI_CHECK_ARG(q && k && v && out && counts && (lists || capacity == 0), FSI_ERR_INVALID_ARG,
+                  "sparse_attn: null pointer");
+    return fsi_attn_generic::sparse_attn(q, qs_b, qs_h, qs_t, k, ks_b, ks_h, ks_t, v, vs_b, vs_h, vs_t, B, Hq, Hkv, T,
+                                         head_dim, block, mode, window, lists, ls_b, ls_q, capacity, counts, cs_b,
+                                         cs_q, scale, dtype, out, os_b, os_h, os_t, err, stream);
+  }
   FSI_CHECK_ARG(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128, FSI_ERR_SHAPE,
                 "sparse_attn: head_dim %lld (16, 32, 64 or 128)", (long long)head_dim);
   FSI_CHECK_ARG(B > 0 && T > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, FSI_ERR_SHAPE,

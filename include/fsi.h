@@ -385,6 +385,22 @@ FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_poo
                             int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale,
                             void* out, void* workspace, size_t workspace_bytes, int* err, void* stream);
 
+/* Decode attention over the reference's contiguous cache layout
+ * (FovealKVCache k_cache / v_cache (B, Hkv, max_seq, head_dim), attention.py:45-57),
+ * fp32 or bf16, any page size, head_dim 1..256: the same support as
+ * fsi_decode_attn (tokens [max(0, pos + 1 - window), pos], then every token of
+ * each page remote_pages[b, :remote_counts[b]], concatenated as attention.py:341-352
+ * gathers them) and the same result, computed in fp32.  Cache strides in
+ * elements (unit stride over head_dim); q and out contiguous (B, Hq, head_dim)
+ * of `dtype`.  Tokens beyond max_seq are skipped and reported through err.
+ * Replaces the gather + repeat_interleave + SDPA of attention.py:339-365. */
+FSI_API int fsi_decode_attn_dense(const void* q, const void* k_cache, const void* v_cache, int64_t ks_b, int64_t ks_h,
+                                  int64_t ks_t, int64_t vs_b, int64_t vs_h, int64_t vs_t, int64_t max_seq,
+                                  const int32_t* pos_rows, int64_t pos, int64_t window, int64_t page_size,
+                                  const int32_t* remote_pages, const int32_t* remote_counts, int64_t capacity,
+                                  int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale, int dtype,
+                                  void* out, int* err, void* stream);
+
 /* fsi_decode_attn without a workspace argument and without any allocation.
  * No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
@@ -428,10 +444,13 @@ typedef enum fsi_sattn_mode {
 
 FSI_API size_t fsi_sparse_attn_workspace_size(int64_t B, int64_t Hkv, int64_t T, int64_t head_dim);
 
-/* head_dim 16, 32, 64 or 128; block a multiple of 16; capacity <= 4096; window > 0 for
- * FSI_SATTN_LOCAL_REMOTE.  Strides multiples of 8 elements (out: 4), q, k, v
- * 16-byte aligned.  Replaces the dense masked SDPA of attention.py:211-218 and
- * the Triton kernel launch of triton_ops.py:298-312. */
+/* dtype FSI_DTYPE_BF16 or FSI_DTYPE_F32 (fp32 math either way, output in dtype);
+ * head_dim 1..256; any block; capacity <= 4096; window > 0 for
+ * FSI_SATTN_LOCAL_REMOTE.  bf16 with head_dim 16, 32, 64 or 128, block a
+ * multiple of 16, strides multiples of 8 elements (out: 4) and q, k, v 16-byte
+ * aligned runs the MFMA kernels; everything else the generic fp32-math kernel.
+ * Replaces the dense masked SDPA of attention.py:211-218 and the Triton kernel
+ * launch of triton_ops.py:298-312. */
 FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, const void* k, int64_t ks_b,
                             int64_t ks_h, int64_t ks_t, const void* v, int64_t vs_b, int64_t vs_h, int64_t vs_t,
                             int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t head_dim, int64_t block, int mode,

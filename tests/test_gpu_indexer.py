@@ -118,10 +118,25 @@ def test_foveal_indexer_module(fsi, dev):
     assert add.shape == (2, 64, 64)
 
 
-def test_forward_only_guard(fsi, dev):
-    """Ops without a backward refuse to record autograd (the indexer
-    representations are differentiable: test_gpu_indexer_backward)."""
-    w = torch.randn(128, 64, device=dev, dtype=torch.bfloat16, requires_grad=True)
-    x = torch.randn(4, 64, device=dev, dtype=torch.bfloat16)
-    with pytest.raises(NotImplementedError, match="inference-only"):
-        fsi.block_sparse_linear(x, w, None, torch.tensor([0], dtype=torch.int32, device=dev), 64)
+def test_block_sparse_linear_gradients_bf16(fsi, dev):
+    """The bf16 MFMA forward of block_sparse_linear records autograd: gradients of
+    x, weight and bias match the fp64 gather -> linear -> scatter product
+    (block_matmul.py:215-232) on the active column blocks."""
+    g = torch.Generator().manual_seed(4)
+    w = (torch.randn(256, 128, generator=g) * 0.1).bfloat16()
+    b = torch.randn(256, generator=g).bfloat16()
+    x = torch.randn(40, 128, generator=g).bfloat16()
+    active = torch.tensor([0, 3], dtype=torch.int32)
+    wd, bd, xd = (t.to(dev).requires_grad_() for t in (w, b, x))
+    y = fsi.block_sparse_linear(xd, wd, bd, active.to(dev), 64)
+    dy = torch.randn(40, 256, generator=g).bfloat16()
+    y.backward(dy.to(dev))
+    wr, br, xr = (t.double().requires_grad_() for t in (w, b, x))
+    cols = torch.cat([torch.arange(0, 64), torch.arange(192, 256)])
+    yr = torch.zeros(40, 256, dtype=torch.float64)
+    yr[:, cols] = xr @ wr[cols].t() + br[cols]
+    yr.backward(dy.double())
+    for got, want in ((y, yr), (xd.grad, xr.grad), (wd.grad, wr.grad), (bd.grad, br.grad)):
+        err = (got.detach().double().cpu() - want).norm() / want.norm()
+        assert err <= 1e-2
+    assert not wd.grad[64:192].any() and not bd.grad[64:192].any()

@@ -15,14 +15,15 @@ the replay stream bracket the timed region.
 
 The default line also carries, under "workloads", one sub-object per other
 config (each with its own roofline and CPU baseline, 20 graph-replayed steps):
-C2 routing, C4 decode attention, C5 block-sparse GEMM and prefill attention
-(skip them with --no-workloads).  Each can also run alone as its own line:
+C2 routing, C4 decode attention, C5 block-sparse GEMM, prefill attention and the
+fused indexer attention (skip them with --no-workloads).  Each can also run alone as its own line:
   --workload routing      C2: fused 16-D cosine scoring + top-p selection, 8192 queries x 4096 keys
   --workload decode_attn  C4: foveal paged-KV decode attention, 32 sequences x 131072 context
   --workload prefill_attn block-sparse prefill attention, 16384 tokens, Llama-3-8B attention heads
   --workload block_sparse C5: 2-D tile-sparse matmul, 4096 x 8192 by 8192 x 8192, 128 x 128 tiles
   --workload teacher_targets dense block-energy distillation targets, Llama-3-8B MLP, 4096 tokens
   --workload hbm_stream   the HBM read ceiling (fsi_stream_read probe; torch copy and sum beside it)
+  --workload sram_attn    fused 16-D indexer + greedy selection + block attention, the reference's 3 SRAM configs
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-prefill] [--workload W]
 """
@@ -30,6 +31,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -522,6 +524,78 @@ def bench_teacher_targets(fsi, args, dev):
     return res
 
 
+SRAM_CONFIGS = [(64, 64, 16), (32, 256, 16), (16, 1024, 32)]  # (batch, seq_len, block_size)
+SRAM_REF_A10G_MS = [0.0566, 0.0515, 0.0619]  # the reference's fused kernel on A10G, BENCHMARKS.md:308-314
+
+
+def bench_sram_attn(fsi, args, dev):
+    """The reference's SRAM-fused indexer benchmark (benchmark_a10g_full.py:314-376):
+    fp16, 4 heads, head_dim 32, max_remote 2, top_p 0.8, three (batch, seq_len,
+    block) configs; one call of each per step.  HBM bytes per call: q and the
+    output once, k and v of the self block plus every attended pick per query
+    block and head, q16 / k16 once."""
+    H, D, R = 4, 32, 2
+    g = torch.Generator(device=dev).manual_seed(0)
+    cases, bytes_call, per_cfg = [], 0, []
+    for B, N, bs in SRAM_CONFIGS:
+        M = N // bs
+        q, k, v = (torch.randn(B, H, N, D, device=dev, generator=g).half() for _ in range(3))
+        q16, k16 = (torch.randn(B, M, 16, device=dev, generator=g).half() for _ in range(2))
+        _, sel = fsi.sram_indexer_attention(q, k, v, q16, k16, max_remote_blocks=R, block_size=bs,
+                                            return_selection=True)
+        attended = int((sel >= 0).sum())
+        b = 2 * (2 * B * H * N * D) + 2 * H * (B * M + attended) * bs * D * 2 + 2 * 2 * B * M * 16
+        bytes_call += b
+        cases.append((q, k, v, q16, k16, bs))
+        per_cfg.append(b)
+    out = {}
+
+    def step(i):
+        for j, (q, k, v, q16, k16, bs) in enumerate(cases):
+            out[j] = fsi.sram_indexer_attention(q, k, v, q16, k16, max_remote_blocks=R, block_size=bs)
+
+    t, _ = time_graph(step, args.steps, args.warmup, dev)
+    per = t / args.steps
+    ms_each = []
+    for j, (q, k, v, q16, k16, bs) in enumerate(cases):
+        def one(i, j=j):
+            q_, k_, v_, a_, b_, bs_ = cases[j]
+            out[j] = fsi.sram_indexer_attention(q_, k_, v_, a_, b_, max_remote_blocks=R, block_size=bs_)
+
+        tj, _ = time_graph(one, args.steps, 1, dev)
+        ms_each.append(round(tj / args.steps * 1e3, 5))
+    gbs = bytes_call / per / 1e9
+    res = _result("fused indexer attention: ms per call of the reference's 3 SRAM configs (sum)",
+                  round(per * 1e3, 5), "ms", args.steps, args.warmup, round(per * 1e3, 5), "fp16",
+                  "synthetic (seeded N(0,1) q, k, v, q16, k16)",
+                  {"workload": "triton_fused_sram_indexer_attention: (B, N, block) in "
+                               f"{SRAM_CONFIGS}, 4 heads, head_dim 32, max_remote 2, top_p 0.8",
+                   "ms_per_config": ms_each, "reference_a10g_ms_per_config": SRAM_REF_A10G_MS},
+                  higher=False)
+    res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": None,
+                       "kernel": "sram_attn_kernel (one launch per config; latency bound at these sizes)",
+                       "bytes_per_launch": per_cfg}
+    if not args.no_cpu_baseline:
+        from oracle import attention as OA
+
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        q, k, v, q16, k16, bs = cases[1]
+        qc, kc, vc, ac, bc = (t.cpu() for t in (q, k, v, q16, k16))
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            picks, _ = OA.sram_select(ac, bc, 0.8, R)
+            OA.sram_attention_f64(qc, kc, vc, picks, bs, 1.0 / math.sqrt(D))
+            ts.append(time.perf_counter() - t0)
+        med = sorted(ts)[1]
+        res["cpu_baseline"] = {"value": round(med * 1e3, 3), "unit": "ms", "cores": cores, "kind": "port",
+                               "sample": "oracle sram_select (fp32) + sram_attention_f64 on the second config "
+                                         "(B 32, N 256, block 16), median of 3"}
+    return res
+
+
 def bench_hbm_stream(fsi, args, dev):
     """The practical HBM ceiling the HBM-bound kernels are measured against: a
     plain device copy (read + write) and a read-only sum, 4 GiB each, timed with
@@ -581,7 +655,7 @@ def main():
                     help="only the C3 line (skip the C2 / C4 / C5 / prefill-attention sub-objects)")
     ap.add_argument("--workload", default="pattention",
                     choices=["pattention", "routing", "decode_attn", "prefill_attn", "block_sparse",
-                             "teacher_targets", "hbm_stream"])
+                             "teacher_targets", "hbm_stream", "sram_attn"])
     ap.add_argument("--eager", action="store_true", help="no graph capture (for per-dispatch counter runs)")
     ap.add_argument("--no-pack", action="store_true",
                     help="decode from the parameters in place (4-kernel split-K path) instead of packed weights")
@@ -610,7 +684,7 @@ def main():
     if args.workload != "pattention":
         fn = {"routing": bench_routing, "decode_attn": bench_decode_attn, "prefill_attn": bench_prefill_attn,
               "block_sparse": bench_block_sparse, "teacher_targets": bench_teacher_targets,
-              "hbm_stream": bench_hbm_stream}[args.workload]
+              "hbm_stream": bench_hbm_stream, "sram_attn": bench_sram_attn}[args.workload]
         with torch.no_grad():
             print(json.dumps(fn(fsi, args, dev)), flush=True)
         return
@@ -727,7 +801,8 @@ def main():
         sub_args.steps, sub_args.warmup = max(1, min(args.steps, 20)), max(1, min(args.warmup, 3))
         result["workloads"] = {}
         for name, fn in (("C2_routing", bench_routing), ("C4_decode_attention", bench_decode_attn),
-                         ("C5_block_sparse", bench_block_sparse), ("prefill_attention", bench_prefill_attn)):
+                         ("C5_block_sparse", bench_block_sparse), ("prefill_attention", bench_prefill_attn),
+                         ("sram_indexer_attention", bench_sram_attn)):
             with torch.no_grad():
                 r = fn(fsi, sub_args, dev)
             result["workloads"][name] = {k: r[k] for k in ("metric", "value", "unit", "steps", "ms_per_step",

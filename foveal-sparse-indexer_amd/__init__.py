@@ -36,7 +36,9 @@ from .attention import (
     decode_attention,
     decode_route,
     sparse_attention,
+    sram_indexer_attention,
     triton_foveal_sparse_attention,
+    triton_fused_sram_indexer_attention,
 )
 from .block_matmul import (
     BlockSparseLinear,
@@ -72,6 +74,8 @@ __all__ = [
     "decode_attention",
     "sparse_attention",
     "triton_foveal_sparse_attention",
+    "triton_fused_sram_indexer_attention",
+    "sram_indexer_attention",
     "FovealKVCache",
     "FovealSparseAttention",
     "FovealPattentionMLP",

@@ -29,6 +29,7 @@ FSI_ERR_WORKSPACE = -8
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2  # fsi_sram_indexer_attention only
 
 ACTIVATIONS = {"swiglu": 0, "silu": 1, "gelu": 2, "relu": 3, "relu2": 4}
 ROUNDING = {"eager": 0, "fused": 1, "fp32": 2}
@@ -161,6 +162,11 @@ SIGNATURES: dict[str, tuple] = {
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64,
          _c_ptr, _c_i64, _c_i64, ctypes.c_float, _c_int, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_size,
          _c_ptr, _c_ptr],
+    ),
+    "fsi_sram_indexer_attention": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         ctypes.c_float, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr],
     ),
     "fsi_block_sparse_linear_workspace_size": (_c_size, [_c_i64, _c_i64]),
     "fsi_block_sparse_linear": (

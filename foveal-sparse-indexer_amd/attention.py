@@ -553,6 +553,81 @@ def triton_foveal_sparse_attention(
     return res.contiguous()
 
 
+_SRAM_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
+
+
+def sram_indexer_attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    q16: Tensor,
+    k16: Tensor,
+    scale: Optional[float] = None,
+    top_p: float = 0.8,
+    max_remote_blocks: int = 2,
+    block_size: int = 16,
+    return_selection: bool = False,
+):
+    """Fused 16-D block indexer, greedy block selection and block attention in
+    one HIP launch (fsi_sram_indexer_attention).  q, k, v: (B, H, N, D) fp32,
+    bf16 or fp16; q16, k16: (B, N / block_size, 16) in q's dtype or fp32.  With
+    return_selection, also returns the (B, N / block_size, max_remote_blocks)
+    int32 picks (-1 where a pick is not attended).  No autograd, as the
+    reference kernel."""
+    what = "triton_fused_sram_indexer_attention"
+    if not q.is_cuda:
+        raise RuntimeError(f"{what} requires a GPU tensor (the HIP library)")
+    B, H, N, D = q.shape
+    if N % block_size != 0:
+        raise AssertionError(f"N ({N}) must be divisible by block_size ({block_size})")
+    M = N // block_size
+    if q.dtype not in _SRAM_DTYPES:
+        raise TypeError(f"{what}: dtype {q.dtype} unsupported (float32, bfloat16 or float16)")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError(f"{what}: q, k and v must share one dtype")
+    if tuple(k.shape) != (B, H, N, D) or tuple(v.shape) != (B, H, N, D):
+        raise ValueError(f"{what}: k and v must be {(B, H, N, D)}")
+    if tuple(q16.shape) != (B, M, 16) or tuple(k16.shape) != (B, M, 16):
+        raise ValueError(f"{what}: q16 and k16 must be {(B, M, 16)}")
+    idx_dtype = q.dtype if q16.dtype == q.dtype and k16.dtype == q.dtype else torch.float32
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q, k, v = (t.detach().contiguous() for t in (q, k, v))
+    q16 = q16.detach().to(idx_dtype).contiguous()
+    k16 = k16.detach().to(idx_dtype).contiguous()
+    out = torch.empty_like(q)
+    sel = torch.empty(B, M, max_remote_blocks, dtype=torch.int32, device=q.device) if return_selection else None
+    dev = q.device
+    st = _lib.lib().fsi_sram_indexer_attention(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _SRAM_DTYPES[q.dtype], q16.data_ptr(), k16.data_ptr(),
+        _SRAM_DTYPES[idx_dtype], B, H, N, D, block_size, max_remote_blocks, float(scale), float(top_p),
+        out.data_ptr(), _lib.ptr(sel), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return (out, sel) if return_selection else out
+
+
+def triton_fused_sram_indexer_attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    q16: Tensor,
+    k16: Tensor,
+    scale: Optional[float] = None,
+    top_p: float = 0.8,
+    max_remote_blocks: int = 2,
+    block_size: int = 16,
+) -> Tensor:
+    """Foveal sparse attention with the 16-D indexing and routing fused into the
+    attention launch (triton_ops.py:373-435, kernel :142-249): query block m
+    scores all blocks with q16 . k16 / 4, softmaxes over the other blocks, takes
+    up to max_remote_blocks greedy picks while the picked mass stays below top_p
+    (each pick > 1e-4), and attends its own block plus the picks (no causal
+    mask).  q, k, v: (B, H, N, D); q16, k16: (B, N / block_size, 16).  The
+    `triton_` name is kept for compatibility; the kernel is HIP."""
+    return sram_indexer_attention(q, k, v, q16, k16, scale=scale, top_p=top_p, max_remote_blocks=max_remote_blocks,
+                                  block_size=block_size)
+
+
 class FovealSparseAttention(nn.Module):
     """Causal foveal sparse attention (attention.py:97-379): same constructor,
     parameters (state_dict compatible), `init_kv_cache` and `decode_step`.

@@ -46,7 +46,9 @@ typedef enum fsi_status {
   FSI_ERR_WORKSPACE = -8     /* workspace missing or smaller than required        */
 } fsi_status;
 
-typedef enum fsi_dtype { FSI_DTYPE_F32 = 0, FSI_DTYPE_BF16 = 1 } fsi_dtype;
+/* FSI_DTYPE_F16 is accepted only where an entry point says so
+ * (fsi_sram_indexer_attention). */
+typedef enum fsi_dtype { FSI_DTYPE_F32 = 0, FSI_DTYPE_BF16 = 1, FSI_DTYPE_F16 = 2 } fsi_dtype;
 
 /* Size of the zero-initialised arrival-counter area at the start of every workspace. */
 #define FSI_WORKSPACE_COUNTER_BYTES 65536
@@ -458,6 +460,24 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
                             const int32_t* counts, int64_t cs_b, int64_t cs_q, float scale, int dtype, void* out,
                             int64_t os_b, int64_t os_h, int64_t os_t, void* workspace, size_t workspace_bytes,
                             int* err, void* stream);
+
+/* Fused 16-D block indexer + greedy block selection + block attention
+ * (triton_fused_sram_indexer_attention, foveal_indexer/triton_ops.py:142-249,373-435).
+ * q, k, v, out: contiguous (B, H, N, head_dim) of `dtype` (F32, BF16 or F16;
+ * fp32 math); q16, k16: contiguous (B, N / block_size, 16), shared by the heads,
+ * of idx_dtype (`dtype` or F32).  Query block m scores every block j by <q16[m], k16[j]> / 4,
+ * softmaxes over j != m (sum + 1e-6), then takes max_remote greedy picks (largest
+ * remaining probability, lowest index on ties); a pick is attended iff the mass
+ * of the picks before it is < top_p and its probability > 1e-4.  The block's
+ * queries attend the self block then the attended picks (no causal mask).
+ * selected (optional, int32 [B, N / block_size, max_remote]) receives each
+ * pick's block, or -1 where the pick is not attended.  Limits: block_size <= 64,
+ * head_dim <= 256, block_size * head_dim <= 8192, N / block_size <= 8192,
+ * max_remote <= 64, B * H <= 65535 (FSI_ERR_CAPACITY). */
+FSI_API int fsi_sram_indexer_attention(const void* q, const void* k, const void* v, int dtype, const void* q16,
+                                       const void* k16, int idx_dtype, int64_t B, int64_t H, int64_t N, int64_t head_dim,
+                                       int64_t block_size, int64_t max_remote, float scale, float top_p, void* out,
+                                       int32_t* selected, void* stream);
 
 /* ------------------------------------------------------------------------- *
  * Block-sparse GEMMs (bf16 in, fp32 accumulate, bf16 out) on 128 x 128 MFMA

@@ -19,6 +19,12 @@
                            (the Triton kernel's clamp of l at 1e-6)
   * prefill_forward        FovealSparseAttention.forward (attention.py:180-269) with
                            a given route, and its teacher page mass (:243-265)
+  * sram_select            the in-kernel routing of triton_fused_sram_indexer_attention
+                           (triton_ops.py:164-182,219-245) in fp32: 16-D scores / 4,
+                           softmax over the other blocks (+1e-6), greedy picks gated by
+                           mass < top_p and p > 1e-4
+  * sram_attention_f64     that kernel's attention (triton_ops.py:186-248) as fp64
+                           softmax attention over the self block plus the attended picks
 """
 from __future__ import annotations
 
@@ -199,3 +205,46 @@ def prefill_forward(m, x: Tensor, remote_indices: Tensor, remote_counts: Tensor)
     probs = torch.softmax(s, dim=-1)[:, :, ::ps]
     teacher = probs.view(B, m.num_heads, pages, pages, ps).sum(dim=-1).mean(dim=1)
     return out, teacher
+
+
+def sram_select(q16: Tensor, k16: Tensor, top_p: float, max_remote: int):
+    """Greedy block picks of triton_ops.py:164-182,219-245 in fp32.  q16, k16:
+    (B, M, 16).  Returns (picks (B, M, max_remote) int64 with -1 where a pick is
+    not attended, probs (B, M, M) float32 before any pick is retired)."""
+    B, M, _ = q16.shape
+    s = torch.matmul(q16.float(), k16.float().transpose(1, 2)) * 0.25
+    remote = ~torch.eye(M, dtype=torch.bool)[None].expand(B, -1, -1)
+    s = torch.where(remote, s, torch.full_like(s, -1.0e4))
+    mx = s.amax(dim=-1, keepdim=True)
+    e = torch.where(remote, torch.exp(s - mx), torch.zeros_like(s))
+    probs = e / (e.sum(dim=-1, keepdim=True) + 1e-6)
+    picks = torch.full((B, M, max_remote), -1, dtype=torch.int64)
+    left = probs.clone()
+    for b in range(B):
+        for m in range(M):
+            mass = torch.zeros((), dtype=torch.float32)
+            row = left[b, m]
+            for r in range(max_remote):
+                best = int(torch.argmax(row))  # first index of the maximum
+                bp = row[best].clone()
+                if bool(mass < top_p) and bool(bp > 1e-4):
+                    picks[b, m, r] = best
+                mass = mass + bp
+                row[best] = -1.0
+    return picks, probs
+
+
+def sram_attention_f64(q: Tensor, k: Tensor, v: Tensor, picks: Tensor, block: int, scale: float) -> Tensor:
+    """Attention of every query of block m over the keys of block m and of each
+    attended pick (triton_ops.py:186-248), fp64.  q, k, v: (B, H, N, D); picks:
+    (B, N / block, R) with -1 for a pick that is not attended."""
+    B, H, N, D = q.shape
+    w = torch.zeros(B, N, N, dtype=torch.float64)
+    for b in range(B):
+        for m in range(N // block):
+            rows = slice(m * block, (m + 1) * block)
+            w[b, rows, m * block:(m + 1) * block] = 1.0
+            for kb in picks[b, m].tolist():
+                if kb >= 0:
+                    w[b, rows, kb * block:(kb + 1) * block] = 1.0
+    return weighted_attention_f64(q, k, v, w, scale)

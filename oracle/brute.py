@@ -117,3 +117,31 @@ def tile_route_row(scores, top_p):
         if running < top_p:
             below += 1
     return ranked[: min(below + 1, len(scores))]
+
+
+def sram_pick_row(scores, m, top_p, max_remote):
+    """Greedy picks of one query block m from its raw 16-D scores (already / 4):
+    fp64 softmax over the blocks other than m with the 1e-6 pad, then per round
+    the largest remaining probability (first index on ties), attended iff the
+    mass of all earlier rounds is < top_p and it is > 1e-4; retired either way.
+    Returns the picks, -1 where not attended."""
+    n = len(scores)
+    others = [j for j in range(n) if j != m]
+    probs = [0.0] * n
+    if others:
+        top = max(scores[j] for j in others)
+        top = max(top, -1.0e4)
+        z = sum(math.exp(scores[j] - top) for j in others) + 1e-6
+        for j in others:
+            probs[j] = math.exp(scores[j] - top) / z
+    out, mass = [], 0.0
+    for _ in range(max_remote):
+        best = 0
+        for j in range(1, n):
+            if probs[j] > probs[best]:
+                best = j
+        p = probs[best]
+        out.append(best if (mass < top_p and p > 1e-4) else -1)
+        mass += p
+        probs[best] = -1.0
+    return out

@@ -317,3 +317,25 @@ def raise_device_errors(device: torch.device, what: str) -> None:
     if code != 0:
         e.zero_()
         raise _EXC.get(code, RuntimeError)(f"{what}: device reported: {lib().fsi_status_string(code).decode()}")
+
+
+# ---------------------------------------------------------------------------
+# torch.library registration.  Every kernel launch of the package is a custom op
+# torch.ops.fsi.<name>: its schema comes from the launch function's annotations,
+# `fake` gives the output shapes / dtypes for FakeTensor tracing (torch.compile,
+# torch.export), and the modules' autograd Functions call the forward and
+# backward ops, so a compiled graph holds the HIP launches as single nodes.
+# ---------------------------------------------------------------------------
+NAMESPACE = "fsi"
+
+
+def fsi_op(name: str, fake, mutates_args=()):
+    """Decorator: register `fn` as torch.ops.fsi.<name> and return the op (calling
+    it dispatches through torch.ops)."""
+
+    def deco(fn):
+        op = torch.library.custom_op(f"{NAMESPACE}::{name}", fn, mutates_args=mutates_args)
+        op.register_fake(fake)
+        return op
+
+    return deco

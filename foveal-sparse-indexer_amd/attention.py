@@ -73,17 +73,39 @@ def decode_route(
     else:
         pos_val = int(pos)
     cap = max(int(max_remote_blocks), int(min_remote_blocks), 1)
-    pages = torch.empty((B, cap), dtype=torch.int32, device=dev)
-    counts = torch.empty((B,), dtype=torch.int32, device=dev)
-    ctx = torch.empty((B, d), dtype=q2.dtype, device=dev) if return_context else None
-    st = _lib.lib().fsi_decode_route(
-        q2.data_ptr(), kpc.data_ptr(), _lib.ptr(vpc), code, B, P, d, _lib.ptr(pos_rows), pos_val, int(page_size),
-        int(local_window), int(completed_pages), float(top_p), int(min_remote_blocks), int(max_remote_blocks), cap,
-        pages.data_ptr(), counts.data_ptr(), _lib.ptr(ctx), _lib.stream_handle(dev))
-    _lib.check(st, what)
+    pages, counts, ctx = _decode_route_op(q2, kpc, vpc, pos_rows, pos_val, int(page_size), int(local_window),
+                                          int(completed_pages), float(top_p), int(min_remote_blocks),
+                                          int(max_remote_blocks), cap, bool(return_context))
     if return_context:
         return pages, counts, ctx
     return pages, counts
+
+
+def _decode_route_fake(q2, kp, vp, pos_rows, pos_val, page_size, local_window, completed, top_p, k_min, k_max, cap,
+                       want_ctx):
+    B, d = q2.shape
+    return (q2.new_empty((B, cap), dtype=torch.int32), q2.new_empty((B,), dtype=torch.int32),
+            q2.new_empty((B, d) if want_ctx else (0,)))
+
+
+@_lib.fsi_op("decode_route", _decode_route_fake)
+def _decode_route_op(q2: Tensor, kp: Tensor, vp: Optional[Tensor], pos_rows: Optional[Tensor], pos_val: int,
+                     page_size: int, local_window: int, completed: int, top_p: float, k_min: int, k_max: int,
+                     cap: int, want_ctx: bool) -> Tuple[Tensor, Tensor, Tensor]:
+    """fsi_decode_route: (pages (B, cap) int32, counts (B,) int32, context (B, 16) or empty)."""
+    what = "decode_route"
+    dev = q2.device
+    B, d = q2.shape
+    P = kp.shape[1]
+    pages = torch.empty((B, cap), dtype=torch.int32, device=dev)
+    counts = torch.empty((B,), dtype=torch.int32, device=dev)
+    ctx = torch.empty((B, d) if want_ctx else (0,), dtype=q2.dtype, device=dev)
+    st = _lib.lib().fsi_decode_route(
+        q2.data_ptr(), kp.data_ptr(), _lib.ptr(vp), _lib.dtype_code(q2.dtype, what), B, P, d, _lib.ptr(pos_rows),
+        pos_val, page_size, local_window, completed, top_p, k_min, k_max, cap, pages.data_ptr(), counts.data_ptr(),
+        ctx.data_ptr() if want_ctx else None, _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return pages, counts, ctx
 
 
 PAGE_SIZE = 64
@@ -184,15 +206,8 @@ class FovealKVCache:
             k = k.contiguous()
         if v.stride(-1) != 1:
             v = v.contiguous()
-        dev = _lib.require_gpu(k, v, self.k_cache, what=what)
-        err = _lib.error_word(dev)
-        st = _lib.lib().fsi_kv_write(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2), v.stride(0),
-                                     v.stride(1), v.stride(2), B, H, n, hd, None, start, self.page_table.data_ptr(),
-                                     self.max_pages, self.n_phys_pages, self.k_cache.data_ptr(),
-                                     self.v_cache.data_ptr(), err.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
-        if _lib.checks_enabled():
-            _lib.raise_device_errors(dev, what)
+        _lib.require_gpu(k, v, self.k_cache, what=what)
+        _kv_write_op(k, v, int(start), self.page_table, self.max_pages, self.n_phys_pages, self.k_cache, self.v_cache)
 
     def update(self, k_step: Tensor, v_step: Tensor, ki_step: Tensor, vi_step: Tensor) -> int:
         """Append one token's KV and 16-D index representation (attention.py:62-94)."""
@@ -206,12 +221,7 @@ class FovealKVCache:
             self.partial_kp[:, offset] = ki_step.reshape(self.batch_size, self.index_dim)
             self.partial_vp[:, offset] = vi_step.reshape(self.batch_size, self.index_dim)
         if offset == self.page_size - 1:
-            dev = self.kp_cache.device
-            st = _lib.lib().fsi_kv_page_pool(
-                self.partial_kp.data_ptr(), self.partial_vp.data_ptr(), _lib.dtype_code(self.dtype, "kv_page_pool"),
-                self.batch_size, self.page_size, self.index_dim, self.kp_cache[:, page].data_ptr(),
-                self.vp_cache[:, page].data_ptr(), self.max_pages * self.index_dim, _lib.stream_handle(dev))
-            _lib.check(st, "FovealKVCache.update")
+            _kv_page_pool_op(self.partial_kp, self.partial_vp, self.kp_cache, self.vp_cache, page)
             self.completed_pages += 1
         self.seq_len += 1
         return pos
@@ -229,21 +239,62 @@ class FovealKVCache:
             sel = batch if batch is not None else slice(None)
             return self.k_cache[sel, :, :n].clone(), self.v_cache[sel, :, :n].clone()
         rows = self.page_table[batch] if batch is not None else self.page_table
-        rows = rows.contiguous()
-        shape = (rows.shape[0], self.num_kv_heads, n, self.head_dim)
-        k = torch.empty(shape, dtype=self.dtype, device=self.k_cache.device)
-        v = torch.empty_like(k)
-        st = _lib.lib().fsi_kv_read(self.k_cache.data_ptr(), self.v_cache.data_ptr(), rows.shape[0],
-                                    self.num_kv_heads, n, self.head_dim, rows.data_ptr(), self.max_pages,
-                                    self.n_phys_pages, k.data_ptr(), v.data_ptr(),
-                                    _lib.stream_handle(self.k_cache.device))
-        _lib.check(st, "FovealKVCache.to_dense")
-        return k, v
+        return _kv_read_op(self.k_cache, self.v_cache, rows.contiguous(), self.num_kv_heads, n, self.head_dim,
+                           self.max_pages, self.n_phys_pages)
 
 
-def _decode_attention_launch(q3: Tensor, cache: FovealKVCache, pos_rows: Optional[Tensor], pos_val: int,
-                             window: int, remote_pages: Optional[Tensor], remote_counts: Optional[Tensor], cap: int,
-                             scale: float, out: Tensor) -> Tensor:
+@_lib.fsi_op("kv_write", lambda k, v, start, page_table, max_pages, n_phys, k_cache, v_cache: None,
+             mutates_args=("k_cache", "v_cache"))
+def _kv_write_op(k: Tensor, v: Tensor, start: int, page_table: Tensor, max_pages: int, n_phys: int, k_cache: Tensor,
+                 v_cache: Tensor) -> None:
+    """fsi_kv_write: (B, H, n, hd) K/V at positions start .. start + n - 1 into the paged pool."""
+    what = "FovealKVCache"
+    dev = k.device
+    B, H, n, hd = k.shape
+    err = _lib.error_word(dev)
+    st = _lib.lib().fsi_kv_write(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2), v.stride(0),
+                                 v.stride(1), v.stride(2), B, H, n, hd, None, start, page_table.data_ptr(), max_pages,
+                                 n_phys, k_cache.data_ptr(), v_cache.data_ptr(), err.data_ptr(),
+                                 _lib.stream_handle(dev))
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+
+
+@_lib.fsi_op("kv_page_pool", lambda partial_kp, partial_vp, kp_cache, vp_cache, page: None,
+             mutates_args=("kp_cache", "vp_cache"))
+def _kv_page_pool_op(partial_kp: Tensor, partial_vp: Tensor, kp_cache: Tensor, vp_cache: Tensor, page: int) -> None:
+    """fsi_kv_page_pool: mean of the page's 16-D rows into kp_cache[:, page] / vp_cache[:, page]."""
+    B, page_size, d = partial_kp.shape
+    st = _lib.lib().fsi_kv_page_pool(
+        partial_kp.data_ptr(), partial_vp.data_ptr(), _lib.dtype_code(partial_kp.dtype, "kv_page_pool"), B,
+        page_size, d, kp_cache[:, page].data_ptr(), vp_cache[:, page].data_ptr(), kp_cache.shape[1] * d,
+        _lib.stream_handle(kp_cache.device))
+    _lib.check(st, "FovealKVCache.update")
+
+
+def _kv_read_fake(k_cache, v_cache, rows, heads, n, hd, max_pages, n_phys):
+    k = k_cache.new_empty((rows.shape[0], heads, n, hd))
+    return k, torch.empty_like(k)
+
+
+@_lib.fsi_op("kv_read", _kv_read_fake)
+def _kv_read_op(k_cache: Tensor, v_cache: Tensor, rows: Tensor, heads: int, n: int, hd: int, max_pages: int,
+                n_phys: int) -> Tuple[Tensor, Tensor]:
+    """fsi_kv_read: positions [0, n) of the sequences whose page-table rows are given, (b, H, n, hd)."""
+    k = torch.empty((rows.shape[0], heads, n, hd), dtype=k_cache.dtype, device=k_cache.device)
+    v = torch.empty_like(k)
+    st = _lib.lib().fsi_kv_read(k_cache.data_ptr(), v_cache.data_ptr(), rows.shape[0], heads, n, hd, rows.data_ptr(),
+                                max_pages, n_phys, k.data_ptr(), v.data_ptr(), _lib.stream_handle(k_cache.device))
+    _lib.check(st, "FovealKVCache.to_dense")
+    return k, v
+
+
+def _decode_launch(q3: Tensor, k_cache: Tensor, v_cache: Tensor, page_table: Optional[Tensor], max_pages: int,
+                   n_phys: int, max_seq_len: int, page_size: int, n_kv_heads: int, pos_rows: Optional[Tensor],
+                   pos_val: int, window: int, remote_pages: Optional[Tensor], remote_counts: Optional[Tensor],
+                   cap: int, scale: float, out: Tensor) -> Tensor:
+    """Paged pool (page_table given): fsi_decode_attn; contiguous cache: fsi_decode_attn_dense."""
     what = "decode_attention"
     dev = q3.device
     B, Hq, hd = q3.shape
@@ -252,24 +303,48 @@ def _decode_attention_launch(q3: Tensor, cache: FovealKVCache, pos_rows: Optiona
     err = _lib.error_word(dev)
     rp = _lib.ptr(remote_pages) if cap else None
     rc = _lib.ptr(remote_counts) if cap else None
-    if cache.paged:
-        ws = _lib.workspace(dev, L.fsi_decode_attn_workspace_size(B, Hq, cache.num_kv_heads, hd, window, cap,
-                                                                   cache.max_pages), stream)
-        st = L.fsi_decode_attn(q3.data_ptr(), cache.k_cache.data_ptr(), cache.v_cache.data_ptr(),
-                               cache.page_table.data_ptr(), cache.max_pages, cache.n_phys_pages, _lib.ptr(pos_rows),
-                               pos_val, int(window), rp, rc, cap, B, Hq, cache.num_kv_heads, hd, float(scale),
-                               out.data_ptr(), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
+    if page_table is not None:
+        ws = _lib.workspace(dev, L.fsi_decode_attn_workspace_size(B, Hq, n_kv_heads, hd, window, cap, max_pages),
+                            stream)
+        st = L.fsi_decode_attn(q3.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), page_table.data_ptr(),
+                               max_pages, n_phys, _lib.ptr(pos_rows), pos_val, window, rp, rc, cap, B, Hq, n_kv_heads,
+                               hd, scale, out.data_ptr(), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
     else:
-        k, v = cache.k_cache, cache.v_cache
+        k, v = k_cache, v_cache
         st = L.fsi_decode_attn_dense(q3.data_ptr(), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
-                                     k.stride(2), v.stride(0), v.stride(1), v.stride(2), cache.max_seq_len,
-                                     _lib.ptr(pos_rows), pos_val, int(window), cache.page_size, rp, rc, cap, B, Hq,
-                                     cache.num_kv_heads, hd, float(scale), _lib.dtype_code(q3.dtype, what),
-                                     out.data_ptr(), err.data_ptr(), stream)
+                                     k.stride(2), v.stride(0), v.stride(1), v.stride(2), max_seq_len,
+                                     _lib.ptr(pos_rows), pos_val, window, page_size, rp, rc, cap, B, Hq, n_kv_heads,
+                                     hd, scale, _lib.dtype_code(q3.dtype, what), out.data_ptr(), err.data_ptr(),
+                                     stream)
     _lib.check(st, what)
     if _lib.checks_enabled():
         _lib.raise_device_errors(dev, what)
     return out
+
+
+@_lib.fsi_op("decode_attention", lambda q3, *rest: torch.empty_like(q3))
+def _decode_op(q3: Tensor, k_cache: Tensor, v_cache: Tensor, page_table: Optional[Tensor], max_pages: int,
+               n_phys: int, max_seq_len: int, page_size: int, n_kv_heads: int, pos_rows: Optional[Tensor],
+               pos_val: int, window: int, remote_pages: Optional[Tensor], remote_counts: Optional[Tensor], cap: int,
+               scale: float) -> Tensor:
+    """Decode attention into a new (B, Hq, hd) tensor."""
+    return _decode_launch(q3, k_cache, v_cache, page_table, max_pages, n_phys, max_seq_len, page_size, n_kv_heads,
+                          pos_rows, pos_val, window, remote_pages, remote_counts, cap, scale, torch.empty_like(q3))
+
+
+def _cache_args(cache: FovealKVCache):
+    return (cache.k_cache, cache.v_cache, cache.page_table if cache.paged else None, cache.max_pages,
+            cache.n_phys_pages if cache.paged else 0, cache.max_seq_len, cache.page_size, cache.num_kv_heads)
+
+
+def _decode_attention_launch(q3: Tensor, cache: FovealKVCache, pos_rows: Optional[Tensor], pos_val: int,
+                             window: int, remote_pages: Optional[Tensor], remote_counts: Optional[Tensor], cap: int,
+                             scale: float, out: Optional[Tensor] = None) -> Tensor:
+    args = (*_cache_args(cache), pos_rows, int(pos_val), int(window), remote_pages, remote_counts, int(cap),
+            float(scale))
+    if out is None:
+        return _decode_op(q3, *args)
+    return _decode_launch(q3, *args, out)
 
 
 def _decode_support(cache: FovealKVCache, b: int, pos: int, window: int, pages: List[int]):
@@ -292,8 +367,7 @@ class _DecodeAttnFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q3, cache, pos_rows, pos_val, window, remote_pages, remote_counts, cap, scale):
-        out = torch.empty_like(q3)
-        _decode_attention_launch(q3, cache, pos_rows, pos_val, window, remote_pages, remote_counts, cap, scale, out)
+        out = _decode_attention_launch(q3, cache, pos_rows, pos_val, window, remote_pages, remote_counts, cap, scale)
         ctx.cache, ctx.meta = cache, (pos_val, window, cap, scale)
         ctx.save_for_backward(q3, pos_rows, remote_pages, remote_counts)
         return out
@@ -364,8 +438,6 @@ def decode_attention(
         if out is not None:
             out.copy_(res.detach())
         return res
-    if out is None:
-        out = torch.empty((B, Hq, hd), dtype=q3.dtype, device=dev)
     return _decode_attention_launch(q3.detach().contiguous(), cache, pos_rows, pos_val, int(window), remote_pages,
                                     remote_counts, cap, float(scale), out)
 
@@ -405,6 +477,18 @@ def _sparse_attention_launch(q, k, v, lists, counts, cap, block, mode, window, s
     return out
 
 
+def _sparse_out(q: Tensor) -> Tensor:
+    B, Hq, T, hd = q.shape
+    return q.new_empty((B, T, Hq, hd)).transpose(1, 2)
+
+
+@_lib.fsi_op("sparse_attention", lambda q, k, v, lists, counts, cap, block, mode, window, scale: _sparse_out(q))
+def _sparse_attn_op(q: Tensor, k: Tensor, v: Tensor, lists: Optional[Tensor], counts: Tensor, cap: int, block: int,
+                    mode: int, window: int, scale: float) -> Tensor:
+    """fsi_sparse_attn into a new (B, Hq, T, hd) tensor laid out as (B, T, Hq, hd)."""
+    return _sparse_attention_launch(q, k, v, lists, counts, cap, block, mode, window, scale, _sparse_out(q))
+
+
 def _sparse_logit_bias(lists, counts, cap, B, T, block, mode, window, dev):
     """(B, 1, T, T) additive logit bias of a sparse pattern: 0 for an allowed key
     (log of its multiplicity for block lists), -inf elsewhere.  The dense form of
@@ -439,9 +523,7 @@ class _SparseAttnFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, lists, counts, cap, block, mode, window, scale):
-        B, Hq, T, hd = q.shape
-        out = torch.empty((B, T, Hq, hd), dtype=q.dtype, device=q.device).transpose(1, 2)
-        _sparse_attention_launch(q, k, v, lists, counts, cap, block, mode, window, scale, out)
+        out = _sparse_attn_op(q, k, v, lists, counts, cap, block, mode, window, scale)
         ctx.save_for_backward(q, k, v, lists, counts)
         ctx.meta = (cap, block, mode, window, scale)
         return out
@@ -521,8 +603,9 @@ def sparse_attention(
             out.copy_(res.detach())
         return res
     if out is None:
-        out = torch.empty((B, T, Hq, hd), dtype=qa.dtype, device=dev).transpose(1, 2)
-    elif tuple(out.shape) != (B, Hq, T, hd) or out.dtype != qa.dtype or out.stride(3) != 1:
+        return _sparse_attn_op(qa.detach(), ka.detach(), va.detach(), lists, counts, cap, int(block), int(mode),
+                               int(window), float(scale))
+    if tuple(out.shape) != (B, Hq, T, hd) or out.dtype != qa.dtype or out.stride(3) != 1:
         raise ValueError(f"{what}: out must be a (B, Hq, T, hd) {qa.dtype} tensor with unit stride over hd")
     return _sparse_attention_launch(qa.detach(), ka.detach(), va.detach(), lists, counts, cap, block, mode, window,
                                     scale, out)
@@ -595,15 +678,30 @@ def sram_indexer_attention(
     q, k, v = (t.detach().contiguous() for t in (q, k, v))
     q16 = q16.detach().to(idx_dtype).contiguous()
     k16 = k16.detach().to(idx_dtype).contiguous()
+    out, sel = _sram_op(q, k, v, q16, k16, float(scale), float(top_p), int(max_remote_blocks), int(block_size),
+                        bool(return_selection))
+    return (out, sel) if return_selection else out
+
+
+def _sram_fake(q, k, v, q16, k16, scale, top_p, max_remote, block_size, want_sel):
+    B, M = q16.shape[0], q16.shape[1]
+    return torch.empty_like(q), q.new_empty((B, M, max_remote) if want_sel else (0,), dtype=torch.int32)
+
+
+@_lib.fsi_op("sram_indexer_attention", _sram_fake)
+def _sram_op(q: Tensor, k: Tensor, v: Tensor, q16: Tensor, k16: Tensor, scale: float, top_p: float, max_remote: int,
+             block_size: int, want_sel: bool) -> Tuple[Tensor, Tensor]:
+    """fsi_sram_indexer_attention: (out (B, H, N, D), picks (B, M, max_remote) int32 or empty)."""
+    B, H, N, D = q.shape
+    M = q16.shape[1]
     out = torch.empty_like(q)
-    sel = torch.empty(B, M, max_remote_blocks, dtype=torch.int32, device=q.device) if return_selection else None
-    dev = q.device
+    sel = torch.empty((B, M, max_remote) if want_sel else (0,), dtype=torch.int32, device=q.device)
     st = _lib.lib().fsi_sram_indexer_attention(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), _SRAM_DTYPES[q.dtype], q16.data_ptr(), k16.data_ptr(),
-        _SRAM_DTYPES[idx_dtype], B, H, N, D, block_size, max_remote_blocks, float(scale), float(top_p),
-        out.data_ptr(), _lib.ptr(sel), _lib.stream_handle(dev))
-    _lib.check(st, what)
-    return (out, sel) if return_selection else out
+        _SRAM_DTYPES[q16.dtype], B, H, N, D, block_size, max_remote, scale, top_p, out.data_ptr(),
+        sel.data_ptr() if want_sel else None, _lib.stream_handle(q.device))
+    _lib.check(st, "triton_fused_sram_indexer_attention")
+    return out, sel
 
 
 def triton_fused_sram_indexer_attention(

@@ -41,6 +41,14 @@ def _linear_launch(x2d: Tensor, weight: Tensor, bias: Optional[Tensor], idx: Ten
     return out
 
 
+@_lib.fsi_op("block_sparse_linear", lambda x2d, weight, bias, idx, block_size:
+             x2d.new_empty((x2d.shape[0], weight.shape[0])))
+def _linear_op(x2d: Tensor, weight: Tensor, bias: Optional[Tensor], idx: Tensor, block_size: int) -> Tensor:
+    """fsi_block_sparse_linear into a new (M, N) tensor."""
+    out = torch.empty((x2d.shape[0], weight.shape[0]), dtype=x2d.dtype, device=x2d.device)
+    return _linear_launch(x2d, weight, bias, idx, block_size, out)
+
+
 def _column_mask(idx: Tensor, n_blocks: int, block_size: int) -> Tensor:
     """(N,) float mask of the active column blocks' output columns."""
     m = torch.zeros(n_blocks, dtype=torch.float32, device=idx.device)
@@ -57,8 +65,7 @@ class _BlockSparseLinearFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x2d, weight, bias, idx, block_size):
-        out = torch.empty((x2d.shape[0], weight.shape[0]), dtype=x2d.dtype, device=x2d.device)
-        _linear_launch(x2d, weight, bias, idx, block_size, out)
+        out = _linear_op(x2d, weight, bias, idx, block_size)
         ctx.save_for_backward(x2d, weight, idx)
         ctx.block_size, ctx.has_bias = block_size, bias is not None
         return out
@@ -98,7 +105,7 @@ def block_sparse_linear(x2d: Tensor, weight: Tensor, bias: Optional[Tensor], act
             out.copy_(res.detach())
         return res
     if out is None:
-        out = torch.empty((M, N), dtype=x2d.dtype, device=dev)
+        return _linear_op(x2d, weight, bias, idx, int(block_size))
     return _linear_launch(x2d, weight, bias, idx, int(block_size), out)
 
 
@@ -138,7 +145,7 @@ def blockwise_matmul(x2d: Tensor, weight: Tensor, tile_mask: Tensor, block_k: in
             out.copy_(res.detach())
         return res
     if out is None:
-        out = torch.empty((M, weight.shape[0]), dtype=x2d.dtype, device=dev)
+        return _blockwise_op(x2d, weight, m8, int(block_k), int(block_n), int(rpg))
     return _blockwise_launch(x2d, weight, m8, int(block_k), int(block_n), int(rpg), out)
 
 
@@ -158,6 +165,14 @@ def _blockwise_launch(x2d: Tensor, weight: Tensor, m8: Tensor, block_k: int, blo
     return out
 
 
+@_lib.fsi_op("blockwise_matmul", lambda x2d, weight, m8, block_k, block_n, rpg:
+             x2d.new_empty((x2d.shape[0], weight.shape[0])))
+def _blockwise_op(x2d: Tensor, weight: Tensor, m8: Tensor, block_k: int, block_n: int, rpg: int) -> Tensor:
+    """fsi_blockwise_matmul into a new (M, N) tensor."""
+    out = torch.empty((x2d.shape[0], weight.shape[0]), dtype=x2d.dtype, device=x2d.device)
+    return _blockwise_launch(x2d, weight, m8, block_k, block_n, rpg, out)
+
+
 def _expand_tiles(m: Tensor, N: int, K: int, block_k: int, block_n: int) -> Tensor:
     """(nkb * nnb,) k-major tile mask -> (N, K) element mask of the weight."""
     nkb, nnb = K // block_k, N // block_n
@@ -172,8 +187,7 @@ class _BlockwiseMatmulFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x2d, weight, m8, block_k, block_n, rpg):
-        out = torch.empty((x2d.shape[0], weight.shape[0]), dtype=x2d.dtype, device=x2d.device)
-        _blockwise_launch(x2d, weight, m8, block_k, block_n, rpg, out)
+        out = _blockwise_op(x2d, weight, m8, block_k, block_n, rpg)
         ctx.save_for_backward(x2d, weight, m8)
         ctx.meta = (block_k, block_n, rpg)
         return out
@@ -210,17 +224,35 @@ def tile_route(scores: Tensor, top_p: float, base_tiles: int, rows_per_group: Op
         raise ValueError(f"{what}: scores must be (rows, tiles), got {tuple(scores.shape)}")
     if scores.stride(1) != 1:
         scores = scores.contiguous()
-    rows, T = scores.shape
+    rows = scores.shape[0]
     rpg = max(rows, 1) if rows_per_group is None else int(rows_per_group)
+    mask, probs, needed = _tile_route_op(scores, float(top_p), int(base_tiles), rpg)
+    return mask.view(torch.bool), probs, needed
+
+
+def _tile_route_fake(scores, top_p, base_tiles, rpg):
+    rows, T = scores.shape
+    groups = max(1, -(-rows // rpg)) if rows else 1
+    return (scores.new_empty((groups, T), dtype=torch.uint8), scores.new_empty((rows, T)),
+            scores.new_empty((rows,), dtype=torch.int32))
+
+
+@_lib.fsi_op("tile_route", _tile_route_fake)
+def _tile_route_op(scores: Tensor, top_p: float, base_tiles: int, rpg: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """fsi_tile_route: (mask (groups, T) uint8, probs (rows, T), needed (rows,) int32)."""
+    what = "tile_route"
+    dev = scores.device
+    rows, T = scores.shape
     groups = max(1, -(-rows // rpg)) if rows else 1
     mask = torch.empty((groups, T), dtype=torch.uint8, device=dev)
     probs = torch.empty((rows, T), dtype=scores.dtype, device=dev)
     needed = torch.empty((rows,), dtype=torch.int32, device=dev)
-    st = _lib.lib().fsi_tile_route(scores.data_ptr() if rows else None, code, rows, T, max(scores.stride(0), T), rpg,
-                                   int(base_tiles), float(top_p), mask.data_ptr(), needed.data_ptr() if rows else None,
-                                   probs.data_ptr() if rows else None, _lib.stream_handle(dev))
+    st = _lib.lib().fsi_tile_route(scores.data_ptr() if rows else None, _lib.dtype_code(scores.dtype, what), rows, T,
+                                   max(scores.stride(0), T), rpg, base_tiles, top_p, mask.data_ptr(),
+                                   needed.data_ptr() if rows else None, probs.data_ptr() if rows else None,
+                                   _lib.stream_handle(dev))
     _lib.check(st, what)
-    return mask.view(torch.bool), probs, needed
+    return mask, probs, needed
 
 
 def _eval_active_blocks(block_scores: Tensor, base_blocks: int, top_p: float, max_remote: int, num_blocks: int):

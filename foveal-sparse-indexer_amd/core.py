@@ -22,7 +22,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 from torch import Tensor, nn
@@ -50,36 +50,46 @@ def _as_3d(scores: Tensor, what: str) -> Tensor:
     return scores.contiguous()
 
 
+@_lib.fsi_op("masked_softmax", lambda s3, m8: torch.empty_like(s3))
+def _masked_softmax_op(s3: Tensor, m8: Tensor) -> Tensor:
+    """s3: contiguous (B, Q, N) scores; m8: uint8 mask view over (B, Q, N)."""
+    what = "masked_softmax"
+    dev = s3.device
+    code = _lib.dtype_code(s3.dtype, what)
+    out = torch.empty_like(s3)
+    B, Q, N = s3.shape
+    st = _lib.lib().fsi_masked_softmax(s3.data_ptr(), code, B, Q, N, m8.data_ptr(), m8.stride(0), m8.stride(1),
+                                       m8.stride(2), out.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return out
+
+
+@_lib.fsi_op("masked_softmax_bwd", lambda s3, g, m8: torch.empty_like(s3))
+def _masked_softmax_bwd_op(s3: Tensor, g: Tensor, m8: Tensor) -> Tensor:
+    what = "masked_softmax backward"
+    dev = _lib.require_gpu(g, s3, what=what)
+    gc = g.to(s3.dtype).contiguous()
+    ds = torch.empty_like(s3)
+    B, Q, N = s3.shape
+    st = _lib.lib().fsi_masked_softmax_bwd(s3.data_ptr(), gc.data_ptr(), _lib.dtype_code(s3.dtype, what), B, Q, N,
+                                           m8.data_ptr(), m8.stride(0), m8.stride(1), m8.stride(2), ds.data_ptr(),
+                                           _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return ds
+
+
 class _MaskedSoftmaxFn(torch.autograd.Function):
-    """fsi_masked_softmax with fsi_masked_softmax_bwd as its gradient.
-    s3: contiguous (B, Q, N) scores; m8: uint8 mask view over (B, Q, N)."""
+    """fsi_masked_softmax with fsi_masked_softmax_bwd as its gradient."""
 
     @staticmethod
     def forward(ctx, s3: Tensor, m8: Tensor) -> Tensor:
-        what = "masked_softmax"
-        dev = s3.device
-        code = _lib.dtype_code(s3.dtype, what)
-        out = torch.empty_like(s3)
-        B, Q, N = s3.shape
-        st = _lib.lib().fsi_masked_softmax(s3.data_ptr(), code, B, Q, N, m8.data_ptr(), m8.stride(0), m8.stride(1),
-                                           m8.stride(2), out.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
         ctx.save_for_backward(s3, m8)
-        return out
+        return _masked_softmax_op(s3, m8)
 
     @staticmethod
     def backward(ctx, g: Tensor):
-        what = "masked_softmax backward"
         s3, m8 = ctx.saved_tensors
-        dev = _lib.require_gpu(g, s3, what=what)
-        gc = g.to(s3.dtype).contiguous()
-        ds = torch.empty_like(s3)
-        B, Q, N = s3.shape
-        st = _lib.lib().fsi_masked_softmax_bwd(s3.data_ptr(), gc.data_ptr(), _lib.dtype_code(s3.dtype, what), B, Q, N,
-                                               m8.data_ptr(), m8.stride(0), m8.stride(1), m8.stride(2), ds.data_ptr(),
-                                               _lib.stream_handle(dev))
-        _lib.check(st, what)
-        return ds, None
+        return _masked_softmax_bwd_op(s3, g, m8), None
 
 
 def masked_softmax(scores: Tensor, mask: Tensor) -> Tensor:
@@ -137,6 +147,30 @@ def _route_stats(counts: Tensor, max_remote, dev: torch.device):
     return cap_rate, counts.float().mean(), (counts == 0).float().mean()
 
 
+def _route_fake(scores, causal, local_window_blocks, top_p, k_min, k_max, capacity, p_rows, kmin_rows, kmax_rows,
+                kmax_bound):
+    B, Qb, _ = scores.shape
+    return (scores.new_empty((B, Qb, capacity), dtype=torch.int32), scores.new_empty((B, Qb), dtype=torch.int32))
+
+
+@_lib.fsi_op("route_from_scores", _route_fake)
+def _route_op(scores: Tensor, causal: bool, local_window_blocks: int, top_p: float, k_min: int, k_max: int,
+              capacity: int, p_rows: Optional[Tensor], kmin_rows: Optional[Tensor], kmax_rows: Optional[Tensor],
+              kmax_bound: int) -> Tuple[Tensor, Tensor]:
+    """fsi_route_from_scores: (indices (B, Qb, capacity), counts (B, Qb)) int32."""
+    what = "select_blocks"
+    dev = scores.device
+    B, Qb, Nb = scores.shape
+    indices = torch.empty((B, Qb, capacity), dtype=torch.int32, device=dev)
+    counts = torch.empty((B, Qb), dtype=torch.int32, device=dev)
+    st = _lib.lib().fsi_route_from_scores(
+        scores.data_ptr(), _lib.dtype_code(scores.dtype, what), B, Qb, Nb, int(causal), local_window_blocks, top_p,
+        k_min, k_max, capacity, _lib.ptr(p_rows), _lib.ptr(kmin_rows), _lib.ptr(kmax_rows), kmax_bound,
+        indices.data_ptr(), counts.data_ptr(), None, _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return indices, counts
+
+
 def select_blocks(
     block_scores: Tensor,
     *,
@@ -158,19 +192,40 @@ def select_blocks(
     kmin_val, kmin_rows = _per_row(min_remote_blocks, B, Qb, torch.int32, dev)
     kmax_val, kmax_rows = _per_row(max_remote_blocks, B, Qb, torch.int32, dev)
     kmax_bound = int(kmax_rows.max().item()) if kmax_rows is not None and kmax_rows.numel() else 0
-    indices = torch.empty((B, Qb, remote_capacity), dtype=torch.int32, device=dev)
-    counts = torch.empty((B, Qb), dtype=torch.int32, device=dev)
-    st = _lib.lib().fsi_route_from_scores(
-        scores.data_ptr(), code, B, Qb, Nb, int(bool(causal)), int(local_window_blocks),
-        float(p_val if p_val is not None else 0.0), int(kmin_val if kmin_val is not None else 0),
-        int(kmax_val if kmax_val is not None else 0), int(remote_capacity), _lib.ptr(p_rows), _lib.ptr(kmin_rows),
-        _lib.ptr(kmax_rows), kmax_bound, indices.data_ptr(), counts.data_ptr(), None, _lib.stream_handle(dev))
-    _lib.check(st, what)
+    indices, counts = _route_op(scores, bool(causal), int(local_window_blocks),
+                                float(p_val if p_val is not None else 0.0), int(kmin_val if kmin_val is not None else 0),
+                                int(kmax_val if kmax_val is not None else 0), int(remote_capacity), p_rows, kmin_rows,
+                                kmax_rows, kmax_bound)
     base_indices, base_counts = _route_tables(B, Qb, causal, local_window_blocks, dev)
     cap_rate, mean_remote, base_only = _route_stats(counts, max_remote_blocks, dev)
     return Route(remote_indices=indices, remote_counts=counts, base_indices=base_indices, base_counts=base_counts,
                  block_scores=block_scores, cap_rate=cap_rate, mean_remote_blocks=mean_remote,
                  base_only_rate=base_only)
+
+
+def _score_route_fake(q3, k3, causal, local_window_blocks, top_p, k_min, k_max, capacity, want_mass):
+    B, Q, _ = q3.shape
+    return (q3.new_empty((B, Q, capacity), dtype=torch.int32), q3.new_empty((B, Q), dtype=torch.int32),
+            q3.new_empty((B, Q) if want_mass else (0,), dtype=torch.float32))
+
+
+@_lib.fsi_op("score_and_route", _score_route_fake)
+def _score_route_op(q3: Tensor, k3: Tensor, causal: bool, local_window_blocks: int, top_p: float, k_min: int,
+                    k_max: int, capacity: int, want_mass: bool) -> Tuple[Tensor, Tensor, Tensor]:
+    """fsi_score_and_route: (indices, counts, mass ((B, Q) fp32, or empty without want_mass))."""
+    what = "score_and_route"
+    dev = q3.device
+    B, Q, d = q3.shape
+    Bk, N, _ = k3.shape
+    indices = torch.empty((B, Q, capacity), dtype=torch.int32, device=dev)
+    counts = torch.empty((B, Q), dtype=torch.int32, device=dev)
+    mass = torch.empty((B, Q) if want_mass else (0,), dtype=torch.float32, device=dev)
+    st = _lib.lib().fsi_score_and_route(
+        q3.data_ptr(), k3.data_ptr(), _lib.dtype_code(q3.dtype, what), B, Q, N, d, 0 if Bk == 1 else N * d,
+        int(causal), local_window_blocks, top_p, k_min, k_max, capacity, indices.data_ptr(), counts.data_ptr(),
+        mass.data_ptr() if want_mass else None, _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return indices, counts, mass
 
 
 def score_and_route(
@@ -202,15 +257,9 @@ def score_and_route(
     Bk, N, dk = k3.shape
     if dk != d or Bk not in (1, B):
         raise ValueError(f"{what}: q {tuple(q3.shape)} and k {tuple(k3.shape)} do not match")
-    k_stride = 0 if Bk == 1 else N * d
-    indices = torch.empty((B, Q, remote_capacity), dtype=torch.int32, device=dev)
-    counts = torch.empty((B, Q), dtype=torch.int32, device=dev)
-    mass = torch.empty((B, Q), dtype=torch.float32, device=dev) if return_mass else None
-    st = _lib.lib().fsi_score_and_route(
-        q3.data_ptr(), k3.data_ptr(), code, B, Q, N, d, k_stride, int(bool(causal)), int(local_window_blocks),
-        float(top_p), int(min_remote_blocks), int(max_remote_blocks), int(remote_capacity), indices.data_ptr(),
-        counts.data_ptr(), _lib.ptr(mass), _lib.stream_handle(dev))
-    _lib.check(st, what)
+    indices, counts, mass = _score_route_op(q3, k3, bool(causal), int(local_window_blocks), float(top_p),
+                                            int(min_remote_blocks), int(max_remote_blocks), int(remote_capacity),
+                                            bool(return_mass))
     if return_mass:
         return indices, counts, mass
     return indices, counts
@@ -351,71 +400,94 @@ class FovealIndexer(nn.Module):
         return loss
 
 
+@_lib.fsi_op("distill_kl", lambda s, t, mode, m8, temperature: (s.new_empty((), dtype=torch.float32),
+                                                                   s.new_empty((1,), dtype=torch.int32)))
+def _distill_kl_op(s: Tensor, t: Tensor, mode: int, m8: Optional[Tensor], temperature: float) -> Tuple[Tensor, Tensor]:
+    """fsi_distill_kl_fwd: (loss () fp32, rows averaged (1,) int32)."""
+    what = "distillation_loss"
+    dev = s.device
+    B, Q, N = s.shape
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    n_rows = torch.empty(1, dtype=torch.int32, device=dev)
+    ws = _lib.workspace(dev, L.fsi_distill_kl_workspace_size(B, Q), stream)
+    ms = m8.stride() if m8 is not None else (0, 0, 0)
+    st = L.fsi_distill_kl_fwd(s.data_ptr(), _lib.dtype_code(s.dtype, what), t.data_ptr(),
+                              _lib.dtype_code(t.dtype, what), B, Q, N, mode, _lib.ptr(m8), ms[0], ms[1], ms[2],
+                              temperature, loss.data_ptr(), n_rows.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    _lib.check(st, what)
+    return loss, n_rows
+
+
+@_lib.fsi_op("distill_kl_bwd", lambda s, t, mode, m8, temperature, g, n_rows: torch.empty_like(s))
+def _distill_kl_bwd_op(s: Tensor, t: Tensor, mode: int, m8: Optional[Tensor], temperature: float, g: Tensor,
+                       n_rows: Tensor) -> Tensor:
+    what = "distillation_loss backward"
+    dev = s.device
+    B, Q, N = s.shape
+    ds = torch.empty_like(s)
+    g32 = g.detach().to(device=dev, dtype=torch.float32).reshape(1).contiguous()
+    ms = m8.stride() if m8 is not None else (0, 0, 0)
+    st = _lib.lib().fsi_distill_kl_bwd(s.data_ptr(), _lib.dtype_code(s.dtype, what), t.data_ptr(),
+                                       _lib.dtype_code(t.dtype, what), B, Q, N, mode, _lib.ptr(m8), ms[0], ms[1],
+                                       ms[2], temperature, g32.data_ptr(), n_rows.data_ptr(), ds.data_ptr(),
+                                       _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return ds
+
+
 class _DistillKLFn(torch.autograd.Function):
     """fsi_distill_kl_fwd with fsi_distill_kl_bwd as the gradient in the scores."""
 
     @staticmethod
     def forward(ctx, s: Tensor, t: Tensor, mode: int, m8: Optional[Tensor], temperature: float) -> Tensor:
-        what = "distillation_loss"
-        dev = s.device
-        B, Q, N = s.shape
-        L = _lib.lib()
-        stream = _lib.stream_handle(dev)
-        loss = torch.empty((), dtype=torch.float32, device=dev)
-        n_rows = torch.empty(1, dtype=torch.int32, device=dev)
-        ws = _lib.workspace(dev, L.fsi_distill_kl_workspace_size(B, Q), stream)
-        ms = m8.stride() if m8 is not None else (0, 0, 0)
-        st = L.fsi_distill_kl_fwd(s.data_ptr(), _lib.dtype_code(s.dtype, what), t.data_ptr(),
-                                  _lib.dtype_code(t.dtype, what), B, Q, N, mode, _lib.ptr(m8), ms[0], ms[1], ms[2],
-                                  temperature, loss.data_ptr(), n_rows.data_ptr(), ws.data_ptr(), ws.numel(), stream)
-        _lib.check(st, what)
+        loss, n_rows = _distill_kl_op(s, t, mode, m8, temperature)
         ctx.save_for_backward(s, t, m8, n_rows)
         ctx.mode, ctx.temperature = mode, temperature
         return loss
 
     @staticmethod
     def backward(ctx, g: Tensor):
-        what = "distillation_loss backward"
         s, t, m8, n_rows = ctx.saved_tensors
-        dev = s.device
-        B, Q, N = s.shape
-        ds = torch.empty_like(s)
-        g32 = g.detach().to(device=dev, dtype=torch.float32).reshape(1).contiguous()
-        ms = m8.stride() if m8 is not None else (0, 0, 0)
-        st = _lib.lib().fsi_distill_kl_bwd(s.data_ptr(), _lib.dtype_code(s.dtype, what), t.data_ptr(),
-                                           _lib.dtype_code(t.dtype, what), B, Q, N, ctx.mode, _lib.ptr(m8), ms[0],
-                                           ms[1], ms[2], ctx.temperature, g32.data_ptr(), n_rows.data_ptr(),
-                                           ds.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
-        return ds, None, None, None, None
+        return _distill_kl_bwd_op(s, t, ctx.mode, m8, ctx.temperature, g, n_rows), None, None, None, None
+
+
+@_lib.fsi_op("index_rms_norm", lambda xc, what: torch.empty_like(xc))
+def _rms_norm_op(xc: Tensor, what: str) -> Tensor:
+    dev = xc.device
+    code = _lib.dtype_code(xc.dtype, what)
+    d = xc.shape[-1]
+    out = torch.empty_like(xc)
+    st = _lib.lib().fsi_index_rms_norm(xc.data_ptr(), code, xc.numel() // max(d, 1), d, out.data_ptr(),
+                                       _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return out
+
+
+@_lib.fsi_op("index_rms_norm_bwd", lambda xc, g, what: torch.empty_like(xc))
+def _rms_norm_bwd_op(xc: Tensor, g: Tensor, what: str) -> Tensor:
+    dev = _lib.require_gpu(g, xc, what=what)
+    gc = g.to(xc.dtype).contiguous()
+    dx = torch.empty_like(xc)
+    d = xc.shape[-1]
+    st = _lib.lib().fsi_index_rms_norm_bwd(xc.data_ptr(), gc.data_ptr(), _lib.dtype_code(xc.dtype, what),
+                                           xc.numel() // max(d, 1), d, dx.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return dx
 
 
 class _IndexRmsNormFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, xc: Tensor, what: str) -> Tensor:
-        dev = xc.device
-        code = _lib.dtype_code(xc.dtype, what)
-        d = xc.shape[-1]
-        out = torch.empty_like(xc)
-        st = _lib.lib().fsi_index_rms_norm(xc.data_ptr(), code, xc.numel() // max(d, 1), d, out.data_ptr(),
-                                           _lib.stream_handle(dev))
-        _lib.check(st, what)
         ctx.save_for_backward(xc)
         ctx.what = what
-        return out
+        return _rms_norm_op(xc, what)
 
     @staticmethod
     def backward(ctx, g: Tensor):
         (xc,) = ctx.saved_tensors
-        what = ctx.what + " backward"
-        dev = _lib.require_gpu(g, xc, what=what)
-        gc = g.to(xc.dtype).contiguous()
-        dx = torch.empty_like(xc)
-        d = xc.shape[-1]
-        st = _lib.lib().fsi_index_rms_norm_bwd(xc.data_ptr(), gc.data_ptr(), _lib.dtype_code(xc.dtype, what),
-                                               xc.numel() // max(d, 1), d, dx.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
-        return dx, None
+        return _rms_norm_bwd_op(xc, g, ctx.what + " backward"), None
 
 
 def index_rms_norm(x: Tensor, what: str = "index_rms_norm") -> Tensor:
@@ -425,70 +497,130 @@ def index_rms_norm(x: Tensor, what: str = "index_rms_norm") -> Tensor:
     return _IndexRmsNormFn.apply(x.contiguous(), what)
 
 
+def _pool_fake(k_lin, v_lin, block_size):
+    batch, n_elements, d = k_lin.shape
+    kb = k_lin.new_empty((batch, n_elements // block_size, d))
+    return kb, torch.empty_like(kb)
+
+
+@_lib.fsi_op("pool_kv", _pool_fake)
+def _pool_kv_op(k_lin: Tensor, v_lin: Tensor, block_size: int) -> Tuple[Tensor, Tensor]:
+    what = "compute_kv_blocks_16d"
+    dev = k_lin.device
+    code = _lib.dtype_code(k_lin.dtype, what)
+    batch, n_elements, d = k_lin.shape
+    nb = n_elements // block_size
+    k_blocks = torch.empty((batch, nb, d), dtype=k_lin.dtype, device=dev)
+    v_blocks = torch.empty_like(k_blocks)
+    st = _lib.lib().fsi_index_pool_kv(k_lin.data_ptr(), v_lin.data_ptr(), code, batch, n_elements, d, block_size,
+                                      k_blocks.data_ptr(), v_blocks.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return k_blocks, v_blocks
+
+
+@_lib.fsi_op("pool_kv_bwd", lambda k_lin, gk, gv, block_size: (torch.empty_like(k_lin), torch.empty_like(k_lin)))
+def _pool_kv_bwd_op(k_lin: Tensor, gk: Tensor, gv: Tensor, block_size: int) -> Tuple[Tensor, Tensor]:
+    what = "compute_kv_blocks_16d backward"
+    dev = _lib.require_gpu(k_lin, what=what)
+    batch, n_elements, d = k_lin.shape
+    gk = gk.to(k_lin.dtype).contiguous()
+    gv = gv.to(k_lin.dtype).contiguous()
+    dk, dv = torch.empty_like(k_lin), torch.empty_like(k_lin)
+    st = _lib.lib().fsi_index_pool_kv_bwd(k_lin.data_ptr(), gk.data_ptr(), gv.data_ptr(),
+                                          _lib.dtype_code(k_lin.dtype, what), batch, n_elements, d, block_size,
+                                          dk.data_ptr(), dv.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return dk, dv
+
+
 class _PoolKVFn(torch.autograd.Function):
     """fsi_index_pool_kv with fsi_index_pool_kv_bwd as its gradient (B, N, 16) inputs."""
 
     @staticmethod
     def forward(ctx, k_lin: Tensor, v_lin: Tensor, block_size: int):
-        what = "compute_kv_blocks_16d"
-        dev = k_lin.device
-        code = _lib.dtype_code(k_lin.dtype, what)
-        batch, n_elements, d = k_lin.shape
-        nb = n_elements // block_size
-        k_blocks = torch.empty((batch, nb, d), dtype=k_lin.dtype, device=dev)
-        v_blocks = torch.empty_like(k_blocks)
-        st = _lib.lib().fsi_index_pool_kv(k_lin.data_ptr(), v_lin.data_ptr(), code, batch, n_elements, d, block_size,
-                                          k_blocks.data_ptr(), v_blocks.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
         ctx.save_for_backward(k_lin)
         ctx.block_size = block_size
-        return k_blocks, v_blocks
+        return _pool_kv_op(k_lin, v_lin, block_size)
 
     @staticmethod
     def backward(ctx, gk: Optional[Tensor], gv: Optional[Tensor]):
-        what = "compute_kv_blocks_16d backward"
         (k_lin,) = ctx.saved_tensors
-        dev = _lib.require_gpu(k_lin, what=what)
         batch, n_elements, d = k_lin.shape
         nb = n_elements // ctx.block_size
-        zeros = lambda: torch.zeros((batch, nb, d), dtype=k_lin.dtype, device=dev)  # noqa: E731
-        gk = zeros() if gk is None else gk.to(k_lin.dtype).contiguous()
-        gv = zeros() if gv is None else gv.to(k_lin.dtype).contiguous()
-        dk, dv = torch.empty_like(k_lin), torch.empty_like(k_lin)
-        st = _lib.lib().fsi_index_pool_kv_bwd(k_lin.data_ptr(), gk.data_ptr(), gv.data_ptr(),
-                                              _lib.dtype_code(k_lin.dtype, what), batch, n_elements, d, ctx.block_size,
-                                              dk.data_ptr(), dv.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
+        zeros = lambda: k_lin.new_zeros((batch, nb, d))  # noqa: E731
+        gk = zeros() if gk is None else gk
+        gv = zeros() if gv is None else gv
+        dk, dv = _pool_kv_bwd_op(k_lin, gk, gv, ctx.block_size)
         return dk, dv, None
+
+
+@_lib.fsi_op("block_scores", lambda q, k: q.new_empty((q.shape[0], q.shape[1], k.shape[1])))
+def _block_scores_op(q: Tensor, k: Tensor) -> Tensor:
+    what = "compute_block_scores"
+    dev = q.device
+    B, Q, d = q.shape
+    N = k.shape[1]
+    out = torch.empty((B, Q, N), dtype=q.dtype, device=dev)
+    st = _lib.lib().fsi_block_scores(q.data_ptr(), k.data_ptr(), _lib.dtype_code(q.dtype, what), B, Q, N, d,
+                                     out.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return out
+
+
+@_lib.fsi_op("block_scores_bwd", lambda q, k, g: (torch.empty_like(q), torch.empty_like(k)))
+def _block_scores_bwd_op(q: Tensor, k: Tensor, g: Tensor) -> Tuple[Tensor, Tensor]:
+    what = "compute_block_scores backward"
+    dev = _lib.require_gpu(g, q, k, what=what)
+    gc = g.to(q.dtype).contiguous()
+    B, Q, d = q.shape
+    N = k.shape[1]
+    dq, dk = torch.empty_like(q), torch.empty_like(k)
+    st = _lib.lib().fsi_block_scores_bwd(q.data_ptr(), k.data_ptr(), gc.data_ptr(), _lib.dtype_code(q.dtype, what),
+                                         B, Q, N, d, dq.data_ptr(), dk.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return dq, dk
 
 
 class _BlockScoresFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q: Tensor, k: Tensor) -> Tensor:
-        what = "compute_block_scores"
-        dev = q.device
-        B, Q, d = q.shape
-        N = k.shape[1]
-        out = torch.empty((B, Q, N), dtype=q.dtype, device=dev)
-        st = _lib.lib().fsi_block_scores(q.data_ptr(), k.data_ptr(), _lib.dtype_code(q.dtype, what), B, Q, N, d,
-                                         out.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
         ctx.save_for_backward(q, k)
-        return out
+        return _block_scores_op(q, k)
 
     @staticmethod
     def backward(ctx, g: Tensor):
-        what = "compute_block_scores backward"
         q, k = ctx.saved_tensors
-        dev = _lib.require_gpu(g, q, k, what=what)
-        gc = g.to(q.dtype).contiguous()
-        B, Q, d = q.shape
-        N = k.shape[1]
-        dq, dk = torch.empty_like(q), torch.empty_like(k)
-        st = _lib.lib().fsi_block_scores_bwd(q.data_ptr(), k.data_ptr(), gc.data_ptr(), _lib.dtype_code(q.dtype, what),
-                                             B, Q, N, d, dq.data_ptr(), dk.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
-        return dq, dk
+        return _block_scores_bwd_op(q, k, g)
+
+
+@_lib.fsi_op("additive_context", lambda s, v, causal: v.new_empty((s.shape[0], s.shape[1], v.shape[-1])))
+def _additive_context_op(s: Tensor, v: Tensor, causal: bool) -> Tensor:
+    what = "additive_stream"
+    dev = s.device
+    B, Qb, Nb = s.shape
+    d = v.shape[-1]
+    context = torch.empty((B, Qb, d), dtype=v.dtype, device=dev)
+    st = _lib.lib().fsi_additive_context(s.data_ptr(), v.data_ptr(), _lib.dtype_code(v.dtype, what), B, Qb, Nb, d,
+                                         int(causal), context.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return context
+
+
+@_lib.fsi_op("additive_context_bwd", lambda s, v, g, causal: (torch.empty_like(s), torch.empty_like(v)))
+def _additive_context_bwd_op(s: Tensor, v: Tensor, g: Tensor, causal: bool) -> Tuple[Tensor, Tensor]:
+    what = "additive_stream backward"
+    dev = _lib.require_gpu(g, s, v, what=what)
+    gc = g.to(v.dtype).contiguous()
+    B, Qb, Nb = s.shape
+    d = v.shape[-1]
+    ds, dv = torch.empty_like(s), torch.empty_like(v)
+    lib = _lib.lib()
+    ws = torch.empty(max(1, lib.fsi_additive_context_bwd_workspace_size(B, Qb)), dtype=torch.uint8, device=dev)
+    st = lib.fsi_additive_context_bwd(s.data_ptr(), v.data_ptr(), gc.data_ptr(), _lib.dtype_code(v.dtype, what),
+                                      B, Qb, Nb, d, int(causal), ds.data_ptr(), dv.data_ptr(), ws.data_ptr(),
+                                      ws.numel(), _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return ds, dv
 
 
 class _AdditiveContextFn(torch.autograd.Function):
@@ -496,33 +628,14 @@ class _AdditiveContextFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, s: Tensor, v: Tensor, causal: bool) -> Tensor:
-        what = "additive_stream"
-        dev = s.device
-        B, Qb, Nb = s.shape
-        d = v.shape[-1]
-        context = torch.empty((B, Qb, d), dtype=v.dtype, device=dev)
-        st = _lib.lib().fsi_additive_context(s.data_ptr(), v.data_ptr(), _lib.dtype_code(v.dtype, what), B, Qb, Nb, d,
-                                             int(bool(causal)), context.data_ptr(), _lib.stream_handle(dev))
-        _lib.check(st, what)
         ctx.save_for_backward(s, v)
         ctx.causal = bool(causal)
-        return context
+        return _additive_context_op(s, v, bool(causal))
 
     @staticmethod
     def backward(ctx, g: Tensor):
-        what = "additive_stream backward"
         s, v = ctx.saved_tensors
-        dev = _lib.require_gpu(g, s, v, what=what)
-        gc = g.to(v.dtype).contiguous()
-        B, Qb, Nb = s.shape
-        d = v.shape[-1]
-        ds, dv = torch.empty_like(s), torch.empty_like(v)
-        lib = _lib.lib()
-        ws = torch.empty(max(1, lib.fsi_additive_context_bwd_workspace_size(B, Qb)), dtype=torch.uint8, device=dev)
-        st = lib.fsi_additive_context_bwd(s.data_ptr(), v.data_ptr(), gc.data_ptr(), _lib.dtype_code(v.dtype, what),
-                                          B, Qb, Nb, d, int(ctx.causal), ds.data_ptr(), dv.data_ptr(), ws.data_ptr(),
-                                          ws.numel(), _lib.stream_handle(dev))
-        _lib.check(st, what)
+        ds, dv = _additive_context_bwd_op(s, v, g, ctx.causal)
         return ds, dv, None
 
 

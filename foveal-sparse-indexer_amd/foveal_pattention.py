@@ -56,29 +56,44 @@ def mlp_pooled_route(
     dt = x2d.dtype
     if q_proj_weight.dtype != dt or block_keys.dtype != dt:
         raise TypeError(f"{what}: dtype mismatch {dt}/{q_proj_weight.dtype}/{block_keys.dtype}")
-    code = _lib.dtype_code(dt, what)
+    _lib.dtype_code(dt, what)
     if x2d.stride(-1) != 1:
         x2d = x2d.contiguous()
     wq = q_proj_weight.contiguous()
     keys = block_keys.contiguous()
-    M, D = x2d.shape
-    index_dim = wq.shape[0]
     n_blocks = keys.shape[0]
     if remote_blocks > n_blocks - base_blocks:
         # torch.topk: "selected index k out of range" (foveal_pattention.py:314)
         raise RuntimeError(f"{what}: selected index k out of range ({remote_blocks} > {n_blocks - base_blocks})")
+    active, scores = _mlp_router_op(x2d, wq, keys, int(base_blocks), int(remote_blocks), float(score_scale),
+                                    bool(return_scores))
+    if return_scores:
+        return active, scores
+    return active
+
+
+@_lib.fsi_op("mlp_router", lambda x2d, wq, keys, base_blocks, remote_blocks, score_scale, want_scores: (
+    x2d.new_empty((base_blocks + remote_blocks,), dtype=torch.int32),
+    x2d.new_empty((keys.shape[0] if want_scores else 0,), dtype=torch.float32)))
+def _mlp_router_op(x2d: Tensor, wq: Tensor, keys: Tensor, base_blocks: int, remote_blocks: int, score_scale: float,
+                   want_scores: bool) -> Tuple[Tensor, Tensor]:
+    """fsi_mlp_router: (active blocks int32, router scores fp32 (n_blocks,) or empty)."""
+    what = "mlp_router"
+    dev = x2d.device
+    M, D = x2d.shape
+    index_dim = wq.shape[0]
+    n_blocks = keys.shape[0]
     active = torch.empty(base_blocks + remote_blocks, dtype=torch.int32, device=dev)
-    scores = torch.empty(n_blocks, dtype=torch.float32, device=dev) if return_scores else None
+    scores = torch.empty(n_blocks if want_scores else 0, dtype=torch.float32, device=dev)
     stream = _lib.stream_handle(dev)
     L = _lib.lib()
     ws = _lib.workspace(dev, L.fsi_mlp_router_workspace_size(D, n_blocks), stream)
     st = L.fsi_mlp_router(x2d.data_ptr(), x2d.stride(0), M, D, wq.data_ptr(), index_dim, keys.data_ptr(), n_blocks,
-                          base_blocks, remote_blocks, float(score_scale), code, active.data_ptr(), _lib.ptr(scores),
-                          ws.data_ptr(), ws.numel(), stream)
+                          base_blocks, remote_blocks, score_scale, _lib.dtype_code(x2d.dtype, what),
+                          active.data_ptr(), scores.data_ptr() if want_scores else None, ws.data_ptr(), ws.numel(),
+                          stream)
     _lib.check(st, what)
-    if return_scores:
-        return active, scores
-    return active
+    return active, scores
 
 
 class _EvalPattentionFn(torch.autograd.Function):

@@ -7,7 +7,7 @@ hand-written HIP for gfx950 (csrc/pattention.hip), not Triton.
 """
 from __future__ import annotations
 
-from typing import Literal, Optional
+from typing import Literal, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -85,7 +85,6 @@ def pattention_forward(
         v_transposed = False  # the fp32 kernels read V as [N_p, D_out]
     if not v_transposed:
         v = _rows_contig(v)
-    ldv = v.stride(1) if v_transposed else v.stride(0)
     if k_up is not None:
         k_up = _rows_contig(k_up)
         if k_up.stride(0) != k_gate.stride(0):
@@ -101,19 +100,27 @@ def pattention_forward(
         raise ValueError(f"{what}: v has {v.shape[0]} rows, k_gate has {N_p}")
     D_out = v.shape[1]
 
-    if active_blocks is not None:
-        idx = _as_index_tensor(active_blocks, dev)
-        n_active = idx.numel()
-    else:
-        idx, n_active = None, 0
-    n_channels = N_p if idx is None else n_active * block_n
-
+    idx = _as_index_tensor(active_blocks, dev) if active_blocks is not None else None
     if out is None:
-        out = torch.empty((M, D_out), dtype=dt, device=dev)
+        return _pattention_op(x2d, k_gate, k_up, v, idx, block_n, act, rnd, v_transposed)
+    return _pattention_launch(x2d, k_gate, k_up, v, idx, block_n, act, rnd, v_transposed, out)
+
+
+def _pattention_launch(x2d: Tensor, k_gate: Tensor, k_up: Optional[Tensor], v: Tensor, idx: Optional[Tensor],
+                       block_n: int, act: int, rnd: int, v_transposed: bool, out: Tensor) -> Tensor:
+    what = "pattention"
+    dev = x2d.device
+    M, K = x2d.shape
+    N_p = k_gate.shape[0]
+    D_out = v.shape[1]
+    n_active = 0 if idx is None else idx.numel()
+    n_channels = N_p if idx is None else n_active * block_n
     if idx is not None and n_active == 0:
         # An empty block list contributes nothing (pattention_triton.py:141 loop never runs).  The
         # ABI reads a null list as "all blocks", and an empty tensor's data pointer is null.
         return out.zero_()
+    code = _lib.dtype_code(x2d.dtype, what)
+    ldv = v.stride(1) if v_transposed else v.stride(0)
     stream = _lib.stream_handle(dev)
     L = _lib.lib()
     ws_bytes = L.fsi_pattention_workspace_size(M, K, D_out, max(n_channels, 1), code)
@@ -128,6 +135,15 @@ def pattention_forward(
     if _lib.checks_enabled():
         _lib.raise_device_errors(dev, what)
     return out
+
+
+@_lib.fsi_op("pattention", lambda x2d, k_gate, k_up, v, idx, block_n, act, rnd, v_transposed:
+             x2d.new_empty((x2d.shape[0], v.shape[1])))
+def _pattention_op(x2d: Tensor, k_gate: Tensor, k_up: Optional[Tensor], v: Tensor, idx: Optional[Tensor],
+                   block_n: int, act: int, rnd: int, v_transposed: bool) -> Tensor:
+    """fsi_pattention_fwd into a new (M, D_out) tensor (arguments prepared by pattention_forward)."""
+    out = torch.empty((x2d.shape[0], v.shape[1]), dtype=x2d.dtype, device=x2d.device)
+    return _pattention_launch(x2d, k_gate, k_up, v, idx, block_n, act, rnd, v_transposed, out)
 
 
 class PackedPattentionWeights:
@@ -174,19 +190,30 @@ def pack_pattention_weights(k_gate: Tensor, k_up: Tensor, v: Tensor, block_n: in
     v_transposed = v.stride(0) == 1 and v.stride(1) >= v.shape[0] and v.shape[1] > 1
     if not v_transposed:
         v = _rows_contig(v)
-    ldv = v.stride(1) if v_transposed else v.stride(0)
     N_p, K = k_gate.shape
     D_out = v.shape[1]
     if tuple(k_up.shape) != (N_p, K) or v.shape[0] != N_p:
         raise ValueError(f"{what}: k_gate {tuple(k_gate.shape)}, k_up {tuple(k_up.shape)}, v {tuple(v.shape)}")
+    buf = _pack_op(k_gate, k_up, v, bool(v_transposed), int(block_n))
+    return PackedPattentionWeights(buf, N_p, K, D_out, block_n, key)
+
+
+@_lib.fsi_op("pattention_pack", lambda k_gate, k_up, v, v_transposed, block_n: k_gate.new_empty(
+    (_lib.lib().fsi_pattention_packed_size(k_gate.shape[0], k_gate.shape[1], v.shape[1]),), dtype=torch.uint8))
+def _pack_op(k_gate: Tensor, k_up: Tensor, v: Tensor, v_transposed: bool, block_n: int) -> Tensor:
+    """fsi_pattention_pack into a new byte buffer (arguments prepared by pack_pattention_weights)."""
+    what = "pack_pattention_weights"
+    N_p, K = k_gate.shape
+    D_out = v.shape[1]
+    ldv = v.stride(1) if v_transposed else v.stride(0)
     L = _lib.lib()
     nbytes = L.fsi_pattention_packed_size(N_p, K, D_out)
-    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=k_gate.device)
     st = L.fsi_pattention_pack(k_gate.data_ptr(), k_up.data_ptr(), k_gate.stride(0), v.data_ptr(), ldv,
                                int(v_transposed), N_p, K, D_out, block_n, _lib.DTYPE_BF16, buf.data_ptr(), nbytes,
-                               _lib.stream_handle(dev))
+                               _lib.stream_handle(k_gate.device))
     _lib.check(st, what)
-    return PackedPattentionWeights(buf, N_p, K, D_out, block_n, key)
+    return buf
 
 
 def pattention_decode_packed(
@@ -210,29 +237,42 @@ def pattention_decode_packed(
     M, K = x2d.shape
     if K != packed.K:
         raise ValueError(f"{what}: x has K={K}, weights {packed.K}")
-    if active_blocks is not None:
-        idx = _as_index_tensor(active_blocks, dev)
-        n_active = idx.numel()
-    else:
-        idx, n_active = None, 0
-    n_ch = packed.N_p if idx is None else n_active * packed.block_n
+    idx = _as_index_tensor(active_blocks, dev) if active_blocks is not None else None
+    rnd = _lib.ROUNDING[rounding]
     if out is None:
-        out = torch.empty((M, packed.D_out), dtype=torch.bfloat16, device=dev)
+        return _packed_op(x2d, packed.buf, idx, packed.N_p, packed.D_out, packed.block_n, rnd)
+    return _packed_launch(x2d, packed.buf, idx, packed.N_p, packed.D_out, packed.block_n, rnd, out)
+
+
+def _packed_launch(x2d: Tensor, buf: Tensor, idx: Optional[Tensor], N_p: int, D_out: int, block_n: int, rnd: int,
+                   out: Tensor) -> Tensor:
+    what = "pattention_decode_packed"
+    dev = x2d.device
+    M, K = x2d.shape
+    n_active = 0 if idx is None else idx.numel()
+    n_ch = N_p if idx is None else n_active * block_n
     if idx is not None and n_active == 0:
         return out.zero_()
     L = _lib.lib()
     stream = _lib.stream_handle(dev)
-    ws = _lib.workspace(dev, L.fsi_pattention_packed_workspace_size(M, K, packed.D_out, n_ch, packed.block_n),
-                        stream)
+    ws = _lib.workspace(dev, L.fsi_pattention_packed_workspace_size(M, K, D_out, n_ch, block_n), stream)
     err = _lib.error_word(dev)
     st = L.fsi_pattention_fwd_packed(
-        x2d.data_ptr(), x2d.stride(0), packed.buf.data_ptr(), _lib.ptr(idx), n_active, packed.block_n, M, K,
-        packed.N_p, packed.D_out, _lib.DTYPE_BF16, _lib.ROUNDING[rounding], out.data_ptr(), out.stride(0),
-        ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
+        x2d.data_ptr(), x2d.stride(0), buf.data_ptr(), _lib.ptr(idx), n_active, block_n, M, K, N_p, D_out,
+        _lib.DTYPE_BF16, rnd, out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
     _lib.check(st, what)
     if _lib.checks_enabled():
         _lib.raise_device_errors(dev, what)
     return out
+
+
+@_lib.fsi_op("pattention_packed", lambda x2d, buf, idx, N_p, D_out, block_n, rnd:
+             x2d.new_empty((x2d.shape[0], D_out)))
+def _packed_op(x2d: Tensor, buf: Tensor, idx: Optional[Tensor], N_p: int, D_out: int, block_n: int,
+               rnd: int) -> Tensor:
+    """fsi_pattention_fwd_packed into a new (M, D_out) bf16 tensor."""
+    out = torch.empty((x2d.shape[0], D_out), dtype=torch.bfloat16, device=x2d.device)
+    return _packed_launch(x2d, buf, idx, N_p, D_out, block_n, rnd, out)
 
 
 def triton_pattention(
@@ -261,6 +301,7 @@ def triton_pattention(
     return out
 
 
+@_lib.fsi_op("swiglu", lambda g, u, rounding: torch.empty_like(g, memory_format=torch.contiguous_format))
 def _swiglu_launch(g: Tensor, u: Tensor, rounding: str) -> Tensor:
     what = "swiglu"
     dev = _lib.require_gpu(g, u, what=what)
@@ -273,6 +314,19 @@ def _swiglu_launch(g: Tensor, u: Tensor, rounding: str) -> Tensor:
                                _lib.ROUNDING[rounding], _lib.stream_handle(dev))
     _lib.check(st, what)
     return out
+
+
+@_lib.fsi_op("swiglu_bwd", lambda dout, g, u: (torch.empty_like(g), torch.empty_like(u)))
+def _swiglu_bwd_op(dout: Tensor, g: Tensor, u: Tensor) -> Tuple[Tensor, Tensor]:
+    what = "swiglu backward"
+    dev = _lib.require_gpu(dout, g, u, what=what)
+    code = _lib.dtype_code(g.dtype, what)
+    d = dout.to(g.dtype).contiguous()
+    dg, du = torch.empty_like(g), torch.empty_like(u)
+    st = _lib.lib().fsi_swiglu_bwd(d.data_ptr(), g.data_ptr(), u.data_ptr(), dg.data_ptr(), du.data_ptr(),
+                                   g.numel(), code, _lib.stream_handle(dev))
+    _lib.check(st, what)
+    return dg, du
 
 
 class FusedSwiGLUFunction(torch.autograd.Function):
@@ -290,15 +344,7 @@ class FusedSwiGLUFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout: Tensor):
         g, u = ctx.saved_tensors
-        what = "swiglu backward"
-        dev = _lib.require_gpu(dout, g, u, what=what)
-        code = _lib.dtype_code(g.dtype, what)
-        d = dout.to(g.dtype).contiguous()
-        dg, du = torch.empty_like(g), torch.empty_like(u)
-        st = _lib.lib().fsi_swiglu_bwd(d.data_ptr(), g.data_ptr(), u.data_ptr(), dg.data_ptr(), du.data_ptr(),
-                                       g.numel(), code, _lib.stream_handle(dev))
-        _lib.check(st, what)
-        return dg, du
+        return _swiglu_bwd_op(dout, g, u)
 
 
 def triton_fused_swiglu(g: Tensor, u: Tensor) -> Tensor:
@@ -356,21 +402,32 @@ def dense_block_targets(norm_h: Tensor, gate_w: Tensor, up_w: Tensor, down_w: Te
     lead = norm_h.shape[:-1]
     h = _aligned_rows(norm_h.reshape(-1, D))
     gw, uw, dw = _aligned_rows(gate_w), _aligned_rows(up_w), _aligned_rows(down_w)
-    M = h.shape[0]
     nb = I // block_size
-    out = torch.empty((M, nb), dtype=torch.float32, device=dev)
-    if M == 0:
-        return out.reshape(*lead, nb)
+    if h.shape[0] == 0:
+        return torch.empty((*lead, nb), dtype=torch.float32, device=dev)
     if gw.stride(0) != uw.stride(0):
         uw = uw.contiguous()
         gw = gw.contiguous()
+    return _block_targets_op(h, gw, uw, dw, block_size, float(temperature)).reshape(*lead, nb)
+
+
+@_lib.fsi_op("dense_block_targets", lambda h, gw, uw, dw, block_size, temperature:
+             h.new_empty((h.shape[0], gw.shape[0] // block_size), dtype=torch.float32))
+def _block_targets_op(h: Tensor, gw: Tensor, uw: Tensor, dw: Tensor, block_size: int, temperature: float) -> Tensor:
+    """fsi_dense_block_targets: (M, I / block_size) fp32 (arguments prepared by dense_block_targets)."""
+    what = "dense_block_targets"
+    dev = h.device
+    M, D = h.shape
+    I = gw.shape[0]
+    nb = I // block_size
+    out = torch.empty((M, nb), dtype=torch.float32, device=dev)
     lib = _lib.lib()
     ws = torch.empty(lib.fsi_dense_block_targets_workspace_size(M, D, I, block_size), dtype=torch.uint8, device=dev)
     st = lib.fsi_dense_block_targets(h.data_ptr(), h.stride(0), gw.data_ptr(), uw.data_ptr(), gw.stride(0),
-                                     dw.data_ptr(), dw.stride(0), M, D, I, block_size, float(temperature),
+                                     dw.data_ptr(), dw.stride(0), M, D, I, block_size, temperature,
                                      out.data_ptr(), nb, ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
     _lib.check(st, what)
-    return out.reshape(*lead, nb)
+    return out
 
 
 class TritonSwiGLUPattentionMLP(nn.Module):

@@ -255,12 +255,10 @@ def bench_decode_attn(fsi, args, dev):
     outs = {}
 
     def step(i):
-        pages, counts, ctx = fsi.decode_route(qi, cache.kp_cache, cache.vp_cache, pos=pos, page_size=PAGE,
-                                              local_window=W, completed_pages=P, top_p=TOP_P, min_remote_blocks=0,
-                                              max_remote_blocks=KMAX, return_context=True)
-        outs["o"] = fsi.decode_attention(q, cache, pos=pos, window=W, remote_pages=pages, remote_counts=counts,
-                                         scale=scale)
-        outs["c"] = counts
+        # routing beside the local-window attention partials, then the selected pages and the merge
+        outs["o"], pages, outs["c"], ctx = fsi.decode_step_attention(
+            q, qi, cache, pos=pos, window=W, completed_pages=P, top_p=TOP_P, min_remote_blocks=0,
+            max_remote_blocks=KMAX, scale=scale, return_context=True)
 
     t, _ = time_graph(step, args.steps, args.warmup, dev)
     per = t / args.steps
@@ -277,7 +275,8 @@ def bench_decode_attn(fsi, args, dev):
                    "mean_selected_pages": round(k_sel, 2)})
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C4_TRAFFIC_BYTES,
-                       "kernel": "decode_route + decode_attn_partial + decode_attn_merge (3 launches)",
+                       "kernel": "decode_step_kernel (route workgroups beside the local-window partials) + "
+                                 "decode_attn_partial (selected pages) + decode_attn_merge (3 launches)",
                        "bytes_per_launch": algo}
     if not args.no_cpu_baseline:
         from oracle import attention as A

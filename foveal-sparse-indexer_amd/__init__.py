@@ -35,6 +35,7 @@ from .attention import (
     FovealSparseAttention,
     decode_attention,
     decode_route,
+    decode_step_attention,
     sparse_attention,
     sram_indexer_attention,
     triton_foveal_sparse_attention,
@@ -72,6 +73,7 @@ __all__ = [
     "tile_route",
     "triton_block_sparse_linear",
     "decode_attention",
+    "decode_step_attention",
     "sparse_attention",
     "triton_foveal_sparse_attention",
     "triton_fused_sram_indexer_attention",

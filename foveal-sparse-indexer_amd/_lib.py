@@ -144,6 +144,12 @@ SIGNATURES: dict[str, tuple] = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_ptr, _c_size, _c_ptr, _c_ptr],
     ),
+    "fsi_decode_step_attn": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, ctypes.c_float, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,
+         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         ctypes.c_float, _c_int, _c_ptr, _c_ptr, _c_size, _c_ptr, _c_ptr],
+    ),
     "fsi_decode_attn_dense": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64,

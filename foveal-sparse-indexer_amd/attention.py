@@ -332,6 +332,80 @@ def _decode_op(q3: Tensor, k_cache: Tensor, v_cache: Tensor, page_table: Optiona
                           pos_rows, pos_val, window, remote_pages, remote_counts, cap, scale, torch.empty_like(q3))
 
 
+def _decode_step_fake(qi, kp, vp, completed, top_p, k_min, k_max, cap, want_ctx, q3, k_cache, v_cache, page_table,
+                      max_pages, n_phys, pos_rows, pos_val, window, n_kv_heads, scale, batch0):
+    B = q3.shape[0]
+    return (torch.empty_like(q3), q3.new_empty((B, cap), dtype=torch.int32), q3.new_empty((B,), dtype=torch.int32),
+            qi.new_empty((B, qi.shape[-1]) if want_ctx else (0,)))
+
+
+@_lib.fsi_op("decode_step_attention", _decode_step_fake)
+def _decode_step_op(qi: Tensor, kp: Tensor, vp: Optional[Tensor], completed: int, top_p: float, k_min: int,
+                    k_max: int, cap: int, want_ctx: bool, q3: Tensor, k_cache: Tensor, v_cache: Tensor,
+                    page_table: Tensor, max_pages: int, n_phys: int, pos_rows: Optional[Tensor], pos_val: int,
+                    window: int, n_kv_heads: int, scale: float, batch0: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """fsi_decode_step_attn: (attention (B, Hq, hd), pages (B, cap), counts (B,), context (B, 16) or empty)."""
+    what = "decode_step"
+    dev = q3.device
+    B, Hq, hd = q3.shape
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    out = torch.empty_like(q3)
+    pages = torch.empty((B, cap), dtype=torch.int32, device=dev)
+    counts = torch.empty((B,), dtype=torch.int32, device=dev)
+    ctx = torch.empty((B, qi.shape[-1]) if want_ctx else (0,), dtype=qi.dtype, device=dev)
+    ws = _lib.workspace(dev, L.fsi_decode_attn_workspace_size(B, Hq, n_kv_heads, hd, window, cap, max_pages), stream)
+    err = _lib.error_word(dev)
+    st = L.fsi_decode_step_attn(
+        qi.data_ptr(), kp.data_ptr(), _lib.ptr(vp), kp.shape[1], completed, top_p, k_min, k_max, cap,
+        pages.data_ptr(), counts.data_ptr(), ctx.data_ptr() if want_ctx else None, q3.data_ptr(),
+        k_cache.data_ptr(), v_cache.data_ptr(), page_table.data_ptr(), max_pages, n_phys, _lib.ptr(pos_rows), pos_val,
+        window, B, Hq, n_kv_heads, hd, scale, int(batch0), out.data_ptr(), ws.data_ptr(), ws.numel(), err.data_ptr(),
+        stream)
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+    return out, pages, counts, ctx
+
+
+def decode_step_attention(q: Tensor, qi: Tensor, cache: FovealKVCache, *, pos: int | Tensor, window: int,
+                          completed_pages: int, top_p: float, min_remote_blocks: int, max_remote_blocks: int,
+                          scale: float, return_context: bool = False, batch0: bool = False):
+    """Page routing and decode attention of one step (decode_route + decode_attention)
+    in two launches on one stream: the workgroups routing each sequence run beside
+    the local-window attention partials, then the selected pages and the merge
+    (fsi_decode_step_attn).  Needs the paged bf16 cache and a bf16 index query.
+    batch0: every sequence attends sequence 0's pages (attention.py:348).
+    Returns (attention (B, Hq, hd), pages (B, cap), counts (B,)[, context (B, 16)]),
+    cap = max(K_max, K_min, 1); no autograd (use decode_route + decode_attention)."""
+    what = "decode_step"
+    dev = _lib.require_gpu(q, qi, cache.kp_cache, what=what)
+    if not cache.paged:
+        raise ValueError(f"{what}: the fused step needs the paged cache layout")
+    B = q.shape[0]
+    Hq, hd = q.shape[1], q.shape[-1]
+    q3 = q.detach().reshape(B, Hq, hd).contiguous()
+    q2 = qi.detach().reshape(B, -1).contiguous()
+    if q3.dtype != torch.bfloat16 or q2.dtype != torch.bfloat16 or q2.shape[1] != 16:
+        raise TypeError(f"{what}: bf16 q and (B, 16) bf16 index query required")
+    if B != cache.batch_size or hd != cache.head_dim:
+        raise ValueError(f"{what}: q {tuple(q.shape)} does not match the cache")
+    pos_rows, pos_val = None, 0
+    if isinstance(pos, Tensor):
+        pos_rows = pos.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+    else:
+        pos_val = int(pos)
+    cap = max(int(max_remote_blocks), int(min_remote_blocks), 1)
+    vp = cache.vp_cache if return_context else None
+    out, pages, counts, ctx = _decode_step_op(
+        q2, cache.kp_cache, vp, int(completed_pages), float(top_p), int(min_remote_blocks), int(max_remote_blocks),
+        cap, bool(return_context), q3, cache.k_cache, cache.v_cache, cache.page_table, cache.max_pages,
+        cache.n_phys_pages, pos_rows, pos_val, int(window), cache.num_kv_heads, float(scale), bool(batch0))
+    if return_context:
+        return out, pages, counts, ctx
+    return out, pages, counts
+
+
 def _cache_args(cache: FovealKVCache):
     return (cache.k_cache, cache.v_cache, cache.page_table if cache.paged else None, cache.max_pages,
             cache.n_phys_pages if cache.paged else 0, cache.max_seq_len, cache.page_size, cache.num_kv_heads)
@@ -880,6 +954,16 @@ class FovealSparseAttention(nn.Module):
 
         completed = kv_cache.completed_pages
         want_ctx = self.use_additive_stream and completed > 0
+        fused = (kv_cache.paged and qi.dtype == torch.bfloat16
+                 and not (torch.is_grad_enabled() and q.requires_grad))
+        if fused:  # routing beside the local-window attention, one stream
+            res = decode_step_attention(
+                q, qi, kv_cache, pos=pos, window=self.local_window, completed_pages=completed,
+                top_p=self.indexer.top_p, min_remote_blocks=self.indexer.min_remote_blocks,
+                max_remote_blocks=self.indexer.max_remote_blocks, scale=self.scale, return_context=want_ctx,
+                batch0=self.reference_batch0_pages)
+            attn, pages, counts = res[0], res[1], res[2]
+            return self._decode_finish(attn, pages, counts, res[3] if want_ctx else None, batch)
         routed = decode_route(
             qi, kv_cache.kp_cache, kv_cache.vp_cache, pos=pos, page_size=self.page_size,
             local_window=self.local_window, completed_pages=completed, top_p=self.indexer.top_p,
@@ -892,9 +976,12 @@ class FovealSparseAttention(nn.Module):
             att_counts = counts[:1].expand(batch).contiguous()
         attn = decode_attention(q, kv_cache, pos=pos, window=self.local_window, remote_pages=att_pages,
                                 remote_counts=att_counts, scale=self.scale)
+        return self._decode_finish(attn, pages, counts, routed[2] if want_ctx else None, batch)
+
+    def _decode_finish(self, attn: Tensor, pages: Tensor, counts: Tensor, ctx: Optional[Tensor], batch: int):
         out = self.out_proj(attn.reshape(batch, 1, self.num_heads * self.head_dim))
-        if want_ctx:
-            out = out + self.indexer.out_proj(routed[2].view(batch, 1, -1))
+        if ctx is not None:
+            out = out + self.indexer.out_proj(ctx.view(batch, 1, -1))
         cnt = counts.tolist()
         rows = pages.tolist()
         selected: List[List[int]] = [rows[b][:cnt[b]] for b in range(batch)]

@@ -24,6 +24,9 @@
 // torch.sort leaves the order of equal probabilities unspecified; lower index
 // first is used here.  That, and ulp-level exp/sum differences, are the only
 // ways a selection can differ from the CPU reference (near-ties).
+#include <atomic>
+
+#include "decode_attn_body.h"
 #include "fsi_common.h"
 
 using namespace fsi;
@@ -83,25 +86,38 @@ __device__ __forceinline__ void bitonic_desc(uint64_t (&v)[E]) {
   }
 }
 
-// Number of keys >= t in the row: one compare mask and scalar popcount per
-// register slot, no cross-lane data movement.
+// Sum of an int over the wave with VALU operations only: DPP steps inside each
+// row of 16 lanes (quad xor 1, quad xor 2, half-row mirror, row mirror), then
+// gfx950's permlane16 / permlane32 swaps across the four rows.  Every lane
+// receives the total.
+__device__ __forceinline__ int wave_sum_dpp(int x) {
+  x += __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);
+  x += __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);
+  x += __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);
+  x += __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false);
+  const auto a = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(x), static_cast<uint32_t>(x), false, false);
+  x = static_cast<int>(a[0]) + static_cast<int>(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(x), static_cast<uint32_t>(x), false, false);
+  return static_cast<int>(b[0]) + static_cast<int>(b[1]);
+}
+
+// Number of keys >= t in the row: a per-lane compare-and-add over the register
+// slots, then one wave sum.  (A ballot + scalar popcount per slot chains every
+// compare to a scalar instruction; this form measured 1.2x faster at 32 slots
+// and 1.8x at 64 on gfx950.)
 template <int PL>
 __device__ __forceinline__ int count_ge(const uint32_t (&key)[PL], uint32_t t) {
   int c = 0;
 #pragma unroll
-  for (int i = 0; i < PL; ++i) c += __popcll(__ballot(key[i] >= t));
-  return c;
+  for (int i = 0; i < PL; ++i) c += key[i] >= t ? 1 : 0;
+  return __builtin_amdgcn_readfirstlane(wave_sum_dpp(c));
 }
 
-// The R largest keys (0 < R <= min(64 E, #candidates)), sorted descending into
-// out[] (element k at lane k % 64, slot k / 64); entries k >= R hold 0.
-// lds_k / lds_i: this wave's 64 E words each.
-template <int PL, int E>
-__device__ void rank_top(const uint32_t (&key)[PL], int R, uint64_t (&out)[E], uint32_t* lds_k, uint32_t* lds_i) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int e = 0; e < E; ++e) out[e] = 0;
-  if (R <= 0) return;
+// Threshold of the R largest keys of the wave (R > 0; keys 0 are never counted):
+// T = the R-th largest key (or 1 when fewer than R keys are non-zero) and
+// clo = the number of keys >= T, found by bisection on scalars.
+template <int PL>
+__device__ __forceinline__ void top_threshold(const uint32_t (&key)[PL], int R, uint32_t& T, int& clo) {
   uint32_t mx = 0;
 #pragma unroll
   for (int i = 0; i < PL; ++i) mx = key[i] > mx ? key[i] : mx;
@@ -109,9 +125,10 @@ __device__ void rank_top(const uint32_t (&key)[PL], int R, uint64_t (&out)[E], u
     const uint32_t o = __shfl_xor(mx, off, 64);
     mx = o > mx ? o : mx;
   }
-  // Invariant: count_ge(lo) >= R > count_ge(hi).
+  mx = __builtin_amdgcn_readfirstlane(mx);  // uniform: the bisection runs on scalars
+  // Invariant: count_ge(lo) >= R > count_ge(hi) (or lo = 1 with fewer keys).
   uint32_t lo = 1, hi = mx + 1;
-  int clo = count_ge<PL>(key, lo);
+  clo = count_ge<PL>(key, lo);
   while (clo != R && hi - lo > 1) {
     const uint32_t mid = lo + (hi - lo) / 2;
     const int c = count_ge<PL>(key, mid);
@@ -122,8 +139,16 @@ __device__ void rank_top(const uint32_t (&key)[PL], int R, uint64_t (&out)[E], u
       hi = mid;
     }
   }
-  const uint32_t T = lo;
-  // clo == R: take every key >= T.  Otherwise take keys > T, then keys == T by index.
+  T = lo;
+}
+
+// The R largest keys by (key desc, slot asc), compacted in slot order (slot i of
+// lane l is element 64 i + l) into lds_k[0..n) with index idx(i) in lds_i;
+// returns n = min(R, #non-zero keys).  When clo == R every key >= T is taken;
+// otherwise the keys > T, then keys == T in slot order.
+template <int PL, class IdxFn>
+__device__ __forceinline__ int take_top(const uint32_t (&key)[PL], int R, uint32_t T, int clo, uint32_t* lds_k,
+                                        uint32_t* lds_i, IdxFn idx) {
   const uint32_t strict = clo == R ? T : T + 1;
   int base = 0;
 #pragma unroll
@@ -133,7 +158,7 @@ __device__ void rank_top(const uint32_t (&key)[PL], int R, uint64_t (&out)[E], u
     if (take) {
       const int pos = base + lanes_below(b);
       lds_k[pos] = key[i];
-      lds_i[pos] = static_cast<uint32_t>(i * 64 + lane);
+      lds_i[pos] = idx(i);
     }
     base += __popcll(b);
   }
@@ -145,11 +170,19 @@ __device__ void rank_top(const uint32_t (&key)[PL], int R, uint64_t (&out)[E], u
       const int pos = base + lanes_below(b);
       if (eq && pos < R) {
         lds_k[pos] = key[i];
-        lds_i[pos] = static_cast<uint32_t>(i * 64 + lane);
+        lds_i[pos] = idx(i);
       }
       base += __popcll(b);
     }
   }
+  return base < R ? base : R;
+}
+
+// Composite keys of lds_k / lds_i[0..R), sorted descending into out[] (element k
+// at lane k % 64, slot k / 64); entries k >= R hold 0.
+template <int E>
+__device__ __forceinline__ void sort_taken(int R, uint64_t (&out)[E], const uint32_t* lds_k, const uint32_t* lds_i) {
+  const int lane = lane_id();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -159,6 +192,22 @@ __device__ void rank_top(const uint32_t (&key)[PL], int R, uint64_t (&out)[E], u
     out[e] = k < R ? comp_key(lds_k[k], lds_i[k]) : 0;
   }
   bitonic_desc<E>(out);
+}
+
+// The R largest keys (0 < R <= min(64 E, #candidates)), sorted descending into
+// out[] (element k at lane k % 64, slot k / 64); entries k >= R hold 0.
+// lds_k / lds_i: this wave's 64 E words each.
+template <int PL, int E>
+__device__ void rank_top(const uint32_t (&key)[PL], int R, uint64_t (&out)[E], uint32_t* lds_k, uint32_t* lds_i) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int e = 0; e < E; ++e) out[e] = 0;
+  if (R <= 0) return;
+  uint32_t T;
+  int clo;
+  top_threshold<PL>(key, R, T, clo);
+  take_top<PL>(key, R, T, clo, lds_k, lds_i, [&](int i) { return static_cast<uint32_t>(i * 64 + lane); });
+  sort_taken<E>(R, out, lds_k, lds_i);
 }
 
 // Running mass of the sorted probabilities for k < n; 0 elsewhere.
@@ -488,17 +537,18 @@ __global__ __launch_bounds__(64 * SR_WAVES) void score_route_kernel(const void* 
 
 // ---------------------------------------------------------------------------
 // decode_step page routing (attention.py:313-337) and additive-stream context
-// (attention.py:369-376), one 16-wave workgroup per sequence.
+// (attention.py:369-376), one 4-wave workgroup per sequence.
 //   qi: (B, d) 16-D query (dtype), kp: (B, P, d) fp32 page keys,
 //   vp: (B, P, d) page values (dtype); pages [0, completed) are complete.
 // Every thread scores pages t, t + 1024, ... into LDS; the context is the
 // softmax over all completed pages (probabilities cast to vp's dtype)
 // contracted with vp; routing runs when completed > flp > 0 (flp = first local
 // page) over pages [0, flp): count = max(K_min, min(#(cum < top_p) + 1,
-// min(K_max, flp))), at most flp.  The top candidates are selected by all 16
-// waves from the LDS scores and sorted by wave 0.
+// min(K_max, flp))), at most flp.  The top candidates are selected in two
+// stages (every wave over its slice, then wave 0 over their candidates) and
+// sorted by wave 0.
 // ---------------------------------------------------------------------------
-constexpr int DR_THREADS = 1024;
+constexpr int DR_THREADS = 256;
 constexpr int DR_WAVES = DR_THREADS / 64;
 
 __device__ __forceinline__ float dr_block_max(float v, float* red) {
@@ -577,135 +627,36 @@ __device__ __forceinline__ float dr_wave_sum16_scatter(const float (&v)[16], int
   return e;
 }
 
-// Sum of the DR_WAVES per-wave words at w (16-byte aligned), read as four
-// 16-byte vectors (every lane reads the same words: broadcast reads).
-__device__ __forceinline__ int dr_sum16(const int* w) {
-  const int4* v = reinterpret_cast<const int4*>(w);
-  int total = 0;
-#pragma unroll
-  for (int q = 0; q < DR_WAVES / 4; ++q) {
-    const int4 a = v[q];
-    total += a.x + a.y + a.z + a.w;
-  }
-  return total;
-}
+struct RouteArgs {
+  const void* qi;
+  const float* kp;
+  const void* vp;
+  const int32_t* pos_rows;
+  int32_t* out_pages;
+  int32_t* out_cnt;
+  void* out_ctx;
+  int B, P, pos, page, window, completed, k_min, k_max, cap;
+  float top_p, sqrt_d;
+};
 
-// Candidates >= t in the workgroup (thread t holds candidates t + DR_THREADS i):
-// one ballot per key slot, one LDS word per wave, one barrier.  cnt holds two
-// banks of DR_WAVES words used alternately, so a bank is rewritten only after
-// every wave has passed the barrier that followed its last read.
-template <int NPT>
-__device__ __forceinline__ int dr_count_ge(const uint32_t (&key)[NPT], uint32_t t, int* cnt, int& bank) {
-  int c = 0;
-#pragma unroll
-  for (int i = 0; i < NPT; ++i) c += __popcll(__ballot(key[i] >= t));
-  if (lane_id() == 0) cnt[bank * DR_WAVES + (threadIdx.x >> 6)] = c;
-  __syncthreads();
-  const int total = dr_sum16(cnt + bank * DR_WAVES);
-  bank ^= 1;
-  return total;
-}
-
-// Workgroup-wide form of rank_top's selection: the R largest keys (R > 0) are
-// found by the same bisection, with every wave counting its own keys, and are
-// compacted in candidate order (ties at the threshold by lower index) into
-// lds_k / lds_i.  Every thread of the workgroup calls it; sorting is left to
-// the caller.
-template <int NPT>
-__device__ void dr_select_top(const uint32_t (&key)[NPT], int R, uint32_t* lds_k, uint32_t* lds_i, int* cnt) {
-  const int lane = lane_id(), wave = threadIdx.x >> 6;
-  int bank = 0;
-  uint32_t mx = 0;
-#pragma unroll
-  for (int i = 0; i < NPT; ++i) mx = key[i] > mx ? key[i] : mx;
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t o = __shfl_xor(mx, off, 64);
-    mx = o > mx ? o : mx;
-  }
-  if (lane == 0) cnt[wave] = static_cast<int>(mx);
-  __syncthreads();
-  {
-    const int4* v = reinterpret_cast<const int4*>(cnt);
-    mx = 0;
-#pragma unroll
-    for (int q = 0; q < DR_WAVES / 4; ++q) {
-      const int4 a = v[q];
-      const uint32_t m0 = static_cast<uint32_t>(a.x) > static_cast<uint32_t>(a.y) ? a.x : a.y;
-      const uint32_t m1 = static_cast<uint32_t>(a.z) > static_cast<uint32_t>(a.w) ? a.z : a.w;
-      const uint32_t m2 = m0 > m1 ? m0 : m1;
-      mx = m2 > mx ? m2 : mx;
-    }
-  }
-  bank = 1;
-  // Invariant: count_ge(lo) >= R > count_ge(hi).  All values are uniform.
-  uint32_t lo = 1, hi = mx + 1;
-  int clo = dr_count_ge<NPT>(key, lo, cnt, bank);
-  while (clo != R && hi - lo > 1) {
-    const uint32_t mid = lo + (hi - lo) / 2;
-    const int c = dr_count_ge<NPT>(key, mid, cnt, bank);
-    if (c >= R) {
-      lo = mid;
-      clo = c;
-    } else {
-      hi = mid;
-    }
-  }
-  const uint32_t T = lo;
-  const uint32_t strict = clo == R ? T : T + 1;
-  // two passes (keys > T, then keys == T while fewer than R), each in candidate
-  // order: slot i, then wave, then lane; the counts use their own two banks
-  int* cc = cnt + 2 * DR_WAVES;
-  bank = 0;
-  int base = 0;
-  for (int pass = 0; pass < 2; ++pass) {
-    if (pass == 1 && (strict == T || base >= R)) break;  // uniform
-#pragma unroll
-    for (int i = 0; i < NPT; ++i) {
-      const bool take = pass == 0 ? key[i] >= strict : key[i] == T;
-      const uint64_t b = __ballot(take);
-      if (lane == 0) cc[bank * DR_WAVES + wave] = __popcll(b);
-      __syncthreads();
-      int before = 0, total = 0;
-      const int4* v4 = reinterpret_cast<const int4*>(cc + bank * DR_WAVES);
-#pragma unroll
-      for (int q = 0; q < DR_WAVES / 4; ++q) {
-        const int4 a = v4[q];
-        const int vals[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          before += 4 * q + e < wave ? vals[e] : 0;
-          total += vals[e];
-        }
-      }
-      bank ^= 1;
-      const int pos = base + before + lanes_below(b);
-      if (take && pos < R) {
-        lds_k[pos] = key[i];
-        lds_i[pos] = static_cast<uint32_t>(threadIdx.x + DR_THREADS * i);
-      }
-      base += total;
-    }
-  }
-  __syncthreads();
-}
-
+// Routing of sequence b by one DR_THREADS workgroup.
 template <int PL, int E, bool BF16>
-__global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __restrict__ qi,
-                                                                  const float* __restrict__ kp,
-                                                                  const void* __restrict__ vp, int P,
-                                                                  const int32_t* __restrict__ pos_rows, int pos,
-                                                                  int page, int window, int completed, float top_p,
-                                                                  int k_min, int k_max, int cap, float sqrt_d,
-                                                                  int32_t* __restrict__ out_pages,
-                                                                  int32_t* __restrict__ out_cnt,
-                                                                  void* __restrict__ out_ctx) {
+__device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
+  const void* __restrict__ qi = A.qi;
+  const float* __restrict__ kp = A.kp;
+  const void* __restrict__ vp = A.vp;
+  const int32_t* __restrict__ pos_rows = A.pos_rows;
+  int32_t* __restrict__ out_pages = A.out_pages;
+  int32_t* __restrict__ out_cnt = A.out_cnt;
+  void* __restrict__ out_ctx = A.out_ctx;
+  const int P = A.P, pos = A.pos, page = A.page, window = A.window, completed = A.completed;
+  const int k_min = A.k_min, k_max = A.k_max, cap = A.cap;
+  const float top_p = A.top_p, sqrt_d = A.sqrt_d;
   __shared__ float sc[64 * PL];
   __shared__ float red[DR_WAVES];
   __shared__ float ctx_part[DR_WAVES][SR_D];
   __shared__ uint32_t lk[64 * E], li[64 * E];
-  __shared__ __attribute__((aligned(16))) int dr_cnt[4 * DR_WAVES];
   const int lane = lane_id(), wave = threadIdx.x >> 6;
-  const int b = blockIdx.x;
   const int mypos = pos_rows ? pos_rows[b] : pos;
   const int local_start = mypos + 1 - window > 0 ? mypos + 1 - window : 0;
   const int flp = local_start / page;
@@ -833,23 +784,58 @@ __global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __
   int R = kcap > k_min ? kcap : k_min;
   R = R < flp ? R : flp;
   R = R < cap ? R : cap;
-  if (route && R > 0) {  // uniform: every thread takes part in the selection
-    uint32_t key[NPT];
+  // Selection in two stages when the pages fill every wave: wave w takes the R
+  // best of its own slice [64 PW w, 64 PW (w + 1)) (key desc, index asc), then
+  // wave 0 takes the R best of those <= DR_WAVES R candidates, kept in index
+  // order so ties resolve as over the whole row.  (The R best of the row are
+  // among the candidates: a page with R pages of its slice ahead of it has R
+  // pages of the row ahead of it.)  Each stage is a scalar bisection without
+  // workgroup barriers; one barrier separates them.
+  constexpr int PW = PL / DR_WAVES;  // slots per lane of one wave's slice
+  constexpr int RS = 64 * E;         // candidate slots per wave
+  __shared__ uint32_t cand_k[PW >= 1 ? DR_WAVES * RS : 1], cand_i[PW >= 1 ? DR_WAVES * RS : 1];
+  __shared__ int n_cand[DR_WAVES];
+  if constexpr (PW >= 1) {
+    if (route && R > 0) {  // uniform
+      uint32_t key[PW];
 #pragma unroll
-    for (int i = 0; i < NPT; ++i) {
-      const int j = threadIdx.x + DR_THREADS * i;
-      key[i] = j < flp ? __float_as_uint(expf(sc[j] - mx) / z) + 1u : 0u;
+      for (int i = 0; i < PW; ++i) {
+        const int j = 64 * (PW * wave + i) + lane;
+        key[i] = j < flp ? __float_as_uint(expf(sc[j] - mx) / z) + 1u : 0u;
+      }
+      uint32_t T;
+      int clo;
+      top_threshold<PW>(key, R, T, clo);
+      const int n = take_top<PW>(key, R, T, clo, cand_k + wave * RS, cand_i + wave * RS,
+                                 [&](int i) { return static_cast<uint32_t>(64 * (PW * wave + i) + lane); });
+      if (lane == 0) n_cand[wave] = n;
     }
-    dr_select_top<NPT>(key, R, lk, li, dr_cnt);
+    __syncthreads();
   }
-  if (wave != 0) return;  // sorting and output by wave 0 only; no workgroup barrier follows
+  if (wave != 0) return;  // no workgroup barrier follows
   if (route && R > 0) {
+    if constexpr (PW >= 1) {
+      constexpr int PC = DR_WAVES * RS / 64;  // candidate slots per lane
+      uint32_t key[PC];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int k = e * 64 + lane;
-      sorted[e] = k < R ? comp_key(lk[k], li[k]) : 0;
+      for (int i = 0; i < PC; ++i) {
+        const int f = 64 * i + lane;  // candidate f = slot f % RS of wave f / RS: index order
+        key[i] = f % RS < n_cand[f / RS] ? cand_k[f] : 0u;
+      }
+      uint32_t T;
+      int clo;
+      top_threshold<PC>(key, R, T, clo);
+      take_top<PC>(key, R, T, clo, lk, li, [&](int i) { return cand_i[64 * i + lane]; });
+      sort_taken<E>(R, sorted, lk, li);
+    } else {
+      uint32_t key[PL];
+#pragma unroll
+      for (int i = 0; i < PL; ++i) {
+        const int j = 64 * i + lane;
+        key[i] = j < flp ? __float_as_uint(expf(sc[j] - mx) / z) + 1u : 0u;
+      }
+      rank_top<PL, E>(key, R, sorted, lk, li);
     }
-    bitonic_desc<E>(sorted);
     float cum[E];
     running_mass<E, false>(sorted, R, cum);
     const int first = first_reaching<E>(cum, R, top_p);
@@ -867,6 +853,11 @@ __global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(const void* __
   }
   for (int k = 64 * E + lane; k < cap; k += 64) pages[k] = -1;
   if (lane == 0) out_cnt[b] = count;
+}
+
+template <int PL, int E, bool BF16>
+__global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(RouteArgs A) {
+  decode_route_block<PL, E, BF16>(A, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -992,6 +983,80 @@ int pick_e(int64_t r) { return r <= 64 ? 1 : 4; }
     __VA_ARGS__;                \
   }
 
+int decode_route_check(const void* qi, const float* kp, const void* vp, int dtype, int64_t B, int64_t P,
+                       int64_t index_dim, int64_t pos, int64_t page_size, int64_t window, int64_t completed_pages,
+                       int capacity, const int32_t* out_pages, const int32_t* out_counts, const void* out_context) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "decode_route: dtype %d", dtype);
+  FSI_CHECK_ARG(index_dim == SR_D, FSI_ERR_SHAPE, "decode_route: index_dim %lld != %d", (long long)index_dim, SR_D);
+  FSI_CHECK_ARG(B >= 0 && P >= 0 && page_size > 0 && window >= 0 && pos >= 0 && completed_pages >= 0 &&
+                    completed_pages <= P && pos < (int64_t)0x7fffffff,
+                FSI_ERR_SHAPE, "decode_route: inconsistent sizes");
+  FSI_CHECK_ARG(completed_pages <= FSI_ROUTE_MAX_BLOCKS, FSI_ERR_CAPACITY, "decode_route: %lld pages > %d",
+                (long long)completed_pages, FSI_ROUTE_MAX_BLOCKS);
+  FSI_CHECK_ARG(capacity >= 0 && capacity <= R_MAX, FSI_ERR_CAPACITY, "decode_route: capacity %d > %d", capacity,
+                R_MAX);
+  if (B == 0) return FSI_OK;
+  FSI_CHECK_ARG(B <= (int64_t)0x7fffffff, FSI_ERR_SHAPE, "decode_route: batch too large");
+  FSI_CHECK_ARG(qi && kp && out_pages && out_counts && (vp || !out_context), FSI_ERR_INVALID_ARG,
+                "decode_route: null pointer");
+  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(kp) % 16 == 0 &&
+                    (!out_context || reinterpret_cast<uintptr_t>(vp) % 16 == 0),
+                FSI_ERR_ALIGN, "decode_route: page keys/values must be 16-byte aligned");
+  return FSI_OK;
+}
+
+
+// Ranked slots a routing call needs: min(max(K_max, K_min), capacity).
+int64_t want_of(int k_min, int k_max, int capacity) {
+  const int64_t want = k_max > k_min ? k_max : k_min;
+  return want < capacity ? want : capacity;
+}
+
+// Workgroups of `kernel` one CU holds at once (DR_THREADS threads, no dynamic LDS).
+template <class K>
+int resident_per_cu(K kernel) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, DR_THREADS, 0) != hipSuccess || n <= 0) n = 1;
+  return n;
+}
+
+// Compute units of the current device (queried once per device).
+int compute_units() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+RouteArgs route_args(const void* qi, const float* kp, const void* vp, int64_t B, int64_t P, const int32_t* pos_rows,
+                     int64_t pos, int64_t page_size, int64_t window, int64_t completed_pages, float top_p, int k_min,
+                     int k_max, int capacity, int32_t* out_pages, int32_t* out_counts, void* out_context) {
+  const int win = static_cast<int>(window < 0x7fffffff ? window : 0x7fffffff);
+  const float sqrt_d = static_cast<float>(sqrt(static_cast<double>(SR_D)));
+  return RouteArgs{qi, kp, vp, pos_rows, out_pages, out_counts, out_context, (int)B, (int)P, (int)pos,
+                   (int)page_size, win, (int)completed_pages, k_min, k_max, capacity, top_p, sqrt_d};
+}
+
+// Fused decode step, launch 1: workgroups [0, B) route sequence b (bf16 index
+// query and page values) while the others run the local-window attention
+// partials, DS_WAVES independent waves each; the routing workgroups come first
+// in dispatch order.
+constexpr int DS_WAVES = DR_THREADS / 64;
+
+template <int PL, int E, int HD>
+__global__ __launch_bounds__(DR_THREADS) void decode_step_kernel(RouteArgs A, DecodeParams L) {
+  if (static_cast<int>(blockIdx.x) < A.B) {
+    decode_route_block<PL, E, true>(A, blockIdx.x);
+    return;
+  }
+  decode_partial_wave<HD>(L, (static_cast<int>(blockIdx.x) - A.B) * DS_WAVES + (threadIdx.x >> 6));
+}
+
 }  // namespace
 
 extern "C" {
@@ -1080,41 +1145,77 @@ FSI_API int fsi_decode_route(const void* qi, const float* kp, const void* vp, in
                              int64_t window, int64_t completed_pages, float top_p, int k_min, int k_max,
                              int capacity, int32_t* out_pages, int32_t* out_counts, void* out_context,
                              void* stream) {
-  using namespace fsi_host;
-  FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "decode_route: dtype %d", dtype);
-  FSI_CHECK_ARG(index_dim == SR_D, FSI_ERR_SHAPE, "decode_route: index_dim %lld != %d", (long long)index_dim, SR_D);
-  FSI_CHECK_ARG(B >= 0 && P >= 0 && page_size > 0 && window >= 0 && pos >= 0 && completed_pages >= 0 &&
-                    completed_pages <= P && pos < (int64_t)0x7fffffff,
-                FSI_ERR_SHAPE, "decode_route: inconsistent sizes");
-  FSI_CHECK_ARG(completed_pages <= FSI_ROUTE_MAX_BLOCKS, FSI_ERR_CAPACITY, "decode_route: %lld pages > %d",
-                (long long)completed_pages, FSI_ROUTE_MAX_BLOCKS);
-  FSI_CHECK_ARG(capacity >= 0 && capacity <= R_MAX, FSI_ERR_CAPACITY, "decode_route: capacity %d > %d", capacity,
-                R_MAX);
-  if (B == 0) return FSI_OK;
-  FSI_CHECK_ARG(B <= (int64_t)0x7fffffff, FSI_ERR_SHAPE, "decode_route: batch too large");
-  FSI_CHECK_ARG(qi && kp && out_pages && out_counts && (vp || !out_context), FSI_ERR_INVALID_ARG,
-                "decode_route: null pointer");
-  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(kp) % 16 == 0 &&
-                    (!out_context || reinterpret_cast<uintptr_t>(vp) % 16 == 0),
-                FSI_ERR_ALIGN, "decode_route: page keys/values must be 16-byte aligned");
+  const int c = decode_route_check(qi, kp, vp, dtype, B, P, index_dim, pos, page_size, window, completed_pages,
+                                   capacity, out_pages, out_counts, out_context);
+  if (c != FSI_OK || B == 0) return c;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const float sqrt_d = static_cast<float>(sqrt(static_cast<double>(index_dim)));
+  const RouteArgs A = route_args(qi, kp, vp, B, P, pos_rows, pos, page_size, window, completed_pages, top_p, k_min,
+                                 k_max, capacity, out_pages, out_counts, out_context);
   int64_t want = k_max > k_min ? k_max : k_min;
   want = want < capacity ? want : capacity;
-  const int win = static_cast<int>(window < 0x7fffffff ? window : 0x7fffffff);
   FSI_DISPATCH_PL(pick_pl(completed_pages), FSI_DISPATCH_E(pick_e(want), {
     if (dtype == FSI_DTYPE_BF16)
-      decode_route_kernel<PL, E, true><<<(unsigned)B, DR_THREADS, 0, st>>>(
-          qi, kp, vp, (int)P, pos_rows, (int)pos, (int)page_size, win, (int)completed_pages, top_p, k_min, k_max,
-          capacity, sqrt_d, out_pages, out_counts, out_context);
+      decode_route_kernel<PL, E, true><<<(unsigned)B, DR_THREADS, 0, st>>>(A);
     else
-      decode_route_kernel<PL, E, false><<<(unsigned)B, DR_THREADS, 0, st>>>(
-          qi, kp, vp, (int)P, pos_rows, (int)pos, (int)page_size, win, (int)completed_pages, top_p, k_min, k_max,
-          capacity, sqrt_d, out_pages, out_counts, out_context);
+      decode_route_kernel<PL, E, false><<<(unsigned)B, DR_THREADS, 0, st>>>(A);
   }))
   FSI_HIP_LAUNCH_CHECK("decode_route");
   return FSI_OK;
 }
+
+FSI_API int fsi_decode_step_attn(const void* qi, const float* kp, const void* vp, int64_t P, int64_t completed_pages,
+                                 float top_p, int k_min, int k_max, int capacity, int32_t* out_pages,
+                                 int32_t* out_counts, void* out_context, const void* q, const void* k_pool,
+                                 const void* v_pool, const int32_t* page_table, int64_t max_pages,
+                                 int64_t n_phys_pages, const int32_t* pos_rows, int64_t pos, int64_t window,
+                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale, int batch0,
+                                 void* out, void* workspace, size_t workspace_bytes, int* err, void* stream) {
+  int c = decode_route_check(qi, kp, vp, FSI_DTYPE_BF16, B, P, SR_D, pos, PAGE, window, completed_pages, capacity,
+                             out_pages, out_counts, out_context);
+  if (c != FSI_OK) return c;
+  c = decode_attn_check(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window, out_pages,
+                        out_counts, capacity, B, Hq, Hkv, head_dim, out);
+  if (c != FSI_OK || B == 0) return c;
+  const size_t need = FSI_WORKSPACE_COUNTER_BYTES +
+                      decode_attn_partials_bytes(B, Hq, Hkv, head_dim, window, capacity, max_pages) + 256;
+  FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE,
+                "decode_step_attn: workspace %zu < %zu bytes", workspace_bytes, need);
+  FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, FSI_ERR_ALIGN,
+                "decode_step_attn: workspace must be 16-byte aligned");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES;
+  const RouteArgs A = route_args(qi, kp, vp, B, P, pos_rows, pos, PAGE, window, completed_pages, top_p, k_min, k_max,
+                                 capacity, out_pages, out_counts, out_context);
+  // launch 1: routing workgroups [0, B) beside the local-window partials (which read no routing result),
+  // with as many local waves as fit beside the routing workgroups in one round of resident workgroups,
+  // so that no second round trails the first
+  int per_cu = 1;
+  FSI_DISPATCH_PL(pick_pl(completed_pages), FSI_DISPATCH_E(pick_e(want_of(k_min, k_max, capacity)), {
+    per_cu = head_dim == 128 ? resident_per_cu(decode_step_kernel<PL, E, 128>)
+                             : resident_per_cu(decode_step_kernel<PL, E, 64>);
+  }))
+  const int64_t slots = static_cast<int64_t>(compute_units()) * per_cu;
+  const int s_fit = slots > B ? static_cast<int>((slots - B) * DS_WAVES / (B * Hkv)) : 1;
+  const int s_local = s_fit > 0 ? s_fit : 1;
+  const DecodeParams L = decode_params(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
+                                       nullptr, nullptr, capacity, capacity, B, Hq, Hkv, scale, ws, err, DA_LOCAL,
+                                       s_local);
+  const int64_t local_waves = B * Hkv * L.S_sub;
+  const unsigned grid = static_cast<unsigned>(B + (local_waves + DS_WAVES - 1) / DS_WAVES);
+  FSI_DISPATCH_PL(pick_pl(completed_pages), FSI_DISPATCH_E(pick_e(want_of(k_min, k_max, capacity)), {
+    if (head_dim == 128) decode_step_kernel<PL, E, 128><<<grid, DR_THREADS, 0, st>>>(A, L);
+    else decode_step_kernel<PL, E, 64><<<grid, DR_THREADS, 0, st>>>(A, L);
+  }))
+  FSI_HIP_LAUNCH_CHECK("decode_step_attn route + local");
+  // launch 2: the remote pages' partials and the merge of both
+  const DecodeParams R = decode_params(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
+                                       out_pages, out_counts, batch0 ? 0 : capacity, capacity, B, Hq, Hkv, scale, ws,
+                                       err, DA_REMOTE, s_local);
+  c = decode_partial_launch(R, head_dim, st);
+  return c != FSI_OK ? c : decode_merge_launch(R, head_dim, out, st);
+}
+
+
 
 FSI_API int fsi_masked_softmax(const void* scores, int dtype, int64_t B, int64_t Q, int64_t N, const uint8_t* mask,
                                int64_t mask_stride_b, int64_t mask_stride_q, int64_t mask_stride_n, void* out,

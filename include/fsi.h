@@ -387,6 +387,24 @@ FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_poo
                             int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale,
                             void* out, void* workspace, size_t workspace_bytes, int* err, void* stream);
 
+/* Fused decode step: fsi_decode_route (bf16 index query and page values, page
+ * size 64, index_dim 16) and fsi_decode_attn (bf16 paged pools) in two
+ * launches: workgroups routing each sequence run beside the local-window
+ * attention partials (which read no routing result), then the selected pages'
+ * partials and the merge.  Outputs as the two calls: pages / counts (context
+ * optional) and out.  batch0 != 0: every sequence attends sequence 0's pages,
+ * as the reference's decode_step does (attention.py:348).  Workspace:
+ * fsi_decode_attn_workspace_size(B, Hq, Hkv, head_dim, window, capacity,
+ * max_pages).  Replaces decode_step's routing + attention
+ * (attention.py:313-365). */
+FSI_API int fsi_decode_step_attn(const void* qi, const float* kp, const void* vp, int64_t P, int64_t completed_pages,
+                                 float top_p, int k_min, int k_max, int capacity, int32_t* out_pages,
+                                 int32_t* out_counts, void* out_context, const void* q, const void* k_pool,
+                                 const void* v_pool, const int32_t* page_table, int64_t max_pages,
+                                 int64_t n_phys_pages, const int32_t* pos_rows, int64_t pos, int64_t window,
+                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale, int batch0,
+                                 void* out, void* workspace, size_t workspace_bytes, int* err, void* stream);
+
 /* Decode attention over the reference's contiguous cache layout
  * (FovealKVCache k_cache / v_cache (B, Hkv, max_seq, head_dim), attention.py:45-57),
  * fp32 or bf16, any page size, head_dim 1..256: the same support as

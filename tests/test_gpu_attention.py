@@ -73,6 +73,80 @@ def test_decode_attention_parity(fsi, dev, case):
     assert Pt.rel_l2(out.float(), ref.float()) <= TOL
 
 
+FUSED_CASES = [
+    # B, Hq, Hkv, hd, max_seq, pos (int or per-sequence), window, K_min, K_max, top_p
+    (2, 8, 2, 128, 1024, 900, 128, 0, 3, 0.8),
+    (3, 16, 4, 64, 4096, [4000, 3000, 2500], 512, 1, 6, 0.9),
+    (4, 32, 8, 128, 8192, 8191, 1024, 0, 32, 0.9),
+    (1, 8, 8, 64, 2048, 2047, 64, 2, 70, 0.95),  # more than 64 candidates: 4 sort slots per lane
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=[f"f{i}" for i in range(len(FUSED_CASES))])
+@pytest.mark.parametrize("batch0", [False, True])
+def test_decode_step_attention_fused(fsi, dev, case, batch0):
+    """fsi_decode_step_attn: routing workgroups beside the local-window partials,
+    then the selected pages and the merge.  Pages, counts and context equal the
+    separate decode_route call exactly (same routing code); the attention is
+    checked against the fp64 oracle over the routed pages."""
+    B, Hq, Hkv, hd, max_seq, pos, W, kmin, kmax, top_p = case
+    print(f"[case] fused decode step {case} batch0={batch0}", flush=True)
+    c, k, v = _cache(fsi, dev, B, Hkv, hd, max_seq, seed=B * 7 + hd)
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(B, Hq, hd, generator=g).bfloat16().to(dev)
+    qi = torch.nn.functional.rms_norm(torch.randn(B, 16, generator=g), (16,)).bfloat16().to(dev)
+    c.kp_cache.copy_(torch.nn.functional.normalize(torch.randn(B, c.max_pages, 16, generator=g), dim=-1).to(dev))
+    c.vp_cache.copy_(torch.randn(B, c.max_pages, 16, generator=g).bfloat16().to(dev))
+    pos_arg = torch.tensor(pos, dtype=torch.int32, device=dev) if isinstance(pos, list) else pos
+    pos_max = max(pos) if isinstance(pos, list) else pos
+    completed = (pos_max + 1) // 64
+    scale = 1.0 / math.sqrt(hd)
+    with torch.no_grad():
+        out, pages, counts, ctx = fsi.decode_step_attention(
+            q, qi, c, pos=pos_arg, window=W, completed_pages=completed, top_p=top_p, min_remote_blocks=kmin,
+            max_remote_blocks=kmax, scale=scale, return_context=True, batch0=batch0)
+        rp, rc, rctx = fsi.decode_route(qi, c.kp_cache, c.vp_cache, pos=pos_arg, page_size=64, local_window=W,
+                                        completed_pages=completed, top_p=top_p, min_remote_blocks=kmin,
+                                        max_remote_blocks=kmax, return_context=True)
+    assert torch.equal(pages, rp) and torch.equal(counts, rc) and torch.equal(ctx, rctx)
+    cnt = counts.cpu().tolist()
+    sel = [pages[b, :cnt[b]].cpu().tolist() for b in range(B)]
+    att = [sel[0]] * B if batch0 else sel
+    ref = A.decode_attention_f64(q.cpu().float(), k, v, pos, W, att, 64, scale)
+    assert Pt.rel_l2(out.cpu().float(), ref.float()) <= TOL
+
+
+def test_decode_step_attention_graph_replays(fsi, dev):
+    """The fused step captured in a graph and replayed with eager work in between:
+    every replay equals the eager result."""
+    B, Hq, Hkv, hd, max_seq, pos, W, kmin, kmax, top_p = FUSED_CASES[2]
+    c, k, v = _cache(fsi, dev, B, Hkv, hd, max_seq, seed=21)
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(B, Hq, hd, generator=g).bfloat16().to(dev)
+    qi = torch.nn.functional.rms_norm(torch.randn(B, 16, generator=g), (16,)).bfloat16().to(dev)
+    c.kp_cache.copy_(torch.nn.functional.normalize(torch.randn(B, c.max_pages, 16, generator=g), dim=-1).to(dev))
+
+    def step():
+        return fsi.decode_step_attention(q, qi, c, pos=pos, window=W, completed_pages=(pos + 1) // 64, top_p=top_p,
+                                         min_remote_blocks=kmin, max_remote_blocks=kmax, scale=0.08)
+
+    with torch.no_grad():
+        eager = step()
+        outs = {}
+        graph = torch.cuda.CUDAGraph()
+        st = torch.cuda.Stream(dev)
+        st.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(st), torch.cuda.graph(graph, stream=st):
+            outs["r"] = step()
+        torch.cuda.synchronize(dev)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize(dev)
+            for a, b in zip(outs["r"], eager):
+                assert torch.equal(a, b)
+            torch.randn(1024, 1024, device=dev).sum().item()  # eager work between replays
+
+
 def test_decode_attention_per_sequence_positions(fsi, dev):
     B, Hq, Hkv, hd = 4, 8, 2, 128
     c, k, v = _cache(fsi, dev, B, Hkv, hd, 1024, seed=7)

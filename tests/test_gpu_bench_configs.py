@@ -119,6 +119,14 @@ def test_c4_decode_attention_full_size(fsi, dev):
         err = P.rel_l2(out[b:b + 1].float(), ref.float())
         print(f"C4 seq {b} support {n} rel-L2 {err:.3e}", flush=True)
         assert n == W + PAGE * c["KMAX"] and err <= 2e-3
+    # the fused step the bench times: same pages, attention within bf16 summation-order noise
+    with torch.no_grad():
+        out2, pages2, counts2 = fsi.decode_step_attention(q, qi, cache, pos=pos, window=W,
+                                                          completed_pages=CTX // PAGE, top_p=c["TOP_P"],
+                                                          min_remote_blocks=0, max_remote_blocks=c["KMAX"],
+                                                          scale=scale)
+    assert torch.equal(pages2.cpu(), pages.cpu()) and torch.equal(counts2.cpu(), counts.cpu())
+    assert P.rel_l2(out2.cpu().float(), out.float()) <= 1e-3
 
 
 @pytest.mark.parametrize("density", bench.C5["DENSITIES"])

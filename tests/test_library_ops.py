@@ -12,7 +12,7 @@ from torch.fx.experimental.proxy_tensor import make_fx
 
 EXPECTED = {
     "additive_context", "additive_context_bwd", "block_scores", "block_scores_bwd", "block_sparse_linear",
-    "blockwise_matmul", "decode_attention", "decode_route", "dense_block_targets", "distill_kl", "distill_kl_bwd",
+    "blockwise_matmul", "decode_attention", "decode_route", "decode_step_attention", "dense_block_targets", "distill_kl", "distill_kl_bwd",
     "index_rms_norm", "index_rms_norm_bwd", "kv_page_pool", "kv_read", "kv_write", "masked_softmax",
     "masked_softmax_bwd", "mlp_router", "pattention", "pattention_pack", "pattention_packed", "pool_kv",
     "pool_kv_bwd", "route_from_scores", "score_and_route", "sparse_attention", "sram_indexer_attention", "swiglu",

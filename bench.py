@@ -61,7 +61,7 @@ DECODE_TRAFFIC_BYTES_UNPACKED = int(140566.8 * 1024)
 PREFILL_TRAFFIC_BYTES = int((393549 + 33260 + 196761 + 34494) * 1024)
 C4_TRAFFIC_BYTES = int((407891 + 4617) * 1024)
 C2_TRAFFIC_BYTES = int((2335 + 2112) * 1024)
-C5_TRAFFIC_BYTES = {0.10: (714 + 64) << 20, 0.25: (1665 + 64) << 20, 0.50: (2910 + 64) << 20}
+C5_TRAFFIC_BYTES = {0.10: (578 + 64) << 20, 0.25: (1366 + 64) << 20, 0.50: (2583 + 64) << 20}
 # C2: wave-level VALU instructions of one score_route_kernel launch (rocprofv3 SQ_INSTS_VALU)
 C2_VALU_INSTS = 84_080_701
 VALU_PEAK_GIPS = 256 * 4 * 2.4 / 4  # G wave64 VALU instructions/s: 256 CUs x 4 SIMDs x 2.4 GHz / 4 cycles
@@ -450,7 +450,7 @@ def bench_block_sparse(fsi, args, dev):
                                  for d, v in lines.items()}})
     res["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                        "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": C5_TRAFFIC_BYTES[0.25],
-                       "kernel": "bsgemm_kernel<N_DIRECT, K_LIST> (+3 small list-building launches)",
+                       "kernel": "tile_list_gemm_kernel (k-block lists built in its prologue)",
                        "flops_per_launch": flops}
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))

@@ -138,7 +138,13 @@ def blockwise_matmul(x2d: Tensor, weight: Tensor, tile_mask: Tensor, block_k: in
     if mask.dim() == 1:
         mask = mask[None]
     rpg = rows_per_group if rows_per_group is not None else max(M, 1)
-    m8 = mask.to(torch.uint8).contiguous()
+    # bool and uint8 masks are read in place as bytes (any nonzero byte is active)
+    if mask.dtype == torch.bool:
+        m8 = mask.contiguous().view(torch.uint8)
+    elif mask.dtype == torch.uint8:
+        m8 = mask.contiguous()
+    else:
+        m8 = (mask != 0).to(torch.uint8).contiguous()
     if torch.is_grad_enabled() and (x2d.requires_grad or weight.requires_grad):
         res = _BlockwiseMatmulFn.apply(x2d, weight, m8, int(block_k), int(block_n), int(rpg))
         if out is not None:

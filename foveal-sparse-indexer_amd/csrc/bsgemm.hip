@@ -9,8 +9,8 @@
 //     (active column blocks of BlockSparseLinear, gate/up rows of the active
 //     Pattention blocks);
 //   * K advances in 64-wide steps, each with its own A and B column offset
-//     (dense K, K gathered by active blocks for the Pattention down
-//     projection, or a per-tile list of active 2-D tiles).
+//     (dense K, or K gathered by active blocks for the Pattention down
+//     projection).  2-D tile-sparse products run on csrc/tile_gemm.hip.
 // Per K-step the workgroup stages A and B (16 KiB each) through a double-
 // buffered, XOR-swizzled LDS tile: the global loads are 1 KiB contiguous per
 // wave instruction and the MFMA fragment reads are free of bank conflicts.
@@ -25,9 +25,6 @@
 using namespace fsi;
 
 namespace fsi_bs_generic {  // csrc/bsgemm_generic.hip: fp32 and the bf16 tilings below do not take
-int tile_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, const uint8_t* mask,
-              int64_t groups, int64_t rows_per_group, int64_t block_k, int64_t block_n, int64_t M, int64_t N,
-              int64_t K, int dtype, void* out, int64_t ldo, hipStream_t st);
 int column_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
                 const int32_t* active_blocks, int64_t n_active, int64_t block_size, int64_t M, int64_t N, int64_t K,
                 int dtype, void* out, int64_t ldo, uint8_t* mask_ws, int* err, hipStream_t st);
@@ -52,7 +49,7 @@ constexpr int SUB = 32;  // N gather granularity
 constexpr int KTAB_MAX = 2048;
 
 enum NMode { N_DIRECT = 0, N_GATHER = 1, N_DUAL = 2 };
-enum KMode { K_DENSE = 0, K_GATHER_B = 1, K_LIST = 2 };
+enum KMode { K_DENSE = 0, K_GATHER_B = 1 };
 enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_ENERGY = 2 };
 
 struct GemmArgs {
@@ -69,13 +66,6 @@ struct GemmArgs {
   int block;                   // block size in columns (multiple of 32)
   int n_rows_total;            // rows of B (bounds for gathered ids)
   int scatter_c;               // N_GATHER: write C at the gathered column (1) or compactly (0)
-  const int32_t* tile_n;       // K_LIST: per work item, n tile index
-  const int32_t* tile_m;       // K_LIST: per work item, m tile index
-  const int32_t* klist_off;    // K_LIST: per work item, offset into klist
-  const int32_t* klist;        // K_LIST: k offsets (elements, multiple of 64)
-  int n_items;                 // K_LIST: work items
-  const uint8_t* tmask;        // K_LIST: [groups][nkb * nnb] tile mask (k-major tile ids)
-  int tgroups, rows_per_group, nkb, nnb, block_k, block_n;
   int m_tiles, n_tiles;        // dense grid (non-list modes)
   int act, rounding;           // EPI_SWIGLU
   int* err;
@@ -172,19 +162,10 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
   const int wm = wave >> 1, wn = wave & 1;
 
   // ---- which tile ----------------------------------------------------------
-  int mt, nt, kcount, koff = 0;
-  if (KM == K_LIST) {
-    const int item = blockIdx.x;
-    mt = g.tile_m[item];
-    nt = g.tile_n[item];
-    koff = g.klist_off[item];
-    kcount = g.klist_off[item + 1] - koff;
-  } else {
-    // consecutive workgroups walk down M for one N tile: the B tile stays hot in L2
-    mt = blockIdx.x % g.m_tiles;
-    nt = blockIdx.x / g.m_tiles;
-    kcount = KM == K_GATHER_B ? g.n_blocks * (g.block / TK) : (g.K + TK - 1) / TK;
-  }
+  // consecutive workgroups walk down M for one N tile: the B tile stays hot in L2
+  const int mt = blockIdx.x % g.m_tiles;
+  const int nt = blockIdx.x / g.m_tiles;
+  const int kcount = KM == K_GATHER_B ? g.n_blocks * (g.block / TK) : (g.K + TK - 1) / TK;
   const int m0 = mt * TM;
 
   // ---- per 32-column sub-block: B row base (and pointer) and C column base --
@@ -221,25 +202,12 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
       set_error(g.err, FSI_ERR_INDEX_RANGE);
   }
 
-  // K_LIST: the tile mask row of this tile's row group and each sub-block's n block
-  const uint8_t* gmask = nullptr;
-  int nbs[4] = {0, 0, 0, 0};
-  if (KM == K_LIST) {
-    int grp = m0 / g.rows_per_group;
-    grp = grp < g.tgroups ? grp : g.tgroups - 1;
-    gmask = g.tmask + static_cast<int64_t>(grp) * g.nkb * g.nnb;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) nbs[s] = (nt * TN + s * SUB) / g.block_n;
-  }
-
   // ---- global -> register staging: thread loads 4 A chunks and 4 B chunks ----
   // chunk q = tid + 256 i: row q / 8, k chunk q % 8 (16 B)
   const int lrow0 = tid >> 3, lchunk = tid & 7;
   // K_GATHER_B: kb_rows = columns of B (bounds for the gathered blocks)
   auto k_cols = [&](int step, int64_t& a_k, int64_t& b_k) -> bool {
-    if (KM == K_LIST) {
-      a_k = b_k = g.klist[koff + step];
-    } else if (KM == K_GATHER_B) {
+    if (KM == K_GATHER_B) {
       const int per = g.block / TK;
       const int col = ktab[step / per];
       a_k = static_cast<int64_t>(step) * TK;
@@ -258,12 +226,6 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
     const bool kval = k_cols(step, a_k, b_k);
     if (!kval && g.err) set_error(g.err, FSI_ERR_INDEX_RANGE);
     const int kk = static_cast<int>((KM == K_DENSE ? a_k : 0) + lchunk * 8);  // element k within the problem
-    bool tile_on[4] = {true, true, true, true};
-    if (KM == K_LIST) {  // (k block, n block) tiles outside the mask contribute nothing
-      const int kb = static_cast<int>(a_k / g.block_k);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) tile_on[s] = nbs[s] < g.nnb && gmask[kb * g.nnb + nbs[s]] != 0;
-    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = lrow0 + 32 * i;
@@ -275,7 +237,7 @@ __global__ __launch_bounds__(GT, GEMM_WG_PER_CU) void bsgemm_kernel(GemmArgs g) 
       const bf16_t* bp = (NM == N_DUAL && s >= 2) ? g.B1 : g.B0;
       const int64_t row = brow[s] + (r % SUB);
       const bool rin = NM != N_DIRECT || row < g.N;  // direct N: rows past N (N % 32 != 0) are not read
-      if (bval[s] && rin && kin && kval && tile_on[s])
+      if (bval[s] && rin && kin && kval)
         rb[i] = *reinterpret_cast<const u32x4_t*>(bp + row * g.ldb + b_k + lchunk * 8);
       else rb[i] = u32x4_t{0u, 0u, 0u, 0u};
     }
@@ -539,7 +501,6 @@ __device__ __forceinline__ void grouped_tile(int lid, int m_tiles, int n_tiles, 
 
 template <int NM, int KM, int EPI>
 __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
-  static_assert(KM != K_LIST, "tile lists run on the 128 x 128 kernel");
   __shared__ __attribute__((aligned(16))) bf16_t lds[2][2][BM * BK];  // [stage][A/B][row * 32 + k]
   __shared__ int32_t ktab[KM == K_GATHER_B ? KTAB_MAX : 1];
   const int tid = threadIdx.x;
@@ -845,7 +806,6 @@ template <int NM, int KM, int EPI, bool PB = false>
 __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   static_assert(!PB || (NM == N_DUAL && KM == K_DENSE) || (NM == N_DIRECT && KM == K_GATHER_B),
                 "packed B: gate/up (dual, dense K) or down (direct, gathered K)");
-  static_assert(KM != K_LIST, "tile lists run on the 128 x 128 kernel");
   __shared__ __attribute__((aligned(1024))) bf16_t lds[DSTAGES][2][BM * DK];  // [stage][A/B][row * 32 + k]
   __shared__ int32_t ktab[KM == K_GATHER_B ? KTAB_MAX : 1];
   const int tid = threadIdx.x;
@@ -1237,75 +1197,6 @@ __global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t* __restrict__ p, i
 }
 
 // Work list of a 2-D tile mask: one item per (128-row tile, 128-column tile).
-// mask: [groups][num_k_blocks * num_n_blocks] uint8, tile id k_b * num_n_blocks + n_b
-// (block_matmul.py:384-385).  Item (mt, nt) gathers the 64-wide k steps of
-// every k block at which any n block of column tile nt is active; the GEMM
-// loader zeroes the weight rows of (k block, n block) tiles outside the mask,
-// so a column tile holding several n blocks with different masks stays exact.
-__global__ __launch_bounds__(256) void tile_list_kernel(const uint8_t* __restrict__ mask, int groups, int rows_per_group,
-                                                        int m_tiles, int n_tiles, int nkb, int nnb, int block_k,
-                                                        int block_n, int32_t* __restrict__ item_m,
-                                                        int32_t* __restrict__ item_n, int32_t* __restrict__ counts) {
-  const int item = blockIdx.x * 256 + threadIdx.x;
-  if (item >= m_tiles * n_tiles) return;
-  const int mt = item / n_tiles, nt = item % n_tiles;
-  const int grp = (mt * TM) / rows_per_group;
-  const uint8_t* gm = mask + static_cast<int64_t>(grp < groups ? grp : groups - 1) * nkb * nnb;
-  const int nb0 = (nt * TN) / block_n, nb1 = ((nt + 1) * TN - 1) / block_n;
-  int cnt = 0;
-  for (int kb = 0; kb < nkb; ++kb) {
-    bool any = false;
-    for (int nb = nb0; nb <= nb1 && nb < nnb; ++nb) any |= gm[kb * nnb + nb] != 0;
-    if (any) cnt += block_k / TK;
-  }
-  item_m[item] = mt;
-  item_n[item] = nt;
-  counts[item] = cnt;
-}
-
-__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ counts, int n,
-                                                     int32_t* __restrict__ offsets) {
-  // single workgroup exclusive scan (n items), offsets[n] = total
-  __shared__ int32_t part[1024];
-  const int t = threadIdx.x;
-  const int per = (n + 1023) / 1024;
-  int s = 0;
-  for (int i = t * per; i < (t + 1) * per && i < n; ++i) s += counts[i];
-  part[t] = s;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int v = t >= off ? part[t - off] : 0;
-    __syncthreads();
-    part[t] += v;
-    __syncthreads();
-  }
-  int run = t > 0 ? part[t - 1] : 0;
-  for (int i = t * per; i < (t + 1) * per && i < n; ++i) {
-    offsets[i] = run;
-    run += counts[i];
-  }
-  if (t == 1023) offsets[n] = part[1023];
-}
-
-__global__ __launch_bounds__(256) void tile_klist_kernel(const uint8_t* __restrict__ mask, int groups,
-                                                         int rows_per_group, int n_tiles, int nkb, int nnb,
-                                                         int block_k, int block_n, const int32_t* __restrict__ offsets,
-                                                         int n_items, int32_t* __restrict__ klist) {
-  const int item = blockIdx.x * 256 + threadIdx.x;
-  if (item >= n_items) return;
-  const int mt = item / n_tiles, nt = item % n_tiles;
-  const int grp = (mt * TM) / rows_per_group;
-  const uint8_t* gm = mask + static_cast<int64_t>(grp < groups ? grp : groups - 1) * nkb * nnb;
-  const int nb0 = (nt * TN) / block_n, nb1 = ((nt + 1) * TN - 1) / block_n;
-  int o = offsets[item];
-  for (int kb = 0; kb < nkb; ++kb) {
-    bool any = false;
-    for (int nb = nb0; nb <= nb1 && nb < nnb; ++nb) any |= gm[kb * nnb + nb] != 0;
-    if (any)
-      for (int s = 0; s < block_k / TK; ++s) klist[o++] = kb * block_k + s * TK;
-  }
-}
-
 template <int NM, int KM, int EPI>
 hipError_t launch(const GemmArgs& a, unsigned grid, hipStream_t st) {
   bsgemm_kernel<NM, KM, EPI><<<grid, GT, 0, st>>>(a);
@@ -1328,11 +1219,9 @@ hipError_t launch_tiled(GemmArgs& a, bool big, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles;
   // Direct-to-LDS for dense K; the K-gathered down projection reads half lines
   // per 32-wide step and runs better on the 64-wide-step kernel.
-  if constexpr (KM != K_LIST) {
-    if (big && FSI_GEMM_DMA && (KM == K_GATHER_B ? FSI_GEMM_DMA_KGATHER != 0 : a.K % DK == 0)) {
-      bsgemm_dma_kernel<NM, KM, EPI><<<grid, DTHREADS, 0, st>>>(a);
-      return hipGetLastError();
-    }
+  if (big && FSI_GEMM_DMA && (KM == K_GATHER_B ? FSI_GEMM_DMA_KGATHER != 0 : a.K % DK == 0)) {
+    bsgemm_dma_kernel<NM, KM, EPI><<<grid, DTHREADS, 0, st>>>(a);
+    return hipGetLastError();
   }
   if constexpr (EPI != EPI_ENERGY) {
     if (big) {
@@ -1560,90 +1449,6 @@ FSI_API int fsi_block_sparse_linear(const void* x, int64_t ldx, const void* w, i
   a.err = err;
   const hipError_t e = launch_tiled<N_GATHER, K_DENSE, EPI_STORE>(a, M >= BIG_MIN_M, st);
   FSI_CHECK_ARG(e == hipSuccess, FSI_ERR_HIP, "block_sparse_linear: launch failed: %s", hipGetErrorString(e));
-  return FSI_OK;
-}
-
-FSI_API size_t fsi_blockwise_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int64_t block_k) {
-  (void)block_k;
-  const int64_t items = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
-  const int64_t ksteps = (K + TK - 1) / TK;
-  return FSI_WORKSPACE_COUNTER_BYTES + static_cast<size_t>(4 * (3 * items + 1) + 4 * items * ksteps) + 256;
-}
-
-FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int64_t ldw,
-                                 const uint8_t* tile_mask, int64_t groups, int64_t rows_per_group, int64_t block_k,
-                                 int64_t block_n, int64_t M, int64_t N, int64_t K, int dtype, void* out, int64_t ldo,
-                                 void* workspace, size_t workspace_bytes, void* stream) {
-  using namespace fsi_host;
-  FSI_CHECK_ARG(dtype == FSI_DTYPE_BF16 || dtype == FSI_DTYPE_F32, FSI_ERR_DTYPE, "blockwise_matmul: dtype %d",
-                dtype);
-  FSI_CHECK_ARG(M >= 0 && N > 0 && K > 0 && groups > 0 && rows_per_group > 0, FSI_ERR_SHAPE,
-                "blockwise_matmul: bad sizes");
-  if (dtype == FSI_DTYPE_F32 || block_k % TK != 0 || !(block_n % TN == 0 || TN % block_n == 0) ||
-      !(rows_per_group % TM == 0 || groups == 1) || ldx % 8 || ldw % 8 || ldo % 8) {
-    // fp32, and bf16 tilings the MFMA engine does not take: the generic kernel
-    if (M == 0) return FSI_OK;
-    FSI_CHECK_ARG(x && w && tile_mask && out, FSI_ERR_INVALID_ARG, "blockwise_matmul: null pointer");
-    return fsi_bs_generic::tile_gemm(x, ldx, w, ldw, nullptr, tile_mask, groups, rows_per_group, block_k, block_n,
-                                     M, N, K, dtype, out, ldo, reinterpret_cast<hipStream_t>(stream));
-  }
-  FSI_CHECK_ARG(block_k % TK == 0 && block_k > 0 && K % block_k == 0 && block_n > 0 && N % block_n == 0 &&
-                    (block_n % TN == 0 || TN % block_n == 0),
-                FSI_ERR_SHAPE, "blockwise_matmul: tiles %lldx%lld must be multiples of %d (K) and divide or be "
-                "multiples of %d (N)", (long long)block_k, (long long)block_n, TK, TN);
-  FSI_CHECK_ARG(rows_per_group % TM == 0 || groups == 1, FSI_ERR_SHAPE,
-                "blockwise_matmul: rows_per_group %lld must be a multiple of %d", (long long)rows_per_group, TM);
-  FSI_CHECK_ARG(ldx % 8 == 0 && ldw % 8 == 0 && ldo % 8 == 0 && ldx >= K && ldw >= K && ldo >= N, FSI_ERR_ALIGN,
-                "blockwise_matmul: leading dimensions");
-  FSI_CHECK_ARG(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, FSI_ERR_SHAPE,
-                "blockwise_matmul: sizes beyond int32");
-  if (M == 0) return FSI_OK;
-  FSI_CHECK_ARG(x && w && tile_mask && out, FSI_ERR_INVALID_ARG, "blockwise_matmul: null pointer");
-  const size_t need = fsi_blockwise_matmul_workspace_size(M, N, K, block_k);
-  FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE, "blockwise_matmul: workspace %zu < %zu",
-                workspace_bytes, need);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int m_tiles = (int)((M + TM - 1) / TM), n_tiles = (int)((N + TN - 1) / TN);
-  const int items = m_tiles * n_tiles;
-  const int nkb = (int)(K / block_k), nnb = (int)(N / block_n);
-  int32_t* base = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES);
-  int32_t* item_m = base;
-  int32_t* item_n = item_m + items;
-  int32_t* counts = item_n + items;
-  int32_t* offsets = counts + items;  // items + 1
-  int32_t* klist = offsets + items + 1;
-  const unsigned g1 = static_cast<unsigned>((items + 255) / 256);
-  tile_list_kernel<<<g1, 256, 0, st>>>(tile_mask, (int)groups, (int)rows_per_group, m_tiles, n_tiles, nkb, nnb,
-                                       (int)block_k, (int)block_n, item_m, item_n, counts);
-  scan_kernel<<<1, 1024, 0, st>>>(counts, items, offsets);
-  tile_klist_kernel<<<g1, 256, 0, st>>>(tile_mask, (int)groups, (int)rows_per_group, n_tiles, nkb, nnb,
-                                        (int)block_k, (int)block_n, offsets, items, klist);
-  FSI_HIP_LAUNCH_CHECK("blockwise_matmul lists");
-  GemmArgs a{};
-  a.A = static_cast<const bf16_t*>(x);
-  a.B0 = a.B1 = static_cast<const bf16_t*>(w);
-  a.C = static_cast<bf16_t*>(out);
-  a.lda = ldx;
-  a.ldb = ldw;
-  a.ldc = ldo;
-  a.M = (int)M;
-  a.N = (int)N;
-  a.K = (int)K;
-  a.tile_m = item_m;
-  a.tile_n = item_n;
-  a.klist_off = offsets;
-  a.klist = klist;
-  a.n_items = items;
-  a.tmask = tile_mask;
-  a.tgroups = (int)groups;
-  a.rows_per_group = (int)rows_per_group;
-  a.nkb = nkb;
-  a.nnb = nnb;
-  a.block_k = (int)block_k;
-  a.block_n = (int)block_n;
-  const unsigned grid = static_cast<unsigned>(items);
-  const hipError_t e = launch<N_DIRECT, K_LIST, EPI_STORE>(a, grid, st);
-  FSI_CHECK_ARG(e == hipSuccess, FSI_ERR_HIP, "blockwise_matmul: launch failed: %s", hipGetErrorString(e));
   return FSI_OK;
 }
 

@@ -520,9 +520,13 @@ FSI_API size_t fsi_blockwise_matmul_workspace_size(int64_t M, int64_t N, int64_t
  * out = x (w o T)^T where T expands tile_mask to elements: tile (k_b, n_b) of
  * size block_k x block_n is active iff tile_mask[g][k_b * (N / block_n) + n_b],
  * with g the row group of the output row (rows_per_group rows each; groups = 1
- * applies one mask to every row).  block_k multiple of 64 dividing K; block_n
- * divides N and divides or is a multiple of 128; rows_per_group a multiple of
- * 128 when groups > 1.  Rows of a group whose tiles are all inactive get 0. */
+ * applies one mask to every row).  block_k divides K, block_n divides N.  The
+ * MFMA kernel takes bf16 with block_k a multiple of 32, block_n a multiple of
+ * 128 or one of 16, 32, 64, K / block_k <= 2048, rows_per_group a multiple of
+ * 128 (or groups = 1) and 16-byte aligned x, w rows; other problems and fp32
+ * run on a generic kernel.  Rows of a group whose tiles are all inactive get 0.
+ * The workspace (fsi_blockwise_matmul_workspace_size bytes, or null) is not
+ * written: every tile builds its k-block list on chip. */
 FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int64_t ldw,
                                  const uint8_t* tile_mask, int64_t groups, int64_t rows_per_group, int64_t block_k,
                                  int64_t block_n, int64_t M, int64_t N, int64_t K, int dtype, void* out, int64_t ldo,

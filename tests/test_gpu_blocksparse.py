@@ -54,6 +54,13 @@ def test_block_sparse_linear_bad_block_reported(fsi, dev, monkeypatch):
     (384, 512, 256, 64, 64, 0.3, 3),
     (200, 256, 512, 64, 128, 0.5, 1),
     (512, 1024, 1024, 128, 128, 0.1, 4),
+    (256, 512, 384, 32, 16, 0.3, 2),       # 32-wide k blocks, 8 n blocks per 128-column tile
+    (130, 256, 320, 64, 32, 0.4, 1),       # ragged M and N (N % 128 == 64)
+    (256, 8192, 256, 32, 128, 0.6, 1),     # ~150 active k blocks per tile: list read 64 at a time
+    (128, 16384, 256, 32, 256, 0.05, 1),   # 512 k blocks: two rounds of the list build; 256-wide n blocks
+    (384, 1024, 512, 128, 64, 0.0, 3),     # empty masks: every tile stores zeros
+    (256, 512, 512, 64, 128, 1.0, 2),      # dense masks
+    (96, 192, 96, 64, 48, 0.5, 1),         # n block dividing neither way: generic kernel
 ])
 def test_blockwise_matmul(fsi, dev, M, K, N, bk, bn, density, groups):
     print(f"[case] blockwise_matmul M={M} K={K} N={N} tile={bk}x{bn} d={density} groups={groups}", flush=True)
@@ -66,6 +73,9 @@ def test_blockwise_matmul(fsi, dev, M, K, N, bk, bn, density, groups):
     rpg = -(-rpg // 128) * 128 if groups > 1 else rpg
     out = fsi.blockwise_matmul(x.to(dev), w.to(dev), masks.to(dev), bk, bn, rows_per_group=rpg).cpu()
     ref = BS.blockwise_matmul_f64(x, w, masks, bk, bn, rpg)
+    if not masks.any():
+        assert torch.equal(out, torch.zeros_like(out))
+        return
     assert _rel(out, ref) <= TOL
 
 

@@ -20,6 +20,7 @@ from .pattention import (
     pattention_forward,
     triton_fused_swiglu,
     triton_pattention,
+    unpack_pattention_weights,
 )
 from .core import (
     FovealIndexer,
@@ -54,6 +55,7 @@ from .foveal_pattention import (
     compute_teacher_dense_block_targets,
     load_foveal_pattention_mlps,
     mlp_pooled_route,
+    release_unpacked_weights,
     sparsify_model_with_foveal_pattention,
 )
 
@@ -89,6 +91,8 @@ __all__ = [
     "pattention_forward",
     "pattention_decode_packed",
     "pack_pattention_weights",
+    "unpack_pattention_weights",
+    "release_unpacked_weights",
     "PackedPattentionWeights",
     "dense_block_targets",
     "compute_teacher_dense_block_targets",

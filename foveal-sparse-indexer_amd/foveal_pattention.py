@@ -27,6 +27,7 @@ from torch import Tensor, nn
 from . import _lib
 from .pattention import (
     FusedSwiGLUFunction,
+    PACKED_PREFILL_MIN_M,
     PackedPattentionWeights,
     dense_block_targets,
     _weights_key,
@@ -35,6 +36,7 @@ from .pattention import (
     pattention_decode_packed,
     pattention_forward,
     triton_fused_swiglu,
+    unpack_pattention_weights,
 )
 
 
@@ -117,10 +119,7 @@ class _EvalPattentionFn(torch.autograd.Function):
     def backward(ctx, dy: Tensor):
         m = ctx.module
         x_2d, active_blocks = ctx.saved_tensors
-        idx = (active_blocks.view(-1, 1).to(torch.int64) * m.block_size + m.offsets).flatten()
-        kg = m.k_gate.detach().index_select(0, idx)
-        ku = m.k_up.detach().index_select(0, idx)
-        v = m.v.detach().index_select(0, idx)
+        kg, ku, v = m._active_rows(active_blocks)
         g = F.linear(x_2d, kg)
         u = F.linear(x_2d, ku)
         dh = F.linear(dy.to(x_2d.dtype), v)
@@ -138,6 +137,8 @@ class _SavedGU:
 
 class FovealPattentionMLP(nn.Module):
     """Foveal block-sparse SwiGLU Pattention layer (foveal_pattention.py:54-352)."""
+
+    _released = False  # pack-in-place inference mode (release_unpacked_weights)
 
     def __init__(
         self,
@@ -200,11 +201,18 @@ class FovealPattentionMLP(nn.Module):
             return None
         g = getattr(self, "_gathered", None)
         if g is None or g[0] is not blocks:
-            idx = (blocks.view(-1, 1).to(torch.int64) * self.block_size + self.offsets).flatten()
-            g = (blocks, self.k_gate[idx].detach().contiguous(), self.k_up[idx].detach().contiguous(),
-                 self.v[idx].detach().contiguous())
+            g = (blocks, *self._active_rows(blocks))
             self._gathered = g
         return g[1 + which]
+
+    def _active_rows(self, blocks: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+        """Detached contiguous rows of k_gate, k_up and v for the given blocks,
+        from the parameters or, once they are released, from the packed copy."""
+        if self._released:
+            return unpack_pattention_weights(self._packed, blocks.reshape(-1).to(torch.int64))
+        idx = (blocks.view(-1, 1).to(torch.int64) * self.block_size + self.offsets).flatten()
+        return (self.k_gate.detach().index_select(0, idx), self.k_up.detach().index_select(0, idx),
+                self.v.detach().index_select(0, idx))
 
     def _cache_attr_set(self, value) -> None:
         # The reference's caches are plain attributes that callers reset with None
@@ -224,14 +232,80 @@ class FovealPattentionMLP(nn.Module):
         the tensors' version counters, which is how in-place changes through the
         parameters themselves are detected).  load_state_dict and module moves
         call it."""
+        if self._released:
+            raise RuntimeError("the packed copy is the only copy of k_gate / k_up / v "
+                               "(release_unpacked_weights); call unpack_weights() first")
         self._packed = None
 
+    # -- pack-in-place inference mode ----------------------------------------
+    def release_unpacked_weights(self) -> int:
+        """Keep only the packed copy of k_gate, k_up and v and free the parameters'
+        storage: decode and prefill read nothing else, so an inference-only
+        model holds the MLP weights once instead of twice (336 MiB less per
+        Llama-3-8B layer).  Returns the bytes released.
+
+        While released: eval forward runs for bf16 tokens of any count (65..255
+        tokens in 64-token pieces of the decode kernels) and still gives input
+        gradients; state_dict() returns the weights unpacked from the packed copy,
+        and _cached_kg / _cached_ku / _cached_v are unpacked on demand; a module
+        move (.to, .cuda, ...) and load_state_dict unpack first.  Training
+        forward, fp32 input, calibrate_offline_svd and reset_parameters raise
+        until unpack_weights() restores the parameters (bit-exact)."""
+        if self._released:
+            return 0
+        what = "release_unpacked_weights"
+        _lib.require_gpu(self.k_gate, what=what)
+        if self.k_gate.dtype != torch.bfloat16:
+            raise TypeError(f"{what}: bfloat16 weights required, not {self.k_gate.dtype}")
+        n_ch = self.total_active_blocks * self.block_size
+        for m in (1, PACKED_PREFILL_MIN_M):
+            if not packed_decode_supported(m, self.hidden_dim, self.v.shape[1], self.intermediate_dim,
+                                           self.block_size, n_ch):
+                raise ValueError(f"{what}: the packed kernels do not take this layer's shape "
+                                 f"(hidden {self.hidden_dim}, intermediate {self.intermediate_dim}, "
+                                 f"block {self.block_size}, {n_ch} active channels)")
+        self._packed_weights()
+        freed = 0
+        for p in (self.k_gate, self.k_up, self.v):
+            freed += p.numel() * p.element_size()
+            p.data = torch.empty(0, dtype=p.dtype, device=p.device)
+        self._released = True
+        self._gathered = None
+        return freed
+
+    def unpack_weights(self) -> None:
+        """Leave the pack-in-place mode: rebuild k_gate, k_up and v from the packed
+        copy (bit-exact; v in its down_proj storage order), which stays valid."""
+        if not self._released:
+            return
+        kg, ku, v = unpack_pattention_weights(self._packed)
+        self.k_gate.data = kg
+        self.k_up.data = ku
+        self.v.data = v.t().contiguous().t()
+        self._released = False
+        self._packed.key = _weights_key(self.k_gate, self.k_up, self.v)
+
+    def _require_unpacked(self, what: str) -> None:
+        if self._released:
+            raise RuntimeError(f"{what} needs k_gate / k_up / v, which release_unpacked_weights() freed; "
+                               "call unpack_weights() first")
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        if self._released:
+            kg, ku, v = unpack_pattention_weights(self._packed)
+            destination[prefix + "k_gate"] = kg
+            destination[prefix + "k_up"] = ku
+            destination[prefix + "v"] = v
+
     def _load_from_state_dict(self, *args, **kwargs):
+        self.unpack_weights()
         self.invalidate_packed_weights()
         self._gathered = None
         return super()._load_from_state_dict(*args, **kwargs)
 
     def _apply(self, fn, *args, **kwargs):
+        self.unpack_weights()
         self.invalidate_packed_weights()
         self._gathered = None
         return super()._apply(fn, *args, **kwargs)
@@ -248,6 +322,7 @@ class FovealPattentionMLP(nn.Module):
         self._gathered = None
 
     def reset_parameters(self) -> None:
+        self._require_unpacked("reset_parameters")
         std = self.hidden_dim ** -0.5
         nn.init.normal_(self.k_gate, std=std)
         nn.init.normal_(self.k_up, std=std)
@@ -308,6 +383,7 @@ class FovealPattentionMLP(nn.Module):
         The SVD, the fp32 products and the solve are library calls (torch.linalg,
         hipBLASLt): this is a one-time conversion step.  Singular vectors carry an
         arbitrary sign per component; the router scores do not depend on it."""
+        self._require_unpacked("calibrate_offline_svd")
         _lib.require_gpu(self.k_gate, what="calibrate_offline_svd")
         device = self.k_gate.device
         orig_dtype = self.k_gate.dtype
@@ -354,6 +430,8 @@ class FovealPattentionMLP(nn.Module):
                                             self.block_size, active_blocks.numel() * self.block_size))
 
     def _packed_weights(self) -> PackedPattentionWeights:
+        if self._released:
+            return self._packed
         key = _weights_key(self.k_gate, self.k_up, self.v)
         if self._packed is None or self._packed.key != key:
             self._packed = None
@@ -370,6 +448,15 @@ class FovealPattentionMLP(nn.Module):
         HIP kernels: packed weights for bf16 decode / prefill shapes, the
         parameters in place otherwise."""
         with torch.no_grad():
+            if self._released:
+                if x_2d.dtype != torch.bfloat16:
+                    self._require_unpacked(f"eval forward of {x_2d.dtype} tokens")
+                M = x_2d.shape[0]
+                if 64 < M < PACKED_PREFILL_MIN_M:  # neither decode nor prefill shape: 64-token pieces
+                    return torch.cat([pattention_decode_packed(x_2d[i:i + 64], self._packed, active_blocks,
+                                                               rounding=self._rounding())
+                                      for i in range(0, M, 64)])
+                return pattention_decode_packed(x_2d, self._packed, active_blocks, rounding=self._rounding())
             if self._decode_packed(x_2d, active_blocks):
                 return pattention_decode_packed(x_2d, self._packed_weights(), active_blocks,
                                                 rounding=self._rounding())
@@ -416,6 +503,7 @@ class FovealPattentionMLP(nn.Module):
 
     def forward(self, x: Tensor, return_router_info: bool = False):
         if self.training:
+            self._require_unpacked("training forward")
             return self._train_forward(x.reshape(-1, x.shape[-1]), x.shape, return_router_info)
         orig_shape = x.shape
         D = orig_shape[-1]
@@ -442,6 +530,12 @@ class FovealPattentionMLP(nn.Module):
                 "sparsity": (1.0 - self.total_active_blocks / self.num_blocks) * 100.0,
             }
         return out
+
+
+def release_unpacked_weights(model: nn.Module) -> int:
+    """Pack-in-place inference mode for every FovealPattentionMLP in `model`
+    (FovealPattentionMLP.release_unpacked_weights); returns the bytes released."""
+    return sum(m.release_unpacked_weights() for m in model.modules() if isinstance(m, FovealPattentionMLP))
 
 
 def sparsify_model_with_foveal_pattention(

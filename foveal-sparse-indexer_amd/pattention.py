@@ -198,6 +198,34 @@ def pack_pattention_weights(k_gate: Tensor, k_up: Tensor, v: Tensor, block_n: in
     return PackedPattentionWeights(buf, N_p, K, D_out, block_n, key)
 
 
+def unpack_pattention_weights(packed: PackedPattentionWeights,
+                              blocks: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
+    """Inverse of pack_pattention_weights: k_gate, k_up (N_p, K) and v (N_p, D_out)
+    rebuilt from the packed buffer as new contiguous bf16 tensors (tensor views and
+    one permuted copy each, no kernel of this library).  With `blocks` (block
+    ids of block_n channels) only those blocks' rows, in that order.
+
+    Buffer layout (fsi_pattention_pack): gate tiles at byte 0, up tiles at
+    align256(2 N_p K), down tiles at twice that.  Gate / up tile (ct, s) holds
+    W[16 ct + r][32 s + 8 q + e] at element (16 q + r) 8 + e; down tile (b, dt, cl)
+    holds V[b block_n + 32 cl + 8 q + e][16 dt + r] at the same position."""
+    N_p, K, D, bn = packed.N_p, packed.K, packed.D_out, packed.block_n
+    mat = (2 * N_p * K + 255) // 256 * 256
+    buf = packed.buf
+
+    def rows(off: int) -> Tensor:
+        t = buf[off:off + 2 * N_p * K].view(torch.bfloat16).view(N_p // bn, bn // 16, K // 32, 4, 16, 8)
+        if blocks is not None:
+            t = t.index_select(0, blocks)
+        return t.permute(0, 1, 4, 2, 3, 5).reshape(-1, K)
+
+    d = buf[2 * mat:2 * mat + 2 * N_p * D].view(torch.bfloat16).view(N_p // bn, D // 16, bn // 32, 4, 16, 8)
+    if blocks is not None:
+        d = d.index_select(0, blocks)
+    v = d.permute(0, 2, 3, 5, 1, 4).reshape(-1, D)
+    return rows(0), rows(mat), v
+
+
 @_lib.fsi_op("pattention_pack", lambda k_gate, k_up, v, v_transposed, block_n: k_gate.new_empty(
     (_lib.lib().fsi_pattention_packed_size(k_gate.shape[0], k_gate.shape[1], v.shape[1]),), dtype=torch.uint8))
 def _pack_op(k_gate: Tensor, k_up: Tensor, v: Tensor, v_transposed: bool, block_n: int) -> Tensor:

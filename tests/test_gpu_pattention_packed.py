@@ -186,3 +186,76 @@ def test_packed_back_to_back_calls(fsi, dev):
     for x, act, got in cases:
         ref = P.mlp_eval_forward(x, kg, ku, v.contiguous(), act, block_n, fused=True)
         assert P.rel_l2(got.cpu(), ref) <= BF16_TOL
+
+
+def test_unpack_inverts_pack(fsi, dev):
+    """unpack_pattention_weights of the device pack: every weight back bit-exact,
+    also for a block subset, V in either storage order."""
+    g = torch.Generator().manual_seed(11)
+    for vt in (True, False):
+        kg, ku, v = _weights(1024, 512, 96, g, vt)
+        pk = fsi.pack_pattention_weights(kg.to(dev), ku.to(dev), v.to(dev), 64)
+        ukg, uku, uv = fsi.unpack_pattention_weights(pk)
+        assert torch.equal(ukg.cpu(), kg) and torch.equal(uku.cpu(), ku) and torch.equal(uv.cpu(), v)
+        blocks = torch.tensor([7, 0, 3])
+        skg, sku, sv = fsi.unpack_pattention_weights(pk, blocks.to(dev))
+        idx = (blocks.view(-1, 1) * 64 + torch.arange(64)).flatten()
+        assert torch.equal(skg.cpu(), kg[idx]) and torch.equal(sku.cpu(), ku[idx]) and torch.equal(sv.cpu(), v[idx])
+
+
+def test_module_pack_in_place_inference(fsi, dev):
+    """release_unpacked_weights: the parameters' storage is freed, eval outputs
+    (decode, 65..255 tokens in 64-token pieces, prefill) and input gradients stay
+    those of the unreleased module, state_dict and the active-row caches return the
+    original weights, training and fp32 input raise, unpack_weights restores the
+    parameters bit-exactly."""
+    torch.manual_seed(3)
+    m = fsi.FovealPattentionMLP(hidden_dim=512, intermediate_dim=2048, block_size=64, base_blocks=2,
+                                remote_blocks=6, dtype=torch.bfloat16).to(dev).eval()
+    orig = {k: t.detach().clone() for k, t in m.state_dict().items()}
+    v_stride = m.v.stride()
+    xs = {M: (torch.randn(M, 512, device=dev) * 0.5).bfloat16() for M in (16, 100, 300)}
+    m.set_active_blocks(torch.tensor([0, 1, 9, 17, 4, 30, 22, 11], dtype=torch.int32))
+    with torch.no_grad():
+        before = {M: m(x) for M, x in xs.items()}
+    xg = xs[16].clone().requires_grad_()
+    m(xg).float().square().sum().backward()
+    dx_before = xg.grad.clone()
+
+    freed = m.release_unpacked_weights()
+    assert freed == 3 * 2048 * 512 * 2
+    assert m.k_gate.numel() == 0 and m.k_up.numel() == 0 and m.v.numel() == 0
+    with torch.no_grad():
+        after = {M: m(x) for M, x in xs.items()}
+    assert torch.equal(after[16], before[16]) and torch.equal(after[300], before[300])
+    # 100 tokens ran pattention_forward before and 64-token packed pieces now
+    assert P.rel_l2(after[100].cpu().float(), before[100].cpu().float()) <= BF16_TOL
+    xg = xs[16].clone().requires_grad_()
+    m(xg).float().square().sum().backward()
+    assert torch.equal(xg.grad, dx_before)
+    sd = m.state_dict()
+    for k in ("k_gate", "k_up", "v"):
+        assert torch.equal(sd[k], orig[k]), k
+    idx = (m._cached_active_blocks.view(-1, 1).long().cpu() * 64 + torch.arange(64)).flatten()
+    assert torch.equal(m._cached_kg.cpu(), orig["k_gate"].cpu()[idx])
+    assert torch.equal(m._cached_v.cpu(), orig["v"].cpu()[idx])
+    with pytest.raises(RuntimeError):
+        m.train()(xs[16])
+    m.eval()
+    with pytest.raises(RuntimeError):
+        m(xs[16].float())
+    with pytest.raises(RuntimeError):
+        m.reset_parameters()
+
+    m.unpack_weights()
+    assert m.v.stride() == v_stride
+    for k in ("k_gate", "k_up", "v"):
+        assert torch.equal(getattr(m, k).detach(), orig[k]), k
+    with torch.no_grad():
+        assert torch.equal(m(xs[16]), before[16])
+
+    # a module move unpacks first
+    m.release_unpacked_weights()
+    m.to(dev)
+    assert m.k_gate.shape == (2048, 512) and torch.equal(m.k_gate.detach(), orig["k_gate"])
+    assert fsi.release_unpacked_weights(m) == freed

@@ -573,7 +573,7 @@ def bench_sram_attn(fsi, args, dev):
                   higher=False)
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": None,
-                       "kernel": "sram_attn_kernel (one launch per config; latency bound at these sizes)",
+                       "kernel": "sram_attn_mfma_kernel (fp16: 16x16x16 MFMA tiles; one launch per config, latency bound at these sizes)",
                        "bytes_per_launch": per_cfg}
     if not args.no_cpu_baseline:
         from oracle import attention as OA

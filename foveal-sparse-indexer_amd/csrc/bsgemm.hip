@@ -775,7 +775,16 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
 #ifndef FSI_GEMM_DMA_KGATHER
 #define FSI_GEMM_DMA_KGATHER 0
 #endif
-constexpr int DK = 32, DSTAGES = FSI_GEMM_DMA_STAGES, DTHREADS = 512;
+// Waves of the direct-to-LDS kernel: 8 (2 x 4 waves of 128 x 64) or 4 (2 x 2 waves
+// of 128 x 128, accumulators in AGPRs: 16 fragment reads per 64 MFMAs instead of
+// 12 per 32).  Measured at the 8B prefill shape, 4 waves run the K-gathered down
+// projection no faster (131.6 vs 131.4 us: one wave per SIMD leaves the barrier and
+// load waits exposed) and spill in the gate/up SwiGLU epilogue, so 8 is the default.
+#ifndef FSI_GEMM_DMA_WAVES
+#define FSI_GEMM_DMA_WAVES 8
+#endif
+constexpr int DK = 32, DSTAGES = FSI_GEMM_DMA_STAGES, DWAVES = FSI_GEMM_DMA_WAVES, DTHREADS = 64 * DWAVES;
+static_assert(DWAVES == 4 || DWAVES == 8, "direct-to-LDS GEMM waves");
 constexpr int PK_TILE_ELEMS = 512;  // bf16 elements of one packed 16 x 32 operand tile
 
 // Chunk swizzle of 64-byte LDS rows.  A 128-bit LDS read is served eight lanes at a
@@ -786,7 +795,10 @@ constexpr int PK_TILE_ELEMS = 512;  // bf16 elements of one packed 16 x 32 opera
 // 100 B/clk for a swizzle on row bits 2-3 (the SQ_LDS_BANK_CONFLICT count of the
 // GEMM drops to zero).
 __device__ __forceinline__ int dswz(int r) { return (r >> 1) & 3; }
-constexpr int DLOADS = 4;  // global_load_lds per wave and K-step: 2 KiB of A, 2 KiB of B
+constexpr int DFPW = 16 / DWAVES;      // fragments of A (and of B) each wave loads per K-step
+constexpr int DLOADS = 2 * DFPW;       // global_load_lds per wave and K-step
+constexpr int DFB = 32 / DWAVES;       // B fragments a wave multiplies (A: 8)
+constexpr int DFBH = DFB / 2;          // of them in each 128-column half (gate / up)
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
@@ -815,7 +827,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   }
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves of 128 x 64
+  const int wm = wave / (DWAVES / 2), wn = wave % (DWAVES / 2);  // 2 x (DWAVES / 2) waves
 
   const int lid = xcd_group_id(blockIdx.x, gridDim.x);
   int mt, nt;
@@ -857,21 +869,21 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
 
   // ---- this lane's source rows.  A stage holds each operand row-major, 64 bytes
   // (4 chunks of 16) per row, the chunk of row r at physical slot chunk ^ dswz(r).
-  // Wave w loads KiB 2 w and 2 w + 1 of A and of B (16 rows each): lane l lands at
-  // row 16 KiB + l / 4, slot l % 4, so it loads the logical chunk (l % 4) ^ dswz(row).
-  // Packed B: the stage holds B as 16 fragments of 1 KiB in lane order (fragment
-  // fi = tile columns 16 fi .. 16 fi + 15) and wave w loads fragments 2 w, 2 w + 1
-  // straight from their packed tiles: one contiguous KiB per load.
-  const bf16_t* asrc[2];
-  const bf16_t* bsrc[2];
+  // Wave w loads KiB DFPW w .. DFPW w + DFPW - 1 of A and of B (16 rows each): lane l
+  // lands at row 16 KiB + l / 4, slot l % 4, so it loads the logical chunk
+  // (l % 4) ^ dswz(row).  Packed B: the stage holds B as 16 fragments of 1 KiB in
+  // lane order (fragment fi = tile columns 16 fi .. 16 fi + 15) and wave w loads its
+  // fragments straight from their packed tiles: one contiguous KiB per load.
+  const bf16_t* asrc[DFPW];
+  const bf16_t* bsrc[DFPW];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 16 * (2 * wave + j) + (lane >> 2);
+  for (int j = 0; j < DFPW; ++j) {
+    const int r = 16 * (DFPW * wave + j) + (lane >> 2);
     const int lc = (lane & 3) ^ dswz(r);
     const int m = m0 + r < g.M ? m0 + r : g.M - 1;
     asrc[j] = g.A + static_cast<int64_t>(m) * g.lda + lc * 8;
     if (PB) {
-      const int fi = 2 * wave + j;
+      const int fi = DFPW * wave + j;
       if (NM == N_DUAL) {
         const int sb = fi >> 1;                                     // 32-row sub-block
         const int64_t ct = (brow[sb] >> 4) + (fi & 1);              // 16-row packed tile
@@ -930,28 +942,31 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
       b_k = static_cast<int64_t>(step) * PK_TILE_ELEMS;  // k-step s of every row tile
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      bf16_t* da = &lds[stage][0][(2 * wave + j) * 512];
-      bf16_t* db = &lds[stage][1][(2 * wave + j) * 512];
+    for (int j = 0; j < DFPW; ++j) {
+      bf16_t* da = &lds[stage][0][(DFPW * wave + j) * 512];
+      bf16_t* db = &lds[stage][1][(DFPW * wave + j) * 512];
       __builtin_amdgcn_global_load_lds((glb_void_t*)(asrc[j] + a_k), (lds_void_t*)da, 16, 0, 0);
       __builtin_amdgcn_global_load_lds((glb_void_t*)(bsrc[j] + b_k), (lds_void_t*)db, 16, 0, 0);
     }
   };
 
-  f32x4_t acc[8][4];
+  f32x4_t acc[8][DFB];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < DFB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // wave fragments: A fragments 8 wm + i; B fragments of tile columns {32 wn + 16 f}
-  // (f < 2) and {128 + 32 wn + 16 (f - 2)}: a gate column and its up column share a lane
+  // wave fragments: A fragments 8 wm + i; B fragments of tile columns
+  // {16 DFBH wn + 16 f} (f < DFBH) and {128 + 16 DFBH wn + 16 (f - DFBH)}: a gate column
+  // and its up column share a lane
   const int frow = lane & 15;
-  auto bcol = [&](int f) { return f < 2 ? 32 * wn + 16 * f : 128 + 32 * wn + 16 * (f - 2); };
+  auto bcol = [&](int f) {
+    return f < DFBH ? 16 * DFBH * wn + 16 * f : 128 + 16 * DFBH * wn + 16 * (f - DFBH);
+  };
   const int fchunk = lane >> 4;
-  auto read_frags = [&](int stage, u32x4_t (&fa)[8], u32x4_t (&fb)[4]) {
+  auto read_frags = [&](int stage, u32x4_t (&fa)[8], u32x4_t (&fb)[DFB]) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
+    for (int f = 0; f < DFB; ++f) {
       if (PB) {
         fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[stage][1][(bcol(f) >> 4) * PK_TILE_ELEMS + lane * 8]);
       } else {
@@ -965,11 +980,11 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
       fa[i] = *reinterpret_cast<const u32x4_t*>(&lds[stage][0][r * DK + (fchunk ^ dswz(r)) * 8]);
     }
   };
-  auto mfmas = [&](const u32x4_t (&fa)[8], const u32x4_t (&fb)[4]) {
+  auto mfmas = [&](const u32x4_t (&fa)[8], const u32x4_t (&fb)[DFB]) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fb[f], fa[i], acc[i][f]);  // C^T fragment
+      for (int f = 0; f < DFB; ++f) acc[i][f] = mfma16x16x32(fb[f], fa[i], acc[i][f]);  // C^T fragment
   };
 #if FSI_GEMM_DMA_PREFETCH
   // Step s + 2 must have landed at the end of iteration s (its fragments are read
@@ -983,23 +998,26 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   };
   // One K-step: issue step + DSTAGES - 1, read step + 1's fragments while step's
   // MFMAs run.
-  auto iteration = [&](int step, const u32x4_t (&ca)[8], const u32x4_t (&cb)[4], u32x4_t (&na)[8],
-                       u32x4_t (&nb)[4]) {
+  auto iteration = [&](int step, const u32x4_t (&ca)[8], const u32x4_t (&cb)[DFB], u32x4_t (&na)[8],
+                       u32x4_t (&nb)[DFB]) {
     // the stage of step + DSTAGES - 1 was last read during iteration step - 2
     if (step + DSTAGES - 1 < kcount) issue(step + DSTAGES - 1, (step + DSTAGES - 1) % DSTAGES);
     // unconditional (past the last step it reads a stale stage that is never
     // used), so the compiler's wait before the MFMAs counts only older reads
     read_frags((step + 1) % DSTAGES, na, nb);
     mfmas(ca, cb);
-    // spread the 12 fragment reads over the MFMAs (two MFMAs first, then one read
-    // per two MFMAs) instead of leaving them to the end of the step
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    // spread the 8 + DFB fragment reads over the 8 DFB MFMAs (a few MFMAs first,
+    // then one read per 2 (8 waves) or 3 (4 waves) MFMAs) instead of leaving them
+    // to the end of the step
+    constexpr int HEAD = DWAVES == 8 ? 2 : 4, PER = DWAVES == 8 ? 2 : 3;
+    constexpr int TAIL = 8 * DFB - HEAD - (8 + DFB) * PER;
+    __builtin_amdgcn_sched_group_barrier(0x008, HEAD, 0);
 #pragma unroll
-    for (int r = 0; r < 12; ++r) {
+    for (int r = 0; r < 8 + DFB; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, TAIL, 0);
     wait_through(step);
     stage_barrier();
   };
@@ -1011,7 +1029,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   else if (pre >= 3) wait_vmcnt<DLOADS>();
   else wait_vmcnt<0>();
   stage_barrier();
-  u32x4_t fa0[8], fb0[4], fa1[8], fb1[4];
+  u32x4_t fa0[8], fb0[DFB], fa1[8], fb1[DFB];
   if (kcount > 0) read_frags(0, fa0, fb0);
   int step = 0;
   for (; step + 1 < kcount; step += 2) {
@@ -1031,7 +1049,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   stage_barrier();
   for (int step = 0; step < kcount; ++step) {
     if (step + DSTAGES - 1 < kcount) issue(step + DSTAGES - 1, (step + DSTAGES - 1) % DSTAGES);
-    u32x4_t fa[8], fb[4];
+    u32x4_t fa[8], fb[DFB];
     read_frags(step % DSTAGES, fa, fb);
     mfmas(fa, fb);
     const int last = kcount - 1 < step + DSTAGES - 1 ? kcount - 1 : step + DSTAGES - 1;
@@ -1055,27 +1073,36 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
   const bool vec = (reinterpret_cast<uintptr_t>(g.C) & 7) == 0 && (g.ldc & 3) == 0;
   const bool rows_in = m0 + BM <= g.M;
   if (EPI == EPI_SWIGLU) {
-    const bool live = bval[wn] && bval[4 + wn];  // both gate fragments lie in sub-block wn
-    const int ch0 = ccol[0] + 32 * wn + cq;
+    // gate fragment f (< DFBH) and up fragment f + DFBH: tile channel 16 DFBH wn + 16 f,
+    // in sub-block (16 DFBH wn + 16 f) / 32 of each half
+    bool live[DFBH];
+    bool all_live = true;
+#pragma unroll
+    for (int f = 0; f < DFBH; ++f) {
+      const int sb = (16 * DFBH * wn + 16 * f) / SUB;
+      live[f] = bval[sb] && bval[4 + sb];
+      all_live = all_live && live[f];
+    }
+    const int ch0 = ccol[0] + 16 * DFBH * wn + cq;
     auto interior = [&](auto rnd) {
       constexpr int R = decltype(rnd)::value;
 #pragma unroll
-      for (int f = 0; f < 2; ++f)
+      for (int f = 0; f < DFBH; ++f)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           float h[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) h[j] = swiglu_epi<R>(acc[i][f][j], acc[i][f + 2][j]);
+          for (int j = 0; j < 4; ++j) h[j] = swiglu_epi<R>(acc[i][f][j], acc[i][f + DFBH][j]);
           store4_fast(g.C, static_cast<int64_t>(crow + 16 * i) * g.ldc + ch0 + 16 * f, h);
         }
     };
-    if (vec && rows_in && live && ccol[0] + 128 <= g.N) {
+    if (vec && rows_in && all_live && ccol[0] + 128 <= g.N) {
       if (g.rounding == FSI_ROUND_FP32) interior(std::integral_constant<int, FSI_ROUND_FP32>{});
       else if (g.rounding == FSI_ROUND_FUSED) interior(std::integral_constant<int, FSI_ROUND_FUSED>{});
       else interior(std::integral_constant<int, FSI_ROUND_EAGER>{});
     } else {
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
+      for (int f = 0; f < DFBH; ++f) {
         const int ch = ch0 + 16 * f;
         if (ch >= g.N) continue;
         const int n = g.N - ch;
@@ -1086,36 +1113,41 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
           float h[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            h[j] = live ? pattention_act<ACT_SWIGLU>(acc[i][f][j], acc[i][f + 2][j], g.rounding) : 0.f;
+            h[j] = live[f] ? pattention_act<ACT_SWIGLU>(acc[i][f][j], acc[i][f + DFBH][j], g.rounding) : 0.f;
           store4_bf16(g.C, static_cast<int64_t>(m) * g.ldc + ch, h, n, vec);
         }
       }
     }
   } else if (EPI == EPI_ENERGY) {
-    // wave wn holds the tile's channels 32 wn .. 32 wn + 31 (gate fragments f = 0, 1):
-    // each lane sums its 8 channels of row 16 i + r, then the four lanes r, r + 16,
-    // r + 32, r + 48 of the row are added
-    const int grp_ch = ccol[0] + 32 * wn;
-    if (grp_ch < g.N) {
-      const bool live = bval[wn] && bval[4 + wn];
-      auto sums = [&](auto rnd) {
-        constexpr int R = decltype(rnd)::value;
+    // wave wn holds the tile's channels 16 DFBH wn .. + 16 DFBH, DFBH / 2 groups of 32
+    // (gate fragments f = 2 gi, 2 gi + 1): each lane sums its 8 channels of row
+    // 16 i + r, then the four lanes r, r + 16, r + 32, r + 48 of the row are added
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float e = 0.f;
-          if (live) {
+    for (int gi = 0; gi < DFBH / 2; ++gi) {
+      const int grp_ch = ccol[0] + 16 * DFBH * wn + 32 * gi;
+      if (grp_ch < g.N) {
+        const int sb = (16 * DFBH * wn + 32 * gi) / SUB;
+        const bool live = bval[sb] && bval[4 + sb];
+        auto sums = [&](auto rnd) {
+          constexpr int R = decltype(rnd)::value;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              e += energy_term(acc[i][0][j], acc[i][2][j], R) + energy_term(acc[i][1][j], acc[i][3][j], R);
+          for (int i = 0; i < 8; ++i) {
+            float e = 0.f;
+            if (live) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                e += energy_term(acc[i][2 * gi][j], acc[i][2 * gi + DFBH][j], R) +
+                     energy_term(acc[i][2 * gi + 1][j], acc[i][2 * gi + 1 + DFBH][j], R);
+            }
+            e = sum_rows4(e);
+            const int m = crow + 16 * i;
+            if (fchunk == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
           }
-          e = sum_rows4(e);
-          const int m = crow + 16 * i;
-          if (fchunk == 0 && m < g.M) g.E[static_cast<int64_t>(m) * g.ldc + grp_ch / SUB] = e;
-        }
-      };
-      if (g.rounding == FSI_ROUND_FP32) sums(std::integral_constant<int, FSI_ROUND_FP32>{});
-      else if (g.rounding == FSI_ROUND_FUSED) sums(std::integral_constant<int, FSI_ROUND_FUSED>{});
-      else sums(std::integral_constant<int, FSI_ROUND_EAGER>{});
+        };
+        if (g.rounding == FSI_ROUND_FP32) sums(std::integral_constant<int, FSI_ROUND_FP32>{});
+        else if (g.rounding == FSI_ROUND_FUSED) sums(std::integral_constant<int, FSI_ROUND_FUSED>{});
+        else sums(std::integral_constant<int, FSI_ROUND_EAGER>{});
+      }
     }
   } else {
     bool all = vec && rows_in;
@@ -1123,7 +1155,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
     for (int sb = 0; sb < 8; ++sb) all = all && (NM == N_DIRECT ? ccol[sb] + SUB <= g.N : bval[sb]);
     if (all) {
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
+      for (int f = 0; f < DFB; ++f) {
         const int tc = bcol(f);
         const int s = tc / SUB;
         const int col = ccol[s] + (tc % SUB) + cq;
@@ -1143,7 +1175,7 @@ __global__ __launch_bounds__(DTHREADS, 1) void bsgemm_dma_kernel(GemmArgs g) {
       }
     } else {
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
+      for (int f = 0; f < DFB; ++f) {
         const int tc = bcol(f);
         const int s = tc / SUB;
         if (NM != N_DIRECT && !bval[s]) continue;
@@ -1196,7 +1228,6 @@ __global__ __launch_bounds__(256) void fill_u8_kernel(uint8_t* __restrict__ p, i
     p[i] = 0;
 }
 
-// Work list of a 2-D tile mask: one item per (128-row tile, 128-column tile).
 template <int NM, int KM, int EPI>
 hipError_t launch(const GemmArgs& a, unsigned grid, hipStream_t st) {
   bsgemm_kernel<NM, KM, EPI><<<grid, GT, 0, st>>>(a);

@@ -166,15 +166,17 @@ __device__ __forceinline__ void decode_partial_wave(const DecodeParams& P, int w
     // V [2][HD][32]: the half is the outer index
     const bf16_t* kp = P.k_pool + head_base + half * CHUNK * 32;
     const bf16_t* vp = P.v_pool + head_base + half * CHUNK * HD;
+    // every K / V byte is read once per decode step: non-temporal loads keep the
+    // stream from displacing the queries, page tables and partials in L2
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        kr[tile * KS + ks] =
-            *reinterpret_cast<const u32x4_t*>(kp + ks * PAGE * 32 + (16 * tile + h) * 32 + 8 * grp);
+        kr[tile * KS + ks] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(kp + ks * PAGE * 32 + (16 * tile + h) * 32 + 8 * grp));
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      vr[dt] = *reinterpret_cast<const u32x4_t*>(vp + (16 * dt + h) * CHUNK + 8 * grp);
+      vr[dt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vp + (16 * dt + h) * CHUNK + 8 * grp));
   };
 
   if (c0 < c1) load_chunk(c0, kcur, vcur);

@@ -146,3 +146,31 @@ def test_blockwise_matmul_module(fsi, dev):
         ref = ref.view(2, 3, 512) + md.out_proj(ctx).double().cpu()
     assert aux["active_tiles"] == int(mask.sum())
     assert _rel(out, ref) <= 1e-2
+
+
+def test_blockwise_matmul_graph_replays(fsi, dev):
+    """The tile-sparse GEMM (k-block lists built on chip) captured in a graph and
+    replayed with eager work in between, the mask changed in place between
+    replays: every replay equals an eager call on the same mask."""
+    g = torch.Generator().manual_seed(5)
+    M, K, N, T = 256, 1024, 512, 128
+    x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16().to(dev)
+    masks = torch.rand(2, (K // T) * (N // T), generator=g) < 0.4
+    mask = masks.to(dev)
+    with torch.no_grad():
+        outs = {}
+        graph = torch.cuda.CUDAGraph()
+        st = torch.cuda.Stream(dev)
+        st.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(st), torch.cuda.graph(graph, stream=st):
+            outs["y"] = fsi.blockwise_matmul(x, w, mask, T, T, rows_per_group=T)
+        torch.cuda.synchronize(dev)
+        for r in range(3):
+            if r == 2:
+                mask.copy_((torch.rand(2, (K // T) * (N // T), generator=g) < 0.7).to(dev))
+            graph.replay()
+            torch.cuda.synchronize(dev)
+            eager = fsi.blockwise_matmul(x, w, mask, T, T, rows_per_group=T)
+            assert torch.equal(outs["y"], eager)
+            torch.randn(1024, 1024, device=dev).sum().item()  # eager work between replays

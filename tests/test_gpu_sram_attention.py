@@ -104,3 +104,26 @@ def test_reference_wrapper_and_errors(fsi, dev):
         big = torch.randn(1, 1, 256, 8, device=dev)
         fsi.triton_fused_sram_indexer_attention(big, big, big, torch.randn(1, 2, 16, device=dev),
                                                 torch.randn(1, 2, 16, device=dev), block_size=128)
+
+
+def test_graph_replays(fsi, dev):
+    """The MFMA kernel captured in a graph and replayed with eager work in between:
+    every replay equals the eager result."""
+    g = torch.Generator().manual_seed(4)
+    B, H, N, D, bs = 4, 4, 256, 32, 32
+    q, k, v = (torch.randn(B, H, N, D, generator=g).half().to(dev) for _ in range(3))
+    q16, k16 = (torch.randn(B, N // bs, 16, generator=g).half().to(dev) for _ in range(2))
+    with torch.no_grad():
+        eager = fsi.sram_indexer_attention(q, k, v, q16, k16, block_size=bs, max_remote_blocks=2)
+        outs = {}
+        graph = torch.cuda.CUDAGraph()
+        st = torch.cuda.Stream(dev)
+        st.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(st), torch.cuda.graph(graph, stream=st):
+            outs["o"] = fsi.sram_indexer_attention(q, k, v, q16, k16, block_size=bs, max_remote_blocks=2)
+        torch.cuda.synchronize(dev)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize(dev)
+            assert torch.equal(outs["o"], eager)
+            torch.randn(1024, 1024, device=dev).sum().item()

@@ -362,7 +362,7 @@ def bench_prefill_attn(fsi, args, dev):
                    "mean_remote_pages": round(float(counts.float().mean()), 2)})
     res["roofline"] = {"bound": "mfma", "achieved": round(tfs, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                        "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": None,
-                       "kernel": "sa_vt_kernel + sparse_attn_lds_kernel (2 launches)", "flops_per_launch": flops}
+                       "kernel": "sa_vmax_kernel + sa_vt16_kernel + sparse_attn_lds_kernel (3 launches)", "flops_per_launch": flops}
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))
         torch.set_num_threads(cores)

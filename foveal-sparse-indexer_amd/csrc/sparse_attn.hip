@@ -20,7 +20,12 @@
 //                                            S^T's accumulators, as a bf16 hi + lo
 //                                            pair so P keeps ~16 bits)
 // V^T comes from a workspace copy of v, dim-major per 32-token chunk with the
-// chunk's tokens in the MFMA k order of P^T, written by a first kernel.
+// chunk's tokens in the MFMA k order of P^T, written by a first kernel.  The
+// 64-query kernel (sparse_attn_lds_kernel) takes that copy in fp16, scaled per
+// (sequence, KV head) by a power of two that puts the largest finite |v| in
+// [2^14, 2^15), and P in fp16 (P <= 2^8 under its lazy running max): one
+// v_mfma_f32_16x16x32_f16 per P V tile with 11-bit P, where bf16 needs the hi +
+// lo pair to stay inside the bf16 output tolerance.
 #include <algorithm>
 #include <type_traits>
 
@@ -77,12 +82,115 @@ __global__ __launch_bounds__(256) void sa_vt_kernel(const bf16_t* __restrict__ v
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp16 V^T for sparse_attn_lds_kernel, in two kernels:
+//   sa_vmax_kernel: one wave per (b, g, 32-token chunk) writes the chunk's
+//     largest finite |v| as a bf16 magnitude pattern (0 .. 0x7f7f) to cmax;
+//   sa_vt16_kernel: workgroup (x, bg) reduces head bg's chunk maxima to the
+//     head exponent e (largest finite |v| 2^-e in [2^14, 2^15)), stores it in
+//     head_e, and writes chunks [x SA_VT_CHUNKS, ..) of the head as fp16 v 2^-e
+//     in the layout of sa_vt_kernel.
+// Values below the largest by more than 2^28 become fp16 subnormals (absolute
+// error <= 2^-25 of the largest); infinities and NaNs stay what they are.
+// ---------------------------------------------------------------------------
+constexpr int SA_VT_CHUNKS = 8;  // chunks per sa_vt16_kernel workgroup
+
+template <int HD>
+__global__ __launch_bounds__(256) void sa_vmax_kernel(const bf16_t* __restrict__ v, int64_t vs_b, int64_t vs_g,
+                                                      int64_t vs_t, int B, int Hkv, int T, int n32,
+                                                      uint32_t* __restrict__ cmax) {
+  constexpr int PIECES = HD / 8;
+  constexpr int PER = SA_CHUNK * PIECES / 64;  // 16-byte pieces per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (id >= static_cast<int64_t>(B) * Hkv * n32) return;
+  const int c = static_cast<int>(id % n32);
+  const int64_t bg = id / n32;
+  const int b = static_cast<int>(bg / Hkv), g = static_cast<int>(bg % Hkv);
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int idx = i * 64 + lane;
+    const int t = c * SA_CHUNK + idx / PIECES, piece = idx % PIECES;
+    if (t < T) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(v + b * vs_b + g * vs_g + t * vs_t + 8 * piece);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = w[j] & 0x7fffu, hi = (w[j] >> 16) & 0x7fffu;
+        m = lo < 0x7f80u && lo > m ? lo : m;  // infinities and NaNs (>= 0x7f80) are left out
+        m = hi < 0x7f80u && hi > m ? hi : m;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t o = __shfl_xor(m, off, 64);
+    m = o > m ? o : m;
+  }
+  if (lane == 0) cmax[id] = m;
+}
+
+// Exponent e with the bf16 magnitude pattern mag 2^-e in [2^14, 2^15); 0 for an
+// all-zero head, at least -100 (2^100 is the largest scale applied).
+__device__ __forceinline__ int sa_head_exponent(uint32_t mag) {
+  if (mag == 0) return 0;
+  const int E = static_cast<int>(mag >> 7);  // biased exponent; E == 0: subnormal, below 2^-126
+  const int e = (E == 0 ? -127 : E - 127) - 14;
+  return e < -100 ? -100 : e;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void sa_vt16_kernel(const bf16_t* __restrict__ v, int64_t vs_b, int64_t vs_g,
+                                                      int64_t vs_t, int Hkv, int T, int n32,
+                                                      const uint32_t* __restrict__ cmax, int32_t* __restrict__ head_e,
+                                                      uint16_t* __restrict__ vt) {
+  constexpr int PIECES = HD / 8;
+  const int bg = blockIdx.y;
+  const int b = bg / Hkv, g = bg % Hkv;
+  uint32_t m = 0;
+  for (int c = threadIdx.x; c < n32; c += 256) {
+    const uint32_t x = cmax[static_cast<int64_t>(bg) * n32 + c];
+    m = x > m ? x : m;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t o = __shfl_xor(m, off, 64);
+    m = o > m ? o : m;
+  }
+  __shared__ uint32_t red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = red[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) m = red[w] > m ? red[w] : m;
+  const int e = sa_head_exponent(m);
+  if (blockIdx.x == 0 && threadIdx.x == 0) head_e[bg] = e;
+  const float sc = __builtin_ldexpf(1.f, -e);  // exact power of two
+  const int t0 = blockIdx.x * SA_VT_CHUNKS * SA_CHUNK;
+  constexpr int ITEMS = SA_VT_CHUNKS * SA_CHUNK * PIECES;
+  for (int it = threadIdx.x; it < ITEMS; it += 256) {
+    const int t = t0 + it / PIECES, piece = it % PIECES;
+    if (t >= n32 * SA_CHUNK) break;
+    u32x4_t val = u32x4_t{0u, 0u, 0u, 0u};
+    if (t < T) val = *reinterpret_cast<const u32x4_t*>(v + b * vs_b + g * vs_g + t * vs_t + 8 * piece);
+    const int c = t / SA_CHUNK, tau = t % SA_CHUNK;
+    uint16_t* o = vt + ((static_cast<int64_t>(bg) * n32 + c) * HD * SA_CHUNK) + sa_slot(tau);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = val[j >> 1];
+      const float f = __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+      o[(8 * piece + j) * SA_CHUNK] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f * sc));
+    }
+  }
+}
+
 struct SAParams {
   const bf16_t* q;
   int64_t qs_b, qs_h, qs_t;
   const bf16_t* k;
   int64_t ks_b, ks_h, ks_t;
-  const bf16_t* vt;  // workspace copy of v
+  const bf16_t* vt;  // workspace copy of v (fp16, scaled by 2^-head_e, for sparse_attn_lds_kernel)
+  const int32_t* head_e;  // (B, Hkv) exponents of the fp16 copy
   int B, Hq, Hkv, G, T, n32, block, mode, window;
   const int32_t* lists;  // (B, Qb, cap) page / block ids, strides ls_b, ls_q
   int64_t ls_b, ls_q;
@@ -305,9 +413,9 @@ __global__ __launch_bounds__(64 * SA_WAVES) void sparse_attn_kernel(SAParams P) 
 // query tiles are formed first, then their softmax, then the P V products, so
 // consecutive MFMAs are independent.  The softmax skips the per-key mask for
 // chunks every query sees, moves its running max only by jumps above 2^8
-// (rescaling the accumulators rarely), and builds the bf16 hi + lo halves of P
-// with v_cvt_pk_bf16_f32.  Query blocks run from the last (most keys) to the
-// first.
+// (rescaling the accumulators rarely), and packs P in fp16 for one f16 MFMA
+// per P V tile against the fp16 V^T copy (sa_vt16_kernel).  Query blocks run
+// from the last (most keys) to the first.
 // ---------------------------------------------------------------------------
 // Two fp32 values to a packed bf16 pair (round to nearest even) with gfx950's
 // v_cvt_pk_bf16_f32.
@@ -315,6 +423,20 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
   typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
   const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// Two fp32 values to a packed fp16 pair (round to nearest even).
+__device__ __forceinline__ uint32_t cvt_pk_f16(float a, float b) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  const f16x2_t v = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// v_mfma_f32_16x16x32_f16 with the operand layout of mfma16x16x32.
+__device__ __forceinline__ f32x4_t mfma16x16x32_f16(const u32x4_t& a, const u32x4_t& b, f32x4_t c) {
+  typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+                                                0, 0);
 }
 
 #ifndef FSI_SAL_QT
@@ -375,6 +497,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   const int h = g * P.G + (head_live ? hg : 0);
   const int r = lane & 15, grp = lane >> 4;
   const int qb = qblk0 / P.block;
+  const float vscale = __builtin_ldexpf(1.f, P.head_e[b * P.Hkv + g]);  // undoes the fp16 copy's 2^-e
 
   // ---- listed pages: validity, first-listing de-duplication, compaction ----
   int cnt = P.counts[b * P.cs_b + qb * P.cs_q];
@@ -557,7 +680,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
                                  kc0 + SA_CHUNK <= P.T)
                               : (hi == SA_CHUNK && kc0 + SA_CHUNK - 1 <= q0 - P.window);
     float alpha[SAL_QT];
-    u32x4_t pbh[SAL_QT], pbl[SAL_QT];
+    u32x4_t pb[SAL_QT];
 #pragma unroll
     for (int qt = 0; qt < SAL_QT; ++qt) {
       const int myq = q0 + 16 * qt + r;
@@ -592,24 +715,22 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
       alpha[qt] = bump ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;  // exp2(-inf) = 0 on the first bump
       const float m_use = m_new == -INFINITY ? 0.f : m_new;  // no valid key yet: every p is exp2(-inf) = 0
       float psum = 0.f;
-      uint32_t pk_hi[4], pk_lo[4];
+      uint32_t pk[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        // P as a bf16 hi + lo pair, converted with v_cvt_pk_bf16_f32 (round to nearest even)
+        // P in fp16 (round to nearest even; P <= 2^8)
         const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w], P.scale_log2, -m_use));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w + 1], P.scale_log2, -m_use));
         psum += p0 + p1;
-        pk_hi[w] = cvt_pk_bf16(p0, p1);
-        pk_lo[w] = cvt_pk_bf16(p0 - lo_bf16(pk_hi[w]), p1 - hi_bf16(pk_hi[w]));
+        pk[w] = cvt_pk_f16(p0, p1);
       }
       psum = sum_rows4(psum);
       l_run[qt] = l_run[qt] * alpha[qt] + psum;
       m_run[qt] = m_new;
-      pbh[qt] = u32x4_t{pk_hi[0], pk_hi[1], pk_hi[2], pk_hi[3]};
-      pbl[qt] = u32x4_t{pk_lo[0], pk_lo[1], pk_lo[2], pk_lo[3]};
+      pb[qt] = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
     }
     // phase 3: rescale (skipped while no query's running max moved) and P V
-    // (hi then lo halves; consecutive MFMAs independent)
+    // (consecutive MFMAs independent)
 #pragma unroll
     for (int qt = 0; qt < SAL_QT; ++qt) {
       if (__ballot(alpha[qt] != 1.f) != 0) {
@@ -622,11 +743,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int qt = 0; qt < SAL_QT; ++qt) acc[qt][dt] = mfma16x16x32(vf[dt], pbh[qt], acc[qt][dt]);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int qt = 0; qt < SAL_QT; ++qt) acc[qt][dt] = mfma16x16x32(vf[dt], pbl[qt], acc[qt][dt]);
+      for (int qt = 0; qt < SAL_QT; ++qt) acc[qt][dt] = mfma16x16x32_f16(vf[dt], pb[qt], acc[qt][dt]);
   }
 
   if (!head_live) return;
@@ -638,8 +755,8 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
       bf16_t* o = P.out + b * P.os_b + h * P.os_h + static_cast<int64_t>(myq) * P.os_t + 4 * grp;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const u32x2_t w = u32x2_t{pack_bf16x2(acc[qt][dt][0] * inv, acc[qt][dt][1] * inv),
-                                  pack_bf16x2(acc[qt][dt][2] * inv, acc[qt][dt][3] * inv)};
+        const u32x2_t w = u32x2_t{pack_bf16x2(acc[qt][dt][0] * inv * vscale, acc[qt][dt][1] * inv * vscale),
+                                  pack_bf16x2(acc[qt][dt][2] * inv * vscale, acc[qt][dt][3] * inv * vscale)};
         *reinterpret_cast<u32x2_t*>(o + 16 * dt) = w;
       }
     }
@@ -653,8 +770,11 @@ extern "C" {
 FSI_API size_t fsi_sparse_attn_workspace_size(int64_t B, int64_t Hkv, int64_t T, int64_t head_dim) {
   if (B <= 0 || Hkv <= 0 || T <= 0 || head_dim <= 0) return FSI_WORKSPACE_COUNTER_BYTES;
   const int64_t n32 = (T + SA_CHUNK - 1) / SA_CHUNK;
+  // V^T copy (bf16 or fp16), the per-chunk maxima and the per-head exponents
   return FSI_WORKSPACE_COUNTER_BYTES +
-         fsi_host::align_up(sizeof(bf16_t) * static_cast<size_t>(B * Hkv * n32 * SA_CHUNK * head_dim), 256);
+         fsi_host::align_up(sizeof(bf16_t) * static_cast<size_t>(B * Hkv * n32 * SA_CHUNK * head_dim), 256) +
+         fsi_host::align_up(sizeof(uint32_t) * static_cast<size_t>(B * Hkv * n32), 256) +
+         fsi_host::align_up(sizeof(int32_t) * static_cast<size_t>(B * Hkv), 256);
 }
 
 FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, const void* k, int64_t ks_b,
@@ -717,7 +837,12 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
                 workspace_bytes, need);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int n32 = static_cast<int>((T + SA_CHUNK - 1) / SA_CHUNK);
-  bf16_t* vt = reinterpret_cast<bf16_t*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES);
+  char* wsp = static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES;
+  bf16_t* vt = reinterpret_cast<bf16_t*>(wsp);
+  wsp += fsi_host::align_up(sizeof(bf16_t) * static_cast<size_t>(B * Hkv * n32 * SA_CHUNK * head_dim), 256);
+  uint32_t* cmax = reinterpret_cast<uint32_t*>(wsp);
+  wsp += fsi_host::align_up(sizeof(uint32_t) * static_cast<size_t>(B * Hkv * n32), 256);
+  int32_t* head_e = reinterpret_cast<int32_t*>(wsp);
   const int64_t vt_items = B * Hkv * static_cast<int64_t>(n32) * SA_CHUNK * (head_dim / 8);
   const unsigned g1 = static_cast<unsigned>(std::min<int64_t>((vt_items + 255) / 256, 1 << 20));
 
@@ -731,6 +856,7 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
   P.ks_h = ks_h;
   P.ks_t = ks_t;
   P.vt = vt;
+  P.head_e = head_e;
   P.B = static_cast<int>(B);
   P.Hq = static_cast<int>(Hq);
   P.Hkv = static_cast<int>(Hkv);
@@ -759,14 +885,26 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
   // 64 queries per wave when a query block holds whole 64-query tiles and its list fits one wave
   const bool wide = block % 64 == 0 && fsi_host::is_pow2(block) && capacity <= SAL_MAX_CAP && scale > 0.f;
   const dim3 grid_w(static_cast<unsigned>((T + 63) / 64), grid.y);
+  const unsigned g_vmax = static_cast<unsigned>((B * Hkv * static_cast<int64_t>(n32) + 3) / 4);
+  const dim3 g_vt16(static_cast<unsigned>((n32 + SA_VT_CHUNKS - 1) / SA_VT_CHUNKS), static_cast<unsigned>(B * Hkv));
   auto launch = [&](auto hd_tag) -> int {
     constexpr int HD = decltype(hd_tag)::value;
-    sa_vt_kernel<HD><<<g1, 256, 0, st>>>(static_cast<const bf16_t*>(v), vs_b, vs_h, vs_t, P.B, P.Hkv, P.T, n32, vt);
+    const bf16_t* vb = static_cast<const bf16_t*>(v);
+    if constexpr (HD >= 64) {
+      if (wide) {  // fp16 V^T scaled per head, then the 64-query kernel
+        sa_vmax_kernel<HD><<<g_vmax, 256, 0, st>>>(vb, vs_b, vs_h, vs_t, P.B, P.Hkv, P.T, n32, cmax);
+        FSI_HIP_LAUNCH_CHECK("sparse_attn v maxima");
+        sa_vt16_kernel<HD><<<g_vt16, 256, 0, st>>>(vb, vs_b, vs_h, vs_t, P.Hkv, P.T, n32, cmax, head_e,
+                                                   reinterpret_cast<uint16_t*>(vt));
+        FSI_HIP_LAUNCH_CHECK("sparse_attn v copy");
+        sparse_attn_lds_kernel<HD><<<grid_w, 64 * SAL_WAVES, 0, st>>>(P);
+        FSI_HIP_LAUNCH_CHECK("sparse_attn");
+        return FSI_OK;
+      }
+    }
+    sa_vt_kernel<HD><<<g1, 256, 0, st>>>(vb, vs_b, vs_h, vs_t, P.B, P.Hkv, P.T, n32, vt);
     FSI_HIP_LAUNCH_CHECK("sparse_attn v copy");
-    if (wide && HD >= 64)
-      sparse_attn_lds_kernel<(HD >= 64 ? HD : 64)><<<grid_w, 64 * SAL_WAVES, 0, st>>>(P);
-    else
-      sparse_attn_kernel<HD><<<grid, 64 * SA_WAVES, 0, st>>>(P);
+    sparse_attn_kernel<HD><<<grid, 64 * SA_WAVES, 0, st>>>(P);
     FSI_HIP_LAUNCH_CHECK("sparse_attn");
     return FSI_OK;
   };

@@ -119,6 +119,37 @@ def test_strided_views_in_place(fsi, dev):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_value_range_per_head(fsi, dev, hd):
+    """The 64-query kernel takes V as fp16 scaled by a power of two per (sequence,
+    KV head): heads whose values sit near the ends of the bf16 range, a head with
+    one outlier 2^20 above the rest and an all-zero head all stay within the bf16
+    bar, head by head, against fp64 attention."""
+    B, Hq, Hkv, T, blk, W, cap = 2, 8, 4, 448, 64, 96, 3
+    print(f"[case] sparse_attention value range hd={hd}", flush=True)
+    q, k, v, g = _qkv(B, Hq, Hkv, T, hd, seed=31 + hd)
+    v = v.float()
+    v[:, 0] *= 1e30
+    v[:, 1] *= 1e-30
+    v[0, 2, 77, 5] = 2.0 ** 20
+    v[1, 3] = 0.0
+    v = v.bfloat16()
+    Qb = -(-T // blk)
+    idx = torch.randint(0, Qb, (B, Qb, cap), generator=g, dtype=torch.int32)
+    cnt = torch.randint(0, cap + 1, (B, Qb), generator=g, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(hd)
+    out = fsi.sparse_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), cnt.to(dev), block=blk, mode=0,
+                               window=W, scale=scale).cpu().float()
+    ref = A.weighted_attention_f64(q, k, v, A.sparse_mask(B, T, W, blk, idx, cnt), scale).float()
+    assert torch.equal(out[1, 6:8], torch.zeros_like(out[1, 6:8]))  # KV head 3 of sequence 1 is zero
+    for b in range(B):
+        for h in range(Hq):
+            if b == 1 and h >= 6:
+                continue
+            err = Pt.rel_l2(out[b, h], ref[b, h])
+            assert err <= TOL, (b, h, err)
+
+
 def test_invalid_block_reported(fsi, dev, monkeypatch):
     q, k, v, _ = _qkv(1, 2, 1, 128, 64, seed=5)
     idx = torch.tensor([[[0], [5]]], dtype=torch.int32, device=dev)  # 2 blocks exist

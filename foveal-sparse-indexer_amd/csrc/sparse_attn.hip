@@ -407,7 +407,7 @@ __global__ __launch_bounds__(64 * SA_WAVES) void sparse_attn_kernel(SAParams P) 
 // into a ring of LDS stages with direct-to-LDS loads, SAL_AHEAD chunks ahead,
 // and read from there by all 8 waves: a chunk serves 4 heads x 64 queries.  The
 // 16-byte pieces of each LDS row are XOR-swizzled so the 16 rows of a fragment
-// read fall on 16 different bank groups.  Q^T operands are parked in LDS.  The
+// read fall on 16 different bank groups.  Q^T operands stay in registers.  The
 // block's remote pages are checked, de-duplicated and compacted once; chunks
 // are described by wave-uniform scalar code.  Per chunk the S^T tiles of all
 // query tiles are formed first, then their softmax, then the P V products, so
@@ -469,17 +469,13 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   constexpr int LPW = LOADS / SAL_WAVES;        // per wave
   static_assert(LOADS % SAL_WAVES == 0, "chunk loads must split over the waves");
   constexpr int KPR = KROW / 16;                // 16-byte pieces per key row
-  // One LDS array holds the chunk ring, the Q^T operand tiles of each wave
-  // ((query tile, k-step) KiB in lane order) and the block list.  Separate
-  // __shared__ arrays would get alias scopes, and the compiler would then make
-  // every ring read wait for all direct loads in flight (vmcnt(0)), including the
-  // chunks issued ahead; with one array the explicit waits below order the ring.
-  constexpr int QBYTES = SAL_QT * KS * 1024;
-  __shared__ __attribute__((aligned(1024))) char smem[SAL_STAGES * STAGE + SAL_WAVES * QBYTES +
-                                                      SAL_MAX_CAP * 4];
+  // One LDS array holds the chunk ring and the block list.  Separate __shared__
+  // arrays would get alias scopes, and the compiler would then make every ring
+  // read wait for all direct loads in flight (vmcnt(0)), including the chunks
+  // issued ahead; with one array the explicit waits below order the ring.
+  __shared__ __attribute__((aligned(1024))) char smem[SAL_STAGES * STAGE + SAL_MAX_CAP * 4];
   char (*ring)[STAGE] = reinterpret_cast<char (*)[STAGE]>(smem);
-  char (*qlds)[QBYTES] = reinterpret_cast<char (*)[QBYTES]>(smem + SAL_STAGES * STAGE);
-  int* wl = reinterpret_cast<int*>(smem + SAL_STAGES * STAGE + SAL_WAVES * QBYTES);
+  int* wl = reinterpret_cast<int*>(smem + SAL_STAGES * STAGE);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -593,16 +589,16 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
     }
   };
 
-  // Q^T operands (lane (r, grp) holds Q[query 16 qt + r][32 ks + 8 grp .. +8]) parked in LDS
+  // Q^T operands in registers for the whole kernel: lane (r, grp) holds
+  // Q[query 16 qt + r][32 ks + 8 grp .. +8]
+  u32x4_t qreg[SAL_QT][KS];
 #pragma unroll
   for (int qt = 0; qt < SAL_QT; ++qt) {
     const int myq = q0 + 16 * qt + r;
     const int qq = myq < P.T ? myq : P.T - 1;
     const bf16_t* qp = P.q + b * P.qs_b + h * P.qs_h + static_cast<int64_t>(qq) * P.qs_t + 8 * grp;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      *reinterpret_cast<u32x4_t*>(&qlds[wave][(qt * KS + ks) * 1024 + lane * 16]) =
-          *reinterpret_cast<const u32x4_t*>(qp + 32 * ks);
+    for (int ks = 0; ks < KS; ++ks) qreg[qt][ks] = *reinterpret_cast<const u32x4_t*>(qp + 32 * ks);
   }
   f32x4_t acc[SAL_QT][DT];
   float m_run[SAL_QT], l_run[SAL_QT];
@@ -669,9 +665,9 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int qt = 0; qt < SAL_QT; ++qt) {
-        const u32x4_t qop = *reinterpret_cast<const u32x4_t*>(&qlds[wave][(qt * KS + ks) * 1024 + lane * 16]);
 #pragma unroll
-        for (int tile = 0; tile < 2; ++tile) st[qt][tile] = mfma16x16x32(kf[tile * KS + ks], qop, st[qt][tile]);
+        for (int tile = 0; tile < 2; ++tile)
+          st[qt][tile] = mfma16x16x32(kf[tile * KS + ks], qreg[qt][ks], st[qt][tile]);
       }
     // phase 2: online softmax of the 4 query tiles.  Chunks whose keys every
     // query of the wave sees (inside all windows, or a page wholly before them)

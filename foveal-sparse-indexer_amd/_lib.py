@@ -287,19 +287,29 @@ def ptr(t: torch.Tensor | None) -> int | None:
 # ---------------------------------------------------------------------------
 # Workspaces: one zero-initialised byte buffer per (device, stream).  Kernels
 # leave their arrival counters at zero, so a buffer is zeroed only when it is
-# (re)allocated.  Calls on one stream are ordered, so they can share it.
+# (re)allocated.  Calls on one stream are ordered, so they can share it.  A HIP
+# graph captured on a stream replays its launches on the buffer that stream had
+# at capture time, so once a capture has used a stream's buffer, growing it keeps
+# the old one alive (in _ws_kept) for as long as the process runs.
 # ---------------------------------------------------------------------------
 _ws: dict[tuple[int, int], torch.Tensor] = {}
+_ws_captured: set[tuple[int, int]] = set()
+_ws_kept: list[torch.Tensor] = []
 _err: dict[int, torch.Tensor] = {}
 
 
 def workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor:
     key = (device.index, stream)
+    capturing = torch.cuda.is_current_stream_capturing()
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None and (capturing or key in _ws_captured):
+            _ws_kept.append(buf)  # a captured graph may still launch kernels on it
         size = max(int(nbytes * 1.25) + 4096, 1 << 20)
         buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _ws[key] = buf
+    if capturing:
+        _ws_captured.add(key)
     return buf
 
 

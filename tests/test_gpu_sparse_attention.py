@@ -197,3 +197,46 @@ def test_prefill_forward_module(fsi, dev):
     assert aux["additive_out"] is not None and out.shape == (B, T, D)
     ref_loss = IX.distillation_loss(scores, teacher, causal=True, temperature=mc.indexer.distill_temperature)
     assert math.isclose(float(aux["distill_loss"]), float(ref_loss), rel_tol=1e-2, abs_tol=1e-5)
+
+
+def test_graph_replays_after_workspace_growth(fsi, dev):
+    """The fp16 V^T path (three launches) captured in a graph on a side stream and
+    replayed with eager work between replays: every replay equals the eager
+    result, also after a larger eager call on the same stream has grown that
+    stream's workspace (the captured buffer stays alive and untouched by others)."""
+    B, Hq, Hkv, T, hd, blk, W, cap = 1, 8, 2, 512, 128, 64, 128, 3
+    q, k, v, g = _qkv(B, Hq, Hkv, T, hd, seed=77)
+    Qb = T // blk
+    idx = torch.randint(0, Qb, (B, Qb, cap), generator=g, dtype=torch.int32).to(dev)
+    cnt = torch.randint(0, cap + 1, (B, Qb), generator=g, dtype=torch.int32).to(dev)
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    qb, kb, vb = (torch.randn(1, 8, 8192, hd, generator=g).bfloat16().to(dev) for _ in range(3))
+    big_idx = torch.zeros(1, 8192 // blk, cap, dtype=torch.int32, device=dev)
+    big_cnt = torch.zeros(1, 8192 // blk, dtype=torch.int32, device=dev)
+
+    def call():
+        return fsi.sparse_attention(q, k, v, idx, cnt, block=blk, mode=0, window=W, scale=0.09)
+
+    with torch.no_grad():
+        eager = call()
+        st = torch.cuda.Stream(dev)
+        st.wait_stream(torch.cuda.current_stream(dev))
+        outs = {}
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(st):
+            call()  # warm-up on the capture stream: its workspace exists before the capture
+            torch.cuda.synchronize(dev)
+            with torch.cuda.graph(graph, stream=st):
+                outs["o"] = call()
+            # a larger call on the same stream grows its workspace
+            fsi.sparse_attention(qb, kb[:, :2], vb[:, :2], big_idx, big_cnt, block=blk, mode=0, window=W, scale=0.09)
+        torch.cuda.synchronize(dev)
+        # blocks of the sizes a freed workspace of this call would offer for reuse
+        fill = [torch.full((n // 4,), 7, dtype=torch.int32, device=dev)
+                for n in (1 << 20, 3 << 19, 1 << 21) for _ in range(8)]
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize(dev)
+            assert torch.equal(outs["o"], eager)
+            torch.randn(1024, 1024, device=dev).sum().item()
+        assert all(bool((f == 7).all()) for f in fill)

@@ -23,9 +23,10 @@
 // chunk's tokens in the MFMA k order of P^T, written by a first kernel.  The
 // 64-query kernel (sparse_attn_lds_kernel) takes that copy in fp16, scaled per
 // (sequence, KV head) by a power of two that puts the largest finite |v| in
-// [2^14, 2^15), and P in fp16 (P <= 2^8 under its lazy running max): one
-// v_mfma_f32_16x16x32_f16 per P V tile with 11-bit P, where bf16 needs the hi +
-// lo pair to stay inside the bf16 output tolerance.
+// [2^14, 2^15), and P in fp16 (P <= 2^8 under its lazy running max, rounded
+// toward zero, the softmax denominators summed from the same fp16 values): one
+// v_mfma_f32_16x16x32_f16 per P V tile, where bf16 P needs the hi + lo pair to
+// stay inside the bf16 output tolerance.
 #include <algorithm>
 #include <type_traits>
 
@@ -414,21 +415,15 @@ __global__ __launch_bounds__(64 * SA_WAVES) void sparse_attn_kernel(SAParams P) 
 // consecutive MFMAs are independent.  The softmax skips the per-key mask for
 // chunks every query sees, moves its running max only by jumps above 2^8
 // (rescaling the accumulators rarely), and packs P in fp16 for one f16 MFMA
-// per P V tile against the fp16 V^T copy (sa_vt16_kernel).  Query blocks run
-// from the last (most keys) to the first.
+// per P V tile against the fp16 V^T copy (sa_vt16_kernel); the softmax
+// denominators are one more MFMA per query tile.  Query blocks run from the last
+// (most keys) to the first.
 // ---------------------------------------------------------------------------
 // Two fp32 values to a packed bf16 pair (round to nearest even) with gfx950's
 // v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
   typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
   const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// Two fp32 values to a packed fp16 pair (round to nearest even).
-__device__ __forceinline__ uint32_t cvt_pk_f16(float a, float b) {
-  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-  const f16x2_t v = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
   return __builtin_bit_cast(uint32_t, v);
 }
 
@@ -601,11 +596,16 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
     for (int ks = 0; ks < KS; ++ks) qreg[qt][ks] = *reinterpret_cast<const u32x4_t*>(qp + 32 * ks);
   }
   f32x4_t acc[SAL_QT][DT];
-  float m_run[SAL_QT], l_run[SAL_QT];
+  // Softmax denominators come out of one more MFMA per query tile, against an
+  // all-ones fp16 A operand: every row of lsum[qt] is the sum of the same fp16 P
+  // the P V product uses, so the rounding of P (toward zero) leaves no bias.
+  float m_run[SAL_QT];
+  f32x4_t lsum[SAL_QT];
+  const u32x4_t ones = u32x4_t{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
 #pragma unroll
   for (int qt = 0; qt < SAL_QT; ++qt) {
     m_run[qt] = -INFINITY;
-    l_run[qt] = 0.f;
+    lsum[qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < DT; ++i) acc[qt][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
@@ -710,18 +710,14 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
       const float m_new = bump ? m_cand : m_run[qt];
       alpha[qt] = bump ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;  // exp2(-inf) = 0 on the first bump
       const float m_use = m_new == -INFINITY ? 0.f : m_new;  // no valid key yet: every p is exp2(-inf) = 0
-      float psum = 0.f;
       uint32_t pk[4];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        // P in fp16 (round to nearest even; P <= 2^8)
+        // P in fp16, one v_cvt_pkrtz_f16_f32 per pair (P <= 2^8)
         const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w], P.scale_log2, -m_use));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w + 1], P.scale_log2, -m_use));
-        psum += p0 + p1;
-        pk[w] = cvt_pk_f16(p0, p1);
+        pk[w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0, p1));
       }
-      psum = sum_rows4(psum);
-      l_run[qt] = l_run[qt] * alpha[qt] + psum;
       m_run[qt] = m_new;
       pb[qt] = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
     }
@@ -734,12 +730,16 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[qt][dt][j] *= alpha[qt];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lsum[qt][j] *= alpha[qt];
       }
     }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int qt = 0; qt < SAL_QT; ++qt) acc[qt][dt] = mfma16x16x32_f16(vf[dt], pb[qt], acc[qt][dt]);
+#pragma unroll
+    for (int qt = 0; qt < SAL_QT; ++qt) lsum[qt] = mfma16x16x32_f16(ones, pb[qt], lsum[qt]);
   }
 
   if (!head_live) return;
@@ -747,7 +747,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   for (int qt = 0; qt < SAL_QT; ++qt) {
     const int myq = q0 + 16 * qt + r;
     if (myq < P.T) {
-      const float inv = l_run[qt] > 0.f ? 1.f / l_run[qt] : 0.f;
+      const float inv = lsum[qt][0] > 0.f ? 1.f / lsum[qt][0] : 0.f;
       bf16_t* o = P.out + b * P.os_b + h * P.os_h + static_cast<int64_t>(myq) * P.os_t + 4 * grp;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {

@@ -599,12 +599,13 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   // Softmax denominators come out of one more MFMA per query tile, against an
   // all-ones fp16 A operand: every row of lsum[qt] is the sum of the same fp16 P
   // the P V product uses, so the rounding of P (toward zero) leaves no bias.
-  float m_run[SAL_QT];
+  float m_run[SAL_QT], m_thr[SAL_QT];  // m_thr: raw score whose log2-scaled value is m_run + 8
   f32x4_t lsum[SAL_QT];
   const u32x4_t ones = u32x4_t{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
 #pragma unroll
   for (int qt = 0; qt < SAL_QT; ++qt) {
     m_run[qt] = -INFINITY;
+    m_thr[qt] = -INFINITY;
     lsum[qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < DT; ++i) acc[qt][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -701,14 +702,27 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
             sv[tile * 4 + j] = ok ? st[qt][tile][j] : -INFINITY;
           }
       }
-      float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-      mx = max_rows4(mx);
       // The running max (log2 units) moves only when a score exceeds it by more
       // than 8: P then stays below 2^8 and the accumulators are rescaled rarely.
-      const float m_cand = mx * P.scale_log2;
-      const bool bump = m_cand > m_run[qt] + 8.f;
-      const float m_new = bump ? m_cand : m_run[qt];
-      alpha[qt] = bump ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;  // exp2(-inf) = 0 on the first bump
+      // Most chunks only need to know that no score of the wave passes that
+      // threshold (one compare per score, the lane masks ORed in scalar
+      // registers); the row maxima are formed only when one does.
+      uint64_t over = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) over |= __ballot(sv[e] > m_thr[qt]);
+      float m_new = m_run[qt];
+      alpha[qt] = 1.f;
+      if (over != 0) {  // uniform
+        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                         fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        mx = max_rows4(mx);
+        const float m_cand = mx * P.scale_log2;
+        const bool bump = m_cand > m_run[qt] + 8.f;
+        m_new = bump ? m_cand : m_run[qt];
+        alpha[qt] = bump ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;  // exp2(-inf) = 0 on the first bump
+        // scores above this move the max; scale_log2 > 0 on this kernel's path
+        m_thr[qt] = (m_new + 8.f) / P.scale_log2;
+      }
       const float m_use = m_new == -INFINITY ? 0.f : m_new;  // no valid key yet: every p is exp2(-inf) = 0
       uint32_t pk[4];
 #pragma unroll

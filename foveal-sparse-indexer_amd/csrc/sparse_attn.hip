@@ -842,6 +842,8 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
   FSI_CHECK_ARG(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(v) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0,
                 FSI_ERR_ALIGN, "sparse_attn: q, k, v 16-byte and out 8-byte aligned");
+  FSI_CHECK_ARG(B * Hkv * ((T + SA_CHUNK - 1) / SA_CHUNK) <= (int64_t(1) << 32), FSI_ERR_SHAPE,
+                "sparse_attn: B x Hkv x T / 32 = %lld chunks beyond the grid", (long long)(B * Hkv * ((T + 31) / 32)));
   const size_t need = fsi_sparse_attn_workspace_size(B, Hkv, T, head_dim);
   FSI_CHECK_ARG(workspace && workspace_bytes >= need, FSI_ERR_WORKSPACE, "sparse_attn: workspace %zu < %zu",
                 workspace_bytes, need);

@@ -121,13 +121,17 @@ __device__ __forceinline__ void top_threshold(const uint32_t (&key)[PL], int R, 
   uint32_t mx = 0;
 #pragma unroll
   for (int i = 0; i < PL; ++i) mx = key[i] > mx ? key[i] : mx;
+  uint32_t mn = mx;  // smallest lane maximum: every lane holds a key >= it, so >= 64 keys do
   for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t o = __shfl_xor(mx, off, 64);
+    const uint32_t o = __shfl_xor(mx, off, 64), p = __shfl_xor(mn, off, 64);
     mx = o > mx ? o : mx;
+    mn = p < mn ? p : mn;
   }
   mx = __builtin_amdgcn_readfirstlane(mx);  // uniform: the bisection runs on scalars
-  // Invariant: count_ge(lo) >= R > count_ge(hi) (or lo = 1 with fewer keys).
-  uint32_t lo = 1, hi = mx + 1;
+  mn = __builtin_amdgcn_readfirstlane(mn);
+  // Invariant: count_ge(lo) >= R > count_ge(hi) (or lo = 1 with fewer keys).  For
+  // R <= 64 the search starts at the smallest lane maximum.
+  uint32_t lo = R <= 64 && mn > 0 ? mn : 1, hi = mx + 1;
   clo = count_ge<PL>(key, lo);
   while (clo != R && hi - lo > 1) {
     const uint32_t mid = lo + (hi - lo) / 2;

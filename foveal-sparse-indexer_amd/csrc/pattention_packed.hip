@@ -144,8 +144,11 @@ struct PkArgs {
 constexpr int WS_CONS = PK_WAVES;
 constexpr int WS_PROD = 4;
 constexpr int WS_THREADS = 64 * (WS_CONS + WS_PROD);
+// Gate/up weight chunks each consumer keeps in flight.  At the 8B decode shape 4-6
+// measured 1.5 % faster per step than 10: a deeper weight ring only crowds the x
+// stream the producers need.
 #ifndef FSI_WS_GU_RING
-#define FSI_WS_GU_RING 10
+#define FSI_WS_GU_RING 5
 #endif
 #ifndef FSI_WS_DN_RING
 #define FSI_WS_DN_RING 16

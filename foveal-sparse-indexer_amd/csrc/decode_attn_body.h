@@ -343,9 +343,15 @@ __global__ __launch_bounds__(64 * MG_WAVES) void decode_attn_merge_kernel(const 
   for (int i = 0; i < DPL; ++i) dst[i] = f32_to_bf16(L > 0.f ? o[i] / L : 0.f);
 }
 
+// Partial waves a decode launch aims for: one round of resident waves on the chip
+// (256 CUs x 8 waves of these kernels).
+#ifndef FSI_DA_TARGET_WAVES
+#define FSI_DA_TARGET_WAVES 2048
+#endif
+
 int split_count(int64_t B, int64_t Hkv, int64_t max_chunks) {
-  // enough waves to cover the chip several times, at most 64 chunks per wave
-  int64_t S = (2048 + B * Hkv - 1) / (B * Hkv);
+  // enough waves to cover the chip, at most 64 chunks per wave
+  int64_t S = (FSI_DA_TARGET_WAVES + B * Hkv - 1) / (B * Hkv);
   const int64_t min_s = (max_chunks + MAX_CHUNKS_PER_WAVE - 1) / MAX_CHUNKS_PER_WAVE;
   if (S < min_s) S = min_s;
   if (S > max_chunks) S = max_chunks;
@@ -367,7 +373,7 @@ int64_t max_chunks_of(int64_t window, int64_t cap, int64_t max_pages) {
 
 // Partial slots per (sequence, KV head): S for the one-launch form, and
 // S_local + S_remote for the local / remote launches, each of which is sized on
-// its own to put about 2048 waves on the chip (at most MAX_CHUNKS_PER_WAVE
+// its own to put about FSI_DA_TARGET_WAVES waves on the chip (at most MAX_CHUNKS_PER_WAVE
 // chunks per wave, at least one chunk per wave).
 struct DecodeSplit {
   int S, S_local, S_remote;
@@ -375,7 +381,7 @@ struct DecodeSplit {
 };
 
 int part_waves(int64_t B, int64_t Hkv, int64_t chunks) {
-  int64_t s = (2048 + B * Hkv - 1) / (B * Hkv);
+  int64_t s = (FSI_DA_TARGET_WAVES + B * Hkv - 1) / (B * Hkv);
   s = std::max<int64_t>(s, (chunks + MAX_CHUNKS_PER_WAVE - 1) / MAX_CHUNKS_PER_WAVE);
   s = std::min<int64_t>(s, std::max<int64_t>(chunks, 1));
   return static_cast<int>(std::max<int64_t>(s, 1));

@@ -302,39 +302,64 @@ __device__ void select_row(float (&s)[PL], int N, int qb, int64_t row, const Sel
   const int k_min = sp.k_min_rows ? sp.k_min_rows[row] : sp.k_min;
   const int k_max = sp.k_max_rows ? sp.k_max_rows[row] : sp.k_max;
 
-  // masked_softmax over complete entries (core.py:36-43)
-  float mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const int j = i * 64 + lane;
-    if (j < N && mask_kind(j, qb, sp.causal, sp.local_window)) mx = fmaxf(mx, s[i]);
-  }
-  mx = wave_max(mx);
-  if (!isfinite(mx)) mx = 0.0f;
-  float z = 0.f;
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const int j = i * 64 + lane;
-    s[i] = j < N && mask_kind(j, qb, sp.causal, sp.local_window) ? expf(s[i] - mx) : 0.0f;
-    z += s[i];
-  }
-  z = fmaxf(wave_sum(z), 1e-20f);
+  // masked_softmax over complete entries (core.py:36-43).  A non-causal row with
+  // no local window over N >= 64 PL keys has every slot complete and remote: it
+  // takes passes without per-slot masks (kept live across the three passes, 64
+  // lane masks overflow the scalar registers).
   float lmass = 0.f;
   int avail = 0;
   uint32_t key[PL];
+  if (!sp.causal && sp.local_window == 0 && N >= 64 * PL) {  // uniform
+    float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const int j = i * 64 + lane;
-    const int kind = j < N ? mask_kind(j, qb, sp.causal, sp.local_window) : 0;
-    float p = s[i] / z;
-    if (RB) p = round_bf16(p);
-    if (kind == 1) lmass += p;
-    key[i] = kind == 2 ? __float_as_uint(p) + 1u : 0u;
-    avail += kind == 2;
+    for (int i = 0; i < PL; ++i) mx = fmaxf(mx, s[i]);
+    mx = wave_max(mx);
+    if (!isfinite(mx)) mx = 0.0f;
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      s[i] = expf(s[i] - mx);
+      z += s[i];
+    }
+    z = fmaxf(wave_sum(z), 1e-20f);
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      float p = s[i] / z;
+      if (RB) p = round_bf16(p);
+      key[i] = __float_as_uint(p) + 1u;
+    }
+    avail = 64 * PL;
+  } else {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int j = i * 64 + lane;
+      if (j < N && mask_kind(j, qb, sp.causal, sp.local_window)) mx = fmaxf(mx, s[i]);
+    }
+    mx = wave_max(mx);
+    if (!isfinite(mx)) mx = 0.0f;
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int j = i * 64 + lane;
+      s[i] = j < N && mask_kind(j, qb, sp.causal, sp.local_window) ? expf(s[i] - mx) : 0.0f;
+      z += s[i];
+    }
+    z = fmaxf(wave_sum(z), 1e-20f);
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int j = i * 64 + lane;
+      const int kind = j < N ? mask_kind(j, qb, sp.causal, sp.local_window) : 0;
+      float p = s[i] / z;
+      if (RB) p = round_bf16(p);
+      if (kind == 1) lmass += p;
+      key[i] = kind == 2 ? __float_as_uint(p) + 1u : 0u;
+      avail += kind == 2;
+    }
+    lmass = wave_sum(lmass);
+    if (RB) lmass = round_bf16(lmass);
+    avail = wave_sum_i(avail);
   }
-  lmass = wave_sum(lmass);
-  if (RB) lmass = round_bf16(lmass);
-  avail = wave_sum_i(avail);
 
   int R = k_max > sp.capacity ? k_max : sp.capacity;
   R = R < avail ? R : avail;

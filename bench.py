@@ -51,16 +51,16 @@ DECODE_BATCH, PREFILL_TOKENS = 64, 4096
 
 # HBM bytes of one decode step measured with rocprofv3 FETCH_SIZE and WRITE_SIZE
 # passes, scaled by a 512 MiB copy (profiles/pattention_decode_prefill_8b.md):
-#   packed path  : (34908.0 + 18510.7) KiB x 1.99979 read + (512 + 512) KiB written
+#   packed path  : (34908.2 + 18503.2) KiB x 1.99983 read + (512 + 512) KiB written
 #   --no-pack    : (34872.4 + 4129.5 + 18477.7 + 4109.0) KiB x 1.9997 read + 17408 KiB written
-DECODE_TRAFFIC_BYTES = int(107850.0 * 1024)
+DECODE_TRAFFIC_BYTES = int(107837.0 * 1024)
 DECODE_TRAFFIC_BYTES_UNPACKED = int(140566.8 * 1024)
-# Same method for the other workloads (KiB read after the x 1.99979 scale + KiB written;
+# Same method for the other workloads (KiB read after the x 1.99983 scale + KiB written;
 # profiles/pattention_decode_prefill_8b.md, decode_attention_c4.md, indexer_routing_c2.md,
 # block_sparse_gemm_c5.md).
-PREFILL_TRAFFIC_BYTES = int((393529 + 33237 + 196727 + 34084) * 1024)
-C4_TRAFFIC_BYTES = int((161110 + 291002 + 8273 + 3814 + 4352 + 256) * 1024)
-C2_TRAFFIC_BYTES = int((2296 + 2112) * 1024)
+PREFILL_TRAFFIC_BYTES = int((393537 + 33270 + 196732 + 34374) * 1024)
+C4_TRAFFIC_BYTES = int((161152 + 291023 + 8273 + 3814 + 4352 + 256) * 1024)
+C2_TRAFFIC_BYTES = int((2057 + 2112) * 1024)
 C5_TRAFFIC_BYTES = {0.10: (578 + 64) << 20, 0.25: (1366 + 64) << 20, 0.50: (2583 + 64) << 20}
 # C2: wave-level VALU instructions of one score_route_kernel launch (rocprofv3 SQ_INSTS_VALU)
 C2_VALU_INSTS = 70_114_379

@@ -8,7 +8,7 @@
 //   * prologue: the workgroup reads its group's mask column(s) for its n
 //     block(s) and compacts the active k blocks, in ascending order, into an
 //     LDS list (ballot + prefix over 64-block chunks) -- no list-building
-//     launches and no workspace;
+//     launches;
 //   * main loop: 32-wide K-steps over the active blocks only, operands going
 //     global -> LDS with global_load_lds_dwordx4 into a ring of STAGES stages
 //     (16 KiB each), so STAGES - 1 steps are in flight without staging
@@ -22,6 +22,15 @@
 //     other XCDs' copies are still in the last-level cache.  Bands of several m
 //     tiles (W shared in L2 as well) measured slower: tiles with different
 //     k-block lists drift apart and the shared W tiles are evicted between uses.
+//   * load balance: a tile's time grows with its number of active k blocks,
+//     and the hardware hands tiles to free workgroup slots in dispatch order,
+//     so a grid of several rounds ends with the slots that drew the heaviest
+//     late tiles.  Given a workspace, a pre-pass (tile_order_kernel, one
+//     workgroup per band) counts the active k blocks of the band's tiles and
+//     writes them heaviest first (a counting sort); each band's positions keep
+//     their place in the walk above, so the last tiles an XCD runs are the
+//     lightest of its last band.  A global heaviest-first order mixed all
+//     groups on every XCD and ran 1.6x slower: X tiles stop being shared.
 // When block_n < 128 a tile spans several n blocks whose masks differ; the list
 // then holds every k block at which any of them is active, with the per-n-block
 // bits beside it, and a B fragment (16 columns, inside one n block) of an
@@ -73,6 +82,7 @@ struct TileArgs {
   const uint8_t* mask;  // [groups][nkb * nnb], tile id k_b * nnb + n_b
   int groups, rows_per_group, nkb, nnb, block_k, block_n;
   int m_tiles, n_tiles;
+  const int32_t* order;  // tile ids heaviest first (tile_order_kernel), or null: dispatch order
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -119,6 +129,114 @@ __device__ __forceinline__ int xcd_contiguous(int b, int n) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + (b >> 3);
 }
 
+// Logical tile lid -> (m tile, n tile): bands of GROUP_M m tiles walked across N.
+__device__ __forceinline__ void tile_coords(const TileArgs& g, int lid, int& mt, int& nt) {
+  const int per_band = GROUP_M * g.n_tiles;
+  const int band = lid / per_band, within = lid - band * per_band;
+  const int mfirst = band * GROUP_M;
+  const int bh = g.m_tiles - mfirst < GROUP_M ? g.m_tiles - mfirst : GROUP_M;
+  mt = mfirst + within % bh;
+  nt = within / bh;
+}
+
+// Active k blocks in [kb0, kb0 + ORDER_KB_CHUNK) of tile (mt, nt): those at which
+// any of its n blocks is active (the tile's share of the list the GEMM prologue
+// builds).  The chunk's loads are independent and issued together.
+constexpr int ORDER_KB_CHUNK = 16;
+__device__ int tile_kcount_chunk(const TileArgs& g, int mt, int nt, int kb0) {
+  int grp = mt * TT / g.rows_per_group;
+  grp = grp < g.groups ? grp : g.groups - 1;
+  const int nsub = g.block_n < TT ? TT / g.block_n : 1;
+  const int nb0 = nt * TT / g.block_n;
+  const int cnt = (nb0 + nsub < g.nnb ? nb0 + nsub : g.nnb) - nb0;  // 1 .. TT / 16 (block_n >= 16)
+  const uint8_t* col = g.mask + static_cast<int64_t>(grp) * g.nkb * g.nnb + nb0;
+  int n = 0;
+#pragma unroll
+  for (int k = 0; k < ORDER_KB_CHUNK; ++k) {
+    const int kb = kb0 + k;
+    if (kb < g.nkb) {
+      const uint8_t* row = col + static_cast<int64_t>(kb) * g.nnb;
+      bool any = row[0] != 0;
+#pragma unroll
+      for (int j = 1; j < TT / 16; ++j)
+        if (j < cnt) any |= row[j] != 0;
+      n += any;
+    }
+  }
+  return n;
+}
+
+constexpr int ORDER_THREADS = 256;
+constexpr int64_t ORDER_MIN_TILES = 512;           // at most one round of workgroup slots: nothing to balance
+constexpr int64_t ORDER_MAX_MASK_READS = 1 << 22;  // mask bytes one pre-pass workgroup may read
+constexpr int ORDER_MAX_BAND = 4096;               // tiles of one band (counts held in LDS)
+constexpr int ORDER_OWN = (LIST_MAX + 1 + ORDER_THREADS - 1) / ORDER_THREADS;
+
+// Workgroup b sorts band b (GROUP_M m tiles x all n tiles, logical positions
+// [b GROUP_M n_tiles, ...)) by active k-block count, largest first: order[p] is
+// the logical tile run at position p.  Positions keep their band, so the
+// tiles an XCD runs at once still share their group's X tiles in its L2; only
+// the order inside a band changes.  Counting sort; ties in any order (every
+// tile's result is independent of the workgroup that computes it).
+__global__ __launch_bounds__(ORDER_THREADS) void tile_order_kernel(TileArgs g, int32_t* __restrict__ order) {
+  __shared__ int32_t start[LIST_MAX + 1];  // tiles per bin, then the next position of each bin
+  __shared__ int32_t kcs[ORDER_MAX_BAND];  // active k blocks per tile of the band
+  __shared__ int32_t wave_sum[ORDER_THREADS / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per_band = GROUP_M * g.n_tiles;
+  const int first = blockIdx.x * per_band;
+  const int mfirst = blockIdx.x * GROUP_M;
+  const int count = (g.m_tiles - mfirst < GROUP_M ? g.m_tiles - mfirst : GROUP_M) * g.n_tiles;
+  const int nbins = g.nkb + 1;  // bin p holds count nkb - p (descending)
+  for (int i = tid; i < nbins; i += ORDER_THREADS) start[i] = 0;
+  for (int i = tid; i < count; i += ORDER_THREADS) kcs[i] = 0;
+  __syncthreads();
+  // (tile, 16-k-block chunk) items; neighbouring threads take neighbouring tiles,
+  // i.e. neighbouring mask bytes of one row
+  const int chunks = (g.nkb + ORDER_KB_CHUNK - 1) / ORDER_KB_CHUNK;
+  for (int it = tid; it < count * chunks; it += ORDER_THREADS) {
+    const int i = it % count, c = it / count;
+    int mt, nt;
+    tile_coords(g, first + i, mt, nt);
+    const int n = tile_kcount_chunk(g, mt, nt, c * ORDER_KB_CHUNK);
+    if (n) atomicAdd(&kcs[i], n);
+  }
+  __syncthreads();
+  for (int i = tid; i < count; i += ORDER_THREADS) atomicAdd(&start[g.nkb - kcs[i]], 1);
+  __syncthreads();
+  // exclusive scan of the bins: thread t owns bins [t per, (t + 1) per)
+  const int per = (nbins + ORDER_THREADS - 1) / ORDER_THREADS;
+  int own[ORDER_OWN];
+  int sum = 0;
+#pragma unroll
+  for (int i = 0; i < ORDER_OWN; ++i) {
+    const int b = tid * per + i;
+    own[i] = i < per && b < nbins ? start[b] : 0;
+    sum += own[i];
+  }
+  int incl = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int v = __shfl_up(incl, d);
+    if (lane >= d) incl += v;
+  }
+  if (lane == 63) wave_sum[wave] = incl;
+  __syncthreads();
+  int base = first + incl - sum;
+  for (int w = 0; w < wave; ++w) base += wave_sum[w];
+#pragma unroll
+  for (int i = 0; i < ORDER_OWN; ++i) {
+    const int b = tid * per + i;
+    if (i < per && b < nbins) start[b] = base;
+    base += own[i];
+  }
+  __syncthreads();
+  for (int i = tid; i < count; i += ORDER_THREADS) {
+    const int pos = atomicAdd(&start[g.nkb - kcs[i]], 1);
+    if (pos < first + count) order[pos] = first + i;
+  }
+}
+
 template <bool MASKED>
 __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(TileArgs g) {
   __shared__ __attribute__((aligned(1024))) bf16_t lds[STAGES][2][TT * KS];  // [stage][A/B][row * 32 + k]
@@ -128,13 +246,11 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // ---- which tile: bands of GROUP_M m tiles walked across N --------------------
-  const int lid = xcd_contiguous(blockIdx.x, gridDim.x);
-  const int per_band = GROUP_M * g.n_tiles;
-  const int band = lid / per_band, within = lid - band * per_band;
-  const int mfirst = band * GROUP_M;
-  const int bh = g.m_tiles - mfirst < GROUP_M ? g.m_tiles - mfirst : GROUP_M;
-  const int mt = mfirst + within % bh, nt = within / bh;
+  // ---- which tile ---------------------------------------------------------------
+  const int pos = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int lid = g.order ? g.order[pos] : pos;
+  int mt, nt;
+  tile_coords(g, lid, mt, nt);
   const int m0 = mt * TT, n0 = nt * TT;
 
   // ---- active k blocks of this tile -> klist -----------------------------------
@@ -362,13 +478,13 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
 extern "C" {
 
 FSI_API size_t fsi_blockwise_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int64_t block_k) {
-  (void)M;
-  (void)N;
   (void)K;
   (void)block_k;
-  // Every tile builds its k-block list in LDS; the workspace argument is kept for
-  // the interface and needs no bytes beyond the counter area.
-  return FSI_WORKSPACE_COUNTER_BYTES;
+  // Every tile builds its k-block list in LDS; the workspace holds the tile order
+  // (one int32 per 128 x 128 output tile) after the counter area.
+  if (M <= 0 || N <= 0) return FSI_WORKSPACE_COUNTER_BYTES;
+  const int64_t tiles = ((M + TT - 1) / TT) * ((N + TT - 1) / TT);
+  return FSI_WORKSPACE_COUNTER_BYTES + static_cast<size_t>(tiles) * sizeof(int32_t);
 }
 
 FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int64_t ldw,
@@ -423,6 +539,18 @@ FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int6
   const int64_t tiles = static_cast<int64_t>(a.m_tiles) * a.n_tiles;
   FSI_CHECK_ARG(tiles <= 0x7fffffff, FSI_ERR_SHAPE, "blockwise_matmul: too many tiles");
   const unsigned grid = static_cast<unsigned>(tiles);
+  // Heaviest-first order inside each band when the grid takes several rounds of
+  // workgroup slots and a band's counting pass (nkb x its n blocks' mask bytes per
+  // tile) is small.
+  const int64_t nsub = block_n < TT ? TT / block_n : 1;
+  const int64_t bands = (a.m_tiles + GROUP_M - 1) / GROUP_M;
+  if (workspace != nullptr && workspace_bytes >= FSI_WORKSPACE_COUNTER_BYTES + tiles * sizeof(int32_t) &&
+      tiles > ORDER_MIN_TILES && int64_t{GROUP_M} * a.n_tiles <= ORDER_MAX_BAND &&
+      int64_t{GROUP_M} * a.n_tiles * nkb * nsub <= ORDER_MAX_MASK_READS) {
+    int32_t* order = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES);
+    tile_order_kernel<<<static_cast<unsigned>(bands), ORDER_THREADS, 0, st>>>(a, order);
+    a.order = order;
+  }
   if (block_n < TT) tile_list_gemm_kernel<true><<<grid, NTHREADS, 0, st>>>(a);
   else tile_list_gemm_kernel<false><<<grid, NTHREADS, 0, st>>>(a);
   const hipError_t e = hipGetLastError();

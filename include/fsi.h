@@ -525,8 +525,12 @@ FSI_API size_t fsi_blockwise_matmul_workspace_size(int64_t M, int64_t N, int64_t
  * 128 or one of 16, 32, 64, K / block_k <= 2048, rows_per_group a multiple of
  * 128 (or groups = 1) and 16-byte aligned x, w rows; other problems and fp32
  * run on a generic kernel.  Rows of a group whose tiles are all inactive get 0.
- * The workspace (fsi_blockwise_matmul_workspace_size bytes, or null) is not
- * written: every tile builds its k-block list on chip. */
+ * Every tile builds its k-block list on chip.  The workspace
+ * (fsi_blockwise_matmul_workspace_size bytes: one int32 per 128 x 128 output
+ * tile after the counter area) receives the tile order from a pre-pass when
+ * the grid spans several rounds of workgroups: inside each 128-row band of
+ * output tiles, heaviest k-block list first.  With a null or smaller workspace
+ * tiles run in dispatch order.  Results do not depend on the order. */
 FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int64_t ldw,
                                  const uint8_t* tile_mask, int64_t groups, int64_t rows_per_group, int64_t block_k,
                                  int64_t block_n, int64_t M, int64_t N, int64_t K, int dtype, void* out, int64_t ldo,

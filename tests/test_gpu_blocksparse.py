@@ -61,6 +61,9 @@ def test_block_sparse_linear_bad_block_reported(fsi, dev, monkeypatch):
     (384, 1024, 512, 128, 64, 0.0, 3),     # empty masks: every tile stores zeros
     (256, 512, 512, 64, 128, 1.0, 2),      # dense masks
     (96, 192, 96, 64, 48, 0.5, 1),         # n block dividing neither way: generic kernel
+    (4608, 512, 2048, 128, 128, 0.3, 36),  # 576 tiles: heaviest-first tile order from the pre-pass
+    (4096, 256, 2304, 32, 64, 0.25, 4),    # 576 tiles, 2 n blocks per tile, 8 m tiles per group
+    (4200, 256, 2176, 64, 128, 0.5, 3),    # 561 tiles, ragged M, with the tile order
 ])
 def test_blockwise_matmul(fsi, dev, M, K, N, bk, bn, density, groups):
     print(f"[case] blockwise_matmul M={M} K={K} N={N} tile={bk}x{bn} d={density} groups={groups}", flush=True)
@@ -146,6 +149,40 @@ def test_blockwise_matmul_module(fsi, dev):
         ref = ref.view(2, 3, 512) + md.out_proj(ctx).double().cpu()
     assert aux["active_tiles"] == int(mask.sum())
     assert _rel(out, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("bn,density", [(128, 0.25), (64, 0.4), (128, 0.0)])
+def test_blockwise_matmul_tile_order_matches_dispatch_order(fsi, dev, bn, density):
+    """Above 512 output tiles the workspace receives a tile order, heaviest first
+    inside each 128-row band; without a workspace the tiles run in dispatch order.
+    Both give the same bits (each tile's result does not depend on the workgroup
+    that computes it) and match the fp64 reference.  Group masks range from empty
+    to dense."""
+    print(f"[case] tile order bn={bn} density={density}", flush=True)
+    from foveal_sparse_indexer_amd import _lib
+    g = torch.Generator().manual_seed(bn + int(density * 100))
+    M, K, N, bk, groups = 5120, 512, 2048, 64, 20
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    T = (K // bk) * (N // bn)
+    dens = torch.linspace(0.0, 1.0, groups).unsqueeze(1) if density > 0 else torch.zeros(groups, 1)
+    masks = torch.rand(groups, T, generator=g) < dens
+    rpg = M // groups
+    xd, wd, md = x.to(dev), w.to(dev), masks.to(dev)
+    ordered = fsi.blockwise_matmul(xd, wd, md, bk, bn, rows_per_group=rpg)
+    L = _lib.lib()
+    m8 = md.to(torch.uint8).contiguous()
+    plain = torch.empty_like(ordered)
+    st = L.fsi_blockwise_matmul(xd.data_ptr(), K, wd.data_ptr(), K, m8.data_ptr(), groups, rpg, bk, bn, M, N, K,
+                                _lib.dtype_code(xd.dtype, "blockwise_matmul"), plain.data_ptr(), N, None, 0,
+                                _lib.stream_handle(dev))
+    _lib.check(st, "blockwise_matmul")
+    torch.cuda.synchronize(dev)
+    assert torch.equal(ordered, plain)
+    if masks.any():
+        assert _rel(ordered, BS.blockwise_matmul_f64(x, w, masks, bk, bn, rpg)) <= TOL
+    else:
+        assert torch.equal(ordered.cpu(), torch.zeros(M, N, dtype=torch.bfloat16))
 
 
 def test_blockwise_matmul_graph_replays(fsi, dev):

@@ -61,7 +61,7 @@ DECODE_TRAFFIC_BYTES_UNPACKED = int(140566.8 * 1024)
 PREFILL_TRAFFIC_BYTES = int((393537 + 33270 + 196732 + 34374) * 1024)
 C4_TRAFFIC_BYTES = int((161152 + 291023 + 8273 + 3814 + 4352 + 256) * 1024)
 C2_TRAFFIC_BYTES = int((2057 + 2112) * 1024)
-C5_TRAFFIC_BYTES = {0.10: (578 + 64) << 20, 0.25: (1366 + 64) << 20, 0.50: (2583 + 64) << 20}
+C5_TRAFFIC_BYTES = {0.10: (515 + 64) << 20, 0.25: (1175 + 64) << 20, 0.50: (2249 + 64) << 20}
 # C2: wave-level VALU instructions of one score_route_kernel launch (rocprofv3 SQ_INSTS_VALU)
 C2_VALU_INSTS = 70_114_379
 VALU_PEAK_GIPS = 256 * 4 * 2.4 / 4  # G wave64 VALU instructions/s: 256 CUs x 4 SIMDs x 2.4 GHz / 4 cycles

@@ -150,19 +150,25 @@ __device__ int tile_kcount_chunk(const TileArgs& g, int mt, int nt, int kb0) {
   const int nb0 = nt * TT / g.block_n;
   const int cnt = (nb0 + nsub < g.nnb ? nb0 + nsub : g.nnb) - nb0;  // 1 .. TT / 16 (block_n >= 16)
   const uint8_t* col = g.mask + static_cast<int64_t>(grp) * g.nkb * g.nnb + nb0;
-  int n = 0;
+  // branch-free: rows past nkb re-read the last row and are not counted, so the
+  // chunk's loads issue together
+  uint32_t any[ORDER_KB_CHUNK];
 #pragma unroll
   for (int k = 0; k < ORDER_KB_CHUNK; ++k) {
-    const int kb = kb0 + k;
-    if (kb < g.nkb) {
-      const uint8_t* row = col + static_cast<int64_t>(kb) * g.nnb;
-      bool any = row[0] != 0;
+    const int kb = kb0 + k < g.nkb ? kb0 + k : g.nkb - 1;
+    any[k] = col[static_cast<int64_t>(kb) * g.nnb];
+  }
+  if (cnt > 1) {
 #pragma unroll
-      for (int j = 1; j < TT / 16; ++j)
-        if (j < cnt) any |= row[j] != 0;
-      n += any;
+    for (int k = 0; k < ORDER_KB_CHUNK; ++k) {
+      const int kb = kb0 + k < g.nkb ? kb0 + k : g.nkb - 1;
+      const uint8_t* row = col + static_cast<int64_t>(kb) * g.nnb;
+      for (int j = 1; j < cnt; ++j) any[k] |= row[j];
     }
   }
+  int n = 0;
+#pragma unroll
+  for (int k = 0; k < ORDER_KB_CHUNK; ++k) n += (kb0 + k < g.nkb) & (any[k] != 0u);
   return n;
 }
 

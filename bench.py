@@ -22,7 +22,7 @@ fused indexer attention (skip them with --no-workloads).  Each can also run alon
   --workload prefill_attn block-sparse prefill attention, 16384 tokens, Llama-3-8B attention heads
   --workload block_sparse C5: 2-D tile-sparse matmul, 4096 x 8192 by 8192 x 8192, 128 x 128 tiles
   --workload teacher_targets dense block-energy distillation targets, Llama-3-8B MLP, 4096 tokens
-  --workload hbm_stream   the HBM read ceiling (fsi_stream_read probe; torch copy and sum beside it)
+  --workload hbm_stream   the HBM read ceiling (torch sum and copy over 4 GiB)
   --workload sram_attn    fused 16-D indexer + greedy selection + block attention, the reference's 3 SRAM configs
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-prefill] [--workload W]
@@ -325,22 +325,36 @@ def prefill_attn_flops(lists, counts, T: int, W: int, page: int, hq: int, hd: in
     return int(keys.sum()) * hq * hd * 4
 
 
-def bench_prefill_attn(fsi, args, dev):
-    B, HQ, HKV, HD, T, PAGE, WB, KMAX, TOP_P = 1, 32, 8, 128, 16384, 64, 16, 32, 0.9
-    W = WB * PAGE
+PREFILL_ATTN = dict(B=1, HQ=32, HKV=8, HD=128, T=16384, PAGE=64, WB=16, KMAX=32, TOP_P=0.9)
+
+
+def prefill_attn_inputs(fsi, dev):
+    """The prefill-attention workload: seeded N(0,1) q (B, 32, 16384, 128) and
+    k, v (B, 8, 16384, 128) bf16, and the pages routed as
+    FovealSparseAttention.forward does: cosine/4 block scores of block-anchor
+    16-D queries against normalised 16-D page keys, causal top-p with the
+    16-page local window.  Returns (q, k, v, lists, counts)."""
+    c = PREFILL_ATTN
+    B, HQ, HKV, HD, T, PAGE = c["B"], c["HQ"], c["HKV"], c["HD"], c["T"], c["PAGE"]
     Qb = T // PAGE
     g = torch.Generator(device=dev).manual_seed(0)
     q = torch.randn(B, HQ, T, HD, device=dev, generator=g).bfloat16()
     k = torch.randn(B, HKV, T, HD, device=dev, generator=g).bfloat16()
     v = torch.randn(B, HKV, T, HD, device=dev, generator=g).bfloat16()
-    # pages routed as FovealSparseAttention.forward does: cosine/4 block scores of
-    # the block-anchor 16-D queries against normalised 16-D page keys, causal top-p
     qi = torch.nn.functional.normalize(torch.randn(B, Qb, 16, device=dev, generator=g), dim=-1)
     kp = torch.nn.functional.normalize(torch.randn(B, Qb, 16, device=dev, generator=g), dim=-1)
     scores = torch.bmm(qi, kp.transpose(1, 2).contiguous()) / 4.0
-    route = fsi.select_blocks(scores, causal=True, block_size=PAGE, local_window_blocks=WB, top_p=TOP_P,
-                              min_remote_blocks=0, max_remote_blocks=KMAX, remote_capacity=KMAX)
-    lists, counts = route.remote_indices, route.remote_counts
+    route = fsi.select_blocks(scores, causal=True, block_size=PAGE, local_window_blocks=c["WB"], top_p=c["TOP_P"],
+                              min_remote_blocks=0, max_remote_blocks=c["KMAX"], remote_capacity=c["KMAX"])
+    return q, k, v, route.remote_indices, route.remote_counts
+
+
+def bench_prefill_attn(fsi, args, dev):
+    c = PREFILL_ATTN
+    B, HQ, HKV, HD, T, PAGE, WB = c["B"], c["HQ"], c["HKV"], c["HD"], c["T"], c["PAGE"], c["WB"]
+    W = WB * PAGE
+    Qb = T // PAGE
+    q, k, v, lists, counts = prefill_attn_inputs(fsi, dev)
     out = torch.empty(B, T, HQ, HD, dtype=torch.bfloat16, device=dev)
     scale = 1.0 / HD ** 0.5
 
@@ -615,29 +629,12 @@ def bench_hbm_stream(fsi, args, dev):
     t_r, _ = time_graph(read_step, args.steps, args.warmup, dev)
     copy_gbs = 2 * n / (t_c / args.steps) / 1e9
     read_gbs = n / (t_r / args.steps) / 1e9
-    # the library's stream-read probe over launch shapes: the best is the read ceiling
-    from foveal_sparse_indexer_amd import _lib
-
-    L = _lib.lib()
-    sink = torch.empty(16384 * 256, dtype=torch.int32, device=dev)
-    probe = {}
-    for wgs in (1024, 2048, 4096, 8192, 16384):
-        for unroll in (4, 8, 16):
-            def probe_step(i, wgs=wgs, unroll=unroll):
-                _lib.check(L.fsi_stream_read(a.data_ptr(), n, wgs, unroll, sink.data_ptr(),
-                                             torch.cuda.current_stream(dev).cuda_stream), "stream_read")
-
-            t_p, _ = time_graph(probe_step, args.steps, args.warmup, dev)
-            probe[f"{wgs}x256/u{unroll}"] = round(n / (t_p / args.steps) / 1e9, 1)
-    best = max(probe, key=probe.get)
-    res = _result("HBM stream bandwidth GB/s (best stream-read probe shape)", probe[best], "GB/s", args.steps,
-                  args.warmup, round(n / probe[best] / 1e6, 6), "u8", "synthetic (4 GiB buffers)",
-                  {"workload": "fsi_stream_read over 4 GiB at several launch shapes; torch copy_ of 4 GiB (read + "
-                               "write); torch sum over 4 GiB of fp32 (read)",
-                   "probe_gbs": probe, "best_shape": best, "torch_copy_gbs": round(copy_gbs, 1),
-                   "torch_sum_gbs": round(read_gbs, 1)})
-    res["roofline"] = {"bound": "hbm", "achieved": probe[best], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(probe[best] / HBM_PEAK_GBS, 4), "traffic": None}
+    res = _result("HBM stream bandwidth GB/s (torch sum over 4 GiB)", round(read_gbs, 1), "GB/s", args.steps,
+                  args.warmup, round(t_r / args.steps * 1e3, 6), "u8", "synthetic (4 GiB buffers)",
+                  {"workload": "torch sum over 4 GiB of fp32 (read); torch copy_ of 4 GiB (read + write)",
+                   "torch_copy_gbs": round(copy_gbs, 1), "torch_sum_gbs": round(read_gbs, 1)})
+    res["roofline"] = {"bound": "hbm", "achieved": round(read_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(read_gbs / HBM_PEAK_GBS, 4), "traffic": None}
     return res
 
 

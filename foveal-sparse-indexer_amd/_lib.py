@@ -190,7 +190,6 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
     ),
-    "fsi_stream_read": (_c_int, [_c_ptr, _c_i64, _c_i64, _c_int, _c_ptr, _c_ptr]),
 }
 
 ROUTE_MAX_BLOCKS = 4096

@@ -125,7 +125,9 @@ def blockwise_matmul(x2d: Tensor, weight: Tensor, tile_mask: Tensor, block_k: in
                      rows_per_group: Optional[int] = None, out: Optional[Tensor] = None) -> Tensor:
     """out = x (weight o expand(tile_mask))^T.  tile_mask: bool (T,) or (groups, T)
     with tile id k_b * (N / block_n) + n_b (block_matmul.py:384-385); with
-    groups > 1, row group g covers rows [g rows_per_group, (g+1) rows_per_group)."""
+    groups > 1, row group g covers rows [g rows_per_group, (g+1) rows_per_group)
+    and the groups must cover every row (ValueError otherwise); one group
+    applies to every row whatever rows_per_group says."""
     what = "blockwise_matmul"
     dev = _lib.require_gpu(x2d, weight, tile_mask, what=what)
     if x2d.dtype != weight.dtype:
@@ -138,6 +140,10 @@ def blockwise_matmul(x2d: Tensor, weight: Tensor, tile_mask: Tensor, block_k: in
     if mask.dim() == 1:
         mask = mask[None]
     rpg = rows_per_group if rows_per_group is not None else max(M, 1)
+    if mask.shape[0] == 1:
+        rpg = max(M, 1)
+    elif int(rpg) <= 0 or mask.shape[0] * int(rpg) < M:
+        raise ValueError(f"{what}: {mask.shape[0]} row groups of {rpg} rows do not cover {M} rows")
     # bool and uint8 masks are read in place as bytes (any nonzero byte is active)
     if mask.dtype == torch.bool:
         m8 = mask.contiguous().view(torch.uint8)
@@ -203,10 +209,11 @@ class _BlockwiseMatmulFn(torch.autograd.Function):
         x2d, weight, m8 = ctx.saved_tensors
         block_k, block_n, rpg = ctx.meta
         N, K = weight.shape
-        dx = torch.empty_like(x2d)
+        M = x2d.shape[0]
+        dx = torch.zeros_like(x2d)
         dw = torch.zeros_like(weight)
-        for g in range(m8.shape[0]):
-            rows = slice(g * rpg, min((g + 1) * rpg, x2d.shape[0]))
+        for g in range(m8.shape[0]):  # the groups cover every row (checked in blockwise_matmul)
+            rows = slice(min(g * rpg, M), min((g + 1) * rpg, M))
             em = _expand_tiles(m8[g].bool(), N, K, block_k, block_n).to(weight.dtype)
             dx[rows] = dy[rows] @ (weight * em)
             dw += (dy[rows].t() @ x2d[rows]) * em

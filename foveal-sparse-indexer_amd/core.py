@@ -391,8 +391,11 @@ class FovealIndexer(nn.Module):
             no_rows = self.causal and s.shape[1] <= 1
         else:
             mode = 2
-            m8 = torch.broadcast_to(valid_mask.to(device=dev, dtype=torch.bool), s.shape).view(torch.uint8)
-            no_rows = False
+            vm = valid_mask.to(device=dev, dtype=torch.bool)
+            m8 = torch.broadcast_to(vm, s.shape).view(torch.uint8)
+            # the loss comes back in fp32; only the no-valid-entry result (scores.sum() * 0)
+            # carries the scores' dtype, so only a non-fp32 caller needs the (syncing) check
+            no_rows = s.dtype != torch.float32 and not bool(vm.any())
         loss = _DistillKLFn.apply(s.contiguous(), t, mode, m8, float(self.distill_temperature))
         if no_rows:
             # no query block has a candidate: the reference returns scores.sum() * 0

@@ -445,7 +445,12 @@ DecodeParams decode_params(const void* q, const void* k_pool, const void* v_pool
                            int64_t remote_stride, int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, float scale,
                            char* ws, int* err, int mode, int s_local = 0) {
   DecodeSplit split = decode_split(B, Hkv, window, capacity, max_pages);
-  if (s_local > 0 && s_local < split.S_local) split.S_local = s_local;  // fewer local waves, same layout
+  if (s_local > 0 && s_local < split.S_local) {
+    // fewer local waves, same layout, but never so few that a wave would get
+    // more than MAX_CHUNKS_PER_WAVE chunks of the window (the wave stops there)
+    const int64_t min_s = (local_chunks_of(window, max_pages) + MAX_CHUNKS_PER_WAVE - 1) / MAX_CHUNKS_PER_WAVE;
+    split.S_local = static_cast<int>(std::max<int64_t>(s_local, min_s));
+  }
   const int S = mode == DA_ALL ? split.S : split.S_local + split.S_remote;
   const int64_t parts = B * Hkv * S;
   DecodeParams P;

@@ -507,6 +507,9 @@ FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int6
                 (long long)block_n, (long long)K, (long long)N);
   FSI_CHECK_ARG(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, FSI_ERR_SHAPE,
                 "blockwise_matmul: sizes beyond int32");
+  FSI_CHECK_ARG(groups == 1 || groups * rows_per_group >= M, FSI_ERR_SHAPE,
+                "blockwise_matmul: %lld row groups of %lld rows do not cover %lld rows", (long long)groups,
+                (long long)rows_per_group, (long long)M);
   if (M == 0) return FSI_OK;
   FSI_CHECK_ARG(x && w && tile_mask && out, FSI_ERR_INVALID_ARG, "blockwise_matmul: null pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

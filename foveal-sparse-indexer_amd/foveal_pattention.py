@@ -189,8 +189,15 @@ class FovealPattentionMLP(nn.Module):
 
     # -- cache state machine (foveal_pattention.py:108-122) -----------------
     def clear_cache(self) -> None:
+        """Forget the active block list; the next eval call routes again and, as the
+        reference re-gathers the active rows from the current weights
+        (foveal_pattention.py:108-122, 310-322), rebuilds the packed copy, so weight
+        writes that bypass the version counters (`.data` assignments) are seen.  In
+        the pack-in-place mode the packed copy is the weights and stays."""
         self._cached_active_blocks = None
         self._gathered = None
+        if not self._released:
+            self._packed = None
 
     def _gathered_rows(self, which: int) -> Optional[Tensor]:
         """Contiguous detached copies of the active rows of (k_gate, k_up, v), made

@@ -520,7 +520,8 @@ FSI_API size_t fsi_blockwise_matmul_workspace_size(int64_t M, int64_t N, int64_t
  * out = x (w o T)^T where T expands tile_mask to elements: tile (k_b, n_b) of
  * size block_k x block_n is active iff tile_mask[g][k_b * (N / block_n) + n_b],
  * with g the row group of the output row (rows_per_group rows each; groups = 1
- * applies one mask to every row).  block_k divides K, block_n divides N.  The
+ * applies one mask to every row; with groups > 1 they must cover all M rows,
+ * groups * rows_per_group >= M, else FSI_ERR_SHAPE).  block_k divides K, block_n divides N.  The
  * MFMA kernel takes bf16 with block_k a multiple of 32, block_n a multiple of
  * 128 or one of 16, 32, 64, K / block_k <= 2048, rows_per_group a multiple of
  * 128 (or groups = 1) and 16-byte aligned x, w rows; other problems and fp32
@@ -550,13 +551,6 @@ FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int6
 FSI_API int fsi_tile_route(const void* scores, int dtype, int64_t rows, int64_t n_tiles, int64_t ld_scores,
                            int64_t rows_per_group, int64_t base_tiles, float top_p, uint8_t* out_mask,
                            int32_t* out_needed, void* out_probs, void* stream);
-
-/* HBM read-bandwidth probe (measurement only; no counterpart in the reference):
- * reads `bytes` (multiple of 16, 16-byte aligned src) once with `workgroups` x 256
- * lanes, `unroll` (1, 4, 8 or 16) 16-byte loads in flight per lane; sink receives
- * workgroups * 256 dwords.  bench.py uses it as the practical HBM ceiling. */
-FSI_API int fsi_stream_read(const void* src, int64_t bytes, int64_t workgroups, int unroll, uint32_t* sink,
-                            void* stream);
 
 #ifdef __cplusplus
 }

@@ -86,7 +86,11 @@ class DecodeStepOracle:
         self.completed = 0
 
     @torch.no_grad()
-    def step(self, x: Tensor):
+    def step(self, x: Tensor, attend=None):
+        """One decode step.  attend: per-sequence page lists to attend instead of
+        this step's own selection (a checker's hook for comparing outputs over
+        the same support where a near-tie made two selections differ); the
+        returned pages and route are always this step's own."""
         m = self.m
         B = x.shape[0]
         pos = self.seq_len
@@ -110,6 +114,8 @@ class DecodeStepOracle:
                          m.indexer.min_remote_blocks, m.indexer.max_remote_blocks)
         pages = r["pages"]
         att_pages = [pages[0]] * B if self.batch0 else pages
+        if attend is not None:
+            att_pages = attend
         attn = decode_attention_f64(q[:, :, 0].float(), self.k, self.v, pos, m.local_window, att_pages, m.page_size,
                                     m.scale).to(x.dtype)
         out = m.out_proj(attn.reshape(B, 1, m.num_heads * m.head_dim))

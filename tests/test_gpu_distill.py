@@ -58,6 +58,19 @@ def test_distillation_loss_no_valid_rows(fsi, dev):
     assert not s.grad.any()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_distillation_loss_all_false_mask(fsi, dev, dtype):
+    """An explicit valid mask with no valid entry: the reference's scores.sum() * 0,
+    a zero in the scores' dtype with a zero gradient (core.py:351-353)."""
+    m = fsi.FovealIndexer(hidden_size=32, causal=False)
+    s = torch.randn(2, 3, 5, device=dev, dtype=dtype, requires_grad=True)
+    mask = torch.zeros(2, 3, 5, dtype=torch.bool, device=dev)
+    loss = m.distillation_loss(s, torch.rand(2, 3, 5, device=dev), mask)
+    loss.backward()
+    assert float(loss) == 0.0 and loss.dtype == dtype
+    assert not s.grad.any()
+
+
 def test_distillation_loss_broadcast_mask_and_teacher(fsi, dev):
     """A (Q, N) valid mask and a teacher broadcast over the batch."""
     g = torch.Generator().manual_seed(11)

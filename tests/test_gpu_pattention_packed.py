@@ -170,6 +170,34 @@ def test_module_decode_uses_packed_weights_and_repacks(fsi, dev):
         assert P.rel_l2(out3.cpu().reshape(-1, D), ref2) <= BF16_TOL
 
 
+def test_module_data_write_then_clear_cache(fsi, dev):
+    """The reference idiom for new weights: write through .data (no version bump),
+    then clear_cache(); the next eval forward routes again and reads the new
+    weights (foveal_pattention.py:108-122, 310-322), on the packed path too."""
+    torch.manual_seed(2)
+    D, N_p, base, remote = 512, 2048, 2, 6
+    m = fsi.FovealPattentionMLP(hidden_dim=D, intermediate_dim=N_p, base_blocks=base, remote_blocks=remote,
+                                dtype=torch.bfloat16).to(dev).eval()
+    x = torch.randn(8, 1, D).bfloat16()
+    g = torch.Generator().manual_seed(3)
+    with torch.no_grad():
+        m(x.to(dev))
+        assert m._packed is not None
+        new = {n: (torch.randn(N_p, D, generator=g) * 0.03).bfloat16() for n in ("k_gate", "k_up", "v")}
+        m.k_gate.data.copy_(new["k_gate"].to(dev))
+        m.k_up.data.copy_(new["k_up"].to(dev))
+        m.v.data = new["v"].to(dev)
+        m.clear_cache()
+        assert m._packed is None and m._cached_active_blocks is None
+        out = m(x.to(dev))
+        cpu = {k: t.detach().cpu() for k, t in m.state_dict().items()}
+        active = m._cached_active_blocks.cpu()
+        assert torch.equal(active, R.mlp_pooled_route(x.reshape(-1, D), cpu["q_proj_16d.weight"],
+                                                      cpu["block_keys_16d"], base, remote))
+        ref = P.mlp_eval_forward(x.reshape(-1, D), new["k_gate"], new["k_up"], new["v"], active, 64, fused=True)
+        assert P.rel_l2(out.cpu().reshape(-1, D), ref) <= BF16_TOL
+
+
 def test_packed_back_to_back_calls(fsi, dev):
     """Consecutive calls on one stream with different inputs and shapes reuse
     the workspace (partials and arrival counters): each result must match its

@@ -44,6 +44,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA, TFLOP/s
+FP32_PEAK_TFLOPS = 157.3       # MI355X fp32 (vector and dense matrix), TFLOP/s
 
 D_MODEL, N_PARAM, BLOCK, BASE, REMOTE = 4096, 14336, 64, 8, 56
 DECODE_BATCH, PREFILL_TOKENS = 64, 4096
@@ -62,6 +63,9 @@ PREFILL_TRAFFIC_BYTES = int((393537 + 33270 + 196732 + 34374) * 1024)
 C4_TRAFFIC_BYTES = int((161152 + 291023 + 8273 + 3814 + 4352 + 256) * 1024)
 C2_TRAFFIC_BYTES = int((2057 + 2112) * 1024)
 C5_TRAFFIC_BYTES = {0.10: (515 + 64) << 20, 0.25: (1175 + 64) << 20, 0.50: (2249 + 64) << 20}
+# Prefill attention, one step (sa_vmax + sa_vt16 + sparse_attn_lds, profiles/sparse_attention_prefill_16k.md):
+# (878131.0 + 16426.1 + 16467.6) KiB x 1.99983 read + (131315.0 + 32 + 33663.0) KiB written
+PREFILL_ATTN_TRAFFIC_BYTES = int(911024.8 * 1.99983 * 1024 + 165010.0 * 1024)
 # C2: wave-level VALU instructions of one score_route_kernel launch (rocprofv3 SQ_INSTS_VALU)
 C2_VALU_INSTS = 70_114_379
 VALU_PEAK_GIPS = 256 * 4 * 2.4 / 4  # G wave64 VALU instructions/s: 256 CUs x 4 SIMDs x 2.4 GHz / 4 cycles
@@ -191,16 +195,24 @@ def bench_routing(fsi, args, dev):
                   "synthetic (seeded Dirichlet(0.3) mixes of 4 N(0,1)-normalised keys + N(0,0.1) noise, bf16)",
                   {"workload": "C2: 8192 queries x 4096 block keys, index_dim 16, top-p 0.9, K_min 4, K_max 64, "
                                "capacity 64, non-causal", "mean_selected": round(float(counts.mean()), 2)})
-    # VALU issue roofline: the launch's wave-level VALU instruction count (rocprofv3
+    # Algorithmic roofline: per query 4096 16-D scores (65,536 FMA = 131,072 flop) and
+    # 4096 exps, counted one flop each, against the fp32 peak; the top-64 rank per
+    # query has no flop count of its own, so this fraction understates the work.
+    # Diagnostic beside it: the launch's wave-level VALU instruction count (rocprofv3
     # SQ_INSTS_VALU, profiles/indexer_routing_c2.md) over the issue peak of 256 CUs x
     # 4 SIMDs x 2.4 GHz / 4 cycles per wave64 instruction.
+    flops = Q * N * (2 * 16 + 1)
+    tfs = flops / per / 1e12
     gips = C2_VALU_INSTS / per / 1e9
-    res["roofline"] = {"bound": "valu", "achieved": round(gips, 1), "peak": VALU_PEAK_GIPS,
-                       "unit": "G VALU wave-instructions/s", "frac": round(gips / VALU_PEAK_GIPS, 4),
-                       "traffic": C2_TRAFFIC_BYTES, "kernel": "score_route_kernel (1 launch)",
-                       "valu_insts_per_launch": C2_VALU_INSTS, "bytes_per_launch": algo,
-                       "hbm_gbs": round(algo / per / 1e9, 2),
-                       "note": "not HBM-bound: 33.5 M scores, exps and a top-64 rank per launch"}
+    res["roofline"] = {"bound": "valu", "achieved": round(tfs, 3), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                       "frac": round(tfs / FP32_PEAK_TFLOPS, 4), "traffic": C2_TRAFFIC_BYTES,
+                       "kernel": "score_route_kernel (1 launch)", "flops_per_launch": flops,
+                       "bytes_per_launch": algo, "hbm_gbs": round(algo / per / 1e9, 2),
+                       "valu_issue": {"achieved": round(gips, 1), "peak": VALU_PEAK_GIPS,
+                                      "unit": "G VALU wave-instructions/s", "frac": round(gips / VALU_PEAK_GIPS, 4),
+                                      "valu_insts_per_launch": C2_VALU_INSTS},
+                       "note": "not HBM-bound: 33.5 M scores, exps and a top-64 rank per launch; the rank "
+                               "(threshold bisection) takes most of the VALU issue"}
     if not args.no_cpu_baseline:
         from oracle import routing as R
 
@@ -375,7 +387,7 @@ def bench_prefill_attn(fsi, args, dev):
                                "window 1024, top-p 0.9, K_max 32",
                    "mean_remote_pages": round(float(counts.float().mean()), 2)})
     res["roofline"] = {"bound": "mfma", "achieved": round(tfs, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                       "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                       "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": PREFILL_ATTN_TRAFFIC_BYTES,
                        "kernel": "sa_vmax_kernel + sa_vt16_kernel + sparse_attn_lds_kernel (3 launches)", "flops_per_launch": flops}
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))
@@ -513,7 +525,7 @@ def bench_teacher_targets(fsi, args, dev):
                   {"workload": "compute_teacher_dense_block_targets per layer: h (4096, 4096), gate/up (14336, 4096), "
                                "down (4096, 14336), block 64 (224 blocks), T = 1"})
     res["roofline"] = {"bound": "mfma", "achieved": round(tfs, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                       "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                       "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": PREFILL_ATTN_TRAFFIC_BYTES,
                        "kernel": "bsgemm_dma_kernel<N_DUAL, K_DENSE, EPI_ENERGY> (+ column_sumsq_kernel, "
                                  "column_norms_kernel, block_mean_kernel, block_softmax_kernel: 5 launches)",
                        "flops_per_launch": flops}
@@ -606,6 +618,39 @@ def bench_sram_attn(fsi, args, dev):
         res["cpu_baseline"] = {"value": round(med * 1e3, 3), "unit": "ms", "cores": cores, "kind": "port",
                                "sample": "oracle sram_select (fp32) + sram_attention_f64 on the second config "
                                          "(B 32, N 256, block 16), median of 3"}
+    return res
+
+
+def library_gemm_ceiling(dev, n_active: int, steps: int) -> dict:
+    """hipBLASLt (torch F.linear, bf16) on dense GEMMs of the prefill shapes: x (4096
+    tokens x 4096) times the active gate+up rows (2 x 64 n_active x 4096) and H
+    (4096 x 64 n_active) times the active V^T, timed like the prefill step.  The
+    same FLOPs on the vendor library on this box: the practical MFMA ceiling."""
+    n_ch = 64 * n_active
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(PREFILL_TOKENS, D_MODEL, device=dev, generator=g).bfloat16()
+    wgu = (torch.randn(2 * n_ch, D_MODEL, device=dev, generator=g) * 0.02).bfloat16()
+    h = torch.randn(PREFILL_TOKENS, n_ch, device=dev, generator=g).bfloat16()
+    wd = (torch.randn(D_MODEL, n_ch, device=dev, generator=g) * 0.02).bfloat16()
+    outs = {}
+
+    def gu(i):
+        outs["g"] = torch.nn.functional.linear(x, wgu)
+
+    def dn(i):
+        outs["d"] = torch.nn.functional.linear(h, wd)
+
+    res = {}
+    for name, fn, fl in (("gateup", gu, 2 * PREFILL_TOKENS * D_MODEL * 2 * n_ch),
+                         ("down", dn, 2 * PREFILL_TOKENS * n_ch * D_MODEL)):
+        t, _ = time_graph(fn, steps, 2, dev)
+        tf = fl / (t / steps) / 1e12
+        res[name] = {"ms": round(t / steps * 1e3, 4), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+    total = res["gateup"]["ms"] + res["down"]["ms"]
+    tf = prefill_flops(n_active, PREFILL_TOKENS) / (total * 1e-3) / 1e12
+    res["both"] = {"ms": round(total, 4), "tflops": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+    res["note"] = "torch F.linear (hipBLASLt) on dense operands of the same shapes; context, not this library"
+    del x, wgu, h, wd, outs
     return res
 
 
@@ -767,6 +812,7 @@ def main():
                          "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                          "traffic": PREFILL_TRAFFIC_BYTES if n_active == BASE + REMOTE else None,
                          "flops_per_launch": flops},
+            "library_gemm": library_gemm_ceiling(dev, n_active, args.prefill_steps),
         }
 
     if not args.no_cpu_baseline:

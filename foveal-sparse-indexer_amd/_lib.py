@@ -192,8 +192,8 @@ SIGNATURES: dict[str, tuple] = {
     ),
 }
 
-ROUTE_MAX_BLOCKS = 4096
-SCORE_ROUTE_MAX_KEYS = 4096
+ROUTE_MAX_BLOCKS = 65536
+SCORE_ROUTE_MAX_KEYS = 65536
 ROUTE_MAX_RANKED = 256
 
 _lib = None

@@ -14,7 +14,7 @@ select_blocks / route take no gradient (the reference detaches the scores).
 Differences by design:
   * equal probabilities are ranked lower index first (torch.sort leaves their
     order unspecified);
-  * select_blocks handles up to 4096 blocks per row and
+  * select_blocks handles up to 65536 blocks per row and
     min(max(K_max, capacity), blocks) <= 256 (RuntimeError beyond);
   * scores must be float32 or bfloat16.
 """

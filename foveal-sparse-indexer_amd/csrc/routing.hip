@@ -890,6 +890,483 @@ __global__ __launch_bounds__(DR_THREADS) void decode_route_kernel(RouteArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// Rows longer than one wave holds (more than 64 x 64 entries, up to
+// LARGE_MAX): one LW-wave workgroup per row.  Wave w holds the contiguous slice
+// [64 PLW w, 64 PLW (w + 1)) of the row (element j in lane j % 64, slot
+// (j / 64) % PLW).  The softmax maximum and sum, the local mass and the
+// candidate count are combined across the waves through LDS (waves summed in
+// wave order).  Each wave ranks the R best of its slice (threshold bisection,
+// ties in index order) into its candidate list; wave 0 then ranks the R best of
+// the LW lists, read wave-major with each list in slice order, which keeps
+// equal keys in index order: the R best of the row are among the candidates,
+// since an entry with R entries of its slice ahead of it has R entries of the
+// row ahead of it.
+// ---------------------------------------------------------------------------
+constexpr int LW = 16;
+constexpr int LW_THREADS = 64 * LW;
+constexpr int LARGE_MAX = 64 * 64 * LW;
+
+template <int E>
+struct LargeLds {
+  float redf[LW];
+  int redi[LW];
+  int other[LW];
+  int n_cand[LW];
+  uint32_t cand_k[LW * 64 * E], cand_i[LW * 64 * E];
+  uint32_t lk[64 * E], li[64 * E];
+};
+
+// Workgroup maximum / sum (waves added in wave order) / integer sum; every
+// thread of the LW waves must call them, and every thread gets the result.
+__device__ __forceinline__ float lw_max(float v, float* red) {
+  v = wave_max(v);
+  __syncthreads();
+  if (lane_id() == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < LW; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+__device__ __forceinline__ float lw_sum(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane_id() == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < LW; ++w) r += red[w];
+  return r;
+}
+__device__ __forceinline__ int lw_sum_i(int v, int* red) {
+  v = wave_sum_i(v);
+  __syncthreads();
+  if (lane_id() == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int r = 0;
+#pragma unroll
+  for (int w = 0; w < LW; ++w) r += red[w];
+  return r;
+}
+
+// Stage 1 (every wave, over its slice) and stage 2 (wave 0, over the
+// candidates) of the R-best ranking; wave 0 returns the R best sorted
+// descending in sorted[] (the other waves' sorted[] stay 0).  Ends with every
+// wave past the barrier between the stages.
+template <int PLW, int E, class IdxFn>
+__device__ __forceinline__ void lw_rank_top(const uint32_t (&key)[PLW], int R, uint64_t (&sorted)[E], LargeLds<E>& L,
+                                            IdxFn idx) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  constexpr int RS = 64 * E;
+#pragma unroll
+  for (int e = 0; e < E; ++e) sorted[e] = 0;
+  if (R > 0) {  // uniform across the workgroup
+    uint32_t T;
+    int clo;
+    top_threshold<PLW>(key, R, T, clo);
+    const int n = take_top<PLW>(key, R, T, clo, L.cand_k + wave * RS, L.cand_i + wave * RS, idx);
+    if (lane == 0) L.n_cand[wave] = n;
+  }
+  __syncthreads();
+  if (wave != 0 || R <= 0) return;
+  constexpr int PC = LW * E;  // candidate slots per lane
+  uint32_t ck[PC];
+#pragma unroll
+  for (int i = 0; i < PC; ++i) {
+    const int f = 64 * i + lane;  // candidate f: slot f % RS of wave f / RS
+    ck[i] = f % RS < L.n_cand[f / RS] ? L.cand_k[f] : 0u;
+  }
+  uint32_t T;
+  int clo;
+  top_threshold<PC>(ck, R, T, clo);
+  take_top<PC>(ck, R, T, clo, L.lk, L.li, [&](int i) { return L.cand_i[64 * i + lane]; });
+  sort_taken<E>(R, sorted, L.lk, L.li);
+}
+
+// select_row for a row held by the LW waves of the workgroup (s: this wave's
+// slice, upcast to fp32).  Same outputs and rules as select_row.
+template <int PLW, int E, bool RB>
+__device__ void select_row_large(float (&s)[PLW], int N, int qb, int64_t row, const SelectParams& sp,
+                                 int32_t* __restrict__ out_idx, int32_t* __restrict__ out_cnt,
+                                 float* __restrict__ out_mass, LargeLds<E>& L) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const float top_p = sp.top_p_rows ? sp.top_p_rows[row] : sp.top_p;
+  const int k_min = sp.k_min_rows ? sp.k_min_rows[row] : sp.k_min;
+  const int k_max = sp.k_max_rows ? sp.k_max_rows[row] : sp.k_max;
+  auto elem = [&](int i) { return (wave * PLW + i) * 64 + lane; };
+
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PLW; ++i) {
+    const int j = elem(i);
+    if (j < N && mask_kind(j, qb, sp.causal, sp.local_window)) mx = fmaxf(mx, s[i]);
+  }
+  mx = lw_max(mx, L.redf);
+  if (!isfinite(mx)) mx = 0.0f;
+  float z = 0.f;
+#pragma unroll
+  for (int i = 0; i < PLW; ++i) {
+    const int j = elem(i);
+    s[i] = j < N && mask_kind(j, qb, sp.causal, sp.local_window) ? expf(s[i] - mx) : 0.0f;
+    z += s[i];
+  }
+  z = fmaxf(lw_sum(z, L.redf), 1e-20f);
+  float lm = 0.f;
+  int av = 0, ot = 0;
+  uint32_t key[PLW];
+#pragma unroll
+  for (int i = 0; i < PLW; ++i) {
+    const int j = elem(i);
+    const int kind = j < N ? mask_kind(j, qb, sp.causal, sp.local_window) : 0;
+    float p = s[i] / z;
+    if (RB) p = round_bf16(p);
+    if (kind == 1) lm += p;
+    key[i] = kind == 2 ? __float_as_uint(p) + 1u : 0u;
+    av += kind == 2;
+    ot += j < N && kind != 2;
+  }
+  float lmass = lw_sum(lm, L.redf);
+  if (RB) lmass = round_bf16(lmass);
+  ot = wave_sum_i(ot);
+  if (lane == 0) L.other[wave] = ot;
+  const int avail = lw_sum_i(av, L.redi);  // its barriers also publish L.other
+
+  int R = k_max > sp.capacity ? k_max : sp.capacity;
+  R = R < avail ? R : avail;
+  R = R < 64 * E ? R : 64 * E;  // the host guarantees this does not truncate
+  int32_t* idx = out_idx + row * sp.capacity;
+  if (sp.capacity > R) {
+    // R == avail here: the non-remote entries (ranked -1) follow in index order
+    int base = R;
+    for (int w = 0; w < wave; ++w) base += L.other[w];
+#pragma unroll
+    for (int i = 0; i < PLW; ++i) {
+      const int j = elem(i);
+      const bool other = j < N && mask_kind(j, qb, sp.causal, sp.local_window) != 2;
+      const uint64_t b = __ballot(other);
+      const int pos = base + lanes_below(b);
+      if (other && pos < sp.capacity) idx[pos] = j;
+      base += __popcll(b);
+    }
+  }
+  uint64_t sorted[E];
+  lw_rank_top<PLW, E>(key, R, sorted, L, [&](int i) { return static_cast<uint32_t>(elem(i)); });
+  if (wave != 0) return;
+
+  const float target = RB ? fmaxf(round_bf16(round_bf16(top_p) - lmass), 0.0f) : fmaxf(top_p - lmass, 0.0f);
+  int nr = k_max < avail ? k_max : avail;
+  nr = nr < 0 ? 0 : nr;
+  nr = nr < R ? nr : R;
+  float cum[E];
+  running_mass<E, RB>(sorted, nr, cum);
+  int count;
+  if (avail <= 0) {
+    count = 0;
+  } else {
+    const int first = first_reaching<E>(cum, nr, target);
+    int needed = first >= nr ? 0x7fffffff : first + (target > 0.0f ? 1 : 0);
+    needed = needed > k_min ? needed : k_min;
+    count = needed < avail ? needed : avail;
+  }
+  count = count < k_max ? count : k_max;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int k = e * 64 + lane;
+    if (k < R && k < sp.capacity) idx[k] = comp_index(sorted[e]);
+  }
+  const float ck = count > 0 ? element_at<E>(cum, count - 1) : 0.f;
+  if (lane == 0) {
+    out_cnt[row] = count;
+    if (out_mass) out_mass[row] = count > 0 ? (RB ? round_bf16(lmass + ck) : lmass + ck) : lmass;
+  }
+}
+
+// select_blocks on materialised scores, one workgroup per row of N > 64 x 64.
+template <int PLW, int E, bool BF16>
+__global__ __launch_bounds__(LW_THREADS) void route_scores_large_kernel(const void* __restrict__ scores, int Qb,
+                                                                        int N, SelectParams sp,
+                                                                        int32_t* __restrict__ out_idx,
+                                                                        int32_t* __restrict__ out_cnt,
+                                                                        float* __restrict__ out_mass) {
+  __shared__ LargeLds<E> L;
+  const int64_t row = blockIdx.x;
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  float s[PLW];
+#pragma unroll
+  for (int i = 0; i < PLW; ++i) {
+    const int j = (wave * PLW + i) * 64 + lane;
+    if (BF16) s[i] = j < N ? bf16_to_f32(static_cast<const bf16_t*>(scores)[row * N + j]) : 0.f;
+    else s[i] = j < N ? static_cast<const float*>(scores)[row * N + j] : 0.f;
+  }
+  select_row_large<PLW, E, BF16>(s, N, static_cast<int>(row % Qb), row, sp, out_idx, out_cnt, out_mass, L);
+}
+
+// fp32 cosine / sqrt(d) score of query qa (normalised) against key j, with the
+// arithmetic of score_route_kernel (key L2-normalised in fp32, products summed
+// in component order).
+template <bool BF16>
+__device__ __forceinline__ float cosine_score(const char* kb, int j, const float (&qa)[SR_D], float sqrt_d) {
+  float v[SR_D];
+  if (BF16) {
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(reinterpret_cast<const bf16_t*>(kb) +
+                                                           static_cast<int64_t>(j) * SR_D);
+    const u32x4_t a = src[0], c2 = src[1];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      v[2 * w] = lo_bf16(a[w]);
+      v[2 * w + 1] = hi_bf16(a[w]);
+      v[8 + 2 * w] = lo_bf16(c2[w]);
+      v[8 + 2 * w + 1] = hi_bf16(c2[w]);
+    }
+  } else {
+    const float4* src = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(kb) +
+                                                        static_cast<int64_t>(j) * SR_D);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float4 f = src[w];
+      v[4 * w] = f.x;
+      v[4 * w + 1] = f.y;
+      v[4 * w + 2] = f.z;
+      v[4 * w + 3] = f.w;
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < SR_D; ++c) ss = fmaf(v[c], v[c], ss);
+  const float nrm = fmaxf(sqrtf(ss), 1e-12f);
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < SR_D; ++c) acc = fmaf(qa[c], v[c] / nrm, acc);
+  return acc / sqrt_d;
+}
+
+// Fused cosine scoring + select_blocks for rows of N > 64 x 64 keys: one
+// workgroup per query row (grid (Q, B)).
+template <int PLW, int E, bool BF16>
+__global__ __launch_bounds__(LW_THREADS) void score_route_large_kernel(const void* __restrict__ q,
+                                                                       const void* __restrict__ k, int Q, int N,
+                                                                       int64_t k_batch_stride, float sqrt_d,
+                                                                       SelectParams sp,
+                                                                       int32_t* __restrict__ out_idx,
+                                                                       int32_t* __restrict__ out_cnt,
+                                                                       float* __restrict__ out_mass) {
+  __shared__ LargeLds<E> L;
+  __shared__ float qn[SR_D];
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int row_q = blockIdx.x, b = blockIdx.y;
+  if (threadIdx.x == 0) {
+    float v[SR_D];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < SR_D; ++c) {
+      const int64_t off = (static_cast<int64_t>(b) * Q + row_q) * SR_D + c;
+      v[c] = BF16 ? bf16_to_f32(static_cast<const bf16_t*>(q)[off]) : static_cast<const float*>(q)[off];
+      ss = fmaf(v[c], v[c], ss);
+    }
+    const float nrm = fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+    for (int c = 0; c < SR_D; ++c) qn[c] = v[c] / nrm;
+  }
+  __syncthreads();
+  float qa[SR_D];
+#pragma unroll
+  for (int c = 0; c < SR_D; ++c) qa[c] = qn[c];
+  const char* kb = static_cast<const char*>(k) + static_cast<int64_t>(b) * k_batch_stride * (BF16 ? 2 : 4);
+  float s[PLW];
+#pragma unroll
+  for (int i = 0; i < PLW; ++i) {
+    const int j = (wave * PLW + i) * 64 + lane;
+    s[i] = j < N ? cosine_score<BF16>(kb, j, qa, sqrt_d) : 0.f;
+  }
+  select_row_large<PLW, E, false>(s, N, row_q, static_cast<int64_t>(b) * Q + row_q, sp, out_idx, out_cnt, out_mass,
+                                  L);
+}
+
+// decode_route_block for more than 64 x 64 completed pages: one LW-wave
+// workgroup per sequence, the page scores in registers.
+template <int PLW, int E, bool BF16>
+__global__ __launch_bounds__(LW_THREADS) void decode_route_large_kernel(RouteArgs A) {
+  __shared__ LargeLds<E> L;
+  __shared__ float ctx_part[LW][SR_D];
+  const int b = blockIdx.x;
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int P = A.P, page = A.page, window = A.window, completed = A.completed;
+  const int k_min = A.k_min, k_max = A.k_max, cap = A.cap;
+  const int mypos = A.pos_rows ? A.pos_rows[b] : A.pos;
+  const int local_start = mypos + 1 - window > 0 ? mypos + 1 - window : 0;
+  const int flp = local_start / page;
+  auto elem = [&](int i) { return (wave * PLW + i) * 64 + lane; };
+
+  float qv[SR_D];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < SR_D; ++c) {
+    const int64_t off = static_cast<int64_t>(b) * SR_D + c;
+    qv[c] = BF16 ? bf16_to_f32(static_cast<const bf16_t*>(A.qi)[off]) : static_cast<const float*>(A.qi)[off];
+    ss = fmaf(qv[c], qv[c], ss);
+  }
+  const float nrm = fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+  for (int c = 0; c < SR_D; ++c) qv[c] = qv[c] / nrm;
+  float sc[PLW];
+#pragma unroll
+  for (int i = 0; i < PLW; ++i) {
+    const int j = elem(i);
+    float acc = 0.f;
+    if (j < completed) {
+      const float4* kr = reinterpret_cast<const float4*>(A.kp + (static_cast<int64_t>(b) * P + j) * SR_D);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float4 f = kr[w];
+        acc = fmaf(qv[4 * w], f.x, acc);
+        acc = fmaf(qv[4 * w + 1], f.y, acc);
+        acc = fmaf(qv[4 * w + 2], f.z, acc);
+        acc = fmaf(qv[4 * w + 3], f.w, acc);
+      }
+    }
+    sc[i] = acc / A.sqrt_d;
+  }
+
+  if (A.out_ctx) {  // uniform: softmax over every completed page, contracted with vp
+    float ctx = 0.f;
+    if (completed > 0) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < PLW; ++i)
+        if (elem(i) < completed) m = fmaxf(m, sc[i]);
+      const float cmx = lw_max(m, L.redf);
+      float zz = 0.f;
+#pragma unroll
+      for (int i = 0; i < PLW; ++i)
+        if (elem(i) < completed) zz += expf(sc[i] - cmx);
+      const float cz = lw_sum(zz, L.redf);
+      float part[SR_D];
+#pragma unroll
+      for (int c = 0; c < SR_D; ++c) part[c] = 0.f;
+#pragma unroll
+      for (int i = 0; i < PLW; ++i) {
+        const int j = elem(i);
+        if (j >= completed) continue;
+        float pj = expf(sc[i] - cmx) / cz;
+        const int64_t off = (static_cast<int64_t>(b) * P + j) * SR_D;
+        if (BF16) {
+          pj = round_bf16(pj);
+          const u32x4_t* vr = reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(A.vp) + off);
+          const u32x4_t a = vr[0], c2 = vr[1];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            part[2 * w] = fmaf(pj, lo_bf16(a[w]), part[2 * w]);
+            part[2 * w + 1] = fmaf(pj, hi_bf16(a[w]), part[2 * w + 1]);
+            part[8 + 2 * w] = fmaf(pj, lo_bf16(c2[w]), part[8 + 2 * w]);
+            part[9 + 2 * w] = fmaf(pj, hi_bf16(c2[w]), part[9 + 2 * w]);
+          }
+        } else {
+          const float4* vr = reinterpret_cast<const float4*>(static_cast<const float*>(A.vp) + off);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float4 f = vr[w];
+            part[4 * w] = fmaf(pj, f.x, part[4 * w]);
+            part[4 * w + 1] = fmaf(pj, f.y, part[4 * w + 1]);
+            part[4 * w + 2] = fmaf(pj, f.z, part[4 * w + 2]);
+            part[4 * w + 3] = fmaf(pj, f.w, part[4 * w + 3]);
+          }
+        }
+      }
+      int which;
+      const float t = dr_wave_sum16_scatter(part, which);
+      if ((lane & 3) == 0) ctx_part[wave][which] = t;
+      __syncthreads();
+      if (threadIdx.x < SR_D) {
+#pragma unroll
+        for (int w = 0; w < LW; ++w) ctx += ctx_part[w][threadIdx.x];
+      }
+    }
+    if (threadIdx.x < SR_D) {
+      const int64_t off = static_cast<int64_t>(b) * SR_D + threadIdx.x;
+      if (BF16) static_cast<bf16_t*>(A.out_ctx)[off] = f32_to_bf16(ctx);
+      else static_cast<float*>(A.out_ctx)[off] = ctx;
+    }
+  }
+
+  const bool route = completed > flp && flp > 0;  // uniform
+  const int kcap = k_max < flp ? k_max : flp;     // k_max = min(K_max, first_local_page)
+  int R = kcap > k_min ? kcap : k_min;
+  R = R < flp ? R : flp;
+  R = R < cap ? R : cap;
+  if (!route) R = 0;
+  uint32_t key[PLW];
+#pragma unroll
+  for (int i = 0; i < PLW; ++i) key[i] = 0u;
+  if (R > 0) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PLW; ++i)
+      if (elem(i) < flp) m = fmaxf(m, sc[i]);
+    const float mx = lw_max(m, L.redf);
+    float zz = 0.f;
+#pragma unroll
+    for (int i = 0; i < PLW; ++i)
+      if (elem(i) < flp) zz += expf(sc[i] - mx);
+    const float z = lw_sum(zz, L.redf);
+#pragma unroll
+    for (int i = 0; i < PLW; ++i)
+      if (elem(i) < flp) key[i] = __float_as_uint(expf(sc[i] - mx) / z) + 1u;
+  }
+  uint64_t sorted[E];
+  lw_rank_top<PLW, E>(key, R, sorted, L, [&](int i) { return static_cast<uint32_t>(elem(i)); });
+  if (wave != 0) return;
+  int count = 0;
+  if (R > 0) {
+    float cum[E];
+    running_mass<E, false>(sorted, R, cum);
+    const int first = first_reaching<E>(cum, R, A.top_p);
+    const int needed = first >= R ? 0x7fffffff : first + 1;  // #(cum < top_p) + 1
+    count = needed < kcap ? needed : kcap;
+    count = count > k_min ? count : k_min;
+    count = count < flp ? count : flp;
+    count = count < cap ? count : cap;
+  }
+  int32_t* pages = A.out_pages + static_cast<int64_t>(b) * cap;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int k = e * 64 + lane;
+    if (k < cap) pages[k] = k < count ? comp_index(sorted[e]) : -1;
+  }
+  for (int k = 64 * E + lane; k < cap; k += 64) pages[k] = -1;
+  if (lane == 0) A.out_cnt[b] = count;
+}
+
+// Slots per lane of one wave's slice for a large row of n entries.
+int pick_plw(int64_t n) {
+  const int64_t per_wave = (n + LW - 1) / LW;
+  const int plw = static_cast<int>((per_wave + 63) / 64);
+  if (plw <= 8) return 8;
+  if (plw <= 16) return 16;
+  if (plw <= 32) return 32;
+  return 64;
+}
+
+#define FSI_DISPATCH_PLW(PLV, ...) \
+  switch (PLV) {                   \
+    case 8: {                      \
+      constexpr int PLW = 8;       \
+      __VA_ARGS__;                 \
+    } break;                       \
+    case 16: {                     \
+      constexpr int PLW = 16;      \
+      __VA_ARGS__;                 \
+    } break;                       \
+    case 32: {                     \
+      constexpr int PLW = 32;      \
+      __VA_ARGS__;                 \
+    } break;                       \
+    default: {                     \
+      constexpr int PLW = 64;      \
+      __VA_ARGS__;                 \
+    } break;                       \
+  }
+
+// ---------------------------------------------------------------------------
 // masked_softmax (core.py:36-43): fp32 softmax over mask, masked entries 0,
 // all-masked rows 0, result in the scores' dtype.  One workgroup per row;
 // three passes over the row (max, sum, write), the later two from L2.
@@ -1114,6 +1591,19 @@ FSI_API int fsi_route_from_scores(const void* scores, int dtype, int64_t B, int6
   FSI_CHECK_ARG(scores && out_indices && out_counts, FSI_ERR_INVALID_ARG, "route_from_scores: null pointer");
   SelectParams sp{causal, local_window_blocks, capacity, top_p, k_min, k_max, top_p_rows, k_min_rows, k_max_rows};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (Nb > 64 * 64) {  // one workgroup per row
+    FSI_CHECK_ARG(rows <= (int64_t)0x7fffffff, FSI_ERR_SHAPE, "route_from_scores: too many rows");
+    FSI_DISPATCH_PLW(pick_plw(Nb), FSI_DISPATCH_E(pick_e(want), {
+      if (dtype == FSI_DTYPE_BF16)
+        route_scores_large_kernel<PLW, E, true><<<(unsigned)rows, LW_THREADS, 0, st>>>(
+            scores, (int)Qb, (int)Nb, sp, out_indices, out_counts, out_mass);
+      else
+        route_scores_large_kernel<PLW, E, false><<<(unsigned)rows, LW_THREADS, 0, st>>>(
+            scores, (int)Qb, (int)Nb, sp, out_indices, out_counts, out_mass);
+    }))
+    FSI_HIP_LAUNCH_CHECK("route_from_scores");
+    return FSI_OK;
+  }
   const dim3 grid(static_cast<unsigned>((rows + RS_WAVES - 1) / RS_WAVES));
   FSI_DISPATCH_PL(pick_pl(Nb), FSI_DISPATCH_E(pick_e(want), {
     if (dtype == FSI_DTYPE_BF16)
@@ -1151,8 +1641,21 @@ FSI_API int fsi_score_and_route(const void* q, const void* k, int dtype, int64_t
                 FSI_ERR_ALIGN, "score_and_route: keys must be 16-byte aligned");
   SelectParams sp{causal, local_window_blocks, capacity, top_p, k_min, k_max, nullptr, nullptr, nullptr};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>((Q + SR_WAVES - 1) / SR_WAVES), static_cast<unsigned>(B));
   const float sqrt_d = static_cast<float>(sqrt(static_cast<double>(index_dim)));
+  if (N > 64 * 64) {  // one workgroup per query row
+    const dim3 lgrid(static_cast<unsigned>(Q), static_cast<unsigned>(B));
+    FSI_DISPATCH_PLW(pick_plw(N), FSI_DISPATCH_E(pick_e(want), {
+      if (dtype == FSI_DTYPE_BF16)
+        score_route_large_kernel<PLW, E, true><<<lgrid, LW_THREADS, 0, st>>>(
+            q, k, (int)Q, (int)N, k_batch_stride, sqrt_d, sp, out_indices, out_counts, out_mass);
+      else
+        score_route_large_kernel<PLW, E, false><<<lgrid, LW_THREADS, 0, st>>>(
+            q, k, (int)Q, (int)N, k_batch_stride, sqrt_d, sp, out_indices, out_counts, out_mass);
+    }))
+    FSI_HIP_LAUNCH_CHECK("score_and_route");
+    return FSI_OK;
+  }
+  const dim3 grid(static_cast<unsigned>((Q + SR_WAVES - 1) / SR_WAVES), static_cast<unsigned>(B));
   int pl = pick_pl(N);
   pl = pl < 16 ? 16 : pl;
   FSI_DISPATCH_PL(pl, FSI_DISPATCH_E(pick_e(want), {
@@ -1182,6 +1685,16 @@ FSI_API int fsi_decode_route(const void* qi, const float* kp, const void* vp, in
                                  k_max, capacity, out_pages, out_counts, out_context);
   int64_t want = k_max > k_min ? k_max : k_min;
   want = want < capacity ? want : capacity;
+  if (completed_pages > 64 * 64) {  // one 16-wave workgroup per sequence
+    FSI_DISPATCH_PLW(pick_plw(completed_pages), FSI_DISPATCH_E(pick_e(want), {
+      if (dtype == FSI_DTYPE_BF16)
+        decode_route_large_kernel<PLW, E, true><<<(unsigned)B, LW_THREADS, 0, st>>>(A);
+      else
+        decode_route_large_kernel<PLW, E, false><<<(unsigned)B, LW_THREADS, 0, st>>>(A);
+    }))
+    FSI_HIP_LAUNCH_CHECK("decode_route");
+    return FSI_OK;
+  }
   FSI_DISPATCH_PL(pick_pl(completed_pages), FSI_DISPATCH_E(pick_e(want), {
     if (dtype == FSI_DTYPE_BF16)
       decode_route_kernel<PL, E, true><<<(unsigned)B, DR_THREADS, 0, st>>>(A);
@@ -1215,6 +1728,20 @@ FSI_API int fsi_decode_step_attn(const void* qi, const float* kp, const void* vp
   char* ws = static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES;
   const RouteArgs A = route_args(qi, kp, vp, B, P, pos_rows, pos, PAGE, window, completed_pages, top_p, k_min, k_max,
                                  capacity, out_pages, out_counts, out_context);
+  if (completed_pages > 64 * 64) {
+    // more pages than the routing workgroups of the fused launch hold: the
+    // large-row routing kernel, then the selected pages and the window in one
+    // partial launch and the merge (same workspace layout)
+    FSI_DISPATCH_PLW(pick_plw(completed_pages), FSI_DISPATCH_E(pick_e(want_of(k_min, k_max, capacity)), {
+      decode_route_large_kernel<PLW, E, true><<<(unsigned)B, LW_THREADS, 0, st>>>(A);
+    }))
+    FSI_HIP_LAUNCH_CHECK("decode_step_attn route");
+    const DecodeParams D = decode_params(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
+                                         out_pages, out_counts, batch0 ? 0 : capacity, capacity, B, Hq, Hkv, scale, ws,
+                                         err, DA_ALL);
+    c = decode_partial_launch(D, head_dim, st);
+    return c != FSI_OK ? c : decode_merge_launch(D, head_dim, out, st);
+  }
   // launch 1: routing workgroups [0, B) beside the local-window partials (which read no routing result),
   // with as many local waves as fit beside the routing workgroups in one round of resident workgroups,
   // so that no second round trails the first

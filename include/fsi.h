@@ -182,8 +182,8 @@ FSI_API int fsi_mlp_router(const void* x, int64_t ldx, int64_t M, int64_t D, con
  *   needed = #(cum < target) + (target > 0); max(needed, K_min) if any remote
  *   count  = min(needed, available, K_max)
  * ------------------------------------------------------------------------- */
-#define FSI_ROUTE_MAX_BLOCKS 4096      /* blocks (or pages) per routed row           */
-#define FSI_SCORE_ROUTE_MAX_KEYS 4096  /* keys per row of fsi_score_and_route        */
+#define FSI_ROUTE_MAX_BLOCKS 65536     /* blocks (or pages) per routed row           */
+#define FSI_SCORE_ROUTE_MAX_KEYS 65536 /* keys per row of fsi_score_and_route        */
 #define FSI_ROUTE_MAX_RANKED 256       /* bound on min(max(K_max, capacity), blocks) */
 
 /* masked_softmax (foveal_indexer/core.py:36-43): fp32 softmax of scores over

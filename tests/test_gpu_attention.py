@@ -144,6 +144,40 @@ def test_decode_step_attention_wide_batch_long_window(fsi, dev):
     assert Pt.rel_l2(out[::16].cpu().float(), ref.float()) <= TOL
 
 
+@pytest.mark.parametrize("batch0", [False, True])
+def test_decode_step_attention_many_pages(fsi, dev, batch0):
+    """More complete pages (5000, 320 K tokens) than the fused launch's routing
+    workgroups hold: the step runs the 16-wave routing kernel, then the window
+    and the selected pages.  Pages equal the separate decode_route; attention
+    against fp64 over the routed pages."""
+    B, Hq, Hkv, hd, W, kmax = 2, 8, 2, 64, 1024, 32
+    max_seq = 64 * 5000
+    pos = max_seq - 1
+    print(f"[case] fused decode step, 5000 pages, batch0={batch0}", flush=True)
+    c, k, v = _cache(fsi, dev, B, Hkv, hd, max_seq, seed=91)
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(B, Hq, hd, generator=g).bfloat16().to(dev)
+    qi = torch.nn.functional.rms_norm(torch.randn(B, 16, generator=g), (16,)).bfloat16().to(dev)
+    c.kp_cache.copy_(torch.nn.functional.normalize(torch.randn(B, c.max_pages, 16, generator=g), dim=-1).to(dev))
+    c.vp_cache.copy_(torch.randn(B, c.max_pages, 16, generator=g).bfloat16().to(dev))
+    completed = (pos + 1) // 64
+    scale = 1.0 / math.sqrt(hd)
+    with torch.no_grad():
+        out, pages, counts, ctx = fsi.decode_step_attention(
+            q, qi, c, pos=pos, window=W, completed_pages=completed, top_p=0.9, min_remote_blocks=0,
+            max_remote_blocks=kmax, scale=scale, return_context=True, batch0=batch0)
+        rp, rc, rctx = fsi.decode_route(qi, c.kp_cache, c.vp_cache, pos=pos, page_size=64, local_window=W,
+                                        completed_pages=completed, top_p=0.9, min_remote_blocks=0,
+                                        max_remote_blocks=kmax, return_context=True)
+    assert torch.equal(pages, rp) and torch.equal(counts, rc) and torch.equal(ctx, rctx)
+    cnt = counts.cpu().tolist()
+    assert min(cnt) > 0
+    sel = [pages[b, :cnt[b]].cpu().tolist() for b in range(B)]
+    att = [sel[0]] * B if batch0 else sel
+    ref = A.decode_attention_f64(q.cpu().float(), k, v, pos, W, att, 64, scale)
+    assert Pt.rel_l2(out.cpu().float(), ref.float()) <= TOL
+
+
 def test_decode_step_attention_graph_replays(fsi, dev):
     """The fused step captured in a graph and replayed with eager work in between:
     every replay equals the eager result."""

@@ -103,8 +103,30 @@ def test_select_blocks_stats_and_empty_rows(fsi, dev):
     assert route.block_scores is not None
 
 
+LARGE_CASES = [
+    # rows longer than one wave holds (> 4096 blocks): one 16-wave workgroup per row
+    # (B, Qb, Nb, causal, local, top_p, kmin, kmax, cap, scale)
+    (1, 3, 8192, False, 0, 0.9, 4, 64, 64, 6.0),        # 8 slots per lane per wave
+    (1, 2, 16384, False, 16, 0.95, 2, 200, 256, 4.0),   # 16 slots, local window, 256 ranked
+    (1, 2, 40000, False, 0, 0.8, 0, 32, 32, 8.0),       # 64 slots, ragged last wave
+    (1, 4200, 4200, True, 8, 0.9, 1, 16, 16, 6.0),      # causal: early rows have fewer candidates than capacity
+]
+
+
+@pytest.mark.parametrize("case", LARGE_CASES, ids=[f"L{i}" for i in range(len(LARGE_CASES))])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_select_blocks_large_rows(fsi, dev, case, dtype):
+    B, Qb, Nb, causal, lw, p, kmin, kmax, cap, scale = case
+    print(f"[case] select_blocks large {case} {dtype}", flush=True)
+    s = _scores(B, Qb, Nb, seed=Nb + 7, scale=scale, dtype=dtype)
+    route, ora = _compare(fsi, dev, s, causal=causal, local_window_blocks=lw, top_p=p, min_remote_blocks=kmin,
+                          max_remote_blocks=kmax, remote_capacity=cap)
+    same = route.remote_counts.cpu() == ora["remote_counts"]
+    assert int(same.sum()) >= same.numel() - max(2, same.numel() // 500)
+
+
 def test_select_blocks_capacity_limits(fsi, dev):
-    s = torch.zeros(1, 1, 5000, device=dev)
+    s = torch.zeros(1, 1, 70000, device=dev)
     with pytest.raises(RuntimeError, match="blocks per row"):
         fsi.select_blocks(s, causal=False)
     s = torch.zeros(1, 1, 1000, device=dev)
@@ -174,6 +196,25 @@ def test_score_and_route_batched_and_causal(fsi, dev):
     assert not bad, bad
 
 
+@pytest.mark.parametrize("Q,N,kmin,kmax,cap", [(20, 8192, 4, 64, 64), (6, 16384, 2, 100, 128), (3, 65536, 0, 16, 16)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_score_and_route_large_rows(fsi, dev, Q, N, kmin, kmax, cap, dtype):
+    print(f"[case] score_and_route large Q={Q} N={N} {dtype}", flush=True)
+    q, k = _c2_inputs(Q, N, seed=N + Q, dtype=dtype)
+    idx, cnt, mass = fsi.score_and_route(q.to(dev), k.to(dev), causal=False, top_p=0.9, min_remote_blocks=kmin,
+                                         max_remote_blocks=kmax, remote_capacity=cap, return_mass=True)
+    s = R.cosine_scores_f32(q[None], k[None])
+    ora = R.select_route(s, causal=False, top_p=0.9, min_remote_blocks=kmin, max_remote_blocks=kmax,
+                         remote_capacity=cap)
+    bad = check_rows(idx, cnt, ora, torch.ones(Q, N, dtype=torch.bool), 1e-6, 1e-5)
+    assert not bad, bad
+    oc = ora["remote_counts"][0].long()
+    cm = ora["cumulative"][0]
+    ref_mass = torch.where(oc > 0, cm.gather(1, (oc - 1).clamp_min(0)[:, None])[:, 0], torch.zeros(Q))
+    same = cnt.cpu()[0].long() == oc
+    assert torch.allclose(mass.cpu()[0][same], ref_mass[same], atol=2e-6)
+
+
 def _decode_inputs(B, P, seed):
     g = torch.Generator().manual_seed(seed)
     kp = torch.nn.functional.normalize(torch.randn(B, P, 16, generator=g), dim=-1)
@@ -187,6 +228,9 @@ def _decode_inputs(B, P, seed):
     (32, 2048, 64, 1024, 131071, 0, 32, 0.9),
     (3, 100, 16, 32, 16 * 100 - 1, 2, 64, 0.95),
     (2, 10, 64, 1024, 500, 0, 8, 0.9),         # no remote pages yet
+    (3, 5000, 64, 1024, 64 * 5000 - 1, 0, 32, 0.9),     # more pages than one wave holds: 16-wave workgroup
+    (2, 16384, 64, 2048, 64 * 16384 - 1, 4, 64, 0.95),  # 1 M tokens of context
+    (2, 40000, 16, 256, 16 * 40000 - 7, 0, 256, 0.99),  # 64 slots per lane, 256 ranked
 ])
 def test_decode_route_parity(fsi, dev, B, P, page, W, pos, kmin, kmax, top_p):
     print(f"[case] decode_route B={B} P={P} pos={pos}", flush=True)

@@ -162,6 +162,13 @@ SIGNATURES: dict[str, tuple] = {
          _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr],
     ),
     "fsi_sparse_attn_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "fsi_sparse_attn_bwd_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "fsi_sparse_attn_bwd": (
+        _c_int,
+        [_c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64,
+         _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64,
+         _c_ptr, _c_i64, _c_i64, ctypes.c_float, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr, _c_ptr]),
     "fsi_sparse_attn": (
         _c_int,
         [_c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64,

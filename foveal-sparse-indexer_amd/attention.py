@@ -563,10 +563,64 @@ def _sparse_attn_op(q: Tensor, k: Tensor, v: Tensor, lists: Optional[Tensor], co
     return _sparse_attention_launch(q, k, v, lists, counts, cap, block, mode, window, scale, _sparse_out(q))
 
 
+def _sparse_attention_bwd(q, k, v, out, dout, lists, counts, cap, block, mode, window, scale):
+    """fsi_sparse_attn_bwd: fp32 (dq, dk, dv) of sparse_attention over the same
+    pattern, from the saved operands and output, without any (T, T) tensor."""
+    what = "sparse_attention backward"
+    dev = q.device
+    B, Hq, T, hd = q.shape
+    Hkv = k.shape[1]
+    dout = _attn_operand(dout.to(q.dtype), what, "grad")
+    dq = torch.empty((B, Hq, T, hd), dtype=torch.float32, device=dev)
+    dk = torch.empty((B, Hkv, T, hd), dtype=torch.float32, device=dev)
+    dv = torch.empty_like(dk)
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    ws = _lib.workspace(dev, L.fsi_sparse_attn_bwd_workspace_size(B, Hq, T, int(block)), stream)
+    err = _lib.error_word(dev)
+    st = L.fsi_sparse_attn_bwd(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), out.data_ptr(), out.stride(0), out.stride(1),
+        out.stride(2), dout.data_ptr(), dout.stride(0), dout.stride(1), dout.stride(2), B, Hq, Hkv, T, hd,
+        int(block), int(mode), int(window), _lib.ptr(lists), lists.stride(0) if cap else 0,
+        lists.stride(1) if cap else 0, cap, counts.data_ptr(), counts.stride(0), counts.stride(1), float(scale),
+        _lib.dtype_code(q.dtype, what), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(),
+        err.data_ptr(), stream)
+    _lib.check(st, what)
+    if _lib.checks_enabled():
+        _lib.raise_device_errors(dev, what)
+    return dq, dk, dv
+
+
+class _SparseAttnFn(torch.autograd.Function):
+    """sparse_attention with gradients for q, k and v.  The forward is the HIP
+    kernel; the backward is the HIP backward (fsi_sparse_attn_bwd): the block
+    map of the pattern, then per 64-query tile the row statistics and dQ, and
+    per 64-key tile dK and dV accumulated over the query tiles that reach it, in
+    fp32 on LDS tiles; memory O(T hd) plus (T / block)^2 block entries, never
+    the (T, T) scores the reference's masked SDPA materialises."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, lists, counts, cap, block, mode, window, scale):
+        out = _sparse_attn_op(q, k, v, lists, counts, cap, block, mode, window, scale)
+        ctx.save_for_backward(q, k, v, lists, counts, out)
+        ctx.meta = (cap, block, mode, window, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, lists, counts, out = ctx.saved_tensors
+        cap, block, mode, window, scale = ctx.meta
+        if q.shape[-1] <= 128:
+            dq, dk, dv = _sparse_attention_bwd(q, k, v, out, dout, lists, counts, cap, block, mode, window, scale)
+        else:  # head_dim 129..256: the LDS tiles do not fit; dense fp32 recompute over the pattern
+            dq, dk, dv = _sparse_attention_bwd_dense(q, k, v, dout, lists, counts, cap, block, mode, window, scale)
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None, None, None)
+
+
 def _sparse_logit_bias(lists, counts, cap, B, T, block, mode, window, dev):
     """(B, 1, T, T) additive logit bias of a sparse pattern: 0 for an allowed key
-    (log of its multiplicity for block lists), -inf elsewhere.  The dense form of
-    what the kernels walk, for the recompute in the backward (the reference
+    (log of its multiplicity for block lists), -inf elsewhere (the reference
     builds the same boolean mask, attention.py:148-176)."""
     nb = -(-T // block)
     mult = torch.zeros(B, nb, nb + 1, dtype=torch.float32, device=dev)  # last column: ids out of range
@@ -589,38 +643,23 @@ def _sparse_logit_bias(lists, counts, cap, B, T, block, mode, window, dev):
     return bias[:, None]
 
 
-class _SparseAttnFn(torch.autograd.Function):
-    """sparse_attention with gradients for q, k and v.  The forward is the HIP
-    kernel; the backward recomputes the attention densely in fp32 over the same
-    pattern (library matmuls and softmax, B x Hq x T x T memory, as the
-    reference's own masked SDPA) and differentiates it."""
-
-    @staticmethod
-    def forward(ctx, q, k, v, lists, counts, cap, block, mode, window, scale):
-        out = _sparse_attn_op(q, k, v, lists, counts, cap, block, mode, window, scale)
-        ctx.save_for_backward(q, k, v, lists, counts)
-        ctx.meta = (cap, block, mode, window, scale)
-        return out
-
-    @staticmethod
-    def backward(ctx, dout):
-        q, k, v, lists, counts = ctx.saved_tensors
-        cap, block, mode, window, scale = ctx.meta
-        B, Hq, T, hd = q.shape
-        G = Hq // k.shape[1]
-        bias = _sparse_logit_bias(lists, counts, cap, B, T, block, mode, window, q.device)
-        with torch.enable_grad():
-            qf = q.detach().float().requires_grad_()
-            kf = k.detach().float().requires_grad_()
-            vf = v.detach().float().requires_grad_()
-            ke = kf.repeat_interleave(G, dim=1)
-            ve = vf.repeat_interleave(G, dim=1)
-            s = torch.matmul(qf, ke.transpose(-1, -2).contiguous()) * scale + bias
-            empty = torch.isneginf(s).all(dim=-1, keepdim=True)  # rows with no key give 0
-            p = torch.softmax(s.masked_fill(empty, 0.0), dim=-1).masked_fill(empty, 0.0)
-            o = torch.matmul(p, ve)
-            dq, dk, dv = torch.autograd.grad(o, (qf, kf, vf), dout.float())
-        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None, None, None)
+def _sparse_attention_bwd_dense(q, k, v, dout, lists, counts, cap, block, mode, window, scale):
+    """Gradients of sparse_attention by a dense fp32 recompute over the pattern
+    (B x Hq x T x T memory) with library matmuls; only for head_dim > 128."""
+    B, Hq, T, hd = q.shape
+    G = Hq // k.shape[1]
+    bias = _sparse_logit_bias(lists, counts, cap, B, T, block, mode, window, q.device)
+    with torch.enable_grad():
+        qf = q.detach().float().requires_grad_()
+        kf = k.detach().float().requires_grad_()
+        vf = v.detach().float().requires_grad_()
+        ke = kf.repeat_interleave(G, dim=1)
+        ve = vf.repeat_interleave(G, dim=1)
+        s = torch.matmul(qf, ke.transpose(-1, -2).contiguous()) * scale + bias
+        empty = torch.isneginf(s).all(dim=-1, keepdim=True)  # rows with no key give 0
+        p = torch.softmax(s.masked_fill(empty, 0.0), dim=-1).masked_fill(empty, 0.0)
+        o = torch.matmul(p, ve)
+        return torch.autograd.grad(o, (qf, kf, vf), dout.float())
 
 
 def sparse_attention(

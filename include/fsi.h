@@ -479,6 +479,25 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
                             int64_t os_b, int64_t os_h, int64_t os_t, void* workspace, size_t workspace_bytes,
                             int* err, void* stream);
 
+/* Backward of fsi_sparse_attn (autograd of the masked SDPA of attention.py:211-218
+ * and of triton_ops.py:26-93): dq (B, Hq, T, head_dim), dk and dv (B, Hkv, T,
+ * head_dim), contiguous fp32, written, from q, k, v, the forward's out and dout
+ * (element strides as in fsi_sparse_attn, unit stride over head_dim) and the same
+ * pattern arguments.  fp32 math on 64 x 64 LDS tiles; no (T, T) tensor: the
+ * workspace (fsi_sparse_attn_bwd_workspace_size bytes) holds the counter area, a
+ * (B, ceil(T / block)^2) int32 block map and three fp32 (B, Hq, T) row
+ * statistics.  head_dim 1..128, dtype FSI_DTYPE_BF16 or FSI_DTYPE_F32. */
+FSI_API size_t fsi_sparse_attn_bwd_workspace_size(int64_t B, int64_t Hq, int64_t T, int64_t block);
+FSI_API int fsi_sparse_attn_bwd(const void* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, const void* k, int64_t ks_b,
+                                int64_t ks_h, int64_t ks_t, const void* v, int64_t vs_b, int64_t vs_h, int64_t vs_t,
+                                const void* out, int64_t os_b, int64_t os_h, int64_t os_t, const void* dout,
+                                int64_t ds_b, int64_t ds_h, int64_t ds_t, int64_t B, int64_t Hq, int64_t Hkv,
+                                int64_t T, int64_t head_dim, int64_t block, int mode, int64_t window,
+                                const int32_t* lists, int64_t ls_b, int64_t ls_q, int64_t capacity,
+                                const int32_t* counts, int64_t cs_b, int64_t cs_q, float scale, int dtype, float* dq,
+                                float* dk, float* dv, void* workspace, size_t workspace_bytes, int* err,
+                                void* stream);
+
 /* Fused 16-D block indexer + greedy block selection + block attention
  * (triton_fused_sram_indexer_attention, foveal_indexer/triton_ops.py:142-249,373-435).
  * q, k, v, out: contiguous (B, H, N, head_dim) of `dtype` (F32, BF16 or F16;

@@ -162,6 +162,11 @@ SIGNATURES: dict[str, tuple] = {
          _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr],
     ),
     "fsi_sparse_attn_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "fsi_decode_attn_bwd_q": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64,
+         _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         ctypes.c_float, _c_int, _c_ptr, _c_ptr, _c_ptr]),
     "fsi_sparse_attn_bwd_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "fsi_sparse_attn_bwd": (
         _c_int,

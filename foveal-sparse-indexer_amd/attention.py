@@ -421,23 +421,12 @@ def _decode_attention_launch(q3: Tensor, cache: FovealKVCache, pos_rows: Optiona
     return _decode_launch(q3, *args, out)
 
 
-def _decode_support(cache: FovealKVCache, b: int, pos: int, window: int, pages: List[int]):
-    """(K, V) of one sequence's support, (Hkv, n, hd), in the order the kernels and
-    the reference (attention.py:341-352) attend it."""
-    ls = max(0, pos + 1 - window)
-    toks = list(range(ls, pos + 1))
-    for p in pages:
-        toks.extend(range(p * cache.page_size, (p + 1) * cache.page_size))
-    idx = torch.tensor(toks, dtype=torch.long, device=cache.k_cache.device)
-    k, v = cache.to_dense(max(idx.max().item() + 1, 1) if toks else 1, batch=slice(b, b + 1))
-    return k[0].index_select(1, idx), v[0].index_select(1, idx)
-
-
 class _DecodeAttnFn(torch.autograd.Function):
     """Decode attention with a gradient for the query.  The cached keys and values
     are inference state (the kernels read them in place), so they are constants
-    here; the backward recomputes each sequence's softmax over its gathered
-    support in fp32: dq = scale * sum_t p_t (dO . v_t - dO . o) k_t."""
+    here; the backward (fsi_decode_attn_bwd_q) recomputes each sequence's softmax
+    over its support on the device in fp32, one wave per (sequence, query head):
+    dq = scale * sum_t p_t (dO . v_t - dO . o) k_t."""
 
     @staticmethod
     def forward(ctx, q3, cache, pos_rows, pos_val, window, remote_pages, remote_counts, cap, scale):
@@ -451,21 +440,28 @@ class _DecodeAttnFn(torch.autograd.Function):
         q3, pos_rows, remote_pages, remote_counts = ctx.saved_tensors
         cache = ctx.cache
         pos_val, window, cap, scale = ctx.meta
+        what = "decode_attention backward"
+        dev = q3.device
         B, Hq, hd = q3.shape
-        G = Hq // cache.num_kv_heads
-        dq = torch.empty_like(q3, dtype=torch.float32)
-        pos_list = pos_rows.tolist() if pos_rows is not None else [pos_val] * B
-        cnts = remote_counts.tolist() if cap else [0] * B
-        pages_all = remote_pages.tolist() if cap else [[] for _ in range(B)]
-        for b in range(B):
-            k, v = _decode_support(cache, b, int(pos_list[b]), window, pages_all[b][:max(0, min(cnts[b], cap))])
-            k = k.float().repeat_interleave(G, dim=0)  # (Hq, n, hd)
-            v = v.float().repeat_interleave(G, dim=0)
-            qb, gb = q3[b].float(), dout[b].float()
-            p = torch.softmax(torch.bmm(k, qb[:, :, None]).squeeze(-1) * scale, dim=-1)  # (Hq, n)
-            o = torch.bmm(p[:, None], v).squeeze(1)
-            dp = torch.bmm(v, gb[:, :, None]).squeeze(-1) - (gb * o).sum(-1, keepdim=True)
-            dq[b] = torch.bmm((p * dp)[:, None], k).squeeze(1) * scale
+        dq = torch.empty((B, Hq, hd), dtype=torch.float32, device=dev)
+        g = dout.reshape(B, Hq, hd).to(q3.dtype).contiguous()
+        q = q3.contiguous()
+        k, v = cache.k_cache, cache.v_cache
+        paged = cache.paged
+        ks = (0, 0, 0) if paged else (k.stride(0), k.stride(1), k.stride(2))
+        vs = (0, 0, 0) if paged else (v.stride(0), v.stride(1), v.stride(2))
+        L = _lib.lib()
+        err = _lib.error_word(dev)
+        st = L.fsi_decode_attn_bwd_q(
+            q.data_ptr(), g.data_ptr(), k.data_ptr(), v.data_ptr(), *ks, *vs, cache.max_seq_len,
+            cache.page_table.data_ptr() if paged else None, cache.max_pages, cache.n_phys_pages if paged else 0,
+            _lib.ptr(pos_rows), int(pos_val), int(window), cache.page_size,
+            _lib.ptr(remote_pages) if cap else None, _lib.ptr(remote_counts) if cap else None, int(cap), B, Hq,
+            cache.num_kv_heads, hd, float(scale), _lib.dtype_code(q3.dtype, what), dq.data_ptr(), err.data_ptr(),
+            _lib.stream_handle(dev))
+        _lib.check(st, what)
+        if _lib.checks_enabled():
+            _lib.raise_device_errors(dev, what)
         return dq.to(q3.dtype), None, None, None, None, None, None, None, None
 
 

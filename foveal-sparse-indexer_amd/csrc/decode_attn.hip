@@ -241,3 +241,272 @@ FSI_API int fsi_decode_attn_noalloc(const void* q, const void* k_pool, const voi
 }
 
 }  // extern "C"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Query gradient of decode attention (the cache is inference state, a
+// constant): dq_h = scale sum_t p_t (dout_h . v_t - dout_h . o_h) k_t over
+// each sequence's support (window tokens, then every token of each selected
+// page, as the forward attends it).  One wave per (sequence, query head), two
+// passes over the support in chunks of 64 tokens: the softmax statistics and
+// o, then dq.  Paged pools (bf16, page 64) are read through the page table in
+// their MFMA layouts; the contiguous reference-layout cache by its strides.
+// ---------------------------------------------------------------------------
+struct DecodeBwdParams {
+  const void* q;     // (B, Hq, hd) contiguous
+  const void* dout;  // (B, Hq, hd) contiguous
+  const void* k;
+  const void* v;
+  int64_t ks_b, ks_h, ks_t, vs_b, vs_h, vs_t;  // contiguous cache strides
+  const int32_t* page_table;                   // paged pools
+  int max_pages;
+  int64_t n_phys;
+  int S;  // tokens the contiguous cache holds
+  const int32_t* pos_rows;
+  int pos, window, page;
+  const int32_t* remote;
+  const int32_t* counts;
+  int cap;
+  int B, Hq, Hkv, hd;
+  float scale;
+  float* dq;  // (B, Hq, hd) fp32
+  int* err;
+};
+
+constexpr int DB_WAVES = 4;
+constexpr int DB_MAX_HD = 256;
+constexpr int DB_DPL = DB_MAX_HD / 64;
+
+template <typename T>
+__device__ __forceinline__ float db_ld(const T* p, int64_t i);
+template <>
+__device__ __forceinline__ float db_ld<float>(const float* p, int64_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float db_ld<bf16_t>(const bf16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+
+// Element d of key / value token `tok` (offsets per token computed once):
+// paged K: kb + (d / 32) * 64 * 32 + d % 32, V: vb + d * 32; contiguous: kb + d, vb + d.
+template <bool PAGED>
+__device__ __forceinline__ int64_t db_koff(int64_t kb, int d) {
+  return PAGED ? kb + (d >> 5) * (PAGE * CHUNK) + (d & 31) : kb + d;
+}
+template <bool PAGED>
+__device__ __forceinline__ int64_t db_voff(int64_t vb, int d) {
+  return PAGED ? vb + static_cast<int64_t>(d) * CHUNK : vb + d;
+}
+
+template <typename T, bool PAGED>
+__global__ __launch_bounds__(64 * DB_WAVES) void decode_bwd_q_kernel(DecodeBwdParams P) {
+  __shared__ float qs_all[DB_WAVES][DB_MAX_HD], gs_all[DB_WAVES][DB_MAX_HD];
+  __shared__ float ps_all[DB_WAVES][64];
+  __shared__ int64_t kb_all[DB_WAVES][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * DB_WAVES + w;  // (b, h)
+  if (row >= static_cast<int64_t>(P.B) * P.Hq) return;  // whole wave; no workgroup barrier follows
+  const int b = static_cast<int>(row / P.Hq), h = static_cast<int>(row % P.Hq);
+  const int g = h / (P.Hq / P.Hkv);
+  const T* q = static_cast<const T*>(P.q) + row * P.hd;
+  const T* go = static_cast<const T*>(P.dout) + row * P.hd;
+  for (int d = lane; d < P.hd; d += 64) {
+    qs_all[w][d] = db_ld<T>(q, d);
+    gs_all[w][d] = db_ld<T>(go, d);
+  }
+  __builtin_amdgcn_wave_barrier();
+  const T* kp = static_cast<const T*>(P.k);
+  const T* vp = static_cast<const T*>(P.v);
+  const int pos = P.pos_rows ? P.pos_rows[b] : P.pos;
+  const int ls = max(0, pos + 1 - P.window);
+  const int n_local = pos >= 0 ? pos - ls + 1 : 0;
+  int cnt = P.cap > 0 ? P.counts[b] : 0;
+  cnt = cnt < 0 ? 0 : (cnt > P.cap ? P.cap : cnt);
+  const int total = n_local + cnt * P.page;
+  bool bad = false;
+  // token i of the support -> (key offset, value offset), or -1 when skipped
+  auto locate = [&](int i, int64_t& kb, int64_t& vb) {
+    int tok = -1;
+    if (i < n_local) {
+      tok = ls + i;
+    } else if (i < total) {
+      const int j = (i - n_local) / P.page;
+      const int pg = P.remote[static_cast<int64_t>(b) * P.cap + j];
+      if (pg >= 0) tok = pg * P.page + (i - n_local) % P.page;
+    }
+    kb = vb = -1;
+    if (tok < 0) {
+      if (i < total) bad = true;
+      return;
+    }
+    if (PAGED) {
+      const int lp = tok / PAGE, off = tok % PAGE;
+      if (lp >= P.max_pages) {
+        bad = true;
+        return;
+      }
+      const int64_t phys = P.page_table[static_cast<int64_t>(b) * P.max_pages + lp];
+      if (phys < 0 || phys >= P.n_phys) {
+        bad = true;
+        return;
+      }
+      const int64_t base = (phys * P.Hkv + g) * PAGE * P.hd;
+      kb = base + off * CHUNK;
+      vb = base + (off / CHUNK) * P.hd * CHUNK + v_slot(off % CHUNK);
+    } else {
+      if (tok >= P.S) {
+        bad = true;
+        return;
+      }
+      kb = b * P.ks_b + g * P.ks_h + static_cast<int64_t>(tok) * P.ks_t;
+      vb = b * P.vs_b + g * P.vs_h + static_cast<int64_t>(tok) * P.vs_t;
+    }
+  };
+  auto score = [&](int64_t kb) {
+    float acc = 0.f;
+    for (int d = 0; d < P.hd; ++d) acc = fmaf(qs_all[w][d], db_ld<T>(kp, db_koff<PAGED>(kb, d)), acc);
+    return acc * P.scale;
+  };
+
+  // pass 1: m, l and o = sum p v (lanes over head dims for o)
+  float m = -INFINITY, l = 0.f;
+  float o[DB_DPL] = {0.f, 0.f, 0.f, 0.f};
+  for (int base = 0; base < total; base += 64) {
+    int64_t kb, vb;
+    locate(base + lane, kb, vb);
+    const float s = kb >= 0 ? score(kb) : -INFINITY;
+    const float cm = wave_max(s);
+    if (cm == -INFINITY) continue;
+    const float mn = fmaxf(m, cm);
+    const float alpha = m == -INFINITY ? 0.f : expf(m - mn);
+    const float p = kb >= 0 ? expf(s - mn) : 0.f;
+    l = l * alpha + wave_sum(p);
+    m = mn;
+    ps_all[w][lane] = p;
+    kb_all[w][lane] = vb;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int e = 0; e < DB_DPL; ++e) {
+      const int d = lane + 64 * e;
+      if (d >= P.hd) break;
+      float acc = o[e] * alpha;
+      for (int j = 0; j < 64; ++j) {
+        const int64_t r = kb_all[w][j];
+        if (r >= 0) acc = fmaf(ps_all[w][j], db_ld<T>(vp, db_voff<PAGED>(r, d)), acc);
+      }
+      o[e] = acc;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  float dd = 0.f;  // D = dout . o
+#pragma unroll
+  for (int e = 0; e < DB_DPL; ++e) {
+    const int d = lane + 64 * e;
+    if (d < P.hd) dd = fmaf(gs_all[w][d], l > 0.f ? o[e] / l : 0.f, dd);
+  }
+  dd = wave_sum(dd);
+
+  // pass 2: dq = scale sum_t p_t (dout . v_t - D) k_t (lanes over head dims)
+  float gq[DB_DPL] = {0.f, 0.f, 0.f, 0.f};
+  if (l > 0.f) {
+    for (int base = 0; base < total; base += 64) {
+      int64_t kb, vb;
+      locate(base + lane, kb, vb);
+      float ds = 0.f;
+      if (kb >= 0) {
+        const float p = expf(score(kb) - m) / l;
+        float dp = 0.f;
+        for (int d = 0; d < P.hd; ++d) dp = fmaf(gs_all[w][d], db_ld<T>(vp, db_voff<PAGED>(vb, d)), dp);
+        ds = p * (dp - dd);
+      }
+      ps_all[w][lane] = ds;
+      kb_all[w][lane] = kb;
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int e = 0; e < DB_DPL; ++e) {
+        const int d = lane + 64 * e;
+        if (d >= P.hd) break;
+        float acc = gq[e];
+        for (int j = 0; j < 64; ++j) {
+          const int64_t r = kb_all[w][j];
+          if (r >= 0) acc = fmaf(ps_all[w][j], db_ld<T>(kp, db_koff<PAGED>(r, d)), acc);
+        }
+        gq[e] = acc;
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  if (bad && P.err) set_error(P.err, FSI_ERR_INDEX_RANGE);
+#pragma unroll
+  for (int e = 0; e < DB_DPL; ++e) {
+    const int d = lane + 64 * e;
+    if (d < P.hd) P.dq[row * P.hd + d] = gq[e] * P.scale;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+FSI_API int fsi_decode_attn_bwd_q(const void* q, const void* dout, const void* k_cache, const void* v_cache,
+                                  int64_t ks_b, int64_t ks_h, int64_t ks_t, int64_t vs_b, int64_t vs_h, int64_t vs_t,
+                                  int64_t max_seq, const int32_t* page_table, int64_t max_pages, int64_t n_phys_pages,
+                                  const int32_t* pos_rows, int64_t pos, int64_t window, int64_t page_size,
+                                  const int32_t* remote_pages, const int32_t* remote_counts, int64_t capacity,
+                                  int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale, int dtype,
+                                  float* dq, int* err, void* stream) {
+  using namespace fsi_host;
+  FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "decode_attn_bwd_q: dtype %d",
+                dtype);
+  FSI_CHECK_ARG(head_dim > 0 && head_dim <= DB_MAX_HD, FSI_ERR_SHAPE, "decode_attn_bwd_q: head_dim %lld (1..%d)",
+                (long long)head_dim, DB_MAX_HD);
+  FSI_CHECK_ARG(B >= 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && window >= 0 && capacity >= 0 && page_size > 0,
+                FSI_ERR_SHAPE, "decode_attn_bwd_q: bad sizes");
+  const bool paged = page_table != nullptr;
+  FSI_CHECK_ARG(!paged || (dtype == FSI_DTYPE_BF16 && page_size == PAGE && (head_dim == 64 || head_dim == 128) &&
+                           max_pages > 0 && n_phys_pages > 0),
+                FSI_ERR_SHAPE, "decode_attn_bwd_q: paged pools hold bf16 pages of 64 tokens, head_dim 64 or 128");
+  FSI_CHECK_ARG(paged || (max_seq > 0 && max_seq <= 0x7fffffff), FSI_ERR_SHAPE, "decode_attn_bwd_q: max_seq");
+  FSI_CHECK_ARG(B * Hq <= (int64_t)0x7fffffff && (paged ? max_pages * PAGE : max_seq) <= 0x7fffffff, FSI_ERR_SHAPE,
+                "decode_attn_bwd_q: sizes beyond int32");
+  if (B == 0) return FSI_OK;
+  FSI_CHECK_ARG(q && dout && k_cache && v_cache && dq, FSI_ERR_INVALID_ARG, "decode_attn_bwd_q: null pointer");
+  FSI_CHECK_ARG(capacity == 0 || (remote_pages && remote_counts), FSI_ERR_INVALID_ARG,
+                "decode_attn_bwd_q: remote page list or counts missing");
+  DecodeBwdParams P{};
+  P.q = q;
+  P.dout = dout;
+  P.k = k_cache;
+  P.v = v_cache;
+  P.ks_b = ks_b;
+  P.ks_h = ks_h;
+  P.ks_t = ks_t;
+  P.vs_b = vs_b;
+  P.vs_h = vs_h;
+  P.vs_t = vs_t;
+  P.page_table = page_table;
+  P.max_pages = (int)max_pages;
+  P.n_phys = n_phys_pages;
+  P.S = (int)max_seq;
+  P.pos_rows = pos_rows;
+  P.pos = (int)pos;
+  P.window = (int)(window < 0x7fffffff ? window : 0x7fffffff);
+  P.page = (int)page_size;
+  P.remote = remote_pages;
+  P.counts = remote_counts;
+  P.cap = (int)capacity;
+  P.B = (int)B;
+  P.Hq = (int)Hq;
+  P.Hkv = (int)Hkv;
+  P.hd = (int)head_dim;
+  P.scale = scale;
+  P.dq = dq;
+  P.err = err;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned grid = static_cast<unsigned>((B * Hq + DB_WAVES - 1) / DB_WAVES);
+  if (paged) decode_bwd_q_kernel<bf16_t, true><<<grid, 64 * DB_WAVES, 0, st>>>(P);
+  else if (dtype == FSI_DTYPE_F32) decode_bwd_q_kernel<float, false><<<grid, 64 * DB_WAVES, 0, st>>>(P);
+  else decode_bwd_q_kernel<bf16_t, false><<<grid, 64 * DB_WAVES, 0, st>>>(P);
+  FSI_HIP_LAUNCH_CHECK("decode_attn_bwd_q");
+  return FSI_OK;
+}
+
+}  // extern "C"

@@ -439,6 +439,22 @@ FSI_API int fsi_decode_attn_noalloc(const void* q, const void* k_pool, const voi
                                     int64_t capacity, int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim,
                                     float scale, void* out, int* err, void* stream);
 
+/* Query gradient of decode attention (autograd of attention.py:339-367 in q;
+ * the cache is a constant): dq = scale sum_t p_t (dout . v_t - dout . o) k_t over
+ * each sequence's support, fp32 math, written to dq (B, Hq, head_dim) fp32.  q,
+ * dout: contiguous (B, Hq, head_dim) of dtype.  With page_table (paged bf16
+ * pools of fsi_decode_attn: page 64, head_dim 64 or 128) the pools are read
+ * through it; without, k_cache / v_cache are the contiguous (B, Hkv, max_seq,
+ * head_dim) cache given by element strides (any page_size, head_dim <= 256).
+ * Other arguments as fsi_decode_attn / fsi_decode_attn_dense. */
+FSI_API int fsi_decode_attn_bwd_q(const void* q, const void* dout, const void* k_cache, const void* v_cache,
+                                  int64_t ks_b, int64_t ks_h, int64_t ks_t, int64_t vs_b, int64_t vs_h, int64_t vs_t,
+                                  int64_t max_seq, const int32_t* page_table, int64_t max_pages, int64_t n_phys_pages,
+                                  const int32_t* pos_rows, int64_t pos, int64_t window, int64_t page_size,
+                                  const int32_t* remote_pages, const int32_t* remote_counts, int64_t capacity,
+                                  int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale, int dtype,
+                                  float* dq, int* err, void* stream);
+
 /* ------------------------------------------------------------------------- *
  * Block-sparse prefill attention (bf16 in, fp32 softmax and accumulate, bf16 out).
  * q: (B, Hq, T, head_dim), k and v: (B, Hkv, T, head_dim), out: (B, Hq, T,

@@ -224,6 +224,48 @@ def test_decode_attention_per_sequence_positions(fsi, dev):
     assert Pt.rel_l2(out.float(), ref.float()) <= TOL
 
 
+@pytest.mark.parametrize("layout", ["paged_bf16", "dense_f32", "dense_bf16_page16"])
+def test_decode_attention_query_gradient(fsi, dev, layout):
+    """dq of decode_attention on the device (fsi_decode_attn_bwd_q) against fp64
+    autograd of softmax attention over the same support (window tokens then the
+    selected pages), per-sequence positions, one sequence without pages: fp32
+    rel-L2 2e-5, bf16 1e-2."""
+    B, Hq, Hkv, hd, S = 3, 8, 2, 64, 512
+    dtype = torch.float32 if layout == "dense_f32" else torch.bfloat16
+    page = 16 if layout.endswith("page16") else 64
+    g = torch.Generator().manual_seed(31)
+    k = torch.randn(B, Hkv, S, hd, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, S, hd, generator=g).to(dtype)
+    if layout == "paged_bf16":
+        n_phys = B * (S // 64) + 2
+        table = torch.randperm(n_phys, generator=g)[:B * (S // 64)].view(B, S // 64).to(torch.int32)
+        c = fsi.FovealKVCache(B, S, Hkv, hd, 16, 64, dev, dtype, n_phys_pages=n_phys, page_table=table)
+    else:
+        c = fsi.FovealKVCache(B, S, Hkv, hd, 16, page, dev, dtype, paged=False)
+    assert c.paged == (layout == "paged_bf16")
+    c.load_dense(k.to(dev), v.to(dev))
+    q = torch.randn(B, Hq, hd, generator=g).to(dtype)
+    dout = torch.randn(B, Hq, hd, generator=g).to(dtype)
+    pos = [S - 1, 300, 40]
+    pages = [[0, 2], [1], []]
+    cap = 2
+    rp = torch.full((B, cap), -1, dtype=torch.int32)
+    for b, p in enumerate(pages):
+        rp[b, :len(p)] = torch.tensor(p, dtype=torch.int32)
+    cnt = torch.tensor([len(p) for p in pages], dtype=torch.int32)
+    W, scale = 100, hd ** -0.5
+    qd = q.to(dev).requires_grad_()
+    out = fsi.decode_attention(qd, c, pos=torch.tensor(pos).to(dev), window=W, remote_pages=rp.to(dev),
+                               remote_counts=cnt.to(dev), scale=scale)
+    out.backward(dout.to(dev))
+    q64 = q.double().requires_grad_()
+    ref = A.decode_attention_f64(q64, k, v, pos, W, pages, page, scale)
+    ref.backward(dout.double())
+    tol = 2e-5 if dtype == torch.float32 else 1e-2
+    assert qd.grad.dtype == dtype
+    assert Pt.rel_l2(qd.grad.cpu().float(), q64.grad.float()) <= tol
+
+
 def test_decode_attention_invalid_page_reported(fsi, dev, monkeypatch):
     c, k, v = _cache(fsi, dev, 1, 1, 64, 256, seed=3)
     q = torch.randn(1, 1, 64).bfloat16().to(dev)

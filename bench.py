@@ -547,31 +547,8 @@ def bench_teacher_targets(fsi, args, dev):
                   "synthetic (seeded N(0,1) hidden states, N(0,0.02) gate/up/down weights)",
                   {"workload": "compute_teacher_dense_block_targets per layer: h (4096, 4096), gate/up (14336, 4096), "
                                "down (4096, 14336), block 64 (224 blocks), T = 1"})
-    # the backward (fsi_sparse_attn_bwd, training through FovealSparseAttention.forward)
-    # on the same pattern, timed eagerly: 2.5 x the forward's products (Q K^T and dP
-    # recomputed, dV, dQ, dK), fp32 arithmetic
-    from foveal_sparse_indexer_amd import attention as fatt
-
-    out4 = out.transpose(1, 2)
-    g = torch.Generator(device=dev).manual_seed(5)
-    dout = torch.randn(B, HQ, T, HD, device=dev, generator=g).bfloat16()
-    for _ in range(2):
-        fatt._sparse_attention_bwd(q, k, v, out4, dout, lists, counts, c["KMAX"], PAGE, 0, W, scale)
-    torch.cuda.synchronize(dev)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n_bwd = 3
-    ev0.record()
-    for _ in range(n_bwd):
-        fatt._sparse_attention_bwd(q, k, v, out4, dout, lists, counts, c["KMAX"], PAGE, 0, W, scale)
-    ev1.record()
-    torch.cuda.synchronize(dev)
-    bwd_ms = ev0.elapsed_time(ev1) / n_bwd
-    bwd_tf = 2.5 * flops / (bwd_ms * 1e-3) / 1e12
-    res["backward"] = {"ms": round(bwd_ms, 3), "tflops": round(bwd_tf, 1), "fp32_frac": round(bwd_tf / FP32_PEAK_TFLOPS, 4),
-                       "flops": int(2.5 * flops), "kernel": "sab_map + sab_q (statistics, dQ) + sab_kv (dK, dV)",
-                       "note": "fp32 VALU on 64 x 64 LDS tiles; memory O(T hd), no (T, T) tensor"}
     res["roofline"] = {"bound": "mfma", "achieved": round(tfs, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                       "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": PREFILL_ATTN_TRAFFIC_BYTES,
+                       "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": None,
                        "kernel": "bsgemm_dma_kernel<N_DUAL, K_DENSE, EPI_ENERGY> (+ column_sumsq_kernel, "
                                  "column_norms_kernel, block_mean_kernel, block_softmax_kernel: 5 launches)",
                        "flops_per_launch": flops}

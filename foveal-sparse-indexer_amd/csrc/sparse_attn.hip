@@ -437,12 +437,16 @@ __device__ __forceinline__ f32x4_t mfma16x16x32_f16(const u32x4_t& a, const u32x
 #ifndef FSI_SAL_QT
 #define FSI_SAL_QT 2
 #endif
+#ifndef FSI_SAL_AHEAD
+#define FSI_SAL_AHEAD 2
+#endif
 constexpr int SAL_QT = FSI_SAL_QT;           // query tiles per wave
 constexpr int SAL_HALVES = 4 / SAL_QT;       // waves per query head (64 queries split)
 constexpr int SAL_WAVES = 4 * SAL_HALVES;    // 4 query heads per workgroup
-constexpr int SAL_MAX_CAP = 64;  // listed pages per query block
-constexpr int SAL_AHEAD = 3;     // chunks in flight ahead of the one computed
-constexpr int SAL_STAGES = SAL_AHEAD + 1;
+constexpr int SAL_MAX_CAP = 64;              // listed pages per query block
+constexpr int SAL_AHEAD = FSI_SAL_AHEAD;     // 64-key stages in flight ahead of the one computed
+constexpr int SAL_RING = SAL_AHEAD + 1;      // 64-key pairs held by the LDS ring
+constexpr int SAL_SLOTS = 2 * SAL_RING;       // 32-key chunk slots of the LDS ring
 typedef __attribute__((address_space(3))) void sal_lds_t;
 typedef __attribute__((address_space(1))) void sal_glb_t;
 
@@ -451,6 +455,23 @@ __device__ __forceinline__ void sal_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 __device__ __forceinline__ void sal_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// Keeps the compiler's scheduler from moving instructions across this point: the
+// fragment reads issued before it stay ahead of the MFMAs / softmax after it.
+#ifndef FSI_SAL_PF
+#define FSI_SAL_PF 1
+#endif
+__device__ __forceinline__ void sal_order() {
+#if FSI_SAL_PF
+  __builtin_amdgcn_sched_barrier(0);
+#endif
+}
+
+// Largest of 8 values with v_max3_f32 (4 instructions).
+__device__ __forceinline__ float sal_max8(const float* v) {
+  return __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(v[0], v[1]), v[2]),
+                         __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(v[3], v[4]), v[5]),
+                                         __builtin_fmaxf(__builtin_fmaxf(v[6], v[7]), -INFINITY)));
+}
 
 template <int HD>
 __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParams P) {
@@ -459,18 +480,19 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   constexpr int KROW = HD * 2;                  // bytes of one key row
   constexpr int KBYTES = SA_CHUNK * KROW;       // K rows of a chunk
   constexpr int VBYTES = HD * SA_CHUNK * 2;     // V^T of a chunk: HD rows of 64 B
-  constexpr int STAGE = KBYTES + VBYTES;
-  constexpr int LOADS = STAGE / 1024;           // 1 KiB direct loads per chunk
+  constexpr int SLOT = KBYTES + VBYTES;         // one 32-key chunk in LDS
+  constexpr int LOADS = SLOT / 1024;            // 1 KiB direct loads per chunk
   constexpr int LPW = LOADS / SAL_WAVES;        // per wave
-  static_assert(LOADS % SAL_WAVES == 0, "chunk loads must split over the waves");
+  static_assert(LPW >= 1 && LOADS % SAL_WAVES == 0, "chunk loads must split over the waves");
+  static_assert(KBYTES % (1024 * LPW) == 0, "a wave's loads of a chunk are all K or all V^T");
   constexpr int KPR = KROW / 16;                // 16-byte pieces per key row
   // One LDS array holds the chunk ring and the block list.  Separate __shared__
   // arrays would get alias scopes, and the compiler would then make every ring
   // read wait for all direct loads in flight (vmcnt(0)), including the chunks
   // issued ahead; with one array the explicit waits below order the ring.
-  __shared__ __attribute__((aligned(1024))) char smem[SAL_STAGES * STAGE + SAL_MAX_CAP * 4];
-  char (*ring)[STAGE] = reinterpret_cast<char (*)[STAGE]>(smem);
-  int* wl = reinterpret_cast<int*>(smem + SAL_STAGES * STAGE);
+  __shared__ __attribute__((aligned(1024))) char smem[SAL_SLOTS * SLOT + SAL_MAX_CAP * 4];
+  char (*ring)[SLOT] = reinterpret_cast<char (*)[SLOT]>(smem);
+  int* wl = reinterpret_cast<int*>(smem + SAL_SLOTS * SLOT);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -489,6 +511,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   const int r = lane & 15, grp = lane >> 4;
   const int qb = qblk0 / P.block;
   const float vscale = __builtin_ldexpf(1.f, P.head_e[b * P.Hkv + g]);  // undoes the fp16 copy's 2^-e
+  const float sl2 = P.scale_log2, inv_sl2 = 1.f / P.scale_log2;
 
   // ---- listed pages: validity, first-listing de-duplication, compaction ----
   int cnt = P.counts[b * P.cs_b + qb * P.cs_q];
@@ -509,78 +532,87 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   if (wave == 0 && okl) wl[__popcll(vmask & ((uint64_t(1) << lane) - 1))] = myblk;
   const int n_remote = __popcll(vmask);
 
-  int n_local = 0, c_lo = 0;
+  // local window chunks [c_lo, c_hi], walked in 64-key pairs from the even chunk c_lo2
+  int n_lp = 0, c_lo = 0, c_hi = -1, c_lo2 = 0;
   if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
     const int klo = qblk0 - P.window + 1 > 0 ? qblk0 - P.window + 1 : 0;
     const int khi = qblk0 + 63 < P.T - 1 ? qblk0 + 63 : P.T - 1;
     c_lo = klo / SA_CHUNK;
-    n_local = khi / SA_CHUNK - c_lo + 1;
+    c_hi = khi / SA_CHUNK;
+    c_lo2 = c_lo & ~1;
+    n_lp = (c_hi - c_lo2) / 2 + 1;
   }
-  const int per_block = P.block / SA_CHUNK;  // a power of two (host-checked)
-  const int pb_shift = __builtin_ctz(per_block);
-  const int n_chunks = n_local + n_remote * per_block;
+  const int pp_block = P.block / (2 * SA_CHUNK);  // 64-key pairs per page, a power of two (host-checked)
+  const int pp_shift = __builtin_ctz(pp_block);
+  const int n_pairs = n_lp + n_remote * pp_block;
   __syncthreads();  // wl is written
-  // Each wave keeps the page list in a register (lane i holds entry i) and reads it
-  // with v_readlane: an LDS read inside the chunk loop would make the compiler wait
-  // for every direct-to-LDS chunk load in flight before the loop's LDS reads.
-  const int wl_reg = wl[lane < SAL_MAX_CAP ? lane : 0];
+  // Each wave keeps, per listed page (lane i: entry i), the page's first chunk and
+  // its number of keys inside the sequence, and reads them with v_readlane: an LDS
+  // read inside the loop would make the compiler wait for every direct-to-LDS
+  // chunk load in flight before the loop's LDS reads.
+  const int blk_j = lane < n_remote ? wl[lane] : 0;
+  const int pg_c0 = blk_j * (P.block / SA_CHUNK);
+  const int pg_len = P.T - blk_j * P.block < P.block ? P.T - blk_j * P.block : P.block;
 
-  // chunk i: absolute chunk c, keys [0, hi) of it, local-window chunk or page chunk
-  auto describe = [&](int i, int& c, int& hi, bool& local) {
-    if (i < n_local) {
-      c = c_lo + i;
-      hi = SA_CHUNK;
+  // pair p: chunks c0 and c0 + 1, of which keys [0, hi0) and [0, hi1) are taken
+  // (local pairs take whole chunks; keys past the sequence are masked)
+  auto describe = [&](int p, int& c0, int& hi0, int& hi1, bool& local) {
+    if (p < n_lp) {
+      c0 = c_lo2 + 2 * p;
+      hi0 = c0 >= c_lo ? SA_CHUNK : 0;
+      hi1 = c0 + 1 <= c_hi ? SA_CHUNK : 0;
       local = true;
     } else {
-      const int j = i - n_local;
-      const int blk = __builtin_amdgcn_readlane(wl_reg, j >> pb_shift);
-      const int k0 = blk * P.block;
-      const int k1 = k0 + P.block < P.T ? k0 + P.block : P.T;
-      c = k0 / SA_CHUNK + (j & (per_block - 1));
-      hi = k1 - c * SA_CHUNK;
-      hi = hi > SA_CHUNK ? SA_CHUNK : hi;
-      if (hi <= 0) {  // past the end of the sequence: load the page's first chunk, use nothing
-        c = k0 / SA_CHUNK;
-        hi = 0;
-      }
+      const int j = p - n_lp;
+      const int pg = j >> pp_shift, sub = j & (pp_block - 1);
+      c0 = __builtin_amdgcn_readlane(pg_c0, pg) + 2 * sub;
+      const int len = __builtin_amdgcn_readlane(pg_len, pg) - 2 * SA_CHUNK * sub;
+      hi0 = len <= 0 ? 0 : (len > SA_CHUNK ? SA_CHUNK : len);
+      hi1 = len <= SA_CHUNK ? 0 : (len > 2 * SA_CHUNK ? SA_CHUNK : len - SA_CHUNK);
       local = false;
     }
   };
 
-  // ---- direct loads of chunk c into stage st: this wave's LPW KiB of it ----
-  const bf16_t* kbase = P.k + b * P.ks_b + g * P.ks_h;
-  const bf16_t* vtbase = P.vt + (static_cast<int64_t>(b) * P.Hkv + g) * P.n32 * HD * SA_CHUNK;
-  // Per-lane parts of the addresses, fixed for the whole kernel: load i of this
-  // wave is K row krow[i] / 16-byte piece, or V^T row / piece of the chunk.
-  int64_t loff[LPW];
+  // ---- direct loads of chunk c into ring slot sl: this wave's LPW KiB of it ----
+  const char* kbase = reinterpret_cast<const char*>(P.k + b * P.ks_b + g * P.ks_h);
+  const char* vtbase =
+      reinterpret_cast<const char*>(P.vt + (static_cast<int64_t>(b) * P.Hkv + g) * P.n32 * HD * SA_CHUNK);
+  // Per-lane byte offsets, fixed for the whole kernel: load i of this wave is K
+  // row krow[i] / 16-byte piece, or V^T row / piece of the chunk.  Whether a load
+  // is K or V^T depends on the wave only, so the base pointer is scalar.
+  const bool wave_k = wave * LPW * 1024 < KBYTES;
+  uint32_t loff[LPW];
   int krow[LPW];
-  bool isk[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
-    const int inst = wave * LPW + i;
-    const int off = inst * 1024 + lane * 16;  // byte offset in the stage
-    isk[i] = off < KBYTES;
-    if (isk[i]) {
+    const int off = (wave * LPW + i) * 1024 + lane * 16;  // byte offset in the slot
+    if (wave_k) {
       const int row = off / KROW, slot = (off % KROW) / 16;  // key row, 16-byte slot
       krow[i] = row;
-      loff[i] = static_cast<int64_t>(row) * P.ks_t + 8 * (slot ^ (row & (KPR - 1) & 15));
+      loff[i] = static_cast<uint32_t>(row * P.ks_t * 2 + 16 * (slot ^ (row & (KPR - 1) & 15)));
     } else {
       const int vo = off - KBYTES;
       const int row = vo / 64, slot = (vo % 64) / 16;  // V^T row (dim), 16-byte slot
       krow[i] = 0;
-      loff[i] = row * SA_CHUNK + 8 * (slot ^ ((row >> 2) & 3));
+      loff[i] = static_cast<uint32_t>(row * SA_CHUNK * 2 + 16 * (slot ^ ((row >> 1) & 3)));
     }
   }
-  auto issue = [&](int c, int st) {
-    const bf16_t* kc = kbase + static_cast<int64_t>(c) * SA_CHUNK * P.ks_t;
-    const bf16_t* vc = vtbase + static_cast<int64_t>(c) * HD * SA_CHUNK;
-    const bool tail = (c + 1) * SA_CHUNK > P.T;  // uniform: rows past T read row T - 1
+  auto issue = [&](int c, int sl) {
+    c = c < P.n32 - 1 ? c : P.n32 - 1;  // an empty chunk past the sequence loads the last one
+    const char* base = wave_k ? kbase + static_cast<int64_t>(c) * SA_CHUNK * P.ks_t * 2
+                              : vtbase + static_cast<int64_t>(c) * HD * SA_CHUNK * 2;
+    sal_lds_t* dst = (sal_lds_t*)(&ring[sl][wave * LPW * 1024]);
+    if (!wave_k || (c + 1) * SA_CHUNK <= P.T) {
 #pragma unroll
-    for (int i = 0; i < LPW; ++i) {
-      const bf16_t* src = isk[i] ? kc + loff[i] : vc + loff[i];
-      if (tail && isk[i] && c * SA_CHUNK + krow[i] >= P.T)
-        src = kbase + static_cast<int64_t>(P.T - 1) * P.ks_t + (loff[i] - static_cast<int64_t>(krow[i]) * P.ks_t);
-      __builtin_amdgcn_global_load_lds((sal_glb_t*)src, (sal_lds_t*)(&ring[st][(wave * LPW + i) * 1024]), 16, 0, 0);
+      for (int i = 0; i < LPW; ++i)
+        __builtin_amdgcn_global_load_lds((sal_glb_t*)(base + loff[i]), (sal_lds_t*)((char __attribute__((address_space(3)))*)dst + i * 1024), 16, 0, 0);
+    } else {  // the sequence's last chunk: rows past T read row T - 1
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) {
+        const int row = c * SA_CHUNK + krow[i] < P.T ? krow[i] : P.T - 1 - c * SA_CHUNK;
+        const char* src = base + loff[i] + static_cast<int64_t>(row - krow[i]) * P.ks_t * 2;
+        __builtin_amdgcn_global_load_lds((sal_glb_t*)src, (sal_lds_t*)((char __attribute__((address_space(3)))*)dst + i * 1024), 16, 0, 0);
+      }
     }
   };
 
@@ -599,13 +631,15 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   // Softmax denominators come out of one more MFMA per query tile, against an
   // all-ones fp16 A operand: every row of lsum[qt] is the sum of the same fp16 P
   // the P V product uses, so the rounding of P (toward zero) leaves no bias.
+  // The running max (log2 units) starts at a finite -1e30: the first valid score
+  // passes its threshold, and masked scores (-inf) give p = 0 without a special case.
   float m_run[SAL_QT], m_thr[SAL_QT];  // m_thr: raw score whose log2-scaled value is m_run + 8
   f32x4_t lsum[SAL_QT];
   const u32x4_t ones = u32x4_t{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
 #pragma unroll
   for (int qt = 0; qt < SAL_QT; ++qt) {
-    m_run[qt] = -INFINITY;
-    m_thr[qt] = -INFINITY;
+    m_run[qt] = -1e30f;
+    m_thr[qt] = (-1e30f + 8.f) * inv_sl2;
     lsum[qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < DT; ++i) acc[qt][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -614,129 +648,132 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
   // the Q loads above are this wave's only other vector loads: let them land
   // before the ring's vmcnt accounting starts
   sal_wait_vmcnt<0>();
-  for (int i = 0; i < SAL_AHEAD; ++i) {
-    if (i >= n_chunks) break;
-    int c, hi;
+  for (int p = 0; p < SAL_AHEAD; ++p) {
+    if (p >= n_pairs) break;
+    int c0, hi0, hi1;
     bool lc;
-    describe(i, c, hi, lc);
-    issue(c, i % SAL_STAGES);
+    describe(p, c0, hi0, hi1, lc);
+    issue(c0, 2 * p);
+    issue(c0 + 1, 2 * p + 1);
   }
 
-  for (int i = 0; i < n_chunks; ++i) {
-    // chunk i landed: at most the loads of chunks i + 1 .. i + AHEAD - 1 remain
-    const int later = (i + SAL_AHEAD - 1 < n_chunks - 1 ? i + SAL_AHEAD - 1 : n_chunks - 1) - i;
-    if (later >= 2) sal_wait_vmcnt<2 * LPW>();
-    else if (later == 1) sal_wait_vmcnt<LPW>();
-    else sal_wait_vmcnt<0>();
-    sal_barrier();
-    if (i + SAL_AHEAD < n_chunks) {  // into the stage chunk i - 1 used
-      int c, hi;
-      bool lc;
-      describe(i + SAL_AHEAD, c, hi, lc);
-      issue(c, (i + SAL_AHEAD) % SAL_STAGES);
+  // Scores of pair p (its slots sl, sl + 1) into st.
+  f32x4_t st[2][SAL_QT][2];
+  auto scores = [&](int sl) {
+    // K fragments of both chunks, all read before the first MFMA (the LDS latency
+    // is paid once per pair): lane (r, grp) reads key 16 tile + r, dims 32 ks + 8 grp .. +8
+    u32x4_t kf[2][2 * KS];
+#pragma unroll
+    for (int hc = 0; hc < 2; ++hc)
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int row = 16 * tile + r;
+          kf[hc][tile * KS + ks] = *reinterpret_cast<const u32x4_t*>(
+              ring[sl + hc] + row * KROW + 16 * ((4 * ks + grp) ^ (row & (KPR - 1) & 15)));
+        }
+    sal_order();
+    // query tile by query tile, so the softmax of the first can start while the
+    // MFMAs of the second run
+#pragma unroll
+    for (int qt = 0; qt < SAL_QT; ++qt) {
+#pragma unroll
+      for (int hc = 0; hc < 2; ++hc) st[hc][qt][0] = st[hc][qt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int hc = 0; hc < 2; ++hc)
+#pragma unroll
+          for (int tile = 0; tile < 2; ++tile)
+            st[hc][qt][tile] = mfma16x16x32(kf[hc][tile * KS + ks], qreg[qt][ks], st[hc][qt][tile]);
     }
-    int c, hi;
-    bool local;
-    describe(i, c, hi, local);
-    if (hi <= 0 || !head_live) continue;  // uniform: an empty chunk or an idle wave
-    const char* stg = ring[i % SAL_STAGES];
-    // K fragments: lane (r, grp) reads key 16 tile + r, dims 32 ks + 8 grp .. +8
-    u32x4_t kf[2 * KS];
+  };
+
+  // Softmax of the scores in st and the P V products of the pair in slots sl,
+  // sl + 1 (chunks c0, c0 + 1 with keys [0, hi0), [0, hi1) taken).
+  auto finish = [&](int sl, int c0, int hi0, int hi1, bool local) {
+    const int kc0 = c0 * SA_CHUNK;
+    // V^T fragments of both chunks, read ahead of the softmax so their LDS latency
+    // hides under it: lane (r, grp) reads dim 16 dt + r, slots 8 grp .. +8
+    u32x4_t vf[2][DT];
 #pragma unroll
-    for (int tile = 0; tile < 2; ++tile)
+    for (int hc = 0; hc < 2; ++hc)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int row = 16 * tile + r;
-        kf[tile * KS + ks] = *reinterpret_cast<const u32x4_t*>(
-            stg + row * KROW + 16 * ((4 * ks + grp) ^ (row & (KPR - 1) & 15)));
+      for (int dt = 0; dt < DT; ++dt) {
+        const int row = 16 * dt + r;
+        vf[hc][dt] = *reinterpret_cast<const u32x4_t*>(ring[sl + hc] + KBYTES + row * 64 + 16 * (grp ^ ((row >> 1) & 3)));
       }
-    // V^T fragments: lane (r, grp) reads dim 16 dt + r, slots 8 grp .. +8
-    u32x4_t vf[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int row = 16 * dt + r;
-      vf[dt] = *reinterpret_cast<const u32x4_t*>(stg + KBYTES + row * 64 + 16 * (grp ^ ((row >> 2) & 3)));
-    }
-    const int kc0 = c * SA_CHUNK;
-    // phase 1: S^T tiles of the 4 query tiles (8 independent accumulator chains)
-    f32x4_t st[SAL_QT][2];
-#pragma unroll
-    for (int qt = 0; qt < SAL_QT; ++qt) st[qt][0] = st[qt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int qt = 0; qt < SAL_QT; ++qt) {
-#pragma unroll
-        for (int tile = 0; tile < 2; ++tile)
-          st[qt][tile] = mfma16x16x32(kf[tile * KS + ks], qreg[qt][ks], st[qt][tile]);
-      }
-    // phase 2: online softmax of the 4 query tiles.  Chunks whose keys every
-    // query of the wave sees (inside all windows, or a page wholly before them)
-    // skip the per-key mask.
-    const bool nomask = local ? (kc0 + SA_CHUNK - 1 <= q0 && kc0 > q0 + 16 * SAL_QT - 1 - P.window &&
-                                 kc0 + SA_CHUNK <= P.T)
-                              : (hi == SA_CHUNK && kc0 + SA_CHUNK - 1 <= q0 - P.window);
+    sal_order();
+    // Pairs whose keys every query of the wave sees (inside all windows, or a page
+    // wholly before them) skip the per-key mask.
+    const bool full = hi0 == SA_CHUNK && hi1 == SA_CHUNK;
+    const bool nomask =
+        full && (local ? (kc0 + 2 * SA_CHUNK - 1 <= q0 && kc0 > q0 + 16 * SAL_QT - 1 - P.window &&
+                          kc0 + 2 * SA_CHUNK <= P.T)
+                       : (P.mode != FSI_SATTN_LOCAL_REMOTE || kc0 + 2 * SA_CHUNK - 1 <= q0 - P.window));
     float alpha[SAL_QT];
-    u32x4_t pb[SAL_QT];
+    u32x4_t pb[2][SAL_QT];
 #pragma unroll
     for (int qt = 0; qt < SAL_QT; ++qt) {
       const int myq = q0 + 16 * qt + r;
-      float sv[8];  // raw scores, -inf where masked
-      if (nomask) {
+      float sv[16];  // raw scores of chunk hc, key tile t, row j at 8 hc + 4 t + j; -inf where masked
+#pragma unroll
+      for (int hc = 0; hc < 2; ++hc)
 #pragma unroll
         for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) sv[tile * 4 + j] = st[qt][tile][j];
-      } else {
+          for (int j = 0; j < 4; ++j) sv[8 * hc + 4 * tile + j] = st[hc][qt][tile][j];
+      if (!nomask) {
 #pragma unroll
-        for (int tile = 0; tile < 2; ++tile)
+        for (int hc = 0; hc < 2; ++hc)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int tau = 16 * tile + 4 * grp + j;
-            const int key = kc0 + tau;
-            bool ok = tau < hi && key < P.T;
-            if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
-              const bool in_win = key <= myq && key > myq - P.window;
-              ok = ok && (local ? in_win : !in_win);
+          for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int tau = 16 * tile + 4 * grp + j;
+              const int key = kc0 + SA_CHUNK * hc + tau;
+              bool ok = tau < (hc ? hi1 : hi0) && key < P.T;
+              if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
+                const bool in_win = key <= myq && key > myq - P.window;
+                ok = ok && (local ? in_win : !in_win);
+              }
+              if (!ok) sv[8 * hc + 4 * tile + j] = -INFINITY;
             }
-            sv[tile * 4 + j] = ok ? st[qt][tile][j] : -INFINITY;
-          }
       }
       // The running max (log2 units) moves only when a score exceeds it by more
       // than 8: P then stays below 2^8 and the accumulators are rescaled rarely.
-      // Most chunks only need to know that no score of the wave passes that
-      // threshold (one compare per score, the lane masks ORed in scalar
-      // registers); the row maxima are formed only when one does.
-      uint64_t over = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) over |= __ballot(sv[e] > m_thr[qt]);
-      float m_new = m_run[qt];
+      // Most pairs only need to know that no score of the wave passes that
+      // threshold (a max3 tree and one compare); the row maxima are formed only
+      // when one does.
+      float mx = __builtin_fmaxf(sal_max8(sv), sal_max8(sv + 8));
       alpha[qt] = 1.f;
-      if (over != 0) {  // uniform
-        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                         fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+#ifdef FSI_SAL_ALWAYSMAX
+      if (true) {
+#else
+      if (__ballot(mx > m_thr[qt]) != 0) {  // uniform
+#endif
         mx = max_rows4(mx);
-        const float m_cand = mx * P.scale_log2;
+        const float m_cand = mx * sl2;
         const bool bump = m_cand > m_run[qt] + 8.f;
-        m_new = bump ? m_cand : m_run[qt];
-        alpha[qt] = bump ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;  // exp2(-inf) = 0 on the first bump
+        const float m_new = bump ? m_cand : m_run[qt];
+        alpha[qt] = bump ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;
+        m_run[qt] = m_new;
         // scores above this move the max; scale_log2 > 0 on this kernel's path
-        m_thr[qt] = (m_new + 8.f) / P.scale_log2;
+        m_thr[qt] = (m_new + 8.f) * inv_sl2;
       }
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // no valid key yet: every p is exp2(-inf) = 0
-      uint32_t pk[4];
+      uint32_t pk[8];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < 8; ++w) {
         // P in fp16, one v_cvt_pkrtz_f16_f32 per pair (P <= 2^8)
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w], P.scale_log2, -m_use));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w + 1], P.scale_log2, -m_use));
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w], sl2, -m_run[qt]));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[2 * w + 1], sl2, -m_run[qt]));
         pk[w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0, p1));
       }
-      m_run[qt] = m_new;
-      pb[qt] = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
+      pb[0][qt] = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
+      pb[1][qt] = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
     }
-    // phase 3: rescale (skipped while no query's running max moved) and P V
-    // (consecutive MFMAs independent)
+    // rescale (skipped while no query's running max moved), then P V per chunk
 #pragma unroll
     for (int qt = 0; qt < SAL_QT; ++qt) {
       if (__ballot(alpha[qt] != 1.f) != 0) {
@@ -749,11 +786,45 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
       }
     }
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+    for (int hc = 0; hc < 2; ++hc) {
+      if ((hc ? hi1 : hi0) == 0) continue;  // uniform: an empty chunk (its slot holds other keys)
 #pragma unroll
-      for (int qt = 0; qt < SAL_QT; ++qt) acc[qt][dt] = mfma16x16x32_f16(vf[dt], pb[qt], acc[qt][dt]);
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int qt = 0; qt < SAL_QT; ++qt) lsum[qt] = mfma16x16x32_f16(ones, pb[qt], lsum[qt]);
+        for (int qt = 0; qt < SAL_QT; ++qt) acc[qt][dt] = mfma16x16x32_f16(vf[hc][dt], pb[hc][qt], acc[qt][dt]);
+#pragma unroll
+      for (int qt = 0; qt < SAL_QT; ++qt) lsum[qt] = mfma16x16x32_f16(ones, pb[hc][qt], lsum[qt]);
+    }
+  };
+
+  for (int p = 0; p < n_pairs; ++p) {
+    // pair p landed: at most the loads of pairs p + 1 .. p + AHEAD - 1 remain
+    const int later = (p + SAL_AHEAD - 1 < n_pairs - 1 ? p + SAL_AHEAD - 1 : n_pairs - 1) - p;
+    if constexpr (SAL_AHEAD >= 3) {
+      if (later >= 2) sal_wait_vmcnt<4 * LPW>();
+      else if (later == 1) sal_wait_vmcnt<2 * LPW>();
+      else sal_wait_vmcnt<0>();
+    } else {
+      if (later >= 1) sal_wait_vmcnt<2 * LPW>();
+      else sal_wait_vmcnt<0>();
+    }
+    sal_barrier();
+    if (p + SAL_AHEAD < n_pairs) {  // into the slots of pair p - 1, which every wave has finished
+      const int pn = p + SAL_AHEAD;
+      const int sn = 2 * (pn % SAL_RING);
+      int n0, nh0, nh1;
+      bool nl;
+      describe(pn, n0, nh0, nh1, nl);
+      issue(n0, sn);
+      issue(n0 + 1, sn + 1);
+    }
+    int c0, hi0, hi1;
+    bool local;
+    describe(p, c0, hi0, hi1, local);
+    if ((hi0 | hi1) == 0 || !head_live) continue;  // uniform: an empty pair or an idle wave
+    const int sl = 2 * (p % SAL_RING);
+    scores(sl);
+    finish(sl, c0, hi0, hi1, local);
   }
 
   if (!head_live) return;

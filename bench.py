@@ -501,6 +501,23 @@ def bench_block_sparse(fsi, args, dev):
                        "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": C5_TRAFFIC_BYTES[0.25],
                        "kernel": "tile_list_gemm_kernel (k-block lists built in its prologue)",
                        "flops_per_launch": flops}
+    # the same 25% product in fp32 (the reference modules' default dtype):
+    # tile_list_gemm_kernel<float> on v_mfma_f32_16x16x4_f32, graded against the
+    # fp32 matrix peak
+    x32, w32 = x.float(), w.float()
+    mask, n_tiles = c5_mask(scores, 0.25)
+    outs32 = {}
+
+    def step32(i):
+        outs32["o"] = fsi.blockwise_matmul(x32, w32, mask, T, T, rows_per_group=T)
+
+    t32, _ = time_graph(step32, max(1, args.steps // 2), args.warmup, dev)
+    per32 = t32 / max(1, args.steps // 2)
+    tf32 = flops / per32 / 1e12
+    res["fp32"] = {"ms_per_step": round(per32 * 1e3, 4), "tflops": round(tf32, 2), "peak": FP32_PEAK_TFLOPS,
+                   "frac": round(tf32 / FP32_PEAK_TFLOPS, 4), "density": 0.25,
+                   "kernel": "tile_list_gemm_kernel<float> (v_mfma_f32_16x16x4_f32)"}
+    del x32, w32, outs32
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))
         torch.set_num_threads(cores)

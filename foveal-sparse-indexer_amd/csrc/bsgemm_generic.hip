@@ -1,7 +1,8 @@
-// Tile-masked GEMM for the shapes and dtypes outside the bf16 MFMA engines of
-// bsgemm.hip: fp32 (the reference modules' default dtype) and bf16 with block
-// sizes those engines do not tile (block_k not a multiple of 64, column blocks
-// not a multiple of 32, unaligned rows).
+// Tile-masked GEMM for the shapes outside the MFMA engines of bsgemm.hip and
+// tile_gemm.hip (which also runs fp32, the reference modules' default dtype):
+// block sizes those engines do not tile (block_k not a multiple of 16 fp32 /
+// 32 bf16, column blocks neither a divisor >= 16 nor a multiple of 128,
+// unaligned rows).
 //
 //   out[m, n] = sum_k x[m, k] w[n, k] [tile (k / block_k, n / block_n) active for
 //               the row group of m]  (+ bias[n] where n's column block is active)
@@ -138,6 +139,12 @@ __global__ __launch_bounds__(256) void col_mask_kernel(const int32_t* __restrict
 
 }  // namespace
 
+namespace fsi_tile {  // csrc/tile_gemm.hip: 1 when the tiling does not fit the list kernel
+int tile_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, const uint8_t* mask,
+              int64_t groups, int64_t rows_per_group, int64_t block_k, int64_t block_n, int64_t M, int64_t N,
+              int64_t K, int dtype, void* out, int64_t ldo, int32_t* order_ws, hipStream_t st);
+}  // namespace fsi_tile
+
 namespace fsi_bs_generic {
 
 // 2-D tile mask form.  rows_per_group must be a multiple of 64 unless groups == 1.
@@ -191,6 +198,10 @@ int column_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, const vo
   const int nnb = static_cast<int>(N / block_size);
   col_mask_kernel<<<1, 256, 0, st>>>(active_blocks, static_cast<int>(n_active), nnb, mask_ws, err);
   FSI_HIP_LAUNCH_CHECK("block_sparse_linear mask");
+  // the list-driven MFMA tile kernel when the tiling fits it (csrc/tile_gemm.hip)
+  const int rc = fsi_tile::tile_gemm(x, ldx, w, ldw, bias, mask_ws, 1, M, K, block_size, M, N, K, dtype, out, ldo,
+                                     nullptr, st);
+  if (rc != 1) return rc;
   return tile_gemm(x, ldx, w, ldw, bias, mask_ws, 1, M, K, block_size, M, N, K, dtype, out, ldo, st);
 }
 

@@ -74,9 +74,10 @@ constexpr int LOADS = 4;            // global_load_lds per wave and step: 2 A + 
 constexpr int FRAG_ELEMS = 16 * KS;  // one 16-row fragment of a stage
 
 struct TileArgs {
-  const bf16_t* A;
-  const bf16_t* B;
-  bf16_t* C;
+  const void* A;  // bf16 or fp32 (the kernel's element type)
+  const void* B;
+  void* C;
+  const void* bias;  // optional, block_k == K only: added on the columns of active n blocks
   int64_t lda, ldb, ldc;
   int M, N, K;
   const uint8_t* mask;  // [groups][nkb * nnb], tile id k_b * nnb + n_b
@@ -243,8 +244,15 @@ __global__ __launch_bounds__(ORDER_THREADS) void tile_order_kernel(TileArgs g, i
   }
 }
 
-template <bool MASKED>
+// fp32 runs the same byte layout: a 64-byte LDS row holds 32 bf16 or 16 fp32 k
+// values, a fragment read 8 bf16 (one v_mfma_f32_16x16x32_bf16) or 4 fp32 (four
+// v_mfma_f32_16x16x4_f32, k-step kk taking k = 4 (lane / 16) + kk: A and B use the
+// same k order, so the four steps together cover the 16 k of the row).
+template <typename T, bool MASKED>
 __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(TileArgs g) {
+  constexpr bool F32 = sizeof(T) == 4;
+  constexpr int KSE = 64 / static_cast<int>(sizeof(T));  // K-step in elements (64 bytes of a row)
+  constexpr int CE = 16 / static_cast<int>(sizeof(T));   // elements per 16-byte chunk
   __shared__ __attribute__((aligned(1024))) bf16_t lds[STAGES][2][TT * KS];  // [stage][A/B][row * 32 + k]
   __shared__ int32_t klist[LIST_MAX];  // k block | active n-block bits << 16 (MASKED)
   __shared__ int32_t chunk_count[LIST_MAX / 64];
@@ -303,22 +311,22 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   }
   __syncthreads();
   nact = __builtin_amdgcn_readfirstlane(nact);
-  const int per = g.block_k / KS;
+  const int per = g.block_k / KSE;
   const int kcount = nact * per;
 
   // ---- this lane's source rows: wave w loads fragments 2 w, 2 w + 1 of A and B;
   // lane l lands at fragment row l / 4, slot l % 4, holding logical chunk
   // (l % 4) ^ chunk_swz(row) --------------------------------------------------
-  const bf16_t* asrc[2];
-  const bf16_t* bsrc[2];
+  const T* asrc[2];
+  const T* bsrc[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int r = 16 * (2 * wave + j) + (lane >> 2);
     const int lc = (lane & 3) ^ chunk_swz(r);
     const int m = m0 + r < g.M ? m0 + r : g.M - 1;  // rows past M read row M - 1, never stored
     const int n = n0 + r < g.N ? n0 + r : g.N - 1;
-    asrc[j] = g.A + static_cast<int64_t>(m) * g.lda + lc * 8;
-    bsrc[j] = g.B + static_cast<int64_t>(n) * g.ldb + lc * 8;
+    asrc[j] = static_cast<const T*>(g.A) + static_cast<int64_t>(m) * g.lda + lc * CE;
+    bsrc[j] = static_cast<const T*>(g.B) + static_cast<int64_t>(n) * g.ldb + lc * CE;
   }
   // list entries in registers, 64 at a time (lane i holds entry 64 c + i): an LDS
   // read in the issue path would wait for the direct-to-LDS loads in flight
@@ -328,7 +336,7 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   int rd_blk = 0, rd_sub = 0, rd_cur = iss_cur, rd_next = iss_next;
   auto issue = [&](int stage) {
     const int e = __builtin_amdgcn_readlane(iss_cur, iss_blk & 63);
-    const int64_t k = static_cast<int64_t>(e & 0xffff) * g.block_k + iss_sub * KS;
+    const int64_t k = static_cast<int64_t>(e & 0xffff) * g.block_k + iss_sub * KSE;
     if (++iss_sub == per) {
       iss_sub = 0;
       if ((++iss_blk & 63) == 0) {
@@ -382,10 +390,23 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
     }
   };
   auto mfmas = [&](const u32x4_t (&fa)[4], const u32x4_t (&fb)[4]) {
+    if constexpr (F32) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-      for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fb[f], fa[i], acc[i][f]);  // C^T fragment
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int f = 0; f < 4; ++f)  // C^T fragment
+            // (element by value: this clang's __builtin_bit_cast of a vector element
+            // reads element 0 whatever the index)
+            acc[i][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(fb[f][kk]), __uint_as_float(fa[i][kk]),
+                                                              acc[i][f], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fb[f], fa[i], acc[i][f]);  // C^T fragment
+    }
   };
 #if FSI_TG_PREFETCH
   // step s + 2 must have landed at the end of iteration s (its fragments are read
@@ -402,13 +423,14 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
     // unconditional: past the last step it reads a stage that is never used
     read_frags((step + 1) % STAGES, na, nb);
     mfmas(ca, cb);
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    constexpr int MF = F32 ? 8 : 2;  // MFMAs per fragment read of the next step
+    __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, F32 ? 0 : 2, 0);
     wait_through(step);
     stage_barrier();
   };
@@ -452,16 +474,39 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   // 16 i + r of the wave's rows and columns 4 q .. 4 q + 3 of the fragment ----------
   const int crow = m0 + 64 * wm + frow;
   const int ccol = n0 + 64 * wn + 4 * fchunk;
-  const bool vec = (reinterpret_cast<uintptr_t>(g.C) & 7) == 0 && (g.ldc & 3) == 0;
+  T* C = static_cast<T*>(g.C);
+  if (g.bias) {  // block_k == K: the bias of the columns whose n block is active
+    const T* bias = static_cast<const T*>(g.bias);
+    const uint8_t* row0 = g.mask + static_cast<int64_t>(grp) * g.nkb * g.nnb;
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = ccol + 16 * f + j;
+        float bv = 0.f;
+        if (n < g.N && row0[n / g.block_n]) {
+          if constexpr (F32) bv = bias[n];
+          else bv = bf16_to_f32(bias[n]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][f][j] += bv;
+      }
+  }
+  const bool vec = (reinterpret_cast<uintptr_t>(g.C) & (F32 ? 15 : 7)) == 0 && (g.ldc & 3) == 0;
   if (vec && m0 + TT <= g.M && n0 + TT <= g.N) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int f = 0; f < 4; ++f) {
-        uint2 w;
-        w.x = cvt_pk_bf16(acc[i][f][0], acc[i][f][1]);
-        w.y = cvt_pk_bf16(acc[i][f][2], acc[i][f][3]);
-        *reinterpret_cast<uint2*>(g.C + static_cast<int64_t>(crow + 16 * i) * g.ldc + ccol + 16 * f) = w;
+        T* dst = C + static_cast<int64_t>(crow + 16 * i) * g.ldc + ccol + 16 * f;
+        if constexpr (F32) {
+          *reinterpret_cast<f32x4_t*>(dst) = acc[i][f];
+        } else {
+          uint2 w;
+          w.x = cvt_pk_bf16(acc[i][f][0], acc[i][f][1]);
+          w.y = cvt_pk_bf16(acc[i][f][2], acc[i][f][3]);
+          *reinterpret_cast<uint2*>(dst) = w;
+        }
       }
   } else {
 #pragma unroll
@@ -473,13 +518,83 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int n = ccol + 16 * f + j;
-          if (n < g.N) g.C[static_cast<int64_t>(m) * g.ldc + n] = f32_to_bf16(acc[i][f][j]);
+          if (n < g.N) {
+            if constexpr (F32) C[static_cast<int64_t>(m) * g.ldc + n] = acc[i][f][j];
+            else C[static_cast<int64_t>(m) * g.ldc + n] = f32_to_bf16(acc[i][f][j]);
+          }
         }
     }
   }
 }
 
 }  // namespace
+
+namespace fsi_tile {
+
+// The list-driven tile GEMM (bf16 or fp32) when the tiling fits it: block_k a
+// multiple of the 64-byte K-step, block_n a multiple or a divisor (>= 16) of 128,
+// row groups of whole 128-row tiles, 16-byte aligned rows.  Returns 1 when the
+// shape does not fit (the caller runs the generic kernel), else an FSI status.
+// `order_ws` (tiles int32, may be null) takes the heaviest-first tile order.
+int tile_gemm(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, const uint8_t* mask,
+              int64_t groups, int64_t rows_per_group, int64_t block_k, int64_t block_n, int64_t M, int64_t N,
+              int64_t K, int dtype, void* out, int64_t ldo, int32_t* order_ws, hipStream_t st) {
+  using namespace fsi_host;
+  const int64_t esz = dtype == FSI_DTYPE_F32 ? 4 : 2;
+  const int64_t kse = 64 / esz, ce = 16 / esz;
+  const int64_t nkb = K / block_k, nnb = N / block_n;
+  const bool tiles_ok = block_k % kse == 0 && (block_n % TT == 0 || (TT % block_n == 0 && block_n >= 16)) &&
+                        nkb <= LIST_MAX && (rows_per_group % TT == 0 || groups == 1) &&
+                        (bias == nullptr || nkb == 1);
+  const bool aligned = ldx % ce == 0 && ldw % ce == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(w) & 15) == 0;  // 16-byte direct-to-LDS loads
+  if (!tiles_ok || !aligned) return 1;
+  TileArgs a{};
+  a.A = x;
+  a.B = w;
+  a.C = out;
+  a.bias = bias;
+  a.lda = ldx;
+  a.ldb = ldw;
+  a.ldc = ldo;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.mask = mask;
+  a.groups = (int)groups;
+  a.rows_per_group = (int)(rows_per_group < 0x7fffffff ? rows_per_group : 0x7fffffff);
+  a.nkb = (int)nkb;
+  a.nnb = (int)nnb;
+  a.block_k = (int)block_k;
+  a.block_n = (int)block_n;
+  a.m_tiles = (int)((M + TT - 1) / TT);
+  a.n_tiles = (int)((N + TT - 1) / TT);
+  const int64_t tiles = static_cast<int64_t>(a.m_tiles) * a.n_tiles;
+  FSI_CHECK_ARG(tiles <= 0x7fffffff, FSI_ERR_SHAPE, "blockwise_matmul: too many tiles");
+  const unsigned grid = static_cast<unsigned>(tiles);
+  // Heaviest-first order inside each band when the grid takes several rounds of
+  // workgroup slots and a band's counting pass (nkb x its n blocks' mask bytes per
+  // tile) is small.
+  const int64_t nsub = block_n < TT ? TT / block_n : 1;
+  const int64_t bands = (a.m_tiles + GROUP_M - 1) / GROUP_M;
+  if (order_ws != nullptr && tiles > ORDER_MIN_TILES && int64_t{GROUP_M} * a.n_tiles <= ORDER_MAX_BAND &&
+      int64_t{GROUP_M} * a.n_tiles * nkb * nsub <= ORDER_MAX_MASK_READS) {
+    tile_order_kernel<<<static_cast<unsigned>(bands), ORDER_THREADS, 0, st>>>(a, order_ws);
+    a.order = order_ws;
+  }
+  if (dtype == FSI_DTYPE_F32) {
+    if (block_n < TT) tile_list_gemm_kernel<float, true><<<grid, NTHREADS, 0, st>>>(a);
+    else tile_list_gemm_kernel<float, false><<<grid, NTHREADS, 0, st>>>(a);
+  } else {
+    if (block_n < TT) tile_list_gemm_kernel<bf16_t, true><<<grid, NTHREADS, 0, st>>>(a);
+    else tile_list_gemm_kernel<bf16_t, false><<<grid, NTHREADS, 0, st>>>(a);
+  }
+  const hipError_t e = hipGetLastError();
+  FSI_CHECK_ARG(e == hipSuccess, FSI_ERR_HIP, "blockwise_matmul: launch failed: %s", hipGetErrorString(e));
+  return FSI_OK;
+}
+
+}  // namespace fsi_tile
 
 extern "C" {
 
@@ -513,58 +628,19 @@ FSI_API int fsi_blockwise_matmul(const void* x, int64_t ldx, const void* w, int6
   if (M == 0) return FSI_OK;
   FSI_CHECK_ARG(x && w && tile_mask && out, FSI_ERR_INVALID_ARG, "blockwise_matmul: null pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int64_t nkb = K / block_k, nnb = N / block_n;
-  const bool tiles_ok = block_k % KS == 0 && (block_n % TT == 0 || (TT % block_n == 0 && block_n >= 16)) &&
-                        nkb <= LIST_MAX && (rows_per_group % TT == 0 || groups == 1);
   FSI_CHECK_ARG(ldx >= K && ldw >= K && ldo >= N, FSI_ERR_SHAPE, "blockwise_matmul: leading dimensions");
-  const bool aligned = ldx % 8 == 0 && ldw % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
-                       (reinterpret_cast<uintptr_t>(w) & 15) == 0;  // 16-byte direct-to-LDS loads
-  if (dtype == FSI_DTYPE_F32 || !tiles_ok || !aligned) {
-    // fp32, and bf16 tilings this kernel does not take: the generic kernel
-    return fsi_bs_generic::tile_gemm(x, ldx, w, ldw, nullptr, tile_mask, groups, rows_per_group, block_k, block_n,
-                                     M, N, K, dtype, out, ldo, st);
-  }
   FSI_CHECK_ARG(workspace == nullptr || workspace_bytes >= FSI_WORKSPACE_COUNTER_BYTES, FSI_ERR_WORKSPACE,
                 "blockwise_matmul: workspace %zu < %d", workspace_bytes, FSI_WORKSPACE_COUNTER_BYTES);
-  TileArgs a{};
-  a.A = static_cast<const bf16_t*>(x);
-  a.B = static_cast<const bf16_t*>(w);
-  a.C = static_cast<bf16_t*>(out);
-  a.lda = ldx;
-  a.ldb = ldw;
-  a.ldc = ldo;
-  a.M = (int)M;
-  a.N = (int)N;
-  a.K = (int)K;
-  a.mask = tile_mask;
-  a.groups = (int)groups;
-  a.rows_per_group = (int)(rows_per_group < 0x7fffffff ? rows_per_group : 0x7fffffff);
-  a.nkb = (int)nkb;
-  a.nnb = (int)nnb;
-  a.block_k = (int)block_k;
-  a.block_n = (int)block_n;
-  a.m_tiles = (int)((M + TT - 1) / TT);
-  a.n_tiles = (int)((N + TT - 1) / TT);
-  const int64_t tiles = static_cast<int64_t>(a.m_tiles) * a.n_tiles;
-  FSI_CHECK_ARG(tiles <= 0x7fffffff, FSI_ERR_SHAPE, "blockwise_matmul: too many tiles");
-  const unsigned grid = static_cast<unsigned>(tiles);
-  // Heaviest-first order inside each band when the grid takes several rounds of
-  // workgroup slots and a band's counting pass (nkb x its n blocks' mask bytes per
-  // tile) is small.
-  const int64_t nsub = block_n < TT ? TT / block_n : 1;
-  const int64_t bands = (a.m_tiles + GROUP_M - 1) / GROUP_M;
-  if (workspace != nullptr && workspace_bytes >= FSI_WORKSPACE_COUNTER_BYTES + tiles * sizeof(int32_t) &&
-      tiles > ORDER_MIN_TILES && int64_t{GROUP_M} * a.n_tiles <= ORDER_MAX_BAND &&
-      int64_t{GROUP_M} * a.n_tiles * nkb * nsub <= ORDER_MAX_MASK_READS) {
-    int32_t* order = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES);
-    tile_order_kernel<<<static_cast<unsigned>(bands), ORDER_THREADS, 0, st>>>(a, order);
-    a.order = order;
-  }
-  if (block_n < TT) tile_list_gemm_kernel<true><<<grid, NTHREADS, 0, st>>>(a);
-  else tile_list_gemm_kernel<false><<<grid, NTHREADS, 0, st>>>(a);
-  const hipError_t e = hipGetLastError();
-  FSI_CHECK_ARG(e == hipSuccess, FSI_ERR_HIP, "blockwise_matmul: launch failed: %s", hipGetErrorString(e));
-  return FSI_OK;
+  const int64_t tiles = ((M + TT - 1) / TT) * ((N + TT - 1) / TT);
+  int32_t* order = workspace != nullptr && workspace_bytes >= FSI_WORKSPACE_COUNTER_BYTES + tiles * sizeof(int32_t)
+                       ? reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES)
+                       : nullptr;
+  const int rc = fsi_tile::tile_gemm(x, ldx, w, ldw, nullptr, tile_mask, groups, rows_per_group, block_k, block_n, M,
+                                     N, K, dtype, out, ldo, order, st);
+  if (rc != 1) return rc;
+  // tilings the list kernel does not take: the generic kernel
+  return fsi_bs_generic::tile_gemm(x, ldx, w, ldw, nullptr, tile_mask, groups, rows_per_group, block_k, block_n, M,
+                                   N, K, dtype, out, ldo, st);
 }
 
 }  // extern "C"

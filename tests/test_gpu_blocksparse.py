@@ -18,13 +18,16 @@ def _rel(got, ref):
     return P.rel_l2(got.float().cpu(), ref.float())
 
 
-@pytest.mark.parametrize("M,K,N,bs,active,bias", [
+BSL_CASES = [
     (1, 64, 256, 64, [3, 0], False),
     (100, 256, 512, 32, [15, 2, 7, 9], True),
     (300, 1000, 384, 128, [1, 2], True),
     (257, 128, 1024, 64, list(range(16)), False),
     (64, 512, 256, 64, [], True),
-])
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs,active,bias", BSL_CASES)
 def test_block_sparse_linear(fsi, dev, M, K, N, bs, active, bias):
     print(f"[case] block_sparse_linear M={M} K={K} N={N} bs={bs} n_active={len(active)}", flush=True)
     g = torch.Generator().manual_seed(M + K)
@@ -51,7 +54,7 @@ def test_block_sparse_linear_bad_block_reported(fsi, dev, monkeypatch):
         fsi.triton_block_sparse_linear(x, w, None, torch.tensor([5], dtype=torch.int32, device=dev), block_size=64)
 
 
-@pytest.mark.parametrize("M,K,N,bk,bn,density,groups", [
+BW_CASES = [
     (256, 512, 512, 128, 128, 0.25, 1),
     (384, 512, 256, 64, 64, 0.3, 3),
     (200, 256, 512, 64, 128, 0.5, 1),
@@ -66,7 +69,10 @@ def test_block_sparse_linear_bad_block_reported(fsi, dev, monkeypatch):
     (4608, 512, 2048, 128, 128, 0.3, 36),  # 576 tiles: heaviest-first tile order from the pre-pass
     (4096, 256, 2304, 32, 64, 0.25, 4),    # 576 tiles, 2 n blocks per tile, 8 m tiles per group
     (4200, 256, 2176, 64, 128, 0.5, 3),    # 561 tiles, ragged M, with the tile order
-])
+]
+
+
+@pytest.mark.parametrize("M,K,N,bk,bn,density,groups", BW_CASES)
 def test_blockwise_matmul(fsi, dev, M, K, N, bk, bn, density, groups):
     print(f"[case] blockwise_matmul M={M} K={K} N={N} tile={bk}x{bn} d={density} groups={groups}", flush=True)
     g = torch.Generator().manual_seed(K + N)
@@ -82,6 +88,54 @@ def test_blockwise_matmul(fsi, dev, M, K, N, bk, bn, density, groups):
         assert torch.equal(out, torch.zeros_like(out))
         return
     assert _rel(out, ref) <= TOL
+
+
+# fp32 (the reference modules' default dtype): the list-driven tile kernel on
+# v_mfma_f32_16x16x4_f32 where the tiling fits it (k blocks of 16-multiples), the
+# generic kernel otherwise (k blocks of 8, n blocks of 48, K = 1000).  fp32 bar:
+# rel-L2 <= 1e-5 against fp64.
+TOL_F32 = 1e-5
+
+
+@pytest.mark.parametrize("M,K,N,bk,bn,density,groups", BW_CASES + [
+    (256, 512, 384, 16, 16, 0.3, 2),       # 16-wide k blocks: one fp32 K-step each
+    (192, 256, 256, 8, 64, 0.5, 1),        # 8-wide k blocks: generic kernel
+])
+def test_blockwise_matmul_f32(fsi, dev, M, K, N, bk, bn, density, groups):
+    print(f"[case] blockwise_matmul fp32 M={M} K={K} N={N} tile={bk}x{bn} d={density} groups={groups}", flush=True)
+    g = torch.Generator().manual_seed(K + N + 1)
+    x = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) * 0.05
+    T = (K // bk) * (N // bn)
+    masks = torch.rand(groups, T, generator=g) < density
+    rpg = -(-M // groups) if groups > 1 else M
+    rpg = -(-rpg // 128) * 128 if groups > 1 else rpg
+    out = fsi.blockwise_matmul(x.to(dev), w.to(dev), masks.to(dev), bk, bn, rows_per_group=rpg).cpu()
+    assert out.dtype == torch.float32
+    ref = BS.blockwise_matmul_f64(x, w, masks, bk, bn, rpg)
+    if not masks.any():
+        assert torch.equal(out, torch.zeros_like(out))
+        return
+    assert _rel(out, ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("M,K,N,bs,active,bias", BSL_CASES + [(130, 4096, 512, 16, [0, 5, 31], True)])
+def test_block_sparse_linear_f32(fsi, dev, M, K, N, bs, active, bias):
+    print(f"[case] block_sparse_linear fp32 M={M} K={K} N={N} bs={bs} n_active={len(active)}", flush=True)
+    g = torch.Generator().manual_seed(M + K + 1)
+    x = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) * 0.05
+    b = torch.randn(N, generator=g) if bias else None
+    act = torch.tensor(active, dtype=torch.int32)
+    out = fsi.triton_block_sparse_linear(x.to(dev), w.to(dev), None if b is None else b.to(dev), act.to(dev),
+                                         block_size=bs).cpu()
+    ref = BS.block_sparse_linear_f64(x, w, b, active, bs)
+    inactive = torch.ones(N, dtype=torch.bool)
+    for a in active:
+        inactive[a * bs:(a + 1) * bs] = False
+    assert torch.all(out[:, inactive] == 0)
+    if active:
+        assert _rel(out, ref) <= TOL_F32
 
 
 @pytest.mark.parametrize("M,rounding", [(300, "fused"), (512, "eager"), (256, "fp32")])
@@ -173,8 +227,9 @@ def test_blockwise_matmul_module(fsi, dev):
     assert _rel(out, ref) <= 1e-2
 
 
-@pytest.mark.parametrize("bn,density", [(128, 0.25), (64, 0.4), (128, 0.0)])
-def test_blockwise_matmul_tile_order_matches_dispatch_order(fsi, dev, bn, density):
+@pytest.mark.parametrize("bn,density,dtype", [(128, 0.25, torch.bfloat16), (64, 0.4, torch.bfloat16),
+                                             (128, 0.0, torch.bfloat16), (64, 0.4, torch.float32)])
+def test_blockwise_matmul_tile_order_matches_dispatch_order(fsi, dev, bn, density, dtype):
     """Above 512 output tiles the workspace receives a tile order, heaviest first
     inside each 128-row band; without a workspace the tiles run in dispatch order.
     Both give the same bits (each tile's result does not depend on the workgroup
@@ -184,8 +239,8 @@ def test_blockwise_matmul_tile_order_matches_dispatch_order(fsi, dev, bn, densit
     from foveal_sparse_indexer_amd import _lib
     g = torch.Generator().manual_seed(bn + int(density * 100))
     M, K, N, bk, groups = 5120, 512, 2048, 64, 20
-    x = torch.randn(M, K, generator=g).bfloat16()
-    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(dtype)
     T = (K // bk) * (N // bn)
     dens = torch.linspace(0.0, 1.0, groups).unsqueeze(1) if density > 0 else torch.zeros(groups, 1)
     masks = torch.rand(groups, T, generator=g) < dens
@@ -202,9 +257,10 @@ def test_blockwise_matmul_tile_order_matches_dispatch_order(fsi, dev, bn, densit
     torch.cuda.synchronize(dev)
     assert torch.equal(ordered, plain)
     if masks.any():
-        assert _rel(ordered, BS.blockwise_matmul_f64(x, w, masks, bk, bn, rpg)) <= TOL
+        tol = TOL_F32 if dtype == torch.float32 else TOL
+        assert _rel(ordered, BS.blockwise_matmul_f64(x, w, masks, bk, bn, rpg)) <= tol
     else:
-        assert torch.equal(ordered.cpu(), torch.zeros(M, N, dtype=torch.bfloat16))
+        assert torch.equal(ordered.cpu(), torch.zeros(M, N, dtype=dtype))
 
 
 def test_blockwise_matmul_graph_replays(fsi, dev):

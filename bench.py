@@ -406,6 +406,22 @@ def bench_prefill_attn(fsi, args, dev):
     torch.cuda.synchronize(dev)
     bwd_ms = ev0.elapsed_time(ev1) / n_bwd
     bwd_tf = 2.5 * flops / (bwd_ms * 1e-3) / 1e12
+    # the same forward in fp32 (FovealSparseAttention's default dtype): the fp32
+    # MFMA kernel (sparse_attn_f32_kernel), graded against the fp32 matrix peak
+    q32, k32, v32 = q.float(), k.float(), v.float()
+    out32 = torch.empty(B, T, HQ, HD, dtype=torch.float32, device=dev)
+
+    def step32(i):
+        fsi.sparse_attention(q32, k32, v32, lists, counts, block=PAGE, mode=0, window=W, scale=scale,
+                             out=out32.transpose(1, 2))
+
+    n32s = max(1, args.steps // 2)
+    t32, _ = time_graph(step32, n32s, args.warmup, dev)
+    tf32 = flops / (t32 / n32s) / 1e12
+    res["fp32"] = {"ms_per_step": round(t32 / n32s * 1e3, 4), "tflops": round(tf32, 1), "peak": FP32_PEAK_TFLOPS,
+                   "frac": round(tf32 / FP32_PEAK_TFLOPS, 4),
+                   "kernel": "vt32_kernel + sparse_attn_f32_kernel<128> (v_mfma_f32_16x16x4_f32)"}
+    del q32, k32, v32, out32
     res["backward"] = {"ms": round(bwd_ms, 3), "tflops": round(bwd_tf, 1), "fp32_frac": round(bwd_tf / FP32_PEAK_TFLOPS, 4),
                        "flops": int(2.5 * flops), "kernel": "sab_map + sab_q (statistics, dQ) + sab_kv (dK, dV)",
                        "note": "fp32 VALU on 64 x 64 LDS tiles; memory O(T hd), no (T, T) tensor"}

@@ -43,6 +43,15 @@ int sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, const v
                 int64_t os_t, int* err, void* stream);
 }  // namespace fsi_attn_generic
 
+namespace fsi_attn_f32 {  // csrc/sparse_attn_f32.hip: 1 when the shape does not fit its kernel
+int sparse_attn(const float* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, const float* k, int64_t ks_b, int64_t ks_h,
+                int64_t ks_t, const float* v, int64_t vs_b, int64_t vs_h, int64_t vs_t, int64_t B, int64_t Hq,
+                int64_t Hkv, int64_t T, int64_t head_dim, int64_t block, int mode, int64_t window,
+                const int32_t* lists, int64_t ls_b, int64_t ls_q, int64_t capacity, const int32_t* counts,
+                int64_t cs_b, int64_t cs_q, float scale, float* out, int64_t os_b, int64_t os_h, int64_t os_t,
+                float* vt, int* err, hipStream_t st);
+}  // namespace fsi_attn_f32
+
 namespace {
 
 constexpr int SA_WAVES = 4;   // query heads per workgroup
@@ -851,9 +860,10 @@ extern "C" {
 FSI_API size_t fsi_sparse_attn_workspace_size(int64_t B, int64_t Hkv, int64_t T, int64_t head_dim) {
   if (B <= 0 || Hkv <= 0 || T <= 0 || head_dim <= 0) return FSI_WORKSPACE_COUNTER_BYTES;
   const int64_t n32 = (T + SA_CHUNK - 1) / SA_CHUNK;
-  // V^T copy (bf16 or fp16), the per-chunk maxima and the per-head exponents
+  // V^T copy (fp16 / bf16, or fp32 for the fp32 kernel: 4 bytes an element are
+  // reserved either way), the per-chunk maxima and the per-head exponents
   return FSI_WORKSPACE_COUNTER_BYTES +
-         fsi_host::align_up(sizeof(bf16_t) * static_cast<size_t>(B * Hkv * n32 * SA_CHUNK * head_dim), 256) +
+         fsi_host::align_up(sizeof(float) * static_cast<size_t>(B * Hkv * n32 * SA_CHUNK * head_dim), 256) +
          fsi_host::align_up(sizeof(uint32_t) * static_cast<size_t>(B * Hkv * n32), 256) +
          fsi_host::align_up(sizeof(int32_t) * static_cast<size_t>(B * Hkv), 256);
 }
@@ -877,6 +887,18 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
       vs_b % 8 == 0 && os_t % 4 == 0 && os_h % 4 == 0 && os_b % 4 == 0 &&
       reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
       reinterpret_cast<uintptr_t>(v) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0;
+  if (dtype == FSI_DTYPE_F32 && B > 0 && T > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && capacity >= 0 &&
+      (mode != FSI_SATTN_LOCAL_REMOTE || window > 0) && q && k && v && out && counts && (lists || capacity == 0) &&
+      workspace && workspace_bytes >= fsi_sparse_attn_workspace_size(B, Hkv, T, head_dim)) {
+    // fp32 on MFMA when the shape fits the 64-query kernel (csrc/sparse_attn_f32.hip)
+    const int rc = fsi_attn_f32::sparse_attn(
+        static_cast<const float*>(q), qs_b, qs_h, qs_t, static_cast<const float*>(k), ks_b, ks_h, ks_t,
+        static_cast<const float*>(v), vs_b, vs_h, vs_t, B, Hq, Hkv, T, head_dim, block, mode, window, lists, ls_b,
+        ls_q, capacity, counts, cs_b, cs_q, scale, static_cast<float*>(out), os_b, os_h, os_t,
+        reinterpret_cast<float*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES), err,
+        reinterpret_cast<hipStream_t>(stream));
+    if (rc != 1) return rc;
+  }
   if (!mfma_path) {
     FSI_CHECK_ARG(B > 0 && T > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, FSI_ERR_SHAPE,
                   "sparse_attn: B=%lld T=%lld Hq=%lld Hkv=%lld", (long long)B, (long long)T, (long long)Hq,
@@ -922,7 +944,7 @@ FSI_API int fsi_sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t q
   const int n32 = static_cast<int>((T + SA_CHUNK - 1) / SA_CHUNK);
   char* wsp = static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES;
   bf16_t* vt = reinterpret_cast<bf16_t*>(wsp);
-  wsp += fsi_host::align_up(sizeof(bf16_t) * static_cast<size_t>(B * Hkv * n32 * SA_CHUNK * head_dim), 256);
+  wsp += fsi_host::align_up(sizeof(float) * static_cast<size_t>(B * Hkv * n32 * SA_CHUNK * head_dim), 256);
   uint32_t* cmax = reinterpret_cast<uint32_t*>(wsp);
   wsp += fsi_host::align_up(sizeof(uint32_t) * static_cast<size_t>(B * Hkv * n32), 256);
   int32_t* head_e = reinterpret_cast<int32_t*>(wsp);

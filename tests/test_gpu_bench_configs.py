@@ -157,19 +157,23 @@ def test_c4_decode_attention_full_size(fsi, dev):
     assert P.rel_l2(out2.cpu().float(), out.float()) <= 1e-3
 
 
-def test_prefill_attention_16k_sampled_blocks(fsi, dev):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_prefill_attention_16k_sampled_blocks(fsi, dev, dtype):
     """The timed prefill-attention workload exactly (bench.prefill_attn_inputs:
     16384 tokens, 32 / 8 heads, hd 128, window 1024, <= 32 routed pages, output
-    through the same strided view): sampled query blocks, including the first
-    ones, the first with a full window, and the last (window and 32 far pages
-    all live), against fp64 attention under the oracle's sparse_mask
-    (attention.py:148-218), each block's keys gathered on the host."""
-    print("[case] prefill attention 16K sampled blocks", flush=True)
+    through the same strided view; bf16, and the bench's fp32 leg on the same
+    inputs): sampled query blocks, including the first ones, the first with a
+    full window, and the last (window and 32 far pages all live), against fp64
+    attention under the oracle's sparse_mask (attention.py:148-218), each
+    block's keys gathered on the host.  Bars: bf16 2e-3, fp32 1e-5."""
+    print(f"[case] prefill attention 16K sampled blocks {dtype}", flush=True)
     c = bench.PREFILL_ATTN
     B, HQ, HKV, HD, T, PAGE, W = c["B"], c["HQ"], c["HKV"], c["HD"], c["T"], c["PAGE"], c["WB"] * c["PAGE"]
     q, k, v, lists, counts = bench.prefill_attn_inputs(fsi, dev)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    tol = 2e-3 if dtype == torch.bfloat16 else 1e-5
     scale = 1.0 / HD ** 0.5
-    out = torch.empty(B, T, HQ, HD, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(B, T, HQ, HD, dtype=dtype, device=dev)
     with torch.no_grad():
         fsi.sparse_attention(q, k, v, lists, counts, block=PAGE, mode=0, window=W, scale=scale,
                              out=out.transpose(1, 2))
@@ -186,7 +190,7 @@ def test_prefill_attention_16k_sampled_blocks(fsi, dev):
         ref = A.weighted_attention_f64(qc[:, :, q0:q1], kc[:, :, keys], vc[:, :, keys], rows[:, :, keys], scale)
         err = P.rel_l2(oc[:, :, q0:q1].float(), ref.float())
         print(f"prefill 16K block {qb}: {keys.numel()} keys, {int(cnt[0, qb])} pages, rel-L2 {err:.3e}", flush=True)
-        assert err <= 2e-3
+        assert err <= tol
 
 
 @pytest.mark.parametrize("density", bench.C5["DENSITIES"])

@@ -99,6 +99,78 @@ def test_block_list_parity(fsi, dev, case):
     assert err <= TOL, err
 
 
+# fp32 (FovealSparseAttention's default dtype): the fp32 MFMA kernel for pages
+# of a power-of-two multiple of 64 and head_dim 64 / 128, the generic kernel for
+# the other cases of the same lists.  fp32 bar: rel-L2 <= 1e-5 against fp64.
+TOL_F32 = 1e-5
+
+
+@pytest.mark.parametrize("case", LR_CASES, ids=[f"c{i}" for i in range(len(LR_CASES))])
+def test_local_remote_parity_f32(fsi, dev, case):
+    B, Hq, Hkv, hd, T, blk, W, cap = case
+    print(f"[case] sparse_attention fp32 local_remote {case}", flush=True)
+    q, k, v, g = _qkv(B, Hq, Hkv, T, hd, seed=sum(case) + 1)
+    q, k, v = q.float(), k.float(), v.float()
+    Qb = -(-T // blk)
+    idx = torch.randint(0, Qb, (B, Qb, max(cap, 1)), generator=g, dtype=torch.int32)[:, :, :cap]
+    cnt = torch.randint(0, cap + 1, (B, Qb), generator=g, dtype=torch.int32)
+    if cap >= 2:
+        idx[0, Qb - 1, :2] = torch.tensor([0, 0], dtype=torch.int32)
+        cnt[0, Qb - 1] = 2
+    scale = 1.0 / math.sqrt(hd)
+    out = fsi.sparse_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev) if cap else None, cnt.to(dev), block=blk,
+                               mode=0, window=W, scale=scale)
+    assert out.dtype == torch.float32
+    mask = A.sparse_mask(B, T, W, blk, idx, cnt)
+    ref = A.weighted_attention_f64(q, k, v, mask, scale)
+    err = Pt.rel_l2(out.cpu(), ref.float())
+    assert err <= TOL_F32, err
+
+
+@pytest.mark.parametrize("case", BL_CASES, ids=[f"c{i}" for i in range(len(BL_CASES))])
+def test_block_list_parity_f32(fsi, dev, case):
+    B, H, N, D, bs, mx = case
+    print(f"[case] triton_foveal_sparse_attention fp32 {case}", flush=True)
+    q, k, v, g = _qkv(B, H, H, N, D, seed=7 * sum(case) + 1)
+    q, k, v = q.float(), k.float(), v.float()
+    M = N // bs
+    idx = torch.randint(0, M, (B, M, mx), generator=g, dtype=torch.int32)
+    cnt = torch.randint(0, mx + 1, (B, M), generator=g, dtype=torch.int32)
+    cnt[0, 0] = 0
+    idx[0, 1, :2] = 1
+    cnt[0, 1] = max(int(cnt[0, 1]), 2)
+    out = fsi.triton_foveal_sparse_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), cnt.to(dev),
+                                             block_size=bs).cpu()
+    w = A.block_list_weights(B, N, bs, idx, cnt)
+    ref = A.weighted_attention_f64(q, k, v, w, 1.0 / math.sqrt(D))
+    assert torch.equal(out[0, :, :bs], torch.zeros(H, bs, D))
+    err = Pt.rel_l2(out, ref.float())
+    assert err <= TOL_F32, err
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_value_range_f32(fsi, dev, hd):
+    """Scores spreading over tens of log2 units (the running max moves several
+    times and the accumulators are rescaled) and values of very different size
+    per KV head, fp32 end to end."""
+    B, Hq, Hkv, T, blk, W, cap = 1, 8, 2, 640, 64, 192, 4
+    g = torch.Generator().manual_seed(hd)
+    q = torch.randn(B, Hq, T, hd, generator=g) * 2.0
+    k = torch.randn(B, Hkv, T, hd, generator=g) * torch.linspace(0.1, 2.0, T).view(1, 1, T, 1)
+    v = torch.randn(B, Hkv, T, hd, generator=g) * torch.tensor([1e-3, 1e3]).view(1, 2, 1, 1)
+    Qb = T // blk
+    idx = torch.randint(0, Qb, (B, Qb, cap), generator=g, dtype=torch.int32)
+    cnt = torch.full((B, Qb), cap, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(hd)
+    out = fsi.sparse_attention(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), cnt.to(dev), block=blk, mode=0,
+                               window=W, scale=scale)
+    ref = A.weighted_attention_f64(q, k, v, A.sparse_mask(B, T, W, blk, idx, cnt), scale)
+    for hk in range(Hkv):  # per KV head group: values of 1e-3 and 1e3
+        hs = slice(hk * (Hq // Hkv), (hk + 1) * (Hq // Hkv))
+        err = Pt.rel_l2(out[:, hs].cpu(), ref[:, hs].float())
+        assert err <= TOL_F32, (hk, err)
+
+
 def test_strided_views_in_place(fsi, dev):
     """q, k, v as (B, T, H, hd) projections viewed (B, H, T, hd), output written
     into such a view."""

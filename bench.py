@@ -266,9 +266,11 @@ def bench_decode_attn(fsi, args, dev):
     scale = 1.0 / (HD ** 0.5)
     outs = {}
 
+    outs_pages = {}
+
     def step(i):
         # routing beside the local-window attention partials, then the selected pages and the merge
-        outs["o"], pages, outs["c"], ctx = fsi.decode_step_attention(
+        outs["o"], outs_pages["p"], outs["c"], ctx = fsi.decode_step_attention(
             q, qi, cache, pos=pos, window=W, completed_pages=P, top_p=TOP_P, min_remote_blocks=0,
             max_remote_blocks=KMAX, scale=scale, return_context=True)
 
@@ -290,6 +292,29 @@ def bench_decode_attn(fsi, args, dev):
                        "kernel": "decode_step_kernel (route workgroups beside the local-window partials) + "
                                  "decode_attn_partial (selected pages) + decode_attn_merge (3 launches)",
                        "bytes_per_launch": algo}
+    # fp32 over the reference's contiguous cache layout (FovealKVCache's default dtype),
+    # all 32 sequences (34.4 GB of K / V), the same pages: dec32_partial_kernel + merge
+    nb = B
+    c32 = fsi.FovealKVCache(nb, CTX, HKV, HD, 16, PAGE, dev, torch.float32)
+    g32 = torch.Generator(device=dev).manual_seed(1)
+    c32.k_cache.normal_(generator=g32)
+    c32.v_cache.normal_(generator=g32)
+    q32 = q[:nb].float()
+    pg32, ct32 = outs_pages["p"][:nb].contiguous(), outs["c"][:nb].contiguous()
+    o32 = {}
+
+    def step32(i):
+        o32["o"] = fsi.decode_attention(q32, c32, pos=pos, window=W, remote_pages=pg32, remote_counts=ct32,
+                                        scale=scale)
+
+    t32, _ = time_graph(step32, args.steps, args.warmup, dev)
+    per32 = t32 / args.steps
+    k32 = float(ct32.float().mean())
+    b32 = int(nb * (W + PAGE * k32) * HKV * HD * 4 * 2)
+    res["fp32"] = {"ms_per_step": round(per32 * 1e3, 4), "sequences": nb, "kv_bytes": b32,
+                   "gbs": round(b32 / per32 / 1e9, 1), "frac": round(b32 / per32 / 1e9 / HBM_PEAK_GBS, 4),
+                   "kernel": "dec32_partial_kernel<128> + dec32_merge_kernel<128> (contiguous fp32 cache)"}
+    del c32
     if not args.no_cpu_baseline:
         from oracle import attention as A
 

@@ -150,11 +150,12 @@ SIGNATURES: dict[str, tuple] = {
          _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          ctypes.c_float, _c_int, _c_ptr, _c_ptr, _c_size, _c_ptr, _c_ptr],
     ),
+    "fsi_decode_attn_dense_workspace_size": (_c_size, [_c_i64] * 7),
     "fsi_decode_attn_dense": (
         _c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64,
          _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_int, _c_ptr, _c_ptr,
-         _c_ptr],
+         _c_size, _c_ptr, _c_ptr],
     ),
     "fsi_decode_attn_noalloc": (
         _c_int,

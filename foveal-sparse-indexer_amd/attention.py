@@ -311,11 +311,13 @@ def _decode_launch(q3: Tensor, k_cache: Tensor, v_cache: Tensor, page_table: Opt
                                hd, scale, out.data_ptr(), ws.data_ptr(), ws.numel(), err.data_ptr(), stream)
     else:
         k, v = k_cache, v_cache
+        ws = _lib.workspace(dev, L.fsi_decode_attn_dense_workspace_size(B, Hq, hd, window, cap, page_size,
+                                                                        max_seq_len), stream)
         st = L.fsi_decode_attn_dense(q3.data_ptr(), k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
                                      k.stride(2), v.stride(0), v.stride(1), v.stride(2), max_seq_len,
                                      _lib.ptr(pos_rows), pos_val, window, page_size, rp, rc, cap, B, Hq, n_kv_heads,
-                                     hd, scale, _lib.dtype_code(q3.dtype, what), out.data_ptr(), err.data_ptr(),
-                                     stream)
+                                     hd, scale, _lib.dtype_code(q3.dtype, what), out.data_ptr(), ws.data_ptr(),
+                                     ws.numel(), err.data_ptr(), stream)
     _lib.check(st, what)
     if _lib.checks_enabled():
         _lib.raise_device_errors(dev, what)

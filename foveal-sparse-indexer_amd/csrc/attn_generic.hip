@@ -252,6 +252,16 @@ __global__ __launch_bounds__(64 * GA_WAVES) void sparse_attn_generic_kernel(GenS
 
 }  // namespace
 
+namespace fsi_dec32 {  // csrc/decode_attn_f32.hip: run() returns 1 when the call does not fit its kernels
+size_t workspace_bytes(int64_t B, int64_t Hq, int64_t head_dim, int64_t window, int64_t capacity, int64_t page_size,
+                       int64_t max_seq);
+int run(const float* q, const float* k, const float* v, int64_t ks_b, int64_t ks_h, int64_t ks_t, int64_t vs_b,
+        int64_t vs_h, int64_t vs_t, int64_t max_seq, const int32_t* pos_rows, int64_t pos, int64_t window,
+        int64_t page_size, const int32_t* remote_pages, const int32_t* remote_counts, int64_t capacity, int64_t B,
+        int64_t Hq, int64_t Hkv, int64_t head_dim, float scale, float* out, float* part, size_t part_bytes, int* err,
+        hipStream_t st);
+}  // namespace fsi_dec32
+
 // Generic prefill launch used by fsi_sparse_attn for the cases its MFMA kernels
 // do not take (fp32, block % 16 != 0, head_dim outside {16, 32, 64, 128}).
 namespace fsi_attn_generic {
@@ -315,12 +325,21 @@ int sparse_attn(const void* q, int64_t qs_b, int64_t qs_h, int64_t qs_t, const v
 
 extern "C" {
 
+FSI_API size_t fsi_decode_attn_dense_workspace_size(int64_t B, int64_t Hq, int64_t head_dim, int64_t window,
+                                                    int64_t capacity, int64_t page_size, int64_t max_seq) {
+  // the counter area every workspace starts with, then the split partials
+  if (B <= 0 || Hq <= 0 || head_dim <= 0) return FSI_WORKSPACE_COUNTER_BYTES;
+  return FSI_WORKSPACE_COUNTER_BYTES +
+         fsi_dec32::workspace_bytes(B, Hq, head_dim, window < 0 ? 0 : window, capacity < 0 ? 0 : capacity,
+                                    page_size < 1 ? 1 : page_size, max_seq < 1 ? 1 : max_seq);
+}
+
 FSI_API int fsi_decode_attn_dense(const void* q, const void* k_cache, const void* v_cache, int64_t ks_b, int64_t ks_h,
                                   int64_t ks_t, int64_t vs_b, int64_t vs_h, int64_t vs_t, int64_t max_seq,
                                   const int32_t* pos_rows, int64_t pos, int64_t window, int64_t page_size,
                                   const int32_t* remote_pages, const int32_t* remote_counts, int64_t capacity,
                                   int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale, int dtype,
-                                  void* out, int* err, void* stream) {
+                                  void* out, void* workspace, size_t workspace_bytes, int* err, void* stream) {
   FSI_CHECK_ARG(dtype == FSI_DTYPE_F32 || dtype == FSI_DTYPE_BF16, FSI_ERR_DTYPE, "decode_attn_dense: dtype %d",
                 dtype);
   FSI_CHECK_ARG(head_dim > 0 && head_dim <= GA_MAX_HD, FSI_ERR_SHAPE, "decode_attn_dense: head_dim %lld (1..%d)",
@@ -335,6 +354,17 @@ FSI_API int fsi_decode_attn_dense(const void* q, const void* k_cache, const void
   FSI_CHECK_ARG(q && k_cache && v_cache && out, FSI_ERR_INVALID_ARG, "decode_attn_dense: null pointer");
   FSI_CHECK_ARG(capacity == 0 || (remote_pages && remote_counts), FSI_ERR_INVALID_ARG,
                 "decode_attn_dense: remote page list or counts missing");
+  if (dtype == FSI_DTYPE_F32 && workspace != nullptr && workspace_bytes > FSI_WORKSPACE_COUNTER_BYTES) {
+    // fp32 over the keys split across waves, on MFMA (csrc/decode_attn_f32.hip)
+    const int rc = fsi_dec32::run(static_cast<const float*>(q), static_cast<const float*>(k_cache),
+                                  static_cast<const float*>(v_cache), ks_b, ks_h, ks_t, vs_b, vs_h, vs_t, max_seq,
+                                  pos_rows, pos, window, page_size, remote_pages, remote_counts, capacity, B, Hq, Hkv,
+                                  head_dim, scale, static_cast<float*>(out),
+                                  reinterpret_cast<float*>(static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES),
+                                  workspace_bytes - FSI_WORKSPACE_COUNTER_BYTES, err,
+                                  reinterpret_cast<hipStream_t>(stream));
+    if (rc != 1) return rc;
+  }
   DenseDecodeParams P{};
   P.q = q;
   P.k = k_cache;

@@ -413,13 +413,20 @@ FSI_API int fsi_decode_step_attn(const void* qi, const float* kp, const void* vp
  * gathers them) and the same result, computed in fp32.  Cache strides in
  * elements (unit stride over head_dim); q and out contiguous (B, Hq, head_dim)
  * of `dtype`.  Tokens beyond max_seq are skipped and reported through err.
- * Replaces the gather + repeat_interleave + SDPA of attention.py:339-365. */
+ * Replaces the gather + repeat_interleave + SDPA of attention.py:339-365.
+ * With a workspace of fsi_decode_attn_dense_workspace_size(B, Hq, head_dim,
+ * window, capacity, page_size, max_seq) bytes, fp32 caches with head_dim 64 or
+ * 128 and 16-byte aligned K rows run split over the keys on MFMA (partials in
+ * the workspace, then a merge); otherwise (workspace NULL, bf16, other head
+ * dims) one wave per query head. */
+FSI_API size_t fsi_decode_attn_dense_workspace_size(int64_t B, int64_t Hq, int64_t head_dim, int64_t window,
+                                                    int64_t capacity, int64_t page_size, int64_t max_seq);
 FSI_API int fsi_decode_attn_dense(const void* q, const void* k_cache, const void* v_cache, int64_t ks_b, int64_t ks_h,
                                   int64_t ks_t, int64_t vs_b, int64_t vs_h, int64_t vs_t, int64_t max_seq,
                                   const int32_t* pos_rows, int64_t pos, int64_t window, int64_t page_size,
                                   const int32_t* remote_pages, const int32_t* remote_counts, int64_t capacity,
                                   int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, float scale, int dtype,
-                                  void* out, int* err, void* stream);
+                                  void* out, void* workspace, size_t workspace_bytes, int* err, void* stream);
 
 /* fsi_decode_attn without a workspace argument and without any allocation.
  * No counterpart in the reference: it is for callers that cannot allocate

@@ -200,6 +200,48 @@ def test_dense_decode_attention_parity(fsi, dev, dtype, page, hd):
     assert out.dtype == dtype and Pt.rel_l2(out.cpu().float(), ref.float()) <= tol
 
 
+@pytest.mark.parametrize("hd,Hq,Hkv,page,W,pages_per_seq", [
+    (128, 32, 8, 64, 1024, 20),   # the C4 head shape: 2304 keys in 18 splits per sequence
+    (64, 8, 8, 64, 200, 3),       # one query head per KV head
+    (128, 40, 2, 32, 96, 5),      # 20 query heads per KV head: two MFMA column blocks
+    (64, 12, 3, 16, 0, 6),        # no window, pages only
+])
+def test_dense_decode_attention_f32_split(fsi, dev, hd, Hq, Hkv, page, W, pages_per_seq):
+    """fp32 contiguous-cache decode on the split MFMA kernels (head_dim 64 / 128):
+    per-sequence positions, pages listed twice and pages inside the window (both
+    counted, attention.py:341-352), a sequence with no key at all, against fp64."""
+    print(f"[case] dense decode fp32 hd={hd} Hq={Hq} Hkv={Hkv} page={page} W={W} pages={pages_per_seq}", flush=True)
+    g = torch.Generator().manual_seed(hd + Hq + page + W)
+    B, S = 4, 64 * page
+    c = fsi.FovealKVCache(B, S, Hkv, hd, 16, page, dev, torch.float32)
+    assert not c.paged
+    k = torch.randn(B, Hkv, S, hd, generator=g)
+    v = torch.randn(B, Hkv, S, hd, generator=g)
+    c.load_dense(k.to(dev), v.to(dev))
+    q = torch.randn(B, Hq, hd, generator=g)
+    pos = [S - 1, S // 2 + 7, 3 * page - 1, -1]
+    pages = []
+    for b in range(B):
+        done = max((pos[b] + 1) // page, 0)
+        n = min(pages_per_seq, done) if b < 3 else 0
+        lst = torch.randint(0, max(done, 1), (n,), generator=g).tolist()
+        if n >= 2:
+            lst[1] = lst[0]  # listed twice: counted twice
+        pages.append(lst)
+    cap = max(len(p) for p in pages) or 1
+    rp = torch.full((B, cap), -1, dtype=torch.int32)
+    for b, p in enumerate(pages):
+        if p:
+            rp[b, :len(p)] = torch.tensor(p, dtype=torch.int32)
+    cnt = torch.tensor([len(p) for p in pages], dtype=torch.int32)
+    pos_t = torch.tensor(pos, dtype=torch.int32)
+    out = fsi.decode_attention(q.to(dev), c, pos=pos_t.to(dev), window=W, remote_pages=rp.to(dev),
+                               remote_counts=cnt.to(dev), scale=hd ** -0.5).cpu()
+    ref = A.decode_attention_f64(q, k, v, [max(p, -1) for p in pos], W, pages, page, hd ** -0.5)
+    assert torch.equal(out[3], torch.zeros(Hq, hd))  # no key: 0
+    assert Pt.rel_l2(out[:3], ref[:3].float()) <= 1e-5
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("block,hd,mode", [(8, 16, 0), (16, 24, 0), (64, 64, 0), (8, 32, 1), (32, 100, 1)])
 def test_generic_sparse_attention_parity(fsi, dev, dtype, block, hd, mode):

@@ -64,8 +64,8 @@ C4_TRAFFIC_BYTES = int((161152 + 291023 + 8273 + 3814 + 4352 + 256) * 1024)
 C2_TRAFFIC_BYTES = int((2057 + 2112) * 1024)
 C5_TRAFFIC_BYTES = {0.10: (515 + 64) << 20, 0.25: (1175 + 64) << 20, 0.50: (2249 + 64) << 20}
 # Prefill attention, one step (sa_vmax + sa_vt16 + sparse_attn_lds, profiles/sparse_attention_prefill_16k.md):
-# (878131.0 + 16426.1 + 16467.6) KiB x 1.99983 read + (131315.0 + 32 + 33663.0) KiB written
-PREFILL_ATTN_TRAFFIC_BYTES = int(911024.8 * 1.99983 * 1024 + 165010.0 * 1024)
+# (868556.3 + 16425.6 + 16465.1) KiB x 1.99984 read + (131357.2 + 32 + 32768.0) KiB written
+PREFILL_ATTN_TRAFFIC_BYTES = int(901447.0 * 1.99984 * 1024 + 164157.2 * 1024)
 # C2: wave-level VALU instructions of one score_route_kernel launch (rocprofv3 SQ_INSTS_VALU)
 C2_VALU_INSTS = 70_114_379
 VALU_PEAK_GIPS = 256 * 4 * 2.4 / 4  # G wave64 VALU instructions/s: 256 CUs x 4 SIMDs x 2.4 GHz / 4 cycles
@@ -929,7 +929,8 @@ def main():
             with torch.no_grad():
                 r = fn(fsi, sub_args, dev)
             result["workloads"][name] = {k: r[k] for k in ("metric", "value", "unit", "steps", "ms_per_step",
-                                                           "dtype", "config", "roofline", "cpu_baseline") if k in r}
+                                                           "dtype", "config", "roofline", "cpu_baseline", "fp32",
+                                                           "backward") if k in r}
             torch.cuda.empty_cache()
             print(f"bench: {name} {r['value']} {r['unit']}", file=sys.stderr, flush=True)
     print(json.dumps(result), flush=True)

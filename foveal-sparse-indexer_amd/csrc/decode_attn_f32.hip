@@ -184,6 +184,9 @@ __global__ __launch_bounds__(64 * D_WAVES) void dec32_partial_kernel(D32Params P
   }
 }
 
+// Lane j of the wave takes splits j, j + 64, ...: the maximum and the split
+// weights exp2(m_s - M) come out of two wave reductions, then every lane adds
+// its dims of the weighted split outputs, the splits' loads issued together.
 template <int HD>
 __global__ __launch_bounds__(64 * D_WAVES) void dec32_merge_kernel(D32Params P) {
   const int lane = threadIdx.x & 63;
@@ -194,21 +197,30 @@ __global__ __launch_bounds__(64 * D_WAVES) void dec32_merge_kernel(D32Params P) 
   const int ns = (L.total + D_SPLIT - 1) / D_SPLIT;
   const float* pp = P.part + row * P.n_split * (HD + 2);
   float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = __builtin_fmaxf(M, pp[s * (HD + 2)]);
+  for (int s = lane; s < ns; s += 64) M = __builtin_fmaxf(M, pp[s * (HD + 2)]);
+  M = wave_max(M);
   constexpr int DPL = (HD + 63) / 64;
   float o[DPL] = {};
   float lsum = 0.f;
   if (M != -INFINITY) {
-    for (int s = 0; s < ns; ++s) {
-      const float* q = pp + s * (HD + 2);
-      const float ms = q[0];
-      if (ms == -INFINITY) continue;
-      const float w = __builtin_amdgcn_exp2f(ms - M);
-      lsum += w * q[1];
+    for (int s0 = 0; s0 < ns; s0 += 64) {
+      // lane j: weight of split s0 + j (0 for splits with no key or past the count)
+      float wj = 0.f, lj = 0.f;
+      if (s0 + lane < ns) {
+        const float ms = pp[(s0 + lane) * (HD + 2)];
+        wj = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+        lj = pp[(s0 + lane) * (HD + 2) + 1];
+      }
+      lsum += wave_sum(wj * lj);
+      const int n = ns - s0 < 64 ? ns - s0 : 64;
+      for (int j = 0; j < n; ++j) {
+        const float w = __shfl(wj, j, 64);
+        const float* q = pp + (s0 + j) * (HD + 2) + 2;
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) {
-        const int d = lane + 64 * e;
-        if (d < HD) o[e] += w * q[2 + d];
+        for (int e = 0; e < DPL; ++e) {
+          const int d = lane + 64 * e;
+          if (d < HD) o[e] = fmaf(w, q[d], o[e]);
+        }
       }
     }
   }

@@ -449,7 +449,7 @@ def bench_prefill_attn(fsi, args, dev):
     del q32, k32, v32, out32
     res["backward"] = {"ms": round(bwd_ms, 3), "tflops": round(bwd_tf, 1), "fp32_frac": round(bwd_tf / FP32_PEAK_TFLOPS, 4),
                        "flops": int(2.5 * flops), "kernel": "sab_map + sab_q (statistics, dQ) + sab_kv (dK, dV)",
-                       "note": "fp32 VALU on 64 x 64 LDS tiles; memory O(T hd), no (T, T) tensor"}
+                       "note": "fp32 v_mfma_f32_16x16x4_f32 on 64 x 64 LDS tiles; memory O(T hd), no (T, T) tensor"}
     res["roofline"] = {"bound": "mfma", "achieved": round(tfs, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                        "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": PREFILL_ATTN_TRAFFIC_BYTES,
                        "kernel": "sa_vmax_kernel + sa_vt16_kernel + sparse_attn_lds_kernel (3 launches)", "flops_per_launch": flops}

@@ -13,7 +13,7 @@
 //   dS_ts = P_ts (dP_ts - D_t),    dQ_t = scale sum_s dS_ts k_s,
 //   dK_s = scale sum_t dS_ts q_t   (GQA: summed over the group's query heads).
 //
-// Three kernels, fp32 arithmetic on LDS tiles of 64 queries x 64 keys:
+// Three kernels, fp32 arithmetic (v_mfma_f32_16x16x4_f32) on tiles of 64 queries x 64 keys:
 //   1. sab_map_kernel: for every (query block, key block) pair of the pattern's
 //      block size, its weight class: mode LOCAL_REMOTE 1 = the window reaches
 //      it, 2 = listed (every key counts); mode BLOCK_LIST the listing count.
@@ -58,6 +58,7 @@ struct AbParams {
   int64_t cs_b, cs_q;
   float scale;
   int nb;             // blocks of the pattern: ceil(T / block)
+  bool vec4;          // head_dim one of the tile widths (16 / 32 / 64 / 128), rows 4-element aligned
   int32_t* map;       // (B, nb, nb) weight classes
   float* stat_m;      // (B, Hq, T)
   float* stat_l;
@@ -117,51 +118,81 @@ __device__ __forceinline__ bool sab_tile_live(const AbParams& P, const int32_t* 
   return __syncthreads_or(live) != 0;
 }
 
-// 64 rows of a (T, hd) matrix at row stride rs into an LDS tile of HD (>= hd)
-// columns and row stride HD + 1 floats (rows past T and columns past hd read
-// as 0).
+// 64 rows of a (T, hd) matrix at row stride rs into an LDS tile of row stride
+// HD + 4 floats (rows past T and columns past hd read as 0).  The 4-float pad
+// puts the 8 rows a 128-bit read serves at once on distinct bank groups, and
+// the 16 rows of a column read on two halves of the banks.
+// vec: head_dim == HD and every row starts 4-element aligned (host-checked), so
+// a thread moves 4 consecutive elements at once.
+template <typename T>
+__device__ __forceinline__ f32x4_t ld4(const T* p);
+template <>
+__device__ __forceinline__ f32x4_t ld4<float>(const float* p) { return *reinterpret_cast<const f32x4_t*>(p); }
+template <>
+__device__ __forceinline__ f32x4_t ld4<bf16_t>(const bf16_t* p) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  return f32x4_t{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                 __uint_as_float(w.y & 0xffff0000u)};
+}
 template <typename T, int HD>
-__device__ __forceinline__ void sab_load_tile(const T* base, int64_t rs, int r0, int nrows, int hd, float* tile) {
+__device__ __forceinline__ void sab_load_tile(const T* base, int64_t rs, int r0, int nrows, int hd, float* tile,
+                                              bool vec) {
+  if (vec) {
+    for (int i = threadIdx.x; i < AB_T * HD / 4; i += AB_THREADS) {
+      const int r = i / (HD / 4), d = 4 * (i % (HD / 4));
+      f32x4_t x = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (r0 + r < nrows) x = ld4<T>(base + static_cast<int64_t>(r0 + r) * rs + d);
+      *reinterpret_cast<f32x4_t*>(&tile[r * (HD + 4) + d]) = x;
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < AB_T * HD; i += AB_THREADS) {
     const int r = i / HD, d = i % HD;
-    tile[r * (HD + 1) + d] =
+    tile[r * (HD + 4) + d] =
         r0 + r < nrows && d < hd ? ldv<T>(base, static_cast<int64_t>(r0 + r) * rs + d) : 0.f;
   }
 }
 
-// S[r][c] for this thread's 4 x 4 block (rows 4 ti.., cols 4 tj..): scale x
-// row r of A . row c of B over HD dims.
-template <int HD>
-__device__ __forceinline__ void sab_dot4x4(const float* A, const float* Bm, int ti, int tj, float (&s)[4][4]) {
+// Row `row` (< T) of a (T, hd) matrix as this lane's MFMA k-operand: dims
+// 16 dg + 4 kg .. +4 of every 16-dim group (0 past hd).
+template <typename T, int HD>
+__device__ __forceinline__ void sab_row_frag(const T* base, int64_t rs, int row, int hd, int kg,
+                                             f32x4_t (&f)[HD / 16]) {
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int dg = 0; dg < HD / 16; ++dg)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) s[a][c] = 0.f;
-  for (int d = 0; d < HD; ++d) {
-    float x[4], y[4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a) x[a] = A[(4 * ti + a) * (HD + 1) + d];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) y[c] = Bm[(4 * tj + c) * (HD + 1) + d];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) s[a][c] = fmaf(x[a], y[c], s[a][c]);
-  }
+    for (int kk = 0; kk < 4; ++kk) {
+      const int d = 16 * dg + 4 * kg + kk;
+      f[dg][kk] = d < hd ? ldv<T>(base, static_cast<int64_t>(row) * rs + d) : 0.f;
+    }
 }
 
-// 2. dQ and the row statistics for one (b, h, 64-query tile).
+__device__ __forceinline__ f32x4_t ab_mfma(float a, float b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Class of the block pair (query t, key s), both < T.
+__device__ __forceinline__ int sab_class(const AbParams& P, const int32_t* map_b, int t, int s) {
+  return map_b[static_cast<int64_t>(t / P.block) * P.nb + s / P.block];
+}
+
+// 2. dQ and the row statistics for one (b, h, 64-query tile).  Wave w owns
+//    queries t0 + 16 w .. +16 and keeps their Q and dout rows as the B operand
+//    of S^T = K Q^T and dP^T = V dout^T (v_mfma_f32_16x16x4_f32, k-step kk taking
+//    dims 4 (lane / 16) + kk of each 16-dim group); lane (r, kg) then holds keys
+//    16 t + 4 kg + e of query r, so dS^T's element kk is the B operand of
+//    dQ^T = K^T dS^T for the keys 16 t + 4 kg + kk (K^T read by column from LDS).
 template <typename T, int HD>
 __global__ __launch_bounds__(AB_THREADS) void sab_q_kernel(AbParams P) {
-  constexpr int R = HD + 1;
-  constexpr int DPT = HD / 16;  // dims per thread of dQ
-  __shared__ float Qs[AB_T * R], Os[AB_T * R], Ks[AB_T * R], Vs[AB_T * R];
-  __shared__ float Ss[AB_T * (AB_T + 1)];
-  __shared__ float row_m[AB_T], row_l[AB_T], row_d[AB_T];
+  constexpr int DG = HD / 16, R = HD + 4;
+  __shared__ float Ks[AB_T * R], Vs[AB_T * R];
   const int t0 = blockIdx.x * AB_T;
   const int b = blockIdx.y / P.Hq, h = blockIdx.y % P.Hq;
   const int g = h / (P.Hq / P.Hkv);
-  const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, kg = lane >> 4;
+  const int tq = t0 + 16 * wave + r;             // this lane's query
+  const int tql = tq < P.T ? tq : P.T - 1;       // rows past T read row T - 1, never stored
   const T* q = static_cast<const T*>(P.q) + b * P.qs_b + h * P.qs_h;
   const T* o = static_cast<const T*>(P.o) + b * P.os_b + h * P.os_h;
   const T* dout = static_cast<const T*>(P.dout) + b * P.ds_b + h * P.ds_h;
@@ -169,148 +200,157 @@ __global__ __launch_bounds__(AB_THREADS) void sab_q_kernel(AbParams P) {
   const T* v = static_cast<const T*>(P.v) + b * P.vs_b + g * P.vs_h;
   const int32_t* map_b = P.map + static_cast<int64_t>(b) * P.nb * P.nb;
 
-  sab_load_tile<T, HD>(q, P.qs_t, t0, P.T, P.hd, Qs);
-  sab_load_tile<T, HD>(o, P.os_t, t0, P.T, P.hd, Os);
-  sab_load_tile<T, HD>(dout, P.ds_t, t0, P.T, P.hd, Ks);  // dout staged in Ks for D
-  __syncthreads();
-  if (tid < AB_T) {
-    float d = 0.f;
-    for (int c = 0; c < HD; ++c) d = fmaf(Ks[tid * R + c], Os[tid * R + c], d);
-    row_d[tid] = d;
-    row_m[tid] = -INFINITY;
-    row_l[tid] = 0.f;
-  }
-  __syncthreads();
-  // dout stays in Os from here on (O was only needed for D)
-  for (int i = tid; i < AB_T * R; i += AB_THREADS) Os[i] = Ks[i];
-
-  // pass 1: row maxima and sums over every live key tile
-  for (int s0 = 0; s0 < P.T; s0 += AB_T) {
-    if (!sab_tile_live(P, map_b, t0, s0)) continue;
-    sab_load_tile<T, HD>(k, P.ks_t, s0, P.T, P.hd, Ks);
-    __syncthreads();
-    float s[4][4];
-    sab_dot4x4<HD>(Qs, Ks, ti, tj, s);
+  f32x4_t qf[DG], df[DG];
+  sab_row_frag<T, HD>(q, P.qs_t, tql, P.hd, kg, qf);
+  sab_row_frag<T, HD>(dout, P.ds_t, tql, P.hd, kg, df);
+  float dd;  // D = dout . out of query r
+  {
+    f32x4_t of[DG];
+    sab_row_frag<T, HD>(o, P.os_t, tql, P.hd, kg, of);
+    float part = 0.f;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int t = t0 + 4 * ti + a;
+    for (int dg = 0; dg < DG; ++dg)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int sk = s0 + 4 * tj + c;
-        float w = 0.f;
-        if (t < P.T && sk < P.T) w = sab_weight(P, map_b[static_cast<int64_t>(t / P.block) * P.nb + sk / P.block], t, sk);
-        // the weight folded into the logit: exp(x - m) = w exp(scale q.k - m); m
-        // only stabilises, and every use below takes P with this same m and l
-        Ss[(4 * ti + a) * (AB_T + 1) + 4 * tj + c] = w > 0.f ? s[a][c] * P.scale + logf(w) : -INFINITY;
-      }
-    }
-    __syncthreads();
-    if (tid < AB_T) {  // one thread per row: the online maximum and sum
-      float m = row_m[tid], l = row_l[tid];
-      float cm = -INFINITY;
-      for (int c = 0; c < AB_T; ++c) cm = fmaxf(cm, Ss[tid * (AB_T + 1) + c]);
-      if (cm > -INFINITY) {
-        const float mn = fmaxf(m, cm);
-        float add = 0.f;
-        for (int c = 0; c < AB_T; ++c) {
-          const float x = Ss[tid * (AB_T + 1) + c];
-          if (x > -INFINITY) add += expf(x - mn);
-        }
-        l = (m > -INFINITY ? l * expf(m - mn) : 0.f) + add;
-        row_m[tid] = mn;
-        row_l[tid] = l;
-      }
-    }
-    __syncthreads();
+      for (int kk = 0; kk < 4; ++kk) part = fmaf(df[dg][kk], of[dg][kk], part);
+    dd = sum_rows4(part);
   }
 
-  // pass 2: dQ = scale sum_s dS k_s
-  float acc[4][DPT];
+  // logit of key 16 t + 4 kg + e against query r, with the weight folded in
+  // (exp(x - m) = w exp(scale q.k - m)); -inf where the weight is 0
+  auto logits = [&](int s0, f32x4_t (&st)[4]) {
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int e = 0; e < DPT; ++e) acc[a][e] = 0.f;
-  for (int s0 = 0; s0 < P.T; s0 += AB_T) {
-    if (!sab_tile_live(P, map_b, t0, s0)) continue;
-    sab_load_tile<T, HD>(k, P.ks_t, s0, P.T, P.hd, Ks);
-    sab_load_tile<T, HD>(v, P.vs_t, s0, P.T, P.hd, Vs);
-    __syncthreads();
-    float s[4][4], dp[4][4];
-    sab_dot4x4<HD>(Qs, Ks, ti, tj, s);
-    sab_dot4x4<HD>(Os, Vs, ti, tj, dp);  // dout . v
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int r = 4 * ti + a, t = t0 + r;
-      const float m = row_m[r], l = row_l[r], dd = row_d[r];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int sk = s0 + 4 * tj + c;
-        float ds = 0.f;
-        if (t < P.T && sk < P.T && l > 0.f) {
-          const float w = sab_weight(P, map_b[static_cast<int64_t>(t / P.block) * P.nb + sk / P.block], t, sk);
-          if (w > 0.f) {
-            const float p = w * expf(s[a][c] * P.scale - m) / l;
-            ds = p * (dp[a][c] - dd);
-          }
+      for (int e = 0; e < 4; ++e) {
+        const int sk = s0 + 16 * t + 4 * kg + e;
+        float x = -INFINITY;
+        if (tq < P.T && sk < P.T) {
+          const float w = sab_weight(P, sab_class(P, map_b, tq, sk), tq, sk);
+          if (w > 0.f) x = st[t][e] * P.scale + __logf(w);
         }
-        Ss[r * (AB_T + 1) + 4 * tj + c] = ds;
+        st[t][e] = x;
+      }
+  };
+  // S^T tiles of the 64 keys in Ks against this wave's queries
+  auto scores = [&](f32x4_t (&st)[4], const float* Xs, const f32x4_t (&bf)[DG]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      st[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dg = 0; dg < DG; ++dg) {
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&Xs[(16 * t + r) * R + 16 * dg + 4 * kg]);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) st[t] = ab_mfma(a[kk], bf[dg][kk], st[t]);
       }
     }
+  };
+
+  // pass 1: row maximum and sum over every live key tile (the sum kept per lane
+  // and reduced over the lane group at the end)
+  float m = -INFINITY, lpart = 0.f;
+  for (int s0 = 0; s0 < P.T; s0 += AB_T) {
+    if (!sab_tile_live(P, map_b, t0, s0)) continue;
+    sab_load_tile<T, HD>(k, P.ks_t, s0, P.T, P.hd, Ks, P.vec4);
     __syncthreads();
-    // acc[a][e] += sum_c dS[4 ti + a][c] k[c][tj + 16 e]
-    for (int c = 0; c < AB_T; ++c) {
-      float kk[DPT];
+    f32x4_t st[4];
+    scores(st, Ks, qf);
+    logits(s0, st);
+    float cm = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < DPT; ++e) kk[e] = Ks[c * R + tj + 16 * e];
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const float x = Ss[(4 * ti + a) * (AB_T + 1) + c];
+      for (int e = 0; e < 4; ++e) cm = fmaxf(cm, st[t][e]);
+    cm = max_rows4(cm);
+    if (cm > -INFINITY) {
+      const float mn = fmaxf(m, cm);
+      float add = 0.f;
 #pragma unroll
-        for (int e = 0; e < DPT; ++e) acc[a][e] = fmaf(x, kk[e], acc[a][e]);
-      }
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) add += __expf(st[t][e] - mn);
+      lpart = (m > -INFINITY ? lpart * __expf(m - mn) : 0.f) + add;
+      m = mn;
     }
     __syncthreads();
   }
+  const float l = sum_rows4(lpart);
+
+  // pass 2: dQ^T[dim][query] = scale sum_key K[key][dim] dS[query][key]
+  f32x4_t dqa[DG];
+#pragma unroll
+  for (int dt = 0; dt < DG; ++dt) dqa[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < P.T; s0 += AB_T) {
+    if (!sab_tile_live(P, map_b, t0, s0)) continue;
+    sab_load_tile<T, HD>(k, P.ks_t, s0, P.T, P.hd, Ks, P.vec4);
+    sab_load_tile<T, HD>(v, P.vs_t, s0, P.T, P.hd, Vs, P.vec4);
+    __syncthreads();
+    f32x4_t st[4], dp[4];
+    scores(st, Ks, qf);
+    scores(dp, Vs, df);  // dP^T = V dout^T
+    logits(s0, st);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = l > 0.f ? __expf(st[t][e] - m) / l : 0.f;  // exp(-inf) = 0 where w = 0
+        st[t][e] = p * (dp[t][e] - dd);                            // dS^T
+      }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const float* krow = &Ks[(16 * t + 4 * kg + kk) * R + r];
+#pragma unroll
+        for (int dt = 0; dt < DG; ++dt) dqa[dt] = ab_mfma(krow[16 * dt], st[t][kk], dqa[dt]);
+      }
+    __syncthreads();
+  }
+  // lane (r, kg) holds dQ[query r][dims 16 dt + 4 kg + e]
   const int64_t rowbase = (static_cast<int64_t>(b) * P.Hq + h) * P.T;
+  if (tq < P.T) {
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int t = t0 + 4 * ti + a;
-    if (t >= P.T) continue;
+    for (int dt = 0; dt < DG; ++dt)
 #pragma unroll
-    for (int e = 0; e < DPT; ++e)
-      if (tj + 16 * e < P.hd) P.dq[(rowbase + t) * P.hd + tj + 16 * e] = acc[a][e] * P.scale;
-  }
-  if (tid < AB_T && t0 + tid < P.T) {
-    P.stat_m[rowbase + t0 + tid] = row_m[tid];
-    P.stat_l[rowbase + t0 + tid] = row_l[tid];
-    P.stat_d[rowbase + t0 + tid] = row_d[tid];
+      for (int e = 0; e < 4; ++e) {
+        const int d = 16 * dt + 4 * kg + e;
+        if (d < P.hd) P.dq[(rowbase + tq) * P.hd + d] = dqa[dt][e] * P.scale;
+      }
+    if (kg == 0) {
+      P.stat_m[rowbase + tq] = m;
+      P.stat_l[rowbase + tq] = l;
+      P.stat_d[rowbase + tq] = dd;
+    }
   }
 }
 
 // 3. dK and dV for one (b, g, 64-key tile) over every query tile and query
-//    head of the group.
+//    head of the group.  Wave w owns keys s0 + 16 w .. +16 and keeps their K and
+//    V rows as the B operand of S = Q K^T and dP = dout V^T; lane (r, kg) then
+//    holds queries 16 qt + 4 kg + e of key r, so the elements of P and dS are the
+//    B operands of dV^T = dout^T P and dK^T = Q^T dS (dout^T, Q^T read by column
+//    from LDS).  Accumulated in registers, no atomics.
 template <typename T, int HD>
 __global__ __launch_bounds__(AB_THREADS) void sab_kv_kernel(AbParams P) {
-  constexpr int R = HD + 1;
-  constexpr int DPT = HD / 16;
-  __shared__ float Ks[AB_T * R], Vs[AB_T * R], Qs[AB_T * R], Ds[AB_T * R];
-  __shared__ float Ps[AB_T * (AB_T + 1)];
+  constexpr int DG = HD / 16, R = HD + 4;
+  __shared__ float Qs[AB_T * R], Ds[AB_T * R];
   __shared__ float row_m[AB_T], row_l[AB_T], row_d[AB_T];
   const int s0 = blockIdx.x * AB_T;
   const int b = blockIdx.y / P.Hkv, g = blockIdx.y % P.Hkv;
   const int G = P.Hq / P.Hkv;
-  const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, kg = lane >> 4;
+  const int sk = s0 + 16 * wave + r;       // this lane's key
+  const int skl = sk < P.T ? sk : P.T - 1;
   const T* k = static_cast<const T*>(P.k) + b * P.ks_b + g * P.ks_h;
   const T* v = static_cast<const T*>(P.v) + b * P.vs_b + g * P.vs_h;
   const int32_t* map_b = P.map + static_cast<int64_t>(b) * P.nb * P.nb;
-  sab_load_tile<T, HD>(k, P.ks_t, s0, P.T, P.hd, Ks);
-  sab_load_tile<T, HD>(v, P.vs_t, s0, P.T, P.hd, Vs);
-  // this thread: keys 4 ti + a, dims tj + 16 e
-  float dk[4][DPT], dv[4][DPT];
+  f32x4_t kf[DG], vf[DG];
+  sab_row_frag<T, HD>(k, P.ks_t, skl, P.hd, kg, kf);
+  sab_row_frag<T, HD>(v, P.vs_t, skl, P.hd, kg, vf);
+  f32x4_t dka[DG], dva[DG];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int e = 0; e < DPT; ++e) dk[a][e] = dv[a][e] = 0.f;
+  for (int dt = 0; dt < DG; ++dt) dka[dt] = dva[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
   for (int t0 = 0; t0 < P.T; t0 += AB_T) {
     if (!sab_tile_live(P, map_b, t0, s0)) continue;
     for (int hh = 0; hh < G; ++hh) {
@@ -318,8 +358,8 @@ __global__ __launch_bounds__(AB_THREADS) void sab_kv_kernel(AbParams P) {
       const T* q = static_cast<const T*>(P.q) + b * P.qs_b + h * P.qs_h;
       const T* dout = static_cast<const T*>(P.dout) + b * P.ds_b + h * P.ds_h;
       const int64_t rowbase = (static_cast<int64_t>(b) * P.Hq + h) * P.T;
-      sab_load_tile<T, HD>(q, P.qs_t, t0, P.T, P.hd, Qs);
-      sab_load_tile<T, HD>(dout, P.ds_t, t0, P.T, P.hd, Ds);
+      sab_load_tile<T, HD>(q, P.qs_t, t0, P.T, P.hd, Qs, P.vec4);
+      sab_load_tile<T, HD>(dout, P.ds_t, t0, P.T, P.hd, Ds, P.vec4);
       if (tid < AB_T) {
         const int t = t0 + tid;
         row_m[tid] = t < P.T ? P.stat_m[rowbase + t] : -INFINITY;
@@ -327,73 +367,60 @@ __global__ __launch_bounds__(AB_THREADS) void sab_kv_kernel(AbParams P) {
         row_d[tid] = t < P.T ? P.stat_d[rowbase + t] : 0.f;
       }
       __syncthreads();
-      // this thread's scores: queries 4 ti + a, keys 4 tj + c
-      float s[4][4], dp[4][4];
-      sab_dot4x4<HD>(Qs, Ks, ti, tj, s);
-      sab_dot4x4<HD>(Ds, Vs, ti, tj, dp);
-      float ds[4][4];
+#pragma unroll 1
+      for (int qt = 0; qt < 4; ++qt) {  // not unrolled: K, V, dK and dV already hold 128 registers
+        f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f}, dp = s;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int r = 4 * ti + a, t = t0 + r;
-        const float m = row_m[r], l = row_l[r], dd = row_d[r];
+        for (int dg = 0; dg < DG; ++dg) {
+          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&Qs[(16 * qt + r) * R + 16 * dg + 4 * kg]);
+          const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&Ds[(16 * qt + r) * R + 16 * dg + 4 * kg]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int sk = s0 + 4 * tj + c;
-          float p = 0.f;
-          if (t < P.T && sk < P.T && l > 0.f) {
-            const float w =
-                sab_weight(P, map_b[static_cast<int64_t>(t / P.block) * P.nb + sk / P.block], t, sk);
-            if (w > 0.f) p = w * expf(s[a][c] * P.scale - m) / l;
+          for (int kk = 0; kk < 4; ++kk) {
+            s = ab_mfma(a[kk], kf[dg][kk], s);
+            dp = ab_mfma(c[kk], vf[dg][kk], dp);
           }
-          Ps[r * (AB_T + 1) + 4 * tj + c] = p;
-          ds[a][c] = p * (dp[a][c] - dd);
         }
-      }
-      __syncthreads();
-      // dV[key][dim] += sum_r P[r][key] dout[r][dim]
-      for (int r = 0; r < AB_T; ++r) {
-        float x[DPT];
+        // s[e], dp[e]: query 16 qt + 4 kg + e, key r
+        f32x4_t pp, ds;
 #pragma unroll
-        for (int e = 0; e < DPT; ++e) x[e] = Ds[r * R + tj + 16 * e];
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const float p = Ps[r * (AB_T + 1) + 4 * ti + a];
-#pragma unroll
-          for (int e = 0; e < DPT; ++e) dv[a][e] = fmaf(p, x[e], dv[a][e]);
+        for (int e = 0; e < 4; ++e) {
+          const int rq = 16 * qt + 4 * kg + e, t = t0 + rq;
+          float p = 0.f;
+          const float lq = row_l[rq];
+          if (t < P.T && sk < P.T && lq > 0.f) {
+            const float w = sab_weight(P, sab_class(P, map_b, t, sk), t, sk);
+            if (w > 0.f) p = w * __expf(s[e] * P.scale - row_m[rq]) / lq;
+          }
+          pp[e] = p;
+          ds[e] = p * (dp[e] - row_d[rq]);
         }
-      }
-      __syncthreads();
+        // dV^T[dim][key] += dout[query][dim] P[query][key], dK^T += Q[query][dim] dS[query][key]
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+        for (int kk = 0; kk < 4; ++kk) {
+          const float* drow = &Ds[(16 * qt + 4 * kg + kk) * R + r];
+          const float* qrow = &Qs[(16 * qt + 4 * kg + kk) * R + r];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) Ps[(4 * ti + a) * (AB_T + 1) + 4 * tj + c] = ds[a][c];
-      __syncthreads();
-      // dK[key][dim] += sum_r dS[r][key] q[r][dim]
-      for (int r = 0; r < AB_T; ++r) {
-        float x[DPT];
-#pragma unroll
-        for (int e = 0; e < DPT; ++e) x[e] = Qs[r * R + tj + 16 * e];
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const float d = Ps[r * (AB_T + 1) + 4 * ti + a];
-#pragma unroll
-          for (int e = 0; e < DPT; ++e) dk[a][e] = fmaf(d, x[e], dk[a][e]);
+          for (int dt = 0; dt < DG; ++dt) {
+            dva[dt] = ab_mfma(drow[16 * dt], pp[kk], dva[dt]);
+            dka[dt] = ab_mfma(qrow[16 * dt], ds[kk], dka[dt]);
+          }
         }
       }
       __syncthreads();
     }
   }
+  // lane (r, kg) holds dK, dV [key r][dims 16 dt + 4 kg + e]
   const int64_t kbase = (static_cast<int64_t>(b) * P.Hkv + g) * P.T;
+  if (sk < P.T) {
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int s = s0 + 4 * ti + a;
-    if (s >= P.T) continue;
+    for (int dt = 0; dt < DG; ++dt)
 #pragma unroll
-    for (int e = 0; e < DPT; ++e) {
-      if (tj + 16 * e >= P.hd) continue;
-      P.dk[(kbase + s) * P.hd + tj + 16 * e] = dk[a][e] * P.scale;
-      P.dv[(kbase + s) * P.hd + tj + 16 * e] = dv[a][e];
-    }
+      for (int e = 0; e < 4; ++e) {
+        const int d = 16 * dt + 4 * kg + e;
+        if (d >= P.hd) continue;
+        P.dk[(kbase + sk) * P.hd + d] = dka[dt][e] * P.scale;
+        P.dv[(kbase + sk) * P.hd + d] = dva[dt][e];
+      }
   }
 }
 
@@ -483,6 +510,14 @@ FSI_API int fsi_sparse_attn_bwd(const void* q, int64_t qs_b, int64_t qs_h, int64
   P.cs_q = cs_q;
   P.scale = scale;
   P.nb = (int)nb;
+  {
+    const int64_t esz = dtype == FSI_DTYPE_F32 ? 4 : 2;
+    auto al = [&](const void* p, int64_t sb, int64_t sh, int64_t st) {
+      return reinterpret_cast<uintptr_t>(p) % (4 * esz) == 0 && sb % 4 == 0 && sh % 4 == 0 && st % 4 == 0;
+    };
+    P.vec4 = (head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128) && al(q, qs_b, qs_h, qs_t) && al(k, ks_b, ks_h, ks_t) && al(v, vs_b, vs_h, vs_t) &&
+             al(dout, ds_b, ds_h, ds_t);
+  }
   char* ws = static_cast<char*>(workspace) + FSI_WORKSPACE_COUNTER_BYTES;
   P.map = reinterpret_cast<int32_t*>(ws);
   const size_t st_bytes = align_up(sizeof(float) * static_cast<size_t>(B * Hq * T), 256);

@@ -46,8 +46,18 @@ __global__ __launch_bounds__(256) void token_mean(const float* __restrict__ part
                                                   float* __restrict__ xm) {
   const int d = blockIdx.x * 256 + threadIdx.x;
   if (d >= D) return;
+  // chunk order kept; the loads are issued 16 at a time (a dependent chain of
+  // L2 round trips otherwise)
   float acc = 0.f;
-  for (int c = 0; c < n_chunks; ++c) acc += part[static_cast<int64_t>(c) * D + d];
+  int c = 0;
+  for (; c + 16 <= n_chunks; c += 16) {
+    float v[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = part[static_cast<int64_t>(c + e) * D + d];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc += v[e];
+  }
+  for (; c < n_chunks; ++c) acc += part[static_cast<int64_t>(c) * D + d];
   const float mean = acc / static_cast<float>(M);
   xm[d] = BF16 ? round_bf16(mean) : mean;
 }
@@ -111,7 +121,16 @@ __global__ __launch_bounds__(PR_THREADS) void pooled_route(const float* __restri
   // scores
   for (int b = tid; b < n_blocks; b += PR_THREADS) {
     float acc = 0.f;
-    for (int j = 0; j < index_dim; ++j) acc = fmaf(q[j], ldval<BF16>(keys, static_cast<int64_t>(b) * index_dim + j), acc);
+    if (index_dim == 16) {  // the module's index_dim: the 16 loads issued together
+      float kv[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) kv[j] = ldval<BF16>(keys, static_cast<int64_t>(b) * 16 + j);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc = fmaf(q[j], kv[j], acc);
+    } else {
+      for (int j = 0; j < index_dim; ++j)
+        acc = fmaf(q[j], ldval<BF16>(keys, static_cast<int64_t>(b) * index_dim + j), acc);
+    }
     if (score_scale != 1.0f) {
       if (BF16) acc = round_bf16(acc);
       acc = acc * score_scale;

@@ -100,22 +100,38 @@ __global__ __launch_bounds__(AB_THREADS) void sab_map_kernel(AbParams P) {
   if (bad) set_error(P.err, FSI_ERR_INDEX_RANGE);
 }
 
+// Class of the block pair (query t, key s), both < T.
+__device__ __forceinline__ int sab_class(const AbParams& P, const int32_t* map_b, int t, int s) {
+  return map_b[static_cast<int64_t>(t / P.block) * P.nb + s / P.block];
+}
+
 // Weight of key s for query t (both < T) given the class of their blocks.
 __device__ __forceinline__ float sab_weight(const AbParams& P, int cls, int t, int s) {
   if (P.mode == FSI_SATTN_LOCAL_REMOTE) return ((cls & 2) || (s <= t && s > t - P.window)) ? 1.f : 0.f;
   return static_cast<float>(cls);
 }
 
-// Whether the tile of queries [t0, t0 + 64) and keys [s0, s0 + 64) has a
-// non-zero block class (every thread gets the answer).
-__device__ __forceinline__ bool sab_tile_live(const AbParams& P, const int32_t* map_b, int t0, int s0) {
+// Class of the tile of queries [t0, t0 + 64) and keys [s0, s0 + 64), the
+// same for every thread: the block class (> 0) when the tile lies in one block
+// pair, 0 when every block pair it touches has class 0 (nothing to do), -1
+// when it spans several block pairs and some is non-zero (classes then looked
+// up per element).
+__device__ __forceinline__ int sab_tile_class(const AbParams& P, const int32_t* map_b, int t0, int s0) {
   const int qb0 = t0 / P.block, qb1 = (min(P.T, t0 + AB_T) - 1) / P.block;
   const int kb0 = s0 / P.block, kb1 = (min(P.T, s0 + AB_T) - 1) / P.block;
   const int nq = qb1 - qb0 + 1, nk = kb1 - kb0 + 1;
+  if (nq == 1 && nk == 1) return map_b[static_cast<int64_t>(qb0) * P.nb + kb0];
   int live = 0;
   for (int i = threadIdx.x; i < nq * nk; i += AB_THREADS)
     live |= map_b[static_cast<int64_t>(qb0 + i / nk) * P.nb + kb0 + i % nk] != 0;
-  return __syncthreads_or(live) != 0;
+  return __syncthreads_or(live) != 0 ? -1 : 0;
+}
+
+// Weight of key s for query t (both < T) in a tile of class tcls (as returned by
+// sab_tile_class, non-zero); the block map is read only for a mixed tile.
+__device__ __forceinline__ float sab_tile_weight(const AbParams& P, const int32_t* map_b, int tcls, int t, int s) {
+  if (tcls < 0) return sab_weight(P, sab_class(P, map_b, t, s), t, s);
+  return sab_weight(P, tcls, t, s);
 }
 
 // 64 rows of a (T, hd) matrix at row stride rs into an LDS tile of row stride
@@ -171,9 +187,31 @@ __device__ __forceinline__ f32x4_t ab_mfma(float a, float b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Class of the block pair (query t, key s), both < T.
-__device__ __forceinline__ int sab_class(const AbParams& P, const int32_t* map_b, int t, int s) {
-  return map_b[static_cast<int64_t>(t / P.block) * P.nb + s / P.block];
+// Two floats holding bf16 values as one packed bf16 pair (their upper halves).
+__device__ __forceinline__ uint32_t ab_pk(float x, float y) {
+  return __builtin_amdgcn_perm(__float_as_uint(y), __float_as_uint(x), 0x07060302u);
+}
+// 8 consecutive floats of an LDS row (bf16 values) as a bf16 MFMA operand.
+__device__ __forceinline__ u32x4_t ab_pack8(const float* p) {
+  const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p);
+  const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p + 4);
+  return u32x4_t{ab_pk(a[0], a[1]), ab_pk(a[2], a[3]), ab_pk(b[0], b[1]), ab_pk(b[2], b[3])};
+}
+// Row `row` of a bf16 (T, hd) matrix as this lane's bf16 MFMA operand: dims
+// 32 ks + 8 kg .. +8 of every 32-dim step (0 past hd).
+template <typename T, int HD>
+__device__ __forceinline__ void sab_row_frag_bf(const T* base, int64_t rs, int row, int hd, int kg,
+                                                u32x4_t (&f)[HD / 32]) {
+#pragma unroll
+  for (int ks = 0; ks < HD / 32; ++ks) {
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = 32 * ks + 8 * kg + j;
+      x[j] = d < hd ? ldv<T>(base, static_cast<int64_t>(row) * rs + d) : 0.f;
+    }
+    f[ks] = u32x4_t{ab_pk(x[0], x[1]), ab_pk(x[2], x[3]), ab_pk(x[4], x[5]), ab_pk(x[6], x[7])};
+  }
 }
 
 // 2. dQ and the row statistics for one (b, h, 64-query tile).  Wave w owns
@@ -186,8 +224,10 @@ template <typename T, int HD>
 __global__ __launch_bounds__(AB_THREADS) void sab_q_kernel(AbParams P) {
   constexpr int DG = HD / 16, R = HD + 4;
   __shared__ float Ks[AB_T * R], Vs[AB_T * R];
-  const int t0 = blockIdx.x * AB_T;
-  const int b = blockIdx.y / P.Hq, h = blockIdx.y % P.Hq;
+  // heads fastest and the latest query tiles first: under a causal pattern they
+  // reach the most key tiles, so the longest blocks start first
+  const int t0 = ((P.T + AB_T - 1) / AB_T - 1 - static_cast<int>(blockIdx.x / P.Hq)) * AB_T;
+  const int b = blockIdx.y, h = blockIdx.x % P.Hq;
   const int g = h / (P.Hq / P.Hkv);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kg = lane >> 4;
@@ -200,9 +240,18 @@ __global__ __launch_bounds__(AB_THREADS) void sab_q_kernel(AbParams P) {
   const T* v = static_cast<const T*>(P.v) + b * P.vs_b + g * P.vs_h;
   const int32_t* map_b = P.map + static_cast<int64_t>(b) * P.nb * P.nb;
 
+  // bf16 inputs: S^T and dP^T on v_mfma_f32_16x16x32_bf16 (products of bf16 values
+  // are exact in fp32, so this loses nothing against the fp32 form)
+  constexpr bool BFR = sizeof(T) == 2 && HD >= 32;
+  constexpr int KS32 = HD >= 32 ? HD / 32 : 1;
   f32x4_t qf[DG], df[DG];
   sab_row_frag<T, HD>(q, P.qs_t, tql, P.hd, kg, qf);
   sab_row_frag<T, HD>(dout, P.ds_t, tql, P.hd, kg, df);
+  u32x4_t qb[KS32], db[KS32];
+  if constexpr (BFR) {
+    sab_row_frag_bf<T, HD>(q, P.qs_t, tql, P.hd, kg, qb);
+    sab_row_frag_bf<T, HD>(dout, P.ds_t, tql, P.hd, kg, db);
+  }
   float dd;  // D = dout . out of query r
   {
     f32x4_t of[DG];
@@ -216,8 +265,12 @@ __global__ __launch_bounds__(AB_THREADS) void sab_q_kernel(AbParams P) {
   }
 
   // logit of key 16 t + 4 kg + e against query r, with the weight folded in
-  // (exp(x - m) = w exp(scale q.k - m)); -inf where the weight is 0
-  auto logits = [&](int s0, f32x4_t (&st)[4]) {
+  // (exp(x - m) = w exp(scale q.k - m)); -inf where the weight is 0.  A tile of
+  // one block pair takes its weight from the class (one log per tile); a local
+  // tile of the local/remote pattern tests the window per element.
+  auto logits = [&](int s0, int tcls, f32x4_t (&st)[4]) {
+    const bool all = tcls > 0 && (P.mode == FSI_SATTN_BLOCK_LIST || (tcls & 2));
+    const float lw = all && P.mode == FSI_SATTN_BLOCK_LIST ? __logf(static_cast<float>(tcls)) : 0.f;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -225,22 +278,32 @@ __global__ __launch_bounds__(AB_THREADS) void sab_q_kernel(AbParams P) {
         const int sk = s0 + 16 * t + 4 * kg + e;
         float x = -INFINITY;
         if (tq < P.T && sk < P.T) {
-          const float w = sab_weight(P, sab_class(P, map_b, tq, sk), tq, sk);
-          if (w > 0.f) x = st[t][e] * P.scale + __logf(w);
+          if (all) {
+            x = st[t][e] * P.scale + lw;
+          } else {
+            const float w = sab_tile_weight(P, map_b, tcls, tq, sk);
+            if (w > 0.f) x = st[t][e] * P.scale + __logf(w);
+          }
         }
         st[t][e] = x;
       }
   };
   // S^T tiles of the 64 keys in Ks against this wave's queries
-  auto scores = [&](f32x4_t (&st)[4], const float* Xs, const f32x4_t (&bf)[DG]) {
+  auto scores = [&](f32x4_t (&st)[4], const float* Xs, const f32x4_t (&bf)[DG], const u32x4_t (&bb)[KS32]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       st[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if constexpr (BFR) {
 #pragma unroll
-      for (int dg = 0; dg < DG; ++dg) {
-        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&Xs[(16 * t + r) * R + 16 * dg + 4 * kg]);
+        for (int ks = 0; ks < KS32; ++ks)
+          st[t] = mfma16x16x32(ab_pack8(&Xs[(16 * t + r) * R + 32 * ks + 8 * kg]), bb[ks], st[t]);
+      } else {
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) st[t] = ab_mfma(a[kk], bf[dg][kk], st[t]);
+        for (int dg = 0; dg < DG; ++dg) {
+          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&Xs[(16 * t + r) * R + 16 * dg + 4 * kg]);
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) st[t] = ab_mfma(a[kk], bf[dg][kk], st[t]);
+        }
       }
     }
   };
@@ -249,12 +312,13 @@ __global__ __launch_bounds__(AB_THREADS) void sab_q_kernel(AbParams P) {
   // and reduced over the lane group at the end)
   float m = -INFINITY, lpart = 0.f;
   for (int s0 = 0; s0 < P.T; s0 += AB_T) {
-    if (!sab_tile_live(P, map_b, t0, s0)) continue;
+    const int tcls = sab_tile_class(P, map_b, t0, s0);
+    if (tcls == 0) continue;
     sab_load_tile<T, HD>(k, P.ks_t, s0, P.T, P.hd, Ks, P.vec4);
     __syncthreads();
     f32x4_t st[4];
-    scores(st, Ks, qf);
-    logits(s0, st);
+    scores(st, Ks, qf, qb);
+    logits(s0, tcls, st);
     float cm = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -274,25 +338,27 @@ __global__ __launch_bounds__(AB_THREADS) void sab_q_kernel(AbParams P) {
     __syncthreads();
   }
   const float l = sum_rows4(lpart);
+  const float il = l > 0.f ? 1.f / l : 0.f;
 
   // pass 2: dQ^T[dim][query] = scale sum_key K[key][dim] dS[query][key]
   f32x4_t dqa[DG];
 #pragma unroll
   for (int dt = 0; dt < DG; ++dt) dqa[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < P.T; s0 += AB_T) {
-    if (!sab_tile_live(P, map_b, t0, s0)) continue;
+    const int tcls = sab_tile_class(P, map_b, t0, s0);
+    if (tcls == 0) continue;
     sab_load_tile<T, HD>(k, P.ks_t, s0, P.T, P.hd, Ks, P.vec4);
     sab_load_tile<T, HD>(v, P.vs_t, s0, P.T, P.hd, Vs, P.vec4);
     __syncthreads();
     f32x4_t st[4], dp[4];
-    scores(st, Ks, qf);
-    scores(dp, Vs, df);  // dP^T = V dout^T
-    logits(s0, st);
+    scores(st, Ks, qf, qb);
+    scores(dp, Vs, df, db);  // dP^T = V dout^T
+    logits(s0, tcls, st);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float p = l > 0.f ? __expf(st[t][e] - m) / l : 0.f;  // exp(-inf) = 0 where w = 0
+        const float p = l > 0.f ? __expf(st[t][e] - m) * il : 0.f;  // exp(-inf) = 0 where w = 0
         st[t][e] = p * (dp[t][e] - dd);                            // dS^T
       }
 #pragma unroll
@@ -333,9 +399,11 @@ template <typename T, int HD>
 __global__ __launch_bounds__(AB_THREADS) void sab_kv_kernel(AbParams P) {
   constexpr int DG = HD / 16, R = HD + 4;
   __shared__ float Qs[AB_T * R], Ds[AB_T * R];
-  __shared__ float row_m[AB_T], row_l[AB_T], row_d[AB_T];
-  const int s0 = blockIdx.x * AB_T;
-  const int b = blockIdx.y / P.Hkv, g = blockIdx.y % P.Hkv;
+  __shared__ float row_m[AB_T], row_il[AB_T], row_d[AB_T];
+  // heads fastest and the earliest key tiles first: under a causal pattern the
+  // most query tiles reach them, so the longest blocks start first
+  const int s0 = static_cast<int>(blockIdx.x / P.Hkv) * AB_T;
+  const int b = blockIdx.y, g = blockIdx.x % P.Hkv;
   const int G = P.Hq / P.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kg = lane >> 4;
@@ -344,15 +412,28 @@ __global__ __launch_bounds__(AB_THREADS) void sab_kv_kernel(AbParams P) {
   const T* k = static_cast<const T*>(P.k) + b * P.ks_b + g * P.ks_h;
   const T* v = static_cast<const T*>(P.v) + b * P.vs_b + g * P.vs_h;
   const int32_t* map_b = P.map + static_cast<int64_t>(b) * P.nb * P.nb;
-  f32x4_t kf[DG], vf[DG];
-  sab_row_frag<T, HD>(k, P.ks_t, skl, P.hd, kg, kf);
-  sab_row_frag<T, HD>(v, P.vs_t, skl, P.hd, kg, vf);
+  constexpr bool BFR = sizeof(T) == 2 && HD >= 32;  // S and dP on bf16 MFMA (exact products)
+  constexpr int KS32 = HD >= 32 ? HD / 32 : 1;
+  f32x4_t kf[BFR ? 1 : DG], vf[BFR ? 1 : DG];
+  u32x4_t kb[KS32], vb[KS32];
+  if constexpr (BFR) {
+    sab_row_frag_bf<T, HD>(k, P.ks_t, skl, P.hd, kg, kb);
+    sab_row_frag_bf<T, HD>(v, P.vs_t, skl, P.hd, kg, vb);
+  } else {
+    sab_row_frag<T, HD>(k, P.ks_t, skl, P.hd, kg, kf);
+    sab_row_frag<T, HD>(v, P.vs_t, skl, P.hd, kg, vf);
+  }
   f32x4_t dka[DG], dva[DG];
 #pragma unroll
   for (int dt = 0; dt < DG; ++dt) dka[dt] = dva[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int t0 = 0; t0 < P.T; t0 += AB_T) {
-    if (!sab_tile_live(P, map_b, t0, s0)) continue;
+    const int tcls = sab_tile_class(P, map_b, t0, s0);
+    if (tcls == 0) continue;
+    // weight of the whole tile when it lies in one block pair and needs no window test
+    const float wall = tcls > 0 && (P.mode == FSI_SATTN_BLOCK_LIST || (tcls & 2))
+                           ? (P.mode == FSI_SATTN_BLOCK_LIST ? static_cast<float>(tcls) : 1.f)
+                           : 0.f;
     for (int hh = 0; hh < G; ++hh) {
       const int h = g * G + hh;
       const T* q = static_cast<const T*>(P.q) + b * P.qs_b + h * P.qs_h;
@@ -362,22 +443,31 @@ __global__ __launch_bounds__(AB_THREADS) void sab_kv_kernel(AbParams P) {
       sab_load_tile<T, HD>(dout, P.ds_t, t0, P.T, P.hd, Ds, P.vec4);
       if (tid < AB_T) {
         const int t = t0 + tid;
+        const float lq = t < P.T ? P.stat_l[rowbase + t] : 0.f;
         row_m[tid] = t < P.T ? P.stat_m[rowbase + t] : -INFINITY;
-        row_l[tid] = t < P.T ? P.stat_l[rowbase + t] : 0.f;
+        row_il[tid] = lq > 0.f ? 1.f / lq : 0.f;
         row_d[tid] = t < P.T ? P.stat_d[rowbase + t] : 0.f;
       }
       __syncthreads();
 #pragma unroll 1
       for (int qt = 0; qt < 4; ++qt) {  // not unrolled: K, V, dK and dV already hold 128 registers
         f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f}, dp = s;
+        if constexpr (BFR) {
 #pragma unroll
-        for (int dg = 0; dg < DG; ++dg) {
-          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&Qs[(16 * qt + r) * R + 16 * dg + 4 * kg]);
-          const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&Ds[(16 * qt + r) * R + 16 * dg + 4 * kg]);
+          for (int ks = 0; ks < KS32; ++ks) {
+            s = mfma16x16x32(ab_pack8(&Qs[(16 * qt + r) * R + 32 * ks + 8 * kg]), kb[ks], s);
+            dp = mfma16x16x32(ab_pack8(&Ds[(16 * qt + r) * R + 32 * ks + 8 * kg]), vb[ks], dp);
+          }
+        } else {
 #pragma unroll
-          for (int kk = 0; kk < 4; ++kk) {
-            s = ab_mfma(a[kk], kf[dg][kk], s);
-            dp = ab_mfma(c[kk], vf[dg][kk], dp);
+          for (int dg = 0; dg < DG; ++dg) {
+            const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&Qs[(16 * qt + r) * R + 16 * dg + 4 * kg]);
+            const f32x4_t c = *reinterpret_cast<const f32x4_t*>(&Ds[(16 * qt + r) * R + 16 * dg + 4 * kg]);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+              s = ab_mfma(a[kk], kf[dg][kk], s);
+              dp = ab_mfma(c[kk], vf[dg][kk], dp);
+            }
           }
         }
         // s[e], dp[e]: query 16 qt + 4 kg + e, key r
@@ -386,10 +476,10 @@ __global__ __launch_bounds__(AB_THREADS) void sab_kv_kernel(AbParams P) {
         for (int e = 0; e < 4; ++e) {
           const int rq = 16 * qt + 4 * kg + e, t = t0 + rq;
           float p = 0.f;
-          const float lq = row_l[rq];
-          if (t < P.T && sk < P.T && lq > 0.f) {
-            const float w = sab_weight(P, sab_class(P, map_b, t, sk), t, sk);
-            if (w > 0.f) p = w * __expf(s[e] * P.scale - row_m[rq]) / lq;
+          const float il = row_il[rq];
+          if (t < P.T && sk < P.T && il > 0.f) {
+            const float w = wall > 0.f ? wall : sab_tile_weight(P, map_b, tcls, t, sk);
+            if (w > 0.f) p = w * __expf(s[e] * P.scale - row_m[rq]) * il;
           }
           pp[e] = p;
           ds[e] = p * (dp[e] - row_d[rq]);
@@ -458,7 +548,7 @@ FSI_API int fsi_sparse_attn_bwd(const void* q, int64_t qs_b, int64_t qs_h, int64
   FSI_CHECK_ARG(B > 0 && T > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && block > 0, FSI_ERR_SHAPE,
                 "sparse_attn_bwd: B=%lld T=%lld Hq=%lld Hkv=%lld block=%lld", (long long)B, (long long)T,
                 (long long)Hq, (long long)Hkv, (long long)block);
-  FSI_CHECK_ARG(T <= (int64_t(1) << 30) && B * Hq <= 65535 && (T + AB_T - 1) / AB_T <= 0x7fffffff, FSI_ERR_SHAPE,
+  FSI_CHECK_ARG(T <= (int64_t(1) << 30) && B <= 65535 && (T + AB_T - 1) / AB_T * Hq <= 0x7fffffff, FSI_ERR_SHAPE,
                 "sparse_attn_bwd: sizes beyond range");
   const int64_t nb = (T + block - 1) / block;
   FSI_CHECK_ARG(nb <= 65535 && B * nb * nb <= (int64_t(1) << 31), FSI_ERR_SHAPE,
@@ -531,7 +621,8 @@ FSI_API int fsi_sparse_attn_bwd(const void* q, int64_t qs_b, int64_t qs_h, int64
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   sab_map_kernel<<<dim3(static_cast<unsigned>(nb), static_cast<unsigned>(B)), AB_THREADS, 0, st>>>(P);
   const unsigned ntiles = static_cast<unsigned>((T + AB_T - 1) / AB_T);
-  const dim3 gq(ntiles, static_cast<unsigned>(B * Hq)), gkv(ntiles, static_cast<unsigned>(B * Hkv));
+  const dim3 gq(ntiles * static_cast<unsigned>(Hq), static_cast<unsigned>(B)),
+      gkv(ntiles * static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
   auto run = [&](auto hd_tag) {
     constexpr int HD = decltype(hd_tag)::value;
     if (dtype == FSI_DTYPE_F32) {

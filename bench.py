@@ -413,7 +413,7 @@ def bench_prefill_attn(fsi, args, dev):
                    "mean_remote_pages": round(float(counts.float().mean()), 2)})
     # the backward (fsi_sparse_attn_bwd, training through FovealSparseAttention.forward)
     # on the same pattern, timed eagerly: 2.5 x the forward's products (Q K^T and dP
-    # recomputed, dV, dQ, dK), fp32 arithmetic
+    # recomputed, dV, dQ, dK)
     from foveal_sparse_indexer_amd import attention as fatt
 
     out4 = out.transpose(1, 2)
@@ -447,9 +447,12 @@ def bench_prefill_attn(fsi, args, dev):
                    "frac": round(tf32 / FP32_PEAK_TFLOPS, 4),
                    "kernel": "vt32_kernel + sparse_attn_f32_kernel<128> (v_mfma_f32_16x16x4_f32)"}
     del q32, k32, v32, out32
-    res["backward"] = {"ms": round(bwd_ms, 3), "tflops": round(bwd_tf, 1), "fp32_frac": round(bwd_tf / FP32_PEAK_TFLOPS, 4),
-                       "flops": int(2.5 * flops), "kernel": "sab_map + sab_q (statistics, dQ) + sab_kv (dK, dV)",
-                       "note": "fp32 v_mfma_f32_16x16x4_f32 on 64 x 64 LDS tiles; memory O(T hd), no (T, T) tensor"}
+    res["backward"] = {"ms": round(bwd_ms, 3), "tflops": round(bwd_tf, 1), "peak": BF16_PEAK_TFLOPS,
+                       "frac": round(bwd_tf / BF16_PEAK_TFLOPS, 4),
+                       "flops": int(2.5 * flops), "kernel": "sab_map + sab_q_bf (statistics, dQ) + sab_kv_bf (dK, dV)",
+                       "note": "every product on v_mfma_f32_16x16x32_bf16 over bf16 LDS tiles (row-major and "
+                               "transposed); P and dS enter dV / dK / dQ as bf16 hi + lo pairs (~2^-17 relative), "
+                               "fp32 accumulation; memory O(T hd), no (T, T) tensor"}
     res["roofline"] = {"bound": "mfma", "achieved": round(tfs, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                        "frac": round(tfs / BF16_PEAK_TFLOPS, 4), "traffic": PREFILL_ATTN_TRAFFIC_BYTES,
                        "kernel": "sa_vmax_kernel + sa_vt16_kernel + sparse_attn_lds_kernel (3 launches)", "flops_per_launch": flops}

@@ -13,7 +13,9 @@
 //   dS_ts = P_ts (dP_ts - D_t),    dQ_t = scale sum_s dS_ts k_s,
 //   dK_s = scale sum_t dS_ts q_t   (GQA: summed over the group's query heads).
 //
-// Three kernels, fp32 arithmetic (v_mfma_f32_16x16x4_f32) on tiles of 64 queries x 64 keys:
+// Three kernels on tiles of 64 queries x 64 keys (bf16 inputs with head_dim 32 / 64 / 128:
+// the sab_*_bf kernels below, every product on bf16 MFMA; otherwise fp32 arithmetic on
+// v_mfma_f32_16x16x4_f32):
 //   1. sab_map_kernel: for every (query block, key block) pair of the pattern's
 //      block size, its weight class: mode LOCAL_REMOTE 1 = the window reaches
 //      it, 2 = listed (every key counts); mode BLOCK_LIST the listing count.
@@ -132,6 +134,50 @@ __device__ __forceinline__ int sab_tile_class(const AbParams& P, const int32_t* 
 __device__ __forceinline__ float sab_tile_weight(const AbParams& P, const int32_t* map_b, int tcls, int t, int s) {
   if (tcls < 0) return sab_weight(P, sab_class(P, map_b, t, s), t, s);
   return sab_weight(P, tcls, t, s);
+}
+
+// Logits of keys s0 + 16 t + 4 kg + e against query tq (S^T accumulators st),
+// with the weight folded in (exp(x - m) = w exp(scale q.k - m)); -inf where the
+// weight is 0 or the query / key is past T.  A tile of one block pair takes its
+// weight from the class (one log per tile); a local tile of the local/remote
+// pattern tests the window per element.
+__device__ __forceinline__ void sab_logits(const AbParams& P, const int32_t* map_b, int tq, int kg, int s0, int tcls,
+                                           f32x4_t (&st)[4]) {
+  if (tcls > 0 && (P.mode == FSI_SATTN_BLOCK_LIST || (tcls & 2))) {
+    // one weight for the whole tile: keys below lim are valid
+    const float lw = P.mode == FSI_SATTN_BLOCK_LIST ? __logf(static_cast<float>(tcls)) : 0.f;
+    const int lim = tq < P.T ? P.T : 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int sk = s0 + 16 * t + 4 * kg + e;
+        st[t][e] = sk < lim ? st[t][e] * P.scale + lw : -INFINITY;
+      }
+  } else if (tcls > 0) {
+    // local/remote tile reached by the window only: tq - W < sk <= tq (< T)
+    const int hi = tq < P.T ? tq : -1, lo = tq - P.window;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int sk = s0 + 16 * t + 4 * kg + e;
+        st[t][e] = sk <= hi && sk > lo ? st[t][e] * P.scale : -INFINITY;
+      }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int sk = s0 + 16 * t + 4 * kg + e;
+        float x = -INFINITY;
+        if (tq < P.T && sk < P.T) {
+          const float w = sab_tile_weight(P, map_b, tcls, tq, sk);
+          if (w > 0.f) x = st[t][e] * P.scale + __logf(w);
+        }
+        st[t][e] = x;
+      }
+  }
 }
 
 // 64 rows of a (T, hd) matrix at row stride rs into an LDS tile of row stride
@@ -264,30 +310,7 @@ __global__ __launch_bounds__(AB_THREADS) void sab_q_kernel(AbParams P) {
     dd = sum_rows4(part);
   }
 
-  // logit of key 16 t + 4 kg + e against query r, with the weight folded in
-  // (exp(x - m) = w exp(scale q.k - m)); -inf where the weight is 0.  A tile of
-  // one block pair takes its weight from the class (one log per tile); a local
-  // tile of the local/remote pattern tests the window per element.
-  auto logits = [&](int s0, int tcls, f32x4_t (&st)[4]) {
-    const bool all = tcls > 0 && (P.mode == FSI_SATTN_BLOCK_LIST || (tcls & 2));
-    const float lw = all && P.mode == FSI_SATTN_BLOCK_LIST ? __logf(static_cast<float>(tcls)) : 0.f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int sk = s0 + 16 * t + 4 * kg + e;
-        float x = -INFINITY;
-        if (tq < P.T && sk < P.T) {
-          if (all) {
-            x = st[t][e] * P.scale + lw;
-          } else {
-            const float w = sab_tile_weight(P, map_b, tcls, tq, sk);
-            if (w > 0.f) x = st[t][e] * P.scale + __logf(w);
-          }
-        }
-        st[t][e] = x;
-      }
-  };
+  auto logits = [&](int s0, int tcls, f32x4_t (&st)[4]) { sab_logits(P, map_b, tq, kg, s0, tcls, st); };
   // S^T tiles of the 64 keys in Ks against this wave's queries
   auto scores = [&](f32x4_t (&st)[4], const float* Xs, const f32x4_t (&bf)[DG], const u32x4_t (&bb)[KS32]) {
 #pragma unroll
@@ -514,6 +537,427 @@ __global__ __launch_bounds__(AB_THREADS) void sab_kv_kernel(AbParams P) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 inputs with head_dim 32 / 64 / 128 and 4-element-aligned rows: every
+// product on v_mfma_f32_16x16x32_bf16.  Tiles sit in LDS as bf16, row-major at
+// stride HD + 8 (the 8 rows a 128-bit read serves at once start on distinct
+// bank quads) and, where a product contracts over the tile's rows, transposed
+// as well at stride 64 + 4 (the 16 rows of a 64-bit read on distinct bank
+// pairs).  P and dS enter their products as a pair of bf16 operands hi + lo
+// (hi = the value rounded to bf16, lo = the remainder rounded): the pair holds
+// the value to ~2^-17 relative, the other operand is an exact bf16 input and
+// the MFMA accumulates in fp32.
+//
+// A lane's k slots 8 kg + e of a 32-row product: rows 4 kg + e (e < 4) and
+// 16 + 4 kg + e - 4 (e >= 4) of the 32, i.e. the rows its two 16 x 16
+// accumulators of P / dS hold, so those enter the MFMA where they are; the
+// transposed tile is read at the same rows.
+// ---------------------------------------------------------------------------
+constexpr int BF_TS = AB_T + 4;  // transposed-tile row stride (bf16 elements)
+
+// Rows [r0, r0 + 64) of a (T, HD) bf16 matrix move in two halves, so the next
+// tile's loads can be in flight while the current tile is used: bf_load reads
+// them into registers (thread = 4-row group x 4-dim group, one 8-byte load per
+// row; rows past T read as 0), bf_store writes them to the row-major tile rt
+// and, when TR, to the transposed tile tt after a 4 x 4 transpose in registers.
+// Transposed rows d hold their 4-column groups in the order g ^ ((d >> 4) & 3):
+// the 16 rows 4 apart that one store instruction writes then land on distinct
+// banks, and the 16 consecutive rows of an operand read (one swizzle value)
+// stay on distinct bank pairs.
+template <int HD>
+constexpr int bf_rounds() { return HD >= 64 ? HD / 64 : 1; }
+
+// Rows past T re-read row T - 1: every product that uses them is multiplied by
+// a zero P / dS or masked, so they only need to be finite.
+template <int HD>
+__device__ __forceinline__ void bf_load(const bf16_t* base, int64_t rs, int r0, int T, uint2 (&x)[bf_rounds<HD>()][4]) {
+  constexpr int DGN = HD / 4, QG = AB_THREADS / DGN;
+  const int dg = threadIdx.x % DGN;
+  const int qg0 = QG * bf_rounds<HD>() > AB_T / 4 ? (threadIdx.x / DGN) % (AB_T / 4) : threadIdx.x / DGN;
+#pragma unroll
+  for (int rr = 0; rr < bf_rounds<HD>(); ++rr)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = r0 + 4 * (qg0 + rr * QG) + j;
+      x[rr][j] = *reinterpret_cast<const uint2*>(base + static_cast<int64_t>(r < T ? r : T - 1) * rs + 4 * dg);
+    }
+}
+
+template <int HD, bool TR>
+__device__ __forceinline__ void bf_store(const uint2 (&x)[bf_rounds<HD>()][4], bf16_t* rt, bf16_t* tt) {
+  constexpr int DGN = HD / 4, QG = AB_THREADS / DGN;
+  const int dg = threadIdx.x % DGN, qg0 = threadIdx.x / DGN;
+#pragma unroll
+  for (int rr = 0; rr < bf_rounds<HD>(); ++rr) {
+    const int qg = qg0 + rr * QG;
+    if (QG * bf_rounds<HD>() > AB_T / 4 && qg >= AB_T / 4) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint2*>(&rt[(4 * qg + j) * (HD + 8) + 4 * dg]) = x[rr][j];
+    if constexpr (TR) {
+      constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;  // low / high bf16 of each source
+      const uint2* y = x[rr];
+      bf16_t* t = &tt[4 * dg * BF_TS + 4 * (qg ^ ((dg >> 2) & 3))];
+      *reinterpret_cast<uint2*>(t) =
+          make_uint2(__builtin_amdgcn_perm(y[1].x, y[0].x, LO), __builtin_amdgcn_perm(y[3].x, y[2].x, LO));
+      *reinterpret_cast<uint2*>(t + BF_TS) =
+          make_uint2(__builtin_amdgcn_perm(y[1].x, y[0].x, HI), __builtin_amdgcn_perm(y[3].x, y[2].x, HI));
+      *reinterpret_cast<uint2*>(t + 2 * BF_TS) =
+          make_uint2(__builtin_amdgcn_perm(y[1].y, y[0].y, LO), __builtin_amdgcn_perm(y[3].y, y[2].y, LO));
+      *reinterpret_cast<uint2*>(t + 3 * BF_TS) =
+          make_uint2(__builtin_amdgcn_perm(y[1].y, y[0].y, HI), __builtin_amdgcn_perm(y[3].y, y[2].y, HI));
+    }
+  }
+}
+
+// Class of the tile pair (queries [t0, t0 + 64), keys [s0, s0 + 64)) computed by
+// one thread (sab_tile_class without the workgroup reduction).
+__device__ __forceinline__ int sab_pair_class(const AbParams& P, const int32_t* map_b, int t0, int s0) {
+  const int qb0 = t0 / P.block, qb1 = (min(P.T, t0 + AB_T) - 1) / P.block;
+  const int kb0 = s0 / P.block, kb1 = (min(P.T, s0 + AB_T) - 1) / P.block;
+  if (qb0 == qb1 && kb0 == kb1) return map_b[static_cast<int64_t>(qb0) * P.nb + kb0];
+  int live = 0;
+  for (int qb = qb0; qb <= qb1; ++qb)
+    for (int kb = kb0; kb <= kb1; ++kb) live |= map_b[static_cast<int64_t>(qb) * P.nb + kb] != 0;
+  return live ? -1 : 0;
+}
+
+// The live tiles among [c0, c0 + 256) of one tile row (ROW: the query tile t0 is
+// fixed, key tiles vary) or column (the key tile is fixed), ascending, with their
+// classes, compacted into idx / cls; returns their number (every thread).
+template <bool ROW>
+__device__ __forceinline__ int sab_live_chunk(const AbParams& P, const int32_t* map_b, int fixed0, int c0, int ntiles,
+                                              int* idx, int* cls, int* wcount) {
+  const int i = c0 + static_cast<int>(threadIdx.x), lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int c = 0;
+  if (i < ntiles) c = ROW ? sab_pair_class(P, map_b, fixed0, i * AB_T) : sab_pair_class(P, map_b, i * AB_T, fixed0);
+  const uint64_t bal = __ballot(c != 0);
+  if (lane == 0) wcount[wave] = __popcll(bal);
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < AB_THREADS / 64; ++w) {
+    base += w < wave ? wcount[w] : 0;
+    total += wcount[w];
+  }
+  if (c != 0) {
+    const int pos = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0));
+    idx[pos] = i;
+    cls[pos] = c;
+  }
+  __syncthreads();
+  return total;
+}
+
+// Row `row` of a row-major tile as the lane's operand of a 32-dim step ks.
+template <int HD>
+__device__ __forceinline__ u32x4_t bf_row(const bf16_t* rt, int row, int ks, int kg) {
+  return *reinterpret_cast<const u32x4_t*>(&rt[row * (HD + 8) + 32 * ks + 8 * kg]);
+}
+// Row `row` of a transposed tile at the lane's k slots of the 32 columns
+// [32 j, 32 j + 32): column groups 8 j + kg and 8 j + 4 + kg, stored swizzled.
+__device__ __forceinline__ u32x4_t bf_trow(const bf16_t* tt, int row, int j, int kg) {
+  const int sw = kg ^ ((row >> 4) & 3);
+  const uint2 a = *reinterpret_cast<const uint2*>(&tt[row * BF_TS + 32 * j + 4 * sw]);
+  const uint2 b = *reinterpret_cast<const uint2*>(&tt[row * BF_TS + 32 * j + 16 + 4 * sw]);
+  return u32x4_t{a.x, a.y, b.x, b.y};
+}
+
+__device__ __forceinline__ uint32_t bf_cvt2(float a, float b) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// The lane's 8 k-slot values (4 of accumulator a, then 4 of b) as hi + lo bf16 operands.
+__device__ __forceinline__ void bf_split8(const f32x4_t& a, const f32x4_t& b, u32x4_t& hi, u32x4_t& lo) {
+  float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t h = bf_cvt2(x[2 * w], x[2 * w + 1]);
+    hi[w] = h;
+    lo[w] = bf_cvt2(x[2 * w] - __uint_as_float(h << 16), x[2 * w + 1] - __uint_as_float(h & 0xffff0000u));
+  }
+}
+
+// dQ and the row statistics (as sab_q_kernel) with K, V as bf16 tiles, K also
+// transposed for dQ^T = K^T dS^T.
+template <int HD>
+__global__ __launch_bounds__(AB_THREADS, 2) void sab_q_bf_kernel(AbParams P) {
+  constexpr int DG = HD / 16, KS32 = HD / 32, RS = HD + 8;
+  __shared__ __attribute__((aligned(16))) bf16_t Kr[AB_T * RS], Vr[AB_T * RS], Kt[HD * BF_TS];
+  __shared__ int lt_idx[AB_THREADS], lt_cls[AB_THREADS], wcount[AB_THREADS / 64];
+  const int ntiles = (P.T + AB_T - 1) / AB_T;
+  const int t0 = (ntiles - 1 - static_cast<int>(blockIdx.x / P.Hq)) * AB_T;
+  const int b = blockIdx.y, h = blockIdx.x % P.Hq;
+  const int g = h / (P.Hq / P.Hkv);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, kg = lane >> 4;
+  const int tq = t0 + 16 * wave + r;
+  const int tql = tq < P.T ? tq : P.T - 1;
+  const bf16_t* q = static_cast<const bf16_t*>(P.q) + b * P.qs_b + h * P.qs_h;
+  const bf16_t* o = static_cast<const bf16_t*>(P.o) + b * P.os_b + h * P.os_h;
+  const bf16_t* dout = static_cast<const bf16_t*>(P.dout) + b * P.ds_b + h * P.ds_h;
+  const bf16_t* k = static_cast<const bf16_t*>(P.k) + b * P.ks_b + g * P.ks_h;
+  const bf16_t* v = static_cast<const bf16_t*>(P.v) + b * P.vs_b + g * P.vs_h;
+  const int32_t* map_b = P.map + static_cast<int64_t>(b) * P.nb * P.nb;
+
+  u32x4_t qb[KS32], db[KS32];
+  sab_row_frag_bf<bf16_t, HD>(q, P.qs_t, tql, P.hd, kg, qb);
+  sab_row_frag_bf<bf16_t, HD>(dout, P.ds_t, tql, P.hd, kg, db);
+  float dd;  // D = dout . out of query r
+  {
+    f32x4_t of[DG], df[DG];
+    sab_row_frag<bf16_t, HD>(o, P.os_t, tql, P.hd, kg, of);
+    sab_row_frag<bf16_t, HD>(dout, P.ds_t, tql, P.hd, kg, df);
+    float part = 0.f;
+#pragma unroll
+    for (int d = 0; d < DG; ++d)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) part = fmaf(df[d][kk], of[d][kk], part);
+    dd = sum_rows4(part);
+  }
+  auto scores = [&](f32x4_t (&st)[4], const bf16_t* Xr, const u32x4_t (&bb)[KS32]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      st[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS32; ++ks) st[t] = mfma16x16x32(bf_row<HD>(Xr, 16 * t + r, ks, kg), bb[ks], st[t]);
+    }
+  };
+
+  // pass 1: row maximum and sum over the live key tiles (listed 256 at a time;
+  // the next tile's K rows load while this one's scores run)
+  float m = -INFINITY, lpart = 0.f;
+  uint2 xk[bf_rounds<HD>()][4], xv[bf_rounds<HD>()][4];
+  for (int c0 = 0; c0 < ntiles; c0 += AB_THREADS) {
+   const int n = sab_live_chunk<true>(P, map_b, t0, c0, ntiles, lt_idx, lt_cls, wcount);
+   if (n > 0) bf_load<HD>(k, P.ks_t, lt_idx[0] * AB_T, P.T, xk);
+   for (int li = 0; li < n; ++li) {
+    const int s0 = __builtin_amdgcn_readfirstlane(lt_idx[li]) * AB_T;
+    const int tcls = __builtin_amdgcn_readfirstlane(lt_cls[li]);
+    bf_store<HD, false>(xk, Kr, nullptr);
+    __syncthreads();
+    if (li + 1 < n) bf_load<HD>(k, P.ks_t, lt_idx[li + 1] * AB_T, P.T, xk);
+    f32x4_t st[4];
+    scores(st, Kr, qb);
+    sab_logits(P, map_b, tq, kg, s0, tcls, st);
+    float cm = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cm = fmaxf(cm, st[t][e]);
+    cm = max_rows4(cm);
+    if (cm > -INFINITY) {
+      const float mn = fmaxf(m, cm);
+      float add = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) add += __expf(st[t][e] - mn);
+      lpart = (m > -INFINITY ? lpart * __expf(m - mn) : 0.f) + add;
+      m = mn;
+    }
+    __syncthreads();
+   }
+  }
+  const float l = sum_rows4(lpart);
+  const float il = l > 0.f ? 1.f / l : 0.f;
+
+  // pass 2: dQ^T[dim][query] = sum_key K^T[dim][key] dS^T[key][query]
+  f32x4_t dqa[DG];
+#pragma unroll
+  for (int dt = 0; dt < DG; ++dt) dqa[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < ntiles; c0 += AB_THREADS) {
+   const int n = sab_live_chunk<true>(P, map_b, t0, c0, ntiles, lt_idx, lt_cls, wcount);
+   if (n > 0) {
+     bf_load<HD>(k, P.ks_t, lt_idx[0] * AB_T, P.T, xk);
+     bf_load<HD>(v, P.vs_t, lt_idx[0] * AB_T, P.T, xv);
+   }
+   for (int li = 0; li < n; ++li) {
+    const int s0 = __builtin_amdgcn_readfirstlane(lt_idx[li]) * AB_T;
+    const int tcls = __builtin_amdgcn_readfirstlane(lt_cls[li]);
+    bf_store<HD, true>(xk, Kr, Kt);
+    bf_store<HD, false>(xv, Vr, nullptr);
+    __syncthreads();
+    if (li + 1 < n) {
+      bf_load<HD>(k, P.ks_t, lt_idx[li + 1] * AB_T, P.T, xk);
+      bf_load<HD>(v, P.vs_t, lt_idx[li + 1] * AB_T, P.T, xv);
+    }
+    f32x4_t st[4], dp[4];
+    scores(st, Kr, qb);
+    scores(dp, Vr, db);  // dP^T = V dout^T
+    sab_logits(P, map_b, tq, kg, s0, tcls, st);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = l > 0.f ? __expf(st[t][e] - m) * il : 0.f;
+        st[t][e] = p * (dp[t][e] - dd);  // dS^T
+      }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      u32x4_t hi, lo;
+      bf_split8(st[2 * j], st[2 * j + 1], hi, lo);
+#pragma unroll
+      for (int dt = 0; dt < DG; ++dt) {
+        const u32x4_t a = bf_trow(Kt, 16 * dt + r, j, kg);
+        dqa[dt] = mfma16x16x32(a, hi, dqa[dt]);
+        dqa[dt] = mfma16x16x32(a, lo, dqa[dt]);
+      }
+    }
+    __syncthreads();
+   }
+  }
+  const int64_t rowbase = (static_cast<int64_t>(b) * P.Hq + h) * P.T;
+  if (tq < P.T) {
+#pragma unroll
+    for (int dt = 0; dt < DG; ++dt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) P.dq[(rowbase + tq) * P.hd + 16 * dt + 4 * kg + e] = dqa[dt][e] * P.scale;
+    if (kg == 0) {
+      P.stat_m[rowbase + tq] = m;
+      P.stat_l[rowbase + tq] = l;
+      P.stat_d[rowbase + tq] = dd;
+    }
+  }
+}
+
+// dK and dV (as sab_kv_kernel) with Q and dout as bf16 tiles, both also
+// transposed for dK^T = Q^T dS and dV^T = dout^T P.
+template <int HD>
+__global__ __launch_bounds__(AB_THREADS, 2) void sab_kv_bf_kernel(AbParams P) {
+  constexpr int DG = HD / 16, KS32 = HD / 32, RS = HD + 8;
+  __shared__ __attribute__((aligned(16))) bf16_t Qr[AB_T * RS], Dr[AB_T * RS], Qt[HD * BF_TS], Dt[HD * BF_TS];
+  __shared__ float row_m[AB_T], row_il[AB_T], row_d[AB_T];
+  __shared__ int lt_idx[AB_THREADS], lt_cls[AB_THREADS], wcount[AB_THREADS / 64];
+  const int ntiles = (P.T + AB_T - 1) / AB_T;
+  const int s0 = static_cast<int>(blockIdx.x / P.Hkv) * AB_T;
+  const int b = blockIdx.y, g = blockIdx.x % P.Hkv;
+  const int G = P.Hq / P.Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, kg = lane >> 4;
+  const int sk = s0 + 16 * wave + r;
+  const int skl = sk < P.T ? sk : P.T - 1;
+  const bf16_t* k = static_cast<const bf16_t*>(P.k) + b * P.ks_b + g * P.ks_h;
+  const bf16_t* v = static_cast<const bf16_t*>(P.v) + b * P.vs_b + g * P.vs_h;
+  const int32_t* map_b = P.map + static_cast<int64_t>(b) * P.nb * P.nb;
+  u32x4_t kb[KS32], vb[KS32];
+  sab_row_frag_bf<bf16_t, HD>(k, P.ks_t, skl, P.hd, kg, kb);
+  sab_row_frag_bf<bf16_t, HD>(v, P.vs_t, skl, P.hd, kg, vb);
+  f32x4_t dka[DG], dva[DG];
+#pragma unroll
+  for (int dt = 0; dt < DG; ++dt) dka[dt] = dva[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // (live query tile, query head of the group) pairs, the tiles listed 256 at a
+  // time; the next pair's Q and dout rows and row statistics load while this
+  // pair's products run
+  uint2 xq[bf_rounds<HD>()][4], xd[bf_rounds<HD>()][4];
+  float nm = -INFINITY, nl = 0.f, nd = 0.f;
+  auto load_pair = [&](int li, int hh) {
+    const int t0 = __builtin_amdgcn_readfirstlane(lt_idx[li]) * AB_T, h = g * G + hh;
+    bf_load<HD>(static_cast<const bf16_t*>(P.q) + b * P.qs_b + h * P.qs_h, P.qs_t, t0, P.T, xq);
+    bf_load<HD>(static_cast<const bf16_t*>(P.dout) + b * P.ds_b + h * P.ds_h, P.ds_t, t0, P.T, xd);
+    const int64_t rowbase = (static_cast<int64_t>(b) * P.Hq + h) * P.T;
+    const int t = t0 + tid;
+    if (tid < AB_T && t < P.T) {
+      nm = P.stat_m[rowbase + t];
+      nl = P.stat_l[rowbase + t];
+      nd = P.stat_d[rowbase + t];
+    } else {
+      nm = -INFINITY;
+      nl = 0.f;
+      nd = 0.f;
+    }
+  };
+  for (int c0 = 0; c0 < ntiles; c0 += AB_THREADS) {
+   const int n = sab_live_chunk<false>(P, map_b, s0, c0, ntiles, lt_idx, lt_cls, wcount);
+   if (n > 0) load_pair(0, 0);
+   for (int it = 0; it < n * G; ++it) {
+    const int li = it / G;
+    const int t0 = __builtin_amdgcn_readfirstlane(lt_idx[li]) * AB_T;
+    const int tcls = __builtin_amdgcn_readfirstlane(lt_cls[li]);
+    // one weight for the whole tile (wall > 0), the window only (win), or per element
+    const float wall = tcls > 0 && (P.mode == FSI_SATTN_BLOCK_LIST || (tcls & 2))
+                           ? (P.mode == FSI_SATTN_BLOCK_LIST ? static_cast<float>(tcls) : 1.f)
+                           : 0.f;
+    const bool win = tcls > 0 && wall == 0.f;
+    {
+      bf_store<HD, true>(xq, Qr, Qt);
+      bf_store<HD, true>(xd, Dr, Dt);
+      if (tid < AB_T) {
+        row_m[tid] = nm;
+        row_il[tid] = nl > 0.f ? 1.f / nl : 0.f;
+        row_d[tid] = nd;
+      }
+      __syncthreads();
+      if (it + 1 < n * G) load_pair((it + 1) / G, (it + 1) % G);
+      // two 16-query sub-tiles at a time (not unrolled: the operand reads of all
+      // four would be hoisted past the register budget)
+#pragma unroll 1
+      for (int j = 0; j < 2; ++j) {
+        f32x4_t pp[2], ds[2];  // P, dS [query 32 j + 16 i + 4 kg + e][key r]
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int qt = 2 * j + i;
+          f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f}, dp = s;
+#pragma unroll
+          for (int ks = 0; ks < KS32; ++ks) {
+            s = mfma16x16x32(bf_row<HD>(Qr, 16 * qt + r, ks, kg), kb[ks], s);
+            dp = mfma16x16x32(bf_row<HD>(Dr, 16 * qt + r, ks, kg), vb[ks], dp);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int rq = 16 * qt + 4 * kg + e, t = t0 + rq;
+            const float il = row_il[rq];
+            float p;
+            if (wall > 0.f) {
+              const float x = wall * __expf(s[e] * P.scale - row_m[rq]) * il;
+              p = t < P.T && sk < P.T && il > 0.f ? x : 0.f;
+            } else if (win) {
+              const float x = __expf(s[e] * P.scale - row_m[rq]) * il;
+              p = t < P.T && sk <= t && sk > t - P.window && il > 0.f ? x : 0.f;
+            } else {
+              p = 0.f;
+              if (t < P.T && sk < P.T && il > 0.f) {
+                const float w = sab_tile_weight(P, map_b, tcls, t, sk);
+                if (w > 0.f) p = w * __expf(s[e] * P.scale - row_m[rq]) * il;
+              }
+            }
+            pp[i][e] = p;
+            ds[i][e] = p * (dp[e] - row_d[rq]);
+          }
+        }
+        // dV^T[dim][key] += dout^T[dim][query] P[query][key], dK^T += Q^T dS
+        u32x4_t ph, pl, dh, dl;
+        bf_split8(pp[0], pp[1], ph, pl);
+        bf_split8(ds[0], ds[1], dh, dl);
+#pragma unroll
+        for (int dt = 0; dt < DG; ++dt) {
+          const u32x4_t ad = bf_trow(Dt, 16 * dt + r, j, kg);
+          const u32x4_t aq = bf_trow(Qt, 16 * dt + r, j, kg);
+          dva[dt] = mfma16x16x32(ad, ph, dva[dt]);
+          dva[dt] = mfma16x16x32(ad, pl, dva[dt]);
+          dka[dt] = mfma16x16x32(aq, dh, dka[dt]);
+          dka[dt] = mfma16x16x32(aq, dl, dka[dt]);
+        }
+      }
+      __syncthreads();
+    }
+   }
+  }
+  const int64_t kbase = (static_cast<int64_t>(b) * P.Hkv + g) * P.T;
+  if (sk < P.T) {
+#pragma unroll
+    for (int dt = 0; dt < DG; ++dt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = 16 * dt + 4 * kg + e;
+        P.dk[(kbase + sk) * P.hd + d] = dka[dt][e] * P.scale;
+        P.dv[(kbase + sk) * P.hd + d] = dva[dt][e];
+      }
+  }
+}
+
 // Workspace: the counter area (left untouched), the block map, then m, l, D.
 size_t sab_map_bytes(int64_t B, int64_t T, int64_t block) {
   const int64_t nb = (T + block - 1) / block;
@@ -629,6 +1073,13 @@ FSI_API int fsi_sparse_attn_bwd(const void* q, int64_t qs_b, int64_t qs_h, int64
       sab_q_kernel<float, HD><<<gq, AB_THREADS, 0, st>>>(P);
       sab_kv_kernel<float, HD><<<gkv, AB_THREADS, 0, st>>>(P);
     } else {
+      if constexpr (HD >= 32) {
+        if (head_dim == HD && P.vec4) {
+          sab_q_bf_kernel<HD><<<gq, AB_THREADS, 0, st>>>(P);
+          sab_kv_bf_kernel<HD><<<gkv, AB_THREADS, 0, st>>>(P);
+          return;
+        }
+      }
       sab_q_kernel<bf16_t, HD><<<gq, AB_THREADS, 0, st>>>(P);
       sab_kv_kernel<bf16_t, HD><<<gkv, AB_THREADS, 0, st>>>(P);
     }

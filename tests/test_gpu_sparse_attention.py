@@ -322,6 +322,8 @@ GRAD_CASES = [
     (1, 6, 1, 96, 256, 128, 130, 2, 0, torch.bfloat16),     # head_dim 96 (padded to 128), 128-token blocks
     (2, 4, 2, 64, 256, 32, 0, 4, 1, torch.float32),         # block lists, repeated entries
     (1, 2, 2, 16, 128, 16, 0, 6, 1, torch.bfloat16),
+    (2, 4, 2, 64, 200, 32, 0, 3, 1, torch.bfloat16),       # bf16 tile kernels: block lists, tiles over two blocks
+    (1, 4, 4, 32, 256, 64, 100, 3, 0, torch.bfloat16),      # bf16 tile kernels at head_dim 32
 ]
 
 

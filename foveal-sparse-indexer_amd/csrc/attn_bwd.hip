@@ -574,6 +574,19 @@ __device__ __forceinline__ void bf_load(const bf16_t* base, int64_t rs, int r0, 
   constexpr int DGN = HD / 4, QG = AB_THREADS / DGN;
   const int dg = threadIdx.x % DGN;
   const int qg0 = QG * bf_rounds<HD>() > AB_T / 4 ? (threadIdx.x / DGN) % (AB_T / 4) : threadIdx.x / DGN;
+  if (r0 + AB_T <= T) {
+    // every row inside: a scalar row base and 32-bit lane offsets (row strides
+    // below 2^24 elements, host-checked), one add per load
+    const char* rb = reinterpret_cast<const char*>(base + static_cast<int64_t>(r0) * rs);
+    const uint32_t rsb = static_cast<uint32_t>(rs) * 2u;
+    const uint32_t lo = static_cast<uint32_t>(4 * qg0) * rsb + 8u * static_cast<uint32_t>(dg);
+#pragma unroll
+    for (int rr = 0; rr < bf_rounds<HD>(); ++rr)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        x[rr][j] = *reinterpret_cast<const uint2*>(rb + (lo + static_cast<uint32_t>(4 * rr * QG + j) * rsb));
+    return;
+  }
 #pragma unroll
   for (int rr = 0; rr < bf_rounds<HD>(); ++rr)
 #pragma unroll
@@ -619,6 +632,51 @@ __device__ __forceinline__ int sab_pair_class(const AbParams& P, const int32_t* 
   for (int qb = qb0; qb <= qb1; ++qb)
     for (int kb = kb0; kb <= kb1; ++kb) live |= map_b[static_cast<int64_t>(qb) * P.nb + kb] != 0;
   return live ? -1 : 0;
+}
+
+// sab_logits in log2 units for the bf16 kernels: x2 = scale log2(e) q.k + log2(w)
+// (sl2 = scale log2(e)), -inf where the weight is 0 or the query / key is past
+// T.  Tiles of one weight with every query and key inside T take one fma per score.
+__device__ __forceinline__ void sab_logits2(const AbParams& P, const int32_t* map_b, int tq, int kg, int t0, int s0,
+                                            int tcls, float sl2, f32x4_t (&st)[4]) {
+  if (tcls > 0 && (P.mode == FSI_SATTN_BLOCK_LIST || (tcls & 2))) {
+    const float lw2 = P.mode == FSI_SATTN_BLOCK_LIST ? __log2f(static_cast<float>(tcls)) : 0.f;
+    if (t0 + AB_T <= P.T && s0 + AB_T <= P.T) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st[t][e] = fmaf(st[t][e], sl2, lw2);
+    } else {
+      const int lim = tq < P.T ? P.T : 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          st[t][e] = s0 + 16 * t + 4 * kg + e < lim ? fmaf(st[t][e], sl2, lw2) : -INFINITY;
+    }
+  } else if (tcls > 0) {
+    const int hi = tq < P.T ? tq : -1, lo = tq - P.window;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int sk = s0 + 16 * t + 4 * kg + e;
+        st[t][e] = sk <= hi && sk > lo ? st[t][e] * sl2 : -INFINITY;
+      }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int sk = s0 + 16 * t + 4 * kg + e;
+        float x = -INFINITY;
+        if (tq < P.T && sk < P.T) {
+          const float w = sab_tile_weight(P, map_b, tcls, tq, sk);
+          if (w > 0.f) x = fmaf(st[t][e], sl2, __log2f(w));
+        }
+        st[t][e] = x;
+      }
+  }
 }
 
 // The live tiles among [c0, c0 + 256) of one tile row (ROW: the query tile t0 is
@@ -725,8 +783,9 @@ __global__ __launch_bounds__(AB_THREADS, 2) void sab_q_bf_kernel(AbParams P) {
     }
   };
 
-  // pass 1: row maximum and sum over the live key tiles (listed 256 at a time;
-  // the next tile's K rows load while this one's scores run)
+  // pass 1: row maximum and sum (log2 units) over the live key tiles (listed 256
+  // at a time; the next tile's K rows load while this one's scores run)
+  const float sl2 = P.scale * 1.4426950408889634f;
   float m = -INFINITY, lpart = 0.f;
   uint2 xk[bf_rounds<HD>()][4], xv[bf_rounds<HD>()][4];
   for (int c0 = 0; c0 < ntiles; c0 += AB_THREADS) {
@@ -740,7 +799,7 @@ __global__ __launch_bounds__(AB_THREADS, 2) void sab_q_bf_kernel(AbParams P) {
     if (li + 1 < n) bf_load<HD>(k, P.ks_t, lt_idx[li + 1] * AB_T, P.T, xk);
     f32x4_t st[4];
     scores(st, Kr, qb);
-    sab_logits(P, map_b, tq, kg, s0, tcls, st);
+    sab_logits2(P, map_b, tq, kg, t0, s0, tcls, sl2, st);
     float cm = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -753,15 +812,17 @@ __global__ __launch_bounds__(AB_THREADS, 2) void sab_q_bf_kernel(AbParams P) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) add += __expf(st[t][e] - mn);
-      lpart = (m > -INFINITY ? lpart * __expf(m - mn) : 0.f) + add;
+        for (int e = 0; e < 4; ++e) add += __builtin_amdgcn_exp2f(st[t][e] - mn);
+      lpart = (m > -INFINITY ? lpart * __builtin_amdgcn_exp2f(m - mn) : 0.f) + add;
       m = mn;
     }
     __syncthreads();
    }
   }
   const float l = sum_rows4(lpart);
-  const float il = l > 0.f ? 1.f / l : 0.f;
+  // log2 of the row's softmax denominator: P = exp2(x2 - lse2); +inf for a row
+  // with no key (every P 0, no NaN)
+  const float lse2 = l > 0.f ? m + __log2f(l) : INFINITY;
 
   // pass 2: dQ^T[dim][query] = sum_key K^T[dim][key] dS^T[key][query]
   f32x4_t dqa[DG];
@@ -786,12 +847,12 @@ __global__ __launch_bounds__(AB_THREADS, 2) void sab_q_bf_kernel(AbParams P) {
     f32x4_t st[4], dp[4];
     scores(st, Kr, qb);
     scores(dp, Vr, db);  // dP^T = V dout^T
-    sab_logits(P, map_b, tq, kg, s0, tcls, st);
+    sab_logits2(P, map_b, tq, kg, t0, s0, tcls, sl2, st);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float p = l > 0.f ? __expf(st[t][e] - m) * il : 0.f;
+        const float p = __builtin_amdgcn_exp2f(st[t][e] - lse2);
         st[t][e] = p * (dp[t][e] - dd);  // dS^T
       }
 #pragma unroll
@@ -815,7 +876,7 @@ __global__ __launch_bounds__(AB_THREADS, 2) void sab_q_bf_kernel(AbParams P) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) P.dq[(rowbase + tq) * P.hd + 16 * dt + 4 * kg + e] = dqa[dt][e] * P.scale;
     if (kg == 0) {
-      P.stat_m[rowbase + tq] = m;
+      P.stat_m[rowbase + tq] = lse2;  // the bf16 kernels keep log2 units
       P.stat_l[rowbase + tq] = l;
       P.stat_d[rowbase + tq] = dd;
     }
@@ -828,10 +889,11 @@ template <int HD>
 __global__ __launch_bounds__(AB_THREADS, 2) void sab_kv_bf_kernel(AbParams P) {
   constexpr int DG = HD / 16, KS32 = HD / 32, RS = HD + 8;
   __shared__ __attribute__((aligned(16))) bf16_t Qr[AB_T * RS], Dr[AB_T * RS], Qt[HD * BF_TS], Dt[HD * BF_TS];
-  __shared__ float row_m[AB_T], row_il[AB_T], row_d[AB_T];
+  __shared__ float row_lse[AB_T], row_d[AB_T];  // log2 softmax denominators (+inf past T), D
   __shared__ int lt_idx[AB_THREADS], lt_cls[AB_THREADS], wcount[AB_THREADS / 64];
   const int ntiles = (P.T + AB_T - 1) / AB_T;
   const int s0 = static_cast<int>(blockIdx.x / P.Hkv) * AB_T;
+  const float sl2 = P.scale * 1.4426950408889634f;
   const int b = blockIdx.y, g = blockIdx.x % P.Hkv;
   const int G = P.Hq / P.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -852,7 +914,7 @@ __global__ __launch_bounds__(AB_THREADS, 2) void sab_kv_bf_kernel(AbParams P) {
   // time; the next pair's Q and dout rows and row statistics load while this
   // pair's products run
   uint2 xq[bf_rounds<HD>()][4], xd[bf_rounds<HD>()][4];
-  float nm = -INFINITY, nl = 0.f, nd = 0.f;
+  float nlse = INFINITY, nd = 0.f;
   auto load_pair = [&](int li, int hh) {
     const int t0 = __builtin_amdgcn_readfirstlane(lt_idx[li]) * AB_T, h = g * G + hh;
     bf_load<HD>(static_cast<const bf16_t*>(P.q) + b * P.qs_b + h * P.qs_h, P.qs_t, t0, P.T, xq);
@@ -860,12 +922,10 @@ __global__ __launch_bounds__(AB_THREADS, 2) void sab_kv_bf_kernel(AbParams P) {
     const int64_t rowbase = (static_cast<int64_t>(b) * P.Hq + h) * P.T;
     const int t = t0 + tid;
     if (tid < AB_T && t < P.T) {
-      nm = P.stat_m[rowbase + t];
-      nl = P.stat_l[rowbase + t];
+      nlse = P.stat_m[rowbase + t];
       nd = P.stat_d[rowbase + t];
     } else {
-      nm = -INFINITY;
-      nl = 0.f;
+      nlse = INFINITY;
       nd = 0.f;
     }
   };
@@ -876,17 +936,17 @@ __global__ __launch_bounds__(AB_THREADS, 2) void sab_kv_bf_kernel(AbParams P) {
     const int li = it / G;
     const int t0 = __builtin_amdgcn_readfirstlane(lt_idx[li]) * AB_T;
     const int tcls = __builtin_amdgcn_readfirstlane(lt_cls[li]);
-    // one weight for the whole tile (wall > 0), the window only (win), or per element
-    const float wall = tcls > 0 && (P.mode == FSI_SATTN_BLOCK_LIST || (tcls & 2))
-                           ? (P.mode == FSI_SATTN_BLOCK_LIST ? static_cast<float>(tcls) : 1.f)
-                           : 0.f;
-    const bool win = tcls > 0 && wall == 0.f;
+    // one weight for the whole tile (all: log2 weight lw2; inner: every query and
+    // key inside T), the window only (win), or per element
+    const bool all = tcls > 0 && (P.mode == FSI_SATTN_BLOCK_LIST || (tcls & 2));
+    const bool win = tcls > 0 && !all;
+    const bool inner = t0 + AB_T <= P.T && s0 + AB_T <= P.T;
+    const float lw2 = all && P.mode == FSI_SATTN_BLOCK_LIST ? __log2f(static_cast<float>(tcls)) : 0.f;
     {
       bf_store<HD, true>(xq, Qr, Qt);
       bf_store<HD, true>(xd, Dr, Dt);
       if (tid < AB_T) {
-        row_m[tid] = nm;
-        row_il[tid] = nl > 0.f ? 1.f / nl : 0.f;
+        row_lse[tid] = nlse;
         row_d[tid] = nd;
       }
       __syncthreads();
@@ -908,19 +968,19 @@ __global__ __launch_bounds__(AB_THREADS, 2) void sab_kv_bf_kernel(AbParams P) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int rq = 16 * qt + 4 * kg + e, t = t0 + rq;
-            const float il = row_il[rq];
+            const float lse = row_lse[rq];  // +inf past T: P = 0
             float p;
-            if (wall > 0.f) {
-              const float x = wall * __expf(s[e] * P.scale - row_m[rq]) * il;
-              p = t < P.T && sk < P.T && il > 0.f ? x : 0.f;
+            if (all) {
+              p = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, lw2 - lse));
+              if (!inner) p = sk < P.T ? p : 0.f;
             } else if (win) {
-              const float x = __expf(s[e] * P.scale - row_m[rq]) * il;
-              p = t < P.T && sk <= t && sk > t - P.window && il > 0.f ? x : 0.f;
+              const float x = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, -lse));
+              p = sk <= t && sk > t - P.window ? x : 0.f;
             } else {
               p = 0.f;
-              if (t < P.T && sk < P.T && il > 0.f) {
+              if (t < P.T && sk < P.T) {
                 const float w = sab_tile_weight(P, map_b, tcls, t, sk);
-                if (w > 0.f) p = w * __expf(s[e] * P.scale - row_m[rq]) * il;
+                if (w > 0.f) p = __builtin_amdgcn_exp2f(fmaf(s[e], sl2, __log2f(w) - lse));
               }
             }
             pp[i][e] = p;
@@ -1074,7 +1134,10 @@ FSI_API int fsi_sparse_attn_bwd(const void* q, int64_t qs_b, int64_t qs_h, int64
       sab_kv_kernel<float, HD><<<gkv, AB_THREADS, 0, st>>>(P);
     } else {
       if constexpr (HD >= 32) {
-        if (head_dim == HD && P.vec4) {
+        // the bf16 kernels address a tile's rows with 32-bit offsets: row strides below 2^24
+        const bool short_rows = qs_t < (int64_t(1) << 24) && ks_t < (int64_t(1) << 24) &&
+                                vs_t < (int64_t(1) << 24) && ds_t < (int64_t(1) << 24);
+        if (head_dim == HD && P.vec4 && short_rows) {
           sab_q_bf_kernel<HD><<<gq, AB_THREADS, 0, st>>>(P);
           sab_kv_bf_kernel<HD><<<gkv, AB_THREADS, 0, st>>>(P);
           return;

@@ -734,20 +734,27 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
 #pragma unroll
           for (int j = 0; j < 4; ++j) sv[8 * hc + 4 * tile + j] = st[hc][qt][tile][j];
       if (!nomask) {
+        // Branch-free: a score is kept when its sign word is negative (a taken key
+        // inside T, and inside / outside the window for a local / listed pair).
+        // wlo >= -1 keeps every difference inside int range.
+        // (the lane's key offset passes through an empty asm so the compiler forms
+        // these values here instead of holding them in registers across the loop)
+        int lk = 4 * grp;
+        asm volatile("" : "+v"(lk));
+        const int wlo = myq - (P.window < myq + 1 ? P.window : myq + 1);  // window: wlo < key <= myq
+        const int wmode = P.mode == FSI_SATTN_LOCAL_REMOTE ? (local ? 1 : 2) : 0;
 #pragma unroll
         for (int hc = 0; hc < 2; ++hc)
 #pragma unroll
           for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              const int tau = 16 * tile + 4 * grp + j;
+              const int tau = 16 * tile + lk + j;
               const int key = kc0 + SA_CHUNK * hc + tau;
-              bool ok = tau < (hc ? hi1 : hi0) && key < P.T;
-              if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
-                const bool in_win = key <= myq && key > myq - P.window;
-                ok = ok && (local ? in_win : !in_win);
-              }
-              if (!ok) sv[8 * hc + 4 * tile + j] = -INFINITY;
+              int keep = (tau - (hc ? hi1 : hi0)) & (key - P.T);
+              const int inw = (key - myq - 1) & (wlo - key);
+              keep &= wmode == 0 ? -1 : (wmode == 1 ? inw : ~inw);
+              sv[8 * hc + 4 * tile + j] = keep < 0 ? sv[8 * hc + 4 * tile + j] : -INFINITY;
             }
       }
       // The running max (log2 units) moves only when a score exceeds it by more

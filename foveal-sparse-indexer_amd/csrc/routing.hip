@@ -555,9 +555,19 @@ __global__ __launch_bounds__(64 * SR_WAVES) void score_route_kernel(const void* 
           acc = fmaf(qa[4 * w + 2], f.z, acc);
           acc = fmaf(qa[4 * w + 3], f.w, acc);
         }
-        sa[slot] = acc / sqrt_d;
+        sa[slot] = acc;
       }
     }
+  }
+  // / sqrt(d): a multiply by the exact reciprocal when sqrt(d) is a power of two
+  // (the same rounding as the division), the division otherwise
+  if ((__float_as_uint(sqrt_d) & 0x007fffffu) == 0u) {  // uniform
+    const float inv = 1.f / sqrt_d;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) sa[i] *= inv;
+  } else {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) sa[i] /= sqrt_d;
   }
   if (row_q < Q)
     select_row<PL, E, false>(sa, N, row_q, static_cast<int64_t>(b) * Q + row_q, sp, out_idx, out_cnt, out_mass, lk[wave],

@@ -44,6 +44,7 @@ struct D32Params {
   int S;
   const int32_t* pos_rows;
   int pos, window, page;
+  int page_shift;         // log2(page) for a power-of-two page, else -1
   const int32_t* remote;  // (B, cap)
   const int32_t* counts;  // (B)
   int cap;
@@ -70,12 +71,22 @@ __device__ __forceinline__ KeyList key_list(const D32Params& P, int b) {
 }
 
 // Token of list entry i, or -1 (past the list, or a page outside the cache: *bad).
+// (Branch-free selects here measured slower: their live values took the kernel
+// from 120 to 196 VGPRs, i.e. from four to two waves per SIMD.)
 __device__ __forceinline__ int key_token(const D32Params& P, const KeyList& L, int b, int i, bool& bad) {
   if (i < L.n_local) return L.ls + i < P.S ? L.ls + i : -1;
   if (i >= L.total) return -1;
-  const int j = (i - L.n_local) / P.page;
+  const int ir = i - L.n_local;
+  int j, w;
+  if (P.page_shift >= 0) {  // uniform
+    j = ir >> P.page_shift;
+    w = ir & (P.page - 1);
+  } else {
+    j = ir / P.page;
+    w = ir % P.page;
+  }
   const int pg = P.remote[static_cast<int64_t>(b) * P.cap + j];
-  const int t = pg * P.page + (i - L.n_local) % P.page;
+  const int t = pg * P.page + w;
   if (pg >= 0 && t < P.S) return t;
   bad = true;
   return -1;
@@ -160,9 +171,13 @@ __global__ __launch_bounds__(64 * D_WAVES) void dec32_partial_kernel(D32Params P
     for (int kk = 0; kk < 4; ++kk) {
       const int tv = tok[t][kk];
       const float* vrow = vb + static_cast<int64_t>(tv >= 0 ? tv : 0) * P.vs_t + r;
+      // loads from the clamped row (always inside the cache), then a select: a
+      // masked token's V is 0 (an unwritten row may hold anything)
       float vv[DG];
 #pragma unroll
-      for (int dt = 0; dt < DG; ++dt) vv[dt] = tv >= 0 ? vrow[16 * dt] : 0.f;
+      for (int dt = 0; dt < DG; ++dt) vv[dt] = vrow[16 * dt];
+#pragma unroll
+      for (int dt = 0; dt < DG; ++dt) vv[dt] = tv >= 0 ? vv[dt] : 0.f;
 #pragma unroll
       for (int dt = 0; dt < DG; ++dt) acc[dt] = mfma4(st[t][kk], vv[dt], acc[dt]);
     }
@@ -276,6 +291,7 @@ int run(const float* q, const float* k, const float* v, int64_t ks_b, int64_t ks
   P.pos = static_cast<int>(pos);
   P.window = static_cast<int>(window);
   P.page = static_cast<int>(page_size);
+  P.page_shift = page_size > 0 && (page_size & (page_size - 1)) == 0 ? __builtin_ctzll(static_cast<uint64_t>(page_size)) : -1;
   P.remote = remote_pages;
   P.counts = remote_counts;
   P.cap = static_cast<int>(capacity);

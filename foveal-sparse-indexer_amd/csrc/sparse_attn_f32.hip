@@ -309,18 +309,23 @@ __global__ __launch_bounds__(64 * F_WAVES) void sparse_attn_f32_kernel(F32Params
 #pragma unroll
         for (int e = 0; e < 4; ++e) sv[4 * t + e] = st[qt][t][e];
       if (!nomask) {
+        // Branch-free: a score is kept when its sign word is negative (a taken key
+        // inside T, and inside / outside the window for a local / listed chunk);
+        // wlo >= -1 keeps every difference inside int range.
+        int lk = 4 * kg;
+        asm volatile("" : "+v"(lk));  // formed here, not held across the loop
+        const int wlo = myq - (P.window < myq + 1 ? P.window : myq + 1);  // window: wlo < key <= myq
+        const int wmode = P.mode == FSI_SATTN_LOCAL_REMOTE ? (local ? 1 : 2) : 0;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int tau = 16 * t + 4 * kg + e;
+            const int tau = 16 * t + lk + e;
             const int key = kc0 + tau;
-            bool ok = tau < hi && key < P.T;
-            if (P.mode == FSI_SATTN_LOCAL_REMOTE) {
-              const bool in_win = key <= myq && key > myq - P.window;
-              ok = ok && (local ? in_win : !in_win);
-            }
-            if (!ok) sv[4 * t + e] = -INFINITY;
+            int keep = (tau - hi) & (key - P.T);
+            const int inw = (key - myq - 1) & (wlo - key);
+            keep &= wmode == 0 ? -1 : (wmode == 1 ? inw : ~inw);
+            sv[4 * t + e] = keep < 0 ? sv[4 * t + e] : -INFINITY;
           }
       }
       const float mx = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(sv[0], sv[1]), __builtin_fmaxf(sv[2], sv[3])),

@@ -284,20 +284,14 @@ __global__ __launch_bounds__(64 * DA_WAVES) void decode_attn_partial_kernel(Deco
   decode_partial_wave<HD>(P, blockIdx.x * DA_WAVES + (threadIdx.x >> 6));
 }
 
-// One wave per (sequence, query head): lanes read the split maxima and sums in
-// parallel, then every lane merges HD / 64 dimensions over the splits.
-constexpr int MG_WAVES = 4;
-
+// One wave per (sequence, query head) item: lanes read the split maxima and
+// sums in parallel, then every lane merges HD / 64 dimensions over the splits.
 template <int HD>
-__global__ __launch_bounds__(64 * MG_WAVES) void decode_attn_merge_kernel(const float* __restrict__ m_part,
-                                                                         const float* __restrict__ l_part,
-                                                                         const float* __restrict__ o_part, int B,
-                                                                         int Hq, int Hkv, int G, int S,
-                                                                         bf16_t* __restrict__ out) {
+__device__ __forceinline__ void decode_merge_wave(const float* __restrict__ m_part, const float* __restrict__ l_part,
+                                                  const float* __restrict__ o_part, int Hq, int Hkv, int G, int S,
+                                                  bf16_t* __restrict__ out, int item) {
   constexpr int DPL = HD / 64;  // dimensions per lane
   const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * MG_WAVES + (threadIdx.x >> 6);
-  if (item >= B * Hq) return;
   const int b = item / Hq, hq = item % Hq;
   const int g = hq / G, h = hq % G;
   const int64_t part0 = (static_cast<int64_t>(b) * Hkv + g) * S;
@@ -341,6 +335,38 @@ __global__ __launch_bounds__(64 * MG_WAVES) void decode_attn_merge_kernel(const 
   bf16_t* dst = out + (static_cast<int64_t>(b) * Hq + hq) * HD + lane * DPL;
 #pragma unroll
   for (int i = 0; i < DPL; ++i) dst[i] = f32_to_bf16(L > 0.f ? o[i] / L : 0.f);
+}
+
+constexpr int MG_WAVES = 4;
+
+template <int HD>
+__global__ __launch_bounds__(64 * MG_WAVES) void decode_attn_merge_kernel(const float* __restrict__ m_part,
+                                                                         const float* __restrict__ l_part,
+                                                                         const float* __restrict__ o_part, int B,
+                                                                         int Hq, int Hkv, int G, int S,
+                                                                         bf16_t* __restrict__ out) {
+  const int item = blockIdx.x * MG_WAVES + (threadIdx.x >> 6);
+  if (item >= B * Hq) return;
+  decode_merge_wave<HD>(m_part, l_part, o_part, Hq, Hkv, G, S, out, item);
+}
+
+// Partials and merge in one launch: one workgroup of S_sub waves per (sequence,
+// KV head).  Wave s computes partial slot s_off + s as decode_partial_wave does
+// in its own launch; after the workgroup barrier (workgroup-scope release and
+// acquire: the slots just written are read back by waves of the same
+// workgroup, the slots of an earlier launch are complete) waves merge the
+// group's query heads over all S slots of the pair.  Removes the merge launch
+// and its ramp; taken when S_sub <= FA_MAX_WAVES.
+constexpr int FA_MAX_WAVES = 8;
+
+template <int HD>
+__global__ __launch_bounds__(64 * FA_MAX_WAVES) void decode_attn_fused_kernel(DecodeParams P, bf16_t* out) {
+  const int wave = threadIdx.x >> 6;
+  decode_partial_wave<HD>(P, static_cast<int>(blockIdx.x) * P.S_sub + wave);
+  __syncthreads();
+  const int b = static_cast<int>(blockIdx.x) / P.Hkv, g = static_cast<int>(blockIdx.x) % P.Hkv;
+  for (int h = wave; h < P.G; h += P.S_sub)
+    decode_merge_wave<HD>(P.m_part, P.l_part, P.o_part, P.Hq, P.Hkv, P.G, P.S, out, b * P.Hq + g * P.G + h);
 }
 
 // Partial waves a decode launch aims for: one round of resident waves on the chip
@@ -503,6 +529,22 @@ int decode_merge_launch(const DecodeParams& P, int64_t head_dim, void* out, hipS
   return FSI_OK;
 }
 
+// This launch's partials and the merge of all S slots: one fused launch when a
+// workgroup holds the launch's waves of a (sequence, KV head), otherwise the
+// partial kernel, then the merge kernel.
+int decode_partial_merge_launch(const DecodeParams& P, int64_t head_dim, void* out, hipStream_t st) {
+  if (P.S_sub > FA_MAX_WAVES) {
+    const int c = decode_partial_launch(P, head_dim, st);
+    return c != FSI_OK ? c : decode_merge_launch(P, head_dim, out, st);
+  }
+  const unsigned grid = static_cast<unsigned>(static_cast<int64_t>(P.B) * P.Hkv);
+  const unsigned threads = static_cast<unsigned>(64 * P.S_sub);
+  if (head_dim == 128) decode_attn_fused_kernel<128><<<grid, threads, 0, st>>>(P, static_cast<bf16_t*>(out));
+  else decode_attn_fused_kernel<64><<<grid, threads, 0, st>>>(P, static_cast<bf16_t*>(out));
+  FSI_HIP_LAUNCH_CHECK("decode_attn partial + merge");
+  return FSI_OK;
+}
+
 // The partial and merge kernels in one stream with the partials at `ws`
 // (every byte read is written first in the same call, so it needs no clearing).
 int decode_attn_launch(const void* q, const void* k_pool, const void* v_pool, const int32_t* page_table,
@@ -513,9 +555,7 @@ int decode_attn_launch(const void* q, const void* k_pool, const void* v_pool, co
   const DecodeParams P = decode_params(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
                                        remote_pages, remote_counts, capacity, capacity, B, Hq, Hkv, scale, ws, err,
                                        DA_ALL);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int c = decode_partial_launch(P, head_dim, st);
-  return c != FSI_OK ? c : decode_merge_launch(P, head_dim, out, st);
+  return decode_partial_merge_launch(P, head_dim, out, reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // namespace

@@ -1749,8 +1749,7 @@ FSI_API int fsi_decode_step_attn(const void* qi, const float* kp, const void* vp
     const DecodeParams D = decode_params(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
                                          out_pages, out_counts, batch0 ? 0 : capacity, capacity, B, Hq, Hkv, scale, ws,
                                          err, DA_ALL);
-    c = decode_partial_launch(D, head_dim, st);
-    return c != FSI_OK ? c : decode_merge_launch(D, head_dim, out, st);
+    return decode_partial_merge_launch(D, head_dim, out, st);
   }
   // launch 1: routing workgroups [0, B) beside the local-window partials (which read no routing result),
   // with as many local waves as fit beside the routing workgroups in one round of resident workgroups,
@@ -1773,12 +1772,12 @@ FSI_API int fsi_decode_step_attn(const void* qi, const float* kp, const void* vp
     else decode_step_kernel<PL, E, 64><<<grid, DR_THREADS, 0, st>>>(A, L);
   }))
   FSI_HIP_LAUNCH_CHECK("decode_step_attn route + local");
-  // launch 2: the remote pages' partials and the merge of both
+  // launch 2: the remote pages' partials and the merge of both (one fused launch
+  // when a workgroup holds a pair's remote waves)
   const DecodeParams R = decode_params(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
                                        out_pages, out_counts, batch0 ? 0 : capacity, capacity, B, Hq, Hkv, scale, ws,
                                        err, DA_REMOTE, s_local);
-  c = decode_partial_launch(R, head_dim, st);
-  return c != FSI_OK ? c : decode_merge_launch(R, head_dim, out, st);
+  return decode_partial_merge_launch(R, head_dim, out, st);
 }
 
 

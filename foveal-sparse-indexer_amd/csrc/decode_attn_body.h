@@ -73,20 +73,201 @@ struct DecodeParams {
 
 enum DecodeMode : int { DA_ALL = 0, DA_LOCAL = 1, DA_REMOTE = 2 };
 
+// Pieces of a partial wave, shared by decode_partial_wave and the one-launch
+// decode step (routing.hip).
+//
+// Chunk c of sequence b's list (local-window halves [0, nl), then two halves
+// per listed page, the page ids at remote_row): the element offset of its
+// (page, KV head g) block with the half in bit 0 (blocks are PAGE * HD
+// elements, so the bit is free) and the valid token range [tok_lo, tok_hi)
+// within the half.
+template <int HD>
+__device__ __forceinline__ int64_t decode_chunk_addr(const DecodeParams& P, int b, int g, int c, int nl, int c_lo,
+                                                     int ls, int pos, const int32_t* remote_row, int& tok_lo,
+                                                     int& tok_hi) {
+  int lp, half;
+  tok_lo = 0;
+  tok_hi = CHUNK;
+  if (c < nl) {
+    const int ca = c_lo + c;  // absolute chunk index
+    lp = ca >> 1;
+    half = ca & 1;
+    const int first = ca * CHUNK;
+    tok_lo = ls - first > 0 ? ls - first : 0;
+    tok_hi = pos + 1 - first < CHUNK ? pos + 1 - first : CHUNK;
+  } else {
+    const int r = (c - nl) >> 1;
+    half = (c - nl) & 1;
+    lp = remote_row[r];
+  }
+  int64_t phys = -1;
+  if (lp >= 0 && lp < P.max_pages) phys = P.page_table[static_cast<int64_t>(b) * P.max_pages + lp];
+  if (phys < 0 || phys >= P.n_phys) {
+    if (P.err) set_error(P.err, FSI_ERR_INDEX_RANGE);
+    phys = 0;
+    tok_lo = tok_hi = 0;  // nothing valid: the chunk is read from page 0 and masked out
+  }
+  return ((phys * P.Hkv + g) * PAGE) * HD + half;
+}
+
+// The K and V^T operands of the chunk whose offset (with the half in bit 0) is info.
+template <int HD>
+__device__ __forceinline__ void decode_load_chunk(const DecodeParams& P, int64_t info, u32x4_t (&kr)[HD / 16],
+                                                  u32x4_t (&vr)[HD / 16]) {
+  constexpr int KS = HD / 32;
+  constexpr int DT = HD / 16;
+  const int lane = threadIdx.x & 63;
+  const int h = lane & 15, grp = lane >> 4;
+  const int half = static_cast<int>(info & 1);
+  const int64_t head_base = info - half;
+  // K [HD/32][64][32]: the half starts at token 32 half of every dim chunk;
+  // V [2][HD][32]: the half is the outer index
+  const bf16_t* kp = P.k_pool + head_base + half * CHUNK * 32;
+  const bf16_t* vp = P.v_pool + head_base + half * CHUNK * HD;
+  // every K / V byte is read once per decode step: non-temporal loads keep the
+  // stream from displacing the queries, page tables and partials in L2
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kr[tile * KS + ks] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(kp + ks * PAGE * 32 + (16 * tile + h) * 32 + 8 * grp));
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    vr[dt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vp + (16 * dt + h) * CHUNK + 8 * grp));
+}
+
+// Q^T operand of (sequence b, KV head g): lane supplies Q[h][32 ks + 8 grp .. +8].
+template <int HD>
+__device__ __forceinline__ void decode_load_q(const DecodeParams& P, int b, int g, u32x4_t (&qb)[HD / 32]) {
+  const int lane = threadIdx.x & 63;
+  const int h = lane & 15, grp = lane >> 4;
+#pragma unroll
+  for (int ks = 0; ks < HD / 32; ++ks) {
+    if (h < P.G) {
+      qb[ks] = *reinterpret_cast<const u32x4_t*>(P.q + (static_cast<int64_t>(b) * P.Hq + g * P.G + h) * HD + 32 * ks +
+                                                 8 * grp);
+    } else {
+      qb[ks] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+// One chunk of the online softmax: S^T, the running max and sum, P as a bf16
+// hi + lo pair, O^T += V^T P^T.  Tokens outside [lo_t, hi_t) are masked (their
+// V slots zeroed: the memory may hold anything).
+template <int HD>
+__device__ __forceinline__ void decode_chunk_math(const DecodeParams& P, const u32x4_t (&kcur)[HD / 16],
+                                                  u32x4_t (&vcur)[HD / 16], const u32x4_t (&qb)[HD / 32], int lo_t,
+                                                  int hi_t, float& m_run, float& l_run, f32x4_t (&acc)[HD / 16]) {
+  constexpr int KS = HD / 32;
+  constexpr int DT = HD / 16;
+  const int lane = threadIdx.x & 63;
+  const int grp = lane >> 4;
+  // S^T for the chunk's two 16-token tiles
+  f32x4_t st[2];
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    st[tile] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) st[tile] = mfma16x16x32(kcur[tile * KS + ks], qb[ks], st[tile]);
+  }
+  // lane holds tokens 16 tile + 4 grp + j for head h
+  float sv[8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tau = 16 * tile + 4 * grp + j;
+      const bool ok = tau >= lo_t && tau < hi_t;
+      const float v = ok ? st[tile][j] * P.scale_log2 : -INFINITY;
+      sv[tile * 4 + j] = v;
+      mx = fmaxf(mx, v);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(m_run, mx);
+  float alpha, psum = 0.f;
+  uint32_t pk_hi[4], pk_lo[4];  // P = hi + lo, both bf16: the PV product keeps ~16 bits of P
+  if (m_new == -INFINITY) {
+    alpha = 1.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pk_hi[w] = pk_lo[w] = 0u;
+  } else {
+    alpha = exp2f(m_run - m_new);
+    float hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pe = exp2f(sv[e] - m_new);
+      psum += pe;
+      hi[e] = round_bf16(pe);
+      lo[e] = pe - hi[e];
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      pk_hi[w] = pack_bf16x2(hi[2 * w], hi[2 * w + 1]);
+      pk_lo[w] = pack_bf16x2(lo[2 * w], lo[2 * w + 1]);
+    }
+  }
+  psum += __shfl_xor(psum, 16, 64);
+  psum += __shfl_xor(psum, 32, 64);
+  l_run = l_run * alpha + psum;
+  m_run = m_new;
+  // V^T tile: zero the slots of masked tokens
+  if (lo_t > 0 || hi_t < CHUNK) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int e0 = 2 * w, e1 = 2 * w + 1;
+        const int t0 = e0 < 4 ? 4 * grp + e0 : 16 + 4 * grp + e0 - 4;
+        const int t1 = e1 < 4 ? 4 * grp + e1 : 16 + 4 * grp + e1 - 4;
+        const uint32_t m0 = (t0 >= lo_t && t0 < hi_t) ? 0x0000ffffu : 0u;
+        const uint32_t m1 = (t1 >= lo_t && t1 < hi_t) ? 0xffff0000u : 0u;
+        vcur[dt][w] &= (m0 | m1);
+      }
+  }
+  const u32x4_t pbh = u32x4_t{pk_hi[0], pk_hi[1], pk_hi[2], pk_hi[3]};
+  const u32x4_t pbl = u32x4_t{pk_lo[0], pk_lo[1], pk_lo[2], pk_lo[3]};
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[dt][j] *= alpha;
+    acc[dt] = mfma16x16x32(vcur[dt], pbh, acc[dt]);
+    acc[dt] = mfma16x16x32(vcur[dt], pbl, acc[dt]);
+  }
+}
+
+// The wave's (max, sum, O) into partial slot s of (sequence b, KV head g).
+template <int HD>
+__device__ __forceinline__ void decode_store_partial(const DecodeParams& P, int b, int g, int s, float m_run,
+                                                     float l_run, const f32x4_t (&acc)[HD / 16]) {
+  const int lane = threadIdx.x & 63;
+  const int h = lane & 15, grp = lane >> 4;
+  const int64_t part = (static_cast<int64_t>(b) * P.Hkv + g) * P.S + s;
+  if (grp == 0) {
+    P.m_part[part * 16 + h] = m_run;
+    P.l_part[part * 16 + h] = l_run;
+  }
+  if (h < P.G) {
+    float* o = P.o_part + (part * P.G + h) * HD;
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt) *reinterpret_cast<f32x4_t*>(o + 16 * dt + 4 * grp) = acc[dt];
+  }
+}
+
 // One wave's share of the partials: wave_id in [0, B Hkv S_sub).  Whole-wave
 // work with no workgroup barriers, so it can run in any workgroup shape.
 template <int HD>
 __device__ __forceinline__ void decode_partial_wave(const DecodeParams& P, int wave_id) {
-  constexpr int KS = HD / 32;   // k-steps of the S^T product
-  constexpr int DT = HD / 16;   // dim tiles of O^T
-  constexpr int KLOADS = 2 * KS;
+  constexpr int DT = HD / 16;
   const int lane = threadIdx.x & 63;
   if (wave_id >= P.B * P.Hkv * P.S_sub) return;
   const int s_loc = wave_id % P.S_sub;
   const int s = P.s_off + s_loc;
   const int g = (wave_id / P.S_sub) % P.Hkv;
   const int b = wave_id / (P.S_sub * P.Hkv);
-  const int h = lane & 15, grp = lane >> 4;
 
   const int pos = P.pos_rows ? P.pos_rows[b] : P.pos;
   const int ls = pos + 1 - P.window > 0 ? pos + 1 - P.window : 0;
@@ -105,178 +286,39 @@ __device__ __forceinline__ void decode_partial_wave(const DecodeParams& P, int w
     c1 = c0 + MAX_CHUNKS_PER_WAVE;
   }
 
-  // chunk c0 + lane: element offset of its (page, head) block with the half in
-  // bit 0 (blocks are PAGE * HD elements, so the bit is free), and the valid
-  // token range within the half
+  // chunk c0 + lane: offset with the half in bit 0 and valid token range
   int64_t cbase = 0;
-  int tok_lo = 0, tok_hi = CHUNK;  // valid token range [lo, hi) within the half
-  {
-    const int c = c0 + lane;
-    if (c < c1) {
-      int lp, half;
-      if (c < nl) {
-        const int ca = c_lo + c;  // absolute chunk index
-        lp = ca >> 1;
-        half = ca & 1;
-        const int first = ca * CHUNK;
-        tok_lo = ls - first > 0 ? ls - first : 0;
-        tok_hi = pos + 1 - first < CHUNK ? pos + 1 - first : CHUNK;
-      } else {
-        const int r = (c - nl) >> 1;
-        half = (c - nl) & 1;
-        lp = P.remote[static_cast<int64_t>(b) * P.remote_stride + r];
-      }
-      int64_t phys = -1;
-      if (lp >= 0 && lp < P.max_pages) phys = P.page_table[static_cast<int64_t>(b) * P.max_pages + lp];
-      if (phys < 0 || phys >= P.n_phys) {
-        if (P.err) set_error(P.err, FSI_ERR_INDEX_RANGE);
-        phys = 0;
-        tok_lo = tok_hi = 0;  // nothing valid: the chunk is read from page 0 and masked out
-      }
-      cbase = ((phys * P.Hkv + g) * PAGE) * HD + half;
-    }
-  }
+  int tok_lo = 0, tok_hi = CHUNK;
+  if (c0 + lane < c1)
+    cbase = decode_chunk_addr<HD>(P, b, g, c0 + lane, nl, c_lo, ls, pos,
+                                  P.remote + static_cast<int64_t>(b) * P.remote_stride, tok_lo, tok_hi);
 
-  // Q^T operand: lane supplies Q[h][32 ks + 8 grp .. +8]
-  u32x4_t qb[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    if (h < P.G) {
-      qb[ks] = *reinterpret_cast<const u32x4_t*>(P.q + (static_cast<int64_t>(b) * P.Hq + g * P.G + h) * HD + 32 * ks +
-                                                 8 * grp);
-    } else {
-      qb[ks] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-  }
-
+  u32x4_t qb[HD / 32];
+  decode_load_q<HD>(P, b, g, qb);
   f32x4_t acc[DT];
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  u32x4_t kcur[KLOADS], vcur[DT], knxt[KLOADS], vnxt[DT];
-  auto load_chunk = [&](int c, u32x4_t (&kr)[KLOADS], u32x4_t (&vr)[DT]) {
-    const int i = c - c0;
+  auto info_of = [&](int i) {
     const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(cbase), i);
     const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(cbase >> 32), i);
-    const int64_t info = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-    const int half = static_cast<int>(info & 1);
-    const int64_t head_base = info - half;
-    // K [HD/32][64][32]: the half starts at token 32 half of every dim chunk;
-    // V [2][HD][32]: the half is the outer index
-    const bf16_t* kp = P.k_pool + head_base + half * CHUNK * 32;
-    const bf16_t* vp = P.v_pool + head_base + half * CHUNK * HD;
-    // every K / V byte is read once per decode step: non-temporal loads keep the
-    // stream from displacing the queries, page tables and partials in L2
-#pragma unroll
-    for (int tile = 0; tile < 2; ++tile)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        kr[tile * KS + ks] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4_t*>(kp + ks * PAGE * 32 + (16 * tile + h) * 32 + 8 * grp));
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      vr[dt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vp + (16 * dt + h) * CHUNK + 8 * grp));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
   };
-
-  if (c0 < c1) load_chunk(c0, kcur, vcur);
+  u32x4_t kcur[DT], vcur[DT], knxt[DT], vnxt[DT];
+  if (c0 < c1) decode_load_chunk<HD>(P, info_of(0), kcur, vcur);
   for (int c = c0; c < c1; ++c) {
     const int cn = c + 1 < c1 ? c + 1 : c;  // straight-line prefetch (the last one re-reads)
-    load_chunk(cn, knxt, vnxt);
+    decode_load_chunk<HD>(P, info_of(cn - c0), knxt, vnxt);
     const int i = c - c0;
-    const int lo_t = __builtin_amdgcn_readlane(tok_lo, i);
-    const int hi_t = __builtin_amdgcn_readlane(tok_hi, i);
-
-    // S^T for the chunk's two 16-token tiles
-    f32x4_t st[2];
+    decode_chunk_math<HD>(P, kcur, vcur, qb, __builtin_amdgcn_readlane(tok_lo, i), __builtin_amdgcn_readlane(tok_hi, i),
+                          m_run, l_run, acc);
 #pragma unroll
-    for (int tile = 0; tile < 2; ++tile) {
-      st[tile] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) st[tile] = mfma16x16x32(kcur[tile * KS + ks], qb[ks], st[tile]);
-    }
-    // lane holds tokens 16 tile + 4 grp + j for head h
-    float sv[8];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int tile = 0; tile < 2; ++tile)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tau = 16 * tile + 4 * grp + j;
-        const bool ok = tau >= lo_t && tau < hi_t;
-        const float v = ok ? st[tile][j] * P.scale_log2 : -INFINITY;
-        sv[tile * 4 + j] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    float alpha, psum = 0.f;
-    uint32_t pk_hi[4], pk_lo[4];  // P = hi + lo, both bf16: the PV product keeps ~16 bits of P
-    if (m_new == -INFINITY) {
-      alpha = 1.f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) pk_hi[w] = pk_lo[w] = 0u;
-    } else {
-      alpha = exp2f(m_run - m_new);
-      float hi[8], lo[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float pe = exp2f(sv[e] - m_new);
-        psum += pe;
-        hi[e] = round_bf16(pe);
-        lo[e] = pe - hi[e];
-      }
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        pk_hi[w] = pack_bf16x2(hi[2 * w], hi[2 * w + 1]);
-        pk_lo[w] = pack_bf16x2(lo[2 * w], lo[2 * w + 1]);
-      }
-    }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    // V^T tile: zero the slots of masked tokens (their memory may hold anything)
-    if (lo_t > 0 || hi_t < CHUNK) {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const int e0 = 2 * w, e1 = 2 * w + 1;
-          const int t0 = e0 < 4 ? 4 * grp + e0 : 16 + 4 * grp + e0 - 4;
-          const int t1 = e1 < 4 ? 4 * grp + e1 : 16 + 4 * grp + e1 - 4;
-          const uint32_t m0 = (t0 >= lo_t && t0 < hi_t) ? 0x0000ffffu : 0u;
-          const uint32_t m1 = (t1 >= lo_t && t1 < hi_t) ? 0xffff0000u : 0u;
-          vcur[dt][w] &= (m0 | m1);
-        }
-    }
-    const u32x4_t pbh = u32x4_t{pk_hi[0], pk_hi[1], pk_hi[2], pk_hi[3]};
-    const u32x4_t pbl = u32x4_t{pk_lo[0], pk_lo[1], pk_lo[2], pk_lo[3]};
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[dt][j] *= alpha;
-      acc[dt] = mfma16x16x32(vcur[dt], pbh, acc[dt]);
-      acc[dt] = mfma16x16x32(vcur[dt], pbl, acc[dt]);
-    }
-#pragma unroll
-    for (int t = 0; t < KLOADS; ++t) kcur[t] = knxt[t];
+    for (int t = 0; t < DT; ++t) kcur[t] = knxt[t];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) vcur[dt] = vnxt[dt];
   }
-
-  const int64_t part = (static_cast<int64_t>(b) * P.Hkv + g) * P.S + s;
-  if (grp == 0) {
-    P.m_part[part * 16 + h] = m_run;
-    P.l_part[part * 16 + h] = l_run;
-  }
-  if (h < P.G) {
-    float* o = P.o_part + (part * P.G + h) * HD;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      *reinterpret_cast<f32x4_t*>(o + 16 * dt + 4 * grp) = acc[dt];
-  }
+  decode_store_partial<HD>(P, b, g, s, m_run, l_run, acc);
 }
 
 template <int HD>
@@ -450,10 +492,18 @@ int decode_attn_check(const void* q, const void* k_pool, const void* v_pool, con
   return FSI_OK;
 }
 
+// Partial slots per (sequence, KV head) of the one-launch decode step
+// (routing.hip, decode_step_fused_kernel: one per wave), which runs only with
+// at least FS_MIN_PAIRS pairs.
+constexpr int FS_SLOTS = 8;
+constexpr int64_t FS_MIN_PAIRS = 128;
+
 // Bytes of per-wave partials (max, sum, O) the partial and merge kernels exchange.
 size_t decode_attn_partials_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t head_dim, int64_t window,
                                   int64_t capacity, int64_t max_pages) {
-  const int64_t parts = B * Hkv * decode_split(B, Hkv, window, capacity, max_pages).slots();
+  int64_t slots = decode_split(B, Hkv, window, capacity, max_pages).slots();
+  if (B * Hkv >= FS_MIN_PAIRS && slots < FS_SLOTS) slots = FS_SLOTS;
+  const int64_t parts = B * Hkv * slots;
   return static_cast<size_t>(parts) * (2 * 16 + (Hq / Hkv) * head_dim) * sizeof(float);
 }
 

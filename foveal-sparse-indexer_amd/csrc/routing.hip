@@ -590,24 +590,53 @@ __global__ __launch_bounds__(64 * SR_WAVES) void score_route_kernel(const void* 
 constexpr int DR_THREADS = 256;
 constexpr int DR_WAVES = DR_THREADS / 64;
 
-__device__ __forceinline__ float dr_block_max(float v, float* red) {
+// Barrier among the DR_THREADS threads that route: the workgroup barrier when
+// the workgroup is exactly those threads (decode_route_kernel), an LDS counter
+// among waves [0, DR_WAVES) when other waves of the workgroup run other work
+// (decode_step_fused_kernel).
+struct DrWgBarrier {
+  __device__ __forceinline__ void operator()() const { __syncthreads(); }
+};
+struct DrSubBarrier {
+  int* ctr;    // LDS, zero before the first use
+  int target;  // arrivals this wave has waited for so far
+  int* err;
+  __device__ __forceinline__ void operator()() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane_id() == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    target += DR_WAVES;
+    // bounded: every routing wave arrives; the bound only guarantees an exit
+    for (int spins = 0; __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target; ++spins) {
+      if (spins >= (1 << 22)) {
+        if (err) set_error(err, FSI_ERR_HIP);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+};
+
+template <class Bar>
+__device__ __forceinline__ float dr_block_max(float v, float* red, Bar& bar) {
   const int wave = threadIdx.x >> 6, lane = lane_id();
   v = wave_max(v);
-  __syncthreads();
+  bar();
   if (lane == 0) red[wave] = v;
-  __syncthreads();
+  bar();
   float r = red[0];
 #pragma unroll
   for (int w = 1; w < DR_WAVES; ++w) r = fmaxf(r, red[w]);
   return r;
 }
 
-__device__ __forceinline__ float dr_block_sum(float v, float* red) {
+template <class Bar>
+__device__ __forceinline__ float dr_block_sum(float v, float* red, Bar& bar) {
   const int wave = threadIdx.x >> 6, lane = lane_id();
   v = wave_sum(v);
-  __syncthreads();
+  bar();
   if (lane == 0) red[wave] = v;
-  __syncthreads();
+  bar();
   float r = red[0];
 #pragma unroll
   for (int w = 1; w < DR_WAVES; ++w) r += red[w];
@@ -678,10 +707,48 @@ struct RouteArgs {
   float top_p, sqrt_d;
 };
 
-// Routing of sequence b by one DR_THREADS workgroup.
-template <int PL, int E, bool BF16>
-__device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
-  const void* __restrict__ qi = A.qi;
+// Loads of decode_route_block for sequence b, issued together so the routing
+// pays one memory latency: the 16-D query and, for pages t + DR_THREADS i of
+// thread t, the page keys and (for the context) the page values.
+template <int PL>
+struct RouteRegs {
+  static constexpr int NPT = (64 * PL + DR_THREADS - 1) / DR_THREADS;
+  float qv[SR_D];
+  float4 kreg[NPT][4];
+  u32x4_t vreg[NPT][2];
+};
+
+template <int PL, bool BF16>
+__device__ __forceinline__ void decode_route_loads(const RouteArgs& A, int b, RouteRegs<PL>& rr) {
+  constexpr int NPT = RouteRegs<PL>::NPT;
+#pragma unroll
+  for (int c = 0; c < SR_D; ++c) {
+    const int64_t off = static_cast<int64_t>(b) * SR_D + c;
+    rr.qv[c] = BF16 ? bf16_to_f32(static_cast<const bf16_t*>(A.qi)[off]) : static_cast<const float*>(A.qi)[off];
+  }
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const int j = threadIdx.x + DR_THREADS * i;
+    const int jj = j < A.completed ? j : 0;
+    const float4* kr = reinterpret_cast<const float4*>(A.kp + (static_cast<int64_t>(b) * A.P + jj) * SR_D);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) rr.kreg[i][w] = kr[w];
+    if (BF16 && A.out_ctx) {
+      const u32x4_t* vr = reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(A.vp) +
+                                                           (static_cast<int64_t>(b) * A.P + jj) * SR_D);
+      rr.vreg[i][0] = vr[0];
+      rr.vreg[i][1] = vr[1];
+    }
+  }
+}
+
+// Routing of sequence b by one DR_THREADS workgroup from the loads in rr.
+// write_out: write the pages and counts (and, when A.out_ctx is set, the
+// context); pg_lds / cnt_lds (optional): wave 0 also leaves the page list
+// (64 E entries, -1 past the count) and the count in LDS.
+template <int PL, int E, bool BF16, class Bar>
+__device__ __forceinline__ void decode_route_compute(const RouteArgs& A, int b, RouteRegs<PL>& rr, bool write_out,
+                                                     int32_t* pg_lds, int* cnt_lds, Bar& bar) {
   const float* __restrict__ kp = A.kp;
   const void* __restrict__ vp = A.vp;
   const int32_t* __restrict__ pos_rows = A.pos_rows;
@@ -699,39 +766,22 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
   const int mypos = pos_rows ? pos_rows[b] : pos;
   const int local_start = mypos + 1 - window > 0 ? mypos + 1 - window : 0;
   const int flp = local_start / page;
+  (void)kp;
+  (void)vp;
+  (void)P;
 
   float qv[SR_D];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < SR_D; ++c) {
-    const int64_t off = static_cast<int64_t>(b) * SR_D + c;
-    qv[c] = BF16 ? bf16_to_f32(static_cast<const bf16_t*>(qi)[off]) : static_cast<const float*>(qi)[off];
+    qv[c] = rr.qv[c];
     ss = fmaf(qv[c], qv[c], ss);
   }
   const float nrm = fmaxf(sqrtf(ss), 1e-12f);
 #pragma unroll
   for (int c = 0; c < SR_D; ++c) qv[c] = qv[c] / nrm;
 
-  // Every load this thread needs (page keys and, for the context, page values
-  // of pages t + DR_THREADS i) is issued up front, so the kernel pays one
-  // memory latency instead of one per pass.
-  constexpr int NPT = (64 * PL + DR_THREADS - 1) / DR_THREADS;
-  float4 kreg[NPT][4];
-  u32x4_t vreg[NPT][2];
-#pragma unroll
-  for (int i = 0; i < NPT; ++i) {
-    const int j = threadIdx.x + DR_THREADS * i;
-    const int jj = j < completed ? j : 0;
-    const float4* kr = reinterpret_cast<const float4*>(kp + (static_cast<int64_t>(b) * P + jj) * SR_D);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) kreg[i][w] = kr[w];
-    if (BF16 && out_ctx) {
-      const u32x4_t* vr = reinterpret_cast<const u32x4_t*>(static_cast<const bf16_t*>(vp) +
-                                                           (static_cast<int64_t>(b) * P + jj) * SR_D);
-      vreg[i][0] = vr[0];
-      vreg[i][1] = vr[1];
-    }
-  }
+  constexpr int NPT = RouteRegs<PL>::NPT;
 #pragma unroll
   for (int i = 0; i < NPT; ++i) {
     const int j = threadIdx.x + DR_THREADS * i;
@@ -739,7 +789,7 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
     float acc = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float4 f = kreg[i][w];
+      const float4 f = rr.kreg[i][w];
       acc = fmaf(qv[4 * w], f.x, acc);
       acc = fmaf(qv[4 * w + 1], f.y, acc);
       acc = fmaf(qv[4 * w + 2], f.z, acc);
@@ -747,17 +797,17 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
     }
     sc[j] = acc / sqrt_d;
   }
-  __syncthreads();
+  bar();
 
-  if (out_ctx) {  // uniform across the workgroup
+  if (out_ctx && write_out) {  // uniform across the workgroup
     float ctx = 0.f;
     if (completed > 0) {
       float mx = -INFINITY;
       for (int j = threadIdx.x; j < completed; j += DR_THREADS) mx = fmaxf(mx, sc[j]);
-      mx = dr_block_max(mx, red);
+      mx = dr_block_max(mx, red, bar);
       float z = 0.f;
       for (int j = threadIdx.x; j < completed; j += DR_THREADS) z += expf(sc[j] - mx);
-      z = dr_block_sum(z, red);
+      z = dr_block_sum(z, red, bar);
       float part[SR_D];
 #pragma unroll
       for (int c = 0; c < SR_D; ++c) part[c] = 0.f;
@@ -766,10 +816,9 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
         const int j = threadIdx.x + DR_THREADS * i;
         if (j >= completed) continue;
         float pj = expf(sc[j] - mx) / z;
-        const int64_t off = (static_cast<int64_t>(b) * P + j) * SR_D;
         if (BF16) {
           pj = round_bf16(pj);
-          const u32x4_t a = vreg[i][0], c2 = vreg[i][1];
+          const u32x4_t a = rr.vreg[i][0], c2 = rr.vreg[i][1];
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             part[2 * w] = fmaf(pj, lo_bf16(a[w]), part[2 * w]);
@@ -778,6 +827,7 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
             part[9 + 2 * w] = fmaf(pj, hi_bf16(c2[w]), part[9 + 2 * w]);
           }
         } else {
+          const int64_t off = (static_cast<int64_t>(b) * P + j) * SR_D;
           const float4* vr = reinterpret_cast<const float4*>(static_cast<const float*>(vp) + off);
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
@@ -792,7 +842,7 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
       int which;
       const float t = dr_wave_sum16_scatter(part, which);
       if ((lane & 3) == 0) ctx_part[wave][which] = t;
-      __syncthreads();
+      bar();
       if (threadIdx.x < SR_D) {
 #pragma unroll
         for (int w = 0; w < DR_WAVES; ++w) ctx += ctx_part[w][threadIdx.x];
@@ -810,10 +860,10 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
   if (route) {  // uniform
     float m = -INFINITY;
     for (int j = threadIdx.x; j < flp; j += DR_THREADS) m = fmaxf(m, sc[j]);
-    mx = dr_block_max(m, red);
+    mx = dr_block_max(m, red, bar);
     float zz = 0.f;
     for (int j = threadIdx.x; j < flp; j += DR_THREADS) zz += expf(sc[j] - mx);
-    z = dr_block_sum(zz, red);
+    z = dr_block_sum(zz, red, bar);
   }
   int count = 0;
   uint64_t sorted[E];
@@ -849,7 +899,7 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
                                  [&](int i) { return static_cast<uint32_t>(64 * (PW * wave + i) + lane); });
       if (lane == 0) n_cand[wave] = n;
     }
-    __syncthreads();
+    bar();
   }
   if (wave != 0) return;  // no workgroup barrier follows
   if (route && R > 0) {
@@ -884,6 +934,12 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
     count = count < flp ? count : flp;  // sorted_idx[b, :needed] has flp entries
     count = count < cap ? count : cap;
   }
+  if (pg_lds) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) pg_lds[e * 64 + lane] = e * 64 + lane < count ? comp_index(sorted[e]) : -1;
+    if (lane == 0) *cnt_lds = count;
+  }
+  if (!write_out) return;
   int32_t* pages = out_pages + static_cast<int64_t>(b) * cap;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -892,6 +948,14 @@ __device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
   }
   for (int k = 64 * E + lane; k < cap; k += 64) pages[k] = -1;
   if (lane == 0) out_cnt[b] = count;
+}
+
+template <int PL, int E, bool BF16>
+__device__ __forceinline__ void decode_route_block(const RouteArgs& A, int b) {
+  RouteRegs<PL> rr;
+  decode_route_loads<PL, BF16>(A, b, rr);
+  DrWgBarrier bar;
+  decode_route_compute<PL, E, BF16>(A, b, rr, true, nullptr, nullptr, bar);
 }
 
 template <int PL, int E, bool BF16>
@@ -1573,6 +1637,164 @@ __global__ __launch_bounds__(DR_THREADS) void decode_step_kernel(RouteArgs A, De
   decode_partial_wave<HD>(L, (static_cast<int>(blockIdx.x) - A.B) * DS_WAVES + (threadIdx.x >> 6));
 }
 
+
+// ---------------------------------------------------------------------------
+// One-launch decode step: one FS_WAVES-wave workgroup per (sequence b, KV head
+// g), nothing exchanged between workgroups, no workgroup barrier between the
+// routing and the attention:
+//   waves [0, DR_WAVES) route sequence b (decode_route_loads /
+//     decode_route_compute, the code of decode_route_kernel with an LDS
+//     counter for its barriers: the same pages, counts and context); wave 0
+//     then looks up the selected pages' physical offsets, leaves them in LDS
+//     and releases a flag;
+//   waves [DR_WAVES, FS_WAVES) meanwhile stream the local-window chunks
+//     (wave w takes chunks w - DR_WAVES + FS_STREAM i), so HBM stays busy
+//     while the routing runs;
+//   every wave then takes the selected pages' chunks one at a time from an
+//   LDS counter (after acquiring the flag), continuing its online softmax,
+//   and writes partial slot w; after one barrier the waves merge the group's
+//   query heads over the FS_SLOTS slots.
+// Every KV head of a sequence routes it again (the workgroups of one sequence
+// run on one XCD, so the page keys come from that XCD's L2); KV head 0 writes
+// the pages, counts and context.
+// ---------------------------------------------------------------------------
+constexpr int FS_WAVES = 8;
+constexpr int FS_THREADS = 64 * FS_WAVES;
+constexpr int FS_STREAM = FS_WAVES - DR_WAVES;  // waves streaming the window while the others route
+constexpr int FS_MAX_PAGES = 64 * 32;           // routing loads held in registers (PL <= 32)
+static_assert(FS_SLOTS == FS_WAVES, "one partial slot per wave of the one-launch step");
+
+template <int PL, int E, int HD>
+__global__ __launch_bounds__(FS_THREADS) void decode_step_fused_kernel(RouteArgs A, DecodeParams L, bf16_t* out) {
+  constexpr int DT = HD / 16;
+  __shared__ int32_t pg_lds[64 * E];
+  __shared__ int64_t rem_off[64 * E];  // element offset of selected page r's (page, g) block, -1 if invalid
+  __shared__ int cnt_lds, flag, bar_ctr, rem_next;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = static_cast<int>(blockIdx.x) % A.B, g = static_cast<int>(blockIdx.x) / A.B;
+  if (threadIdx.x == 0) {
+    flag = 0;
+    bar_ctr = 0;
+    rem_next = 0;
+    cnt_lds = 0;
+  }
+  __syncthreads();
+
+  const int pos = L.pos_rows ? L.pos_rows[b] : L.pos;
+  const int ls = pos + 1 - L.window > 0 ? pos + 1 - L.window : 0;
+  const int c_lo = ls / CHUNK, c_hi = pos / CHUNK;
+  const int nl = c_hi - c_lo + 1;
+
+  // this wave's local-window chunks (streaming waves only): lane i holds chunk sw + FS_STREAM i
+  const int sw = wave - DR_WAVES;
+  const int n_loc = sw >= 0 && sw < nl ? (nl - sw + FS_STREAM - 1) / FS_STREAM : 0;  // <= 64 (host-checked)
+  int tl_loc = 0, th_loc = CHUNK;
+  int64_t cb_loc = 0;
+  if (lane < n_loc)
+    cb_loc = decode_chunk_addr<HD>(L, b, g, sw + FS_STREAM * lane, nl, c_lo, ls, pos, pg_lds, tl_loc, th_loc);
+
+  if (wave < DR_WAVES) {
+    RouteArgs Ab = A;
+    if (g != 0) Ab.out_ctx = nullptr;  // the context is written once per sequence
+    RouteRegs<PL> rr;
+    decode_route_loads<PL, true>(Ab, b, rr);
+    DrSubBarrier bar{&bar_ctr, 0, L.err};
+    decode_route_compute<PL, E, true>(Ab, b, rr, g == 0, pg_lds, &cnt_lds, bar);
+    if (wave == 0) {
+      // physical offsets of the selected pages for KV head g, then the release
+      int cnt = cnt_lds;
+      cnt = cnt < 0 ? 0 : (cnt > L.cap ? L.cap : cnt);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int r = 64 * e + lane;
+        if (r < cnt) {
+          const int lp = pg_lds[r];
+          int64_t phys = -1;
+          if (lp >= 0 && lp < L.max_pages) phys = L.page_table[static_cast<int64_t>(b) * L.max_pages + lp];
+          if (phys < 0 || phys >= L.n_phys) {
+            if (L.err) set_error(L.err, FSI_ERR_INDEX_RANGE);
+            rem_off[r] = -1;
+          } else {
+            rem_off[r] = ((phys * L.Hkv + g) * PAGE) * HD;
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0) __hip_atomic_store(&flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+
+  u32x4_t qb[HD / 32];
+  decode_load_q<HD>(L, b, g, qb);
+  f32x4_t acc[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // chunk sequence of this wave: its local chunks, then selected-page chunks
+  // taken one at a time from rem_next until 2 cnt are taken
+  int taken_loc = 0, n_sel = -1;  // n_sel: 2 cnt once the flag is seen
+  auto next_chunk = [&](int64_t& info, int& lo, int& hi) -> bool {  // uniform
+    if (taken_loc < n_loc) {
+      const uint32_t l32 = __builtin_amdgcn_readlane(static_cast<uint32_t>(cb_loc), taken_loc);
+      const uint32_t h32 = __builtin_amdgcn_readlane(static_cast<uint32_t>(cb_loc >> 32), taken_loc);
+      info = static_cast<int64_t>((static_cast<uint64_t>(h32) << 32) | l32);
+      lo = __builtin_amdgcn_readlane(tl_loc, taken_loc);
+      hi = __builtin_amdgcn_readlane(th_loc, taken_loc);
+      ++taken_loc;
+      return true;
+    }
+    if (n_sel < 0) {
+      n_sel = 0;
+      for (int spins = 0;; ++spins) {  // bounded: wave 0 always releases; the bound only guarantees an exit
+        if (__hip_atomic_load(&flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) {
+          int cnt = cnt_lds;
+          n_sel = 2 * (cnt < 0 ? 0 : (cnt > L.cap ? L.cap : cnt));
+          break;
+        }
+        if (spins >= (1 << 22)) {
+          if (L.err) set_error(L.err, FSI_ERR_HIP);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    int r = 0;
+    if (lane == 0) r = __hip_atomic_fetch_add(&rem_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    r = __builtin_amdgcn_readfirstlane(r);
+    if (r >= n_sel) return false;
+    const int64_t off = rem_off[r >> 1];
+    info = off < 0 ? 0 : off + (r & 1);
+    lo = 0;
+    hi = off < 0 ? 0 : CHUNK;  // an invalid page is read from offset 0 and masked out
+    return true;
+  };
+
+  u32x4_t kcur[DT], vcur[DT], knxt[DT], vnxt[DT];
+  int64_t info;
+  int lo_c, hi_c;
+  bool have = next_chunk(info, lo_c, hi_c);
+  if (have) decode_load_chunk<HD>(L, info, kcur, vcur);
+  while (have) {
+    int lo_n = 0, hi_n = 0;
+    const bool more = next_chunk(info, lo_n, hi_n);
+    if (more) decode_load_chunk<HD>(L, info, knxt, vnxt);
+    decode_chunk_math<HD>(L, kcur, vcur, qb, lo_c, hi_c, m_run, l_run, acc);
+    if (!more) break;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) kcur[d] = knxt[d];
+#pragma unroll
+    for (int d = 0; d < DT; ++d) vcur[d] = vnxt[d];
+    lo_c = lo_n;
+    hi_c = hi_n;
+  }
+  decode_store_partial<HD>(L, b, g, wave, m_run, l_run, acc);
+  __syncthreads();
+  for (int h = wave; h < L.G; h += FS_WAVES)
+    decode_merge_wave<HD>(L.m_part, L.l_part, L.o_part, L.Hq, L.Hkv, L.G, L.S, out, b * L.Hq + g * L.G + h);
+}
+
 }  // namespace
 
 extern "C" {
@@ -1750,6 +1972,29 @@ FSI_API int fsi_decode_step_attn(const void* qi, const float* kp, const void* vp
                                          out_pages, out_counts, batch0 ? 0 : capacity, capacity, B, Hq, Hkv, scale, ws,
                                          err, DA_ALL);
     return decode_partial_merge_launch(D, head_dim, out, st);
+  }
+  // one launch when every (sequence, KV head) pair gets a workgroup of its own on the chip
+  if (!batch0 && completed_pages <= FS_MAX_PAGES && B * Hkv >= FS_MIN_PAIRS && B * Hkv >= compute_units() &&
+      local_chunks_of(window, max_pages) <= FS_STREAM * static_cast<int64_t>(MAX_CHUNKS_PER_WAVE)) {
+    DecodeParams L = decode_params(q, k_pool, v_pool, page_table, max_pages, n_phys_pages, pos_rows, pos, window,
+                                   nullptr, nullptr, capacity, capacity, B, Hq, Hkv, scale, ws, err, DA_LOCAL);
+    const int64_t parts = B * Hkv * FS_SLOTS;  // fits: the workspace holds at least FS_SLOTS slots per pair
+    L.m_part = reinterpret_cast<float*>(ws);
+    L.l_part = L.m_part + parts * 16;
+    L.o_part = L.l_part + parts * 16;
+    L.S = FS_SLOTS;
+    L.S_sub = FS_SLOTS;
+    L.s_off = 0;
+    const unsigned grid = static_cast<unsigned>(B * Hkv);
+    bf16_t* o = static_cast<bf16_t*>(out);
+    FSI_DISPATCH_PL(pick_pl(completed_pages), FSI_DISPATCH_E(pick_e(want_of(k_min, k_max, capacity)), {
+      if constexpr (PL <= 32) {
+        if (head_dim == 128) decode_step_fused_kernel<PL, E, 128><<<grid, FS_THREADS, 0, st>>>(A, L, o);
+        else decode_step_fused_kernel<PL, E, 64><<<grid, FS_THREADS, 0, st>>>(A, L, o);
+      }
+    }))
+    FSI_HIP_LAUNCH_CHECK("decode_step_attn one launch");
+    return FSI_OK;
   }
   // launch 1: routing workgroups [0, B) beside the local-window partials (which read no routing result),
   // with as many local waves as fit beside the routing workgroups in one round of resident workgroups,

@@ -289,8 +289,8 @@ def bench_decode_attn(fsi, args, dev):
                    "mean_selected_pages": round(k_sel, 2)})
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C4_TRAFFIC_BYTES,
-                       "kernel": "decode_step_kernel (route workgroups beside the local-window partials) + "
-                                 "decode_attn_partial (selected pages) + decode_attn_merge (3 launches)",
+                       "kernel": "decode_step_fused_kernel (1 launch: per (sequence, KV head) workgroup, 4 waves "
+                                 "route while 4 stream the window, then all take selected-page chunks, in-workgroup merge)",
                        "bytes_per_launch": algo}
     # fp32 over the reference's contiguous cache layout (FovealKVCache's default dtype),
     # all 32 sequences (34.4 GB of K / V), the same pages: dec32_partial_kernel + merge

@@ -99,11 +99,12 @@ __global__ __launch_bounds__(256) void sa_vt_kernel(const bf16_t* __restrict__ v
 //   sa_vt16_kernel: workgroup (x, bg) reduces head bg's chunk maxima to the
 //     head exponent e (largest finite |v| 2^-e in [2^14, 2^15)), stores it in
 //     head_e, and writes chunks [x SA_VT_CHUNKS, ..) of the head as fp16 v 2^-e
-//     in the layout of sa_vt_kernel.
+//     in the layout of sa_vt_kernel: the chunks' token rows are staged in LDS
+//     with 16-byte loads and every thread writes 16 bytes of one output row.
 // Values below the largest by more than 2^28 become fp16 subnormals (absolute
 // error <= 2^-25 of the largest); infinities and NaNs stay what they are.
 // ---------------------------------------------------------------------------
-constexpr int SA_VT_CHUNKS = 8;  // chunks per sa_vt16_kernel workgroup
+constexpr int SA_VT_CHUNKS = 4;  // chunks per sa_vt16_kernel workgroup
 
 template <int HD>
 __global__ __launch_bounds__(256) void sa_vmax_kernel(const bf16_t* __restrict__ v, int64_t vs_b, int64_t vs_g,
@@ -154,9 +155,26 @@ __global__ __launch_bounds__(256) void sa_vt16_kernel(const bf16_t* __restrict__
                                                       int64_t vs_t, int Hkv, int T, int n32,
                                                       const uint32_t* __restrict__ cmax, int32_t* __restrict__ head_e,
                                                       uint16_t* __restrict__ vt) {
-  constexpr int PIECES = HD / 8;
+  constexpr int PIECES = HD / 8;                        // 16-byte pieces of a token row
+  constexpr int ROW = HD * 2 + 16;                      // LDS row of a token (padded: conflict-free column reads)
+  constexpr int IN = SA_VT_CHUNKS * SA_CHUNK * PIECES;  // input pieces of the workgroup
+  constexpr int OUT = SA_VT_CHUNKS * HD * 4;            // output pieces: (chunk, dim, 8-slot group)
+  static_assert(IN % 256 == 0 && OUT % 256 == 0, "pieces must split over the threads");
+  __shared__ __attribute__((aligned(16))) char tile[SA_VT_CHUNKS * SA_CHUNK * ROW];
+  __shared__ uint32_t red[4];
   const int bg = blockIdx.y;
   const int b = bg / Hkv, g = bg % Hkv;
+  const int c0 = blockIdx.x * SA_VT_CHUNKS;
+
+  // the workgroup's tokens, row-major as in v (one latency for all of them)
+  u32x4_t val[IN / 256];
+#pragma unroll
+  for (int i = 0; i < IN / 256; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    const int t = c0 * SA_CHUNK + q / PIECES, piece = q % PIECES;
+    val[i] = u32x4_t{0u, 0u, 0u, 0u};
+    if (t < T) val[i] = *reinterpret_cast<const u32x4_t*>(v + b * vs_b + g * vs_g + t * vs_t + 8 * piece);
+  }
   uint32_t m = 0;
   for (int c = threadIdx.x; c < n32; c += 256) {
     const uint32_t x = cmax[static_cast<int64_t>(bg) * n32 + c];
@@ -167,8 +185,12 @@ __global__ __launch_bounds__(256) void sa_vt16_kernel(const bf16_t* __restrict__
     const uint32_t o = __shfl_xor(m, off, 64);
     m = o > m ? o : m;
   }
-  __shared__ uint32_t red[4];
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+#pragma unroll
+  for (int i = 0; i < IN / 256; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    *reinterpret_cast<u32x4_t*>(tile + (q / PIECES) * ROW + (q % PIECES) * 16) = val[i];
+  }
   __syncthreads();
   m = red[0];
 #pragma unroll
@@ -176,21 +198,32 @@ __global__ __launch_bounds__(256) void sa_vt16_kernel(const bf16_t* __restrict__
   const int e = sa_head_exponent(m);
   if (blockIdx.x == 0 && threadIdx.x == 0) head_e[bg] = e;
   const float sc = __builtin_ldexpf(1.f, -e);  // exact power of two
-  const int t0 = blockIdx.x * SA_VT_CHUNKS * SA_CHUNK;
-  constexpr int ITEMS = SA_VT_CHUNKS * SA_CHUNK * PIECES;
-  for (int it = threadIdx.x; it < ITEMS; it += 256) {
-    const int t = t0 + it / PIECES, piece = it % PIECES;
-    if (t >= n32 * SA_CHUNK) break;
-    u32x4_t val = u32x4_t{0u, 0u, 0u, 0u};
-    if (t < T) val = *reinterpret_cast<const u32x4_t*>(v + b * vs_b + g * vs_g + t * vs_t + 8 * piece);
-    const int c = t / SA_CHUNK, tau = t % SA_CHUNK;
-    uint16_t* o = vt + ((static_cast<int64_t>(bg) * n32 + c) * HD * SA_CHUNK) + sa_slot(tau);
+
+  // output piece (chunk cc, dim d, slots 8 k .. 8 k + 7): slot 8 k + j holds token
+  // 16 (j >> 2) + 4 k + (j & 3) (the inverse of sa_slot)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t w = val[j >> 1];
-      const float f = __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
-      o[(8 * piece + j) * SA_CHUNK] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f * sc));
+  for (int i = 0; i < OUT / 256; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    const int cc = q / (HD * 4), r = q % (HD * 4);
+    const int d = r >> 2, k = r & 3;
+    const int c = c0 + cc;
+    if (c >= n32) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      uint16_t h2[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int j = 2 * jj + u;
+        const int tau = 16 * (j >> 2) + 4 * k + (j & 3);
+        const uint16_t bits = *reinterpret_cast<const uint16_t*>(tile + (cc * SA_CHUNK + tau) * ROW + 2 * d);
+        const float f = __uint_as_float(static_cast<uint32_t>(bits) << 16);
+        h2[u] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(f * sc));
+      }
+      w[jj] = static_cast<uint32_t>(h2[0]) | (static_cast<uint32_t>(h2[1]) << 16);
     }
+    *reinterpret_cast<u32x4_t*>(vt + ((static_cast<int64_t>(bg) * n32 + c) * HD + d) * SA_CHUNK + 8 * k) =
+        u32x4_t{w[0], w[1], w[2], w[3]};
   }
 }
 

@@ -60,7 +60,9 @@ DECODE_TRAFFIC_BYTES_UNPACKED = int(140566.8 * 1024)
 # profiles/pattention_decode_prefill_8b.md, decode_attention_c4.md, indexer_routing_c2.md,
 # block_sparse_gemm_c5.md).
 PREFILL_TRAFFIC_BYTES = int((393537 + 33270 + 196732 + 34374) * 1024)
-C4_TRAFFIC_BYTES = int((161152 + 291023 + 8273 + 3814 + 4352 + 256) * 1024)
+# C4 (decode_step_fused_kernel, one launch): FETCH 202340.1 KiB x 1.9842 + WRITE 4614.0 KiB x 0.99225, both
+# factors from the 512 MiB copy of the same run (profiles/decode_attention_c4.md)
+C4_TRAFFIC_BYTES = int((202340.1 * 1.9842 + 4614.0 * 0.99225) * 1024)
 C2_TRAFFIC_BYTES = int((2057 + 2112) * 1024)
 C5_TRAFFIC_BYTES = {0.10: (515 + 64) << 20, 0.25: (1175 + 64) << 20, 0.50: (2249 + 64) << 20}
 # Prefill attention, one step (sa_vmax + sa_vt16 + sparse_attn_lds, profiles/sparse_attention_prefill_16k.md):

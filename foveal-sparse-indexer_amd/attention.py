@@ -374,9 +374,10 @@ def decode_step_attention(q: Tensor, qi: Tensor, cache: FovealKVCache, *, pos: i
                           completed_pages: int, top_p: float, min_remote_blocks: int, max_remote_blocks: int,
                           scale: float, return_context: bool = False, batch0: bool = False):
     """Page routing and decode attention of one step (decode_route + decode_attention)
-    in two launches on one stream: the workgroups routing each sequence run beside
-    the local-window attention partials, then the selected pages and the merge
-    (fsi_decode_step_attn).  Needs the paged bf16 cache and a bf16 index query.
+    through fsi_decode_step_attn: one launch when there is at least one (sequence, KV
+    head) pair per compute unit (four waves of each pair's workgroup route the sequence
+    while four stream the local window, then all stream the selected pages), otherwise
+    two (routing beside the local window, then the selected pages and the merge).  Needs the paged bf16 cache and a bf16 index query.
     batch0: every sequence attends sequence 0's pages (attention.py:348).
     Returns (attention (B, Hq, hd), pages (B, cap), counts (B,)[, context (B, 16)]),
     cap = max(K_max, K_min, 1); no autograd (use decode_route + decode_attention)."""

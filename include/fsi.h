@@ -388,11 +388,13 @@ FSI_API int fsi_decode_attn(const void* q, const void* k_pool, const void* v_poo
                             void* out, void* workspace, size_t workspace_bytes, int* err, void* stream);
 
 /* Fused decode step: fsi_decode_route (bf16 index query and page values, page
- * size 64, index_dim 16) and fsi_decode_attn (bf16 paged pools) in two
- * launches: workgroups routing each sequence run beside the local-window
- * attention partials (which read no routing result), then the selected pages'
- * partials and the merge.  Outputs as the two calls: pages / counts (context
- * optional) and out.  batch0 != 0: every sequence attends sequence 0's pages,
+ * size 64, index_dim 16) and fsi_decode_attn (bf16 paged pools).  With at least
+ * one (sequence, KV head) pair per compute unit and at most 2048 complete pages,
+ * one launch: per pair, four waves route the sequence while four stream the
+ * local window, then all stream the selected pages and merge.  Otherwise two
+ * launches: workgroups routing each sequence beside the local-window partials,
+ * then the selected pages' partials and the merge.  Outputs as the two calls:
+ * pages / counts (context optional) and out, bit-identical routing either way.  batch0 != 0: every sequence attends sequence 0's pages,
  * as the reference's decode_step does (attention.py:348).  Workspace:
  * fsi_decode_attn_workspace_size(B, Hq, Hkv, head_dim, window, capacity,
  * max_pages).  Replaces decode_step's routing + attention

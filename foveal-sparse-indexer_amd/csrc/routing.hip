@@ -1650,10 +1650,11 @@ __global__ __launch_bounds__(DR_THREADS) void decode_step_kernel(RouteArgs A, De
 //   waves [DR_WAVES, FS_WAVES) meanwhile stream the local-window chunks
 //     (wave w takes chunks w - DR_WAVES + FS_STREAM i), so HBM stays busy
 //     while the routing runs;
-//   every wave then takes the selected pages' chunks one at a time from an
-//   LDS counter (after acquiring the flag), continuing its online softmax,
-//   and writes partial slot w; after one barrier the waves merge the group's
-//   query heads over the FS_SLOTS slots.
+//   every wave then streams a static, contiguous range of the selected pages'
+//   chunks (after acquiring the flag), continuing its online softmax, the
+//   routing waves taking more of them to make up for their late start, and
+//   writes partial slot w; after one barrier the waves merge the group's query
+//   heads over the FS_SLOTS slots.
 // Every KV head of a sequence routes it again (the workgroups of one sequence
 // run on one XCD, so the page keys come from that XCD's L2); KV head 0 writes
 // the pages, counts and context.
@@ -1662,6 +1663,13 @@ constexpr int FS_WAVES = 8;
 constexpr int FS_THREADS = 64 * FS_WAVES;
 constexpr int FS_STREAM = FS_WAVES - DR_WAVES;  // waves streaming the window while the others route
 constexpr int FS_MAX_PAGES = 64 * 32;           // routing loads held in registers (PL <= 32)
+// The routing's length in chunk times of a streaming wave (about 13 us against
+// ~5 us per chunk at the C4 shape): the routing waves take that many fewer
+// selected-page chunks.
+#ifndef FSI_FS_ROUTE_CHUNKS
+#define FSI_FS_ROUTE_CHUNKS 2
+#endif
+constexpr int FS_ROUTE_CHUNKS = FSI_FS_ROUTE_CHUNKS;
 static_assert(FS_SLOTS == FS_WAVES, "one partial slot per wave of the one-launch step");
 
 template <int PL, int E, int HD>
@@ -1669,14 +1677,13 @@ __global__ __launch_bounds__(FS_THREADS) void decode_step_fused_kernel(RouteArgs
   constexpr int DT = HD / 16;
   __shared__ int32_t pg_lds[64 * E];
   __shared__ int64_t rem_off[64 * E];  // element offset of selected page r's (page, g) block, -1 if invalid
-  __shared__ int cnt_lds, flag, bar_ctr, rem_next;
+  __shared__ int cnt_lds, flag, bar_ctr;
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = static_cast<int>(blockIdx.x) % A.B, g = static_cast<int>(blockIdx.x) / A.B;
   if (threadIdx.x == 0) {
     flag = 0;
     bar_ctr = 0;
-    rem_next = 0;
     cnt_lds = 0;
   }
   __syncthreads();
@@ -1732,9 +1739,14 @@ __global__ __launch_bounds__(FS_THREADS) void decode_step_fused_kernel(RouteArgs
   for (int i = 0; i < DT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  // chunk sequence of this wave: its local chunks, then selected-page chunks
-  // taken one at a time from rem_next until 2 cnt are taken
-  int taken_loc = 0, n_sel = -1;  // n_sel: 2 cnt once the flag is seen
+  // Chunk sequence of this wave: its local chunks, then a contiguous range of the
+  // selected pages' chunks.  The ranges are static (the same inputs give the same
+  // chunks in the same order to every wave, so the output is reproducible bit for
+  // bit) and balance the routing waves' late start: with n = nl + n_sel chunks and
+  // the routing worth FS_ROUTE_CHUNKS chunk times, each wave should finish after
+  // T = (n + DR_WAVES FS_ROUTE_CHUNKS) / FS_WAVES chunk times, so a streaming wave
+  // takes T - nl / FS_STREAM selected chunks and the routing waves share the rest.
+  int taken_loc = 0, n_sel = -1, r_lo = 0, r_hi = 0, r_next = 0;
   auto next_chunk = [&](int64_t& info, int& lo, int& hi) -> bool {  // uniform
     if (taken_loc < n_loc) {
       const uint32_t l32 = __builtin_amdgcn_readlane(static_cast<uint32_t>(cb_loc), taken_loc);
@@ -1759,11 +1771,23 @@ __global__ __launch_bounds__(FS_THREADS) void decode_step_fused_kernel(RouteArgs
         }
         __builtin_amdgcn_s_sleep(1);
       }
+      // chunks per streaming wave (x 8 to keep fractions): T - nl / FS_STREAM, at least 0
+      const int t8 = (8 * (nl + n_sel) + 8 * DR_WAVES * FS_ROUTE_CHUNKS) / FS_WAVES;
+      int per_s = (t8 - 8 * nl / FS_STREAM + 4) / 8;
+      per_s = per_s < 0 ? 0 : (FS_STREAM * per_s > n_sel ? n_sel / FS_STREAM : per_s);
+      const int for_route = n_sel - FS_STREAM * per_s;  // the routing waves' chunks [0, for_route)
+      const int per_r = (for_route + DR_WAVES - 1) / DR_WAVES;
+      if (wave < DR_WAVES) {
+        r_lo = wave * per_r < for_route ? wave * per_r : for_route;
+        r_hi = r_lo + per_r < for_route ? r_lo + per_r : for_route;
+      } else {
+        r_lo = for_route + sw * per_s;
+        r_hi = r_lo + per_s;
+      }
+      r_next = r_lo;
     }
-    int r = 0;
-    if (lane == 0) r = __hip_atomic_fetch_add(&rem_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    r = __builtin_amdgcn_readfirstlane(r);
-    if (r >= n_sel) return false;
+    if (r_next >= r_hi) return false;
+    const int r = r_next++;
     const int64_t off = rem_off[r >> 1];
     info = off < 0 ? 0 : off + (r & 1);
     lo = 0;

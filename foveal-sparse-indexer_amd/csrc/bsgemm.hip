@@ -785,6 +785,7 @@ __global__ __launch_bounds__(BT, 1) void bsgemm_big_kernel(GemmArgs g) {
 #endif
 constexpr int DK = 32, DSTAGES = FSI_GEMM_DMA_STAGES, DWAVES = FSI_GEMM_DMA_WAVES, DTHREADS = 64 * DWAVES;
 static_assert(DWAVES == 4 || DWAVES == 8, "direct-to-LDS GEMM waves");
+static_assert(DSTAGES >= 3, "the fragment prefetch reads the stage after the one being multiplied");
 constexpr int PK_TILE_ELEMS = 512;  // bf16 elements of one packed 16 x 32 operand tile
 
 // Chunk swizzle of 64-byte LDS rows.  A 128-bit LDS read is served eight lanes at a

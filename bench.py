@@ -60,14 +60,14 @@ DECODE_TRAFFIC_BYTES_UNPACKED = int(140566.8 * 1024)
 # profiles/pattention_decode_prefill_8b.md, decode_attention_c4.md, indexer_routing_c2.md,
 # block_sparse_gemm_c5.md).
 PREFILL_TRAFFIC_BYTES = int((393537 + 33270 + 196732 + 34374) * 1024)
-# C4 (decode_step_fused_kernel, one launch): FETCH 202340.1 KiB x 1.9842 + WRITE 4614.0 KiB x 0.99225, both
-# factors from the 512 MiB copy of the same run (profiles/decode_attention_c4.md)
-C4_TRAFFIC_BYTES = int((202340.1 * 1.9842 + 4614.0 * 0.99225) * 1024)
+# C4 (decode_step_fused_kernel, one launch): FETCH 202338.9 KiB x 1.99983 + WRITE 4614.3 KiB, the read
+# factor from the 512 MiB copy of the same run (profiles/decode_attention_c4.md)
+C4_TRAFFIC_BYTES = int((202338.9 * 1.99983 + 4614.3) * 1024)
 C2_TRAFFIC_BYTES = int((2057 + 2112) * 1024)
 C5_TRAFFIC_BYTES = {0.10: (515 + 64) << 20, 0.25: (1175 + 64) << 20, 0.50: (2249 + 64) << 20}
 # Prefill attention, one step (sa_vmax + sa_vt16 + sparse_attn_lds, profiles/sparse_attention_prefill_16k.md):
-# (868556.3 + 16425.6 + 16465.1) KiB x 1.99984 read + (131357.2 + 32 + 32768.0) KiB written
-PREFILL_ATTN_TRAFFIC_BYTES = int(901447.0 * 1.99984 * 1024 + 164157.2 * 1024)
+# (873685.9 + 16425.7 + 16507.2) KiB x 1.99983 read + (131285.4 + 32 + 32768.1) KiB written
+PREFILL_ATTN_TRAFFIC_BYTES = int(906618.8 * 1.99983 * 1024 + 164085.5 * 1024)
 # C2: wave-level VALU instructions of one score_route_kernel launch (rocprofv3 SQ_INSTS_VALU)
 C2_VALU_INSTS = 70_114_379
 VALU_PEAK_GIPS = 256 * 4 * 2.4 / 4  # G wave64 VALU instructions/s: 256 CUs x 4 SIMDs x 2.4 GHz / 4 cycles

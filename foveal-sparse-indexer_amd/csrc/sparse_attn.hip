@@ -510,11 +510,20 @@ __device__ __forceinline__ void sal_order() {
 #endif
 }
 
-// Largest of 8 values with v_max3_f32 (4 instructions).
-__device__ __forceinline__ float sal_max8(const float* v) {
-  return __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(v[0], v[1]), v[2]),
-                         __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(v[3], v[4]), v[5]),
-                                         __builtin_fmaxf(__builtin_fmaxf(v[6], v[7]), -INFINITY)));
+// v_max3_f32 as written: fmaxf's IEEE semantics make the compiler quiet every operand
+// it cannot prove canonical (one v_max_f32 x, x, x each, half the instructions of the
+// tree below); the scores here are finite or -inf.
+__device__ __forceinline__ float sal_max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// Largest of 16 values in 8 v_max3_f32.
+__device__ __forceinline__ float sal_max16(const float* v) {
+  const float a = sal_max3(v[0], v[1], v[2]), b = sal_max3(v[3], v[4], v[5]), c = sal_max3(v[6], v[7], v[8]);
+  const float d = sal_max3(v[9], v[10], v[11]), e = sal_max3(v[12], v[13], v[14]);
+  const float f = sal_max3(a, b, c), g = sal_max3(d, e, v[15]);
+  return sal_max3(f, g, g);
 }
 
 template <int HD>
@@ -797,7 +806,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
       // Most pairs only need to know that no score of the wave passes that
       // threshold (a max3 tree and one compare); the row maxima are formed only
       // when one does.
-      float mx = __builtin_fmaxf(sal_max8(sv), sal_max8(sv + 8));
+      float mx = sal_max16(sv);
       alpha[qt] = 1.f;
 #ifdef FSI_SAL_ALWAYSMAX
       if (true) {

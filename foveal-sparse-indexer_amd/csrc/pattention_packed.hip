@@ -290,9 +290,12 @@ __global__ __launch_bounds__(WS_THREADS) void ws_gateup_kernel(PkArgs a) {
   }
   __syncthreads();
   bf16_t* hb = reinterpret_cast<bf16_t*>(lds + RED);
+  // element (t, j, ln) of the accumulators: token 16 t + 4 (ln / 16) + j, channel ln % 16;
+  // consecutive threads take consecutive ln, so each of the 16 partial reads is one
+  // conflict-free 256-byte row (an element order by token put 4 lanes on each bank)
   for (int e = tid; e < ROWS * 16; e += WS_THREADS) {
-    const int tok = e >> 4, ch = e & 15;
-    const int t = tok >> 4, j = tok & 3, ln = 16 * ((tok & 15) >> 2) + ch;
+    const int ln = e & 63, tj = e >> 6, t = tj >> 2, j = tj & 3;
+    const int tok = 16 * t + 4 * (ln >> 4) + j, ch = ln & 15;
     float g = 0.f, u = 0.f;
 #pragma unroll
     for (int w = 0; w < WS_CONS; ++w) {
@@ -404,9 +407,9 @@ __global__ __launch_bounds__(WS_THREADS) void ws_down_kernel(PkArgs a) {
       for (int j = 0; j < 4; ++j) red[(wave * TT + t) * 256 + j * 64 + lane] = acc[t][j];
   }
   __syncthreads();
-  for (int e = tid; e < ROWS * 16; e += WS_THREADS) {
-    const int tok = e >> 4, d = e & 15;
-    const int t = tok >> 4, j = tok & 3, ln = 16 * ((tok & 15) >> 2) + d;
+  for (int e = tid; e < ROWS * 16; e += WS_THREADS) {  // element order as in ws_gateup_kernel
+    const int ln = e & 63, tj = e >> 6, t = tj >> 2, j = tj & 3;
+    const int tok = 16 * t + 4 * (ln >> 4) + j, d = ln & 15;
     float y = 0.f;
 #pragma unroll
     for (int w = 0; w < WS_CONS; ++w) y += red[(w * TT + t) * 256 + j * 64 + ln];

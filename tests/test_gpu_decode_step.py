@@ -26,6 +26,7 @@ CASES = [
     (32, 32, 8, 128, 2048, 2047, 1024, 0, 32, 0.9, False),     # window over half the context, no context output
     (64, 16, 4, 128, 3072, 3000, 256, 1, 16, 0.8, True),        # 64 sequences x 4 KV heads, GQA group 4
     (256, 4, 1, 64, 44800, 44799, 1024, 0, 12, 0.9, True),      # 700 pages (16 slots per lane), one KV head
+    (32, 32, 8, 128, 4096, "mixed", 1024, 0, 16, 0.9, True),    # some sequences inside their window: no pages
 ]
 
 
@@ -49,8 +50,11 @@ def test_decode_step_one_launch(fsi, dev, case):
     print(f"[case] one-launch decode step {case}", flush=True)
     assert B * Hkv >= torch.cuda.get_device_properties(dev).multi_processor_count, "case must take the one-launch path"
     c, g = _device_cache(fsi, dev, B, Hkv, hd, max_seq, seed=B + hd + Hkv)
-    if pos == "per-seq":
-        pos_list = [max_seq - 1 - (37 * b) % 1500 for b in range(B)]
+    if pos in ("per-seq", "mixed"):
+        if pos == "per-seq":
+            pos_list = [max_seq - 1 - (37 * b) % 1500 for b in range(B)]
+        else:  # positions 0 .. max_seq - 1: the first sequences have no page before their window
+            pos_list = [(b * 131) % max_seq for b in range(B)]
         pos_arg = torch.tensor(pos_list, dtype=torch.int32, device=dev)
     else:
         pos_list = [pos] * B
@@ -72,7 +76,9 @@ def test_decode_step_one_launch(fsi, dev, case):
         assert torch.equal(res[3], ref[2])
     cnt = counts.cpu().tolist()
     assert max(cnt) > 0
-    for b in sorted({0, B // 2, B - 1}):
+    if pos == "mixed":
+        assert min(cnt) == 0  # the case covers sequences with nothing to route
+    for b in sorted({0, 1, B // 2, B - 1}):
         kk, vv = c.to_dense(max_seq, batch=slice(b, b + 1))
         sel = [pages[b, :cnt[b]].cpu().tolist()]
         want = A.decode_attention_f64(q[b:b + 1].cpu().float(), kk.cpu(), vv.cpu(), [pos_list[b]], W, sel, 64, scale)

@@ -27,11 +27,16 @@ using namespace fsi;
 
 namespace {
 
+// 96 keys per wave: at the C4 shape (3072 keys per sequence and KV head) 32 splits fill
+// the chip's 4096 wave slots (four per SIMD) in two whole rounds; 128 (1.5 rounds)
+// measured 0.197-0.203 ms against 0.188-0.189, 64 / 80 / 112 no better than 128 and
+// 192 (two waves per SIMD) 0.245.
 #ifndef FSI_D32_SPLIT
-#define FSI_D32_SPLIT 128
+#define FSI_D32_SPLIT 96
 #endif
 constexpr int D_SPLIT = FSI_D32_SPLIT;  // keys per split (one wave)
 constexpr int D_TILES = D_SPLIT / 16;
+static_assert(D_SPLIT % 16 == 0 && D_SPLIT >= 16, "a split is whole 16-key tiles");
 constexpr int D_WAVES = 4;    // splits per workgroup
 constexpr int D_HG = 16;      // query heads per MFMA column block
 constexpr float D_LOG2E = 1.4426950408889634f;

@@ -772,10 +772,12 @@ def bench_hbm_stream(fsi, args, dev):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=10)
+    # defaults: 1000 timed / 100 warm-up steps for the C3 decode line (a 30 ms timed
+    # window; 200 / 10 measured ~3 % slower per step), 100 / 10 for a workload line
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--layers", type=int, default=8)
-    ap.add_argument("--prefill-steps", type=int, default=16)
+    ap.add_argument("--prefill-steps", type=int, default=64)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-workloads", action="store_true",
@@ -789,6 +791,11 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one plain 512 MiB device copy (reference kernel for HBM counters)")
     args = ap.parse_args()
+    direct = args.workload != "pattention"
+    if args.steps is None:
+        args.steps = 100 if direct else 1000
+    if args.warmup is None:
+        args.warmup = 10 if direct else 100
     global EAGER
     EAGER = args.eager
     if args.gpus != 1:

@@ -49,7 +49,16 @@ namespace {
 
 constexpr int TT = 128;       // output tile edge
 constexpr int KS = 32;        // K-step
-constexpr int NTHREADS = 256;
+#ifndef FSI_TG_WAVES
+#define FSI_TG_WAVES 4
+#endif
+constexpr int NW = FSI_TG_WAVES;  // waves per workgroup: 2 along M x NW / 2 along N
+static_assert(NW == 4 || NW == 8, "wave layouts");
+constexpr int NTHREADS = 64 * NW;
+constexpr int AF = 8 / NW;         // A (and B) 16-row fragments each wave loads per K-step
+constexpr int WNW = NW / 2;        // waves along N
+constexpr int WCOLS = TT / WNW;    // output columns of a wave
+constexpr int FB = WCOLS / 16;     // B fragments a wave multiplies (A: 4)
 #ifndef FSI_TG_STAGES
 #define FSI_TG_STAGES 4
 #endif
@@ -70,7 +79,7 @@ constexpr int GROUP_M = FSI_TG_GROUP_M;
 #define FSI_TG_LIST_MAX 2048
 #endif
 constexpr int LIST_MAX = FSI_TG_LIST_MAX;  // k blocks per tile (K / block_k)
-constexpr int LOADS = 4;            // global_load_lds per wave and step: 2 A + 2 B fragments of 1 KiB
+constexpr int LOADS = 2 * AF;       // global_load_lds per wave and step: AF A + AF B fragments of 1 KiB
 constexpr int FRAG_ELEMS = 16 * KS;  // one 16-row fragment of a stage
 
 struct TileArgs {
@@ -258,7 +267,7 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   __shared__ int32_t chunk_count[LIST_MAX / 64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WNW, wn = wave % WNW;
 
   // ---- which tile ---------------------------------------------------------------
   const int pos = xcd_contiguous(blockIdx.x, gridDim.x);
@@ -293,17 +302,17 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   for (int i = 0; i < MAX_ROUNDS; ++i) {
     if (i < rounds) {
       bal[i] = __ballot(bits[i] != 0);
-      if (lane == 0) chunk_count[i * 4 + wave] = __popcll(bal[i]);
+      if (lane == 0) chunk_count[i * NW + wave] = __popcll(bal[i]);
     }
   }
   __syncthreads();
   int nact = 0;
-  for (int c = 0; c < rounds * 4; ++c) nact += chunk_count[c];
+  for (int c = 0; c < rounds * NW; ++c) nact += chunk_count[c];
 #pragma unroll
   for (int i = 0; i < MAX_ROUNDS; ++i) {
     if (i < rounds && bits[i]) {
       int base = 0;
-      for (int c = 0; c < i * 4 + wave; ++c) base += chunk_count[c];
+      for (int c = 0; c < i * NW + wave; ++c) base += chunk_count[c];
       const int pos = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal[i] >> 32),
                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[i]), 0));
       klist[pos] = (i * NTHREADS + tid) | (MASKED ? static_cast<int>(bits[i] << 16) : 0);
@@ -314,14 +323,14 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   const int per = g.block_k / KSE;
   const int kcount = nact * per;
 
-  // ---- this lane's source rows: wave w loads fragments 2 w, 2 w + 1 of A and B;
-  // lane l lands at fragment row l / 4, slot l % 4, holding logical chunk
+  // ---- this lane's source rows: wave w loads fragments AF w .. AF w + AF - 1 of A
+  // and B; lane l lands at fragment row l / 4, slot l % 4, holding logical chunk
   // (l % 4) ^ chunk_swz(row) --------------------------------------------------
-  const T* asrc[2];
-  const T* bsrc[2];
+  const T* asrc[AF];
+  const T* bsrc[AF];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 16 * (2 * wave + j) + (lane >> 2);
+  for (int j = 0; j < AF; ++j) {
+    const int r = 16 * (AF * wave + j) + (lane >> 2);
     const int lc = (lane & 3) ^ chunk_swz(r);
     const int m = m0 + r < g.M ? m0 + r : g.M - 1;  // rows past M read row M - 1, never stored
     const int n = n0 + r < g.N ? n0 + r : g.N - 1;
@@ -345,34 +354,34 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
       }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < AF; ++j) {
       __builtin_amdgcn_global_load_lds((glb_void_t*)(asrc[j] + k),
-                                       (lds_void_t*)&lds[stage][0][(2 * wave + j) * FRAG_ELEMS], 16, 0, 0);
+                                       (lds_void_t*)&lds[stage][0][(AF * wave + j) * FRAG_ELEMS], 16, 0, 0);
       __builtin_amdgcn_global_load_lds((glb_void_t*)(bsrc[j] + k),
-                                       (lds_void_t*)&lds[stage][1][(2 * wave + j) * FRAG_ELEMS], 16, 0, 0);
+                                       (lds_void_t*)&lds[stage][1][(AF * wave + j) * FRAG_ELEMS], 16, 0, 0);
     }
   };
 
-  f32x4_t acc[4][4];
+  f32x4_t acc[4][FB];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int f = 0; f < 4; ++f) acc[i][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int f = 0; f < FB; ++f) acc[i][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // wave (wm, wn): rows 64 wm + 16 i, columns 64 wn + 16 f of the tile
+  // wave (wm, wn): rows 64 wm + 16 i, columns WCOLS wn + 16 f of the tile
   const int frow = lane & 15, fchunk = lane >> 4;
-  int fsub[4];  // n block (within the tile) of each B fragment
+  int fsub[FB];  // n block (within the tile) of each B fragment
 #pragma unroll
-  for (int f = 0; f < 4; ++f) fsub[f] = MASKED ? (64 * wn + 16 * f) / g.block_n : 0;
-  auto read_frags = [&](int stage, u32x4_t (&fa)[4], u32x4_t (&fb)[4]) {
+  for (int f = 0; f < FB; ++f) fsub[f] = MASKED ? (WCOLS * wn + 16 * f) / g.block_n : 0;
+  auto read_frags = [&](int stage, u32x4_t (&fa)[4], u32x4_t (&fb)[FB]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 64 * wm + 16 * i + frow;
       fa[i] = *reinterpret_cast<const u32x4_t*>(&lds[stage][0][r * KS + (fchunk ^ chunk_swz(r)) * 8]);
     }
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const int c = 64 * wn + 16 * f + frow;
+    for (int f = 0; f < FB; ++f) {
+      const int c = WCOLS * wn + 16 * f + frow;
       fb[f] = *reinterpret_cast<const u32x4_t*>(&lds[stage][1][c * KS + (fchunk ^ chunk_swz(c)) * 8]);
     }
     if (MASKED) {  // zero the B fragments of n blocks inactive at this k block
@@ -385,18 +394,18 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
         }
       }
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
+      for (int f = 0; f < FB; ++f)
         if (!((on >> fsub[f]) & 1u)) fb[f] = u32x4_t{0u, 0u, 0u, 0u};
     }
   };
-  auto mfmas = [&](const u32x4_t (&fa)[4], const u32x4_t (&fb)[4]) {
+  auto mfmas = [&](const u32x4_t (&fa)[4], const u32x4_t (&fb)[FB]) {
     if constexpr (F32) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int f = 0; f < 4; ++f)  // C^T fragment
+          for (int f = 0; f < FB; ++f)  // C^T fragment
             // (element by value: this clang's __builtin_bit_cast of a vector element
             // reads element 0 whatever the index)
             acc[i][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(fb[f][kk]), __uint_as_float(fa[i][kk]),
@@ -405,7 +414,7 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int f = 0; f < 4; ++f) acc[i][f] = mfma16x16x32(fb[f], fa[i], acc[i][f]);  // C^T fragment
+        for (int f = 0; f < FB; ++f) acc[i][f] = mfma16x16x32(fb[f], fa[i], acc[i][f]);  // C^T fragment
     }
   };
 #if FSI_TG_PREFETCH
@@ -416,21 +425,22 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
     const int after = last - (s + 2);
     wait_steps(after > 0 ? after : 0);
   };
-  auto iteration = [&](int step, const u32x4_t (&ca)[4], const u32x4_t (&cb)[4], u32x4_t (&na)[4],
-                       u32x4_t (&nb)[4]) {
+  auto iteration = [&](int step, const u32x4_t (&ca)[4], const u32x4_t (&cb)[FB], u32x4_t (&na)[4],
+                       u32x4_t (&nb)[FB]) {
     // the stage of step + STAGES - 1 was last read during iteration step - 2
     if (step + STAGES - 1 < kcount) issue((step + STAGES - 1) % STAGES);
     // unconditional: past the last step it reads a stage that is never used
     read_frags((step + 1) % STAGES, na, nb);
     mfmas(ca, cb);
-    constexpr int MF = F32 ? 8 : 2;  // MFMAs per fragment read of the next step
+    // MFMAs per fragment read of the next step (4 + FB reads, 4 FB MFMAs, x 4 in fp32)
+    constexpr int MF = (F32 ? 4 : 1) * FB / 2;
     __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
+    for (int r = 0; r < 4 + FB; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, F32 ? 0 : 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, F32 ? 0 : MF, 0);
     wait_through(step);
     stage_barrier();
   };
@@ -440,7 +450,7 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   for (int p = 0; p < pre; ++p) issue(p);
   wait_steps(pre - 2 > 0 ? pre - 2 : 0);
   stage_barrier();
-  u32x4_t fa0[4], fb0[4], fa1[4], fb1[4];
+  u32x4_t fa0[4], fb0[FB], fa1[4], fb1[FB];
   if (kcount > 0) read_frags(0, fa0, fb0);
   int step = 0;
   for (; step + 1 < kcount; step += 2) {
@@ -460,7 +470,7 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   for (int step = 0; step < kcount; ++step) {
     // the stage of step + STAGES - 1 was last read during iteration step - 1
     if (step + STAGES - 1 < kcount) issue((step + STAGES - 1) % STAGES);
-    u32x4_t fa[4], fb[4];
+    u32x4_t fa[4], fb[FB];
     read_frags(step % STAGES, fa, fb);
     mfmas(fa, fb);
     const int last = kcount - 1 < step + STAGES - 1 ? kcount - 1 : step + STAGES - 1;
@@ -473,13 +483,13 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
   // ---- epilogue: lane (q = lane / 16, r = lane % 16) of fragment (i, f) holds row
   // 16 i + r of the wave's rows and columns 4 q .. 4 q + 3 of the fragment ----------
   const int crow = m0 + 64 * wm + frow;
-  const int ccol = n0 + 64 * wn + 4 * fchunk;
+  const int ccol = n0 + WCOLS * wn + 4 * fchunk;
   T* C = static_cast<T*>(g.C);
   if (g.bias) {  // block_k == K: the bias of the columns whose n block is active
     const T* bias = static_cast<const T*>(g.bias);
     const uint8_t* row0 = g.mask + static_cast<int64_t>(grp) * g.nkb * g.nnb;
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
+    for (int f = 0; f < FB; ++f)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = ccol + 16 * f + j;
@@ -497,7 +507,7 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
+      for (int f = 0; f < FB; ++f) {
         T* dst = C + static_cast<int64_t>(crow + 16 * i) * g.ldc + ccol + 16 * f;
         if constexpr (F32) {
           *reinterpret_cast<f32x4_t*>(dst) = acc[i][f];
@@ -514,7 +524,7 @@ __global__ __launch_bounds__(NTHREADS, WG_PER_CU) void tile_list_gemm_kernel(Til
       const int m = crow + 16 * i;
       if (m >= g.M) continue;
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
+      for (int f = 0; f < FB; ++f)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int n = ccol + 16 * f + j;

@@ -488,8 +488,16 @@ constexpr int SAL_QT = FSI_SAL_QT;           // query tiles per wave
 constexpr int SAL_HALVES = 4 / SAL_QT;       // waves per query head (64 queries split)
 constexpr int SAL_WAVES = 4 * SAL_HALVES;    // 4 query heads per workgroup
 constexpr int SAL_MAX_CAP = 64;              // listed pages per query block
-constexpr int SAL_AHEAD = FSI_SAL_AHEAD;     // 64-key stages in flight ahead of the one computed
-constexpr int SAL_RING = SAL_AHEAD + 1;      // 64-key pairs held by the LDS ring
+// Pairs computed per workgroup barrier: G > 1 loads the next G pairs while the
+// current G are computed (one barrier and one wait per group, a ring of 2 G pairs).
+// G = 2 (a 128 KiB ring) measured 0.820-0.823 against 0.824-0.827 ms for one pair per
+// barrier and one pair ahead, in four alternating pairs of 100-step runs.
+#ifndef FSI_SAL_GROUP
+#define FSI_SAL_GROUP 2
+#endif
+constexpr int SAL_GROUP = FSI_SAL_GROUP;
+constexpr int SAL_AHEAD = SAL_GROUP > 1 ? SAL_GROUP : FSI_SAL_AHEAD;  // 64-key stages in flight ahead
+constexpr int SAL_RING = SAL_GROUP > 1 ? 2 * SAL_GROUP : SAL_AHEAD + 1;  // 64-key pairs held by the LDS ring
 constexpr int SAL_SLOTS = 2 * SAL_RING;       // 32-key chunk slots of the LDS ring
 typedef __attribute__((address_space(3))) void sal_lds_t;
 typedef __attribute__((address_space(1))) void sal_glb_t;
@@ -857,6 +865,35 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
     }
   };
 
+#if FSI_SAL_GROUP > 1
+  for (int p0 = 0; p0 < n_pairs; p0 += SAL_GROUP) {
+    sal_wait_vmcnt<0>();  // this group's pairs landed (nothing else is in flight)
+    sal_barrier();
+#pragma unroll
+    for (int j = 0; j < SAL_GROUP; ++j) {  // the next group into the previous group's slots
+      const int pn = p0 + SAL_GROUP + j;
+      if (pn < n_pairs) {
+        const int sn = 2 * (pn % SAL_RING);
+        int n0, nh0, nh1;
+        bool nl;
+        describe(pn, n0, nh0, nh1, nl);
+        issue(n0, sn);
+        issue(n0 + 1, sn + 1);
+      }
+    }
+    for (int j = 0; j < SAL_GROUP; ++j) {
+      const int p = p0 + j;
+      if (p >= n_pairs) break;
+      int c0, hi0, hi1;
+      bool local;
+      describe(p, c0, hi0, hi1, local);
+      if ((hi0 | hi1) == 0 || !head_live) continue;  // uniform: an empty pair or an idle wave
+      const int sl = 2 * (p % SAL_RING);
+      scores(sl);
+      finish(sl, c0, hi0, hi1, local);
+    }
+  }
+#else
   for (int p = 0; p < n_pairs; ++p) {
     // pair p landed: at most the loads of pairs p + 1 .. p + AHEAD - 1 remain
     const int later = (p + SAL_AHEAD - 1 < n_pairs - 1 ? p + SAL_AHEAD - 1 : n_pairs - 1) - p;
@@ -886,6 +923,7 @@ __global__ __launch_bounds__(64 * SAL_WAVES) void sparse_attn_lds_kernel(SAParam
     scores(sl);
     finish(sl, c0, hi0, hi1, local);
   }
+#endif
 
   if (!head_live) return;
 #pragma unroll

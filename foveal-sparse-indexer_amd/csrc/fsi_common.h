@@ -114,6 +114,15 @@ __device__ __forceinline__ float max_rows4(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// v_max3_f32 as written.  fmaxf's IEEE semantics make the compiler quiet every
+// operand it cannot prove canonical (a v_max_f32 x, x, x each); for scores that are
+// finite or -inf (softmax maxima) that doubles the instructions of a max tree.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // Wave-level reductions (64 lanes).
 // ---------------------------------------------------------------------------

@@ -518,20 +518,12 @@ __device__ __forceinline__ void sal_order() {
 #endif
 }
 
-// v_max3_f32 as written: fmaxf's IEEE semantics make the compiler quiet every operand
-// it cannot prove canonical (one v_max_f32 x, x, x each, half the instructions of the
-// tree below); the scores here are finite or -inf.
-__device__ __forceinline__ float sal_max3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-// Largest of 16 values in 8 v_max3_f32.
+// Largest of 16 scores (finite or -inf) in 8 v_max3_f32 (max3_raw: no operand quieting).
 __device__ __forceinline__ float sal_max16(const float* v) {
-  const float a = sal_max3(v[0], v[1], v[2]), b = sal_max3(v[3], v[4], v[5]), c = sal_max3(v[6], v[7], v[8]);
-  const float d = sal_max3(v[9], v[10], v[11]), e = sal_max3(v[12], v[13], v[14]);
-  const float f = sal_max3(a, b, c), g = sal_max3(d, e, v[15]);
-  return sal_max3(f, g, g);
+  const float a = max3_raw(v[0], v[1], v[2]), b = max3_raw(v[3], v[4], v[5]), c = max3_raw(v[6], v[7], v[8]);
+  const float d = max3_raw(v[9], v[10], v[11]), e = max3_raw(v[12], v[13], v[14]);
+  const float f = max3_raw(a, b, c), g = max3_raw(d, e, v[15]);
+  return max3_raw(f, g, g);
 }
 
 template <int HD>

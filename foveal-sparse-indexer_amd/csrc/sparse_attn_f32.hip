@@ -328,8 +328,7 @@ __global__ __launch_bounds__(64 * F_WAVES) void sparse_attn_f32_kernel(F32Params
             sv[4 * t + e] = keep < 0 ? sv[4 * t + e] : -INFINITY;
           }
       }
-      const float mx = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(sv[0], sv[1]), __builtin_fmaxf(sv[2], sv[3])),
-                                       __builtin_fmaxf(__builtin_fmaxf(sv[4], sv[5]), __builtin_fmaxf(sv[6], sv[7])));
+      const float mx = max3_raw(max3_raw(sv[0], sv[1], sv[2]), max3_raw(sv[3], sv[4], sv[5]), max3_raw(sv[6], sv[7], sv[7]));
       if (__ballot(mx > m_thr[qt]) != 0) {  // uniform, rare: the running max moves
         const float m_cand = max_rows4(mx) * sl2;
         const bool bump = m_cand > m_run[qt] + 8.f;

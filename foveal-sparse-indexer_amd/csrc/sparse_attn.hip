@@ -479,8 +479,9 @@ __device__ __forceinline__ f32x4_t mfma16x16x32_f16(const u32x4_t& a, const u32x
 #ifndef FSI_SAL_QT
 #define FSI_SAL_QT 2
 #endif
-// 64-key pairs loaded ahead of the one computed: 1 (a 2-pair ring, 64 KiB) measured
-// 0.9 % faster than 2 at 16K tokens in alternating runs on one box, 3 within noise
+// With one pair per barrier (FSI_SAL_GROUP=1), 64-key pairs loaded ahead of the one
+// computed: 1 (a 2-pair ring, 64 KiB) measured 0.9 % faster than 2 at 16K tokens in
+// alternating runs on one box, 3 within noise
 #ifndef FSI_SAL_AHEAD
 #define FSI_SAL_AHEAD 1
 #endif

@@ -233,7 +233,31 @@ __global__ __launch_bounds__(64 * D_WAVES) void dec32_merge_kernel(D32Params P) 
       }
       lsum += wave_sum(wj * lj);
       const int n = ns - s0 < 64 ? ns - s0 : 64;
-      for (int j = 0; j < n; ++j) {
+      // eight splits' loads issued together, then added in split order (the same
+      // fmaf chain as one split at a time; one at a time left a load latency per split)
+      int j = 0;
+      for (; j + 8 <= n; j += 8) {
+        float qv[8][DPL];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float* q = pp + (s0 + j + u) * (HD + 2) + 2;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) {
+            const int d = lane + 64 * e;
+            qv[u][e] = d < HD ? q[d] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float w = __shfl(wj, j + u, 64);
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) {
+            const int d = lane + 64 * e;
+            if (d < HD) o[e] = fmaf(w, qv[u][e], o[e]);
+          }
+        }
+      }
+      for (; j < n; ++j) {
         const float w = __shfl(wj, j, 64);
         const float* q = pp + (s0 + j) * (HD + 2) + 2;
 #pragma unroll
